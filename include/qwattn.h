@@ -1,0 +1,187 @@
+/*
+ * qwattn.h - C ABI of the MI355X (gfx950) full-attention hot path.
+ *
+ * The ABI is what the reference's Rust runtime would bind in place of its
+ * MLX-backed KV cache and attention calls (crates/mlxcel-core). Every entry
+ * point names the reference interface it replaces (path:line in the
+ * reference tree cr0sh/qw).
+ *
+ * Conventions
+ *   - Plain C: opaque handles, caller-owned device pointers, int status.
+ *   - Device pointers live on the device the cache (or call) runs on; the
+ *     library sets that device for the duration of a call.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the default stream).
+ *     All device work of a call is enqueued on it; no call synchronizes the
+ *     stream except where stated.
+ *   - Tensors use the reference's layouts with the batch dimension of 1
+ *     dropped: q [n_q_heads][n_rows][head_dim], new K/V
+ *     [n_kv_heads][n_tokens][head_dim], attention output like q. Element
+ *     type is IEEE fp16 unless stated.
+ *   - Errors: a non-zero status and a message from qw_last_error() (thread
+ *     local). Invalid shapes return QW_ERR_INVALID_ARGUMENT and enqueue
+ *     nothing. No C++ exception crosses the ABI. The reference instead
+ *     panics (cache.rs:3503-3507) or throws std::invalid_argument
+ *     (mlx_cxx_dlsa_attention.cpp:429-470); the status codes carry the
+ *     same checks.
+ *   - Threading: a cache handle is used by one thread at a time, as the
+ *     reference's KVCache is !Send/!Sync (cache.rs:483-497).
+ */
+#ifndef QWATTN_H
+#define QWATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QWATTN_ABI_VERSION 1
+
+/* Status codes. */
+#define QW_OK 0
+#define QW_ERR_INVALID_ARGUMENT 1
+#define QW_ERR_UNSUPPORTED 2
+#define QW_ERR_OUT_OF_MEMORY 3
+#define QW_ERR_HIP 4
+#define QW_ERR_STATE 5
+
+/* KV storage modes. The reference's KVCacheMode (cache.rs:172-205) has
+ * Fp16, Int8 and the Turbo family; the affine modes are the codec the
+ * reference names at its quantization seam (KvQuantScheme::Uniform,
+ * DEFAULT_KV_GROUP_SIZE = 64, batch_quant.rs:109-158) with MLX `quantize`
+ * semantics (group 64, fp16 scale and bias per group). */
+#define QW_KV_FP16 0
+#define QW_KV_AFFINE8 1
+#define QW_KV_AFFINE4 2
+
+typedef struct qw_kv_cache qw_kv_cache;
+
+/* Version of this header the library was built from. */
+int qw_abi_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* qw_last_error(void);
+
+/* ---------------------------------------------------------------- cache */
+
+/* KVCache::new_with_mode (cache.rs:526). `capacity` rows per KV head are
+ * allocated up front (rounded up to 256, the reference's growth step,
+ * cache.rs:354-466 `step`); appends beyond it grow the buffers. group_size
+ * must be 64 for the affine modes (ignored for fp16). head_dim: 256 or 128
+ * for the affine modes; a multiple of 64 up to 256 for fp16. `device` is the
+ * HIP device ordinal. */
+int qw_kv_create(int mode, int group_size, int n_kv_heads, int head_dim, int capacity,
+                 int device, qw_kv_cache** out);
+
+/* Frees the device buffers (KVCache drop). Waits for the device first. */
+int qw_kv_destroy(qw_kv_cache* cache);
+
+/* Grows the allocation to at least `capacity` rows per head, preserving
+ * contents (the reference's step-growth concatenate, cache.rs:954-1034). */
+int qw_kv_reserve(qw_kv_cache* cache, int capacity, void* stream);
+
+/* KVCache::offset (pub field, cache.rs:354): number of cached tokens. */
+int qw_kv_offset(const qw_kv_cache* cache, int* offset);
+
+/* Allocated rows per head. */
+int qw_kv_capacity(const qw_kv_cache* cache, int* capacity);
+
+/* KVCache::nbytes (cache.rs:3063): device bytes held by the cache buffers. */
+int qw_kv_nbytes(const qw_kv_cache* cache, int64_t* nbytes);
+
+/* KVCache::update (cache.rs:922): quantize-on-append of n_tokens new rows.
+ * k_new, v_new: [n_kv_heads][n_tokens][head_dim] fp16 device pointers. */
+int qw_kv_update(qw_kv_cache* cache, const void* k_new, const void* v_new, int n_tokens,
+                 void* stream);
+
+/* KVCache::update_and_fetch (cache.rs:2709-2834): append, then write the
+ * whole visible cache, dequantized to fp16, to k_out / v_out
+ * [n_kv_heads][offset][head_dim]. Dequantization is MLX's composite
+ * f16(f16(code * scale) + bias). */
+int qw_kv_update_and_fetch(qw_kv_cache* cache, const void* k_new, const void* v_new,
+                           int n_tokens, void* k_out, void* v_out, void* stream);
+
+/* Dequantized rows [start, start + n) of every head into k_out / v_out
+ * [n_kv_heads][n][head_dim] (a window of update_and_fetch without the
+ * append; the oracle route of cache.rs:3652-3697). */
+int qw_kv_dequantize(const qw_kv_cache* cache, int start, int n, void* k_out, void* v_out,
+                     void* stream);
+
+/* KVCache::update_and_turbo4_attention (cache.rs:3495, causal = 0) and
+ * update_and_turbo4_causal_attention (cache.rs:3520, causal = 1), with the
+ * affine codec: the new rows are quantized and appended first and then
+ * attended in their dequantized form (cache.rs:2723, :3508). One fused
+ * dequant-in-attention pass over the packed cache, no fp16 K/V copy.
+ *   q [n_q_heads][n_rows][head_dim] fp16, n_q_heads % n_kv_heads == 0;
+ *   k_new, v_new [n_kv_heads][n_rows][head_dim] fp16 (n_rows new tokens);
+ *   causal: bottom-right, row r sees keys t <= offset_after - n_rows + r;
+ *   out [n_q_heads][n_rows][head_dim] fp16.
+ * Scores are formed as f16(f16(scale) * q) . k and rounded to fp16 before
+ * the fp32 softmax, as MLX's SDPA forms them. */
+int qw_kv_update_and_attention(qw_kv_cache* cache, const void* q, int n_q_heads, int n_rows,
+                               const void* k_new, const void* v_new, float scale, int causal,
+                               void* out, void* stream);
+
+/* Attention of q over the cache as it is, without an append (the fused
+ * prefix call turbo4_fused_attention_prefix, cache.rs:3607). With causal, row
+ * r of n_rows sees keys t <= offset - n_rows + r. */
+int qw_kv_attention(qw_kv_cache* cache, const void* q, int n_q_heads, int n_rows, float scale,
+                    int causal, void* out, void* stream);
+
+/* KVCache::trim (cache.rs:2251): drop the last n tokens (clamped to the
+ * cached length); *trimmed receives the number removed. No device work. */
+int qw_kv_trim(qw_kv_cache* cache, int n, int* trimmed);
+
+/* Snapshot export in the reference's tensor layout (the packed-tensor
+ * snapshot of cache.rs:570-626): for the affine modes
+ *   k_codes, v_codes  [n_kv_heads][offset][head_dim*bits/32] uint32 (MLX
+ *                     packing), k_scales/k_biases/v_scales/v_biases
+ *                     [n_kv_heads][offset][head_dim/64] fp16;
+ * for fp16 mode k_codes/v_codes receive K/V [n_kv_heads][offset][head_dim]
+ * fp16 and the scale/bias pointers are ignored (may be NULL). */
+int qw_kv_export(const qw_kv_cache* cache, void* k_codes, void* k_scales, void* k_biases,
+                 void* v_codes, void* v_scales, void* v_biases, void* stream);
+
+/* Snapshot import (restore_*_snapshot, cache.rs:570-626): replaces the
+ * cache contents with n_tokens rows in the export layout; no requantization. */
+int qw_kv_import(qw_kv_cache* cache, int n_tokens, const void* k_codes, const void* k_scales,
+                 const void* k_biases, const void* v_codes, const void* v_scales,
+                 const void* v_biases, void* stream);
+
+/* ---------------------------------------------------------------- D-LSA */
+
+/* dlsa_attention::sparse_attention (crates/mlxcel-core/src/dlsa_attention.rs:31)
+ * -> mlx_cxx::dlsa_sparse_attention (mlx_cxx_dlsa_attention.cpp:420-556):
+ * every query row r attends over the keys lists[r, 0:lengths[r]] of its KV
+ * head (head h reads KV head h / (n_q_heads / n_kv_heads)); list order is
+ * irrelevant up to fp32 rounding, entries outside [0, n_keys) are skipped,
+ * a row without a valid entry is zeros. Softmax and accumulation in fp32.
+ *   q   [n_q_heads][n_rows][head_dim] fp16
+ *   k,v fp16, element (h, t, d) at k[h*k_head_stride + t*k_row_stride + d]
+ *       (strided views of a larger cache are read in place, never copied)
+ *   lists [n_rows][width] int32, lengths [n_rows] int32 (device)
+ *   out [n_q_heads][n_rows][head_dim] fp16
+ * head_dim in {64, 128, 256}; n_q_heads / n_kv_heads <= 16. */
+int qw_dlsa_sparse_attention(const void* q, const void* k, const void* v, int64_t k_head_stride,
+                             int64_t k_row_stride, int64_t v_head_stride, int64_t v_row_stride,
+                             const int32_t* lists, const int32_t* lengths, int n_rows, int width,
+                             int n_q_heads, int n_kv_heads, int head_dim, int n_keys,
+                             float scale, void* out, void* stream);
+
+/* dlsa_attention::sparse_attention_with (dlsa_attention.rs:44): the same read
+ * with explicit launch knobs; 0 = automatic. parts: split-K partitions of
+ * each list (1 = one pass, at most 128); waves: wavefronts per workgroup
+ * (1..16). */
+int qw_dlsa_sparse_attention_with(const void* q, const void* k, const void* v,
+                                  int64_t k_head_stride, int64_t k_row_stride,
+                                  int64_t v_head_stride, int64_t v_row_stride,
+                                  const int32_t* lists, const int32_t* lengths, int n_rows,
+                                  int width, int n_q_heads, int n_kv_heads, int head_dim,
+                                  int n_keys, float scale, int parts, int waves, void* out,
+                                  void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWATTN_H */

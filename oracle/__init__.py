@@ -1,0 +1,258 @@
+"""CPU oracle for the full-attention hot path (TEST INFRASTRUCTURE ONLY).
+
+This package is the parity checker and the reported CPU baseline. Only
+``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg
+may import it; the product (``qw_amd`` / ``libqwattn.so``) never does.
+
+It wraps ``libqw_oracle.so`` (``qw_oracle.c``, a C restatement of the
+reference's MLX semantics) with numpy-facing helpers. Array conventions follow
+the reference's tensors with the batch dimension of 1 dropped:
+q ``[Hq, L, D]``, k/v ``[Hkv, T, D]``, out ``[Hq, L, D]``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libqw_oracle.so")
+_lib = None
+
+
+def build() -> str:
+    """Compile ``libqw_oracle.so`` with the committed Makefile."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(_LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+_f64 = ctypes.c_double
+
+
+def _declare(L: ctypes.CDLL) -> None:
+    L.qwo_f32_to_f16.restype = ctypes.c_uint16
+    L.qwo_f32_to_f16.argtypes = [_f32]
+    L.qwo_f16_to_f32.restype = _f32
+    L.qwo_f16_to_f32.argtypes = [ctypes.c_uint16]
+    L.qwo_f32_to_f16_array.argtypes = [_p, _p, _i64]
+    L.qwo_f16_to_f32_array.argtypes = [_p, _p, _i64]
+    L.qwo_affine_quantize.restype = _i32
+    L.qwo_affine_quantize.argtypes = [_p, _i64, _i32, _i32, _i32, _p, _p, _p]
+    L.qwo_affine_dequantize.restype = _i32
+    L.qwo_affine_dequantize.argtypes = [_p, _p, _p, _i64, _i32, _i32, _i32, _p]
+    L.qwo_sdpa_mlx_f16.restype = _i32
+    L.qwo_sdpa_mlx_f16.argtypes = [_p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f32, _p, _p, _i32]
+    L.qwo_sdpa_f64.restype = _i32
+    L.qwo_sdpa_f64.argtypes = [_p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f64, _p, _p, _i32]
+    L.qwo_dlsa_attention.restype = _i32
+    L.qwo_dlsa_attention.argtypes = [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p,
+                                     _i32, _i32, _i32, _i32, _i32, _i32, _f32, _p, _i32]
+    L.qwo_affine_layer_call.restype = _i32
+    L.qwo_affine_layer_call.argtypes = [_p, _p, _p, _p, _p, _p, _i64, _i32, _p, _p, _p,
+                                        _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32,
+                                        _p, _i32, _p, _i32]
+
+
+def _ptr(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a: np.ndarray, dtype) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def default_threads() -> int:
+    return max(1, os.cpu_count() or 1)
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise ValueError(f"oracle {what}: bad arguments (rc={rc})")
+
+
+# ------------------------------------------------------------------ fp16
+
+def f32_to_f16(x: np.ndarray) -> np.ndarray:
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().qwo_f32_to_f16_array(_ptr(x), _ptr(out), x.size)
+    return out.view(np.float16)
+
+
+def f16_to_f32(x: np.ndarray) -> np.ndarray:
+    x = _c(np.asarray(x, np.float16).view(np.uint16), np.uint16)
+    out = np.empty(x.shape, np.float32)
+    lib().qwo_f16_to_f32_array(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+# ----------------------------------------------------------- affine codec
+
+def affine_quantize(w: np.ndarray, bits: int, group: int = 64):
+    """MLX affine quantize of fp16 rows ``w[..., dim]``.
+
+    Returns ``(codes uint32 [..., dim*bits/32], scales f16 [..., dim/group],
+    biases f16 [..., dim/group])``.
+    """
+    w = _c(w, np.float16)
+    dim = w.shape[-1]
+    rows = int(np.prod(w.shape[:-1])) if w.ndim > 1 else 1
+    codes = np.empty(w.shape[:-1] + (dim * bits // 32,), np.uint32)
+    scales = np.empty(w.shape[:-1] + (dim // group,), np.float16)
+    biases = np.empty_like(scales)
+    _check(lib().qwo_affine_quantize(_ptr(w), rows, dim, group, bits, _ptr(codes),
+                                     _ptr(scales), _ptr(biases)), "affine_quantize")
+    return codes, scales, biases
+
+
+def affine_dequantize(codes: np.ndarray, scales: np.ndarray, biases: np.ndarray,
+                      bits: int, group: int = 64) -> np.ndarray:
+    codes = _c(codes, np.uint32)
+    scales = _c(scales, np.float16)
+    biases = _c(biases, np.float16)
+    dim = codes.shape[-1] * 32 // bits
+    rows = int(np.prod(codes.shape[:-1])) if codes.ndim > 1 else 1
+    out = np.empty(codes.shape[:-1] + (dim,), np.float16)
+    _check(lib().qwo_affine_dequantize(_ptr(codes), _ptr(scales), _ptr(biases), rows, dim,
+                                       group, bits, _ptr(out)), "affine_dequantize")
+    return out
+
+
+# ------------------------------------------------------------------ SDPA
+
+def _pos(q_pos, L):
+    if q_pos is None:
+        return None
+    q_pos = _c(q_pos, np.int32)
+    assert q_pos.shape == (L,)
+    return q_pos
+
+
+def causal_positions(L: int, T: int) -> np.ndarray:
+    """Bottom-right causal positions: row r sees keys t <= T - L + r."""
+    return np.arange(T - L, T, dtype=np.int32)
+
+
+def sdpa_mlx_f16(q, k, v, scale: float, q_pos=None, threads: int | None = None):
+    """MLX CPU-stream SDPA with its fp16 roundings. q [Hq,L,D], k/v [Hkv,T,D]."""
+    q, k, v = _c(q, np.float16), _c(k, np.float16), _c(v, np.float16)
+    hq, L, D = q.shape
+    hkv, T, _ = k.shape
+    pos = _pos(q_pos, L)
+    out = np.empty((hq, L, D), np.float16)
+    _check(lib().qwo_sdpa_mlx_f16(_ptr(q), _ptr(k), _ptr(v), hq, hkv, L, T, D, scale,
+                                  _ptr(pos), _ptr(out), threads or default_threads()),
+           "sdpa_mlx_f16")
+    return out
+
+
+def sdpa_f64(q, k, v, scale: float, q_pos=None, threads: int | None = None):
+    """Closed-form softmax attention in fp64 (no intermediate rounding)."""
+    q, k, v = _c(q, np.float16), _c(k, np.float16), _c(v, np.float16)
+    hq, L, D = q.shape
+    hkv, T, _ = k.shape
+    pos = _pos(q_pos, L)
+    out = np.empty((hq, L, D), np.float64)
+    _check(lib().qwo_sdpa_f64(_ptr(q), _ptr(k), _ptr(v), hq, hkv, L, T, D, float(scale),
+                              _ptr(pos), _ptr(out), threads or default_threads()), "sdpa_f64")
+    return out
+
+
+def dlsa_attention(q, k, v, lists, lengths, scale: float, threads: int | None = None):
+    """D-LSA gathered read (K2 contract). q [Hq,L,D] f16; k/v [Hkv,T,D] f16
+    (any element strides with a unit last stride); lists [L,W] i32;
+    lengths [L] i32. Returns fp32 [Hq,L,D]."""
+    q = _c(q, np.float16)
+    k = np.asarray(k, np.float16)
+    v = np.asarray(v, np.float16)
+    if k.strides[-1] != 2:
+        k = np.ascontiguousarray(k)
+    if v.strides[-1] != 2:
+        v = np.ascontiguousarray(v)
+    lists, lengths = _c(lists, np.int32), _c(lengths, np.int32)
+    hq, L, D = q.shape
+    hkv, T, _ = k.shape
+    W = lists.shape[1]
+    out = np.empty((hq, L, D), np.float32)
+    _check(lib().qwo_dlsa_attention(
+        _ptr(q), k.ctypes.data_as(ctypes.c_void_p), v.ctypes.data_as(ctypes.c_void_p),
+        k.strides[0] // 2, k.strides[1] // 2, v.strides[0] // 2, v.strides[1] // 2,
+        _ptr(lists), _ptr(lengths), L, W, hq, hkv, D, T, scale, _ptr(out),
+        threads or default_threads()), "dlsa_attention")
+    return out
+
+
+# ------------------------------------------------------ quantized layer call
+
+class AffineCacheOracle:
+    """Host-side quantized KV cache in the reference's layout (row-major codes,
+    separate fp16 scale and bias planes), used to restate one layer call."""
+
+    def __init__(self, n_kv_heads: int, head_dim: int, capacity: int, bits: int,
+                 group: int = 64):
+        self.hkv, self.D, self.cap, self.bits, self.group = n_kv_heads, head_dim, capacity, bits, group
+        wpr, gpr = head_dim * bits // 32, head_dim // group
+        self.k_codes = np.zeros((n_kv_heads, capacity, wpr), np.uint32)
+        self.v_codes = np.zeros_like(self.k_codes)
+        self.k_scales = np.zeros((n_kv_heads, capacity, gpr), np.float16)
+        self.k_biases = np.zeros_like(self.k_scales)
+        self.v_scales = np.zeros_like(self.k_scales)
+        self.v_biases = np.zeros_like(self.k_scales)
+        self.offset = 0
+
+    def update(self, k_new: np.ndarray, v_new: np.ndarray) -> None:
+        """Quantize-on-append of [Hkv, L, D] fp16 rows."""
+        L = k_new.shape[1]
+        assert self.offset + L <= self.cap
+        for name, src in (("k", k_new), ("v", v_new)):
+            c, s, b = affine_quantize(src, self.bits, self.group)
+            getattr(self, name + "_codes")[:, self.offset:self.offset + L] = c
+            getattr(self, name + "_scales")[:, self.offset:self.offset + L] = s
+            getattr(self, name + "_biases")[:, self.offset:self.offset + L] = b
+        self.offset += L
+
+    def fetch(self):
+        """Dequantized visible K and V, [Hkv, offset, D] fp16 (update_and_fetch)."""
+        T = self.offset
+        k = affine_dequantize(self.k_codes[:, :T], self.k_scales[:, :T], self.k_biases[:, :T],
+                              self.bits, self.group)
+        v = affine_dequantize(self.v_codes[:, :T], self.v_scales[:, :T], self.v_biases[:, :T],
+                              self.bits, self.group)
+        return k, v
+
+    def update_and_attention(self, q, k_new, v_new, scale: float, causal: bool,
+                             rows=None, threads: int | None = None) -> np.ndarray:
+        """Append then attend, in C (quantize, MLX dequantize, MLX SDPA).
+        ``rows`` restricts the computed query rows (attention rows are
+        independent, so a subset is exact)."""
+        q = _c(q, np.float16)
+        k_new, v_new = _c(k_new, np.float16), _c(v_new, np.float16)
+        hq, L, D = q.shape
+        assert self.offset + L <= self.cap
+        sel = None if rows is None else _c(rows, np.int32)
+        n_sel = 0 if sel is None else sel.size
+        out = np.empty((hq, n_sel or L, D), np.float16)
+        _check(lib().qwo_affine_layer_call(
+            _ptr(self.k_codes), _ptr(self.k_scales), _ptr(self.k_biases), _ptr(self.v_codes),
+            _ptr(self.v_scales), _ptr(self.v_biases), self.cap, self.offset, _ptr(q),
+            _ptr(k_new), _ptr(v_new), hq, self.hkv, L, D, self.group, self.bits, scale,
+            1 if causal else 0, _ptr(sel), n_sel, _ptr(out), threads or default_threads()),
+            "affine_layer_call")
+        self.offset += L
+        return out

@@ -1,0 +1,323 @@
+"""qw_amd - MI355X (gfx950) full-attention hot path of cr0sh/qw.
+
+The compute lives in ``libqwattn.so`` (hand-written HIP kernels behind the C
+ABI of ``include/qwattn.h``). This module is the thin host mirror of the
+reference's Rust interface for the path, over ctypes, so that Python callers
+and the tests use the reference's names:
+
+* :class:`KVCache` mirrors ``crates/mlxcel-core/src/cache.rs`` ``KVCache``
+  (``update`` :922, ``update_and_fetch`` :2709, ``update_and_turbo4_attention``
+  :3495 / ``update_and_turbo4_causal_attention`` :3520 with the affine codec,
+  ``trim`` :2251, ``offset``, ``nbytes`` :3063, snapshot tensors :570-626).
+* :func:`sparse_attention` / :func:`sparse_attention_with` mirror
+  ``crates/mlxcel-core/src/dlsa_attention.rs:31`` / ``:44``.
+
+Torch is used only to hold device memory and to name the current stream.
+Tensors follow the reference's layouts: ``[1, H, L, D]`` (the batch of 1 may
+be omitted). There is no CPU fallback: every call goes through the HIP
+library and raises :class:`QwError` when it is missing or a call fails.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+__all__ = ["KVCacheMode", "KVCache", "QwError", "sparse_attention", "sparse_attention_with",
+           "lib", "LIB_PATH"]
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libqwattn.so")
+_lib = None
+
+QW_OK = 0
+_STATUS = {1: "invalid argument", 2: "unsupported", 3: "out of memory", 4: "HIP error",
+           5: "invalid state"}
+
+
+class QwError(RuntimeError):
+    """A libqwattn call failed; ``status`` is the C status code."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{_STATUS.get(status, status)}: {message}")
+        self.status = status
+
+
+_p = ctypes.c_void_p
+_i = ctypes.c_int
+_i64 = ctypes.c_int64
+_f = ctypes.c_float
+
+_SIGNATURES = {
+    "qw_abi_version": (_i, []),
+    "qw_last_error": (ctypes.c_char_p, []),
+    "qw_kv_create": (_i, [_i, _i, _i, _i, _i, _i, ctypes.POINTER(_p)]),
+    "qw_kv_destroy": (_i, [_p]),
+    "qw_kv_reserve": (_i, [_p, _i, _p]),
+    "qw_kv_offset": (_i, [_p, ctypes.POINTER(_i)]),
+    "qw_kv_capacity": (_i, [_p, ctypes.POINTER(_i)]),
+    "qw_kv_nbytes": (_i, [_p, ctypes.POINTER(_i64)]),
+    "qw_kv_update": (_i, [_p, _p, _p, _i, _p]),
+    "qw_kv_update_and_fetch": (_i, [_p, _p, _p, _i, _p, _p, _p]),
+    "qw_kv_dequantize": (_i, [_p, _i, _i, _p, _p, _p]),
+    "qw_kv_update_and_attention": (_i, [_p, _p, _i, _i, _p, _p, _f, _i, _p, _p]),
+    "qw_kv_attention": (_i, [_p, _p, _i, _i, _f, _i, _p, _p]),
+    "qw_kv_trim": (_i, [_p, _i, ctypes.POINTER(_i)]),
+    "qw_kv_export": (_i, [_p, _p, _p, _p, _p, _p, _p, _p]),
+    "qw_kv_import": (_i, [_p, _i, _p, _p, _p, _p, _p, _p, _p]),
+    "qw_dlsa_sparse_attention": (_i, [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _i, _i, _i,
+                                      _i, _i, _i, _f, _p, _p]),
+    "qw_dlsa_sparse_attention_with": (_i, [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _i, _i,
+                                           _i, _i, _i, _i, _f, _i, _i, _p, _p]),
+}
+
+
+def lib() -> ctypes.CDLL:
+    """Load libqwattn.so (built by ``qw_amd.build``); raise if it is absent."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise QwError(4, f"{LIB_PATH} is not built; run `python -m qw_amd.build`")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _check(rc: int) -> None:
+    if rc != QW_OK:
+        raise QwError(rc, lib().qw_last_error().decode())
+
+
+def _torch():
+    import torch  # imported lazily: the ABI itself needs no torch
+
+    return torch
+
+
+def _stream(device) -> int:
+    torch = _torch()
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _as3(t, name: str):
+    """Reference tensors are [1, H, L, D]; accept [H, L, D] as well."""
+    if t.dim() == 4:
+        if t.shape[0] != 1:
+            raise QwError(1, f"{name}: batch must be 1")
+        t = t[0]
+    if t.dim() != 3:
+        raise QwError(1, f"{name}: expected [1, H, L, D] or [H, L, D]")
+    torch = _torch()
+    if t.dtype != torch.float16:
+        raise QwError(2, f"{name}: fp16 expected, got {t.dtype}")
+    if not t.is_cuda:
+        raise QwError(1, f"{name}: must be a device tensor")
+    return t.contiguous()
+
+
+class KVCacheMode:
+    """Storage modes (reference ``KVCacheMode``, cache.rs:172, plus the affine codec)."""
+
+    FP16 = 0
+    AFFINE8 = 1
+    AFFINE4 = 2
+
+    @staticmethod
+    def from_str(s: str) -> int:
+        key = s.lower()
+        table = {"fp16": 0, "float16": 0, "affine8": 1, "uniform8": 1, "affine4": 2,
+                 "uniform4": 2}
+        if key not in table:
+            raise ValueError(f'unknown kv-cache-mode "{s}"; expected "fp16", "affine8" or '
+                             f'"affine4"')
+        return table[key]
+
+
+class KVCache:
+    """One layer's KV cache on a GPU (reference ``KVCache``, cache.rs:354)."""
+
+    def __init__(self, mode: int | str, n_kv_heads: int, head_dim: int, capacity: int = 0,
+                 group_size: int = 64, device=None):
+        torch = _torch()
+        if isinstance(mode, str):
+            mode = KVCacheMode.from_str(mode)
+        self.mode = mode
+        self.n_kv_heads = n_kv_heads
+        self.head_dim = head_dim
+        self.bits = {0: 16, 1: 8, 2: 4}[mode]
+        self.device = torch.device("cuda", torch.cuda.current_device() if device is None else
+                                   torch.device(device).index or 0)
+        h = _p()
+        _check(lib().qw_kv_create(mode, group_size, n_kv_heads, head_dim, capacity,
+                                  self.device.index, ctypes.byref(h)))
+        self._h = h
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            lib().qw_kv_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- state
+    @property
+    def offset(self) -> int:
+        v = _i()
+        _check(lib().qw_kv_offset(self._h, ctypes.byref(v)))
+        return v.value
+
+    @property
+    def capacity(self) -> int:
+        v = _i()
+        _check(lib().qw_kv_capacity(self._h, ctypes.byref(v)))
+        return v.value
+
+    def nbytes(self) -> int:
+        v = _i64()
+        _check(lib().qw_kv_nbytes(self._h, ctypes.byref(v)))
+        return v.value
+
+    def reserve(self, capacity: int) -> None:
+        _check(lib().qw_kv_reserve(self._h, capacity, _stream(self.device)))
+
+    # -- append / fetch
+    def update(self, keys, values) -> None:
+        k, v = _as3(keys, "keys"), _as3(values, "values")
+        if k.shape != v.shape or k.shape[0] != self.n_kv_heads or k.shape[2] != self.head_dim:
+            raise QwError(1, "update: keys/values must be [n_kv_heads, L, head_dim]")
+        _check(lib().qw_kv_update(self._h, k.data_ptr(), v.data_ptr(), k.shape[1],
+                                  _stream(self.device)))
+
+    def dequantize(self, start: int = 0, n: int | None = None):
+        torch = _torch()
+        n = self.offset - start if n is None else n
+        k = torch.empty((self.n_kv_heads, n, self.head_dim), dtype=torch.float16,
+                        device=self.device)
+        v = torch.empty_like(k)
+        _check(lib().qw_kv_dequantize(self._h, start, n, k.data_ptr(), v.data_ptr(),
+                                      _stream(self.device)))
+        return k.unsqueeze(0), v.unsqueeze(0)
+
+    def update_and_fetch(self, keys, values):
+        self.update(keys, values)
+        return self.dequantize(0, self.offset)
+
+    # -- attention
+    def _attn(self, q, keys, values, scale: float, causal: bool):
+        torch = _torch()
+        qq = _as3(q, "q")
+        hq, L, D = qq.shape
+        out = torch.empty_like(qq)
+        st = _stream(self.device)
+        if keys is None:
+            _check(lib().qw_kv_attention(self._h, qq.data_ptr(), hq, L, float(scale),
+                                         int(causal), out.data_ptr(), st))
+        else:
+            k, v = _as3(keys, "keys"), _as3(values, "values")
+            if k.shape != v.shape or k.shape[1] != L:
+                raise QwError(1, "attention: new keys/values must have q's row count")
+            _check(lib().qw_kv_update_and_attention(self._h, qq.data_ptr(), hq, L, k.data_ptr(),
+                                                    v.data_ptr(), float(scale), int(causal),
+                                                    out.data_ptr(), st))
+        return out.unsqueeze(0)
+
+    def update_and_attention(self, q, keys, values, scale: float):
+        """Append, then attend without a mask (reference ``update_and_turbo4_attention``)."""
+        return self._attn(q, keys, values, scale, False)
+
+    def update_and_causal_attention(self, q, keys, values, scale: float):
+        """Append, then bottom-right causal attention (``update_and_turbo4_causal_attention``)."""
+        return self._attn(q, keys, values, scale, True)
+
+    def attention(self, q, scale: float, causal: bool = False):
+        """Attend the cache as it is (fused prefix attention, cache.rs:3607)."""
+        return self._attn(q, None, None, scale, causal)
+
+    # -- lifecycle
+    def trim(self, n: int) -> int:
+        v = _i()
+        _check(lib().qw_kv_trim(self._h, n, ctypes.byref(v)))
+        return v.value
+
+    def snapshot_tensors(self) -> dict:
+        """Packed tensors in the reference layout (cache.rs:570-626)."""
+        torch = _torch()
+        n, H, D = self.offset, self.n_kv_heads, self.head_dim
+        st = _stream(self.device)
+        if self.mode == KVCacheMode.FP16:
+            k = torch.empty((H, n, D), dtype=torch.float16, device=self.device)
+            v = torch.empty_like(k)
+            _check(lib().qw_kv_export(self._h, k.data_ptr(), None, None, v.data_ptr(), None, None,
+                                      st))
+            return {"keys": k, "values": v}
+        w = D * self.bits // 32
+        t = {name: torch.empty((H, n, w), dtype=torch.int32, device=self.device)
+             for name in ("k_codes", "v_codes")}
+        for name in ("k_scales", "k_biases", "v_scales", "v_biases"):
+            t[name] = torch.empty((H, n, D // 64), dtype=torch.float16, device=self.device)
+        _check(lib().qw_kv_export(self._h, t["k_codes"].data_ptr(), t["k_scales"].data_ptr(),
+                                  t["k_biases"].data_ptr(), t["v_codes"].data_ptr(),
+                                  t["v_scales"].data_ptr(), t["v_biases"].data_ptr(), st))
+        return t
+
+    def restore_snapshot(self, tensors: dict) -> None:
+        st = _stream(self.device)
+        if self.mode == KVCacheMode.FP16:
+            k, v = tensors["keys"].contiguous(), tensors["values"].contiguous()
+            _check(lib().qw_kv_import(self._h, k.shape[1], k.data_ptr(), None, None, v.data_ptr(),
+                                      None, None, st))
+            return
+        t = {k2: v2.contiguous() for k2, v2 in tensors.items()}
+        n = t["k_codes"].shape[1]
+        _check(lib().qw_kv_import(self._h, n, t["k_codes"].data_ptr(), t["k_scales"].data_ptr(),
+                                  t["k_biases"].data_ptr(), t["v_codes"].data_ptr(),
+                                  t["v_scales"].data_ptr(), t["v_biases"].data_ptr(), st))
+
+
+def _kv_view(t, name: str):
+    """K/V [1, Hkv, T, D] or [Hkv, T, D], any head/row strides, unit last stride."""
+    torch = _torch()
+    if t.dim() == 4:
+        if t.shape[0] != 1:
+            raise QwError(1, f"{name}: batch must be 1")
+        t = t[0]
+    if t.dim() != 3 or t.dtype != torch.float16 or not t.is_cuda:
+        raise QwError(1, f"{name}: fp16 device tensor [1, Hkv, T, D] expected")
+    if t.stride(2) != 1:
+        t = t.contiguous()
+    return t
+
+
+def sparse_attention_with(q, k, v, lists, lengths, scale: float, parts: int = 0,
+                          waves: int = 0):
+    """D-LSA gathered read with launch knobs (dlsa_attention.rs:44)."""
+    torch = _torch()
+    qq = _as3(q, "q")
+    kk, vv = _kv_view(k, "k"), _kv_view(v, "v")
+    if kk.shape != vv.shape or kk.shape[2] != qq.shape[2]:
+        raise QwError(1, "sparse_attention: k/v shapes disagree with q")
+    if lists.dim() != 2 or lists.dtype != torch.int32 or lengths.dim() != 1 or \
+            lengths.dtype != torch.int32 or lists.shape[0] != qq.shape[1] or \
+            lengths.shape[0] != qq.shape[1]:
+        raise QwError(1, "sparse_attention: lists [L,W] i32 and lengths [L] i32 expected")
+    lists = lists.contiguous()
+    lengths = lengths.contiguous()
+    out = torch.empty_like(qq)
+    hq, L, D = qq.shape
+    hkv, T, _ = kk.shape
+    _check(lib().qw_dlsa_sparse_attention_with(
+        qq.data_ptr(), kk.data_ptr(), vv.data_ptr(), kk.stride(0), kk.stride(1), vv.stride(0),
+        vv.stride(1), lists.data_ptr(), lengths.data_ptr(), L, lists.shape[1], hq, hkv, D, T,
+        float(scale), parts, waves, out.data_ptr(), _stream(qq.device)))
+    return out.unsqueeze(0)
+
+
+def sparse_attention(q, k, v, lists, lengths, scale: float):
+    """D-LSA gathered read with the automatic launch policy (dlsa_attention.rs:31)."""
+    return sparse_attention_with(q, k, v, lists, lengths, scale, 0, 0)

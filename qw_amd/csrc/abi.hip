@@ -1,0 +1,195 @@
+// abi.hip - extern "C" entry points of libqwattn.so (declared in
+// include/qwattn.h). Each wrapper validates its handle and forwards to the
+// C++ KVCache / D-LSA implementation; no exception crosses the boundary.
+#include <new>
+
+#include "kv_cache.hpp"
+
+struct qw_kv_cache {
+    qw::KVCache impl;
+};
+
+namespace qw {
+int dlsa_sparse_attention(const void* q, const void* k, const void* v, int64_t k_head_stride,
+                          int64_t k_row_stride, int64_t v_head_stride, int64_t v_row_stride,
+                          const int32_t* lists, const int32_t* lengths, int n_rows, int width,
+                          int n_q_heads, int n_kv_heads, int head_dim, int n_keys, float scale,
+                          int parts, int waves, void* out, hipStream_t stream);
+}
+
+#define QW_HANDLE(c)                                                          \
+    do {                                                                      \
+        if (!(c)) {                                                           \
+            qw::set_error("null qw_kv_cache handle");                         \
+            return QW_ERR_INVALID_ARGUMENT;                                   \
+        }                                                                     \
+    } while (0)
+
+#define QW_GUARDED(expr)                                                      \
+    try {                                                                     \
+        return (expr);                                                        \
+    } catch (const std::bad_alloc&) {                                         \
+        qw::set_error("host allocation failed");                              \
+        return QW_ERR_OUT_OF_MEMORY;                                          \
+    } catch (...) {                                                           \
+        qw::set_error("unexpected C++ exception");                            \
+        return QW_ERR_STATE;                                                  \
+    }
+
+extern "C" {
+
+int qw_abi_version(void) { return QWATTN_ABI_VERSION; }
+
+const char* qw_last_error(void) { return qw::last_error(); }
+
+int qw_kv_create(int mode, int group_size, int n_kv_heads, int head_dim, int capacity,
+                 int device, qw_kv_cache** out) {
+    if (!out) {
+        qw::set_error("qw_kv_create: null out pointer");
+        return QW_ERR_INVALID_ARGUMENT;
+    }
+    *out = nullptr;
+    qw_kv_cache* c = new (std::nothrow) qw_kv_cache();
+    if (!c) {
+        qw::set_error("qw_kv_create: host allocation failed");
+        return QW_ERR_OUT_OF_MEMORY;
+    }
+    int rc;
+    try {
+        rc = c->impl.init(mode, group_size, n_kv_heads, head_dim, capacity, device);
+    } catch (...) {
+        rc = QW_ERR_STATE;
+        qw::set_error("qw_kv_create: unexpected C++ exception");
+    }
+    if (rc != QW_OK) {
+        c->impl.release();
+        delete c;
+        return rc;
+    }
+    *out = c;
+    return QW_OK;
+}
+
+int qw_kv_destroy(qw_kv_cache* cache) {
+    if (!cache) return QW_OK;
+    cache->impl.release();
+    delete cache;
+    return QW_OK;
+}
+
+int qw_kv_reserve(qw_kv_cache* cache, int capacity, void* stream) {
+    QW_HANDLE(cache);
+    QW_GUARDED(cache->impl.reserve(capacity, (hipStream_t)stream));
+}
+
+int qw_kv_offset(const qw_kv_cache* cache, int* offset) {
+    QW_HANDLE(cache);
+    if (!offset) {
+        qw::set_error("qw_kv_offset: null out pointer");
+        return QW_ERR_INVALID_ARGUMENT;
+    }
+    *offset = cache->impl.offset;
+    return QW_OK;
+}
+
+int qw_kv_capacity(const qw_kv_cache* cache, int* capacity) {
+    QW_HANDLE(cache);
+    if (!capacity) {
+        qw::set_error("qw_kv_capacity: null out pointer");
+        return QW_ERR_INVALID_ARGUMENT;
+    }
+    *capacity = cache->impl.cap;
+    return QW_OK;
+}
+
+int qw_kv_nbytes(const qw_kv_cache* cache, int64_t* nbytes) {
+    QW_HANDLE(cache);
+    if (!nbytes) {
+        qw::set_error("qw_kv_nbytes: null out pointer");
+        return QW_ERR_INVALID_ARGUMENT;
+    }
+    *nbytes = cache->impl.nbytes();
+    return QW_OK;
+}
+
+int qw_kv_update(qw_kv_cache* cache, const void* k_new, const void* v_new, int n_tokens,
+                 void* stream) {
+    QW_HANDLE(cache);
+    QW_GUARDED(cache->impl.update(k_new, v_new, n_tokens, (hipStream_t)stream));
+}
+
+int qw_kv_update_and_fetch(qw_kv_cache* cache, const void* k_new, const void* v_new,
+                           int n_tokens, void* k_out, void* v_out, void* stream) {
+    QW_HANDLE(cache);
+    QW_GUARDED(cache->impl.update_and_fetch(k_new, v_new, n_tokens, k_out, v_out,
+                                            (hipStream_t)stream));
+}
+
+int qw_kv_dequantize(const qw_kv_cache* cache, int start, int n, void* k_out, void* v_out,
+                     void* stream) {
+    QW_HANDLE(cache);
+    QW_GUARDED(cache->impl.dequantize(start, n, k_out, v_out, (hipStream_t)stream));
+}
+
+int qw_kv_update_and_attention(qw_kv_cache* cache, const void* q, int n_q_heads, int n_rows,
+                               const void* k_new, const void* v_new, float scale, int causal,
+                               void* out, void* stream) {
+    QW_HANDLE(cache);
+    QW_GUARDED(cache->impl.update_and_attention(q, n_q_heads, n_rows, k_new, v_new, scale,
+                                                causal != 0, out, (hipStream_t)stream));
+}
+
+int qw_kv_attention(qw_kv_cache* cache, const void* q, int n_q_heads, int n_rows, float scale,
+                    int causal, void* out, void* stream) {
+    QW_HANDLE(cache);
+    QW_GUARDED(cache->impl.attention(q, n_q_heads, n_rows, scale, causal != 0, out,
+                                     (hipStream_t)stream));
+}
+
+int qw_kv_trim(qw_kv_cache* cache, int n, int* trimmed) {
+    QW_HANDLE(cache);
+    const int m = cache->impl.trim(n);
+    if (trimmed) *trimmed = m;
+    return QW_OK;
+}
+
+int qw_kv_export(const qw_kv_cache* cache, void* k_codes, void* k_scales, void* k_biases,
+                 void* v_codes, void* v_scales, void* v_biases, void* stream) {
+    QW_HANDLE(cache);
+    QW_GUARDED(cache->impl.export_tensors(k_codes, k_scales, k_biases, v_codes, v_scales,
+                                          v_biases, (hipStream_t)stream));
+}
+
+int qw_kv_import(qw_kv_cache* cache, int n_tokens, const void* k_codes, const void* k_scales,
+                 const void* k_biases, const void* v_codes, const void* v_scales,
+                 const void* v_biases, void* stream) {
+    QW_HANDLE(cache);
+    QW_GUARDED(cache->impl.import_tensors(n_tokens, k_codes, k_scales, k_biases, v_codes,
+                                          v_scales, v_biases, (hipStream_t)stream));
+}
+
+int qw_dlsa_sparse_attention(const void* q, const void* k, const void* v, int64_t k_head_stride,
+                             int64_t k_row_stride, int64_t v_head_stride, int64_t v_row_stride,
+                             const int32_t* lists, const int32_t* lengths, int n_rows, int width,
+                             int n_q_heads, int n_kv_heads, int head_dim, int n_keys,
+                             float scale, void* out, void* stream) {
+    QW_GUARDED(qw::dlsa_sparse_attention(q, k, v, k_head_stride, k_row_stride, v_head_stride,
+                                         v_row_stride, lists, lengths, n_rows, width, n_q_heads,
+                                         n_kv_heads, head_dim, n_keys, scale, 0, 0, out,
+                                         (hipStream_t)stream));
+}
+
+int qw_dlsa_sparse_attention_with(const void* q, const void* k, const void* v,
+                                  int64_t k_head_stride, int64_t k_row_stride,
+                                  int64_t v_head_stride, int64_t v_row_stride,
+                                  const int32_t* lists, const int32_t* lengths, int n_rows,
+                                  int width, int n_q_heads, int n_kv_heads, int head_dim,
+                                  int n_keys, float scale, int parts, int waves, void* out,
+                                  void* stream) {
+    QW_GUARDED(qw::dlsa_sparse_attention(q, k, v, k_head_stride, k_row_stride, v_head_stride,
+                                         v_row_stride, lists, lengths, n_rows, width, n_q_heads,
+                                         n_kv_heads, head_dim, n_keys, scale, parts, waves, out,
+                                         (hipStream_t)stream));
+}
+
+}  // extern "C"

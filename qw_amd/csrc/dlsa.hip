@@ -1,0 +1,386 @@
+// dlsa.hip - D-LSA gathered sparse attention (the K2 read), gfx950.
+//
+// Reference: dlsa_attention::sparse_attention (crates/mlxcel-core/src/
+// dlsa_attention.rs:31-63) -> mlx_cxx::dlsa_sparse_attention
+// (crates/mlxcel-core/cpp/mlx_cxx_dlsa_attention.cpp:81-330 kernels,
+// :379-556 launch policy and validation). Contract: every query row r attends
+// over lists[r, 0:lengths[r]] of its KV head (shared by the G heads of the
+// group), entries outside [0, T) are skipped, a row with no valid entry is
+// zeros, fp32 softmax and accumulation, output in q's dtype (fp16 here),
+// K/V read in place through their strides.
+//
+// Design:
+//   grid (parts, rows, kv_heads), 4 waves a workgroup. A part is a contiguous
+//   slice of the row's list; waves take 16-entry tiles of it in turn.
+//   Q.K^T on MFMA (v_mfma_f32_16x16x32_f16): A = 16 gathered K rows (each
+//   lane 16 contiguous bytes of its row per MFMA), B = the G query heads.
+//   Probabilities go through LDS (one 16x16 fp32 tile a wave) and P.V runs on
+//   the VALU with each lane owning D/64 contiguous dims of every head, so a
+//   gathered V row is one coalesced 512-byte wave load.
+//   Online softmax in the exp2 domain across tiles; the waves merge through
+//   LDS; split-K parts write fp32 partials merged by a second kernel.
+#include <algorithm>
+
+#include "kv_cache.hpp"
+
+namespace qw {
+
+struct DlsaArgs {
+    const f16* q;
+    const f16* k;
+    const f16* v;
+    int64_t khs, krs, vhs, vrs;
+    const int32_t* lists;
+    const int32_t* lengths;
+    f16* out;
+    float* part_o;   // [L][Hq][parts][D]
+    float2* part_ml; // [L][Hq][parts]
+    int L, W, hq, hkv, G, T, parts;
+    float scale2;    // scale * log2(e)
+};
+
+constexpr int kDlsaNT = 2;  // tiles per batch a wave keeps in flight
+
+template <int D, int GMAX>
+__global__ __launch_bounds__(256) void dlsa_kernel(DlsaArgs a) {
+    constexpr int NM = D / 32;
+    constexpr int DPV = D / 64;  // dims a lane owns in P.V
+    const int part = blockIdx.x, r = blockIdx.y, h = blockIdx.z;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int G = a.G;
+    int len = a.lengths[r];
+    len = len < 0 ? 0 : (len > a.W ? a.W : len);
+    const int e_begin = (int)((int64_t)len * part / a.parts);
+    const int e_end = (int)((int64_t)len * (part + 1) / a.parts);
+    const int32_t* list = a.lists + (int64_t)r * a.W;
+
+    // Q operand: column r16 = head h*G + r16 (zero past G), dims 32m + 8g..+7.
+    half8 qop[NM];
+    {
+        const bool ok = r16 < G;
+        const f16* qrow = a.q + ((int64_t)(h * G + (ok ? r16 : 0)) * a.L + r) * D;
+#pragma unroll
+        for (int m = 0; m < NM; m++) qop[m] = ok ? *(const half8*)(qrow + 32 * m + 8 * g) : half8{};
+    }
+
+    __shared__ float sm_p[4][16][17];  // [wave][entry][head], padded
+    float mrun = -INFINITY;             // running max (log2 domain), column r16
+    float lrun = 0.0f;                  // running sum, this lane's share
+    float acc[GMAX][DPV];
+#pragma unroll
+    for (int hh = 0; hh < GMAX; hh++)
+#pragma unroll
+        for (int d = 0; d < DPV; d++) acc[hh][d] = 0.0f;
+
+    const int n_tiles = (e_end - e_begin + 15) / 16;
+    for (int t0 = wave; t0 < n_tiles; t0 += 4 * kDlsaNT) {
+        // ---- gather loads for up to NT tiles
+        u32x4 kc[kDlsaNT][NM];
+        u32x2 vr[kDlsaNT][16];
+        int key_a[kDlsaNT];  // the key of list entry tile*16 + r16 (A-operand row)
+        bool ok_a[kDlsaNT];
+#pragma unroll
+        for (int b = 0; b < kDlsaNT; b++) {
+            const int tile = t0 + 4 * b;
+            const int e = e_begin + 16 * tile + r16;
+            int key = -1;
+            if (tile < n_tiles && e < e_end) key = list[e];
+            ok_a[b] = key >= 0 && key < a.T;
+            key_a[b] = ok_a[b] ? key : 0;
+            const u32x4* krow = (const u32x4*)(a.k + h * a.khs + (int64_t)key_a[b] * a.krs);
+#pragma unroll
+            for (int m = 0; m < NM; m++) kc[b][m] = krow[4 * m + g];
+        }
+#pragma unroll
+        for (int b = 0; b < kDlsaNT; b++) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                // V row of tile entry i: every lane reads its DPV dims.
+                const int key = __builtin_amdgcn_readlane(key_a[b], i);
+                const f16* vrow = a.v + h * a.vhs + (int64_t)key * a.vrs + lane * DPV;
+                if constexpr (DPV == 4)
+                    vr[b][i] = *(const u32x2*)vrow;
+                else if constexpr (DPV == 2)
+                    vr[b][i] = u32x2{*(const uint32_t*)vrow, 0u};
+                else
+                    vr[b][i] = u32x2{(uint32_t) * (const uint16_t*)vrow, 0u};
+            }
+        }
+        // ---- scores: S^T tile, lane holds entries 4g+i for head r16
+        float s[kDlsaNT][4];
+        float bmax = -INFINITY;
+#pragma unroll
+        for (int b = 0; b < kDlsaNT; b++) {
+            float4v sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int m = 0; m < NM; m++)
+                sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(kc[b][m]), qop[m], sacc, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const bool ok = __shfl(ok_a[b] ? 1 : 0, 4 * g + i) != 0 && r16 < G;
+                s[b][i] = ok ? sacc[i] * a.scale2 : -INFINITY;
+                bmax = fmaxf(bmax, s[b][i]);
+            }
+        }
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+        const float mnew = fmaxf(mrun, bmax);
+        const float mref = mnew == -INFINITY ? 0.0f : mnew;
+        const float alpha = mrun == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mrun - mref);
+        mrun = mnew;
+        lrun *= alpha;
+        // Rescale the P.V accumulators: head hh's factor lives in column hh.
+#pragma unroll
+        for (int hh = 0; hh < GMAX; hh++) {
+            const float f = __shfl(alpha, hh);
+#pragma unroll
+            for (int d = 0; d < DPV; d++) acc[hh][d] *= f;
+        }
+#pragma unroll
+        for (int b = 0; b < kDlsaNT; b++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float p = __builtin_amdgcn_exp2f(s[b][i] - mref);
+                lrun += p;
+                sm_p[wave][4 * g + i][r16] = p;
+            }
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                float vf[DPV];
+                if constexpr (DPV == 4) {
+                    const half4v hv = __builtin_bit_cast(half4v, vr[b][i]);
+#pragma unroll
+                    for (int d = 0; d < 4; d++) vf[d] = (float)hv[d];
+                } else if constexpr (DPV == 2) {
+                    const half2v hv = __builtin_bit_cast(half2v, vr[b][i].x);
+                    vf[0] = (float)hv.x;
+                    vf[1] = (float)hv.y;
+                } else {
+                    vf[0] = (float)__builtin_bit_cast(f16, (uint16_t)vr[b][i].x);
+                }
+#pragma unroll
+                for (int hh = 0; hh < GMAX; hh++) {
+                    const float p = sm_p[wave][i][hh];
+#pragma unroll
+                    for (int d = 0; d < DPV; d++) acc[hh][d] = __builtin_fmaf(p, vf[d], acc[hh][d]);
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+    lrun += __shfl_xor(lrun, 16);
+    lrun += __shfl_xor(lrun, 32);
+
+    // ---- merge the waves: (m, l) per head, then the accumulators
+    __shared__ float2 sm_ml[4][16];
+    __shared__ float sm_acc[2][GMAX][D];
+    if (g == 0) sm_ml[wave][r16] = float2{mrun, lrun};
+    __syncthreads();
+    float Mh[GMAX], Lh[GMAX];
+#pragma unroll
+    for (int hh = 0; hh < GMAX; hh++) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; w++) M = fmaxf(M, sm_ml[w][hh].x);
+        float L = 0.0f, own = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float mw = sm_ml[w][hh].x;
+            const float f = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+            L += f * sm_ml[w][hh].y;
+            if (w == wave) own = f;
+        }
+        Mh[hh] = M;
+        Lh[hh] = L;
+#pragma unroll
+        for (int d = 0; d < DPV; d++) acc[hh][d] *= own;
+    }
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int hh = 0; hh < GMAX; hh++)
+            if (hh < G)
+#pragma unroll
+                for (int d = 0; d < DPV; d++) sm_acc[buf][hh][lane * DPV + d] = acc[hh][d];
+    };
+    auto add = [&](int buf) {
+#pragma unroll
+        for (int hh = 0; hh < GMAX; hh++)
+            if (hh < G)
+#pragma unroll
+                for (int d = 0; d < DPV; d++) acc[hh][d] += sm_acc[buf][hh][lane * DPV + d];
+    };
+    if (wave >= 2) store(wave - 2);
+    __syncthreads();
+    if (wave < 2) add(wave);
+    __syncthreads();
+    if (wave == 1) store(0);
+    __syncthreads();
+    if (wave != 0) return;
+    add(0);
+#pragma unroll
+    for (int hh = 0; hh < GMAX; hh++) {
+        if (hh >= G) continue;
+        const int qh = h * G + hh;
+        if (a.parts == 1) {
+            const float inv = Lh[hh] > 0.0f ? 1.0f / Lh[hh] : 0.0f;
+            f16* dst = a.out + ((int64_t)qh * a.L + r) * D + lane * DPV;
+#pragma unroll
+            for (int d = 0; d < DPV; d++) dst[d] = (f16)(acc[hh][d] * inv);
+        } else {
+            const int64_t pr = ((int64_t)r * a.hq + qh) * a.parts + part;
+            float* dst = a.part_o + pr * D + lane * DPV;
+#pragma unroll
+            for (int d = 0; d < DPV; d++) dst[d] = acc[hh][d];
+            if (lane == 0) a.part_ml[pr] = float2{Mh[hh], Lh[hh]};
+        }
+    }
+}
+
+// out[qh, r] = sum_p e^(m_p - M) O_p / sum_p e^(m_p - M) l_p (m in the log2 domain).
+__global__ __launch_bounds__(256) void dlsa_merge_kernel(const float* __restrict__ part_o,
+                                                         const float2* __restrict__ part_ml,
+                                                         int parts, int D, int L, int hq,
+                                                         f16* __restrict__ out) {
+    const int qh = blockIdx.x, r = blockIdx.y;
+    const int64_t base = ((int64_t)r * hq + qh) * parts;
+    float M = -INFINITY;
+    for (int p = 0; p < parts; p++) M = fmaxf(M, part_ml[base + p].x);
+    for (int d = threadIdx.x; d < D; d += blockDim.x) {
+        float Ls = 0.0f, O = 0.0f;
+#pragma unroll 8
+        for (int p = 0; p < parts; p++) {
+            const float2 ml = part_ml[base + p];
+            const float f = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - M);
+            Ls += f * ml.y;
+            O += f * part_o[(base + p) * D + d];
+        }
+        out[((int64_t)qh * L + r) * D + d] = (f16)(Ls > 0.0f ? O / Ls : 0.0f);
+    }
+}
+
+// Split-K workspace shared by the D-LSA calls of a device (grown on demand).
+struct DlsaWorkspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+static DlsaWorkspace g_ws[64];
+
+static int dlsa_workspace(int device, size_t need, void** out) {
+    if (device < 0 || device >= 64) {
+        set_error("dlsa: device ordinal out of range");
+        return QW_ERR_INVALID_ARGUMENT;
+    }
+    DlsaWorkspace& w = g_ws[device];
+    if (need > w.bytes) {
+        if (w.ptr) {
+            QW_HIP_CHECK(hipDeviceSynchronize());
+            (void)hipFree(w.ptr);
+            w.ptr = nullptr;
+            w.bytes = 0;
+        }
+        const size_t nb = std::max(need, (size_t)1 << 20);
+        if (hipMalloc(&w.ptr, nb) != hipSuccess) {
+            (void)hipGetLastError();
+            w.ptr = nullptr;
+            set_error("dlsa: workspace hipMalloc failed");
+            return QW_ERR_OUT_OF_MEMORY;
+        }
+        w.bytes = nb;
+    }
+    *out = w.ptr;
+    return QW_OK;
+}
+
+// Launch policy (the reference's auto_parts, mlx_cxx_dlsa_attention.cpp:379-400,
+// re-derived for 256 CUs): one pass when rows x kv_heads alone give >= 512
+// workgroups, else split each list so that about 1024 workgroups run, keeping
+// at least 16 entries (one tile) a part and at most 128 parts.
+static int auto_parts(int units, int width) {
+    if (units >= 512) return 1;
+    int parts = (1024 + units - 1) / units;
+    parts = std::min(parts, std::max(1, width / 16));
+    return std::max(1, std::min(parts, 128));
+}
+
+int dlsa_sparse_attention(const void* q, const void* k, const void* v, int64_t khs, int64_t krs,
+                          int64_t vhs, int64_t vrs, const int32_t* lists, const int32_t* lengths,
+                          int n_rows, int width, int n_q_heads, int n_kv_heads, int head_dim,
+                          int n_keys, float scale, int parts, int waves, void* out,
+                          hipStream_t stream) {
+    QW_REQUIRE(q && k && v && lists && lengths && out, QW_ERR_INVALID_ARGUMENT,
+               "dlsa_sparse_attention: null pointer");
+    QW_REQUIRE(n_kv_heads > 0 && n_q_heads > 0 && n_q_heads % n_kv_heads == 0 && n_keys > 0 &&
+                   n_rows > 0,
+               QW_ERR_INVALID_ARGUMENT, "dlsa_sparse_attention: bad head or length geometry");
+    const int G = n_q_heads / n_kv_heads;
+    QW_REQUIRE(G <= 16, QW_ERR_INVALID_ARGUMENT,
+               "dlsa_sparse_attention: at most 16 query heads per KV head");
+    QW_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256, QW_ERR_INVALID_ARGUMENT,
+               "dlsa_sparse_attention: head dim must be 64, 128 or 256");
+    QW_REQUIRE(width > 0, QW_ERR_INVALID_ARGUMENT, "dlsa_sparse_attention: empty list width");
+    QW_REQUIRE(parts >= 0 && waves >= 0 && waves <= 16, QW_ERR_INVALID_ARGUMENT,
+               "dlsa_sparse_attention: bad launch knobs");
+    // 16-byte row loads: row starts and strides must keep 8-element alignment.
+    QW_REQUIRE(((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0 && khs % 8 == 0 &&
+                   krs % 8 == 0 && vhs % 8 == 0 && vrs % 8 == 0 && ((uintptr_t)q % 16) == 0,
+               QW_ERR_UNSUPPORTED,
+               "dlsa_sparse_attention: K/V/q must be 16-byte aligned with strides % 8 == 0");
+    int dev = 0;
+    QW_HIP_CHECK(hipGetDevice(&dev));
+    if (parts <= 0) parts = auto_parts(n_rows * n_kv_heads, width);
+    parts = std::max(1, std::min(parts, 128));
+    DlsaArgs a;
+    a.q = (const f16*)q;
+    a.k = (const f16*)k;
+    a.v = (const f16*)v;
+    a.khs = khs;
+    a.krs = krs;
+    a.vhs = vhs;
+    a.vrs = vrs;
+    a.lists = lists;
+    a.lengths = lengths;
+    a.out = (f16*)out;
+    a.part_o = nullptr;
+    a.part_ml = nullptr;
+    a.L = n_rows;
+    a.W = width;
+    a.hq = n_q_heads;
+    a.hkv = n_kv_heads;
+    a.G = G;
+    a.T = n_keys;
+    a.parts = parts;
+    a.scale2 = scale * kLog2e;
+    if (parts > 1) {
+        const size_t no = (size_t)n_rows * n_q_heads * parts;
+        void* ws = nullptr;
+        int rc = dlsa_workspace(dev, no * head_dim * sizeof(float) + no * sizeof(float2), &ws);
+        if (rc) return rc;
+        a.part_o = (float*)ws;
+        a.part_ml = (float2*)((char*)ws + no * head_dim * sizeof(float));
+    }
+    dim3 grid(parts, n_rows, n_kv_heads);
+#define QW_DLSA_LAUNCH(DD, GM) \
+    hipLaunchKernelGGL((dlsa_kernel<DD, GM>), grid, dim3(256), 0, stream, a)
+    if (head_dim == 256) {
+        if (G <= 8) QW_DLSA_LAUNCH(256, 8); else QW_DLSA_LAUNCH(256, 16);
+    } else if (head_dim == 128) {
+        if (G <= 8) QW_DLSA_LAUNCH(128, 8); else QW_DLSA_LAUNCH(128, 16);
+    } else {
+        if (G <= 8) QW_DLSA_LAUNCH(64, 8); else QW_DLSA_LAUNCH(64, 16);
+    }
+#undef QW_DLSA_LAUNCH
+    QW_HIP_CHECK(hipGetLastError());
+    if (parts > 1) {
+        hipLaunchKernelGGL(dlsa_merge_kernel, dim3(n_q_heads, n_rows), dim3(head_dim), 0, stream,
+                           a.part_o, a.part_ml, parts, head_dim, n_rows, n_q_heads, (f16*)out);
+        QW_HIP_CHECK(hipGetLastError());
+    }
+    (void)waves;  // one 4-wave workgroup shape; the knob is accepted for API parity
+    return QW_OK;
+}
+
+}  // namespace qw

@@ -1,0 +1,638 @@
+// kv_cache.hip - KV cache lifecycle, quantize-on-append, dequantize and
+// snapshot kernels for gfx950.
+//
+// Reference behaviour followed (cr0sh/qw):
+//   KVCache::new_with_mode / update / update_and_fetch / trim / nbytes /
+//   snapshot tensors: crates/mlxcel-core/src/cache.rs:526, :922-1157,
+//   :2251-2300, :2709-2834, :3063, :570-626.
+//   Affine codec (MLX `quantize` / `dequantize`, group 64):
+//   crates/mlxcel-core/cpp/mlx_cxx_bridge.cpp:2991-3040, :6347-6393, at the
+//   seam crates/mlxcel-core/src/cache/batch_quant.rs:109-158.
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+
+#include "kv_cache.hpp"
+
+namespace qw {
+
+static thread_local std::string g_last_error;
+void set_error(const std::string& msg) { g_last_error = msg; }
+const char* last_error() { return g_last_error.c_str(); }
+
+// --------------------------------------------------------------- sizes
+
+size_t KVCache::k_data_bytes(int c) const { return (size_t)hkv * c * D * bits / 8; }
+size_t KVCache::k_param_bytes(int c) const {
+    return affine() ? (size_t)hkv * c * (D / kGroup) * 4 : 0;
+}
+size_t KVCache::v_data_bytes(int c) const { return (size_t)hkv * c * D * bits / 8; }
+size_t KVCache::v_param_bytes(int c) const {
+    return affine() ? (size_t)hkv * (c / 8) * (D / kGroup) * 32 : 0;
+}
+
+int64_t KVCache::nbytes() const {
+    return (int64_t)(k_data_bytes(cap) + k_param_bytes(cap) + v_data_bytes(cap) +
+                     v_param_bytes(cap));
+}
+
+static int round_cap(int capacity) {
+    // The reference grows its buffers in steps of 256 tokens (cache.rs `step`).
+    const int step = 256;
+    return std::max(step, (capacity + step - 1) / step * step);
+}
+
+static int alloc_zero(void** p, size_t bytes) {
+    *p = nullptr;
+    if (bytes == 0) return QW_OK;
+    if (hipMalloc(p, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        *p = nullptr;
+        set_error("hipMalloc of " + std::to_string(bytes) + " bytes failed");
+        return QW_ERR_OUT_OF_MEMORY;
+    }
+    // Zeroed so that rows past `offset` dequantize to finite zeros: masked keys
+    // still pass through the P.V MFMA with weight 0.
+    QW_HIP_CHECK(hipMemset(*p, 0, bytes));
+    return QW_OK;
+}
+
+int KVCache::init(int mode_, int group_size, int n_kv_heads, int head_dim, int capacity,
+                  int device_) {
+    QW_REQUIRE(mode_ == QW_KV_FP16 || mode_ == QW_KV_AFFINE8 || mode_ == QW_KV_AFFINE4,
+               QW_ERR_INVALID_ARGUMENT, "qw_kv_create: unknown mode");
+    QW_REQUIRE(n_kv_heads > 0 && capacity >= 0 && head_dim > 0, QW_ERR_INVALID_ARGUMENT,
+               "qw_kv_create: n_kv_heads, head_dim must be > 0 and capacity >= 0");
+    if (mode_ != QW_KV_FP16) {
+        QW_REQUIRE(group_size == kGroup, QW_ERR_UNSUPPORTED,
+                   "qw_kv_create: affine modes use group_size 64");
+        QW_REQUIRE(head_dim == 256 || head_dim == 128, QW_ERR_UNSUPPORTED,
+                   "qw_kv_create: affine modes support head_dim 128 or 256");
+    } else {
+        QW_REQUIRE(head_dim == 256 || head_dim == 128, QW_ERR_UNSUPPORTED,
+                   "qw_kv_create: fp16 mode supports head_dim 128 or 256");
+    }
+    mode = mode_;
+    bits = mode_ == QW_KV_AFFINE4 ? 4 : (mode_ == QW_KV_AFFINE8 ? 8 : 16);
+    D = head_dim;
+    hkv = n_kv_heads;
+    device = device_;
+    offset = 0;
+    cap = 0;
+    DeviceGuard dg(device);
+    QW_REQUIRE(dg.ok, QW_ERR_HIP, "qw_kv_create: hipSetDevice failed");
+    return reserve(capacity, nullptr);
+}
+
+int KVCache::release() {
+    DeviceGuard dg(device);
+    (void)hipDeviceSynchronize();
+    void* ptrs[5] = {k_data, (void*)k_params, v_data, (void*)v_params, ws};
+    for (void* p : ptrs)
+        if (p) (void)hipFree(p);
+    k_data = v_data = ws = nullptr;
+    k_params = v_params = nullptr;
+    ws_bytes = 0;
+    cap = offset = 0;
+    return QW_OK;
+}
+
+int KVCache::reserve(int capacity, hipStream_t stream) {
+    const int nc = round_cap(capacity);
+    if (nc <= cap) return QW_OK;
+    DeviceGuard dg(device);
+    void *nk = nullptr, *nkp = nullptr, *nv = nullptr, *nvp = nullptr;
+    int rc;
+    if ((rc = alloc_zero(&nk, k_data_bytes(nc))) || (rc = alloc_zero(&nkp, k_param_bytes(nc))) ||
+        (rc = alloc_zero(&nv, v_data_bytes(nc))) || (rc = alloc_zero(&nvp, v_param_bytes(nc)))) {
+        void* ps[4] = {nk, nkp, nv, nvp};
+        for (void* p : ps)
+            if (p) (void)hipFree(p);
+        return rc;
+    }
+    if (cap > 0) {
+        // Per head, the first `cap` rows (K, K params) or cap/8 blocks (V, V
+        // params) move to the head's start in the new buffers.
+        const size_t kr = (size_t)D * bits / 8, kpr = affine() ? (size_t)(D / kGroup) * 4 : 0;
+        const size_t vb = (size_t)D * bits, vpb = affine() ? (size_t)(D / kGroup) * 32 : 0;
+        for (int h = 0; h < hkv; h++) {
+            QW_HIP_CHECK(hipMemcpyAsync((char*)nk + h * (size_t)nc * kr,
+                                        (char*)k_data + h * (size_t)cap * kr, cap * kr,
+                                        hipMemcpyDeviceToDevice, stream));
+            QW_HIP_CHECK(hipMemcpyAsync((char*)nv + h * (size_t)(nc / 8) * vb,
+                                        (char*)v_data + h * (size_t)(cap / 8) * vb,
+                                        (cap / 8) * vb, hipMemcpyDeviceToDevice, stream));
+            if (affine()) {
+                QW_HIP_CHECK(hipMemcpyAsync((char*)nkp + h * (size_t)nc * kpr,
+                                            (char*)k_params + h * (size_t)cap * kpr, cap * kpr,
+                                            hipMemcpyDeviceToDevice, stream));
+                QW_HIP_CHECK(hipMemcpyAsync((char*)nvp + h * (size_t)(nc / 8) * vpb,
+                                            (char*)v_params + h * (size_t)(cap / 8) * vpb,
+                                            (cap / 8) * vpb, hipMemcpyDeviceToDevice, stream));
+            }
+        }
+        QW_HIP_CHECK(hipStreamSynchronize(stream));
+        void* old[4] = {k_data, (void*)k_params, v_data, (void*)v_params};
+        for (void* p : old)
+            if (p) (void)hipFree(p);
+    }
+    k_data = nk;
+    k_params = (uint32_t*)nkp;
+    v_data = nv;
+    v_params = (uint32_t*)nvp;
+    cap = nc;
+    return QW_OK;
+}
+
+int KVCache::ensure_workspace(size_t bytes) {
+    if (bytes <= ws_bytes) return QW_OK;
+    DeviceGuard dg(device);
+    if (ws) {
+        QW_HIP_CHECK(hipDeviceSynchronize());
+        (void)hipFree(ws);
+        ws = nullptr;
+        ws_bytes = 0;
+    }
+    const size_t nb = std::max(bytes, (size_t)1 << 20);
+    if (hipMalloc(&ws, nb) != hipSuccess) {
+        (void)hipGetLastError();
+        ws = nullptr;
+        set_error("workspace hipMalloc failed");
+        return QW_ERR_OUT_OF_MEMORY;
+    }
+    ws_bytes = nb;
+    return QW_OK;
+}
+
+int KVCache::trim(int n) {
+    // cache.rs:2251: clamp to the cached length; buffers keep their rows, the
+    // next append overwrites them.
+    const int m = std::min(n, offset);
+    if (m <= 0) return 0;
+    offset -= m;
+    return m;
+}
+
+// ------------------------------------------------ quantize-on-append (A.1)
+//
+// One workgroup (4 waves) per (KV head, 8-token V block touched by the
+// append). Each wave quantizes whole rows (one token of K or V): a lane
+// holds D/64 consecutive dims, a 64-dim group is 64/(D/64) lanes and its
+// min/max are wave shuffles. The group math is MLX's, in fp32 with IEEE
+// division and rint (ties to even):
+//   scale = max((max - min) / n_bins, 1e-7), negated unless |min| > |max|
+//   edge = larger-magnitude extreme; q0 = rint(edge / scale)
+//   if q0 != 0: scale = edge / q0, bias = edge, else bias = 0
+//   code = clamp(rint((w - bias) / scale), 0, n_bins)
+// Codes go through LDS so the V block words (8 keys per dim) are assembled
+// by one thread each: no two threads write the same word.
+
+template <int D>
+__device__ inline void quantize_row(const f16* __restrict__ src, int bits, uint8_t* lds_codes,
+                                    half2v* sb_out /* [D/64] (scale, bias) */) {
+    constexpr int VPL = D / 64;         // values per lane
+    constexpr int LPG = kGroup / VPL;   // lanes per group
+    const int lane = threadIdx.x & 63;
+    float x[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; i++) x[i] = (float)src[lane * VPL + i];
+    float mx = x[0], mn = x[0];
+#pragma unroll
+    for (int i = 1; i < VPL; i++) {
+        mx = mx < x[i] ? x[i] : mx;
+        mn = x[i] < mn ? x[i] : mn;
+    }
+#pragma unroll
+    for (int off = 1; off < LPG; off <<= 1) {
+        const float omx = __shfl_xor(mx, off);
+        const float omn = __shfl_xor(mn, off);
+        mx = mx < omx ? omx : mx;
+        mn = omn < mn ? omn : mn;
+    }
+    const float n_bins = (float)((1 << bits) - 1);
+    const float eps = 1e-7f;
+    const bool neg_side = fabsf(mn) > fabsf(mx);
+    float scale = (mx - mn) / n_bins;
+    scale = scale < eps ? eps : scale;
+    scale = neg_side ? scale : -scale;
+    const float edge = neg_side ? mn : mx;
+    const float q0 = __builtin_rintf(edge / scale);
+    float bias = 0.0f;
+    if (q0 != 0.0f) {
+        scale = edge / q0;
+        bias = edge;
+    }
+#pragma unroll
+    for (int i = 0; i < VPL; i++) {
+        float c = __builtin_rintf((x[i] - bias) / scale);
+        c = c < 0.0f ? 0.0f : (c > n_bins ? n_bins : c);
+        lds_codes[lane * VPL + i] = (uint8_t)c;
+    }
+    if ((lane % LPG) == 0) {
+        half2v sb;
+        sb.x = (f16)scale;
+        sb.y = (f16)bias;
+        sb_out[lane / LPG] = sb;
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void append_affine_kernel(
+    const f16* __restrict__ k_new, const f16* __restrict__ v_new, int n_tokens, int t_old,
+    int bits, int cap, uint32_t* __restrict__ k_codes, uint32_t* __restrict__ k_params,
+    uint32_t* __restrict__ v_codes, f16* __restrict__ v_params) {
+    constexpr int NG = D / kGroup;
+    __shared__ uint8_t kc[8][D];
+    __shared__ uint8_t vc[8][D];
+    __shared__ half2v ksb[8][NG];
+    __shared__ half2v vsb[8][NG];
+    const int h = blockIdx.y;
+    const int blk = t_old / 8 + blockIdx.x;
+    const int wave = threadIdx.x >> 6;
+    const int t_end = t_old + n_tokens;
+    for (int k = wave; k < 8; k += 4) {
+        const int t = blk * 8 + k;
+        if (t < t_old || t >= t_end) continue;
+        const int64_t src = ((int64_t)h * n_tokens + (t - t_old)) * D;
+        quantize_row<D>(k_new + src, bits, kc[k], ksb[k]);
+        quantize_row<D>(v_new + src, bits, vc[k], vsb[k]);
+    }
+    __syncthreads();
+    // K: row-major MLX packing, words of 32/bits codes LSB-first.
+    const int epw = 32 / bits;
+    const int nw = D / epw;
+    for (int i = threadIdx.x; i < 8 * nw; i += blockDim.x) {
+        const int k = i / nw, w = i % nw;
+        const int t = blk * 8 + k;
+        if (t < t_old || t >= t_end) continue;
+        uint32_t word = 0;
+        for (int e = 0; e < epw; e++) word |= (uint32_t)kc[k][w * epw + e] << (e * bits);
+        k_codes[((int64_t)h * cap + t) * nw + w] = word;
+    }
+    for (int i = threadIdx.x; i < 8 * NG; i += blockDim.x) {
+        const int k = i / NG, g = i % NG;
+        const int t = blk * 8 + k;
+        if (t < t_old || t >= t_end) continue;
+        k_params[((int64_t)h * cap + t) * NG + g] = __builtin_bit_cast(uint32_t, ksb[k][g]);
+        f16* vp = v_params + (((int64_t)h * (cap / 8) + blk) * NG + g) * 16;
+        vp[k] = vsb[k][g].x;
+        vp[8 + k] = vsb[k][g].y;
+    }
+    // V: one thread per dim assembles the block word(s), keeping the codes of
+    // slots outside this append (earlier tokens of a partly filled block).
+    const int bw = D * bits / 32;  // words per V block
+    uint32_t* vb = v_codes + ((int64_t)h * (cap / 8) + blk) * bw;
+    for (int d = threadIdx.x; d < D; d += blockDim.x) {
+        const int p = v_phys_dim(d, D, bits);
+        if (bits == 4) {
+            uint32_t word = vb[p];
+            for (int k = 0; k < 8; k++) {
+                const int t = blk * 8 + k;
+                if (t < t_old || t >= t_end) continue;
+                const int sh = 4 * v4_nibble_pos(k);
+                word = (word & ~(0xFu << sh)) | ((uint32_t)vc[k][d] << sh);
+            }
+            vb[p] = word;
+        } else {
+            uint32_t w0 = vb[2 * p], w1 = vb[2 * p + 1];
+            for (int k = 0; k < 8; k++) {
+                const int t = blk * 8 + k;
+                if (t < t_old || t >= t_end) continue;
+                const int sh = 8 * (k & 3);
+                if (k < 4)
+                    w0 = (w0 & ~(0xFFu << sh)) | ((uint32_t)vc[k][d] << sh);
+                else
+                    w1 = (w1 & ~(0xFFu << sh)) | ((uint32_t)vc[k][d] << sh);
+            }
+            vb[2 * p] = w0;
+            vb[2 * p + 1] = w1;
+        }
+    }
+}
+
+// fp16 mode append: K rows copied, V scattered into 8-key blocks.
+template <int D>
+__global__ __launch_bounds__(256) void append_fp16_kernel(const f16* __restrict__ k_new,
+                                                          const f16* __restrict__ v_new,
+                                                          int n_tokens, int t_old, int cap,
+                                                          f16* __restrict__ k_data,
+                                                          f16* __restrict__ v_data) {
+    const int h = blockIdx.y;
+    const int64_t n = (int64_t)n_tokens * D;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int t = (int)(i / D) + t_old, d = (int)(i % D);
+        const f16 kv = k_new[(int64_t)h * n + i];
+        const f16 vv = v_new[(int64_t)h * n + i];
+        k_data[((int64_t)h * cap + t) * D + d] = kv;
+        v_data[(((int64_t)h * (cap / 8) + t / 8) * D + v_phys_dim(d, D, 16)) * 8 + (t & 7)] = vv;
+    }
+}
+
+int KVCache::update(const void* k_new, const void* v_new, int n_tokens, hipStream_t stream) {
+    QW_REQUIRE(n_tokens >= 0, QW_ERR_INVALID_ARGUMENT, "update: n_tokens must be >= 0");
+    if (n_tokens == 0) return QW_OK;
+    QW_REQUIRE(k_new && v_new, QW_ERR_INVALID_ARGUMENT, "update: null K/V pointer");
+    DeviceGuard dg(device);
+    QW_REQUIRE(dg.ok, QW_ERR_HIP, "update: hipSetDevice failed");
+    const int need = offset + n_tokens;
+    if (need > cap) {
+        // Geometric growth keeps appends amortized O(1) per token.
+        int rc = reserve(std::max(need, cap + cap / 2), stream);
+        if (rc) return rc;
+    }
+    if (affine()) {
+        const int nblk = (offset + n_tokens - 1) / 8 - offset / 8 + 1;
+        dim3 grid(nblk, hkv);
+        if (D == 256)
+            hipLaunchKernelGGL(append_affine_kernel<256>, grid, dim3(256), 0, stream,
+                               (const f16*)k_new, (const f16*)v_new, n_tokens, offset, bits, cap,
+                               (uint32_t*)k_data, k_params, (uint32_t*)v_data, (f16*)v_params);
+        else
+            hipLaunchKernelGGL(append_affine_kernel<128>, grid, dim3(256), 0, stream,
+                               (const f16*)k_new, (const f16*)v_new, n_tokens, offset, bits, cap,
+                               (uint32_t*)k_data, k_params, (uint32_t*)v_data, (f16*)v_params);
+    } else {
+        const int64_t n = (int64_t)n_tokens * D;
+        dim3 grid((unsigned)std::min<int64_t>((n + 255) / 256, 1024), hkv);
+        if (D == 256)
+            hipLaunchKernelGGL(append_fp16_kernel<256>, grid, dim3(256), 0, stream,
+                               (const f16*)k_new, (const f16*)v_new, n_tokens, offset, cap,
+                               (f16*)k_data, (f16*)v_data);
+        else
+            hipLaunchKernelGGL(append_fp16_kernel<128>, grid, dim3(256), 0, stream,
+                               (const f16*)k_new, (const f16*)v_new, n_tokens, offset, cap,
+                               (f16*)k_data, (f16*)v_data);
+    }
+    QW_HIP_CHECK(hipGetLastError());
+    offset += n_tokens;
+    return QW_OK;
+}
+
+// ------------------------------------------------------------ dequantize
+//
+// MLX's composite dequantize: out = f16(f16(code * scale) + bias). code *
+// scale is exact in fp32 (<= 8 x 11 significant bits), so the first cast is
+// the fp16 product; the sum is formed in fp32 and cast once more, which is
+// how MLX's CPU float16 type evaluates `a + b`.
+
+__device__ inline f16 mlx_dequant(uint32_t c, f16 s, f16 b) {
+    const f16 prod = (f16)((float)c * (float)s);
+    return (f16)((float)prod + (float)b);
+}
+
+// One thread per (head, row, 8 dims); writes 16 bytes of K and of V.
+__global__ __launch_bounds__(256) void dequant_kernel(const uint32_t* __restrict__ k_codes,
+                                                      const uint32_t* __restrict__ k_params,
+                                                      const uint32_t* __restrict__ v_codes,
+                                                      const f16* __restrict__ v_params,
+                                                      int bits, int D, int cap, int hkv,
+                                                      int start, int n, f16* __restrict__ k_out,
+                                                      f16* __restrict__ v_out) {
+    const int64_t oct = D / 8;
+    const int64_t total = (int64_t)hkv * n * oct;
+    const int NG = D / kGroup;
+    const int nw = D * bits / 32;
+    const uint32_t m = (1u << bits) - 1u;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int h = (int)(i / (n * oct));
+        const int r = (int)((i / oct) % n);
+        const int d0 = (int)(i % oct) * 8;
+        const int t = start + r;
+        const int g = d0 / kGroup;
+        const half2v ksb =
+            __builtin_bit_cast(half2v, k_params[((int64_t)h * cap + t) * NG + g]);
+        const f16* vp = v_params + (((int64_t)h * (cap / 8) + t / 8) * NG + g) * 16;
+        const f16 vs = vp[t & 7], vbias = vp[8 + (t & 7)];
+        const uint32_t* krow = k_codes + ((int64_t)h * cap + t) * nw;
+        const uint32_t* vblk = v_codes + ((int64_t)h * (cap / 8) + t / 8) * (D * bits / 4);
+        half8 ko, vo;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int d = d0 + e;
+            const int epw = 32 / bits;
+            const uint32_t kcode = (krow[d / epw] >> ((d % epw) * bits)) & m;
+            ko[e] = mlx_dequant(kcode, ksb.x, ksb.y);
+            const int p = v_phys_dim(d, D, bits);
+            const int k = t & 7;
+            uint32_t vcode;
+            if (bits == 4)
+                vcode = (vblk[p] >> (4 * v4_nibble_pos(k))) & 0xFu;
+            else
+                vcode = (vblk[2 * p + (k >> 2)] >> (8 * (k & 3))) & 0xFFu;
+            vo[e] = mlx_dequant(vcode, vs, vbias);
+        }
+        const int64_t o = ((int64_t)h * n + r) * D + d0;
+        *(half8*)(k_out + o) = ko;
+        *(half8*)(v_out + o) = vo;
+    }
+}
+
+// fp16 mode: K rows copied; V gathered out of the 8-key blocks.
+__global__ __launch_bounds__(256) void fetch_fp16_kernel(const f16* __restrict__ k_data,
+                                                         const f16* __restrict__ v_data, int D,
+                                                         int cap, int hkv, int start, int n,
+                                                         f16* __restrict__ k_out,
+                                                         f16* __restrict__ v_out) {
+    const int64_t total = (int64_t)hkv * n * D;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int h = (int)(i / ((int64_t)n * D));
+        const int r = (int)((i / D) % n);
+        const int d = (int)(i % D);
+        const int t = start + r;
+        k_out[i] = k_data[((int64_t)h * cap + t) * D + d];
+        v_out[i] =
+            v_data[(((int64_t)h * (cap / 8) + t / 8) * D + v_phys_dim(d, D, 16)) * 8 + (t & 7)];
+    }
+}
+
+int KVCache::dequantize(int start, int n, void* k_out, void* v_out, hipStream_t stream) const {
+    QW_REQUIRE(start >= 0 && n >= 0 && start + n <= offset, QW_ERR_INVALID_ARGUMENT,
+               "dequantize: window [start, start+n) outside the cached rows");
+    if (n == 0) return QW_OK;
+    QW_REQUIRE(k_out && v_out, QW_ERR_INVALID_ARGUMENT, "dequantize: null output");
+    DeviceGuard dg(device);
+    const int64_t work = affine() ? (int64_t)hkv * n * (D / 8) : (int64_t)hkv * n * D;
+    const unsigned blocks = (unsigned)std::min<int64_t>((work + 255) / 256, 4096);
+    if (affine())
+        hipLaunchKernelGGL(dequant_kernel, dim3(blocks), dim3(256), 0, stream,
+                           (const uint32_t*)k_data, k_params, (const uint32_t*)v_data,
+                           (const f16*)v_params, bits, D, cap, hkv, start, n, (f16*)k_out,
+                           (f16*)v_out);
+    else
+        hipLaunchKernelGGL(fetch_fp16_kernel, dim3(blocks), dim3(256), 0, stream,
+                           (const f16*)k_data, (const f16*)v_data, D, cap, hkv, start, n,
+                           (f16*)k_out, (f16*)v_out);
+    QW_HIP_CHECK(hipGetLastError());
+    return QW_OK;
+}
+
+int KVCache::update_and_fetch(const void* k_new, const void* v_new, int n_tokens, void* k_out,
+                              void* v_out, hipStream_t stream) {
+    int rc = update(k_new, v_new, n_tokens, stream);
+    if (rc) return rc;
+    return dequantize(0, offset, k_out, v_out, stream);
+}
+
+// ------------------------------------------------------- snapshot tensors
+//
+// Export/import in the reference's layout: per head, rows [0, offset) of
+// MLX-packed codes and separate fp16 scale and bias planes (cache.rs:570-626
+// exports packed tensors as they are, without requantizing).
+
+// V blocks <-> rows, plus the K param split/merge. dir = 0: export.
+__global__ __launch_bounds__(256) void snapshot_affine_kernel(
+    int dir, int bits, int D, int cap, int hkv, int n, uint32_t* __restrict__ k_params,
+    uint32_t* __restrict__ v_codes, f16* __restrict__ v_params, f16* __restrict__ ks_out,
+    f16* __restrict__ kb_out, uint32_t* __restrict__ vc_rows, f16* __restrict__ vs_rows,
+    f16* __restrict__ vb_rows) {
+    const int NG = D / kGroup;
+    const int nw = D * bits / 32;
+    const int epw = 32 / bits;
+    const uint32_t m = (1u << bits) - 1u;
+    const int64_t total = (int64_t)hkv * n * nw;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int h = (int)(i / ((int64_t)n * nw));
+        const int t = (int)((i / nw) % n);
+        const int w = (int)(i % nw);
+        const int k = t & 7;
+        uint32_t* vblk = v_codes + ((int64_t)h * (cap / 8) + t / 8) * (D * bits / 4);
+        const int64_t row = (int64_t)h * n + t;
+        if (dir == 0) {
+            uint32_t word = 0;
+            for (int e = 0; e < epw; e++) {
+                const int p = v_phys_dim(w * epw + e, D, bits);
+                const uint32_t c = bits == 4 ? (vblk[p] >> (4 * v4_nibble_pos(k))) & m
+                                             : (vblk[2 * p + (k >> 2)] >> (8 * (k & 3))) & m;
+                word |= c << (e * bits);
+            }
+            vc_rows[row * nw + w] = word;
+        }
+        if (w < NG) {
+            const int g = w;
+            const int64_t kp = ((int64_t)h * cap + t) * NG + g;
+            f16* vp = v_params + (((int64_t)h * (cap / 8) + t / 8) * NG + g) * 16;
+            if (dir == 0) {
+                const half2v sb = __builtin_bit_cast(half2v, k_params[kp]);
+                ks_out[row * NG + g] = sb.x;
+                kb_out[row * NG + g] = sb.y;
+                vs_rows[row * NG + g] = vp[k];
+                vb_rows[row * NG + g] = vp[8 + k];
+            } else {
+                half2v sb;
+                sb.x = ks_out[row * NG + g];
+                sb.y = kb_out[row * NG + g];
+                k_params[kp] = __builtin_bit_cast(uint32_t, sb);
+                vp[k] = vs_rows[row * NG + g];
+                vp[8 + k] = vb_rows[row * NG + g];
+            }
+        }
+    }
+}
+
+// Import of V codes: one thread per (head, block, dim) builds the block word(s).
+__global__ __launch_bounds__(256) void import_v_codes_kernel(int bits, int D, int cap, int hkv,
+                                                             int n,
+                                                             const uint32_t* __restrict__ rows,
+                                                             uint32_t* __restrict__ v_codes) {
+    const int nblk = (n + 7) / 8;
+    const int nw = D * bits / 32;
+    const int epw = 32 / bits;
+    const uint32_t m = (1u << bits) - 1u;
+    const int64_t total = (int64_t)hkv * nblk * D;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int h = (int)(i / ((int64_t)nblk * D));
+        const int b = (int)((i / D) % nblk);
+        const int d = (int)(i % D);
+        uint32_t w0 = 0, w1 = 0;
+        for (int k = 0; k < 8; k++) {
+            const int t = b * 8 + k;
+            if (t >= n) break;
+            const uint32_t c = (rows[((int64_t)h * n + t) * nw + d / epw] >> ((d % epw) * bits)) & m;
+            if (bits == 4)
+                w0 |= c << (4 * v4_nibble_pos(k));
+            else if (k < 4)
+                w0 |= c << (8 * k);
+            else
+                w1 |= c << (8 * (k - 4));
+        }
+        uint32_t* vblk = v_codes + ((int64_t)h * (cap / 8) + b) * (D * bits / 4);
+        const int p = v_phys_dim(d, D, bits);
+        if (bits == 4) {
+            vblk[p] = w0;
+        } else {
+            vblk[2 * p] = w0;
+            vblk[2 * p + 1] = w1;
+        }
+    }
+}
+
+int KVCache::export_tensors(void* k_codes, void* k_scales, void* k_biases, void* v_codes,
+                            void* v_scales, void* v_biases, hipStream_t stream) const {
+    QW_REQUIRE(k_codes && v_codes, QW_ERR_INVALID_ARGUMENT, "export: null code pointers");
+    QW_REQUIRE(!affine() || (k_scales && k_biases && v_scales && v_biases),
+               QW_ERR_INVALID_ARGUMENT, "export: null scale/bias pointers");
+    if (offset == 0) return QW_OK;
+    DeviceGuard dg(device);
+    const int n = offset;
+    if (!affine()) {
+        // Same as a full fetch in fp16 mode.
+        return dequantize(0, n, k_codes, v_codes, stream);
+    }
+    const size_t kr = (size_t)D * bits / 8;
+    for (int h = 0; h < hkv; h++)
+        QW_HIP_CHECK(hipMemcpyAsync((char*)k_codes + h * (size_t)n * kr,
+                                    (const char*)k_data + h * (size_t)cap * kr, n * kr,
+                                    hipMemcpyDeviceToDevice, stream));
+    const int64_t work = (int64_t)hkv * n * (D * bits / 32);
+    hipLaunchKernelGGL(snapshot_affine_kernel,
+                       dim3((unsigned)std::min<int64_t>((work + 255) / 256, 4096)), dim3(256), 0,
+                       stream, 0, bits, D, cap, hkv, n, k_params, (uint32_t*)v_data,
+                       (f16*)v_params, (f16*)k_scales, (f16*)k_biases, (uint32_t*)v_codes,
+                       (f16*)v_scales, (f16*)v_biases);
+    QW_HIP_CHECK(hipGetLastError());
+    return QW_OK;
+}
+
+int KVCache::import_tensors(int n_tokens, const void* k_codes, const void* k_scales,
+                            const void* k_biases, const void* v_codes, const void* v_scales,
+                            const void* v_biases, hipStream_t stream) {
+    QW_REQUIRE(n_tokens >= 0, QW_ERR_INVALID_ARGUMENT, "import: n_tokens must be >= 0");
+    QW_REQUIRE(k_codes && v_codes, QW_ERR_INVALID_ARGUMENT, "import: null code pointers");
+    QW_REQUIRE(!affine() || (k_scales && k_biases && v_scales && v_biases),
+               QW_ERR_INVALID_ARGUMENT, "import: null scale/bias pointers");
+    DeviceGuard dg(device);
+    offset = 0;
+    if (n_tokens == 0) return QW_OK;
+    if (!affine()) return update(k_codes, v_codes, n_tokens, stream);
+    int rc = reserve(n_tokens, stream);
+    if (rc) return rc;
+    const int n = n_tokens;
+    const size_t kr = (size_t)D * bits / 8;
+    for (int h = 0; h < hkv; h++)
+        QW_HIP_CHECK(hipMemcpyAsync((char*)k_data + h * (size_t)cap * kr,
+                                    (const char*)k_codes + h * (size_t)n * kr, n * kr,
+                                    hipMemcpyDeviceToDevice, stream));
+    const int64_t work = (int64_t)hkv * n * (D * bits / 32);
+    hipLaunchKernelGGL(snapshot_affine_kernel,
+                       dim3((unsigned)std::min<int64_t>((work + 255) / 256, 4096)), dim3(256), 0,
+                       stream, 1, bits, D, cap, hkv, n, k_params, (uint32_t*)v_data,
+                       (f16*)v_params, (f16*)k_scales, (f16*)k_biases, (uint32_t*)v_codes,
+                       (f16*)v_scales, (f16*)v_biases);
+    QW_HIP_CHECK(hipGetLastError());
+    const int64_t vwork = (int64_t)hkv * ((n + 7) / 8) * D;
+    hipLaunchKernelGGL(import_v_codes_kernel,
+                       dim3((unsigned)std::min<int64_t>((vwork + 255) / 256, 4096)), dim3(256),
+                       0, stream, bits, D, cap, hkv, n, (const uint32_t*)v_codes,
+                       (uint32_t*)v_data);
+    QW_HIP_CHECK(hipGetLastError());
+    offset = n;
+    return QW_OK;
+}
+
+}  // namespace qw

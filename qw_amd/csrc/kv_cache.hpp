@@ -1,0 +1,92 @@
+// kv_cache.hpp - host-side KV cache object behind the C ABI.
+//
+// qw::KVCache mirrors the reference's KVCache (crates/mlxcel-core/src/cache.rs:354)
+// for one full-attention layer: the same method names (update,
+// update_and_fetch, trim, offset, nbytes, snapshot export/import) and the
+// same argument meaning, on caller-owned device pointers instead of MLX
+// arrays, returning status codes instead of panicking.
+#pragma once
+
+#include "qw_common.hpp"
+
+namespace qw {
+
+struct KVCache {
+    int mode = QW_KV_FP16;  // QW_KV_*
+    int bits = 16;          // 4, 8 (affine) or 16 (fp16)
+    int D = 0;              // head_dim
+    int hkv = 0;            // KV heads
+    int device = 0;
+    int offset = 0;         // cached tokens (cache.rs `offset`)
+    int cap = 0;            // allocated rows per head, multiple of 256
+
+    // K plane: affine codes [hkv][cap][D*bits/32] u32 or fp16 [hkv][cap][D].
+    void* k_data = nullptr;
+    // K params: [hkv][cap][D/64] half2(scale, bias); affine only.
+    uint32_t* k_params = nullptr;
+    // V plane: affine 8-key blocks [hkv][cap/8][D*bits/4 bytes] or fp16
+    // 8-key blocks [hkv][cap/8][D][8] f16 (same transposition, 16 bytes a dim).
+    void* v_data = nullptr;
+    // V params: [hkv][cap/8][D/64][16] f16 (s0..s7, b0..b7); affine only.
+    uint32_t* v_params = nullptr;
+
+    // Split-K workspace (partial accumulators), grown on demand.
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+
+    KvLayout layout() const { return KvLayout{bits, D, hkv, cap}; }
+    bool affine() const { return mode != QW_KV_FP16; }
+
+    size_t k_data_bytes(int c) const;
+    size_t k_param_bytes(int c) const;
+    size_t v_data_bytes(int c) const;
+    size_t v_param_bytes(int c) const;
+
+    int init(int mode, int group_size, int n_kv_heads, int head_dim, int capacity, int device);
+    int release();
+    int reserve(int capacity, hipStream_t stream);
+    int ensure_workspace(size_t bytes);
+    int64_t nbytes() const;
+
+    // cache.rs:922 `update`
+    int update(const void* k_new, const void* v_new, int n_tokens, hipStream_t stream);
+    // cache.rs:2709 `update_and_fetch`
+    int update_and_fetch(const void* k_new, const void* v_new, int n_tokens, void* k_out,
+                         void* v_out, hipStream_t stream);
+    int dequantize(int start, int n, void* k_out, void* v_out, hipStream_t stream) const;
+    // cache.rs:3495 / :3520 `update_and_turbo4_(causal_)attention`, affine codec
+    int update_and_attention(const void* q, int n_q_heads, int n_rows, const void* k_new,
+                             const void* v_new, float scale, bool causal, void* out,
+                             hipStream_t stream);
+    // cache.rs:3607 fused prefix attention, no append
+    int attention(const void* q, int n_q_heads, int n_rows, float scale, bool causal, void* out,
+                  hipStream_t stream);
+    // cache.rs:2251 `trim`
+    int trim(int n);
+    // cache.rs:570-626 snapshot tensors
+    int export_tensors(void* k_codes, void* k_scales, void* k_biases, void* v_codes,
+                       void* v_scales, void* v_biases, hipStream_t stream) const;
+    int import_tensors(int n_tokens, const void* k_codes, const void* k_scales,
+                       const void* k_biases, const void* v_codes, const void* v_scales,
+                       const void* v_biases, hipStream_t stream);
+};
+
+// RAII guard that makes `device` current for the duration of a call.
+struct DeviceGuard {
+    int prev = -1;
+    bool ok = true;
+    explicit DeviceGuard(int device) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != device) ok = hipSetDevice(device) == hipSuccess;
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+// Kernel launchers (attend_decode.hip, attend_block.hip).
+int launch_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float scale,
+                     bool causal, void* out, hipStream_t stream);
+
+}  // namespace qw

@@ -1,0 +1,92 @@
+// qw_common.hpp - shared device types, helpers and host error plumbing for
+// the gfx950 full-attention kernels (libqwattn.so).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "qwattn.h"
+
+namespace qw {
+
+typedef _Float16 f16;
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kGroup = 64;  // affine group size along head_dim
+constexpr int kWave = 64;
+
+// Byte layout of one cache mode, shared by every kernel that touches it.
+//   K plane, affine:  codes [hkv][cap][D*bits/32] u32, row-major and packed
+//                     LSB-first exactly as MLX `quantize` packs a row;
+//                     params [hkv][cap][D/64] u32 = half2(scale, bias).
+//   V plane, affine:  8-key blocks, codes [hkv][cap/8][D*bits/4 bytes]:
+//                     for each dim the 8 keys' codes sit in one u32 (4-bit)
+//                     or two u32 (8-bit), so a lane's 128-bit load is
+//                     directly the k-contiguous B operand of the P.V MFMA.
+//                     Dims are stored in "lane order" (see v_phys_dim) so
+//                     the 16 lanes of an MFMA column group read 256
+//                     contiguous bytes per load.
+//                     params [hkv][cap/8][D/64][16] f16: s0..s7, b0..b7.
+//   fp16 mode:        K [hkv][cap][D] f16; V in the same 8-key blocks,
+//                     [hkv][cap/8][D][8] f16 with dims in lane order.
+struct KvLayout {
+    int bits;  // 4, 8, or 16 (fp16 mode)
+    int D;
+    int hkv;
+    int cap;  // rows per head, multiple of 32
+    int64_t k_row_words() const { return (int64_t)D * bits / 32; }
+    int64_t k_param_words() const { return D / kGroup; }
+    int64_t v_block_words() const { return (int64_t)D * bits / 4; }
+    int64_t v_block_param_words() const { return (int64_t)(D / kGroup) * 8; }
+};
+
+// 4-bit V block word: key slot k (0..7) of a dim sits at nibble k/2 + 4*(k%2),
+// so `(w & 0x000F000F)`, `(w & 0x00F000F0)`, `(w>>8 & ..)` yield the key pairs
+// (0,1), (2,3), (4,5), (6,7) as fp16 magic-number halves.
+__host__ __device__ inline int v4_nibble_pos(int k) { return (k >> 1) + 4 * (k & 1); }
+
+// Physical slot of dim d inside a V block, in units of one dim's 8 codes
+// (4 bytes at 4-bit, 8 bytes at 8-bit, 16 bytes for fp16 values). Lane n of
+// an MFMA column group owns dims [n*DPL, (n+1)*DPL), DPL = D/16, and reads
+// them with 128-bit loads; E dims fit in 16 bytes.
+// Slot = 16*E*j + E*n + (d % E) with j = (d % DPL) / E.
+__host__ __device__ inline int v_phys_dim(int d, int D, int bits) {
+    const int dpl = D / 16;
+    const int e = bits == 4 ? 4 : (bits == 8 ? 2 : 1);
+    const int n = d / dpl, r = d % dpl;
+    return 16 * e * (r / e) + e * n + (r % e);
+}
+
+__device__ inline half2v h2(uint32_t x) { return __builtin_bit_cast(half2v, x); }
+__device__ inline half8 as_h8(u32x4 v) { return __builtin_bit_cast(half8, v); }
+
+// Thread-local last-error string for the C ABI.
+void set_error(const std::string& msg);
+const char* last_error();
+
+}  // namespace qw
+
+#define QW_HIP_CHECK(expr)                                                          \
+    do {                                                                            \
+        hipError_t _e = (expr);                                                     \
+        if (_e != hipSuccess) {                                                     \
+            qw::set_error(std::string(#expr) + ": " + hipGetErrorString(_e));       \
+            return QW_ERR_HIP;                                                      \
+        }                                                                           \
+    } while (0)
+
+#define QW_REQUIRE(cond, code, msg)  \
+    do {                             \
+        if (!(cond)) {               \
+            qw::set_error(msg);      \
+            return (code);           \
+        }                            \
+    } while (0)

@@ -1,0 +1,211 @@
+"""GPU parity of the KV cache path through the C ABI (MI355X).
+
+Codes, scales and biases of quantize-on-append must be bit-exact against the
+oracle's restatement of MLX `quantize`; the dequantized fetch bit-exact
+against MLX's composite dequantize; attention outputs within 2e-3 max-abs and
+1e-3 relative-L2 of the oracle's MLX CPU-stream SDPA over the dequantized
+cache (the tolerance BASELINE.json's north_star states).
+"""
+import numpy as np
+import pytest
+
+from conftest import rng
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+MAX_ABS = 2e-3
+REL_L2 = 1e-3
+
+
+def _gpu(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+
+
+def _np(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def _kv(r, H, T, D, jitter=True):
+    s = r.uniform(0.5, 2.0, (H, 1, 1)) if jitter else 1.0
+    return ((r.standard_normal((H, T, D)) * s).astype(np.float16),
+            (r.standard_normal((H, T, D)) * s).astype(np.float16))
+
+
+def assert_close(out, ref, what=""):
+    out = np.asarray(out, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = out - ref
+    mx = np.abs(err).max()
+    rel = np.linalg.norm(err) / max(np.linalg.norm(ref), 1e-30)
+    print(f"{what}: max_abs={mx:.3e} rel_l2={rel:.3e}", flush=True)
+    assert mx <= MAX_ABS and rel <= REL_L2, (what, mx, rel)
+
+
+def _mode(bits):
+    return {4: "affine4", 8: "affine8", 16: "fp16"}[bits]
+
+
+@pytest.mark.parametrize("bits,D", [(4, 256), (8, 256), (4, 128), (8, 128)])
+def test_append_codes_bit_exact(oracle_lib, bits, D):
+    import qw_amd
+
+    r = rng(bits * 1000 + D)
+    H = 4
+    sizes = [1, 7, 13, 256, 300, 1, 1, 37]
+    T = sum(sizes)
+    k, v = _kv(r, H, T, D)
+    cache = qw_amd.KVCache(_mode(bits), H, D, capacity=64)
+    t = 0
+    for n in sizes:
+        cache.update(_gpu(k[:, t:t + n])[None], _gpu(v[:, t:t + n])[None])
+        t += n
+    assert cache.offset == T and cache.capacity >= T
+    snap = {name: _np(x) for name, x in cache.snapshot_tensors().items()}
+    for side, src in (("k", k), ("v", v)):
+        codes, scales, biases = oracle_lib.affine_quantize(src, bits)
+        assert np.array_equal(snap[f"{side}_codes"].view(np.uint32), codes), side
+        assert np.array_equal(snap[f"{side}_scales"].view(np.uint16), scales.view(np.uint16))
+        assert np.array_equal(snap[f"{side}_biases"].view(np.uint16), biases.view(np.uint16))
+    # dequantized fetch == MLX composite dequantize, bit for bit
+    kd, vd = cache.dequantize()
+    for side, src, got in (("k", k, kd), ("v", v, vd)):
+        codes, scales, biases = oracle_lib.affine_quantize(src, bits)
+        want = oracle_lib.affine_dequantize(codes, scales, biases, bits)
+        assert np.array_equal(_np(got)[0].view(np.uint16), want.view(np.uint16)), side
+
+
+@pytest.mark.parametrize("D", [256, 128])
+def test_fp16_mode_fetch_is_identity(D):
+    import qw_amd
+
+    r = rng(D)
+    k, v = _kv(r, 4, 333, D)
+    cache = qw_amd.KVCache("fp16", 4, D, capacity=100)
+    cache.update(_gpu(k[:, :300])[None], _gpu(v[:, :300])[None])
+    kf, vf = cache.update_and_fetch(_gpu(k[:, 300:])[None], _gpu(v[:, 300:])[None])
+    assert np.array_equal(_np(kf)[0], k) and np.array_equal(_np(vf)[0], v)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_trim_then_reappend_equals_never_appended(bits):
+    import qw_amd
+
+    r = rng(50 + bits)
+    k, v = _kv(r, 4, 120, 256)
+    kx, vx = _kv(r, 4, 11, 256)
+    a = qw_amd.KVCache(_mode(bits), 4, 256)
+    a.update(_gpu(k[:, :100])[None], _gpu(v[:, :100])[None])
+    a.update(_gpu(kx)[None], _gpu(vx)[None])           # rejected draft block
+    assert a.trim(11) == 11 and a.offset == 100
+    assert a.trim(0) == 0
+    a.update(_gpu(k[:, 100:])[None], _gpu(v[:, 100:])[None])
+    b = qw_amd.KVCache(_mode(bits), 4, 256)
+    b.update(_gpu(k)[None], _gpu(v)[None])
+    sa, sb = a.snapshot_tensors(), b.snapshot_tensors()
+    for name in sa:
+        assert torch.equal(sa[name], sb[name]), name
+    assert a.trim(10_000) == 120 and a.offset == 0
+
+
+@pytest.mark.parametrize("bits", [4, 8, 16])
+def test_snapshot_round_trip(bits):
+    import qw_amd
+
+    r = rng(70 + bits)
+    k, v = _kv(r, 4, 203, 256)
+    a = qw_amd.KVCache(_mode(bits), 4, 256)
+    a.update(_gpu(k)[None], _gpu(v)[None])
+    snap = a.snapshot_tensors()
+    b = qw_amd.KVCache(_mode(bits), 4, 256, capacity=16)
+    b.restore_snapshot(snap)
+    assert b.offset == 203
+    ka, va = a.dequantize()
+    kb, vb = b.dequantize()
+    assert torch.equal(ka, kb) and torch.equal(va, vb)
+    # and the restored cache keeps working: the same append gives the same state
+    kn, vn = _kv(r, 4, 5, 256)
+    a.update(_gpu(kn)[None], _gpu(vn)[None])
+    b.update(_gpu(kn)[None], _gpu(vn)[None])
+    for name, t in a.snapshot_tensors().items():
+        assert torch.equal(t, b.snapshot_tensors()[name]), name
+
+
+def _layer_call(oracle_lib, qw_amd, bits, T_prefix, L, causal, seed, D=256, hq=24, hkv=4,
+                rows=None):
+    """Prefill a cache with T_prefix rows, then one update_and_attention of L rows,
+    on the GPU and in the oracle; returns (gpu_out, oracle_out, f64_out)."""
+    r = rng(seed)
+    k, v = _kv(r, hkv, T_prefix + L, D)
+    q = r.standard_normal((hq, L, D)).astype(np.float16)
+    cache = qw_amd.KVCache(_mode(bits), hkv, D, capacity=T_prefix + L)
+    if T_prefix:
+        cache.update(_gpu(k[:, :T_prefix])[None], _gpu(v[:, :T_prefix])[None])
+    fn = cache.update_and_causal_attention if causal else cache.update_and_attention
+    out = _np(fn(_gpu(q)[None], _gpu(k[:, T_prefix:])[None], _gpu(v[:, T_prefix:])[None],
+                 1.0 / 16))[0]
+    if bits == 16:
+        pos = oracle_lib.causal_positions(L, T_prefix + L) if causal else None
+        ref = oracle_lib.sdpa_mlx_f16(q, k, v, 1.0 / 16, q_pos=pos)
+        f64 = oracle_lib.sdpa_f64(q, k, v, 1.0 / 16, q_pos=pos)
+        return out, ref, f64
+    orc = oracle_lib.AffineCacheOracle(hkv, D, T_prefix + L, bits)
+    if T_prefix:
+        orc.update(k[:, :T_prefix], v[:, :T_prefix])
+    ref = orc.update_and_attention(q, k[:, T_prefix:], v[:, T_prefix:], 1.0 / 16, causal)
+    kd, vd = orc.fetch()
+    pos = oracle_lib.causal_positions(L, T_prefix + L) if causal else None
+    f64 = oracle_lib.sdpa_f64(q, kd, vd, 1.0 / 16, q_pos=pos)
+    return out, ref, f64
+
+
+@pytest.mark.parametrize("bits,T_prefix,L,causal", [
+    (8, 4095, 1, False),     # config 1 geometry: 4096 keys, 8-bit
+    (4, 32768, 1, False),    # config 2: decode at 32k + 1 appended, 4-bit
+    (4, 1000, 2, True),      # 2-row verify block, bottom-right causal
+    (8, 77, 1, False),       # ragged tail (77 + 1 keys)
+    (4, 0, 1, False),        # first token: a single key
+    (16, 5000, 1, False),    # fp16 cache
+])
+def test_update_and_attention_vs_oracle(oracle_lib, bits, T_prefix, L, causal):
+    import qw_amd
+
+    out, ref, f64 = _layer_call(oracle_lib, qw_amd, bits, T_prefix, L, causal,
+                                seed=bits * 7 + T_prefix + L)
+    assert np.isfinite(out).all()
+    assert_close(out, ref, f"bits={bits} T={T_prefix}+{L} vs oracle")
+    err64 = np.abs(out.astype(np.float64) - f64).max()
+    print(f"  vs fp64 closed form: max_abs={err64:.3e}", flush=True)
+
+
+def test_attention_without_append_equals_fused_call(oracle_lib):
+    import qw_amd
+
+    r = rng(91)
+    k, v = _kv(r, 4, 3000, 256)
+    q = r.standard_normal((24, 1, 256)).astype(np.float16)
+    a = qw_amd.KVCache("affine4", 4, 256)
+    a.update(_gpu(k)[None], _gpu(v)[None])
+    o1 = a.attention(_gpu(q)[None], 1.0 / 16)
+    b = qw_amd.KVCache("affine4", 4, 256)
+    b.update(_gpu(k[:, :2999])[None], _gpu(v[:, :2999])[None])
+    o2 = b.update_and_attention(_gpu(q)[None], _gpu(k[:, 2999:])[None], _gpu(v[:, 2999:])[None],
+                                1.0 / 16)
+    assert torch.equal(o1, o2)
+
+
+def test_invalid_calls_raise():
+    import qw_amd
+
+    c = qw_amd.KVCache("affine4", 4, 256)
+    q = torch.zeros((1, 24, 1, 256), dtype=torch.float16, device="cuda:0")
+    with pytest.raises(qw_amd.QwError):
+        c.attention(q, 0.0625)               # empty cache: fewer keys than rows
+    with pytest.raises(qw_amd.QwError):
+        c.update(torch.zeros((1, 3, 1, 256), dtype=torch.float16, device="cuda:0"),
+                 torch.zeros((1, 3, 1, 256), dtype=torch.float16, device="cuda:0"))
+    q25 = torch.zeros((1, 25, 1, 256), dtype=torch.float16, device="cuda:0")
+    k = torch.zeros((1, 4, 1, 256), dtype=torch.float16, device="cuda:0")
+    with pytest.raises(qw_amd.QwError):
+        c.update_and_attention(q25, k, k, 0.0625)  # 25 heads over 4 KV heads

@@ -1,0 +1,211 @@
+"""Pins the oracle's fp16 conversions and its restatement of MLX's affine codec.
+
+The reference holds no stored affine-KV vectors (it calls MLX `quantize` as a
+black box), so the codec is pinned by what the algorithm fixes: hand-derived
+known answers on grid-aligned groups, exact invariants (edge decodes exactly,
+codes in range, constant groups), brute force (no other code is nearer), and a
+separate numpy restatement for the packing. CPU only.
+"""
+import numpy as np
+import pytest
+
+from conftest import rng
+
+
+# ----------------------------------------------------------------- fp16
+
+def test_f16_to_f32_exhaustive(oracle_lib):
+    o = oracle_lib
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ours = o.f16_to_f32(h.view(np.float16))
+    ref = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(ours), nan)
+    assert np.array_equal(ours[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_matches_numpy_rne(oracle_lib):
+    o = oracle_lib
+    r = rng(1)
+    x = np.concatenate([
+        r.standard_normal(200000).astype(np.float32) * 10.0,
+        r.standard_normal(50000).astype(np.float32) * 1e-5,   # subnormal range
+        np.array([65504, 65519.99, 65520, 65536, 1e9, -65520, 2.0**-24, 2.0**-25,
+                  2.0**-25 * 1.0000001, 3 * 2.0**-26, 6.1035156e-05, 0.0, -0.0,
+                  np.inf, -np.inf], np.float32),
+    ])
+    # all halfway points between consecutive fp16 values (ties)
+    hs = np.arange(0, 0x7bff, dtype=np.uint16).view(np.float16).astype(np.float64)
+    mids = ((hs[:-1] + hs[1:]) / 2).astype(np.float32)
+    x = np.concatenate([x, mids, -mids])
+    ours = o.f32_to_f16(x)
+    ref = x.astype(np.float16)
+    assert np.array_equal(ours.view(np.uint16), ref.view(np.uint16))
+
+
+# ------------------------------------------------------- known answers
+
+def _pack(codes, bits):
+    codes = np.asarray(codes, np.uint64).reshape(-1, 32 // bits)
+    sh = np.arange(32 // bits, dtype=np.uint64) * bits
+    return (codes << sh).sum(axis=1).astype(np.uint32)
+
+
+def _unpack(words, bits, n):
+    words = np.asarray(words, np.uint64).reshape(-1, 1)
+    sh = np.arange(32 // bits, dtype=np.uint64) * bits
+    return ((words >> sh) & ((1 << bits) - 1)).reshape(-1)[:n].astype(np.int64)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_known_answer_positive_edge(oracle_lib, bits):
+    """Grid-aligned group whose larger-magnitude extreme is the max: the edge
+    is the max, the scale is negative, code = n_bins - c, dequant is exact."""
+    n_bins = (1 << bits) - 1
+    step = 0.5 if bits == 4 else 0.25
+    lo = -2.0 if bits == 4 else -10.0
+    c = rng(bits).integers(0, n_bins + 1, 64)
+    c[0], c[1] = 0, n_bins
+    w = (lo + step * c).astype(np.float16)
+    codes, s, b = oracle_lib.affine_quantize(w[None], bits)
+    assert s[0, 0] == np.float16(-step) and b[0, 0] == np.float16(lo + step * n_bins)
+    want = n_bins - c
+    assert np.array_equal(_unpack(codes[0], bits, 64), want)
+    assert np.array_equal(codes[0], _pack(want, bits))
+    deq = oracle_lib.affine_dequantize(codes, s, b, bits)
+    assert np.array_equal(deq[0], w)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_known_answer_negative_edge(oracle_lib, bits):
+    """Mirror case: |min| > |max| makes the min the edge, scale positive, code = c."""
+    n_bins = (1 << bits) - 1
+    step = 0.5 if bits == 4 else 0.25
+    lo = -5.5 if bits == 4 else -60.0
+    c = rng(10 + bits).integers(0, n_bins + 1, 64)
+    c[5], c[9] = 0, n_bins
+    w = (lo + step * c).astype(np.float16)
+    codes, s, b = oracle_lib.affine_quantize(w[None], bits)
+    assert s[0, 0] == np.float16(step) and b[0, 0] == np.float16(lo)
+    assert np.array_equal(_unpack(codes[0], bits, 64), c)
+    assert np.array_equal(oracle_lib.affine_dequantize(codes, s, b, bits)[0], w)
+
+
+def test_known_answer_nibble_order(oracle_lib):
+    """Codes are packed LSB-first: element k of a word sits in bits [4k, 4k+4)."""
+    c = np.array(list(range(16)) * 4)
+    w = (-5.5 + 0.5 * c).astype(np.float16)  # negative edge: code == c
+    codes, _, _ = oracle_lib.affine_quantize(w[None], 4)
+    assert codes[0, 0] == 0x76543210 and codes[0, 1] == 0xFEDCBA98
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_constant_and_zero_groups(oracle_lib, bits):
+    for v in (0.0, 1.0, -3.25, 1000.0):
+        w = np.full((1, 64), v, np.float16)
+        codes, s, b = oracle_lib.affine_quantize(w, bits)
+        assert np.all(codes == 0)
+        assert b[0, 0] == np.float16(v)
+        assert np.array_equal(oracle_lib.affine_dequantize(codes, s, b, bits), w)
+
+
+def test_rint_ties_to_even(oracle_lib):
+    """Exact .5 ties round to even (std::rint, MLX's CPU quantizer). Values
+    0, 0.5, 1.5, 2.5, ..., 7.5 with the min as edge and scale 1: codes for the
+    half-integers x.5 are the even neighbour."""
+    vals = np.array([-8.0, 7.0] + [k + 0.5 - 8.0 for k in range(0, 15)] * 5, np.float32)[:64]
+    w = vals.astype(np.float16)
+    codes, s, b = oracle_lib.affine_quantize(w[None], 4)
+    assert s[0, 0] == 1.0 and b[0, 0] == -8.0
+    got = _unpack(codes[0], 4, 64)
+    exact = vals + 8.0
+    # explicit ties-to-even on the .5 values
+    want = np.array([x if x % 1 == 0 else (np.floor(x) if np.floor(x) % 2 == 0 else np.ceil(x))
+                     for x in exact])
+    assert np.array_equal(got, want.astype(np.int64))
+
+
+# ---------------------------------------------------------- invariants
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_invariants_and_brute_force(oracle_lib, bits):
+    n_bins = (1 << bits) - 1
+    r = rng(100 + bits)
+    w = (r.standard_normal((512, 256)) * r.uniform(0.01, 4.0, (512, 1))
+         + r.uniform(-2, 2, (512, 1))).astype(np.float16)
+    codes, s, b = oracle_lib.affine_quantize(w, bits)
+    deq = oracle_lib.affine_dequantize(codes, s, b, bits).astype(np.float64)
+    c = _unpack(codes.reshape(-1), bits, w.size).reshape(w.shape)
+    assert c.min() >= 0 and c.max() <= n_bins
+    wg = w.astype(np.float64).reshape(512, 4, 64)
+    sg = s.astype(np.float64)[..., None]
+    bg = b.astype(np.float64)[..., None]
+    cg = c.reshape(512, 4, 64)
+    # edge: bias is the larger-magnitude extreme of the group and decodes exactly
+    mx, mn = wg.max(-1), wg.min(-1)
+    edge = np.where(np.abs(mn) > np.abs(mx), mn, mx)
+    assert np.array_equal(bg[..., 0], edge)
+    assert np.array_equal(deq.reshape(512, 4, 64)[cg == 0], np.broadcast_to(bg, cg.shape)[cg == 0])
+    # scale sign is opposite to the edge's (code 0 is the edge, codes grow inward)
+    nz = edge != 0
+    assert np.all(np.sign(sg[..., 0][nz]) == -np.sign(edge[nz]))
+    # |scale| = |edge / q0| with q0 = rint(edge / (range / n_bins)): within
+    # a factor (k + 1/2) / k of range / n_bins, k = |q0|
+    k = np.abs(np.rint(edge / (np.where(nz, (mx - mn) / n_bins, 1.0))))
+    ratio = np.abs(sg[..., 0]) / np.maximum((mx - mn) / n_bins, 1e-30)
+    ok = ~nz | (k == 0) | ((ratio <= (k + 0.5) / np.maximum(k, 1) * (1 + 2.0 ** -10)) &
+                           (ratio >= (k - 0.5) / np.maximum(k, 1) * (1 - 2.0 ** -10)))
+    assert np.all(ok)
+    # brute force: no other code is nearer (up to the fp16 rounding of scale)
+    grid = sg[..., None] * np.arange(n_bins + 1) + bg[..., None]  # [512,4,1,n_bins+1]
+    d_all = np.abs(wg[..., None] - grid)
+    d_own = np.take_along_axis(d_all, cg[..., None], axis=-1)[..., 0]
+    slack = np.abs(sg) * n_bins * 2.0 ** -10 + 1e-7
+    assert np.all(d_own <= d_all.min(-1) + slack)
+
+
+def _numpy_quantize(w, bits):
+    """Independent vectorized restatement, used only to cross-check packing and
+    the C implementation's loops on random data."""
+    n_bins = np.float32((1 << bits) - 1)
+    x = w.astype(np.float32).reshape(-1, 64)
+    mx, mn = x.max(1), x.min(1)
+    neg = np.abs(mn) > np.abs(mx)
+    scale = np.maximum((mx - mn) / n_bins, np.float32(1e-7)).astype(np.float32)
+    scale = np.where(neg, scale, -scale).astype(np.float32)
+    edge = np.where(neg, mn, mx).astype(np.float32)
+    q0 = np.rint(edge / scale).astype(np.float32)
+    nz = q0 != 0
+    scale = np.where(nz, edge / np.where(nz, q0, 1), scale).astype(np.float32)
+    bias = np.where(nz, edge, 0).astype(np.float32)
+    c = np.clip(np.rint((x - bias[:, None]) / scale[:, None]), 0, n_bins).astype(np.uint64)
+    epw = 32 // bits
+    sh = np.arange(epw, dtype=np.uint64) * bits
+    words = (c.reshape(-1, epw) << sh).sum(1).astype(np.uint32)
+    rows = w.shape[0]
+    return (words.reshape(rows, -1), scale.astype(np.float16).reshape(rows, -1),
+            bias.astype(np.float16).reshape(rows, -1))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_numpy_cross_check(oracle_lib, bits):
+    r = rng(7 + bits)
+    w = (r.standard_normal((300, 256)) * r.uniform(0.1, 3, (300, 1))).astype(np.float16)
+    got = oracle_lib.affine_quantize(w, bits)
+    want = _numpy_quantize(w, bits)
+    for g_, w_ in zip(got, want):
+        assert np.array_equal(np.asarray(g_).view(np.uint8), np.asarray(w_).view(np.uint8))
+
+
+def test_dequantize_double_rounding(oracle_lib):
+    """The composite dequant rounds code*scale to fp16 before adding the bias.
+    code 255, scale 3.001953125 (fp16-exact): 255*s = 765.498046875 -> f16
+    765.5; + 0.25 = 765.75 is a tie between 765.5 and 766.0 -> 766.0 (even).
+    A single fused rounding of 765.748046875 would give 765.5."""
+    codes = np.zeros((1, 64 * 8 // 32), np.uint32)
+    codes[0, 0] = 255
+    s = np.array([[3.001953125]], np.float16)
+    b = np.array([[0.25]], np.float16)
+    out = oracle_lib.affine_dequantize(codes, s, b, 8)
+    assert out[0, 0] == np.float16(766.0)
+    assert out[0, 1] == np.float16(0.25)
