@@ -26,7 +26,9 @@
 //   The 4 waves merge through LDS; each workgroup writes one fp32 partial
 //   (m, l, unnormalized O); a small merge kernel combines the partials.
 #include <algorithm>
+#include <type_traits>
 
+#include "dequant.hpp"
 #include "kv_cache.hpp"
 
 namespace qw {
@@ -42,40 +44,6 @@ struct DecodeArgs {
     int cap, T, Tq, G, R, causal, n_sub, nc;
     float scale_h;     // f16(scale) as float
 };
-
-// 8 fp16 values from one 4-bit word: y0 = nibbles (0,4), y1 = (1,5),
-// y2 = (2,6), y3 = (3,7). Nibbles 1,5,3,7 are masked in place (bits 4..7 of
-// each half), so they read as 1024 + 16*code; s1 and s3 carry scale/16 for
-// them. x - 1024 is exact, and one fma per pair gives f16(scale*code + bias).
-__device__ inline half8 deq4(uint32_t w, half2v s0, half2v s1, half2v s2, half2v s3, half2v b0,
-                             half2v b1, half2v b2, half2v b3) {
-    const half2v magic = {(f16)1024.0f, (f16)1024.0f};
-    const uint32_t w8 = w >> 8;
-    const half2v x0 = h2((w & 0x000F000Fu) | 0x64006400u) - magic;
-    const half2v x1 = h2((w & 0x00F000F0u) | 0x64006400u) - magic;
-    const half2v x2 = h2((w8 & 0x000F000Fu) | 0x64006400u) - magic;
-    const half2v x3 = h2((w8 & 0x00F000F0u) | 0x64006400u) - magic;
-    const half2v y0 = __builtin_elementwise_fma(x0, s0, b0);
-    const half2v y1 = __builtin_elementwise_fma(x1, s1, b1);
-    const half2v y2 = __builtin_elementwise_fma(x2, s2, b2);
-    const half2v y3 = __builtin_elementwise_fma(x3, s3, b3);
-    return half8{y0.x, y0.y, y1.x, y1.y, y2.x, y2.y, y3.x, y3.y};
-}
-
-// 8 fp16 values from two 8-bit words (bytes in order).
-__device__ inline half8 deq8(uint32_t w0, uint32_t w1, half2v s0, half2v s1, half2v s2,
-                             half2v s3, half2v b0, half2v b1, half2v b2, half2v b3) {
-    const half2v magic = {(f16)1024.0f, (f16)1024.0f};
-    const half2v x0 = h2(__builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u)) - magic;
-    const half2v x1 = h2(__builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u)) - magic;
-    const half2v x2 = h2(__builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u)) - magic;
-    const half2v x3 = h2(__builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u)) - magic;
-    const half2v y0 = __builtin_elementwise_fma(x0, s0, b0);
-    const half2v y1 = __builtin_elementwise_fma(x1, s1, b1);
-    const half2v y2 = __builtin_elementwise_fma(x2, s2, b2);
-    const half2v y3 = __builtin_elementwise_fma(x3, s3, b3);
-    return half8{y0.x, y0.y, y1.x, y1.y, y2.x, y2.y, y3.x, y3.y};
-}
 
 template <int BITS, int D>
 struct DecodeShape {
@@ -171,35 +139,66 @@ __global__ __launch_bounds__(256, 1) void attend_decode_kernel(DecodeArgs a) {
     // ---- scores (S^T: lane holds keys 8g+i (tile 0) / 8g+4+i (tile 1) of column r16)
     float sc[NSUB][8];
     const int lim = a.causal ? a.T - a.Tq + (row_ok ? rho / a.G : 0) : a.T - 1;
+    // One 16-key tile of Q.K^T; FAST selects the 2-op dequant (dequant.hpp).
+    auto qk_tile = [&](auto fast_tag, int j, int tile) -> float4v {
+        constexpr bool FAST = decltype(fast_tag)::value;
+        float4v acc = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (BITS == 4) {
+            // load cc covers words 16cc + 4g .. +3, all in group 2cc + g/2
+            PairConsts pc[KL];
+#pragma unroll
+            for (int cc = 0; cc < KL; cc++) {
+                const uint32_t raw = (g & 2) ? kp[j][tile][2 * cc + 1] : kp[j][tile][2 * cc];
+                const half2v sb = h2(raw);
+                const half2v s1 = {sb.x, sb.x}, b1 = {sb.y, sb.y};
+                pc[cc] = make_consts<FAST, 4>(s1, s1, s1, s1, b1, b1, b1, b1);
+            }
+#pragma unroll
+            for (int m = 0; m < NM; m++)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    deq4<FAST>(kc[j][tile][m / 4][m % 4], pc[m / 4]), qop[m], acc, 0, 0, 0);
+        } else if constexpr (BITS == 8) {
+            PairConsts pc[NG];
+#pragma unroll
+            for (int gi = 0; gi < NG; gi++) {
+                const half2v sb = h2(kp[j][tile][gi]);
+                const half2v s1 = {sb.x, sb.x}, b1 = {sb.y, sb.y};
+                pc[gi] = make_consts<FAST, 8>(s1, s1, s1, s1, b1, b1, b1, b1);
+            }
+#pragma unroll
+            for (int m = 0; m < NM; m++)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    deq8<FAST>(kc[j][tile][m / 2][2 * (m % 2)], kc[j][tile][m / 2][2 * (m % 2) + 1],
+                               pc[m / 2]),
+                    qop[m], acc, 0, 0, 0);
+        } else {
+#pragma unroll
+            for (int m = 0; m < NM; m++)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(kc[j][tile][m]), qop[m], acc,
+                                                             0, 0, 0);
+        }
+        return acc;
+    };
 #pragma unroll
     for (int j = 0; j < NSUB; j++) {
         const int s = s_begin + wave + 4 * j;
+        bool fast = true;
+        if constexpr (AFF) {
+            // The FAST dequant needs every scale of this sub-chunk in range.
+            const uint32_t lo = BITS == 4 ? kFast4Lo : kFast8Lo;
+            bool ok = true;
+#pragma unroll
+            for (int tile = 0; tile < 2; tile++)
+#pragma unroll
+                for (int gi = 0; gi < NG; gi++)
+                    ok = ok && scale_in_range(kp[j][tile][gi], lo, kFastHi);
+            fast = !__any(!ok);
+        }
 #pragma unroll
         for (int tile = 0; tile < 2; tile++) {
             float4v acc = {0.f, 0.f, 0.f, 0.f};
-            if (s < s_end) {
-#pragma unroll
-                for (int m = 0; m < NM; m++) {
-                    half8 av;
-                    if constexpr (BITS == 4) {
-                        const int grp = (16 * (m / 4) + 4 * g + (m % 4)) / 8;
-                        const half2v sb = h2(kp[j][tile][grp]);
-                        const half2v s1 = {sb.x, sb.x};
-                        const half2v b1 = {sb.y, sb.y};
-                        const half2v s16 = s1 * (half2v){(f16)0.0625f, (f16)0.0625f};
-                        av = deq4(kc[j][tile][m / 4][m % 4], s1, s16, s1, s16, b1, b1, b1, b1);
-                    } else if constexpr (BITS == 8) {
-                        const half2v sb = h2(kp[j][tile][m / 2]);
-                        const half2v s1 = {sb.x, sb.x};
-                        const half2v b1 = {sb.y, sb.y};
-                        av = deq8(kc[j][tile][m / 2][2 * (m % 2)], kc[j][tile][m / 2][2 * (m % 2) + 1],
-                                  s1, s1, s1, s1, b1, b1, b1, b1);
-                    } else {
-                        av = as_h8(kc[j][tile][m]);
-                    }
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qop[m], acc, 0, 0, 0);
-                }
-            }
+            if (s < s_end)
+                acc = fast ? qk_tile(std::true_type{}, j, tile) : qk_tile(std::false_type{}, j, tile);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int key = 32 * s + 8 * g + 4 * tile + i;
@@ -237,33 +236,37 @@ __global__ __launch_bounds__(256, 1) void attend_decode_kernel(DecodeArgs a) {
             lsum += p;
             pop[e] = (f16)p;
         }
-        half2v vs0, vs1, vs2, vs3, vb0, vb1, vb2, vb3;
-        if constexpr (AFF) {
-            vs0 = h2(vp[j][0][0]);
-            vs1 = h2(vp[j][0][1]);
-            vs2 = h2(vp[j][0][2]);
-            vs3 = h2(vp[j][0][3]);
-            vb0 = h2(vp[j][1][0]);
-            vb1 = h2(vp[j][1][1]);
-            vb2 = h2(vp[j][1][2]);
-            vb3 = h2(vp[j][1][3]);
-            if constexpr (BITS == 4) {
-                vs1 = vs1 * (half2v){(f16)0.0625f, (f16)0.0625f};
-                vs3 = vs3 * (half2v){(f16)0.0625f, (f16)0.0625f};
-            }
-        }
+        auto pv = [&](auto fast_tag) {
+            constexpr bool FAST = decltype(fast_tag)::value;
+            PairConsts pc;
+            if constexpr (AFF)
+                pc = make_consts<FAST, BITS>(h2(vp[j][0][0]), h2(vp[j][0][1]), h2(vp[j][0][2]),
+                                             h2(vp[j][0][3]), h2(vp[j][1][0]), h2(vp[j][1][1]),
+                                             h2(vp[j][1][2]), h2(vp[j][1][3]));
 #pragma unroll
-        for (int mm = 0; mm < DPL; mm++) {
-            half8 bv;
-            if constexpr (BITS == 4)
-                bv = deq4(vc[j][mm / 4][mm % 4], vs0, vs1, vs2, vs3, vb0, vb1, vb2, vb3);
-            else if constexpr (BITS == 8)
-                bv = deq8(vc[j][mm / 2][2 * (mm % 2)], vc[j][mm / 2][2 * (mm % 2) + 1], vs0, vs1,
-                          vs2, vs3, vb0, vb1, vb2, vb3);
-            else
-                bv = as_h8(vc[j][mm]);
-            acc_o[mm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop, bv, acc_o[mm], 0, 0, 0);
+            for (int mm = 0; mm < DPL; mm++) {
+                half8 bv;
+                if constexpr (BITS == 4)
+                    bv = deq4<FAST>(vc[j][mm / 4][mm % 4], pc);
+                else if constexpr (BITS == 8)
+                    bv = deq8<FAST>(vc[j][mm / 2][2 * (mm % 2)], vc[j][mm / 2][2 * (mm % 2) + 1], pc);
+                else
+                    bv = as_h8(vc[j][mm]);
+                acc_o[mm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop, bv, acc_o[mm], 0, 0, 0);
+            }
+        };
+        bool fast = true;
+        if constexpr (AFF) {
+            const uint32_t lo = BITS == 4 ? kFast4Lo : kFast8Lo;
+            bool ok = true;
+#pragma unroll
+            for (int i = 0; i < 4; i++) ok = ok && scales_in_range(vp[j][0][i], lo, kFastHi);
+            fast = !__any(!ok);
         }
+        if (fast)
+            pv(std::true_type{});
+        else
+            pv(std::false_type{});
     }
     lsum += __shfl_xor(lsum, 16);
     lsum += __shfl_xor(lsum, 32);

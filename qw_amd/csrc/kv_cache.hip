@@ -281,7 +281,7 @@ __global__ __launch_bounds__(256) void append_affine_kernel(
     }
     // V: one thread per dim assembles the block word(s), keeping the codes of
     // slots outside this append (earlier tokens of a partly filled block).
-    const int bw = D * bits / 32;  // words per V block
+    const int bw = D * bits / 4;  // words per V block (8 keys x D dims)
     uint32_t* vb = v_codes + ((int64_t)h * (cap / 8) + blk) * bw;
     for (int d = threadIdx.x; d < D; d += blockDim.x) {
         const int p = v_phys_dim(d, D, bits);

@@ -209,3 +209,34 @@ def test_invalid_calls_raise():
     k = torch.zeros((1, 4, 1, 256), dtype=torch.float16, device="cuda:0")
     with pytest.raises(qw_amd.QwError):
         c.update_and_attention(q25, k, k, 0.0625)  # 25 heads over 4 KV heads
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_extreme_scales_take_the_exact_slow_dequant(oracle_lib, bits):
+    """Groups with |scale| < 2^-10 or >= 64 miss the 2-op dequant's exactness
+    range; the kernel switches that sub-chunk to the separately rounded path,
+    which must still match MLX's composite dequant."""
+    import qw_amd
+
+    r = rng(300 + bits)
+    H, D, T = 4, 256, 700
+    k, v = _kv(r, H, T + 1, D, jitter=False)
+    k = k.astype(np.float32)
+    v = v.astype(np.float32)
+    k[:, 100:140, :64] *= 1e-3       # tiny scales
+    k[:, 300:301, 64:128] *= 300.0   # |scale| >= 64 (4-bit) / 8-bit range
+    v[:, 200:260, 128:192] *= 1e-3
+    v[:, 500:510, :64] *= 100.0
+    k, v = k.astype(np.float16), v.astype(np.float16)
+    q = r.standard_normal((24, 1, D)).astype(np.float16)
+    cache = qw_amd.KVCache(_mode(bits), H, D)
+    cache.update(_gpu(k[:, :T])[None], _gpu(v[:, :T])[None])
+    out = _np(cache.update_and_attention(_gpu(q)[None], _gpu(k[:, T:])[None],
+                                         _gpu(v[:, T:])[None], 1.0 / 16))[0]
+    orc = oracle_lib.AffineCacheOracle(H, D, T + 1, bits)
+    orc.update(k[:, :T], v[:, :T])
+    ref = orc.update_and_attention(q, k[:, T:], v[:, T:], 1.0 / 16, False).astype(np.float64)
+    err = out.astype(np.float64) - ref
+    rel = np.linalg.norm(err) / np.linalg.norm(ref)
+    print(f"extreme bits={bits}: max_abs={np.abs(err).max():.3e} rel_l2={rel:.3e}")
+    assert rel <= REL_L2 and np.abs(err).max() <= MAX_ABS * max(1.0, np.abs(ref).max())
