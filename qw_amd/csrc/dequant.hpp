@@ -90,14 +90,15 @@ __device__ __forceinline__ PairConsts make_consts(half2v s0, half2v s1, half2v s
     return c;
 }
 
-// 4-bit word -> pairs (nibbles 0,4), (1,5), (2,6), (3,7).
+// 4-bit word -> pairs (nibbles 0,4), (1,5), (2,6), (3,7). `magic` is
+// kMagic held in a VGPR (vconst) so each field costs one v_and_or_b32.
 template <bool FAST>
-__device__ __forceinline__ half8 deq4(uint32_t w, const PairConsts& c) {
+__device__ __forceinline__ half8 deq4(uint32_t w, const PairConsts& c, uint32_t magic) {
     const uint32_t w8 = w >> 8;
-    const half2v y0 = deq_pair<FAST, false>((w & 0x000F000Fu) | kMagic, c.s[0], c.m[0], c.b[0]);
-    const half2v y1 = deq_pair<FAST, true>((w & 0x00F000F0u) | kMagic, c.s[1], c.m[1], c.b[1]);
-    const half2v y2 = deq_pair<FAST, false>((w8 & 0x000F000Fu) | kMagic, c.s[2], c.m[2], c.b[2]);
-    const half2v y3 = deq_pair<FAST, true>((w8 & 0x00F000F0u) | kMagic, c.s[3], c.m[3], c.b[3]);
+    const half2v y0 = deq_pair<FAST, false>((w & 0x000F000Fu) | magic, c.s[0], c.m[0], c.b[0]);
+    const half2v y1 = deq_pair<FAST, true>((w & 0x00F000F0u) | magic, c.s[1], c.m[1], c.b[1]);
+    const half2v y2 = deq_pair<FAST, false>((w8 & 0x000F000Fu) | magic, c.s[2], c.m[2], c.b[2]);
+    const half2v y3 = deq_pair<FAST, true>((w8 & 0x00F000F0u) | magic, c.s[3], c.m[3], c.b[3]);
     return half8{y0.x, y0.y, y1.x, y1.y, y2.x, y2.y, y3.x, y3.y};
 }
 

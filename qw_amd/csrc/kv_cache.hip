@@ -82,15 +82,24 @@ int KVCache::init(int mode_, int group_size, int n_kv_heads, int head_dim, int c
     cap = 0;
     DeviceGuard dg(device);
     QW_REQUIRE(dg.ok, QW_ERR_HIP, "qw_kv_create: hipSetDevice failed");
+    if (hipMalloc(&fast_flag, 256) != hipSuccess) {
+        (void)hipGetLastError();
+        fast_flag = nullptr;
+        set_error("qw_kv_create: hipMalloc failed");
+        return QW_ERR_OUT_OF_MEMORY;
+    }
+    const int one = 1;
+    QW_HIP_CHECK(hipMemcpy(fast_flag, &one, sizeof(int), hipMemcpyHostToDevice));
     return reserve(capacity, nullptr);
 }
 
 int KVCache::release() {
     DeviceGuard dg(device);
     (void)hipDeviceSynchronize();
-    void* ptrs[5] = {k_data, (void*)k_params, v_data, (void*)v_params, ws};
+    void* ptrs[6] = {k_data, (void*)k_params, v_data, (void*)v_params, ws, (void*)fast_flag};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
+    fast_flag = nullptr;
     k_data = v_data = ws = nullptr;
     k_params = v_params = nullptr;
     ws_bytes = 0;
@@ -188,9 +197,17 @@ int KVCache::trim(int n) {
 // Codes go through LDS so the V block words (8 keys per dim) are assembled
 // by one thread each: no two threads write the same word.
 
+// Clears *fast_flag when the stored fp16 scale is outside the exact range of
+// the fused kernels' 2-op dequant (dequant.hpp).
+__device__ inline void check_fast_scale(f16 scale, int bits, int* fast_flag) {
+    const uint32_t a = __builtin_bit_cast(uint16_t, scale) & 0x7FFFu;
+    const uint32_t lo = bits == 4 ? 0x1400u : 0u;
+    if (a < lo || a >= 0x5400u) *fast_flag = 0;
+}
+
 template <int D>
 __device__ inline void quantize_row(const f16* __restrict__ src, int bits, uint8_t* lds_codes,
-                                    half2v* sb_out /* [D/64] (scale, bias) */) {
+                                    half2v* sb_out /* [D/64] (scale, bias) */, int* fast_flag) {
     constexpr int VPL = D / 64;         // values per lane
     constexpr int LPG = kGroup / VPL;   // lanes per group
     const int lane = threadIdx.x & 63;
@@ -234,6 +251,7 @@ __device__ inline void quantize_row(const f16* __restrict__ src, int bits, uint8
         sb.x = (f16)scale;
         sb.y = (f16)bias;
         sb_out[lane / LPG] = sb;
+        check_fast_scale(sb.x, bits, fast_flag);
     }
 }
 
@@ -241,7 +259,7 @@ template <int D>
 __global__ __launch_bounds__(256) void append_affine_kernel(
     const f16* __restrict__ k_new, const f16* __restrict__ v_new, int n_tokens, int t_old,
     int bits, int cap, uint32_t* __restrict__ k_codes, uint32_t* __restrict__ k_params,
-    uint32_t* __restrict__ v_codes, f16* __restrict__ v_params) {
+    uint32_t* __restrict__ v_codes, f16* __restrict__ v_params, int* __restrict__ fast_flag) {
     constexpr int NG = D / kGroup;
     __shared__ uint8_t kc[8][D];
     __shared__ uint8_t vc[8][D];
@@ -251,12 +269,28 @@ __global__ __launch_bounds__(256) void append_affine_kernel(
     const int blk = t_old / 8 + blockIdx.x;
     const int wave = threadIdx.x >> 6;
     const int t_end = t_old + n_tokens;
+    // Codes of earlier tokens in a partly filled block are kept: fetch those
+    // words now so their latency overlaps the quantization.
+    const int bw = D * bits / 4;  // words per V block (8 keys x D dims)
+    uint32_t* vb = v_codes + ((int64_t)h * (cap / 8) + blk) * bw;
+    const bool keep_old = blk * 8 < t_old;
+    uint32_t old0 = 0, old1 = 0;
+    const int d_own = threadIdx.x;  // blockDim.x == 256 >= D
+    const int p_own = d_own < D ? v_phys_dim(d_own, D, bits) : 0;
+    if (keep_old && d_own < D) {
+        if (bits == 4) {
+            old0 = vb[p_own];
+        } else {
+            old0 = vb[2 * p_own];
+            old1 = vb[2 * p_own + 1];
+        }
+    }
     for (int k = wave; k < 8; k += 4) {
         const int t = blk * 8 + k;
         if (t < t_old || t >= t_end) continue;
         const int64_t src = ((int64_t)h * n_tokens + (t - t_old)) * D;
-        quantize_row<D>(k_new + src, bits, kc[k], ksb[k]);
-        quantize_row<D>(v_new + src, bits, vc[k], vsb[k]);
+        quantize_row<D>(k_new + src, bits, kc[k], ksb[k], fast_flag);
+        quantize_row<D>(v_new + src, bits, vc[k], vsb[k], fast_flag);
     }
     __syncthreads();
     // K: row-major MLX packing, words of 32/bits codes LSB-first.
@@ -274,19 +308,18 @@ __global__ __launch_bounds__(256) void append_affine_kernel(
         const int k = i / NG, g = i % NG;
         const int t = blk * 8 + k;
         if (t < t_old || t >= t_end) continue;
-        k_params[((int64_t)h * cap + t) * NG + g] = __builtin_bit_cast(uint32_t, ksb[k][g]);
+        k_params[((int64_t)h * cap + t) * NG + k_param_slot(g, NG)] =
+            __builtin_bit_cast(uint32_t, ksb[k][g]);
         f16* vp = v_params + (((int64_t)h * (cap / 8) + blk) * NG + g) * 16;
         vp[k] = vsb[k][g].x;
         vp[8 + k] = vsb[k][g].y;
     }
     // V: one thread per dim assembles the block word(s), keeping the codes of
-    // slots outside this append (earlier tokens of a partly filled block).
-    const int bw = D * bits / 4;  // words per V block (8 keys x D dims)
-    uint32_t* vb = v_codes + ((int64_t)h * (cap / 8) + blk) * bw;
-    for (int d = threadIdx.x; d < D; d += blockDim.x) {
-        const int p = v_phys_dim(d, D, bits);
+    // slots before this append (earlier tokens of a partly filled block).
+    if (d_own < D) {
+        const int d = d_own, p = p_own;
         if (bits == 4) {
-            uint32_t word = vb[p];
+            uint32_t word = old0;
             for (int k = 0; k < 8; k++) {
                 const int t = blk * 8 + k;
                 if (t < t_old || t >= t_end) continue;
@@ -295,7 +328,7 @@ __global__ __launch_bounds__(256) void append_affine_kernel(
             }
             vb[p] = word;
         } else {
-            uint32_t w0 = vb[2 * p], w1 = vb[2 * p + 1];
+            uint32_t w0 = old0, w1 = old1;
             for (int k = 0; k < 8; k++) {
                 const int t = blk * 8 + k;
                 if (t < t_old || t >= t_end) continue;
@@ -348,11 +381,13 @@ int KVCache::update(const void* k_new, const void* v_new, int n_tokens, hipStrea
         if (D == 256)
             hipLaunchKernelGGL(append_affine_kernel<256>, grid, dim3(256), 0, stream,
                                (const f16*)k_new, (const f16*)v_new, n_tokens, offset, bits, cap,
-                               (uint32_t*)k_data, k_params, (uint32_t*)v_data, (f16*)v_params);
+                               (uint32_t*)k_data, k_params, (uint32_t*)v_data, (f16*)v_params,
+                               fast_flag);
         else
             hipLaunchKernelGGL(append_affine_kernel<128>, grid, dim3(256), 0, stream,
                                (const f16*)k_new, (const f16*)v_new, n_tokens, offset, bits, cap,
-                               (uint32_t*)k_data, k_params, (uint32_t*)v_data, (f16*)v_params);
+                               (uint32_t*)k_data, k_params, (uint32_t*)v_data, (f16*)v_params,
+                               fast_flag);
     } else {
         const int64_t n = (int64_t)n_tokens * D;
         dim3 grid((unsigned)std::min<int64_t>((n + 255) / 256, 1024), hkv);
@@ -402,8 +437,8 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint32_t* __restrict
         const int d0 = (int)(i % oct) * 8;
         const int t = start + r;
         const int g = d0 / kGroup;
-        const half2v ksb =
-            __builtin_bit_cast(half2v, k_params[((int64_t)h * cap + t) * NG + g]);
+        const half2v ksb = __builtin_bit_cast(
+            half2v, k_params[((int64_t)h * cap + t) * NG + k_param_slot(g, NG)]);
         const f16* vp = v_params + (((int64_t)h * (cap / 8) + t / 8) * NG + g) * 16;
         const f16 vs = vp[t & 7], vbias = vp[8 + (t & 7)];
         const uint32_t* krow = k_codes + ((int64_t)h * cap + t) * nw;
@@ -485,7 +520,8 @@ int KVCache::update_and_fetch(const void* k_new, const void* v_new, int n_tokens
 
 // V blocks <-> rows, plus the K param split/merge. dir = 0: export.
 __global__ __launch_bounds__(256) void snapshot_affine_kernel(
-    int dir, int bits, int D, int cap, int hkv, int n, uint32_t* __restrict__ k_params,
+    int dir, int bits, int D, int cap, int hkv, int n, int* __restrict__ fast_flag,
+    uint32_t* __restrict__ k_params,
     uint32_t* __restrict__ v_codes, f16* __restrict__ v_params, f16* __restrict__ ks_out,
     f16* __restrict__ kb_out, uint32_t* __restrict__ vc_rows, f16* __restrict__ vs_rows,
     f16* __restrict__ vb_rows) {
@@ -514,7 +550,7 @@ __global__ __launch_bounds__(256) void snapshot_affine_kernel(
         }
         if (w < NG) {
             const int g = w;
-            const int64_t kp = ((int64_t)h * cap + t) * NG + g;
+            const int64_t kp = ((int64_t)h * cap + t) * NG + k_param_slot(g, NG);
             f16* vp = v_params + (((int64_t)h * (cap / 8) + t / 8) * NG + g) * 16;
             if (dir == 0) {
                 const half2v sb = __builtin_bit_cast(half2v, k_params[kp]);
@@ -529,10 +565,14 @@ __global__ __launch_bounds__(256) void snapshot_affine_kernel(
                 k_params[kp] = __builtin_bit_cast(uint32_t, sb);
                 vp[k] = vs_rows[row * NG + g];
                 vp[8 + k] = vb_rows[row * NG + g];
+                check_fast_scale(sb.x, bits, fast_flag);
+                check_fast_scale(vp[k], bits, fast_flag);
             }
         }
     }
 }
+
+__global__ void set_flag_kernel(int* flag, int v) { *flag = v; }
 
 // Import of V codes: one thread per (head, block, dim) builds the block word(s).
 __global__ __launch_bounds__(256) void import_v_codes_kernel(int bits, int D, int cap, int hkv,
@@ -592,7 +632,7 @@ int KVCache::export_tensors(void* k_codes, void* k_scales, void* k_biases, void*
     const int64_t work = (int64_t)hkv * n * (D * bits / 32);
     hipLaunchKernelGGL(snapshot_affine_kernel,
                        dim3((unsigned)std::min<int64_t>((work + 255) / 256, 4096)), dim3(256), 0,
-                       stream, 0, bits, D, cap, hkv, n, k_params, (uint32_t*)v_data,
+                       stream, 0, bits, D, cap, hkv, n, fast_flag, k_params, (uint32_t*)v_data,
                        (f16*)v_params, (f16*)k_scales, (f16*)k_biases, (uint32_t*)v_codes,
                        (f16*)v_scales, (f16*)v_biases);
     QW_HIP_CHECK(hipGetLastError());
@@ -618,10 +658,12 @@ int KVCache::import_tensors(int n_tokens, const void* k_codes, const void* k_sca
         QW_HIP_CHECK(hipMemcpyAsync((char*)k_data + h * (size_t)cap * kr,
                                     (const char*)k_codes + h * (size_t)n * kr, n * kr,
                                     hipMemcpyDeviceToDevice, stream));
+    // The imported scales decide the fused kernels' dequant path afresh.
+    hipLaunchKernelGGL(set_flag_kernel, dim3(1), dim3(1), 0, stream, fast_flag, 1);
     const int64_t work = (int64_t)hkv * n * (D * bits / 32);
     hipLaunchKernelGGL(snapshot_affine_kernel,
                        dim3((unsigned)std::min<int64_t>((work + 255) / 256, 4096)), dim3(256), 0,
-                       stream, 1, bits, D, cap, hkv, n, k_params, (uint32_t*)v_data,
+                       stream, 1, bits, D, cap, hkv, n, fast_flag, k_params, (uint32_t*)v_data,
                        (f16*)v_params, (f16*)k_scales, (f16*)k_biases, (uint32_t*)v_codes,
                        (f16*)v_scales, (f16*)v_biases);
     QW_HIP_CHECK(hipGetLastError());

@@ -30,6 +30,11 @@ struct KVCache {
     // V params: [hkv][cap/8][D/64][16] f16 (s0..s7, b0..b7); affine only.
     uint32_t* v_params = nullptr;
 
+    // 1 while every stored scale is inside the exact 2-op dequant range of the
+    // fused kernels (dequant.hpp); cleared by an append or import that stores
+    // one outside it. Device int, read by each attention launch.
+    int* fast_flag = nullptr;
+
     // Split-K workspace (partial accumulators), grown on demand.
     void* ws = nullptr;
     size_t ws_bytes = 0;

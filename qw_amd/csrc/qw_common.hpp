@@ -48,6 +48,13 @@ struct KvLayout {
     int64_t v_block_param_words() const { return (int64_t)(D / kGroup) * 8; }
 };
 
+// K params of a row are stored in slot order (0, 2, 1, 3) when a row has four
+// 64-dim groups, so that the two groups a 4-bit decode lane dequantizes
+// (g/2 and 2 + g/2) are one 8-byte load.
+__host__ __device__ inline int k_param_slot(int group, int n_groups) {
+    return n_groups == 4 ? ((group & 1) * 2 + (group >> 1)) : group;
+}
+
 // 4-bit V block word: key slot k (0..7) of a dim sits at nibble k/2 + 4*(k%2),
 // so `(w & 0x000F000F)`, `(w & 0x00F000F0)`, `(w>>8 & ..)` yield the key pairs
 // (0,1), (2,3), (4,5), (6,7) as fp16 magic-number halves.
@@ -66,6 +73,16 @@ __host__ __device__ inline int v_phys_dim(int d, int D, int bits) {
 }
 
 __device__ inline half2v h2(uint32_t x) { return __builtin_bit_cast(half2v, x); }
+
+// A 32-bit constant materialized in a VGPR the compiler cannot see through.
+// gfx9 VOP3 encodings take no literal and at most one SGPR, so `(x & m) | k`
+// with both constants visible compiles to v_and + v_or; with k in a VGPR it
+// becomes one v_and_or_b32.
+__device__ __forceinline__ uint32_t vconst(uint32_t x) {
+    uint32_t r;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(x));
+    return r;
+}
 __device__ inline half8 as_h8(u32x4 v) { return __builtin_bit_cast(half8, v); }
 
 // Thread-local last-error string for the C ABI.
