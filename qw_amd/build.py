@@ -22,7 +22,7 @@ OUT = os.path.join(HERE, "libqwattn.so")
 BUILD_DIR = os.path.join(HERE, "_build")
 ARCH = "gfx950"
 
-SOURCES = ["kv_cache.hip", "attend_decode.hip", "dlsa.hip", "abi.hip"]
+SOURCES = ["kv_cache.hip", "attend_decode.hip", "attend_block.hip", "dlsa.hip", "abi.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

@@ -371,7 +371,8 @@ __global__ __launch_bounds__((64 * decode_waves<BITS, D>()), 1) void attend_deco
         decode_body<BITS, D, NW, false>(a, sm_ml, sm_o, sm_q);
 }
 
-// Combines the per-workgroup partials of one query row: out = sum_c e^(m_c - M)
+// Combines the per-workgroup partials of one query row (partials of a KV head
+// are [nc][rstride] rows, row index = r * G + head-in-group): out = sum_c e^(m_c - M)
 // O_c / sum_c e^(m_c - M) l_c, rounded to fp16 (a row with no visible key is 0).
 // grid (rows, kv_heads, D/64): a workgroup owns 64 dims of one row; lane =
 // dim, wave w sums partials c = w, w+4, ... with every load issued up front.
@@ -379,11 +380,11 @@ constexpr int kMergeMaxPer = 64;  // partials a wave sums (nc <= 256)
 
 __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ part_o,
                                                            const float2* __restrict__ part_ml,
-                                                           int nc, int D, int G, int Tq,
-                                                           f16* __restrict__ out) {
+                                                           int nc, int rstride, int D, int G,
+                                                           int Tq, f16* __restrict__ out) {
     const int row = blockIdx.x, h = blockIdx.y, d = blockIdx.z * 64 + (threadIdx.x & 63);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int64_t base = (int64_t)h * nc * 16 + row;
+    const int64_t base = (int64_t)h * nc * rstride + row;
     // One memory round: every (m, l) and O value this lane needs is loaded
     // first; the max is then exchanged through LDS.
     float v[kMergeMaxPer];
@@ -392,8 +393,8 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
     for (int i = 0; i < kMergeMaxPer; i++) {
         const int c = wave + 4 * i;
         if (c < nc) {
-            ml[i] = part_ml[base + (int64_t)c * 16];
-            v[i] = part_o[(base + (int64_t)c * 16) * D + d];
+            ml[i] = part_ml[base + (int64_t)c * rstride];
+            v[i] = part_o[(base + (int64_t)c * rstride) * D + d];
         } else {
             ml[i] = float2{-INFINITY, 0.0f};
             v[i] = 0.0f;
@@ -465,8 +466,15 @@ static int launch_decode_bits(KVCache& cc, const f16* q, int G, int Tq, float sc
     hipLaunchKernelGGL((attend_decode_kernel<BITS, D>), dim3(nc, cc.hkv), dim3(64 * NW), shmem,
                        stream, a);
     QW_HIP_CHECK(hipGetLastError());
-    hipLaunchKernelGGL(decode_merge_kernel, dim3(a.R, cc.hkv, D / 64), dim3(256), 0, stream,
-                       a.part_o, a.part_ml, nc, D, G, Tq, out);
+    return launch_partial_merge(a.part_o, a.part_ml, nc, 16, a.R, cc.hkv, D, G, Tq, out, stream);
+}
+
+int launch_partial_merge(const float* part_o, const float2* part_ml, int nc, int rstride, int R,
+                         int hkv, int D, int G, int Tq, f16* out, hipStream_t stream) {
+    QW_REQUIRE(nc >= 1 && nc <= 4 * kMergeMaxPer, QW_ERR_INVALID_ARGUMENT,
+               "merge: partial count out of range");
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(R, hkv, D / 64), dim3(256), 0, stream, part_o,
+                       part_ml, nc, rstride, D, G, Tq, out);
     QW_HIP_CHECK(hipGetLastError());
     return QW_OK;
 }
@@ -480,11 +488,11 @@ int launch_attention(KVCache& cc, const void* q, int n_q_heads, int n_rows, floa
     QW_REQUIRE(cc.offset >= n_rows, QW_ERR_INVALID_ARGUMENT,
                "attention: fewer cached keys than query rows");
     const int G = n_q_heads / cc.hkv;
-    QW_REQUIRE(G * n_rows <= 16, QW_ERR_UNSUPPORTED,
-               "attention: more than 16 query rows per KV head not yet supported");
     DeviceGuard dg(cc.device);
+    QW_REQUIRE(dg.ok, QW_ERR_HIP, "attention: hipSetDevice failed");
     const f16* qq = (const f16*)q;
     f16* oo = (f16*)out;
+    if (G * n_rows > 16) return launch_block_attention(cc, qq, G, n_rows, scale, causal, oo, stream);
     if (cc.D == 256) {
         if (cc.bits == 4) return launch_decode_bits<4, 256>(cc, qq, G, n_rows, scale, causal, oo, stream);
         if (cc.bits == 8) return launch_decode_bits<8, 256>(cc, qq, G, n_rows, scale, causal, oo, stream);
@@ -507,8 +515,6 @@ int KVCache::update_and_attention(const void* q, int n_q_heads, int n_rows, cons
                "update_and_attention: null pointer");
     QW_REQUIRE(n_q_heads > 0 && n_q_heads % hkv == 0 && n_rows > 0, QW_ERR_INVALID_ARGUMENT,
                "update_and_attention: bad head or row geometry");
-    QW_REQUIRE((n_q_heads / hkv) * n_rows <= 16, QW_ERR_UNSUPPORTED,
-               "update_and_attention: more than 16 query rows per KV head not yet supported");
     int rc = update(k_new, v_new, n_rows, stream);
     if (rc) return rc;
     return launch_attention(*this, q, n_q_heads, n_rows, scale, causal, out, stream);
