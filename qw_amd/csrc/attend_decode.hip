@@ -68,6 +68,17 @@ constexpr int decode_waves() {
     return D == 128 ? 12 : (BITS == 4 ? QW_DECODE_WAVES_4BIT : 8);
 }
 
+// Register stages a wave streams through (1: load the next sub-chunk after
+// the current one's math; 2: ping-pong, two sub-chunks in flight). Two fit
+// the register budget only for the small 4-bit stages.
+#ifndef QW_DECODE_STAGES_4BIT
+#define QW_DECODE_STAGES_4BIT 1
+#endif
+template <int BITS>
+constexpr int decode_stages() {
+    return BITS == 4 ? QW_DECODE_STAGES_4BIT : 1;
+}
+
 // FAST: every scale in the cache is inside the 2-op dequant's exact range
 // (the cache's fast_flag, maintained by the append and import kernels).
 template <int BITS, int D, int NW, bool FAST>
@@ -156,8 +167,12 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
     // The first sub-chunk's loads go out right behind Q (loads return in
     // issue order, so the Q conversion below waits for Q only).
     int s = s_begin + wave;
-    Stage A;
+    Stage A, B;
     if (s < s_end) load(A, s);
+    // Second stage in flight from the start: a wave's first two sub-chunks
+    // stream in while the first is being computed.
+    if constexpr (decode_stages<BITS>() == 2)
+        if (s + NW < s_end) load(B, s + NW);
     {
         // q' = f16(f16(scale) * q): one packed fp16 multiply rounds exactly
         // like MLX's fp16 `multiply`. Padding rows get scale 0.
@@ -309,12 +324,25 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
         pv(st, pop);
     };
 
-    for (; s < s_end; s += NW) {
-        compute(A, s);
-        // keep the next sub-chunk's loads behind this one's math: hoisting
-        // them would hold two stages live and spill
-        __builtin_amdgcn_sched_barrier(0);
-        if (s + NW < s_end) load(A, s + NW);
+    if constexpr (decode_stages<BITS>() == 2) {
+        // Ping-pong: a stage is refilled right after its math, so one stage's
+        // loads are always in flight behind the other's compute.
+        for (; s < s_end; s += 2 * NW) {
+            compute(A, s);
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + 2 * NW < s_end) load(A, s + 2 * NW);
+            if (s + NW >= s_end) break;
+            compute(B, s + NW);
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + 3 * NW < s_end) load(B, s + 3 * NW);
+        }
+    } else {
+        for (; s < s_end; s += NW) {
+            compute(A, s);
+            // keep the next sub-chunk's loads behind this one's math
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + NW < s_end) load(A, s + NW);
+        }
     }
     float lsum = l_run;
     lsum += __shfl_xor(lsum, 16);

@@ -241,23 +241,52 @@ __global__ __launch_bounds__(256) void dlsa_kernel(DlsaArgs a) {
 }
 
 // out[qh, r] = sum_p e^(m_p - M) O_p / sum_p e^(m_p - M) l_p (m in the log2 domain).
+// grid (q heads, rows, D/64), 4 waves: lane = dim, wave w sums parts w, w+4, ...
+// with every load issued before the first use (one memory round trip).
+constexpr int kDlsaMaxParts = 128;
+
 __global__ __launch_bounds__(256) void dlsa_merge_kernel(const float* __restrict__ part_o,
                                                          const float2* __restrict__ part_ml,
                                                          int parts, int D, int L, int hq,
                                                          f16* __restrict__ out) {
-    const int qh = blockIdx.x, r = blockIdx.y;
+    const int qh = blockIdx.x, r = blockIdx.y, d = blockIdx.z * 64 + (threadIdx.x & 63);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t base = ((int64_t)r * hq + qh) * parts;
-    float M = -INFINITY;
-    for (int p = 0; p < parts; p++) M = fmaxf(M, part_ml[base + p].x);
-    for (int d = threadIdx.x; d < D; d += blockDim.x) {
-        float Ls = 0.0f, O = 0.0f;
-#pragma unroll 8
-        for (int p = 0; p < parts; p++) {
-            const float2 ml = part_ml[base + p];
-            const float f = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - M);
-            Ls += f * ml.y;
-            O += f * part_o[(base + p) * D + d];
+    constexpr int PER = kDlsaMaxParts / 4;
+    float v[PER];
+    float2 ml[PER];
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int p = wave + 4 * i;
+        if (p < parts) {
+            ml[i] = part_ml[base + p];
+            v[i] = part_o[(base + p) * D + d];
+        } else {
+            ml[i] = float2{-INFINITY, 0.0f};
+            v[i] = 0.0f;
         }
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PER; i++) m = fmaxf(m, ml[i].x);
+    __shared__ float sm_m[4];
+    __shared__ float sm[2][4][64];
+    if (lane == 0) sm_m[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(sm_m[0], sm_m[1]), fmaxf(sm_m[2], sm_m[3]));
+    float o = 0.0f, l = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const float f = ml[i].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml[i].x - m);
+        o = __builtin_fmaf(f, v[i], o);
+        l = __builtin_fmaf(f, ml[i].y, l);
+    }
+    sm[0][wave][lane] = o;
+    sm[1][wave][lane] = l;
+    __syncthreads();
+    if (wave == 0) {
+        const float O = (sm[0][0][lane] + sm[0][1][lane]) + (sm[0][2][lane] + sm[0][3][lane]);
+        const float Ls = (sm[1][0][lane] + sm[1][1][lane]) + (sm[1][2][lane] + sm[1][3][lane]);
         out[((int64_t)qh * L + r) * D + d] = (f16)(Ls > 0.0f ? O / Ls : 0.0f);
     }
 }
@@ -332,7 +361,7 @@ int dlsa_sparse_attention(const void* q, const void* k, const void* v, int64_t k
     int dev = 0;
     QW_HIP_CHECK(hipGetDevice(&dev));
     if (parts <= 0) parts = auto_parts(n_rows * n_kv_heads, width);
-    parts = std::max(1, std::min(parts, 128));
+    parts = std::max(1, std::min(parts, kDlsaMaxParts));
     DlsaArgs a;
     a.q = (const f16*)q;
     a.k = (const f16*)k;
@@ -375,8 +404,9 @@ int dlsa_sparse_attention(const void* q, const void* k, const void* v, int64_t k
 #undef QW_DLSA_LAUNCH
     QW_HIP_CHECK(hipGetLastError());
     if (parts > 1) {
-        hipLaunchKernelGGL(dlsa_merge_kernel, dim3(n_q_heads, n_rows), dim3(head_dim), 0, stream,
-                           a.part_o, a.part_ml, parts, head_dim, n_rows, n_q_heads, (f16*)out);
+        hipLaunchKernelGGL(dlsa_merge_kernel, dim3(n_q_heads, n_rows, head_dim / 64), dim3(256), 0,
+                           stream, a.part_o, a.part_ml, parts, head_dim, n_rows, n_q_heads,
+                           (f16*)out);
         QW_HIP_CHECK(hipGetLastError());
     }
     (void)waves;  // one 4-wave workgroup shape; the knob is accepted for API parity
