@@ -68,34 +68,76 @@ constexpr int decode_waves() {
     return D == 128 ? 12 : (BITS == 4 ? QW_DECODE_WAVES_4BIT : 8);
 }
 
+// Word 3 of a raw buffer resource on gfx9-family parts (CDNA): 32-bit data
+// format, no swizzle, no index stride.
+constexpr int kBufWord3 = 0x00020000;
+
 // Register stages a wave streams through (1: load the next sub-chunk after
 // the current one's math; 2: ping-pong, two sub-chunks in flight). Two fit
 // the register budget only for the small 4-bit stages.
 #ifndef QW_DECODE_STAGES_4BIT
-#define QW_DECODE_STAGES_4BIT 1
+#define QW_DECODE_STAGES_4BIT 3
 #endif
 template <int BITS>
 constexpr int decode_stages() {
     return BITS == 4 ? QW_DECODE_STAGES_4BIT : 1;
 }
 
+// LDS-DMA staging (4-bit, D = 256): each wave streams its sub-chunks straight
+// into its own LDS buffers with global_load_lds_dwordx4 (one 1 KB
+// instruction per 64 lanes, no registers held while in flight), two buffers a
+// wave, so a CU's whole share of the cache is requested at launch. The loads
+// are issued from inline asm and waited for with explicit vmcnt counts: the
+// compiler cannot tell the two buffers apart and would wait for both.
+#ifndef QW_DECODE_LDS
+#define QW_DECODE_LDS 0
+#endif
+template <int BITS, int D>
+constexpr bool decode_lds() {
+    return QW_DECODE_LDS && BITS == 4 && D == 256;
+}
+constexpr int kLdsSub = 9216;  // bytes a 32-key 4-bit sub-chunk stages (K 4096, params 1024, V 4096)
+
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+// 64 lanes x 16 bytes from per-lane global addresses to LDS [lds, lds + 1024).
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds)
+                 : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
 // FAST: every scale in the cache is inside the 2-op dequant's exact range
 // (the cache's fast_flag, maintained by the append and import kernels).
 template <int BITS, int D, int NW, bool FAST>
-__device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)[16],
-                                            float* sm_o, half8 (*sm_q)[64]) {
+__device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)[16], float* sm_fw,
+                                            float* sm_o, half8 (*sm_q)[64], char* stage) {
     using S = DecodeShape<BITS, D>;
     constexpr int NM = S::NM, DPL = S::DPL, NG = S::NG, KL = S::KL, VL = S::VL;
+    constexpr bool LDSP = decode_lds<BITS, D>();
     constexpr bool AFF = BITS != 16;
     const int c = blockIdx.x, h = blockIdx.y;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // wave index as a scalar: sub-chunk indices, and so the buffer offsets
+    // below, stay in SGPRs
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
     const int r16 = lane & 15, g = lane >> 4;
-    const int s_begin = (int)((uint32_t)a.n_sub * (uint32_t)c / (uint32_t)a.nc);
-    const int s_end = (int)((uint32_t)a.n_sub * (uint32_t)(c + 1) / (uint32_t)a.nc);
+    // Sub-chunks are dealt round-robin: workgroup c, wave w, round k owns
+    // sub-chunk c + nc * (w + NW * k). At any moment the workgroups of a head
+    // stream adjacent 4 KB blocks, spreading the reads over all HBM channels
+    // (contiguous per-workgroup ranges put the 64 workgroups of a head on a
+    // few channel phases at once).
+    const int SS = a.nc * NW;  // stride between a wave's sub-chunks
+    const int s_end = a.n_sub;
     const uint32_t magic = vconst(kMagic);
 
     // One 32-key sub-chunk's loads; a wave walks its sub-chunks
-    // s_begin + wave + NW*k through one of these.
+    // c + nc * (wave + NW * k) through one of these.
     struct Stage {
         u32x4 kc[2][KL];  // K codes of tiles 0/1 (16 keys each)
         u32x4 kp[2];      // K (scale, bias) of the lane's key, tiles 0/1 (4-bit: the
@@ -103,40 +145,75 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
         u32x4 vc[VL];     // V block of keys 8g..8g+7, the lane's DPL dims
         u32x4 vp[2];      // V scales / biases of that block and dim group
     };
-    const int64_t krow_words = (int64_t)D * BITS / 32;
-    const int64_t vblk_words = (int64_t)D * BITS / 4;
+    // Raw buffer loads over this KV head's rows of each plane: the lane's
+    // byte offset is fixed for the whole kernel (VGPR), the sub-chunk's is a
+    // scalar (SGPR), the parts of a stage differ by immediates. A stage past
+    // the chunk's end gets num_records = 0, so its loads are issued
+    // unconditionally (exact vmcnt accounting with two stages in flight) but
+    // return zeros without touching memory.
+    constexpr int KRB = D * BITS / 8;          // K row bytes
+    constexpr int KPB = AFF ? NG * 4 : 0;      // K param bytes a row
+    constexpr int VBB = D * BITS;              // V block bytes (8 keys: D*BITS/4 words)
+    constexpr int VPB = NG * 32;               // V param bytes a block
+    const int64_t hrow = (int64_t)h * a.cap;
+    const char* kbase = (const char*)a.k_data + hrow * KRB;
+    const char* kpbase = (const char*)a.k_params + hrow * KPB;
+    const char* vbase = (const char*)a.v_data + hrow / 8 * VBB;
+    const char* vpbase = (const char*)a.v_params + hrow / 8 * VPB;
+    const int kkey = 8 * (r16 >> 2) + (r16 & 3);  // the lane's K row in tile 0
+    const int off_k = kkey * KRB + 16 * g;
+    const int off_kp = BITS == 4 && NG == 4 ? kkey * KPB + 8 * (g >> 1)
+                       : BITS == 4          ? kkey * KPB + 4 * (g >> 1)
+                                            : kkey * KPB;
+    const int off_v = g * VBB + 16 * r16;
+    const int off_vp = (g * NG + (r16 * DPL) / 64) * 32;
     auto load = [&](Stage& st, int s) {
+        const bool ok = s < s_end;
+        const int si = ok ? s : 0;
+        const __amdgpu_buffer_rsrc_t rk =
+            __builtin_amdgcn_make_buffer_rsrc((void*)kbase, 0, ok ? a.cap * KRB : 0, kBufWord3);
+        const __amdgpu_buffer_rsrc_t rv =
+            __builtin_amdgcn_make_buffer_rsrc((void*)vbase, 0, ok ? a.cap / 8 * VBB : 0, kBufWord3);
 #pragma unroll
         for (int tile = 0; tile < 2; tile++) {
-            const int key = 32 * s + 8 * (r16 >> 2) + 4 * tile + (r16 & 3);
-            const int64_t row = (int64_t)h * a.cap + key;
-            const u32x4* src = (const u32x4*)(a.k_data + row * krow_words);
 #pragma unroll
-            for (int cc = 0; cc < KL; cc++) st.kc[tile][cc] = src[4 * cc + g];
-            if constexpr (BITS == 4 && NG == 4) {
-                // groups g/2 and 2 + g/2 sit in slots 2(g/2), 2(g/2)+1 (k_param_slot)
-                const u32x2 t2 = *(const u32x2*)(a.k_params + row * NG + 2 * (g >> 1));
-                st.kp[tile] = u32x4{t2.x, t2.y, 0u, 0u};
-            } else if constexpr (BITS == 4) {
-                st.kp[tile] = u32x4{a.k_params[row * NG + (g >> 1)], 0u, 0u, 0u};
-            } else if constexpr (AFF) {
-                if constexpr (NG == 4)
-                    st.kp[tile] = *(const u32x4*)(a.k_params + row * NG);
-                else {
-                    const u32x2 t2 = *(const u32x2*)(a.k_params + row * NG);
-                    st.kp[tile] = u32x4{t2.x, t2.y, 0u, 0u};
+            for (int cc = 0; cc < KL; cc++)
+                st.kc[tile][cc] = __builtin_bit_cast(
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                               rk, off_k + tile * 4 * KRB + 64 * cc, 32 * si * KRB, 0));
+        }
+        if constexpr (AFF) {
+            const __amdgpu_buffer_rsrc_t rkp =
+                __builtin_amdgcn_make_buffer_rsrc((void*)kpbase, 0, ok ? a.cap * KPB : 0, kBufWord3);
+#pragma unroll
+            for (int tile = 0; tile < 2; tile++) {
+                const int o = off_kp + tile * 4 * KPB;
+                if constexpr (BITS == 4 && NG == 4) {
+                    const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(rkp, o, 32 * si * KPB, 0);
+                    st.kp[tile] = u32x4{t2[0], t2[1], 0u, 0u};
+                } else if constexpr (BITS == 4) {
+                    st.kp[tile] = u32x4{__builtin_amdgcn_raw_buffer_load_b32(rkp, o, 32 * si * KPB, 0),
+                                        0u, 0u, 0u};
+                } else if constexpr (NG == 4) {
+                    st.kp[tile] = __builtin_bit_cast(
+                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rkp, o, 32 * si * KPB, 0));
+                } else {
+                    const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(rkp, o, 32 * si * KPB, 0);
+                    st.kp[tile] = u32x4{t2[0], t2[1], 0u, 0u};
                 }
             }
         }
-        const int64_t blk = (int64_t)h * (a.cap / 8) + 4 * s + g;
-        const u32x4* vsrc = (const u32x4*)(a.v_data + blk * vblk_words);
 #pragma unroll
-        for (int jj = 0; jj < VL; jj++) st.vc[jj] = vsrc[16 * jj + r16];
+        for (int jj = 0; jj < VL; jj++)
+            st.vc[jj] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, off_v + 256 * jj, 4 * si * VBB, 0));
         if constexpr (AFF) {
-            const int grp = (r16 * DPL) / 64;
-            const u32x4* psrc = (const u32x4*)(a.v_params + (blk * NG + grp) * 8);
-            st.vp[0] = psrc[0];
-            st.vp[1] = psrc[1];
+            const __amdgpu_buffer_rsrc_t rvp =
+                __builtin_amdgcn_make_buffer_rsrc((void*)vpbase, 0, ok ? a.cap / 8 * VPB : 0, kBufWord3);
+            st.vp[0] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rvp, off_vp, 4 * si * VPB, 0));
+            st.vp[1] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rvp, off_vp + 16, 4 * si * VPB, 0));
         }
     };
 
@@ -148,31 +225,93 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
     const bool row_ok = rho < a.R;
     static_assert(NW >= NM, "one Q slice per wave");
     half8 x[1];
+    const f16* qsrc;
     {
         const int rr = row_ok ? rho : 0;
         const f16* qrow = a.q + ((int64_t)(h * a.G + rr % a.G) * a.Tq + rr / a.G) * D;
-#pragma unroll
-        for (int i = 0; i < 1; i++) {
-            const int m = wave % NM;
-            int base;
-            if constexpr (BITS == 4)
-                base = 8 * (16 * (m / 4) + 4 * g + (m % 4));
-            else if constexpr (BITS == 8)
-                base = 4 * (16 * (m / 2) + 4 * g + 2 * (m % 2));
-            else
-                base = 32 * m + 8 * g;
-            x[i] = *(const half8*)(qrow + base);
-        }
+        const int m = wave % NM;
+        int base;
+        if constexpr (BITS == 4)
+            base = 8 * (16 * (m / 4) + 4 * g + (m % 4));
+        else if constexpr (BITS == 8)
+            base = 4 * (16 * (m / 2) + 4 * g + 2 * (m % 2));
+        else
+            base = 32 * m + 8 * g;
+        qsrc = qrow + base;
+        if constexpr (!LDSP) x[0] = *(const half8*)qsrc;
     }
-    // The first sub-chunk's loads go out right behind Q (loads return in
-    // issue order, so the Q conversion below waits for Q only).
-    int s = s_begin + wave;
+    int s = c + a.nc * wave;
     Stage A, B;
-    if (s < s_end) load(A, s);
-    // Second stage in flight from the start: a wave's first two sub-chunks
-    // stream in while the first is being computed.
-    if constexpr (decode_stages<BITS>() == 2)
-        if (s + NW < s_end) load(B, s + NW);
+    // ---- LDS-DMA staging (LDSP): buffer b of this wave sits at
+    // stage + (2 * wave + b) * kLdsSub. Layout of a buffer: K codes [0, 4096)
+    // as 4 x 1 KB blocks of 8 keys (key r of block i, 16-byte column c at
+    // chunk 8r + (c ^ ((4(r>>1) + i) & 7)): the QK operand reads of a 16-lane
+    // phase hit 16 distinct bank groups), K params [4096, 4608), V params
+    // [4608, 5120), V codes [5120, 9216) (4 blocks of 1 KB as stored).
+    const char* kg = (const char*)a.k_data + (int64_t)h * a.cap * (D * BITS / 8);
+    const char* kpg = (const char*)a.k_params + (int64_t)h * a.cap * (NG * 4);
+    const char* vg = (const char*)a.v_data + (int64_t)h * (a.cap / 8) * (D * BITS);
+    const char* vpg = (const char*)a.v_params + (int64_t)h * (a.cap / 8) * (NG * 32);
+    auto issue = [&](int b, int s) {
+        const uint32_t buf = lds_offset(stage) + (uint32_t)((2 * wave + b) * kLdsSub);
+        const int r = lane >> 3;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int c = (lane & 7) ^ ((4 * (r >> 1) + i) & 7);
+            dma16(kg + ((int64_t)(32 * s + 8 * i + r) * (D * BITS / 8) + 16 * c), buf + 1024 * i);
+        }
+        const char* pg = lane < 32 ? kpg + (int64_t)32 * s * (NG * 4) + 16 * lane
+                                   : vpg + (int64_t)4 * s * (NG * 32) + 16 * (lane - 32);
+        dma16(pg, buf + 4096);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            dma16(vg + ((int64_t)(4 * s + i) * (D * BITS) + 16 * lane), buf + 5120 + 1024 * i);
+    };
+    auto fetch = [&](Stage& st, int b) {
+        const char* buf = stage + (2 * wave + b) * kLdsSub;
+        const int i = r16 >> 2;
+#pragma unroll
+        for (int tile = 0; tile < 2; tile++) {
+            const int r = 4 * tile + (r16 & 3);
+#pragma unroll
+            for (int cc = 0; cc < KL; cc++) {
+                const int c = 4 * cc + g;
+                st.kc[tile][cc] =
+                    *(const u32x4*)(buf + 1024 * i + 16 * (8 * r + (c ^ ((4 * (r >> 1) + i) & 7))));
+            }
+            const int key = 8 * i + r;
+            const u32x2 t2 = *(const u32x2*)(buf + 4096 + key * 16 + 8 * (g >> 1));
+            st.kp[tile] = u32x4{t2.x, t2.y, 0u, 0u};
+        }
+#pragma unroll
+        for (int jj = 0; jj < VL; jj++) st.vc[jj] = *(const u32x4*)(buf + 5120 + g * 1024 + 16 * (16 * jj + r16));
+        const int grp = (r16 * DPL) / 64;
+        st.vp[0] = *(const u32x4*)(buf + 4608 + (g * NG + grp) * 32);
+        st.vp[1] = *(const u32x4*)(buf + 4608 + (g * NG + grp) * 32 + 16);
+    };
+    if constexpr (LDSP) {
+        // Q slice first (raw, into its sm_q slot), then the first two sub-chunks.
+        if (wave < NM) dma16(qsrc, lds_offset(&sm_q[wave][0]));
+        if (s < s_end) issue(0, s);
+        if (s + SS < s_end) issue(1, s + SS);
+        if (wave < NM) {
+            if (s + SS < s_end)
+                wait_vm<18>();
+            else if (s < s_end)
+                wait_vm<9>();
+            else
+                wait_vm<0>();
+            x[0] = sm_q[wave][lane];
+        }
+    } else {
+        // The first sub-chunk's loads go out right behind Q (loads return in
+        // issue order, so the Q conversion below waits for Q only).
+        load(A, s);
+        // Second stage in flight from the start: a wave's first two sub-chunks
+        // stream in while the first is being computed.
+        if constexpr (decode_stages<BITS>() == 2) load(B, s + SS);
+    }
+    constexpr int kVmcnt0 = 0x0F70;  // s_waitcnt vmcnt(0), expcnt/lgkmcnt untouched
     {
         // q' = f16(f16(scale) * q): one packed fp16 multiply rounds exactly
         // like MLX's fp16 `multiply`. Padding rows get scale 0.
@@ -324,63 +463,106 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
         pv(st, pop);
     };
 
-    if constexpr (decode_stages<BITS>() == 2) {
+    if constexpr (LDSP) {
+        // Two buffers a wave: wait for the older one (the other may still be
+        // in flight: 9 instructions behind it), compute it from LDS, refill it
+        // with the sub-chunk two rounds ahead.
+        for (int b = 0; s < s_end; s += SS, b ^= 1) {
+            if (s + SS < s_end)
+                wait_vm<9>();
+            else
+                wait_vm<0>();
+            fetch(A, b);
+            compute(A, s);
+            if (s + 2 * SS < s_end) {
+                wait_lgkm0();
+                issue(b, s + 2 * SS);
+            }
+        }
+    } else if constexpr (decode_stages<BITS>() == 3) {
+        // Wait-then-prefetch ping-pong: a stage's successor is requested only
+        // once the stage itself has landed, so the first half of the cache
+        // arrives at full bandwidth and the second streams in under the
+        // first's math.
+        for (; s < s_end; s += 2 * SS) {
+            __builtin_amdgcn_s_waitcnt(kVmcnt0);
+            load(B, s + SS);
+            compute(A, s);
+            if (s + SS >= s_end) break;
+            __builtin_amdgcn_s_waitcnt(kVmcnt0);
+            load(A, s + 2 * SS);
+            compute(B, s + SS);
+        }
+    } else if constexpr (decode_stages<BITS>() == 2) {
         // Ping-pong: a stage is refilled right after its math, so one stage's
         // loads are always in flight behind the other's compute.
-        for (; s < s_end; s += 2 * NW) {
+        for (; s < s_end; s += 2 * SS) {
             compute(A, s);
             __builtin_amdgcn_sched_barrier(0);
-            if (s + 2 * NW < s_end) load(A, s + 2 * NW);
-            if (s + NW >= s_end) break;
-            compute(B, s + NW);
+            load(A, s + 2 * SS);
+            if (s + SS >= s_end) break;
+            compute(B, s + SS);
             __builtin_amdgcn_sched_barrier(0);
-            if (s + 3 * NW < s_end) load(B, s + 3 * NW);
+            load(B, s + 3 * SS);
         }
     } else {
-        for (; s < s_end; s += NW) {
+        for (; s < s_end; s += SS) {
             compute(A, s);
             // keep the next sub-chunk's loads behind this one's math
             __builtin_amdgcn_sched_barrier(0);
-            if (s + NW < s_end) load(A, s + NW);
+            load(A, s + SS);
         }
     }
     float lsum = l_run;
     lsum += __shfl_xor(lsum, 16);
     lsum += __shfl_xor(lsum, 32);
-    const float mx = m_run;
 
-    // ---- merge the NW waves: each wave parks its accumulators (rows < R) in
-    // LDS once, then all threads form out[row][d] = sum_w f_w O_w[row][d] with
-    // f_w = e^(m_w - M), M the row max over waves, and write the partial.
-    if (g == 0) sm_ml[wave][r16] = float2{mx, lsum};
+    // ---- merge the NW waves. Each wave parks its accumulators in LDS in
+    // their MFMA layout (float4 of rows 4g..4g+3 at dim r16*DPL + mm; only
+    // the lane groups holding rows < R), and its (m, l). One thread a row then
+    // forms the factors f_w = e^(m_w - M) and L; every thread sums its output
+    // elements out[row][d] = sum_w f_w O_w[row][d] and writes the partial.
+    // sm_o row stride: G4 * 16 float4 plus one, so the phase-B reads (16
+    // consecutive dims = 16 values of mm) fall on distinct banks.
+    if constexpr (LDSP) __syncthreads();  // sm_o aliases the staging buffers
     const int R = a.R;
+    const int G4 = (R + 3) >> 2;          // lane groups holding real rows
+    const int RS = G4 * 16 + 1;           // float4 per (wave, mm)
+    if (g == 0) sm_ml[wave][r16] = float2{m_run, lsum};
+    if (g < G4) {
+        float4v* dst = (float4v*)sm_o + (int64_t)wave * DPL * RS + g * 16 + r16;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int row = 4 * g + i;
-        if (row >= R) continue;
-        float* dst = sm_o + ((int64_t)wave * R + row) * D + r16 * DPL;
+        for (int mm = 0; mm < DPL; mm++) dst[mm * RS] = acc_o[mm];
+    }
+    __syncthreads();
+    float* sm_f = (float*)sm_fw;  // [NW][16] factors, then [16] L
+    if (threadIdx.x < 16) {
+        const int row = threadIdx.x;
+        float M = -INFINITY;
 #pragma unroll
-        for (int q4 = 0; q4 < DPL / 4; q4++)
-            *(float4v*)(dst + 4 * q4) = float4v{acc_o[4 * q4][i], acc_o[4 * q4 + 1][i],
-                                                acc_o[4 * q4 + 2][i], acc_o[4 * q4 + 3][i]};
+        for (int w = 0; w < NW; w++) M = fmaxf(M, sm_ml[w][row].x);
+        float L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float2 ml = sm_ml[w][row];
+            const float f = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((ml.x - M) * kLog2e);
+            sm_f[w * 16 + row] = f;
+            L = __builtin_fmaf(f, ml.y, L);
+        }
+        sm_f[NW * 16 + row] = L;
+        sm_f[NW * 16 + 16 + row] = M;
     }
     __syncthreads();
     const int64_t pbase = ((int64_t)h * a.nc + c) * 16;
     for (int o = threadIdx.x; o < R * D; o += 64 * NW) {
         const int row = o / D, d = o % D;
-        float M = -INFINITY;
+        const int rg = row >> 2, ri = row & 3, rl = d / DPL, mm = d % DPL;
+        const float* src = (const float*)sm_o + ((int64_t)mm * RS + rg * 16 + rl) * 4 + ri;
+        float acc = 0.0f;
 #pragma unroll
-        for (int w = 0; w < NW; w++) M = fmaxf(M, sm_ml[w][row].x);
-        float acc = 0.0f, L = 0.0f;
-#pragma unroll
-        for (int w = 0; w < NW; w++) {
-            const float2 ml = sm_ml[w][row];
-            const float f = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((ml.x - M) * kLog2e);
-            acc = __builtin_fmaf(f, sm_o[((int64_t)w * R + row) * D + d], acc);
-            L = __builtin_fmaf(f, ml.y, L);
-        }
+        for (int w = 0; w < NW; w++) acc = __builtin_fmaf(sm_f[w * 16 + row], src[(int64_t)w * DPL * RS * 4], acc);
         a.part_o[(pbase + row) * D + d] = acc;
-        if (d == 0) a.part_ml[pbase + row] = float2{M, L};
+        if (d == 0) a.part_ml[pbase + row] = float2{sm_f[NW * 16 + 16 + row], sm_f[NW * 16 + row]};
     }
 }
 
@@ -389,14 +571,17 @@ __global__ __launch_bounds__((64 * decode_waves<BITS, D>()), 1) void attend_deco
     DecodeArgs a) {
     constexpr int NW = decode_waves<BITS, D>();
     __shared__ float2 sm_ml[NW][16];
+    __shared__ float sm_fw[NW * 16 + 32];
     __shared__ half8 sm_q[D / 32][64];
-    extern __shared__ float sm_o[];  // [NW][R][D]
+    // dynamic LDS: the staging buffers (LDS-DMA path), reused as sm_o
+    // [NW][R][D] by the wave merge
+    extern __shared__ __attribute__((aligned(16))) float sm_o[];
     // One uniform branch for the whole launch: the exact 2-op dequant when
     // every cached scale allows it, else the separately rounded path.
     if (BITS == 16 || *a.fast_flag != 0)
-        decode_body<BITS, D, NW, true>(a, sm_ml, sm_o, sm_q);
+        decode_body<BITS, D, NW, true>(a, sm_ml, sm_fw, sm_o, sm_q, (char*)sm_o);
     else
-        decode_body<BITS, D, NW, false>(a, sm_ml, sm_o, sm_q);
+        decode_body<BITS, D, NW, false>(a, sm_ml, sm_fw, sm_o, sm_q, (char*)sm_o);
 }
 
 // Combines the per-workgroup partials of one query row (partials of a KV head
@@ -490,7 +675,16 @@ static int launch_decode_bits(KVCache& cc, const f16* q, int G, int Tq, float sc
     a.n_sub = n_sub;
     a.nc = nc;
     a.scale_h = (float)(f16)scale;
-    const size_t shmem = (size_t)NW * a.R * D * sizeof(float);
+    size_t shmem = (size_t)NW * (D / 16) * (((a.R + 3) / 4) * 16 + 1) * 16;  // wave-merge sm_o
+    if constexpr (decode_lds<BITS, D>()) shmem = std::max(shmem, (size_t)2 * NW * kLdsSub);
+    // Dynamic LDS above 64 KB must be allowed per kernel; raise the limit to
+    // what this launch needs (once per size, per template instance).
+    static size_t attr_max = 0;
+    if (shmem > attr_max) {
+        QW_HIP_CHECK(hipFuncSetAttribute((const void*)attend_decode_kernel<BITS, D>,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem));
+        attr_max = shmem;
+    }
     hipLaunchKernelGGL((attend_decode_kernel<BITS, D>), dim3(nc, cc.hkv), dim3(64 * NW), shmem,
                        stream, a);
     QW_HIP_CHECK(hipGetLastError());
