@@ -13,20 +13,26 @@
 // Design: the K/V tile of a KV head is dequantized ONCE per workgroup into
 // LDS (fp16, MLX-exact values) and shared by all of the workgroup's query
 // rows, the GQA heads of the group included:
-//   grid (key splits, query tiles, kv heads); NW waves; wave w owns 16 query
-//   rows (row index r * G + head-in-group, the decode kernel's order).
-//   Per tile of KT = 16384 / D keys (64 at D = 256):
-//     every thread loads one 32-dim K slice and one 4-dim V slice of the tile
-//     (codes + scale/bias) for the NEXT tile into registers, dequantizes the
-//     current one into LDS (K rows, V 8-key blocks), then all waves run
-//       S^T = K . Q'^T   v_mfma_f32_16x16x32_f16, A = K rows from LDS,
-//                        B = the wave's 16 query rows held in registers,
-//       online softmax on the fp16-rounded scores (exp2, lazy reference),
-//       O += P . V       A = P straight from the S^T registers, B = 8 keys
-//                        of one V dim from LDS (one ds_read_b128 per MFMA).
+//   grid (key splits, query tiles, kv heads); 8 waves, two a SIMD; wave w owns
+//   RT 16-row MFMA tiles of query rows (row index r * G + head-in-group, the
+//   decode kernel's order), so a workgroup owns 128 * RT rows.
+//   Tiles of KT = 16384 / D keys (64 at D = 256) go through two LDS buffers:
+//   in round t every thread dequantizes tile t+1 (loaded into registers the
+//   round before) into the free buffer, issues the loads of tile t+2, and the
+//   waves run tile t out of the other buffer:
+//     S^T = K . Q'^T   v_mfma_f32_16x16x32_f16, A = K rows from LDS (read once
+//                      a wave and used for all RT row tiles), B = query rows
+//                      held in registers,
+//     online softmax on the fp16-rounded scores (exp2, lazy reference),
+//     O += P . V       A = P straight from the S^T registers, B = 8 keys of one
+//                      V dim from LDS (one ds_read_b128 per MFMA, shared by the
+//                      RT row tiles).
+//   One barrier a tile. RT is chosen per launch so the workgroup count fills
+//   the 256 CUs in whole rounds where the row count allows.
 //   One key split: the workgroup writes normalized fp16 rows. Several:
 //   fp32 partials (m, l, O) and the shared split-K merge kernel.
 #include <algorithm>
+#include <type_traits>
 
 #include "dequant.hpp"
 #include "kv_cache.hpp"
@@ -41,11 +47,17 @@ struct BlockArgs {
     const int* fast_flag;
     const f16* q;       // [hq][Tq][D]
     f16* out;           // [hq][Tq][D], written directly when n_split == 1
-    float* part_o;      // [hkv][n_split][R][D]
-    float2* part_ml;    // [hkv][n_split][R]
+    float* part_o;      // [hkv][n_split][PR][D], rows from prow0
+    float2* part_ml;    // [hkv][n_split][PR]
     int cap, T, Tq, G, R, causal, n_split, tiles_per_split;
+    int qt0;            // first query tile of this launch
+    int prow0, PR;      // first row and row count of this launch's partials
     float scale_h;      // f16(scale) as float
 };
+
+// 8 waves, two a SIMD: one wave a SIMD leaves the MFMA, LDS and VALU
+// latencies of a wave exposed (measured ~1.6x slower at equal work).
+constexpr int kBlockWaves = 8;
 
 template <int D>
 struct BlockShape {
@@ -54,23 +66,33 @@ struct BlockShape {
     static constexpr int NM = D / 32;     // QK MFMAs per 16-key tile
     static constexpr int NT = D / 16;     // P.V MFMAs (16-dim output tiles)
     static constexpr int NG = D / 64;     // affine groups a row
-    static constexpr int TPR = D / 32;    // threads a K row (32 dims each)
+    static constexpr int TPR = D / 32;    // 32-dim K slices a row
     static constexpr int LTPR = TPR == 8 ? 3 : 2;
-    static constexpr int TPB = D / 4;     // threads a V block (4 slots each)
+    static constexpr int TPB = D / 4;     // 4-slot V slices a block
+    static constexpr int KROW = D / 8 + 1;  // K row stride in 16-byte chunks (one pad chunk)
+    static constexpr int KBUF = (KT * KROW + 4 * (KT / 16)) * 16;  // K tile bytes in LDS
+    static constexpr int VROW = D + D / 16;  // V block stride in chunks (a pad chunk per 16 slots)
+    static constexpr int VBUF = (KT / 8) * VROW * 16;               // V tile bytes in LDS
+    static constexpr int BUF = KBUF + VBUF;                         // one buffer
 };
 
-// LDS layouts (16-byte chunks, no padding; XOR/rotation swizzles keep every
-// 16-lane phase of a ds_read_b128 / ds_write_b128 on 16 distinct bank groups):
-//   K  [key][D/8 chunks]: chunk c of key k sits at c ^ kswz(k). The QK A
-//      operand reads keys 8(r>>2) + 4t + (r&3) (r = lane & 15) at one chunk,
-//      and kswz maps those 16 keys to 16 distinct values.
-//   V  [8-key block][D slots][8 keys]: slot s (the V plane's physical dim
-//      order) sits at vswz(s) = (s & ~3) | ((s + (s >> 4)) & 3). A lane writes
-//      slots 4j..4j+3 of its block; the P.V B operand reads slots 16mm + r.
-__device__ __forceinline__ int kswz(int key) { return (key & 3) | (((key >> 3) & 3) << 2); }
-__device__ __forceinline__ int vswz(int s) { return (s & ~3) | ((s + (s >> 4)) & 3); }
-
-constexpr int kBlockWaves = 8;  // 128 query rows a workgroup
+// LDS layouts (16-byte chunks):
+//   K  [key][D/8 + 1 chunks] plus 4 chunks every 16 keys: chunk c of key k
+//      sits at kaddr(k, c) = k * (D/8 + 1) + 4 * (k >> 4) + c. The QK A operand
+//      reads keys 8(r>>2) + 4t + (r&3) (r = lane & 15) at one chunk: k mod 16
+//      takes 0-3 and 8-11 twice, and the (k >> 4) shift moves the second pair
+//      to 4-7 and 12-15, so a 16-lane phase hits 16 distinct bank groups; and
+//      the address of every (sub-block, tile, step) is the lane's base plus an
+//      immediate. The store phase writes 4 keys x 4 slices a phase, also
+//      conflict-free.
+//   V  [8-key block][D slots + D/16 pad][8 keys], slots in the V plane's
+//      physical dim order, slot s at s + (s >> 4): the P.V B operand reads 16
+//      consecutive slots a phase (slot 16mm + r at 17mm + r, an immediate
+//      per mm), and the store phase's lanes (slots 4j + e) land on 16 distinct
+//      bank groups.
+__device__ __forceinline__ int kaddr(int key, int chunk, int krow) {
+    return key * krow + 4 * (key >> 4) + chunk;
+}
 
 // Logical dim of physical slot `slot` of a V block (inverse of v_phys_dim).
 __device__ __forceinline__ int v_logical_dim(int slot, int D, int bits) {
@@ -80,43 +102,55 @@ __device__ __forceinline__ int v_logical_dim(int slot, int D, int bits) {
     return n * dpl + e * j + i;
 }
 
-template <int BITS, int D, int NW, bool FAST>
-__device__ __forceinline__ void block_body(const BlockArgs& a, f16* sK, f16* sV) {
+template <int BITS, int D, int RT, bool FAST>
+__device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     using S = BlockShape<D>;
     constexpr int KT = S::KT, NSUB = S::NSUB, NM = S::NM, NT = S::NT, NG = S::NG;
-    constexpr int TPR = S::TPR, LTPR = S::LTPR, TPB = S::TPB;
+    constexpr int TPR = S::TPR, LTPR = S::LTPR, TPB = S::TPB, BUF = S::BUF, KBUF = S::KBUF;
+    constexpr int KROW = S::KROW, VROW = S::VROW;
+    constexpr int NW = kBlockWaves;
     constexpr bool AFF = BITS != 16;
-    constexpr int KU = BITS / 4;  // u32x4 loads a thread's 32-dim K slice / 4-dim V slice
-    static_assert(KT * TPR == 64 * NW && (KT / 8) * TPB == 64 * NW, "one slice a thread");
+    constexpr int KU = BITS / 4;  // u32x4 loads a 32-dim K slice / a 4-slot V slice
+    constexpr int PER = KT * TPR / (64 * NW);  // slices of each kind a thread owns
+    static_assert(PER * 64 * NW == KT * TPR && (KT / 8) * TPB == KT * TPR, "slices a thread");
 
-    const int sp = blockIdx.x, qt = blockIdx.y, h = blockIdx.z;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int sp = blockIdx.x, qt = blockIdx.y + a.qt0, h = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: wave-uniform branches
     const int r16 = lane & 15, g = lane >> 4;
     const uint32_t magic = vconst(kMagic);
 
     // ---- key range of this workgroup: its split, cut at the last key any of
     // its rows can see.
-    const int row0 = qt * 16 * NW;
-    const int row_last = min(a.R, row0 + 16 * NW) - 1;
+    constexpr int WROWS = 16 * RT;
+    const int row0 = qt * WROWS * NW;
+    const int row_last = min(a.R, row0 + WROWS * NW) - 1;
     const int wg_lim = a.causal ? a.T - a.Tq + row_last / a.G : a.T - 1;
     const int n_tiles = (a.T + KT - 1) / KT;
     const int t0 = sp * a.tiles_per_split;
     const int t1 = min(min(n_tiles, t0 + a.tiles_per_split), wg_lim / KT + 1);
 
-    // ---- the wave's 16 query rows as the B operand of S^T = K . Q'^T
-    // (col = query row r16, k-group g = dims 32m + 8g .. +7 of MFMA step m, in
-    // the order the LDS K row holds them).
-    const int rho = row0 + 16 * wave + r16;
-    const bool row_ok = rho < a.R;
-    const int wave_last = min(a.R, row0 + 16 * wave + 16) - 1;
-    const bool wave_live = row0 + 16 * wave < a.R;
+    // ---- the wave's RT x 16 query rows as the B operand of S^T = K . Q'^T
+    // (col = query row r16 of row tile rt, k-group g = dims 32m + 8g .. +7 of
+    // MFMA step m, in the order the LDS K row holds them).
+    const int wrow0 = row0 + WROWS * wave;
+    const bool wave_live = wrow0 < a.R;
+    const int wave_last = min(a.R, wrow0 + WROWS) - 1;
     const int wave_lim = a.causal ? a.T - a.Tq + wave_last / a.G : a.T - 1;
-    const int lim = a.causal ? a.T - a.Tq + (row_ok ? rho / a.G : 0) : a.T - 1;
-    half8 qb[NM];
-    {
-        const int rr = row_ok ? rho : 0;
+    // the smallest key limit of the wave's live rows (padding rows see nothing
+    // and are never written, so they do not count)
+    const int wave_first_lim = a.causal ? a.T - a.Tq + wrow0 / a.G : a.T - 1;
+    int lim[RT];
+    bool row_ok[RT];
+    half8 qb[RT][NM];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+        const int rho = wrow0 + 16 * rt + r16;
+        row_ok[rt] = rho < a.R;
+        lim[rt] = row_ok[rt] ? (a.causal ? a.T - a.Tq + rho / a.G : a.T - 1) : -1;
+        const int rr = row_ok[rt] ? rho : 0;
         const f16* qrow = a.q + ((int64_t)(h * a.G + rr % a.G) * a.Tq + rr / a.G) * D;
-        const f16 sc = row_ok ? (f16)a.scale_h : (f16)0.0f;
+        const f16 sc = row_ok[rt] ? (f16)a.scale_h : (f16)0.0f;
         const half2v sc2 = {sc, sc};
 #pragma unroll
         for (int m = 0; m < NM; m++) {
@@ -137,233 +171,363 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, f16* sK, f16* sV)
             y.y = __builtin_bit_cast(uint32_t, h2(o.y) * sc2);
             y.z = __builtin_bit_cast(uint32_t, h2(o.z) * sc2);
             y.w = __builtin_bit_cast(uint32_t, h2(o.w) * sc2);
-            qb[m] = __builtin_bit_cast(half8, y);
+            qb[rt][m] = __builtin_bit_cast(half8, y);
         }
     }
 
-    // ---- tile loads: thread -> (key kk, 32-dim slice q32) of K and
-    // (8-key block vb, 4 physical dim slots starting at 4 * vj) of V. Lanes
+    // ---- tile loads: thread slice j (of PER) -> (key kk, 32-dim slice q32)
+    // of K and (8-key block vb, 4 physical dim slots from 4 vj) of V. Lanes
     // 4i..4i+3 take 4 keys of one slice so a 16-lane phase writes 4 keys x 4
-    // slices (distinct banks under kswz).
-    const int q32 = (tid >> 2) & (TPR - 1);
-    const int kk = (tid & 3) | ((tid >> (2 + LTPR)) << 2);
-    const int vb = tid / TPB, vj = tid % TPB;
+    // slices (distinct bank groups under kaddr).
     struct Stage {
-        u32x4 kc[KU];
-        uint32_t kp;
-        u32x4 vc[KU];
-        u32x4 vp[2];
+        u32x4 kc[PER][KU];
+        uint32_t kp[PER];
+        u32x4 vc[PER][KU];
+        u32x4 vp[PER][2];
     };
+    int kk[PER], q32[PER], vb[PER], vj[PER], vgrp[PER];
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int tt = tid + 64 * NW * j;
+        q32[j] = (tt >> 2) & (TPR - 1);
+        kk[j] = (tt & 3) | ((tt >> (2 + LTPR)) << 2);
+        vb[j] = tt / TPB;
+        vj[j] = tt % TPB;
+        vgrp[j] = v_logical_dim(4 * vj[j], D, BITS) / 64;
+    }
     const int64_t krow_words = (int64_t)D * BITS / 32;
     const int64_t vblk_words = (int64_t)D * BITS / 4;
-    const int vgrp = v_logical_dim(4 * vj, D, BITS) / 64;
     auto load = [&](Stage& st, int t) {
-        const int64_t row = (int64_t)h * a.cap + (int64_t)t * KT + kk;
-        const u32x4* ksrc = (const u32x4*)(a.k_data + row * krow_words) + KU * q32;
 #pragma unroll
-        for (int u = 0; u < KU; u++) st.kc[u] = ksrc[u];
-        if constexpr (AFF) st.kp = a.k_params[row * NG + k_param_slot(q32 >> 1, NG)];
-        const int64_t blk = (int64_t)h * (a.cap / 8) + (int64_t)t * (KT / 8) + vb;
-        const u32x4* vsrc = (const u32x4*)(a.v_data + blk * vblk_words) + KU * vj;
+        for (int j = 0; j < PER; j++) {
+            const int64_t row = (int64_t)h * a.cap + (int64_t)t * KT + kk[j];
+            const u32x4* ksrc = (const u32x4*)(a.k_data + row * krow_words) + KU * q32[j];
 #pragma unroll
-        for (int u = 0; u < KU; u++) st.vc[u] = vsrc[u];
-        if constexpr (AFF) {
-            const u32x4* psrc = (const u32x4*)(a.v_params + (blk * NG + vgrp) * 8);
-            st.vp[0] = psrc[0];
-            st.vp[1] = psrc[1];
+            for (int u = 0; u < KU; u++) st.kc[j][u] = ksrc[u];
+            if constexpr (AFF) st.kp[j] = a.k_params[row * NG + k_param_slot(q32[j] >> 1, NG)];
+            const int64_t blk = (int64_t)h * (a.cap / 8) + (int64_t)t * (KT / 8) + vb[j];
+            const u32x4* vsrc = (const u32x4*)(a.v_data + blk * vblk_words) + KU * vj[j];
+#pragma unroll
+            for (int u = 0; u < KU; u++) st.vc[j][u] = vsrc[u];
+            if constexpr (AFF) {
+                const u32x4* psrc = (const u32x4*)(a.v_params + (blk * NG + vgrp[j]) * 8);
+                st.vp[j][0] = psrc[0];
+                st.vp[j][1] = psrc[1];
+            }
         }
     };
-    // Dequantize a stage into LDS: K row kk, chunks 4 q32 .. +3 (dims in the
-    // order of the Q operand); V block vb, slots 4 vj .. +3 (8 keys each).
-    half8* const sK8 = (half8*)sK;
-    half8* const sV8 = (half8*)sV;
-    auto store = [&](const Stage& st) {
-        half8* krow = sK8 + kk * (D / 8);
-        const int kx = kswz(kk);
-        if constexpr (BITS == 4) {
-            const half2v sb = h2(st.kp);
-            const half2v s = {sb.x, sb.x}, b = {sb.y, sb.y};
-            const PairConsts pc = make_consts<FAST, 4>(s, s, s, s, b, b, b, b);
+    // Dequantize a stage into LDS buffer b: K row kk, chunks 4 q32 .. +3 (dims
+    // in the order of the Q operand); V block vb, slots 4 vj .. +3 (8 keys each).
+    auto store = [&](const Stage& st, int b) {
+        half8* const sK8 = (half8*)(lds + BUF * b);
+        half8* const sV8 = (half8*)(lds + BUF * b + KBUF);
 #pragma unroll
-            for (int w = 0; w < 4; w++) krow[(4 * q32 + w) ^ kx] = deq4<FAST>(st.kc[0][w], pc, magic);
-        } else if constexpr (BITS == 8) {
-            const half2v sb = h2(st.kp);
-            const half2v s = {sb.x, sb.x}, b = {sb.y, sb.y};
-            const PairConsts pc = make_consts<FAST, 8>(s, s, s, s, b, b, b, b);
+        for (int j = 0; j < PER; j++) {
+            half8* krow = sK8 + kaddr(kk[j], 4 * q32[j], KROW);
+            if constexpr (BITS == 4) {
+                const half2v sb = h2(st.kp[j]);
+                const half2v s = {sb.x, sb.x}, bb = {sb.y, sb.y};
+                const PairConsts pc = make_consts<FAST, 4>(s, s, s, s, bb, bb, bb, bb);
 #pragma unroll
-            for (int w = 0; w < 4; w++)
-                krow[(4 * q32 + w) ^ kx] =
-                    deq8<FAST>(st.kc[w / 2][2 * (w % 2)], st.kc[w / 2][2 * (w % 2) + 1], pc);
-        } else {
+                for (int w = 0; w < 4; w++) krow[w] = deq4<FAST>(st.kc[j][0][w], pc, magic);
+            } else if constexpr (BITS == 8) {
+                const half2v sb = h2(st.kp[j]);
+                const half2v s = {sb.x, sb.x}, bb = {sb.y, sb.y};
+                const PairConsts pc = make_consts<FAST, 8>(s, s, s, s, bb, bb, bb, bb);
 #pragma unroll
-            for (int w = 0; w < 4; w++) krow[(4 * q32 + w) ^ kx] = as_h8(st.kc[w]);
-        }
-        PairConsts vc;
-        if constexpr (AFF)
-            vc = make_consts<FAST, BITS>(h2(st.vp[0][0]), h2(st.vp[0][1]), h2(st.vp[0][2]),
-                                         h2(st.vp[0][3]), h2(st.vp[1][0]), h2(st.vp[1][1]),
-                                         h2(st.vp[1][2]), h2(st.vp[1][3]));
-        half8* vblk = sV8 + vb * D;
+                for (int w = 0; w < 4; w++)
+                    krow[w] = deq8<FAST>(st.kc[j][w / 2][2 * (w % 2)], st.kc[j][w / 2][2 * (w % 2) + 1], pc);
+            } else {
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            half8 y;
-            if constexpr (BITS == 4)
-                y = deq4<FAST>(st.vc[0][e], vc, magic);
-            else if constexpr (BITS == 8)
-                y = deq8<FAST>(st.vc[e / 2][2 * (e % 2)], st.vc[e / 2][2 * (e % 2) + 1], vc);
-            else
-                y = as_h8(st.vc[e]);
-            vblk[vswz(4 * vj + e)] = y;
+                for (int w = 0; w < 4; w++) krow[w] = as_h8(st.kc[j][w]);
+            }
+            PairConsts vc;
+            if constexpr (AFF)
+                vc = make_consts<FAST, BITS>(h2(st.vp[j][0][0]), h2(st.vp[j][0][1]),
+                                             h2(st.vp[j][0][2]), h2(st.vp[j][0][3]),
+                                             h2(st.vp[j][1][0]), h2(st.vp[j][1][1]),
+                                             h2(st.vp[j][1][2]), h2(st.vp[j][1][3]));
+            half8* vblk = sV8 + vb[j] * VROW;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                half8 y;
+                if constexpr (BITS == 4)
+                    y = deq4<FAST>(st.vc[j][0][e], vc, magic);
+                else if constexpr (BITS == 8)
+                    y = deq8<FAST>(st.vc[j][e / 2][2 * (e % 2)], st.vc[j][e / 2][2 * (e % 2) + 1], vc);
+                else
+                    y = as_h8(st.vc[j][e]);
+                vblk[4 * vj[j] + e + (vj[j] >> 2)] = y;  // slot s at s + (s >> 4)
+            }
         }
     };
 
-    float m_run = -INFINITY;  // softmax reference of column r16 (natural units)
-    float l_run = 0.0f;       // this lane's share of the column sum
-    float4v acc_o[NT];
+    float m_run[RT], l_run[RT];  // softmax reference / this lane's share of the sum, column r16
+    float4v acc_o[RT][NT];
 #pragma unroll
-    for (int mm = 0; mm < NT; mm++) acc_o[mm] = float4v{0.f, 0.f, 0.f, 0.f};
+    for (int rt = 0; rt < RT; rt++) {
+        m_run[rt] = -INFINITY;
+        l_run[rt] = 0.0f;
+#pragma unroll
+        for (int mm = 0; mm < NT; mm++) acc_o[rt][mm] = float4v{0.f, 0.f, 0.f, 0.f};
+    }
 
-    // One 32-key sub-block (keys kb .. kb+31, LDS rows 32u ..) of the tile.
-    auto sub_block = [&](int u, int kb) {
-        // S^T: A row r16 of MFMA tile tt is key 8(r16>>2) + 4tt + (r16&3), so
-        // lane (g, r16) ends up with keys 8g + 4tt + i of column r16.
-        const int key0 = 32 * u + 8 * (r16 >> 2) + (r16 & 3);  // tile 1: key0 + 4
-        const half8* k0 = sK8 + key0 * (D / 8);
-        const half8* k1 = k0 + 4 * (D / 8);
-        const int kx = kswz(key0);  // == kswz(key0 + 4)
-        float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    // One tile (keys kt0 .. kt0 + KT - 1) out of buffer b: the QK MFMAs of all
+    // its 32-key sub-blocks first (independent chains), one softmax step over
+    // the whole tile (one max reduction, one lazy-rescale check), then P.V.
+    auto tile = [&](int b, int kt0) {
+        const half8* sK8 = (const half8*)(lds + BUF * b);
+        const half8* sV8 = (const half8*)(lds + BUF * b + KBUF);
+        // S^T: A row r16 of 16-key MFMA tile (u, tt) is key 32u + 8(r16>>2) +
+        // 4tt + (r16&3), so lane (g, r16) ends up with keys 32u + 8g + 4tt + i
+        // of column r16.
+        const int key0 = 8 * (r16 >> 2) + (r16 & 3);
+        const half8* kbase = sK8 + kaddr(key0, g, KROW);
+        float4v acc[NSUB][2][RT];
+#pragma unroll
+        for (int u = 0; u < NSUB; u++)
+#pragma unroll
+            for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+                for (int rt = 0; rt < RT; rt++) acc[u][tt][rt] = float4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int m = 0; m < NM; m++) {
-            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0[(4 * m + g) ^ kx], qb[m], acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1[(4 * m + g) ^ kx], qb[m], acc1, 0, 0, 0);
-        }
-        float sc[8];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int ka = kb + 8 * g + i, kc = ka + 4;
-            // MLX rounds the score matrix to fp16 before the softmax.
-            sc[i] = row_ok && ka <= lim ? (float)(f16)acc0[i] : -INFINITY;
-            sc[4 + i] = row_ok && kc <= lim ? (float)(f16)acc1[i] : -INFINITY;
-        }
-        // Online softmax with a lazy reference: m_run moves only when a score
-        // exceeds it by more than 5.5 (so p <= e^5.5 stays well inside fp16).
-        float mx = sc[0];
-#pragma unroll
-        for (int e = 1; e < 8; e++) mx = fmaxf(mx, sc[e]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        if (__any(mx > m_run + 5.5f)) {
-            const float m_new = fmaxf(m_run, mx);
-            if (__any(m_run != -INFINITY)) {
-                const float alpha =
-                    m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((m_run - m_new) * kLog2e);
-                l_run *= alpha;
-                float f[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) f[i] = __shfl(alpha, 4 * g + i);
-#pragma unroll
-                for (int mm = 0; mm < NT; mm++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) acc_o[mm][i] *= f[i];
-            }
-            m_run = m_new;
-        }
-        const float mref2 = (m_run == -INFINITY ? 0.0f : m_run) * kLog2e;
-        half8 pop;
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[e], kLog2e, -mref2));
-            l_run += p;
-            pop[e] = (f16)p;
-        }
-        // O += P . V: B = slot 16mm + r16 (column r16 of output tile mm) of
-        // V block 4u + g, i.e. keys 8g .. 8g+7 of the sub-block.
-        const half8* vb8 = sV8 + (4 * u + g) * D;
-#pragma unroll
-        for (int mm = 0; mm < NT; mm++)
-            acc_o[mm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop, vb8[vswz(16 * mm + r16)],
-                                                               acc_o[mm], 0, 0, 0);
-    };
-
-    Stage st;
-    if (t0 < t1) load(st, t0);
-    for (int t = t0; t < t1; t++) {
-        __syncthreads();  // every wave is done reading the previous tile
-        store(st);
-        if (t + 1 < t1) load(st, t + 1);
-        __syncthreads();
-        if (wave_live) {
 #pragma unroll
             for (int u = 0; u < NSUB; u++) {
-                const int kb = t * KT + 32 * u;
-                if (kb <= wave_lim) sub_block(u, kb);
+                // key0 + 32u (+4) keeps key0's 16-key band offset: +2u bands
+                const half8* k0 = kbase + 32 * u * KROW + 8 * u;
+                const half8 ka = k0[4 * m], kb2 = k0[4 * KROW + 4 * m];
+#pragma unroll
+                for (int rt = 0; rt < RT; rt++) {
+                    acc[u][0][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[rt][m], acc[u][0][rt], 0, 0, 0);
+                    acc[u][1][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb2, qb[rt][m], acc[u][1][rt], 0, 0, 0);
+                }
             }
         }
+        half8 pop[NSUB][RT];
+        // Scores -> fp16 rounding -> (mask) -> online softmax -> P; MASKED only
+        // for tiles some row of the wave cannot fully see (a scalar branch: the
+        // common case carries no per-score compares).
+        auto softmax = [&](auto masked) {
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) {
+                float sc[NSUB][8];
+#pragma unroll
+                for (int u = 0; u < NSUB; u++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        // MLX rounds the score matrix to fp16 before the softmax.
+                        sc[u][i] = (float)(f16)acc[u][0][rt][i];
+                        sc[u][4 + i] = (float)(f16)acc[u][1][rt][i];
+                        if constexpr (decltype(masked)::value) {
+                            const int ka = kt0 + 32 * u + 8 * g + i, kc = ka + 4;
+                            sc[u][i] = ka <= lim[rt] ? sc[u][i] : -INFINITY;
+                            sc[u][4 + i] = kc <= lim[rt] ? sc[u][4 + i] : -INFINITY;
+                        }
+                    }
+                // Online softmax with a lazy reference: m_run moves only when a
+                // score exceeds it by more than 5.5 (so p <= e^5.5 stays well
+                // inside fp16).
+                float mx = sc[0][0];
+#pragma unroll
+                for (int u = 0; u < NSUB; u++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) mx = fmaxf(mx, sc[u][e]);
+                mx = fmaxf(mx, __shfl_xor(mx, 16));
+                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                if (__any(mx > m_run[rt] + 5.5f)) {
+                    const float m_new = fmaxf(m_run[rt], mx);
+                    if (__any(m_run[rt] != -INFINITY)) {
+                        const float alpha = m_run[rt] == -INFINITY
+                                                ? 0.0f
+                                                : __builtin_amdgcn_exp2f((m_run[rt] - m_new) * kLog2e);
+                        l_run[rt] *= alpha;
+                        float f[4];
+#pragma unroll
+                        for (int i = 0; i < 4; i++) f[i] = __shfl(alpha, 4 * g + i);
+#pragma unroll
+                        for (int mm = 0; mm < NT; mm++)
+#pragma unroll
+                            for (int i = 0; i < 4; i++) acc_o[rt][mm][i] *= f[i];
+                    }
+                    m_run[rt] = m_new;
+                }
+                const float mref2 = (m_run[rt] == -INFINITY ? 0.0f : m_run[rt]) * kLog2e;
+#pragma unroll
+                for (int u = 0; u < NSUB; u++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[u][e], kLog2e, -mref2));
+                        l_run[rt] += p;
+                        pop[u][rt][e] = (f16)p;
+                    }
+            }
+        };
+        // every row of the wave sees the whole tile: no per-score mask
+        if (kt0 + KT - 1 <= wave_first_lim)
+            softmax(std::false_type{});
+        else
+            softmax(std::true_type{});
+        // O += P . V: B = slot 16mm + r16 (column r16 of output tile mm) of
+        // V block 4u + g, i.e. keys 32u + 8g .. +7.
+#pragma unroll
+        for (int u = 0; u < NSUB; u++) {
+            const half8* vb8 = sV8 + (4 * u + g) * VROW + r16;
+#pragma unroll
+            for (int mm = 0; mm < NT; mm++) {
+                const half8 vv = vb8[17 * mm];  // slot 16mm + r16
+#pragma unroll
+                for (int rt = 0; rt < RT; rt++)
+                    acc_o[rt][mm] =
+                        __builtin_amdgcn_mfma_f32_16x16x32_f16(pop[u][rt], vv, acc_o[rt][mm], 0, 0, 0);
+            }
+        }
+    };
+
+    // ---- main loop: round t dequantizes tile t+1 into buffer (t+1)&1, issues
+    // the loads of tile t+2, computes tile t from buffer t&1; one barrier.
+    Stage st;
+    if (t0 < t1) {
+        load(st, t0);
+        store(st, 0);
+        if (t0 + 1 < t1) load(st, t0 + 1);
+    }
+    __syncthreads();
+    for (int t = t0; t < t1; t++) {
+        const int b = (t - t0) & 1;
+        if (t + 1 < t1) {
+            store(st, b ^ 1);
+            if (t + 2 < t1) load(st, t + 2);
+        }
+        if (wave_live && t * KT <= wave_lim) tile(b, t * KT);
+        __syncthreads();
     }
 
     // ---- epilogue: per column, the row sum over the 4 lane groups.
-    float lsum = l_run;
-    lsum += __shfl_xor(lsum, 16);
-    lsum += __shfl_xor(lsum, 32);
-    const int rbase = row0 + 16 * wave + 4 * g;  // rows of acc_o[.][i] are rbase + i
-    if (a.n_split == 1) {
-        float inv[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float l = __shfl(lsum, 4 * g + i);
-            inv[i] = l > 0.0f ? 1.0f / l : 0.0f;
-        }
+    for (int rt = 0; rt < RT; rt++) {
+        float lsum = l_run[rt];
+        lsum += __shfl_xor(lsum, 16);
+        lsum += __shfl_xor(lsum, 32);
+        const int rbase = wrow0 + 16 * rt + 4 * g;  // rows of acc_o[rt][.][i] are rbase + i
+        if (a.n_split == 1) {
+            float inv[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int row = rbase + i;
-            if (row >= a.R) continue;
-            f16* orow = a.out + ((int64_t)(h * a.G + row % a.G) * a.Tq + row / a.G) * D;
+            for (int i = 0; i < 4; i++) {
+                const float l = __shfl(lsum, 4 * g + i);
+                inv[i] = l > 0.0f ? 1.0f / l : 0.0f;
+            }
 #pragma unroll
-            for (int mm = 0; mm < NT; mm++)
-                orow[v_logical_dim(16 * mm + r16, D, BITS)] = (f16)(acc_o[mm][i] * inv[i]);
-        }
-    } else {
-        const int64_t pbase = ((int64_t)h * a.n_split + sp) * a.R;
-        if (g == 0 && row_ok) a.part_ml[pbase + rho] = float2{m_run, lsum};
+            for (int i = 0; i < 4; i++) {
+                const int row = rbase + i;
+                if (row >= a.R) continue;
+                f16* orow = a.out + ((int64_t)(h * a.G + row % a.G) * a.Tq + row / a.G) * D;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int row = rbase + i;
-            if (row >= a.R) continue;
-            float* prow = a.part_o + (pbase + row) * D;
+                for (int mm = 0; mm < NT; mm++)
+                    orow[v_logical_dim(16 * mm + r16, D, BITS)] = (f16)(acc_o[rt][mm][i] * inv[i]);
+            }
+        } else {
+            const int64_t pbase = ((int64_t)h * a.n_split + sp) * a.PR - a.prow0;
+            const int rho = wrow0 + 16 * rt + r16;
+            if (g == 0 && rho < a.R) a.part_ml[pbase + rho] = float2{m_run[rt], lsum};
 #pragma unroll
-            for (int mm = 0; mm < NT; mm++) prow[v_logical_dim(16 * mm + r16, D, BITS)] = acc_o[mm][i];
+            for (int i = 0; i < 4; i++) {
+                const int row = rbase + i;
+                if (row >= a.R) continue;
+                float* prow = a.part_o + (pbase + row) * D;
+#pragma unroll
+                for (int mm = 0; mm < NT; mm++)
+                    prow[v_logical_dim(16 * mm + r16, D, BITS)] = acc_o[rt][mm][i];
+            }
         }
     }
 }
 
-template <int BITS, int D>
+template <int BITS, int D, int RT>
 __global__ __launch_bounds__(64 * kBlockWaves, 1) void attend_block_kernel(BlockArgs a) {
-    using S = BlockShape<D>;
-    __shared__ __attribute__((aligned(16))) f16 sK[S::KT * D];
-    __shared__ __attribute__((aligned(16))) f16 sV[S::KT * D];
+    // two buffers, each a K and a V tile of KT keys in fp16 (~130 KB)
+    extern __shared__ __attribute__((aligned(16))) char lds_buf[];
     if (BITS == 16 || *a.fast_flag != 0)
-        block_body<BITS, D, kBlockWaves, true>(a, sK, sV);
+        block_body<BITS, D, RT, true>(a, lds_buf);
     else
-        block_body<BITS, D, kBlockWaves, false>(a, sK, sV);
+        block_body<BITS, D, RT, false>(a, lds_buf);
+}
+
+template <int BITS, int D, int RT>
+static int launch_block_rt(KVCache& cc, BlockArgs& a, int n_qt, hipStream_t stream) {
+    const size_t shmem = (size_t)2 * BlockShape<D>::BUF;
+    static bool attr_set = false;
+    if (!attr_set) {
+        QW_HIP_CHECK(hipFuncSetAttribute((const void*)attend_block_kernel<BITS, D, RT>,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem));
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((attend_block_kernel<BITS, D, RT>), dim3(a.n_split, n_qt, cc.hkv),
+                       dim3(64 * kBlockWaves), shmem, stream, a);
+    QW_HIP_CHECK(hipGetLastError());
+    return QW_OK;
+}
+
+// Row tiles a wave owns: the fewest workgroup rounds on 256 CUs (one
+// workgroup a CU), weighing the larger RT's longer rounds.
+#ifndef QW_BLOCK_RT
+#define QW_BLOCK_RT 0  // 0: automatic; 1..3 forces the row tiles a wave owns
+#endif
+#ifndef QW_BLOCK_MAX_RT
+#define QW_BLOCK_MAX_RT 1  // RT >= 2 exceeds the 256-register budget of two waves a SIMD
+#endif
+static int pick_rt(int R, int hkv) {
+    if (QW_BLOCK_RT > 0) return QW_BLOCK_RT;
+    // up to 192 rows a head: one query tile, so the K/V tiles are dequantized
+    // once (verify blocks; the key split fills the CUs)
+    if (R <= 16 * kBlockWaves * QW_BLOCK_MAX_RT) return (R + 16 * kBlockWaves - 1) / (16 * kBlockWaves);
+    int best = 1;
+    double best_cost = 1e30;
+    for (int rt = 1; rt <= QW_BLOCK_MAX_RT; rt++) {
+        const int wg_rows = 16 * kBlockWaves * rt;
+        const int units = ((R + wg_rows - 1) / wg_rows) * hkv;
+        const int rounds = (units + 255) / 256;
+        // a round costs about RT (MFMA work a wave) plus a fixed dequant share
+        const double cost = rounds * (rt + 0.5);
+        if (cost < best_cost - 1e-9) {
+            best_cost = cost;
+            best = rt;
+        }
+    }
+    return best;
+}
+
+template <int BITS, int D>
+static int launch_one(KVCache& cc, BlockArgs a, int rt, int n_qt, hipStream_t stream) {
+    int rc = QW_OK;
+    if constexpr (QW_BLOCK_MAX_RT >= 3 || QW_BLOCK_RT == 3) {
+        if (rt == 3) rc = launch_block_rt<BITS, D, 3>(cc, a, n_qt, stream);
+    }
+    if constexpr (QW_BLOCK_MAX_RT >= 2 || QW_BLOCK_RT == 2) {
+        if (rt == 2) rc = launch_block_rt<BITS, D, 2>(cc, a, n_qt, stream);
+    }
+    if (rt == 1) rc = launch_block_rt<BITS, D, 1>(cc, a, n_qt, stream);
+    return rc;
+}
+
+// Splits `n_tiles` key tiles into about `want` parts of at least 4 tiles.
+static void split_keys(int n_tiles, int want, int* n_split, int* tps) {
+    int ns = std::max(1, std::min({want, (n_tiles + 3) / 4, 256}));
+    *tps = (n_tiles + ns - 1) / ns;
+    *n_split = (n_tiles + *tps - 1) / *tps;
 }
 
 template <int BITS, int D>
 static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float scale, bool causal,
                              f16* out, hipStream_t stream) {
     using S = BlockShape<D>;
-    constexpr int NW = kBlockWaves;
     const int T = cc.offset;
     const int R = G * Tq;
-    const int n_qt = (R + 16 * NW - 1) / (16 * NW);
+    const int rt = pick_rt(R, cc.hkv);
+    const int wg_rows = 16 * kBlockWaves * rt;
+    const int n_qt = (R + wg_rows - 1) / wg_rows;
     const int n_tiles = (T + S::KT - 1) / S::KT;
-    // Split the keys only while the (query tile, head) grid leaves CUs idle;
-    // at least 4 tiles a split, at most 256 partials a row.
     const int units = n_qt * cc.hkv;
-    int n_split = 1;
-    if (units < 256)
-        n_split = std::max(1, std::min({256 / units, (n_tiles + 3) / 4, 256}));
-    const int tps = (n_tiles + n_split - 1) / n_split;
-    n_split = (n_tiles + tps - 1) / tps;
 
     BlockArgs a;
     a.k_data = (const uint32_t*)cc.k_data;
@@ -381,23 +545,49 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     a.G = G;
     a.R = R;
     a.causal = causal ? 1 : 0;
-    a.n_split = n_split;
-    a.tiles_per_split = tps;
     a.scale_h = (float)(f16)scale;
-    if (n_split > 1) {
-        const size_t o_bytes = (size_t)cc.hkv * n_split * R * D * sizeof(float);
-        const size_t need = o_bytes + (size_t)cc.hkv * n_split * R * sizeof(float2);
-        int rc = cc.ensure_workspace(need);
+    a.qt0 = 0;
+    a.prow0 = 0;
+    a.PR = R;
+
+    // Plan (one workgroup a CU, 256 CUs): query tiles that fill whole rounds
+    // run unsplit and write their rows; the rest (all of them when fewer than
+    // 256 units) split the keys so that about 256 workgroups run, and go
+    // through fp32 partials and the merge kernel.
+    int q_main = 0;
+    if (units >= 256 && 256 % cc.hkv == 0) q_main = (units / 256) * (256 / cc.hkv);
+    q_main = std::min(q_main, n_qt);
+    int rc;
+    if (q_main > 0) {
+        BlockArgs m = a;
+        m.n_split = 1;
+        m.tiles_per_split = n_tiles;
+        rc = launch_one<BITS, D>(cc, m, rt, q_main, stream);
         if (rc) return rc;
-        a.part_o = (float*)cc.ws;
-        a.part_ml = (float2*)((char*)cc.ws + o_bytes);
     }
-    hipLaunchKernelGGL((attend_block_kernel<BITS, D>), dim3(n_split, n_qt, cc.hkv),
-                       dim3(64 * NW), 0, stream, a);
-    QW_HIP_CHECK(hipGetLastError());
+    const int q_tail = n_qt - q_main;
+    if (q_tail == 0) return QW_OK;
+    int n_split, tps;
+    split_keys(n_tiles, std::max(1, 256 / (q_tail * cc.hkv)), &n_split, &tps);
+    BlockArgs t = a;
+    t.qt0 = q_main;
+    t.n_split = n_split;
+    t.tiles_per_split = tps;
+    t.prow0 = q_main * wg_rows;
+    t.PR = R - t.prow0;
+    if (n_split > 1) {
+        const size_t o_bytes = (size_t)cc.hkv * n_split * t.PR * D * sizeof(float);
+        const size_t need = o_bytes + (size_t)cc.hkv * n_split * t.PR * sizeof(float2);
+        rc = cc.ensure_workspace(need);
+        if (rc) return rc;
+        t.part_o = (float*)cc.ws;
+        t.part_ml = (float2*)((char*)cc.ws + o_bytes);
+    }
+    rc = launch_one<BITS, D>(cc, t, rt, q_tail, stream);
+    if (rc) return rc;
     if (n_split > 1)
-        return launch_partial_merge(a.part_o, a.part_ml, n_split, R, R, cc.hkv, D, G, Tq, out,
-                                    stream);
+        return launch_partial_merge(t.part_o, t.part_ml, n_split, t.PR, t.prow0, t.PR, cc.hkv, D,
+                                    G, Tq, out, stream);
     return QW_OK;
 }
 

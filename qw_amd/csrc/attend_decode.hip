@@ -593,8 +593,8 @@ constexpr int kMergeMaxPer = 64;  // partials a wave sums (nc <= 256)
 
 __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ part_o,
                                                            const float2* __restrict__ part_ml,
-                                                           int nc, int rstride, int D, int G,
-                                                           int Tq, f16* __restrict__ out) {
+                                                           int nc, int rstride, int row0, int D,
+                                                           int G, int Tq, f16* __restrict__ out) {
     const int row = blockIdx.x, h = blockIdx.y, d = blockIdx.z * 64 + (threadIdx.x & 63);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t base = (int64_t)h * nc * rstride + row;
@@ -635,7 +635,8 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
     if (wave == 0) {
         const float O = (sm[0][0][lane] + sm[0][1][lane]) + (sm[0][2][lane] + sm[0][3][lane]);
         const float L = (sm[1][0][lane] + sm[1][1][lane]) + (sm[1][2][lane] + sm[1][3][lane]);
-        const int qh = h * G + row % G, qr = row / G;
+        const int orow = row0 + row;  // row index r * G + head-in-group
+        const int qh = h * G + orow % G, qr = orow / G;
         out[((int64_t)qh * Tq + qr) * D + d] = (f16)(L > 0.0f ? O / L : 0.0f);
     }
 }
@@ -688,15 +689,48 @@ static int launch_decode_bits(KVCache& cc, const f16* q, int G, int Tq, float sc
     hipLaunchKernelGGL((attend_decode_kernel<BITS, D>), dim3(nc, cc.hkv), dim3(64 * NW), shmem,
                        stream, a);
     QW_HIP_CHECK(hipGetLastError());
-    return launch_partial_merge(a.part_o, a.part_ml, nc, 16, a.R, cc.hkv, D, G, Tq, out, stream);
+    return launch_partial_merge(a.part_o, a.part_ml, nc, 16, 0, a.R, cc.hkv, D, G, Tq, out, stream);
 }
 
-int launch_partial_merge(const float* part_o, const float2* part_ml, int nc, int rstride, int R,
-                         int hkv, int D, int G, int Tq, f16* out, hipStream_t stream) {
+// The same merge for many rows and few partials (block kernels' key splits):
+// one thread an output element, a loop over the nc partials.
+__global__ __launch_bounds__(256) void merge_rows_kernel(const float* __restrict__ part_o,
+                                                         const float2* __restrict__ part_ml,
+                                                         int nc, int rstride, int row0, int R,
+                                                         int D, int G, int Tq,
+                                                         f16* __restrict__ out) {
+    const int h = blockIdx.y;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int row = (int)(idx / D), d = (int)(idx % D);
+    if (row >= R) return;
+    const int64_t base = (int64_t)h * nc * rstride + row;
+    float M = -INFINITY;
+    for (int c = 0; c < nc; c++) M = fmaxf(M, part_ml[base + (int64_t)c * rstride].x);
+    float acc = 0.0f, L = 0.0f;
+    for (int c = 0; c < nc; c++) {
+        const float2 ml = part_ml[base + (int64_t)c * rstride];
+        const float f = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((ml.x - M) * kLog2e);
+        acc = __builtin_fmaf(f, part_o[(base + (int64_t)c * rstride) * D + d], acc);
+        L = __builtin_fmaf(f, ml.y, L);
+    }
+    const int orow = row0 + row;
+    const int qh = h * G + orow % G, qr = orow / G;
+    out[((int64_t)qh * Tq + qr) * D + d] = (f16)(L > 0.0f ? acc / L : 0.0f);
+}
+
+int launch_partial_merge(const float* part_o, const float2* part_ml, int nc, int rstride, int row0,
+                         int R, int hkv, int D, int G, int Tq, f16* out, hipStream_t stream) {
     QW_REQUIRE(nc >= 1 && nc <= 4 * kMergeMaxPer, QW_ERR_INVALID_ARGUMENT,
                "merge: partial count out of range");
+    if (nc <= 8 && R > 16) {
+        const int64_t n = (int64_t)R * D;
+        hipLaunchKernelGGL(merge_rows_kernel, dim3((unsigned)((n + 255) / 256), hkv), dim3(256), 0,
+                           stream, part_o, part_ml, nc, rstride, row0, R, D, G, Tq, out);
+        QW_HIP_CHECK(hipGetLastError());
+        return QW_OK;
+    }
     hipLaunchKernelGGL(decode_merge_kernel, dim3(R, hkv, D / 64), dim3(256), 0, stream, part_o,
-                       part_ml, nc, rstride, D, G, Tq, out);
+                       part_ml, nc, rstride, row0, D, G, Tq, out);
     QW_HIP_CHECK(hipGetLastError());
     return QW_OK;
 }

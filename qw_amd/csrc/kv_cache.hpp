@@ -96,9 +96,9 @@ int launch_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float
 // G * n_rows > 16 query rows per KV head (verify blocks, prefill chunks).
 int launch_block_attention(KVCache& c, const f16* q, int G, int n_rows, float scale, bool causal,
                            f16* out, hipStream_t stream);
-// Split-K merge: out[row] = sum_c e^(m_c - M) O_c / sum_c e^(m_c - M) l_c over
-// nc partials of [rstride][D] fp32 rows per KV head.
-int launch_partial_merge(const float* part_o, const float2* part_ml, int nc, int rstride, int R,
-                         int hkv, int D, int G, int Tq, f16* out, hipStream_t stream);
+// Split-K merge: out[row0 + row] = sum_c e^(m_c - M) O_c / sum_c e^(m_c - M) l_c
+// over nc partials of [rstride][D] fp32 rows per KV head, rows 0 .. R-1.
+int launch_partial_merge(const float* part_o, const float2* part_ml, int nc, int rstride, int row0,
+                         int R, int hkv, int D, int G, int Tq, f16* out, hipStream_t stream);
 
 }  // namespace qw
