@@ -29,6 +29,7 @@
 #include <type_traits>
 
 #include "dequant.hpp"
+#include "quant.hpp"
 #include "kv_cache.hpp"
 
 namespace qw {
@@ -641,10 +642,12 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
     }
 }
 
+// Split-K attention of the Tq rows over the first T cached keys: launches the
+// decode kernel and returns its partials (nc per KV head, 16 rows apart).
 template <int BITS, int D>
-static int launch_decode_bits(KVCache& cc, const f16* q, int G, int Tq, float scale,
-                              bool causal, f16* out, hipStream_t stream) {
-    const int T = cc.offset;
+static int launch_decode_partials(KVCache& cc, const f16* q, int G, int Tq, int T, float scale,
+                                  bool causal, int* nc_out, float** po, float2** pml,
+                                  hipStream_t stream) {
     const int n_sub = (T + 31) / 32;
     // Sub-chunks a wave owns: 4-bit rows are small enough to keep 4 in flight.
     // Sub-chunks a wave keeps in flight per round, and workgroups per KV head:
@@ -689,7 +692,22 @@ static int launch_decode_bits(KVCache& cc, const f16* q, int G, int Tq, float sc
     hipLaunchKernelGGL((attend_decode_kernel<BITS, D>), dim3(nc, cc.hkv), dim3(64 * NW), shmem,
                        stream, a);
     QW_HIP_CHECK(hipGetLastError());
-    return launch_partial_merge(a.part_o, a.part_ml, nc, 16, 0, a.R, cc.hkv, D, G, Tq, out, stream);
+    *nc_out = nc;
+    *po = a.part_o;
+    *pml = a.part_ml;
+    return QW_OK;
+}
+
+template <int BITS, int D>
+static int launch_decode_bits(KVCache& cc, const f16* q, int G, int Tq, float scale,
+                              bool causal, f16* out, hipStream_t stream) {
+    int nc = 0;
+    float* po = nullptr;
+    float2* pml = nullptr;
+    int rc = launch_decode_partials<BITS, D>(cc, q, G, Tq, cc.offset, scale, causal, &nc, &po,
+                                             &pml, stream);
+    if (rc) return rc;
+    return launch_partial_merge(po, pml, nc, 16, 0, G * Tq, cc.hkv, D, G, Tq, out, stream);
 }
 
 // The same merge for many rows and few partials (block kernels' key splits):
@@ -764,6 +782,211 @@ int KVCache::attention(const void* q, int n_q_heads, int n_rows, float scale, bo
     return launch_attention(*this, q, n_q_heads, n_rows, scale, causal, out, stream);
 }
 
+// ---------------------------------------------------- fused decode append
+//
+// One decode row on an affine cache: the decode kernel attends the cached
+// prefix (t keys) and this kernel quantizes-and-appends the new token (MLX
+// quantize, quant.hpp) while merging the split-K partials, folding the new key
+// in as one more partial: (m, l, O) = (f16(q'.k), 1, v), k and v in their
+// dequantized form (the reference attends appended rows dequantized,
+// cache.rs:2723, :3508). This replaces the separate append launch on the
+// decode path; the cache contents it writes equal the append kernel's.
+// grid (G, kv_heads, D/64), 4 waves: workgroup (g, h, b) writes out[h*G + g]
+// dims [64b, 64b+64); the g == 0 workgroups also write group b of the new
+// K row (wave b) and of the new V block slot (wave 0).
+struct MergeAppendArgs {
+    const float* part_o;
+    const float2* part_ml;
+    int nc;                 // partials a KV head (0: empty prefix)
+    const f16* q;           // [hq][1][D]
+    const f16* k_new;       // [hkv][1][D]
+    const f16* v_new;
+    int G, t, cap;          // t: index of the new token
+    float scale_h;          // f16(scale)
+    uint32_t* k_codes;
+    uint32_t* k_params;
+    uint32_t* v_codes;
+    f16* v_params;
+    int* fast_flag;
+    f16* out;               // [hq][1][D]
+};
+
+__device__ __forceinline__ void wave_minmax(float& mn, float& mx) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const float omn = __shfl_xor(mn, off), omx = __shfl_xor(mx, off);
+        mn = omn < mn ? omn : mn;
+        mx = mx < omx ? omx : mx;
+    }
+}
+
+template <int BITS, int D>
+__global__ __launch_bounds__(256) void merge_append_kernel(MergeAppendArgs a) {
+    constexpr int NG = D / 64;
+    const int row = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int d = b * 64 + lane;
+    const int qh = h * a.G + row;
+    // ---- every load first: partials (wave w: c = w, w+4, ...), the new K
+    // row and q (thread = dim), the new V group b (lane = dim)
+    const int64_t base = (int64_t)h * a.nc * 16 + row;
+    float v[kMergeMaxPer];
+    float2 ml[kMergeMaxPer];
+#pragma unroll
+    for (int i = 0; i < kMergeMaxPer; i++) {
+        const int c = wave + 4 * i;
+        if (c < a.nc) {
+            ml[i] = a.part_ml[base + (int64_t)c * 16];
+            v[i] = a.part_o[(base + (int64_t)c * 16) * D + d];
+        } else {
+            ml[i] = float2{-INFINITY, 0.0f};
+            v[i] = 0.0f;
+        }
+    }
+    const bool kdim = (int)threadIdx.x < D;
+    const float kx = kdim ? (float)a.k_new[(int64_t)h * D + threadIdx.x] : 0.0f;
+    const float qx = kdim ? (float)a.q[(int64_t)qh * D + threadIdx.x] : 0.0f;
+    const float vx = (float)a.v_new[(int64_t)h * D + d];
+
+    // ---- new key: wave w < NG quantizes K group w and forms its share of
+    // q' . k (q' = f16(f16(scale) * q), as MLX scales q)
+    __shared__ float sm_s[4];
+    float kcode = 0.0f;
+    f16 ks = (f16)0.0f, kb = (f16)0.0f;
+    if (wave < NG) {
+        float mn = kx, mx = kx;
+        wave_minmax(mn, mx);
+        const AffineGroup g = affine_group(mn, mx, BITS);
+        kcode = affine_code(kx, g, BITS);
+        ks = (f16)g.scale;
+        kb = (f16)g.bias;
+        const float qs = (float)(f16)((float)(f16)a.scale_h * qx);
+        float sp = qs * affine_dequant(kcode, ks, kb);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) sp += __shfl_xor(sp, off);
+        if (lane == 0) sm_s[wave] = sp;
+    }
+    // ---- new value: group b, every wave (lane = dim d)
+    float vmn = vx, vmx = vx;
+    wave_minmax(vmn, vmx);
+    const AffineGroup gv = affine_group(vmn, vmx, BITS);
+    const float vcode = affine_code(vx, gv, BITS);
+    const f16 vs = (f16)gv.scale, vbias = (f16)gv.bias;
+    const float vd = affine_dequant(vcode, vs, vbias);
+
+    // ---- merge: M over the partials and the new score
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kMergeMaxPer; i++) m = fmaxf(m, ml[i].x);
+    __shared__ float sm_m[4];
+    __shared__ float sm[2][4][64];
+    if (lane == 0) sm_m[wave] = m;
+    __syncthreads();
+    float S = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NG; w++) S += sm_s[w];
+    const float s_new = (float)(f16)S;  // MLX rounds the score to fp16
+    m = fmaxf(fmaxf(fmaxf(sm_m[0], sm_m[1]), fmaxf(sm_m[2], sm_m[3])), s_new);
+    float o = 0.0f, l = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMergeMaxPer; i++) {
+        const float w = ml[i].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((ml[i].x - m) * kLog2e);
+        o = __builtin_fmaf(w, v[i], o);
+        l = __builtin_fmaf(w, ml[i].y, l);
+    }
+    sm[0][wave][lane] = o;
+    sm[1][wave][lane] = l;
+    __syncthreads();
+    if (wave == 0) {
+        const float wn = __builtin_amdgcn_exp2f((s_new - m) * kLog2e);
+        const float O = (sm[0][0][lane] + sm[0][1][lane]) + (sm[0][2][lane] + sm[0][3][lane]) + wn * vd;
+        const float L = (sm[1][0][lane] + sm[1][1][lane]) + (sm[1][2][lane] + sm[1][3][lane]) + wn;
+        a.out[(int64_t)qh * D + d] = (f16)(O / L);
+    }
+
+    // ---- append: the g == 0 workgroups write group b of the new row
+    if (row != 0) return;
+    const int t = a.t;
+    if (wave == b && wave < NG) {
+        // K: MLX packing, 32/BITS codes a word, LSB first
+        constexpr int EPW = 32 / BITS;
+        uint32_t piece = (uint32_t)kcode << (BITS * (lane % EPW));
+#pragma unroll
+        for (int off = 1; off < EPW; off <<= 1) piece |= __shfl_xor(piece, off);
+        const int64_t krow = ((int64_t)h * a.cap + t) * (D * BITS / 32);
+        if (lane % EPW == 0) a.k_codes[krow + (64 * b) / EPW + lane / EPW] = piece;
+        if (lane == 0) {
+            half2v sb;
+            sb.x = ks;
+            sb.y = kb;
+            a.k_params[((int64_t)h * a.cap + t) * NG + k_param_slot(b, NG)] =
+                __builtin_bit_cast(uint32_t, sb);
+            check_fast_scale(ks, BITS, a.fast_flag);
+        }
+    }
+    if (wave == 0) {
+        // V: key slot t % 8 of block t / 8, dim d at its lane-order slot
+        const int blk = t / 8, k = t % 8;
+        const int p = v_phys_dim(d, D, BITS);
+        uint32_t* vbp = a.v_codes + ((int64_t)h * (a.cap / 8) + blk) * (D * BITS / 4);
+        const uint32_t code = (uint32_t)vcode;
+        if constexpr (BITS == 4) {
+            const int sh = 4 * v4_nibble_pos(k);
+            vbp[p] = (vbp[p] & ~(0xFu << sh)) | (code << sh);
+        } else {
+            const int idx = 2 * p + (k >> 2), sh = 8 * (k & 3);
+            vbp[idx] = (vbp[idx] & ~(0xFFu << sh)) | (code << sh);
+        }
+        if (lane == 0) {
+            f16* vp = a.v_params + (((int64_t)h * (a.cap / 8) + blk) * NG + b) * 16;
+            vp[k] = vs;
+            vp[8 + k] = vbias;
+            check_fast_scale(vs, BITS, a.fast_flag);
+        }
+    }
+}
+
+template <int BITS, int D>
+static int launch_decode_fused(KVCache& cc, const f16* q, int G, const f16* k_new,
+                               const f16* v_new, float scale, f16* out, hipStream_t stream) {
+    MergeAppendArgs m;
+    m.nc = 0;
+    m.part_o = nullptr;
+    m.part_ml = nullptr;
+    const int t = cc.offset;
+    if (t > 0) {
+        float* po = nullptr;
+        float2* pml = nullptr;
+        int rc = launch_decode_partials<BITS, D>(cc, q, G, 1, t, scale, false, &m.nc, &po, &pml,
+                                                 stream);
+        if (rc) return rc;
+        m.part_o = po;
+        m.part_ml = pml;
+    }
+    m.q = q;
+    m.k_new = k_new;
+    m.v_new = v_new;
+    m.G = G;
+    m.t = t;
+    m.cap = cc.cap;
+    m.scale_h = (float)(f16)scale;
+    m.k_codes = (uint32_t*)cc.k_data;
+    m.k_params = cc.k_params;
+    m.v_codes = (uint32_t*)cc.v_data;
+    m.v_params = (f16*)cc.v_params;
+    m.fast_flag = cc.fast_flag;
+    m.out = out;
+    hipLaunchKernelGGL((merge_append_kernel<BITS, D>), dim3(G, cc.hkv, D / 64), dim3(256), 0,
+                       stream, m);
+    QW_HIP_CHECK(hipGetLastError());
+    cc.offset = t + 1;
+    return QW_OK;
+}
+
+#ifndef QW_FUSED_DECODE_APPEND
+#define QW_FUSED_DECODE_APPEND 1
+#endif
+
 int KVCache::update_and_attention(const void* q, int n_q_heads, int n_rows, const void* k_new,
                                   const void* v_new, float scale, bool causal, void* out,
                                   hipStream_t stream) {
@@ -771,6 +994,25 @@ int KVCache::update_and_attention(const void* q, int n_q_heads, int n_rows, cons
                "update_and_attention: null pointer");
     QW_REQUIRE(n_q_heads > 0 && n_q_heads % hkv == 0 && n_rows > 0, QW_ERR_INVALID_ARGUMENT,
                "update_and_attention: bad head or row geometry");
+    const int G = n_q_heads / hkv;
+    if (QW_FUSED_DECODE_APPEND && affine() && n_rows == 1 && G <= 16) {
+        // decode: the append rides in the split-K merge (one launch fewer)
+        DeviceGuard dg(device);
+        QW_REQUIRE(dg.ok, QW_ERR_HIP, "update_and_attention: hipSetDevice failed");
+        if (offset + 1 > cap) {
+            int rc = reserve(std::max(offset + 1, cap + cap / 2), stream);
+            if (rc) return rc;
+        }
+        const f16* qq = (const f16*)q;
+        const f16* kn = (const f16*)k_new;
+        const f16* vn = (const f16*)v_new;
+        f16* oo = (f16*)out;
+        if (D == 256)
+            return bits == 4 ? launch_decode_fused<4, 256>(*this, qq, G, kn, vn, scale, oo, stream)
+                             : launch_decode_fused<8, 256>(*this, qq, G, kn, vn, scale, oo, stream);
+        return bits == 4 ? launch_decode_fused<4, 128>(*this, qq, G, kn, vn, scale, oo, stream)
+                         : launch_decode_fused<8, 128>(*this, qq, G, kn, vn, scale, oo, stream);
+    }
     int rc = update(k_new, v_new, n_rows, stream);
     if (rc) return rc;
     return launch_attention(*this, q, n_q_heads, n_rows, scale, causal, out, stream);

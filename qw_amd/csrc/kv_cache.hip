@@ -14,6 +14,7 @@
 #include <string>
 
 #include "kv_cache.hpp"
+#include "quant.hpp"
 
 namespace qw {
 
@@ -197,14 +198,6 @@ int KVCache::trim(int n) {
 // Codes go through LDS so the V block words (8 keys per dim) are assembled
 // by one thread each: no two threads write the same word.
 
-// Clears *fast_flag when the stored fp16 scale is outside the exact range of
-// the fused kernels' 2-op dequant (dequant.hpp).
-__device__ inline void check_fast_scale(f16 scale, int bits, int* fast_flag) {
-    const uint32_t a = __builtin_bit_cast(uint16_t, scale) & 0x7FFFu;
-    const uint32_t lo = bits == 4 ? 0x1400u : 0u;
-    if (a < lo || a >= 0x5400u) *fast_flag = 0;
-}
-
 template <int D>
 __device__ inline void quantize_row(const f16* __restrict__ src, int bits, uint8_t* lds_codes,
                                     half2v* sb_out /* [D/64] (scale, bias) */, int* fast_flag) {
@@ -227,29 +220,13 @@ __device__ inline void quantize_row(const f16* __restrict__ src, int bits, uint8
         mx = mx < omx ? omx : mx;
         mn = omn < mn ? omn : mn;
     }
-    const float n_bins = (float)((1 << bits) - 1);
-    const float eps = 1e-7f;
-    const bool neg_side = fabsf(mn) > fabsf(mx);
-    float scale = (mx - mn) / n_bins;
-    scale = scale < eps ? eps : scale;
-    scale = neg_side ? scale : -scale;
-    const float edge = neg_side ? mn : mx;
-    const float q0 = __builtin_rintf(edge / scale);
-    float bias = 0.0f;
-    if (q0 != 0.0f) {
-        scale = edge / q0;
-        bias = edge;
-    }
+    const AffineGroup q = affine_group(mn, mx, bits);
 #pragma unroll
-    for (int i = 0; i < VPL; i++) {
-        float c = __builtin_rintf((x[i] - bias) / scale);
-        c = c < 0.0f ? 0.0f : (c > n_bins ? n_bins : c);
-        lds_codes[lane * VPL + i] = (uint8_t)c;
-    }
+    for (int i = 0; i < VPL; i++) lds_codes[lane * VPL + i] = (uint8_t)affine_code(x[i], q, bits);
     if ((lane % LPG) == 0) {
         half2v sb;
-        sb.x = (f16)scale;
-        sb.y = (f16)bias;
+        sb.x = (f16)q.scale;
+        sb.y = (f16)q.bias;
         sb_out[lane / LPG] = sb;
         check_fast_scale(sb.x, bits, fast_flag);
     }

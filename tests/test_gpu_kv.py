@@ -244,20 +244,57 @@ def test_block_causal_rows_are_prefix_independent(oracle_lib):
         assert_close(blk[:, i:i + 1], row, f"row {i}: block vs decode")
 
 
-def test_attention_without_append_equals_fused_call(oracle_lib):
+@pytest.mark.parametrize("bits", [4, 8])
+def test_attention_without_append_equals_fused_call(oracle_lib, bits):
+    """append-then-attend (the decode path folds the new token in during the
+    split-K merge) equals attending a cache that already holds it: the same
+    stored codes bit for bit, outputs within the stated tolerance."""
     import qw_amd
 
-    r = rng(91)
+    r = rng(91 + bits)
     k, v = _kv(r, 4, 3000, 256)
     q = r.standard_normal((24, 1, 256)).astype(np.float16)
-    a = qw_amd.KVCache("affine4", 4, 256)
+    a = qw_amd.KVCache(_mode(bits), 4, 256)
     a.update(_gpu(k)[None], _gpu(v)[None])
-    o1 = a.attention(_gpu(q)[None], 1.0 / 16)
-    b = qw_amd.KVCache("affine4", 4, 256)
+    o1 = _np(a.attention(_gpu(q)[None], 1.0 / 16))[0]
+    b = qw_amd.KVCache(_mode(bits), 4, 256)
     b.update(_gpu(k[:, :2999])[None], _gpu(v[:, :2999])[None])
-    o2 = b.update_and_attention(_gpu(q)[None], _gpu(k[:, 2999:])[None], _gpu(v[:, 2999:])[None],
-                                1.0 / 16)
-    assert torch.equal(o1, o2)
+    o2 = _np(b.update_and_attention(_gpu(q)[None], _gpu(k[:, 2999:])[None],
+                                    _gpu(v[:, 2999:])[None], 1.0 / 16))[0]
+    for name, t in a.snapshot_tensors().items():
+        assert torch.equal(t, b.snapshot_tensors()[name]), name
+    assert_close(o2, o1, f"bits={bits} fused append vs cached")
+
+
+@pytest.mark.parametrize("bits,D", [(4, 256), (8, 256), (4, 128), (8, 128)])
+def test_decode_steps_store_the_same_codes_as_a_bulk_append(oracle_lib, bits, D):
+    """Token-by-token decode (append fused into the attention call), across
+    partly filled 8-key V blocks and a capacity growth, stores exactly the
+    codes one bulk append of the same rows stores; each step's output matches
+    the oracle."""
+    import qw_amd
+
+    r = rng(500 + bits + D)
+    H, hq, T0, steps = 4, 16, 61, 23
+    k, v = _kv(r, H, T0 + steps, D)
+    q = r.standard_normal((hq, steps, D)).astype(np.float16)
+    a = qw_amd.KVCache(_mode(bits), H, D, capacity=64)
+    a.update(_gpu(k[:, :T0])[None], _gpu(v[:, :T0])[None])
+    orc = oracle_lib.AffineCacheOracle(H, D, T0 + steps, bits)
+    orc.update(k[:, :T0], v[:, :T0])
+    for i in range(steps):
+        t = T0 + i
+        out = _np(a.update_and_attention(_gpu(q[:, i:i + 1])[None], _gpu(k[:, t:t + 1])[None],
+                                         _gpu(v[:, t:t + 1])[None], 1.0 / 16))[0]
+        ref = orc.update_and_attention(np.ascontiguousarray(q[:, i:i + 1]), k[:, t:t + 1],
+                                       v[:, t:t + 1], 1.0 / 16, False)
+        if i in (0, 1, steps - 1):
+            assert_close(out, ref, f"step {i}")
+    assert a.offset == T0 + steps
+    b = qw_amd.KVCache(_mode(bits), H, D)
+    b.update(_gpu(k)[None], _gpu(v)[None])
+    for name, tt in b.snapshot_tensors().items():
+        assert torch.equal(tt, a.snapshot_tensors()[name]), name
 
 
 def test_invalid_calls_raise():
