@@ -385,8 +385,9 @@ def summarize_pmc(fetch_db: str, write_db: str, out: str) -> int:
     w_scale = (COPY_BYTES / 1024.0) / copy_write
     att_k, att_fetch, n_f = pick(fetch, "attend_decode_kernel")
     _, att_write, n_w = pick(write, "attend_decode_kernel")
-    mer_k, mer_fetch, _ = pick(fetch, "decode_merge_kernel")
-    _, mer_write, _ = pick(write, "decode_merge_kernel")
+    mer_key = next(k for k in ("merge_append_kernel", "decode_merge_kernel") if any(k in n for n in fetch))
+    mer_k, mer_fetch, _ = pick(fetch, mer_key)
+    _, mer_write, _ = pick(write, mer_key)
     traffic = (att_fetch * f_scale + att_write * w_scale) * 1024.0
     alg = 32769 * HKV * kv_bytes_per_token_head(4) + 2 * HQ * D * 2
     lines = [

@@ -710,8 +710,10 @@ static int launch_decode_bits(KVCache& cc, const f16* q, int G, int Tq, float sc
     return launch_partial_merge(po, pml, nc, 16, 0, G * Tq, cc.hkv, D, G, Tq, out, stream);
 }
 
-// The same merge for many rows and few partials (block kernels' key splits):
-// one thread an output element, a loop over the nc partials.
+// The same merge for many rows (block kernels' key splits): one thread an
+// output element, every (m, l) and O value of its up to MAXN partials loaded
+// before the first use (one memory round trip).
+template <int MAXN>
 __global__ __launch_bounds__(256) void merge_rows_kernel(const float* __restrict__ part_o,
                                                          const float2* __restrict__ part_ml,
                                                          int nc, int rstride, int row0, int R,
@@ -722,14 +724,27 @@ __global__ __launch_bounds__(256) void merge_rows_kernel(const float* __restrict
     const int row = (int)(idx / D), d = (int)(idx % D);
     if (row >= R) return;
     const int64_t base = (int64_t)h * nc * rstride + row;
+    float v[MAXN];
+    float2 ml[MAXN];
+#pragma unroll
+    for (int c = 0; c < MAXN; c++) {
+        if (c < nc) {
+            ml[c] = part_ml[base + (int64_t)c * rstride];
+            v[c] = part_o[(base + (int64_t)c * rstride) * D + d];
+        } else {
+            ml[c] = float2{-INFINITY, 0.0f};
+            v[c] = 0.0f;
+        }
+    }
     float M = -INFINITY;
-    for (int c = 0; c < nc; c++) M = fmaxf(M, part_ml[base + (int64_t)c * rstride].x);
+#pragma unroll
+    for (int c = 0; c < MAXN; c++) M = fmaxf(M, ml[c].x);
     float acc = 0.0f, L = 0.0f;
-    for (int c = 0; c < nc; c++) {
-        const float2 ml = part_ml[base + (int64_t)c * rstride];
-        const float f = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((ml.x - M) * kLog2e);
-        acc = __builtin_fmaf(f, part_o[(base + (int64_t)c * rstride) * D + d], acc);
-        L = __builtin_fmaf(f, ml.y, L);
+#pragma unroll
+    for (int c = 0; c < MAXN; c++) {
+        const float f = ml[c].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((ml[c].x - M) * kLog2e);
+        acc = __builtin_fmaf(f, v[c], acc);
+        L = __builtin_fmaf(f, ml[c].y, L);
     }
     const int orow = row0 + row;
     const int qh = h * G + orow % G, qr = orow / G;
@@ -740,10 +755,15 @@ int launch_partial_merge(const float* part_o, const float2* part_ml, int nc, int
                          int R, int hkv, int D, int G, int Tq, f16* out, hipStream_t stream) {
     QW_REQUIRE(nc >= 1 && nc <= 4 * kMergeMaxPer, QW_ERR_INVALID_ARGUMENT,
                "merge: partial count out of range");
-    if (nc <= 8 && R > 16) {
+    if (R > 16 && nc <= 64) {
         const int64_t n = (int64_t)R * D;
-        hipLaunchKernelGGL(merge_rows_kernel, dim3((unsigned)((n + 255) / 256), hkv), dim3(256), 0,
-                           stream, part_o, part_ml, nc, rstride, row0, R, D, G, Tq, out);
+        const dim3 grid((unsigned)((n + 255) / 256), hkv);
+        if (nc <= 8)
+            hipLaunchKernelGGL(merge_rows_kernel<8>, grid, dim3(256), 0, stream, part_o, part_ml, nc,
+                               rstride, row0, R, D, G, Tq, out);
+        else
+            hipLaunchKernelGGL(merge_rows_kernel<64>, grid, dim3(256), 0, stream, part_o, part_ml,
+                               nc, rstride, row0, R, D, G, Tq, out);
         QW_HIP_CHECK(hipGetLastError());
         return QW_OK;
     }
