@@ -592,6 +592,15 @@ __global__ __launch_bounds__((64 * decode_waves<BITS, D>()), 1) void attend_deco
 // dim, wave w sums partials c = w, w+4, ... with every load issued up front.
 constexpr int kMergeMaxPer = 64;  // partials a wave sums (nc <= 256)
 
+// Partials a wave sums, as a compile-time bound: the smallest power of two
+// from 4 to kMergeMaxPer that covers nc / 4.
+inline int merge_per(int nc) {
+    int per = 4;
+    while (4 * per < nc) per *= 2;
+    return per;
+}
+
+template <int PER>
 __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ part_o,
                                                            const float2* __restrict__ part_ml,
                                                            int nc, int rstride, int row0, int D,
@@ -601,10 +610,10 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
     const int64_t base = (int64_t)h * nc * rstride + row;
     // One memory round: every (m, l) and O value this lane needs is loaded
     // first; the max is then exchanged through LDS.
-    float v[kMergeMaxPer];
-    float2 ml[kMergeMaxPer];
+    float v[PER];
+    float2 ml[PER];
 #pragma unroll
-    for (int i = 0; i < kMergeMaxPer; i++) {
+    for (int i = 0; i < PER; i++) {
         const int c = wave + 4 * i;
         if (c < nc) {
             ml[i] = part_ml[base + (int64_t)c * rstride];
@@ -616,7 +625,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
     }
     float m = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < kMergeMaxPer; i++) m = fmaxf(m, ml[i].x);
+    for (int i = 0; i < PER; i++) m = fmaxf(m, ml[i].x);
     __shared__ float sm_m[4];
     __shared__ float sm[2][4][64];
     if (lane == 0) sm_m[wave] = m;
@@ -624,7 +633,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
     m = fmaxf(fmaxf(sm_m[0], sm_m[1]), fmaxf(sm_m[2], sm_m[3]));
     float o = 0.0f, l = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kMergeMaxPer; i++) {
+    for (int i = 0; i < PER; i++) {
         const float w =
             ml[i].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((ml[i].x - m) * kLog2e);
         o = __builtin_fmaf(w, v[i], o);
@@ -767,8 +776,28 @@ int launch_partial_merge(const float* part_o, const float2* part_ml, int nc, int
         QW_HIP_CHECK(hipGetLastError());
         return QW_OK;
     }
-    hipLaunchKernelGGL(decode_merge_kernel, dim3(R, hkv, D / 64), dim3(256), 0, stream, part_o,
-                       part_ml, nc, rstride, row0, D, G, Tq, out);
+    const dim3 grid(R, hkv, D / 64);
+    switch (merge_per(nc)) {
+        case 4:
+            hipLaunchKernelGGL(decode_merge_kernel<4>, grid, dim3(256), 0, stream, part_o, part_ml,
+                               nc, rstride, row0, D, G, Tq, out);
+            break;
+        case 8:
+            hipLaunchKernelGGL(decode_merge_kernel<8>, grid, dim3(256), 0, stream, part_o, part_ml,
+                               nc, rstride, row0, D, G, Tq, out);
+            break;
+        case 16:
+            hipLaunchKernelGGL(decode_merge_kernel<16>, grid, dim3(256), 0, stream, part_o, part_ml,
+                               nc, rstride, row0, D, G, Tq, out);
+            break;
+        case 32:
+            hipLaunchKernelGGL(decode_merge_kernel<32>, grid, dim3(256), 0, stream, part_o, part_ml,
+                               nc, rstride, row0, D, G, Tq, out);
+            break;
+        default:
+            hipLaunchKernelGGL(decode_merge_kernel<kMergeMaxPer>, grid, dim3(256), 0, stream, part_o,
+                               part_ml, nc, rstride, row0, D, G, Tq, out);
+    }
     QW_HIP_CHECK(hipGetLastError());
     return QW_OK;
 }
@@ -831,29 +860,29 @@ struct MergeAppendArgs {
     f16* out;               // [hq][1][D]
 };
 
-__device__ __forceinline__ void wave_minmax(float& mn, float& mx) {
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const float omn = __shfl_xor(mn, off), omx = __shfl_xor(mx, off);
-        mn = omn < mn ? omn : mn;
-        mx = mx < omx ? omx : mx;
-    }
-}
-
-template <int BITS, int D>
+template <int BITS, int D, int PER>
 __global__ __launch_bounds__(256) void merge_append_kernel(MergeAppendArgs a) {
     constexpr int NG = D / 64;
     const int row = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int d = b * 64 + lane;
     const int qh = h * a.G + row;
-    // ---- every load first: partials (wave w: c = w, w+4, ...), the new K
-    // row and q (thread = dim), the new V group b (lane = dim)
+    const int t = a.t;
+    // ---- every load first: the V word the new code goes into (row-0
+    // workgroups, wave 0: read-modify-write of the 8-key block slot), the
+    // partials (wave w: c = w, w+4, ...), the new K row and q (thread = dim),
+    // the new V group b (lane = dim)
+    const int vblk = t / 8, vk = t % 8;
+    const int vp = v_phys_dim(d, D, BITS);
+    uint32_t* vbp = a.v_codes + ((int64_t)h * (a.cap / 8) + vblk) * (D * BITS / 4);
+    const int vidx = BITS == 4 ? vp : 2 * vp + (vk >> 2);
+    const bool v_writer = row == 0 && wave == 0;
+    const uint32_t vword = v_writer ? vbp[vidx] : 0u;
     const int64_t base = (int64_t)h * a.nc * 16 + row;
-    float v[kMergeMaxPer];
-    float2 ml[kMergeMaxPer];
+    float v[PER];
+    float2 ml[PER];
 #pragma unroll
-    for (int i = 0; i < kMergeMaxPer; i++) {
+    for (int i = 0; i < PER; i++) {
         const int c = wave + 4 * i;
         if (c < a.nc) {
             ml[i] = a.part_ml[base + (int64_t)c * 16];
@@ -874,21 +903,17 @@ __global__ __launch_bounds__(256) void merge_append_kernel(MergeAppendArgs a) {
     float kcode = 0.0f;
     f16 ks = (f16)0.0f, kb = (f16)0.0f;
     if (wave < NG) {
-        float mn = kx, mx = kx;
-        wave_minmax(mn, mx);
+        const float mn = wave_reduce(kx, OpMin()), mx = wave_reduce(kx, OpMax());
         const AffineGroup g = affine_group(mn, mx, BITS);
         kcode = affine_code(kx, g, BITS);
         ks = (f16)g.scale;
         kb = (f16)g.bias;
         const float qs = (float)(f16)((float)(f16)a.scale_h * qx);
-        float sp = qs * affine_dequant(kcode, ks, kb);
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) sp += __shfl_xor(sp, off);
+        const float sp = wave_reduce(qs * affine_dequant(kcode, ks, kb), OpSum());
         if (lane == 0) sm_s[wave] = sp;
     }
     // ---- new value: group b, every wave (lane = dim d)
-    float vmn = vx, vmx = vx;
-    wave_minmax(vmn, vmx);
+    const float vmn = wave_reduce(vx, OpMin()), vmx = wave_reduce(vx, OpMax());
     const AffineGroup gv = affine_group(vmn, vmx, BITS);
     const float vcode = affine_code(vx, gv, BITS);
     const f16 vs = (f16)gv.scale, vbias = (f16)gv.bias;
@@ -897,7 +922,7 @@ __global__ __launch_bounds__(256) void merge_append_kernel(MergeAppendArgs a) {
     // ---- merge: M over the partials and the new score
     float m = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < kMergeMaxPer; i++) m = fmaxf(m, ml[i].x);
+    for (int i = 0; i < PER; i++) m = fmaxf(m, ml[i].x);
     __shared__ float sm_m[4];
     __shared__ float sm[2][4][64];
     if (lane == 0) sm_m[wave] = m;
@@ -909,7 +934,7 @@ __global__ __launch_bounds__(256) void merge_append_kernel(MergeAppendArgs a) {
     m = fmaxf(fmaxf(fmaxf(sm_m[0], sm_m[1]), fmaxf(sm_m[2], sm_m[3])), s_new);
     float o = 0.0f, l = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kMergeMaxPer; i++) {
+    for (int i = 0; i < PER; i++) {
         const float w = ml[i].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((ml[i].x - m) * kLog2e);
         o = __builtin_fmaf(w, v[i], o);
         l = __builtin_fmaf(w, ml[i].y, l);
@@ -926,7 +951,6 @@ __global__ __launch_bounds__(256) void merge_append_kernel(MergeAppendArgs a) {
 
     // ---- append: the g == 0 workgroups write group b of the new row
     if (row != 0) return;
-    const int t = a.t;
     if (wave == b && wave < NG) {
         // K: MLX packing, 32/BITS codes a word, LSB first
         constexpr int EPW = 32 / BITS;
@@ -944,23 +968,20 @@ __global__ __launch_bounds__(256) void merge_append_kernel(MergeAppendArgs a) {
             check_fast_scale(ks, BITS, a.fast_flag);
         }
     }
-    if (wave == 0) {
+    if (v_writer) {
         // V: key slot t % 8 of block t / 8, dim d at its lane-order slot
-        const int blk = t / 8, k = t % 8;
-        const int p = v_phys_dim(d, D, BITS);
-        uint32_t* vbp = a.v_codes + ((int64_t)h * (a.cap / 8) + blk) * (D * BITS / 4);
         const uint32_t code = (uint32_t)vcode;
         if constexpr (BITS == 4) {
-            const int sh = 4 * v4_nibble_pos(k);
-            vbp[p] = (vbp[p] & ~(0xFu << sh)) | (code << sh);
+            const int sh = 4 * v4_nibble_pos(vk);
+            vbp[vidx] = (vword & ~(0xFu << sh)) | (code << sh);
         } else {
-            const int idx = 2 * p + (k >> 2), sh = 8 * (k & 3);
-            vbp[idx] = (vbp[idx] & ~(0xFFu << sh)) | (code << sh);
+            const int sh = 8 * (vk & 3);
+            vbp[vidx] = (vword & ~(0xFFu << sh)) | (code << sh);
         }
         if (lane == 0) {
-            f16* vp = a.v_params + (((int64_t)h * (a.cap / 8) + blk) * NG + b) * 16;
-            vp[k] = vs;
-            vp[8 + k] = vbias;
+            f16* vpp = a.v_params + (((int64_t)h * (a.cap / 8) + vblk) * NG + b) * 16;
+            vpp[vk] = vs;
+            vpp[8 + vk] = vbias;
             check_fast_scale(vs, BITS, a.fast_flag);
         }
     }
@@ -996,8 +1017,24 @@ static int launch_decode_fused(KVCache& cc, const f16* q, int G, const f16* k_ne
     m.v_params = (f16*)cc.v_params;
     m.fast_flag = cc.fast_flag;
     m.out = out;
-    hipLaunchKernelGGL((merge_append_kernel<BITS, D>), dim3(G, cc.hkv, D / 64), dim3(256), 0,
-                       stream, m);
+    const dim3 grid(G, cc.hkv, D / 64);
+    switch (merge_per(m.nc)) {
+        case 4:
+            hipLaunchKernelGGL((merge_append_kernel<BITS, D, 4>), grid, dim3(256), 0, stream, m);
+            break;
+        case 8:
+            hipLaunchKernelGGL((merge_append_kernel<BITS, D, 8>), grid, dim3(256), 0, stream, m);
+            break;
+        case 16:
+            hipLaunchKernelGGL((merge_append_kernel<BITS, D, 16>), grid, dim3(256), 0, stream, m);
+            break;
+        case 32:
+            hipLaunchKernelGGL((merge_append_kernel<BITS, D, 32>), grid, dim3(256), 0, stream, m);
+            break;
+        default:
+            hipLaunchKernelGGL((merge_append_kernel<BITS, D, kMergeMaxPer>), grid, dim3(256), 0,
+                               stream, m);
+    }
     QW_HIP_CHECK(hipGetLastError());
     cc.offset = t + 1;
     return QW_OK;

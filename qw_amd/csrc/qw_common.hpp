@@ -85,6 +85,34 @@ __device__ __forceinline__ uint32_t vconst(uint32_t x) {
 }
 __device__ inline half8 as_h8(u32x4 v) { return __builtin_bit_cast(half8, v); }
 
+// Wave-wide reductions. Inside each row of 16 lanes the partners come through
+// DPP (quad_perm [1,0,3,2], [2,3,0,1], then row_ror 4 and 8: a VALU operand
+// modifier, no LDS round trip); the two cross-row steps use ds_bpermute.
+// Every lane ends with the result.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+template <class Op>
+__device__ __forceinline__ float wave_reduce(float x, Op op) {
+    x = op(x, dpp_mov<0xB1>(x));   // quad_perm [1,0,3,2]
+    x = op(x, dpp_mov<0x4E>(x));   // quad_perm [2,3,0,1]
+    x = op(x, dpp_mov<0x124>(x));  // row_ror 4
+    x = op(x, dpp_mov<0x128>(x));  // row_ror 8
+    x = op(x, __shfl_xor(x, 16));
+    return op(x, __shfl_xor(x, 32));
+}
+struct OpSum {
+    __device__ float operator()(float a, float b) const { return a + b; }
+};
+struct OpMax {
+    __device__ float operator()(float a, float b) const { return a < b ? b : a; }
+};
+struct OpMin {
+    __device__ float operator()(float a, float b) const { return b < a ? b : a; }
+};
+
 // Thread-local last-error string for the C ABI.
 void set_error(const std::string& msg);
 const char* last_error();
