@@ -74,53 +74,29 @@ constexpr int decode_waves() {
 constexpr int kBufWord3 = 0x00020000;
 
 // Register stages a wave streams through (1: load the next sub-chunk after
-// the current one's math; 2: ping-pong, two sub-chunks in flight). Two fit
-// the register budget only for the small 4-bit stages.
-#ifndef QW_DECODE_STAGES_4BIT
-#define QW_DECODE_STAGES_4BIT 3
-#endif
+// the current one's math; 2: wait-then-prefetch ping-pong, a stage's
+// successor requested once the stage itself has landed). Two fit the register
+// budget only for the small 4-bit stages.
 template <int BITS>
 constexpr int decode_stages() {
-    return BITS == 4 ? QW_DECODE_STAGES_4BIT : 1;
+    return BITS == 4 ? 2 : 1;
 }
-
-// LDS-DMA staging (4-bit, D = 256): each wave streams its sub-chunks straight
-// into its own LDS buffers with global_load_lds_dwordx4 (one 1 KB
-// instruction per 64 lanes, no registers held while in flight), two buffers a
-// wave, so a CU's whole share of the cache is requested at launch. The loads
-// are issued from inline asm and waited for with explicit vmcnt counts: the
-// compiler cannot tell the two buffers apart and would wait for both.
-#ifndef QW_DECODE_LDS
-#define QW_DECODE_LDS 0
-#endif
-template <int BITS, int D>
-constexpr bool decode_lds() {
-    return QW_DECODE_LDS && BITS == 4 && D == 256;
-}
-constexpr int kLdsSub = 9216;  // bytes a 32-key 4-bit sub-chunk stages (K 4096, params 1024, V 4096)
-
-__device__ __forceinline__ uint32_t lds_offset(const void* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-// 64 lanes x 16 bytes from per-lane global addresses to LDS [lds, lds + 1024).
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds)
-                 : "memory", "m0");
-}
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // FAST: every scale in the cache is inside the 2-op dequant's exact range
 // (the cache's fast_flag, maintained by the append and import kernels).
+//
+// K is dequantized exactly as MLX does, f16(f16(code * scale) + bias): the
+// scores are rounded to fp16 next, and a key value one rounding off would
+// move those roundings. V is dequantized as f16(code * scale) only and the
+// bias of each (key, 64-dim group) enters through one more MFMA,
+// O_b += P * Vb with B = the biases of the lane's dim group for the 8 keys
+// of its block, added to every dim of that group at the end (the bias is
+// exact in fp32; only MLX's second rounding of each V element is skipped).
 template <int BITS, int D, int NW, bool FAST>
 __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)[16], float* sm_fw,
-                                            float* sm_o, half8 (*sm_q)[64], char* stage) {
+                                            float* sm_o, half8 (*sm_q)[64]) {
     using S = DecodeShape<BITS, D>;
     constexpr int NM = S::NM, DPL = S::DPL, NG = S::NG, KL = S::KL, VL = S::VL;
-    constexpr bool LDSP = decode_lds<BITS, D>();
     constexpr bool AFF = BITS != 16;
     const int c = blockIdx.x, h = blockIdx.y;
     // wave index as a scalar: sub-chunk indices, and so the buffer offsets
@@ -150,8 +126,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
     // byte offset is fixed for the whole kernel (VGPR), the sub-chunk's is a
     // scalar (SGPR), the parts of a stage differ by immediates. A stage past
     // the chunk's end gets num_records = 0, so its loads are issued
-    // unconditionally (exact vmcnt accounting with two stages in flight) but
-    // return zeros without touching memory.
+    // unconditionally but return zeros without touching memory.
     constexpr int KRB = D * BITS / 8;          // K row bytes
     constexpr int KPB = AFF ? NG * 4 : 0;      // K param bytes a row
     constexpr int VBB = D * BITS;              // V block bytes (8 keys: D*BITS/4 words)
@@ -168,13 +143,12 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
                                             : kkey * KPB;
     const int off_v = g * VBB + 16 * r16;
     const int off_vp = (g * NG + (r16 * DPL) / 64) * 32;
-    auto load = [&](Stage& st, int s) {
+    // K half of a stage (codes + params: 2*KL + 2 loads) and V half (VL + 2).
+    auto load_k = [&](Stage& st, int s) {
         const bool ok = s < s_end;
         const int si = ok ? s : 0;
         const __amdgpu_buffer_rsrc_t rk =
             __builtin_amdgcn_make_buffer_rsrc((void*)kbase, 0, ok ? a.cap * KRB : 0, kBufWord3);
-        const __amdgpu_buffer_rsrc_t rv =
-            __builtin_amdgcn_make_buffer_rsrc((void*)vbase, 0, ok ? a.cap / 8 * VBB : 0, kBufWord3);
 #pragma unroll
         for (int tile = 0; tile < 2; tile++) {
 #pragma unroll
@@ -204,6 +178,12 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
                 }
             }
         }
+    };
+    auto load_v = [&](Stage& st, int s) {
+        const bool ok = s < s_end;
+        const int si = ok ? s : 0;
+        const __amdgpu_buffer_rsrc_t rv =
+            __builtin_amdgcn_make_buffer_rsrc((void*)vbase, 0, ok ? a.cap / 8 * VBB : 0, kBufWord3);
 #pragma unroll
         for (int jj = 0; jj < VL; jj++)
             st.vc[jj] = __builtin_bit_cast(
@@ -217,6 +197,10 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
                 u32x4, __builtin_amdgcn_raw_buffer_load_b128(rvp, off_vp + 16, 4 * si * VPB, 0));
         }
     };
+    auto load = [&](Stage& st, int s) {
+        load_k(st, s);
+        load_v(st, s);
+    };
 
     // ---- Q rows of this KV group as the B operand (col = query row r16).
     // The workgroup's waves share one KV head, so the operand is built once
@@ -225,8 +209,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
     const int rho = r16;
     const bool row_ok = rho < a.R;
     static_assert(NW >= NM, "one Q slice per wave");
-    half8 x[1];
-    const f16* qsrc;
+    half8 x;
     {
         const int rr = row_ok ? rho : 0;
         const f16* qrow = a.q + ((int64_t)(h * a.G + rr % a.G) * a.Tq + rr / a.G) * D;
@@ -238,81 +221,13 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
             base = 4 * (16 * (m / 2) + 4 * g + 2 * (m % 2));
         else
             base = 32 * m + 8 * g;
-        qsrc = qrow + base;
-        if constexpr (!LDSP) x[0] = *(const half8*)qsrc;
+        x = *(const half8*)(qrow + base);
     }
     int s = c + a.nc * wave;
     Stage A, B;
-    // ---- LDS-DMA staging (LDSP): buffer b of this wave sits at
-    // stage + (2 * wave + b) * kLdsSub. Layout of a buffer: K codes [0, 4096)
-    // as 4 x 1 KB blocks of 8 keys (key r of block i, 16-byte column c at
-    // chunk 8r + (c ^ ((4(r>>1) + i) & 7)): the QK operand reads of a 16-lane
-    // phase hit 16 distinct bank groups), K params [4096, 4608), V params
-    // [4608, 5120), V codes [5120, 9216) (4 blocks of 1 KB as stored).
-    const char* kg = (const char*)a.k_data + (int64_t)h * a.cap * (D * BITS / 8);
-    const char* kpg = (const char*)a.k_params + (int64_t)h * a.cap * (NG * 4);
-    const char* vg = (const char*)a.v_data + (int64_t)h * (a.cap / 8) * (D * BITS);
-    const char* vpg = (const char*)a.v_params + (int64_t)h * (a.cap / 8) * (NG * 32);
-    auto issue = [&](int b, int s) {
-        const uint32_t buf = lds_offset(stage) + (uint32_t)((2 * wave + b) * kLdsSub);
-        const int r = lane >> 3;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int c = (lane & 7) ^ ((4 * (r >> 1) + i) & 7);
-            dma16(kg + ((int64_t)(32 * s + 8 * i + r) * (D * BITS / 8) + 16 * c), buf + 1024 * i);
-        }
-        const char* pg = lane < 32 ? kpg + (int64_t)32 * s * (NG * 4) + 16 * lane
-                                   : vpg + (int64_t)4 * s * (NG * 32) + 16 * (lane - 32);
-        dma16(pg, buf + 4096);
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            dma16(vg + ((int64_t)(4 * s + i) * (D * BITS) + 16 * lane), buf + 5120 + 1024 * i);
-    };
-    auto fetch = [&](Stage& st, int b) {
-        const char* buf = stage + (2 * wave + b) * kLdsSub;
-        const int i = r16 >> 2;
-#pragma unroll
-        for (int tile = 0; tile < 2; tile++) {
-            const int r = 4 * tile + (r16 & 3);
-#pragma unroll
-            for (int cc = 0; cc < KL; cc++) {
-                const int c = 4 * cc + g;
-                st.kc[tile][cc] =
-                    *(const u32x4*)(buf + 1024 * i + 16 * (8 * r + (c ^ ((4 * (r >> 1) + i) & 7))));
-            }
-            const int key = 8 * i + r;
-            const u32x2 t2 = *(const u32x2*)(buf + 4096 + key * 16 + 8 * (g >> 1));
-            st.kp[tile] = u32x4{t2.x, t2.y, 0u, 0u};
-        }
-#pragma unroll
-        for (int jj = 0; jj < VL; jj++) st.vc[jj] = *(const u32x4*)(buf + 5120 + g * 1024 + 16 * (16 * jj + r16));
-        const int grp = (r16 * DPL) / 64;
-        st.vp[0] = *(const u32x4*)(buf + 4608 + (g * NG + grp) * 32);
-        st.vp[1] = *(const u32x4*)(buf + 4608 + (g * NG + grp) * 32 + 16);
-    };
-    if constexpr (LDSP) {
-        // Q slice first (raw, into its sm_q slot), then the first two sub-chunks.
-        if (wave < NM) dma16(qsrc, lds_offset(&sm_q[wave][0]));
-        if (s < s_end) issue(0, s);
-        if (s + SS < s_end) issue(1, s + SS);
-        if (wave < NM) {
-            if (s + SS < s_end)
-                wait_vm<18>();
-            else if (s < s_end)
-                wait_vm<9>();
-            else
-                wait_vm<0>();
-            x[0] = sm_q[wave][lane];
-        }
-    } else {
-        // The first sub-chunk's loads go out right behind Q (loads return in
-        // issue order, so the Q conversion below waits for Q only).
-        load(A, s);
-        // Second stage in flight from the start: a wave's first two sub-chunks
-        // stream in while the first is being computed.
-        if constexpr (decode_stages<BITS>() == 2) load(B, s + SS);
-    }
-    constexpr int kVmcnt0 = 0x0F70;  // s_waitcnt vmcnt(0), expcnt/lgkmcnt untouched
+    // The first sub-chunk's loads go out right behind Q (loads return in
+    // issue order, so the Q conversion below waits for Q only).
+    load(A, s);
     {
         // q' = f16(f16(scale) * q): one packed fp16 multiply rounds exactly
         // like MLX's fp16 `multiply`. Padding rows get scale 0.
@@ -320,7 +235,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
         const half2v sc2 = {sc, sc};
         if (wave < NM) {
             const int m = wave;
-            const u32x4 w = __builtin_bit_cast(u32x4, x[0]);
+            const u32x4 w = __builtin_bit_cast(u32x4, x);
             u32x4 o;
             if constexpr (BITS == 4) {
                 // 4-bit K pairs come out as dims (0,4),(1,5),(2,6),(3,7).
@@ -347,6 +262,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
     float4v acc_o[DPL];
 #pragma unroll
     for (int mm = 0; mm < DPL; mm++) acc_o[mm] = float4v{0.f, 0.f, 0.f, 0.f};
+    float4v acc_b = float4v{0.f, 0.f, 0.f, 0.f};  // P * V biases (rows 4g+i, dim group of r16)
 
     // Q.K^T of the two 16-key tiles (S^T: lane holds keys 8g+i / 8g+4+i of
     // column r16); the two MFMA chains interleave to hide each other's latency.
@@ -401,22 +317,24 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
         PairConsts pc;
         if constexpr (AFF)
             pc = make_consts<FAST, BITS>(h2(st.vp[0][0]), h2(st.vp[0][1]), h2(st.vp[0][2]),
-                                         h2(st.vp[0][3]), h2(st.vp[1][0]), h2(st.vp[1][1]),
-                                         h2(st.vp[1][2]), h2(st.vp[1][3]));
+                                         h2(st.vp[0][3]), h2(st.vp[0][0]), h2(st.vp[0][1]),
+                                         h2(st.vp[0][2]), h2(st.vp[0][3]));
 #pragma unroll
         for (int mm = 0; mm < DPL; mm++) {
             half8 bv;
             if constexpr (BITS == 4)
-                bv = deq4<FAST>(st.vc[mm / 4][mm % 4], pc, magic);
+                bv = deq4<FAST, false>(st.vc[mm / 4][mm % 4], pc, magic);
             else if constexpr (BITS == 8)
-                bv = deq8<FAST>(st.vc[mm / 2][2 * (mm % 2)], st.vc[mm / 2][2 * (mm % 2) + 1], pc);
+                bv = deq8<FAST, false>(st.vc[mm / 2][2 * (mm % 2)], st.vc[mm / 2][2 * (mm % 2) + 1], pc);
             else
                 bv = as_h8(st.vc[mm]);
             acc_o[mm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop, bv, acc_o[mm], 0, 0, 0);
         }
+        if constexpr (AFF)
+            acc_b = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop, as_h8(st.vp[1]), acc_b, 0, 0, 0);
     };
 
-    auto compute = [&](const Stage& st, int s) {
+    auto scores = [&](const Stage& st, int s) -> half8 {
         // ---- scores
         float4v acc0, acc1;
         qk(st, acc0, acc1);
@@ -449,6 +367,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
                 for (int mm = 0; mm < DPL; mm++)
 #pragma unroll
                     for (int i = 0; i < 4; i++) acc_o[mm][i] *= f[i];
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc_b[i] *= f[i];
             }
             m_run = m_new;
         }
@@ -460,51 +380,33 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
             l_run += p;
             pop[e] = (f16)p;
         }
-        // ---- P.V
-        pv(st, pop);
+        return pop;
     };
+    auto compute = [&](const Stage& st, int s) { pv(st, scores(st, s)); };
 
-    if constexpr (LDSP) {
-        // Two buffers a wave: wait for the older one (the other may still be
-        // in flight: 9 instructions behind it), compute it from LDS, refill it
-        // with the sub-chunk two rounds ahead.
-        for (int b = 0; s < s_end; s += SS, b ^= 1) {
-            if (s + SS < s_end)
-                wait_vm<9>();
-            else
-                wait_vm<0>();
-            fetch(A, b);
-            compute(A, s);
-            if (s + 2 * SS < s_end) {
-                wait_lgkm0();
-                issue(b, s + 2 * SS);
-            }
-        }
-    } else if constexpr (decode_stages<BITS>() == 3) {
-        // Wait-then-prefetch ping-pong: a stage's successor is requested only
-        // once the stage itself has landed, so the first half of the cache
-        // arrives at full bandwidth and the second streams in under the
-        // first's math.
+    if constexpr (decode_stages<BITS>() == 2) {
+        // Wait-then-prefetch per plane: each K or V half of a stage is
+        // requested once the previous half has landed, and QK starts as soon
+        // as the stage's K half is in, so about one stage of a wave is in
+        // flight at a time (measured faster than both stages in flight from
+        // the start, and than waiting for whole stages).
+        constexpr int NK = 2 * KL + (AFF ? 2 : 0), NV = VL + (AFF ? 2 : 0);
+        static_assert(NK == NV && NK < 16, "equal K and V halves: one vmcnt value");
+        constexpr int kWaitHalf = 0x0F70 | NK;  // vmcnt(NK), expcnt/lgkmcnt untouched
         for (; s < s_end; s += 2 * SS) {
-            __builtin_amdgcn_s_waitcnt(kVmcnt0);
-            load(B, s + SS);
-            compute(A, s);
+            __builtin_amdgcn_s_waitcnt(kWaitHalf);  // K(A) in; V(A) may be in flight
+            load_k(B, s + SS);
+            const half8 pa = scores(A, s);
+            __builtin_amdgcn_s_waitcnt(kWaitHalf);  // V(A) in; K(B) may be in flight
+            load_v(B, s + SS);
+            pv(A, pa);
             if (s + SS >= s_end) break;
-            __builtin_amdgcn_s_waitcnt(kVmcnt0);
-            load(A, s + 2 * SS);
-            compute(B, s + SS);
-        }
-    } else if constexpr (decode_stages<BITS>() == 2) {
-        // Ping-pong: a stage is refilled right after its math, so one stage's
-        // loads are always in flight behind the other's compute.
-        for (; s < s_end; s += 2 * SS) {
-            compute(A, s);
-            __builtin_amdgcn_sched_barrier(0);
-            load(A, s + 2 * SS);
-            if (s + SS >= s_end) break;
-            compute(B, s + SS);
-            __builtin_amdgcn_sched_barrier(0);
-            load(B, s + 3 * SS);
+            __builtin_amdgcn_s_waitcnt(kWaitHalf);
+            load_k(A, s + 2 * SS);
+            const half8 pb = scores(B, s + SS);
+            __builtin_amdgcn_s_waitcnt(kWaitHalf);
+            load_v(A, s + 2 * SS);
+            pv(B, pb);
         }
     } else {
         for (; s < s_end; s += SS) {
@@ -517,7 +419,6 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
     float lsum = l_run;
     lsum += __shfl_xor(lsum, 16);
     lsum += __shfl_xor(lsum, 32);
-
     // ---- merge the NW waves. Each wave parks its accumulators in LDS in
     // their MFMA layout (float4 of rows 4g..4g+3 at dim r16*DPL + mm; only
     // the lane groups holding rows < R), and its (m, l). One thread a row then
@@ -525,7 +426,6 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
     // elements out[row][d] = sum_w f_w O_w[row][d] and writes the partial.
     // sm_o row stride: G4 * 16 float4 plus one, so the phase-B reads (16
     // consecutive dims = 16 values of mm) fall on distinct banks.
-    if constexpr (LDSP) __syncthreads();  // sm_o aliases the staging buffers
     const int R = a.R;
     const int G4 = (R + 3) >> 2;          // lane groups holding real rows
     const int RS = G4 * 16 + 1;           // float4 per (wave, mm)
@@ -533,7 +433,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
     if (g < G4) {
         float4v* dst = (float4v*)sm_o + (int64_t)wave * DPL * RS + g * 16 + r16;
 #pragma unroll
-        for (int mm = 0; mm < DPL; mm++) dst[mm * RS] = acc_o[mm];
+        for (int mm = 0; mm < DPL; mm++) dst[mm * RS] = acc_o[mm] + acc_b;
     }
     __syncthreads();
     float* sm_f = (float*)sm_fw;  // [NW][16] factors, then [16] L
@@ -574,15 +474,14 @@ __global__ __launch_bounds__((64 * decode_waves<BITS, D>()), 1) void attend_deco
     __shared__ float2 sm_ml[NW][16];
     __shared__ float sm_fw[NW * 16 + 32];
     __shared__ half8 sm_q[D / 32][64];
-    // dynamic LDS: the staging buffers (LDS-DMA path), reused as sm_o
-    // [NW][R][D] by the wave merge
+    // dynamic LDS: the wave merge's sm_o [NW][DPL][R] float4
     extern __shared__ __attribute__((aligned(16))) float sm_o[];
     // One uniform branch for the whole launch: the exact 2-op dequant when
     // every cached scale allows it, else the separately rounded path.
     if (BITS == 16 || *a.fast_flag != 0)
-        decode_body<BITS, D, NW, true>(a, sm_ml, sm_fw, sm_o, sm_q, (char*)sm_o);
+        decode_body<BITS, D, NW, true>(a, sm_ml, sm_fw, sm_o, sm_q);
     else
-        decode_body<BITS, D, NW, false>(a, sm_ml, sm_fw, sm_o, sm_q, (char*)sm_o);
+        decode_body<BITS, D, NW, false>(a, sm_ml, sm_fw, sm_o, sm_q);
 }
 
 // Combines the per-workgroup partials of one query row (partials of a KV head
@@ -689,7 +588,6 @@ static int launch_decode_partials(KVCache& cc, const f16* q, int G, int Tq, int 
     a.nc = nc;
     a.scale_h = (float)(f16)scale;
     size_t shmem = (size_t)NW * (D / 16) * (((a.R + 3) / 4) * 16 + 1) * 16;  // wave-merge sm_o
-    if constexpr (decode_lds<BITS, D>()) shmem = std::max(shmem, (size_t)2 * NW * kLdsSub);
     // Dynamic LDS above 64 KB must be allowed per kernel; raise the limit to
     // what this launch needs (once per size, per template instance).
     static size_t attr_max = 0;

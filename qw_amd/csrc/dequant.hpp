@@ -40,18 +40,22 @@ constexpr uint32_t kFastHi = 0x5400u;   // 64
 
 #pragma clang fp contract(off)
 
-template <bool FAST, bool X16>
+// ADDB = false returns f16(code * scale) only: the fused attention adds the
+// bias term of a group separately (scale and bias are per group, so
+// sum_d x_d (c_d s + b) = sum_d x_d f16(c_d s) + b sum_d x_d).
+template <bool FAST, bool X16, bool ADDB = true>
 __device__ __forceinline__ half2v deq_pair(uint32_t magic_bits, half2v s, half2v m, half2v b) {
     const half2v x = h2(magic_bits);
+    half2v p;
     if constexpr (FAST) {
-        const half2v p = __builtin_elementwise_fma(x, s, m);
-        return p + b;
+        p = __builtin_elementwise_fma(x, s, m);
     } else {
         half2v c = x - (half2v){(f16)1024.0f, (f16)1024.0f};
         if constexpr (X16) c = c * (half2v){(f16)0.0625f, (f16)0.0625f};
-        const half2v p = c * s;
-        return p + b;
+        p = c * s;
     }
+    if constexpr (ADDB) p = p + b;
+    return p;
 }
 
 // Constants of the four pairs a word produces. FAST: s[1], s[3] are scale/16
@@ -92,27 +96,27 @@ __device__ __forceinline__ PairConsts make_consts(half2v s0, half2v s1, half2v s
 
 // 4-bit word -> pairs (nibbles 0,4), (1,5), (2,6), (3,7). `magic` is
 // kMagic held in a VGPR (vconst) so each field costs one v_and_or_b32.
-template <bool FAST>
+template <bool FAST, bool ADDB = true>
 __device__ __forceinline__ half8 deq4(uint32_t w, const PairConsts& c, uint32_t magic) {
     const uint32_t w8 = w >> 8;
-    const half2v y0 = deq_pair<FAST, false>((w & 0x000F000Fu) | magic, c.s[0], c.m[0], c.b[0]);
-    const half2v y1 = deq_pair<FAST, true>((w & 0x00F000F0u) | magic, c.s[1], c.m[1], c.b[1]);
-    const half2v y2 = deq_pair<FAST, false>((w8 & 0x000F000Fu) | magic, c.s[2], c.m[2], c.b[2]);
-    const half2v y3 = deq_pair<FAST, true>((w8 & 0x00F000F0u) | magic, c.s[3], c.m[3], c.b[3]);
+    const half2v y0 = deq_pair<FAST, false, ADDB>((w & 0x000F000Fu) | magic, c.s[0], c.m[0], c.b[0]);
+    const half2v y1 = deq_pair<FAST, true, ADDB>((w & 0x00F000F0u) | magic, c.s[1], c.m[1], c.b[1]);
+    const half2v y2 = deq_pair<FAST, false, ADDB>((w8 & 0x000F000Fu) | magic, c.s[2], c.m[2], c.b[2]);
+    const half2v y3 = deq_pair<FAST, true, ADDB>((w8 & 0x00F000F0u) | magic, c.s[3], c.m[3], c.b[3]);
     return half8{y0.x, y0.y, y1.x, y1.y, y2.x, y2.y, y3.x, y3.y};
 }
 
 // Two 8-bit words -> pairs (bytes 0,1), (2,3) of w0, then of w1.
-template <bool FAST>
+template <bool FAST, bool ADDB = true>
 __device__ __forceinline__ half8 deq8(uint32_t w0, uint32_t w1, const PairConsts& c) {
-    const half2v y0 = deq_pair<FAST, false>(__builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u),
-                                            c.s[0], c.m[0], c.b[0]);
-    const half2v y1 = deq_pair<FAST, false>(__builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u),
-                                            c.s[1], c.m[1], c.b[1]);
-    const half2v y2 = deq_pair<FAST, false>(__builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u),
-                                            c.s[2], c.m[2], c.b[2]);
-    const half2v y3 = deq_pair<FAST, false>(__builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u),
-                                            c.s[3], c.m[3], c.b[3]);
+    const half2v y0 = deq_pair<FAST, false, ADDB>(__builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u),
+                                                  c.s[0], c.m[0], c.b[0]);
+    const half2v y1 = deq_pair<FAST, false, ADDB>(__builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u),
+                                                  c.s[1], c.m[1], c.b[1]);
+    const half2v y2 = deq_pair<FAST, false, ADDB>(__builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u),
+                                                  c.s[2], c.m[2], c.b[2]);
+    const half2v y3 = deq_pair<FAST, false, ADDB>(__builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u),
+                                                  c.s[3], c.m[3], c.b[3]);
     return half8{y0.x, y0.y, y1.x, y1.y, y2.x, y2.y, y3.x, y3.y};
 }
 
