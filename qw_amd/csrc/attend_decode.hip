@@ -9,22 +9,26 @@
 // cache (scores f16(q' . k), fp32 softmax, bottom-right causal).
 //
 // Design (one pass over the packed cache, HBM-bound):
-//   grid (chunks, kv_heads), 4 waves a workgroup. The keys of a KV head are
-//   cut into 32-key sub-chunks; a workgroup owns a contiguous run of them and
-//   its waves take every 4th. A wave issues the loads of all its sub-chunks
-//   (K codes, K scale/bias, V codes, V scale/bias) before any math, so the
-//   whole per-CU share of the cache is in flight at once.
-//   Q.K^T: v_mfma_f32_16x16x32_f16 with A = dequantized K (16 keys x 32
-//   dims, one packed 4-bit word or two 8-bit words a lane, dequantized in
-//   registers with the fp16 magic-number trick and one v_pk_fma a pair) and
-//   B = the G*n_rows query rows of the KV group (GQA: each K row is fetched
-//   and dequantized once for all heads of its group).
-//   All of a wave's scores are formed before the softmax, so the wave knows
-//   its row max up front: no running-max rescale of the accumulators.
+//   grid (chunks, kv_heads), 8 waves a workgroup, one workgroup a CU. The
+//   keys of a KV head are cut into 32-key sub-chunks dealt round-robin over
+//   the head's waves (workgroup c, wave w takes c + nc * (w + 8k)).
+//   Each sub-chunk's K half (codes + scale/bias) and V half are requested
+//   with raw buffer loads once the previous half has landed, about one
+//   sub-chunk a wave in flight.
+//   Q.K^T: v_mfma_f32_16x16x32_f16 with A = K dequantized in registers
+//   exactly as MLX does (fp16 magic-number conversion, v_pk_fma, v_pk_add)
+//   and B = the G*n_rows query rows of the KV group from LDS (GQA: each K row
+//   is fetched and dequantized once for all heads of its group).
+//   fp16 score rounding, masking and an online softmax whose reference only
+//   moves when a score exceeds it by 5.5, so the accumulators are rarely
+//   rescaled.
 //   P.V: the same MFMA with A = P (rows x 32 keys, fp16) and B = V straight
-//   out of the 8-key-block V plane (one 128-bit load = 8 keys x 4 dims).
-//   The 4 waves merge through LDS; each workgroup writes one fp32 partial
-//   (m, l, unnormalized O); a small merge kernel combines the partials.
+//   out of the 8-key-block V plane (one 128-bit load = 8 keys x 4 dims),
+//   dequantized as f16(code * scale); the biases enter through one MFMA a
+//   sub-chunk.
+//   The 8 waves merge through LDS; each workgroup writes one fp32 partial
+//   (m, l, unnormalized O); a merge kernel combines the partials (and, on the
+//   decode-with-append path, quantizes and appends the new token).
 #include <algorithm>
 #include <type_traits>
 
