@@ -132,6 +132,16 @@ int qw_kv_attention(qw_kv_cache* cache, const void* q, int n_q_heads, int n_rows
  * cached length); *trimmed receives the number removed. No device work. */
 int qw_kv_trim(qw_kv_cache* cache, int n, int* trimmed);
 
+/* KVCache::demote_fp16_to_turbo4 (cache.rs:3591-3605), to an affine mode: a
+ * QW_KV_FP16 cache holding rows is re-stored as target_mode (QW_KV_AFFINE4 or
+ * QW_KV_AFFINE8) by quantize-appending its rows [0, offset) to an empty cache
+ * of that mode, exactly as qw_kv_update of the same rows would store them;
+ * offset is unchanged. *demoted = 1 when it did so, 0 when the cache is not
+ * fp16 or empty (the reference returns false). Synchronizes `stream`; the
+ * fp16 rows are staged in a temporary device buffer of 2*hkv*offset*D*2 bytes.
+ * The policy deciding when to call it (qwen3_5.rs:929-986) is host code. */
+int qw_kv_demote(qw_kv_cache* cache, int target_mode, void* stream, int* demoted);
+
 /* Snapshot export in the reference's tensor layout (the packed-tensor
  * snapshot of cache.rs:570-626): for the affine modes
  *   k_codes, v_codes  [n_kv_heads][offset][head_dim*bits/32] uint32 (MLX

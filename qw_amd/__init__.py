@@ -61,6 +61,7 @@ _SIGNATURES = {
     "qw_kv_update_and_attention": (_i, [_p, _p, _i, _i, _p, _p, _f, _i, _p, _p]),
     "qw_kv_attention": (_i, [_p, _p, _i, _i, _f, _i, _p, _p]),
     "qw_kv_trim": (_i, [_p, _i, ctypes.POINTER(_i)]),
+    "qw_kv_demote": (_i, [_p, _i, _p, ctypes.POINTER(_i)]),
     "qw_kv_export": (_i, [_p, _p, _p, _p, _p, _p, _p, _p]),
     "qw_kv_import": (_i, [_p, _i, _p, _p, _p, _p, _p, _p, _p]),
     "qw_dlsa_sparse_attention": (_i, [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _i, _i, _i,
@@ -240,6 +241,19 @@ class KVCache:
         return self._attn(q, None, None, scale, causal)
 
     # -- lifecycle
+    def demote_fp16_to_affine(self, target_mode: int | str) -> bool:
+        """Re-store a populated fp16 cache in an affine mode (reference
+        ``demote_fp16_to_turbo4``, cache.rs:3591): False, and nothing done,
+        when the cache is not fp16 or holds no rows."""
+        if isinstance(target_mode, str):
+            target_mode = KVCacheMode.from_str(target_mode)
+        d = _i()
+        _check(lib().qw_kv_demote(self._h, target_mode, _stream(self.device), ctypes.byref(d)))
+        if d.value:
+            self.mode = target_mode
+            self.bits = {0: 16, 1: 8, 2: 4}[target_mode]
+        return bool(d.value)
+
     def trim(self, n: int) -> int:
         v = _i()
         _check(lib().qw_kv_trim(self._h, n, ctypes.byref(v)))

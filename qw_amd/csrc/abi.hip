@@ -153,6 +153,18 @@ int qw_kv_trim(qw_kv_cache* cache, int n, int* trimmed) {
     return QW_OK;
 }
 
+static int demote_call(qw_kv_cache* cache, int target_mode, void* stream, int* demoted) {
+    int d = 0;
+    const int rc = cache->impl.demote(target_mode, (hipStream_t)stream, &d);
+    if (demoted) *demoted = d;
+    return rc;
+}
+
+int qw_kv_demote(qw_kv_cache* cache, int target_mode, void* stream, int* demoted) {
+    QW_HANDLE(cache);
+    QW_GUARDED(demote_call(cache, target_mode, stream, demoted));
+}
+
 int qw_kv_export(const qw_kv_cache* cache, void* k_codes, void* k_scales, void* k_biases,
                  void* v_codes, void* v_scales, void* v_biases, void* stream) {
     QW_HANDLE(cache);

@@ -175,6 +175,52 @@ int KVCache::ensure_workspace(size_t bytes) {
     return QW_OK;
 }
 
+int KVCache::demote(int target_mode, hipStream_t stream, int* demoted) {
+    // cache.rs:3591 demote_fp16_to_turbo4: a populated fp16 cache is re-stored
+    // in the quantized mode by quantize-appending its rows [0, offset) to an
+    // empty cache of that mode; anything else is left alone (returns 0).
+    *demoted = 0;
+    QW_REQUIRE(target_mode == QW_KV_AFFINE4 || target_mode == QW_KV_AFFINE8, QW_ERR_INVALID_ARGUMENT,
+               "demote: target mode must be an affine mode");
+    if (mode != QW_KV_FP16 || offset <= 0) return QW_OK;
+    DeviceGuard dg(device);
+    QW_REQUIRE(dg.ok, QW_ERR_HIP, "demote: hipSetDevice failed");
+    const int n = offset;
+    const size_t bytes = (size_t)hkv * n * D * sizeof(f16);
+    void *tk = nullptr, *tv = nullptr;
+    if (hipMalloc(&tk, bytes) != hipSuccess || hipMalloc(&tv, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        if (tk) (void)hipFree(tk);
+        set_error("demote: hipMalloc of the fp16 staging rows failed");
+        return QW_ERR_OUT_OF_MEMORY;
+    }
+    int rc = dequantize(0, n, tk, tv, stream);  // the fp16 rows, [hkv][n][D]
+    if (rc == QW_OK) rc = hipStreamSynchronize(stream) == hipSuccess ? QW_OK : QW_ERR_HIP;
+    if (rc) {
+        (void)hipFree(tk);
+        (void)hipFree(tv);
+        return rc;
+    }
+    void* old[4] = {k_data, (void*)k_params, v_data, (void*)v_params};
+    const int old_cap = cap;
+    k_data = v_data = nullptr;
+    k_params = v_params = nullptr;
+    cap = 0;
+    offset = 0;
+    mode = target_mode;
+    bits = target_mode == QW_KV_AFFINE4 ? 4 : 8;
+    rc = reserve(old_cap, stream);
+    if (rc == QW_OK) rc = update(tk, tv, n, stream);
+    if (rc == QW_OK) rc = hipStreamSynchronize(stream) == hipSuccess ? QW_OK : QW_ERR_HIP;
+    (void)hipFree(tk);
+    (void)hipFree(tv);
+    if (rc) return rc;  // the cache is left empty in the new mode
+    for (void* p : old)
+        if (p) (void)hipFree(p);
+    *demoted = 1;
+    return QW_OK;
+}
+
 int KVCache::trim(int n) {
     // cache.rs:2251: clamp to the cached length; buffers keep their rows, the
     // next append overwrites them.

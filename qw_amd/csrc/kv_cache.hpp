@@ -52,6 +52,8 @@ struct KVCache {
     int reserve(int capacity, hipStream_t stream);
     int ensure_workspace(size_t bytes);
     int64_t nbytes() const;
+    // cache.rs:3591 demote_fp16_to_turbo4, to an affine mode
+    int demote(int target_mode, hipStream_t stream, int* demoted);
 
     // cache.rs:922 `update`
     int update(const void* k_new, const void* v_new, int n_tokens, hipStream_t stream);

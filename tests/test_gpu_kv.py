@@ -342,3 +342,85 @@ def test_extreme_scales_take_the_exact_slow_dequant(oracle_lib, bits):
     rel = np.linalg.norm(err) / np.linalg.norm(ref)
     print(f"extreme bits={bits}: max_abs={np.abs(err).max():.3e} rel_l2={rel:.3e}")
     assert rel <= REL_L2 and np.abs(err).max() <= MAX_ABS * max(1.0, np.abs(ref).max())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("target,D,T", [("affine4", 256, 3001), ("affine8", 256, 777),
+                                        ("affine4", 128, 65)])
+def test_demote_equals_appending_the_rows_quantized(target, D, T):
+    """cache.rs:3591 demote_fp16_to_turbo4, to an affine mode: the demoted
+    cache holds exactly what appending the same rows in that mode stores
+    (codes, scales, biases bit for bit), keeps its offset, and then behaves as
+    that cache on further appends and attention."""
+    import qw_amd
+
+    r = rng(900 + T + D)
+    H, hq = 4, 16
+    k, v = _kv(r, H, T + 9, D)
+    a = qw_amd.KVCache("fp16", H, D)
+    a.update(_gpu(k[:, :T])[None], _gpu(v[:, :T])[None])
+    assert a.demote_fp16_to_affine(target)
+    assert a.mode == qw_amd.KVCacheMode.from_str(target) and a.offset == T
+    b = qw_amd.KVCache(target, H, D)
+    b.update(_gpu(k[:, :T])[None], _gpu(v[:, :T])[None])
+    ta, tb = a.snapshot_tensors(), b.snapshot_tensors()
+    assert set(ta) == set(tb)
+    for name in tb:
+        assert torch.equal(ta[name], tb[name]), name
+    # both continue identically: append and attend in one call
+    q = r.standard_normal((hq, 9, D)).astype(np.float16)
+    oa = a.update_and_causal_attention(_gpu(q)[None], _gpu(k[:, T:])[None], _gpu(v[:, T:])[None],
+                                       1.0 / 16)
+    ob = b.update_and_causal_attention(_gpu(q)[None], _gpu(k[:, T:])[None], _gpu(v[:, T:])[None],
+                                       1.0 / 16)
+    assert torch.equal(oa, ob)
+    assert a.offset == b.offset == T + 9
+
+
+@pytest.mark.gpu
+def test_demote_is_a_no_op_unless_a_populated_fp16_cache():
+    import qw_amd
+
+    empty = qw_amd.KVCache("fp16", 4, 256)
+    assert not empty.demote_fp16_to_affine("affine4")
+    assert empty.mode == qw_amd.KVCacheMode.FP16
+    r = rng(77)
+    k, v = _kv(r, 4, 40, 256)
+    quant = qw_amd.KVCache("affine8", 4, 256)
+    quant.update(_gpu(k)[None], _gpu(v)[None])
+    before = quant.snapshot_tensors()
+    assert not quant.demote_fp16_to_affine("affine4")
+    for name, t in quant.snapshot_tensors().items():
+        assert torch.equal(t, before[name]), name
+    fp = qw_amd.KVCache("fp16", 4, 256)
+    fp.update(_gpu(k)[None], _gpu(v)[None])
+    with pytest.raises(qw_amd.QwError):
+        fp.demote_fp16_to_affine("fp16")
+    assert fp.mode == qw_amd.KVCacheMode.FP16 and fp.offset == 40
+
+
+@pytest.mark.gpu
+def test_policy_demotes_real_caches_past_the_threshold():
+    """qwen3_5.rs:959 / :968 with real caches: a prefill past the threshold is
+    quantized at its end; a short one is quantized before the forward that
+    crosses the threshold, exactly once."""
+    import qw_amd
+    from qw_amd import policy
+
+    r = rng(4096)
+    thr = policy.QUANTIZE_THRESHOLD_TOKENS
+    conf = qw_amd.KVCacheMode.AFFINE4
+    mode0 = policy.initial_attention_cache_mode(conf)
+    k, v = _kv(r, 4, thr + 1, 128)
+    long_c = qw_amd.KVCache(mode0, 4, 128)
+    long_c.update(_gpu(k)[None], _gpu(v)[None])
+    assert policy.finish_initial_attention_prefill([long_c], conf) == 1
+    assert long_c.mode == conf and long_c.offset == thr + 1
+    short = qw_amd.KVCache(mode0, 4, 128)
+    short.update(_gpu(k[:, :2])[None], _gpu(v[:, :2])[None])
+    assert policy.finish_initial_attention_prefill([short], conf) == 0
+    assert policy.prepare_attention_forward([short], conf, thr - 2, True) == 0
+    assert short.mode == qw_amd.KVCacheMode.FP16
+    assert policy.prepare_attention_forward([short], conf, thr - 1, True) == 1
+    assert short.mode == conf
+    assert policy.prepare_attention_forward([short], conf, thr - 1, True) == 0
