@@ -53,6 +53,12 @@ extern "C" {
 #define QW_KV_FP16 0
 #define QW_KV_AFFINE8 1
 #define QW_KV_AFFINE4 2
+/* The reference's Int8 mode (quantize_per_token / dequantize,
+ * cache.rs:262-316, update_int8 :1042-1157): per (token, KV head) the scale
+ * is f16(absmax / 127) (1 for an all-zero token), codes are
+ * clip(round(f16(x / scale)), -128, 127) and the fetched value is
+ * f16(code * scale). */
+#define QW_KV_INT8 3
 
 typedef struct qw_kv_cache qw_kv_cache;
 
@@ -148,7 +154,10 @@ int qw_kv_demote(qw_kv_cache* cache, int target_mode, void* stream, int* demoted
  *                     packing), k_scales/k_biases/v_scales/v_biases
  *                     [n_kv_heads][offset][head_dim/64] fp16;
  * for fp16 mode k_codes/v_codes receive K/V [n_kv_heads][offset][head_dim]
- * fp16 and the scale/bias pointers are ignored (may be NULL). */
+ * fp16 and the scale/bias pointers are ignored (may be NULL); for Int8 mode
+ * k_codes/v_codes receive [n_kv_heads][offset][head_dim] int8 codes and
+ * k_scales/v_scales [n_kv_heads][offset] fp16 (the reference's keys, values,
+ * key_scales, val_scales), the bias pointers are ignored (may be NULL). */
 int qw_kv_export(const qw_kv_cache* cache, void* k_codes, void* k_scales, void* k_biases,
                  void* v_codes, void* v_scales, void* v_biases, void* stream);
 

@@ -56,6 +56,10 @@ def _declare(L: ctypes.CDLL) -> None:
     L.qwo_affine_quantize.argtypes = [_p, _i64, _i32, _i32, _i32, _p, _p, _p]
     L.qwo_affine_dequantize.restype = _i32
     L.qwo_affine_dequantize.argtypes = [_p, _p, _p, _i64, _i32, _i32, _i32, _p]
+    L.qwo_int8_quantize.restype = _i32
+    L.qwo_int8_quantize.argtypes = [_p, _i64, _i32, _p, _p]
+    L.qwo_int8_dequantize.restype = _i32
+    L.qwo_int8_dequantize.argtypes = [_p, _p, _i64, _i32, _p]
     L.qwo_sdpa_mlx_f16.restype = _i32
     L.qwo_sdpa_mlx_f16.argtypes = [_p, _p, _p, _i32, _i32, _i32, _i32, _i32, _f32, _p, _p, _i32]
     L.qwo_sdpa_f64.restype = _i32
@@ -134,6 +138,32 @@ def affine_dequantize(codes: np.ndarray, scales: np.ndarray, biases: np.ndarray,
     return out
 
 
+# ------------------------------------------------------------ Int8 codec
+
+def int8_quantize(w: np.ndarray):
+    """quantize_per_token of fp16 rows ``w[..., dim]``: (codes int8 [..., dim],
+    scales f16 [...])."""
+    w = _c(w, np.float16)
+    dim = w.shape[-1]
+    rows = int(np.prod(w.shape[:-1])) if w.ndim > 1 else 1
+    codes = np.empty(w.shape, np.int8)
+    scales = np.empty(w.shape[:-1], np.float16)
+    _check(lib().qwo_int8_quantize(_ptr(w), rows, dim, _ptr(codes), _ptr(scales)),
+           "int8_quantize")
+    return codes, scales
+
+
+def int8_dequantize(codes: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    codes = _c(codes, np.int8)
+    scales = _c(scales, np.float16)
+    dim = codes.shape[-1]
+    rows = int(np.prod(codes.shape[:-1])) if codes.ndim > 1 else 1
+    out = np.empty(codes.shape, np.float16)
+    _check(lib().qwo_int8_dequantize(_ptr(codes), _ptr(scales), rows, dim, _ptr(out)),
+           "int8_dequantize")
+    return out
+
+
 # ------------------------------------------------------------------ SDPA
 
 def _pos(q_pos, L):
@@ -199,6 +229,43 @@ def dlsa_attention(q, k, v, lists, lengths, scale: float, threads: int | None = 
 
 
 # ------------------------------------------------------ quantized layer call
+
+class Int8CacheOracle:
+    """Host-side Int8 KV cache (keys/values int8 [Hkv, cap, D], key/value
+    scales f16 [Hkv, cap]); attention is the reference's: fetch (dequantize
+    the visible cache, a6) then the MLX SDPA restatement."""
+
+    def __init__(self, n_kv_heads: int, head_dim: int, capacity: int):
+        self.hkv, self.D, self.cap = n_kv_heads, head_dim, capacity
+        self.keys = np.zeros((n_kv_heads, capacity, head_dim), np.int8)
+        self.values = np.zeros_like(self.keys)
+        self.key_scales = np.zeros((n_kv_heads, capacity), np.float16)
+        self.val_scales = np.zeros_like(self.key_scales)
+        self.offset = 0
+
+    def update(self, k_new: np.ndarray, v_new: np.ndarray) -> None:
+        L = k_new.shape[1]
+        assert self.offset + L <= self.cap
+        sl = slice(self.offset, self.offset + L)
+        self.keys[:, sl], self.key_scales[:, sl] = int8_quantize(k_new)
+        self.values[:, sl], self.val_scales[:, sl] = int8_quantize(v_new)
+        self.offset += L
+
+    def fetch(self):
+        T = self.offset
+        return (int8_dequantize(self.keys[:, :T], self.key_scales[:, :T]),
+                int8_dequantize(self.values[:, :T], self.val_scales[:, :T]))
+
+    def update_and_attention(self, q, k_new, v_new, scale: float, causal: bool,
+                             rows=None, threads: int | None = None) -> np.ndarray:
+        L = q.shape[1]
+        self.update(k_new, v_new)
+        k, v = self.fetch()
+        sel = np.arange(L) if rows is None else np.asarray(rows)
+        pos = causal_positions(L, self.offset)[sel] if causal else None
+        return sdpa_mlx_f16(np.ascontiguousarray(q[:, sel]), k, v, scale,
+                            q_pos=None if pos is None else np.ascontiguousarray(pos),
+                            threads=threads)
 
 class AffineCacheOracle:
     """Host-side quantized KV cache in the reference's layout (row-major codes,

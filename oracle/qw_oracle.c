@@ -20,6 +20,14 @@
  *       the one point only MLX could settle.
  *   qwo_affine_dequantize  pinned by the closed form on every code of
  *       hand-built groups and by the quantize round trip bound.
+ *   qwo_int8_quantize / qwo_int8_dequantize  pinned by the reference's own
+ *       known-answer test values (cache.rs:7480-7545: every coordinate within
+ *       one step absmax/127 after the round trip, the all-zero token), the
+ *       closed form on hand-built rows (the absmax element maps to +-127, the
+ *       zero-token scale is 1), and brute force (no other code in [-128, 127]
+ *       is nearer to x under the stored scale, up to the fp16 rounding of
+ *       x / scale). The tie rule of MLX `round` (rint, ties-to-even) is not
+ *       pinned against MLX itself.
  *   qwo_sdpa_mlx_f16  pinned against qwo_sdpa_f64 (closed form, fp64)
  *       within the fp16-rounding budget, against the D-LSA fixtures'
  *       dense_out (short_dense, tiny), and by the known answers of
@@ -178,6 +186,47 @@ int qwo_affine_quantize(const uint16_t* w, int64_t n_rows, int dim, int group, i
  * added (rounded to fp16 again). The fp16 arithmetic is restated as an f32
  * operation followed by an RNE cast, which is how MLX's CPU float16 type
  * evaluates it. */
+/* cache.rs:270-305 quantize_per_token. MLX evaluates each fp16 op as the
+ * fp32 result rounded to fp16 (correctly rounded: 24 >= 2*11 + 2 bits), so:
+ * absmax is exact, scale = RN16(absmax / 127), x_div = RN16(x / scale). */
+int qwo_int8_quantize(const uint16_t* w, int64_t n_rows, int dim, int8_t* codes,
+                      uint16_t* scales) {
+    if (!w || !codes || !scales || n_rows < 0 || dim <= 0) return -1;
+    pthread_once(&g_table_once, build_table);
+    for (int64_t r = 0; r < n_rows; r++) {
+        const uint16_t* src = w + r * dim;
+        float absmax = 0.0f;
+        for (int j = 0; j < dim; j++) {
+            const float a = fabsf(h2f(src[j]));
+            absmax = absmax < a ? a : absmax;
+        }
+        uint16_t sh = qwo_f32_to_f16(absmax / 127.0f);
+        if (h2f(sh) == 0.0f) sh = qwo_f32_to_f16(1.0f); /* zero-token guard, cache.rs:290-295 */
+        const float s = h2f(sh);
+        scales[r] = sh;
+        for (int j = 0; j < dim; j++) {
+            const float x_div = round_f16(h2f(src[j]) / s);
+            float c = rintf(x_div);
+            c = c < -128.0f ? -128.0f : (c > 127.0f ? 127.0f : c);
+            codes[r * dim + j] = (int8_t)c;
+        }
+    }
+    return 0;
+}
+
+/* cache.rs:313-316 dequantize: astype(f16) is exact, the multiply rounds. */
+int qwo_int8_dequantize(const int8_t* codes, const uint16_t* scales, int64_t n_rows, int dim,
+                        uint16_t* out) {
+    if (!codes || !scales || !out || n_rows < 0 || dim <= 0) return -1;
+    pthread_once(&g_table_once, build_table);
+    for (int64_t r = 0; r < n_rows; r++) {
+        const float s = h2f(scales[r]);
+        for (int j = 0; j < dim; j++)
+            out[r * dim + j] = qwo_f32_to_f16((float)codes[r * dim + j] * s);
+    }
+    return 0;
+}
+
 int qwo_affine_dequantize(const uint32_t* codes, const uint16_t* scales,
                           const uint16_t* biases, int64_t n_rows, int dim, int group,
                           int bits, uint16_t* out) {

@@ -48,6 +48,17 @@ int qwo_affine_dequantize(const uint32_t* codes, const uint16_t* scales,
                           const uint16_t* biases, int64_t n_rows, int dim, int group,
                           int bits, uint16_t* out);
 
+/* Int8 per-token KV codec (cache.rs:262-316 quantize_per_token / dequantize,
+ * MLX fp16 ops): per row of `dim` fp16 values, scale = f16(absmax / 127),
+ * replaced by 1 when it is 0; code = clip(round(f16(x / scale)), -128, 127)
+ * with round ties-to-even (std::rint). codes: n_rows * dim int8; scales:
+ * n_rows fp16. Dequantize: out = f16(code * scale). Return 0, or -1 on a bad
+ * argument. */
+int qwo_int8_quantize(const uint16_t* w, int64_t n_rows, int dim, int8_t* codes,
+                      uint16_t* scales);
+int qwo_int8_dequantize(const int8_t* codes, const uint16_t* scales, int64_t n_rows, int dim,
+                        uint16_t* out);
+
 /* MLX CPU-stream SDPA over fp16 tensors with the fallback's fp16 roundings.
  *   q   [hq, L, D]   (row r of head h at q + (h * L + r) * D)
  *   k,v [hkv, T, D]

@@ -124,15 +124,18 @@ class KVCacheMode:
     FP16 = 0
     AFFINE8 = 1
     AFFINE4 = 2
+    INT8 = 3  # per-token absmax Int8 (cache.rs:262-316)
+
+    BITS = {0: 16, 1: 8, 2: 4, 3: 8}
 
     @staticmethod
     def from_str(s: str) -> int:
         key = s.lower()
         table = {"fp16": 0, "float16": 0, "affine8": 1, "uniform8": 1, "affine4": 2,
-                 "uniform4": 2}
+                 "uniform4": 2, "int8": 3}
         if key not in table:
-            raise ValueError(f'unknown kv-cache-mode "{s}"; expected "fp16", "affine8" or '
-                             f'"affine4"')
+            raise ValueError(f'unknown kv-cache-mode "{s}"; expected "fp16", "affine8", '
+                             f'"affine4" or "int8"')
         return table[key]
 
 
@@ -147,7 +150,7 @@ class KVCache:
         self.mode = mode
         self.n_kv_heads = n_kv_heads
         self.head_dim = head_dim
-        self.bits = {0: 16, 1: 8, 2: 4}[mode]
+        self.bits = KVCacheMode.BITS[mode]
         self.device = torch.device("cuda", torch.cuda.current_device() if device is None else
                                    torch.device(device).index or 0)
         h = _p()
@@ -251,7 +254,7 @@ class KVCache:
         _check(lib().qw_kv_demote(self._h, target_mode, _stream(self.device), ctypes.byref(d)))
         if d.value:
             self.mode = target_mode
-            self.bits = {0: 16, 1: 8, 2: 4}[target_mode]
+            self.bits = KVCacheMode.BITS[target_mode]
         return bool(d.value)
 
     def trim(self, n: int) -> int:
@@ -270,6 +273,16 @@ class KVCache:
             _check(lib().qw_kv_export(self._h, k.data_ptr(), None, None, v.data_ptr(), None, None,
                                       st))
             return {"keys": k, "values": v}
+        if self.mode == KVCacheMode.INT8:
+            # the reference's keys, values [H, T, D] int8; key_scales, val_scales [H, T, 1] f16
+            t = {name: torch.empty((H, n, D), dtype=torch.int8, device=self.device)
+                 for name in ("keys", "values")}
+            for name in ("key_scales", "val_scales"):
+                t[name] = torch.empty((H, n, 1), dtype=torch.float16, device=self.device)
+            _check(lib().qw_kv_export(self._h, t["keys"].data_ptr(), t["key_scales"].data_ptr(),
+                                      None, t["values"].data_ptr(), t["val_scales"].data_ptr(),
+                                      None, st))
+            return t
         w = D * self.bits // 32
         t = {name: torch.empty((H, n, w), dtype=torch.int32, device=self.device)
              for name in ("k_codes", "v_codes")}
@@ -288,6 +301,12 @@ class KVCache:
                                       None, None, st))
             return
         t = {k2: v2.contiguous() for k2, v2 in tensors.items()}
+        if self.mode == KVCacheMode.INT8:
+            n = t["keys"].shape[1]
+            _check(lib().qw_kv_import(self._h, n, t["keys"].data_ptr(), t["key_scales"].data_ptr(),
+                                      None, t["values"].data_ptr(), t["val_scales"].data_ptr(),
+                                      None, st))
+            return
         n = t["k_codes"].shape[1]
         _check(lib().qw_kv_import(self._h, n, t["k_codes"].data_ptr(), t["k_scales"].data_ptr(),
                                   t["k_biases"].data_ptr(), t["v_codes"].data_ptr(),

@@ -53,6 +53,7 @@ struct BlockArgs {
     int qt0;            // first query tile of this launch
     int prow0, PR;      // first row and row count of this launch's partials
     float scale_h;      // f16(scale) as float
+    uint32_t code_off2; // magic offset pair of the separately rounded dequant
 };
 
 // 8 waves, two a SIMD: one wave a SIMD leaves the MFMA, LDS and VALU
@@ -233,7 +234,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
             } else if constexpr (BITS == 8) {
                 const half2v sb = h2(st.kp[j]);
                 const half2v s = {sb.x, sb.x}, bb = {sb.y, sb.y};
-                const PairConsts pc = make_consts<FAST, 8>(s, s, s, s, bb, bb, bb, bb);
+                const PairConsts pc = make_consts<FAST, 8>(s, s, s, s, bb, bb, bb, bb, a.code_off2);
 #pragma unroll
                 for (int w = 0; w < 4; w++)
                     krow[w] = deq8<FAST>(st.kc[j][w / 2][2 * (w % 2)], st.kc[j][w / 2][2 * (w % 2) + 1], pc);
@@ -246,7 +247,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
                 vc = make_consts<FAST, BITS>(h2(st.vp[j][0][0]), h2(st.vp[j][0][1]),
                                              h2(st.vp[j][0][2]), h2(st.vp[j][0][3]),
                                              h2(st.vp[j][1][0]), h2(st.vp[j][1][1]),
-                                             h2(st.vp[j][1][2]), h2(st.vp[j][1][3]));
+                                             h2(st.vp[j][1][2]), h2(st.vp[j][1][3]), a.code_off2);
             half8* vblk = sV8 + vb[j] * VROW;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
@@ -546,6 +547,7 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     a.R = R;
     a.causal = causal ? 1 : 0;
     a.scale_h = (float)(f16)scale;
+    a.code_off2 = cc.code_offset2();
     a.qt0 = 0;
     a.prow0 = 0;
     a.PR = R;

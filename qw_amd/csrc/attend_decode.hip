@@ -49,6 +49,7 @@ struct DecodeArgs {
     float2* part_ml;   // [hkv][nc][16]
     int cap, T, Tq, G, R, causal, n_sub, nc;
     float scale_h;     // f16(scale) as float
+    uint32_t code_off2;  // magic offset pair of the separately rounded dequant
 };
 
 template <int BITS, int D>
@@ -298,8 +299,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
                 const half2v sb0 = h2(st.kp[0][slot]), sb1 = h2(st.kp[1][slot]);
                 const half2v s0 = {sb0.x, sb0.x}, b0 = {sb0.y, sb0.y};
                 const half2v s1 = {sb1.x, sb1.x}, b1 = {sb1.y, sb1.y};
-                const PairConsts p0 = make_consts<FAST, 8>(s0, s0, s0, s0, b0, b0, b0, b0);
-                const PairConsts p1 = make_consts<FAST, 8>(s1, s1, s1, s1, b1, b1, b1, b1);
+                const PairConsts p0 = make_consts<FAST, 8>(s0, s0, s0, s0, b0, b0, b0, b0, a.code_off2);
+                const PairConsts p1 = make_consts<FAST, 8>(s1, s1, s1, s1, b1, b1, b1, b1, a.code_off2);
                 acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                     deq8<FAST>(st.kc[0][m / 2][2 * (m % 2)], st.kc[0][m / 2][2 * (m % 2) + 1], p0),
                     sm_q[m][lane], acc0, 0, 0, 0);
@@ -322,7 +323,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
         if constexpr (AFF)
             pc = make_consts<FAST, BITS>(h2(st.vp[0][0]), h2(st.vp[0][1]), h2(st.vp[0][2]),
                                          h2(st.vp[0][3]), h2(st.vp[0][0]), h2(st.vp[0][1]),
-                                         h2(st.vp[0][2]), h2(st.vp[0][3]));
+                                         h2(st.vp[0][2]), h2(st.vp[0][3]), a.code_off2);
 #pragma unroll
         for (int mm = 0; mm < DPL; mm++) {
             half8 bv;
@@ -591,6 +592,7 @@ static int launch_decode_partials(KVCache& cc, const f16* q, int G, int Tq, int 
     a.n_sub = n_sub;
     a.nc = nc;
     a.scale_h = (float)(f16)scale;
+    a.code_off2 = cc.code_offset2();
     size_t shmem = (size_t)NW * (D / 16) * (((a.R + 3) / 4) * 16 + 1) * 16;  // wave-merge sm_o
     // Dynamic LDS above 64 KB must be allowed per kernel; raise the limit to
     // what this launch needs (once per size, per template instance).
@@ -954,7 +956,7 @@ int KVCache::update_and_attention(const void* q, int n_q_heads, int n_rows, cons
     QW_REQUIRE(n_q_heads > 0 && n_q_heads % hkv == 0 && n_rows > 0, QW_ERR_INVALID_ARGUMENT,
                "update_and_attention: bad head or row geometry");
     const int G = n_q_heads / hkv;
-    if (QW_FUSED_DECODE_APPEND && affine() && n_rows == 1 && G <= 16) {
+    if (QW_FUSED_DECODE_APPEND && affine() && !int8() && n_rows == 1 && G <= 16) {
         // decode: the append rides in the split-K merge (one launch fewer)
         DeviceGuard dg(device);
         QW_REQUIRE(dg.ok, QW_ERR_HIP, "update_and_attention: hipSetDevice failed");

@@ -15,8 +15,9 @@
 //         Exact when -1024*scale is a finite fp16 (|scale| < 64) and, for the
 //         x16 fields, scale/16 is a normal fp16 (|scale| >= 2^-10).
 //   SLOW: c = x - 1024 (exact; x16 fields also * 1/16, exact), then a
-//         separately rounded multiply and add. Used for a sub-chunk whose
-//         scales miss the FAST range.
+//         separately rounded multiply and add. Used for a cache whose
+//         scales miss the FAST range, and for Int8 caches, whose codes are
+//         stored biased by 128: c = x - 1152 is the signed code, bias 0.
 #pragma once
 
 #include "qw_common.hpp"
@@ -44,13 +45,14 @@ constexpr uint32_t kFastHi = 0x5400u;   // 64
 // bias term of a group separately (scale and bias are per group, so
 // sum_d x_d (c_d s + b) = sum_d x_d f16(c_d s) + b sum_d x_d).
 template <bool FAST, bool X16, bool ADDB = true>
-__device__ __forceinline__ half2v deq_pair(uint32_t magic_bits, half2v s, half2v m, half2v b) {
+__device__ __forceinline__ half2v deq_pair(uint32_t magic_bits, half2v s, half2v m, half2v b,
+                                           half2v off) {
     const half2v x = h2(magic_bits);
     half2v p;
     if constexpr (FAST) {
         p = __builtin_elementwise_fma(x, s, m);
     } else {
-        half2v c = x - (half2v){(f16)1024.0f, (f16)1024.0f};
+        half2v c = x - off;
         if constexpr (X16) c = c * (half2v){(f16)0.0625f, (f16)0.0625f};
         p = c * s;
     }
@@ -60,16 +62,19 @@ __device__ __forceinline__ half2v deq_pair(uint32_t magic_bits, half2v s, half2v
 
 // Constants of the four pairs a word produces. FAST: s[1], s[3] are scale/16
 // (the x16 fields of 4-bit words), m[i] = -1024 * s[i]. SLOW: s[i] plain
-// scales, m unused.
+// scales, m unused, off the magic offset (1024, or 1152 for Int8 codes).
 struct PairConsts {
     half2v s[4], m[4], b[4];
+    half2v off;
 };
 
 // Builds the constants from the plain (scale, bias) pairs of the four pairs.
 template <bool FAST, int BITS>
 __device__ __forceinline__ PairConsts make_consts(half2v s0, half2v s1, half2v s2, half2v s3,
-                                                  half2v b0, half2v b1, half2v b2, half2v b3) {
+                                                  half2v b0, half2v b1, half2v b2, half2v b3,
+                                                  uint32_t off2 = kMagic) {
     PairConsts c;
+    c.off = h2(off2);
     c.s[0] = s0;
     c.s[1] = s1;
     c.s[2] = s2;
@@ -99,10 +104,10 @@ __device__ __forceinline__ PairConsts make_consts(half2v s0, half2v s1, half2v s
 template <bool FAST, bool ADDB = true>
 __device__ __forceinline__ half8 deq4(uint32_t w, const PairConsts& c, uint32_t magic) {
     const uint32_t w8 = w >> 8;
-    const half2v y0 = deq_pair<FAST, false, ADDB>((w & 0x000F000Fu) | magic, c.s[0], c.m[0], c.b[0]);
-    const half2v y1 = deq_pair<FAST, true, ADDB>((w & 0x00F000F0u) | magic, c.s[1], c.m[1], c.b[1]);
-    const half2v y2 = deq_pair<FAST, false, ADDB>((w8 & 0x000F000Fu) | magic, c.s[2], c.m[2], c.b[2]);
-    const half2v y3 = deq_pair<FAST, true, ADDB>((w8 & 0x00F000F0u) | magic, c.s[3], c.m[3], c.b[3]);
+    const half2v y0 = deq_pair<FAST, false, ADDB>((w & 0x000F000Fu) | magic, c.s[0], c.m[0], c.b[0], c.off);
+    const half2v y1 = deq_pair<FAST, true, ADDB>((w & 0x00F000F0u) | magic, c.s[1], c.m[1], c.b[1], c.off);
+    const half2v y2 = deq_pair<FAST, false, ADDB>((w8 & 0x000F000Fu) | magic, c.s[2], c.m[2], c.b[2], c.off);
+    const half2v y3 = deq_pair<FAST, true, ADDB>((w8 & 0x00F000F0u) | magic, c.s[3], c.m[3], c.b[3], c.off);
     return half8{y0.x, y0.y, y1.x, y1.y, y2.x, y2.y, y3.x, y3.y};
 }
 
@@ -110,13 +115,13 @@ __device__ __forceinline__ half8 deq4(uint32_t w, const PairConsts& c, uint32_t 
 template <bool FAST, bool ADDB = true>
 __device__ __forceinline__ half8 deq8(uint32_t w0, uint32_t w1, const PairConsts& c) {
     const half2v y0 = deq_pair<FAST, false, ADDB>(__builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u),
-                                                  c.s[0], c.m[0], c.b[0]);
+                                                  c.s[0], c.m[0], c.b[0], c.off);
     const half2v y1 = deq_pair<FAST, false, ADDB>(__builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u),
-                                                  c.s[1], c.m[1], c.b[1]);
+                                                  c.s[1], c.m[1], c.b[1], c.off);
     const half2v y2 = deq_pair<FAST, false, ADDB>(__builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u),
-                                                  c.s[2], c.m[2], c.b[2]);
+                                                  c.s[2], c.m[2], c.b[2], c.off);
     const half2v y3 = deq_pair<FAST, false, ADDB>(__builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u),
-                                                  c.s[3], c.m[3], c.b[3]);
+                                                  c.s[3], c.m[3], c.b[3], c.off);
     return half8{y0.x, y0.y, y1.x, y1.y, y2.x, y2.y, y3.x, y3.y};
 }
 

@@ -61,21 +61,23 @@ static int alloc_zero(void** p, size_t bytes) {
 
 int KVCache::init(int mode_, int group_size, int n_kv_heads, int head_dim, int capacity,
                   int device_) {
-    QW_REQUIRE(mode_ == QW_KV_FP16 || mode_ == QW_KV_AFFINE8 || mode_ == QW_KV_AFFINE4,
+    QW_REQUIRE(mode_ == QW_KV_FP16 || mode_ == QW_KV_AFFINE8 || mode_ == QW_KV_AFFINE4 ||
+                   mode_ == QW_KV_INT8,
                QW_ERR_INVALID_ARGUMENT, "qw_kv_create: unknown mode");
     QW_REQUIRE(n_kv_heads > 0 && capacity >= 0 && head_dim > 0, QW_ERR_INVALID_ARGUMENT,
                "qw_kv_create: n_kv_heads, head_dim must be > 0 and capacity >= 0");
-    if (mode_ != QW_KV_FP16) {
+    if (mode_ == QW_KV_AFFINE8 || mode_ == QW_KV_AFFINE4) {
         QW_REQUIRE(group_size == kGroup, QW_ERR_UNSUPPORTED,
                    "qw_kv_create: affine modes use group_size 64");
         QW_REQUIRE(head_dim == 256 || head_dim == 128, QW_ERR_UNSUPPORTED,
                    "qw_kv_create: affine modes support head_dim 128 or 256");
     } else {
+        // fp16 and the per-token Int8 mode have no group; group_size is ignored
         QW_REQUIRE(head_dim == 256 || head_dim == 128, QW_ERR_UNSUPPORTED,
-                   "qw_kv_create: fp16 mode supports head_dim 128 or 256");
+                   "qw_kv_create: fp16 and int8 modes support head_dim 128 or 256");
     }
     mode = mode_;
-    bits = mode_ == QW_KV_AFFINE4 ? 4 : (mode_ == QW_KV_AFFINE8 ? 8 : 16);
+    bits = mode_ == QW_KV_AFFINE4 ? 4 : (mode_ == QW_KV_FP16 ? 16 : 8);
     D = head_dim;
     hkv = n_kv_heads;
     device = device_;
@@ -89,8 +91,9 @@ int KVCache::init(int mode_, int group_size, int n_kv_heads, int head_dim, int c
         set_error("qw_kv_create: hipMalloc failed");
         return QW_ERR_OUT_OF_MEMORY;
     }
-    const int one = 1;
-    QW_HIP_CHECK(hipMemcpy(fast_flag, &one, sizeof(int), hipMemcpyHostToDevice));
+    // Int8 codes always take the separately rounded dequant (offset 1152).
+    const int fast0 = int8() ? 0 : 1;
+    QW_HIP_CHECK(hipMemcpy(fast_flag, &fast0, sizeof(int), hipMemcpyHostToDevice));
     return reserve(capacity, nullptr);
 }
 
@@ -244,8 +247,38 @@ int KVCache::trim(int n) {
 // Codes go through LDS so the V block words (8 keys per dim) are assembled
 // by one thread each: no two threads write the same word.
 
+// Int8 (cache.rs:270-305 quantize_per_token, MLX fp16 ops): absmax over the
+// row; scale = f16(absmax / 127), 1 where that is 0; code = clip(round(
+// f16(x / scale)), -128, 127), stored as code + 128 with (scale, 0) in every
+// group slot. fp16 division rounded once from the fp32 quotient equals the
+// correctly rounded fp16 division (24 >= 2*11 + 2 bits).
 template <int D>
-__device__ inline void quantize_row(const f16* __restrict__ src, int bits, uint8_t* lds_codes,
+__device__ inline void quantize_row_int8(const float* x, uint8_t* lds_codes, half2v* sb_out) {
+    constexpr int VPL = D / 64;
+    const int lane = threadIdx.x & 63;
+    float am = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPL; i++) am = fmaxf(am, fabsf(x[i]));
+    am = wave_reduce(am, OpMax());
+    f16 sc = (f16)(am / 127.0f);
+    if ((float)sc == 0.0f) sc = (f16)1.0f;
+    const float s = (float)sc;
+#pragma unroll
+    for (int i = 0; i < VPL; i++) {
+        const float c = __builtin_rintf((float)(f16)(x[i] / s));
+        lds_codes[lane * VPL + i] = (uint8_t)((int)fminf(fmaxf(c, -128.0f), 127.0f) + 128);
+    }
+    if (lane < D / kGroup) {
+        half2v sb;
+        sb.x = sc;
+        sb.y = (f16)0.0f;
+        sb_out[lane] = sb;
+    }
+}
+
+template <int D>
+__device__ inline void quantize_row(const f16* __restrict__ src, int bits, bool int8,
+                                    uint8_t* lds_codes,
                                     half2v* sb_out /* [D/64] (scale, bias) */, int* fast_flag) {
     constexpr int VPL = D / 64;         // values per lane
     constexpr int LPG = kGroup / VPL;   // lanes per group
@@ -253,6 +286,10 @@ __device__ inline void quantize_row(const f16* __restrict__ src, int bits, uint8
     float x[VPL];
 #pragma unroll
     for (int i = 0; i < VPL; i++) x[i] = (float)src[lane * VPL + i];
+    if (int8) {
+        quantize_row_int8<D>(x, lds_codes, sb_out);
+        return;
+    }
     float mx = x[0], mn = x[0];
 #pragma unroll
     for (int i = 1; i < VPL; i++) {
@@ -281,7 +318,7 @@ __device__ inline void quantize_row(const f16* __restrict__ src, int bits, uint8
 template <int D>
 __global__ __launch_bounds__(256) void append_affine_kernel(
     const f16* __restrict__ k_new, const f16* __restrict__ v_new, int n_tokens, int t_old,
-    int bits, int cap, uint32_t* __restrict__ k_codes, uint32_t* __restrict__ k_params,
+    int bits, int int8, int cap, uint32_t* __restrict__ k_codes, uint32_t* __restrict__ k_params,
     uint32_t* __restrict__ v_codes, f16* __restrict__ v_params, int* __restrict__ fast_flag) {
     constexpr int NG = D / kGroup;
     __shared__ uint8_t kc[8][D];
@@ -312,8 +349,8 @@ __global__ __launch_bounds__(256) void append_affine_kernel(
         const int t = blk * 8 + k;
         if (t < t_old || t >= t_end) continue;
         const int64_t src = ((int64_t)h * n_tokens + (t - t_old)) * D;
-        quantize_row<D>(k_new + src, bits, kc[k], ksb[k], fast_flag);
-        quantize_row<D>(v_new + src, bits, vc[k], vsb[k], fast_flag);
+        quantize_row<D>(k_new + src, bits, int8 != 0, kc[k], ksb[k], fast_flag);
+        quantize_row<D>(v_new + src, bits, int8 != 0, vc[k], vsb[k], fast_flag);
     }
     __syncthreads();
     // K: row-major MLX packing, words of 32/bits codes LSB-first.
@@ -403,14 +440,14 @@ int KVCache::update(const void* k_new, const void* v_new, int n_tokens, hipStrea
         dim3 grid(nblk, hkv);
         if (D == 256)
             hipLaunchKernelGGL(append_affine_kernel<256>, grid, dim3(256), 0, stream,
-                               (const f16*)k_new, (const f16*)v_new, n_tokens, offset, bits, cap,
-                               (uint32_t*)k_data, k_params, (uint32_t*)v_data, (f16*)v_params,
-                               fast_flag);
+                               (const f16*)k_new, (const f16*)v_new, n_tokens, offset, bits,
+                               int8() ? 1 : 0, cap, (uint32_t*)k_data, k_params,
+                               (uint32_t*)v_data, (f16*)v_params, fast_flag);
         else
             hipLaunchKernelGGL(append_affine_kernel<128>, grid, dim3(256), 0, stream,
-                               (const f16*)k_new, (const f16*)v_new, n_tokens, offset, bits, cap,
-                               (uint32_t*)k_data, k_params, (uint32_t*)v_data, (f16*)v_params,
-                               fast_flag);
+                               (const f16*)k_new, (const f16*)v_new, n_tokens, offset, bits,
+                               int8() ? 1 : 0, cap, (uint32_t*)k_data, k_params,
+                               (uint32_t*)v_data, (f16*)v_params, fast_flag);
     } else {
         const int64_t n = (int64_t)n_tokens * D;
         dim3 grid((unsigned)std::min<int64_t>((n + 255) / 256, 1024), hkv);
@@ -435,8 +472,10 @@ int KVCache::update(const void* k_new, const void* v_new, int n_tokens, hipStrea
 // the fp16 product; the sum is formed in fp32 and cast once more, which is
 // how MLX's CPU float16 type evaluates `a + b`.
 
-__device__ inline f16 mlx_dequant(uint32_t c, f16 s, f16 b) {
-    const f16 prod = (f16)((float)c * (float)s);
+// `off` is 128 for Int8 codes stored biased by 128 (bias 0: the result is
+// f16(code * scale), the reference's Int8 dequantize, cache.rs:313-316).
+__device__ inline f16 mlx_dequant(uint32_t c, int off, f16 s, f16 b) {
+    const f16 prod = (f16)((float)((int)c - off) * (float)s);
     return (f16)((float)prod + (float)b);
 }
 
@@ -445,8 +484,9 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint32_t* __restrict
                                                       const uint32_t* __restrict__ k_params,
                                                       const uint32_t* __restrict__ v_codes,
                                                       const f16* __restrict__ v_params,
-                                                      int bits, int D, int cap, int hkv,
-                                                      int start, int n, f16* __restrict__ k_out,
+                                                      int bits, int code_off, int D, int cap,
+                                                      int hkv, int start, int n,
+                                                      f16* __restrict__ k_out,
                                                       f16* __restrict__ v_out) {
     const int64_t oct = D / 8;
     const int64_t total = (int64_t)hkv * n * oct;
@@ -472,7 +512,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint32_t* __restrict
             const int d = d0 + e;
             const int epw = 32 / bits;
             const uint32_t kcode = (krow[d / epw] >> ((d % epw) * bits)) & m;
-            ko[e] = mlx_dequant(kcode, ksb.x, ksb.y);
+            ko[e] = mlx_dequant(kcode, code_off, ksb.x, ksb.y);
             const int p = v_phys_dim(d, D, bits);
             const int k = t & 7;
             uint32_t vcode;
@@ -480,7 +520,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint32_t* __restrict
                 vcode = (vblk[p] >> (4 * v4_nibble_pos(k))) & 0xFu;
             else
                 vcode = (vblk[2 * p + (k >> 2)] >> (8 * (k & 3))) & 0xFFu;
-            vo[e] = mlx_dequant(vcode, vs, vbias);
+            vo[e] = mlx_dequant(vcode, code_off, vs, vbias);
         }
         const int64_t o = ((int64_t)h * n + r) * D + d0;
         *(half8*)(k_out + o) = ko;
@@ -518,8 +558,8 @@ int KVCache::dequantize(int start, int n, void* k_out, void* v_out, hipStream_t 
     if (affine())
         hipLaunchKernelGGL(dequant_kernel, dim3(blocks), dim3(256), 0, stream,
                            (const uint32_t*)k_data, k_params, (const uint32_t*)v_data,
-                           (const f16*)v_params, bits, D, cap, hkv, start, n, (f16*)k_out,
-                           (f16*)v_out);
+                           (const f16*)v_params, bits, int8() ? 128 : 0, D, cap, hkv, start, n,
+                           (f16*)k_out, (f16*)v_out);
     else
         hipLaunchKernelGGL(fetch_fp16_kernel, dim3(blocks), dim3(256), 0, stream,
                            (const f16*)k_data, (const f16*)v_data, D, cap, hkv, start, n,
@@ -542,8 +582,11 @@ int KVCache::update_and_fetch(const void* k_new, const void* v_new, int n_tokens
 // exports packed tensors as they are, without requantizing).
 
 // V blocks <-> rows, plus the K param split/merge. dir = 0: export.
+// Int8 mode: codes leave and enter as signed bytes (stored + 128, i.e. XOR
+// 0x80 per byte) and one scale per row (the first group's; every group holds
+// it, with bias 0).
 __global__ __launch_bounds__(256) void snapshot_affine_kernel(
-    int dir, int bits, int D, int cap, int hkv, int n, int* __restrict__ fast_flag,
+    int dir, int bits, int int8, int D, int cap, int hkv, int n, int* __restrict__ fast_flag,
     uint32_t* __restrict__ k_params,
     uint32_t* __restrict__ v_codes, f16* __restrict__ v_params, f16* __restrict__ ks_out,
     f16* __restrict__ kb_out, uint32_t* __restrict__ vc_rows, f16* __restrict__ vs_rows,
@@ -569,13 +612,27 @@ __global__ __launch_bounds__(256) void snapshot_affine_kernel(
                                              : (vblk[2 * p + (k >> 2)] >> (8 * (k & 3))) & m;
                 word |= c << (e * bits);
             }
-            vc_rows[row * nw + w] = word;
+            vc_rows[row * nw + w] = int8 ? word ^ 0x80808080u : word;
         }
         if (w < NG) {
             const int g = w;
             const int64_t kp = ((int64_t)h * cap + t) * NG + k_param_slot(g, NG);
             f16* vp = v_params + (((int64_t)h * (cap / 8) + t / 8) * NG + g) * 16;
-            if (dir == 0) {
+            if (int8) {
+                if (dir == 0) {
+                    if (g == 0) {
+                        ks_out[row] = __builtin_bit_cast(half2v, k_params[kp]).x;
+                        vs_rows[row] = vp[k];
+                    }
+                } else {
+                    half2v sb;
+                    sb.x = ks_out[row];
+                    sb.y = (f16)0.0f;
+                    k_params[kp] = __builtin_bit_cast(uint32_t, sb);
+                    vp[k] = vs_rows[row];
+                    vp[8 + k] = (f16)0.0f;
+                }
+            } else if (dir == 0) {
                 const half2v sb = __builtin_bit_cast(half2v, k_params[kp]);
                 ks_out[row * NG + g] = sb.x;
                 kb_out[row * NG + g] = sb.y;
@@ -598,8 +655,8 @@ __global__ __launch_bounds__(256) void snapshot_affine_kernel(
 __global__ void set_flag_kernel(int* flag, int v) { *flag = v; }
 
 // Import of V codes: one thread per (head, block, dim) builds the block word(s).
-__global__ __launch_bounds__(256) void import_v_codes_kernel(int bits, int D, int cap, int hkv,
-                                                             int n,
+__global__ __launch_bounds__(256) void import_v_codes_kernel(int bits, int int8, int D, int cap,
+                                                             int hkv, int n,
                                                              const uint32_t* __restrict__ rows,
                                                              uint32_t* __restrict__ v_codes) {
     const int nblk = (n + 7) / 8;
@@ -624,6 +681,11 @@ __global__ __launch_bounds__(256) void import_v_codes_kernel(int bits, int D, in
             else
                 w1 |= c << (8 * (k - 4));
         }
+        if (int8) {
+            // Int8: signed bytes in, biased bytes stored (slots past n stay 128 = code 0)
+            w0 ^= 0x80808080u;
+            w1 ^= 0x80808080u;
+        }
         uint32_t* vblk = v_codes + ((int64_t)h * (cap / 8) + b) * (D * bits / 4);
         const int p = v_phys_dim(d, D, bits);
         if (bits == 4) {
@@ -635,10 +697,23 @@ __global__ __launch_bounds__(256) void import_v_codes_kernel(int bits, int D, in
     }
 }
 
+// XOR 0x80 into every byte of rows [0, n) of each head's row-major K codes
+// ([hkv][stride][nw] words): signed <-> biased Int8 codes.
+__global__ __launch_bounds__(256) void flip_code_sign_kernel(uint32_t* __restrict__ words, int hkv,
+                                                             int n, int nw, int stride) {
+    const int64_t total = (int64_t)hkv * n * nw;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int h = (int)(i / ((int64_t)n * nw));
+        const int64_t r = i % ((int64_t)n * nw);
+        words[(int64_t)h * stride * nw + r] ^= 0x80808080u;
+    }
+}
+
 int KVCache::export_tensors(void* k_codes, void* k_scales, void* k_biases, void* v_codes,
                             void* v_scales, void* v_biases, hipStream_t stream) const {
     QW_REQUIRE(k_codes && v_codes, QW_ERR_INVALID_ARGUMENT, "export: null code pointers");
-    QW_REQUIRE(!affine() || (k_scales && k_biases && v_scales && v_biases),
+    QW_REQUIRE(!affine() || (k_scales && v_scales && (int8() || (k_biases && v_biases))),
                QW_ERR_INVALID_ARGUMENT, "export: null scale/bias pointers");
     if (offset == 0) return QW_OK;
     DeviceGuard dg(device);
@@ -653,9 +728,14 @@ int KVCache::export_tensors(void* k_codes, void* k_scales, void* k_biases, void*
                                     (const char*)k_data + h * (size_t)cap * kr, n * kr,
                                     hipMemcpyDeviceToDevice, stream));
     const int64_t work = (int64_t)hkv * n * (D * bits / 32);
-    hipLaunchKernelGGL(snapshot_affine_kernel,
-                       dim3((unsigned)std::min<int64_t>((work + 255) / 256, 4096)), dim3(256), 0,
-                       stream, 0, bits, D, cap, hkv, n, fast_flag, k_params, (uint32_t*)v_data,
+    const unsigned nb = (unsigned)std::min<int64_t>((work + 255) / 256, 4096);
+    if (int8()) {
+        hipLaunchKernelGGL(flip_code_sign_kernel, dim3(nb), dim3(256), 0, stream,
+                           (uint32_t*)k_codes, hkv, n, D / 4, n);
+        QW_HIP_CHECK(hipGetLastError());
+    }
+    hipLaunchKernelGGL(snapshot_affine_kernel, dim3(nb), dim3(256), 0, stream, 0, bits,
+                       int8() ? 1 : 0, D, cap, hkv, n, fast_flag, k_params, (uint32_t*)v_data,
                        (f16*)v_params, (f16*)k_scales, (f16*)k_biases, (uint32_t*)v_codes,
                        (f16*)v_scales, (f16*)v_biases);
     QW_HIP_CHECK(hipGetLastError());
@@ -667,7 +747,7 @@ int KVCache::import_tensors(int n_tokens, const void* k_codes, const void* k_sca
                             const void* v_biases, hipStream_t stream) {
     QW_REQUIRE(n_tokens >= 0, QW_ERR_INVALID_ARGUMENT, "import: n_tokens must be >= 0");
     QW_REQUIRE(k_codes && v_codes, QW_ERR_INVALID_ARGUMENT, "import: null code pointers");
-    QW_REQUIRE(!affine() || (k_scales && k_biases && v_scales && v_biases),
+    QW_REQUIRE(!affine() || (k_scales && v_scales && (int8() || (k_biases && v_biases))),
                QW_ERR_INVALID_ARGUMENT, "import: null scale/bias pointers");
     DeviceGuard dg(device);
     offset = 0;
@@ -681,20 +761,26 @@ int KVCache::import_tensors(int n_tokens, const void* k_codes, const void* k_sca
         QW_HIP_CHECK(hipMemcpyAsync((char*)k_data + h * (size_t)cap * kr,
                                     (const char*)k_codes + h * (size_t)n * kr, n * kr,
                                     hipMemcpyDeviceToDevice, stream));
-    // The imported scales decide the fused kernels' dequant path afresh.
-    hipLaunchKernelGGL(set_flag_kernel, dim3(1), dim3(1), 0, stream, fast_flag, 1);
+    // The imported scales decide the fused kernels' dequant path afresh (Int8
+    // always takes the separately rounded one).
+    hipLaunchKernelGGL(set_flag_kernel, dim3(1), dim3(1), 0, stream, fast_flag, int8() ? 0 : 1);
     const int64_t work = (int64_t)hkv * n * (D * bits / 32);
-    hipLaunchKernelGGL(snapshot_affine_kernel,
-                       dim3((unsigned)std::min<int64_t>((work + 255) / 256, 4096)), dim3(256), 0,
-                       stream, 1, bits, D, cap, hkv, n, fast_flag, k_params, (uint32_t*)v_data,
+    const unsigned nb = (unsigned)std::min<int64_t>((work + 255) / 256, 4096);
+    if (int8()) {
+        hipLaunchKernelGGL(flip_code_sign_kernel, dim3(nb), dim3(256), 0, stream,
+                           (uint32_t*)k_data, hkv, n, D / 4, cap);
+        QW_HIP_CHECK(hipGetLastError());
+    }
+    hipLaunchKernelGGL(snapshot_affine_kernel, dim3(nb), dim3(256), 0, stream, 1, bits,
+                       int8() ? 1 : 0, D, cap, hkv, n, fast_flag, k_params, (uint32_t*)v_data,
                        (f16*)v_params, (f16*)k_scales, (f16*)k_biases, (uint32_t*)v_codes,
                        (f16*)v_scales, (f16*)v_biases);
     QW_HIP_CHECK(hipGetLastError());
     const int64_t vwork = (int64_t)hkv * ((n + 7) / 8) * D;
     hipLaunchKernelGGL(import_v_codes_kernel,
                        dim3((unsigned)std::min<int64_t>((vwork + 255) / 256, 4096)), dim3(256),
-                       0, stream, bits, D, cap, hkv, n, (const uint32_t*)v_codes,
-                       (uint32_t*)v_data);
+                       0, stream, bits, int8() ? 1 : 0, D, cap, hkv, n,
+                       (const uint32_t*)v_codes, (uint32_t*)v_data);
     QW_HIP_CHECK(hipGetLastError());
     offset = n;
     return QW_OK;

@@ -40,7 +40,15 @@ struct KVCache {
     size_t ws_bytes = 0;
 
     KvLayout layout() const { return KvLayout{bits, D, hkv, cap}; }
+    // Codes and per-group (scale, bias) in the affine layout: the affine modes
+    // and Int8 (stored as 8-bit codes biased by 128, the token's scale in
+    // every group, bias 0).
     bool affine() const { return mode != QW_KV_FP16; }
+    bool int8() const { return mode == QW_KV_INT8; }
+    // Offset the 8-bit magic-number conversion subtracts to recover a code
+    // (fp16 1024 + stored byte): 1024 for unsigned affine codes, 1152 for
+    // Int8 codes stored biased by 128.
+    uint32_t code_offset2() const { return int8() ? 0x64806480u : 0x64006400u; }
 
     size_t k_data_bytes(int c) const;
     size_t k_param_bytes(int c) const;

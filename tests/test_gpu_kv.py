@@ -424,3 +424,107 @@ def test_policy_demotes_real_caches_past_the_threshold():
     assert policy.prepare_attention_forward([short], conf, thr - 1, True) == 1
     assert short.mode == conf
     assert policy.prepare_attention_forward([short], conf, thr - 1, True) == 0
+
+
+# ------------------------------------------------------------- Int8 mode
+
+def _int8_layer_call(oracle_lib, qw_amd, T_prefix, L, causal, seed, D=256, hq=24, hkv=4):
+    r = rng(seed)
+    k, v = _kv(r, hkv, T_prefix + L, D)
+    q = r.standard_normal((hq, L, D)).astype(np.float16)
+    cache = qw_amd.KVCache("int8", hkv, D, capacity=T_prefix + L)
+    if T_prefix:
+        cache.update(_gpu(k[:, :T_prefix])[None], _gpu(v[:, :T_prefix])[None])
+    fn = cache.update_and_causal_attention if causal else cache.update_and_attention
+    out = _np(fn(_gpu(q)[None], _gpu(k[:, T_prefix:])[None], _gpu(v[:, T_prefix:])[None],
+                 1.0 / 16))[0]
+    orc = oracle_lib.Int8CacheOracle(hkv, D, T_prefix + L)
+    if T_prefix:
+        orc.update(k[:, :T_prefix], v[:, :T_prefix])
+    ref = orc.update_and_attention(q, k[:, T_prefix:], v[:, T_prefix:], 1.0 / 16, causal)
+    kd, vd = orc.fetch()
+    pos = oracle_lib.causal_positions(L, T_prefix + L) if causal else None
+    f64 = oracle_lib.sdpa_f64(q, kd, vd, 1.0 / 16, q_pos=pos)
+    return cache, orc, out, ref, f64
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("D", [256, 128])
+def test_int8_append_and_fetch_bit_exact(oracle_lib, D):
+    """Int8 quantize-on-append (cache.rs:270-305, update_int8 :1042) stores the
+    oracle's codes and scales exactly, across ragged appends that fill partial
+    8-key blocks; the fetch is f16(code * scale) bit for bit (cache.rs:313)."""
+    import qw_amd
+
+    r = rng(8000 + D)
+    H = 4
+    k, v = _kv(r, H, 203, D)
+    k[1, 17] = 0  # an all-zero token: scale 1, codes 0
+    cache = qw_amd.KVCache("int8", H, D, capacity=64)
+    orc = oracle_lib.Int8CacheOracle(H, D, 203)
+    t = 0
+    for n in (1, 6, 13, 40, 1, 142):
+        cache.update(_gpu(k[:, t:t + n])[None], _gpu(v[:, t:t + n])[None])
+        orc.update(k[:, t:t + n], v[:, t:t + n])
+        t += n
+    assert cache.offset == 203
+    snap = cache.snapshot_tensors()
+    assert np.array_equal(_np(snap["keys"]), orc.keys[:, :203])
+    assert np.array_equal(_np(snap["values"]), orc.values[:, :203])
+    assert np.array_equal(_np(snap["key_scales"])[..., 0].view(np.uint16),
+                          orc.key_scales[:, :203].view(np.uint16))
+    assert np.array_equal(_np(snap["val_scales"])[..., 0].view(np.uint16),
+                          orc.val_scales[:, :203].view(np.uint16))
+    kd, vd = cache.dequantize()
+    ko, vo = orc.fetch()
+    assert np.array_equal(_np(kd)[0].view(np.uint16), ko.view(np.uint16))
+    assert np.array_equal(_np(vd)[0].view(np.uint16), vo.view(np.uint16))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T_prefix,L,causal", [
+    (4095, 1, False),    # decode over 4096 keys
+    (1000, 2, True),     # 2-row verify block (decode kernel)
+    (3000, 16, True),    # 16-row verify block (block kernel)
+    (300, 64, False),    # block kernel, no mask
+])
+def test_int8_attention_vs_oracle(oracle_lib, T_prefix, L, causal):
+    """Attention on an Int8 cache equals the reference's fetch-then-SDPA
+    (a6 + a10) within the stated tolerance."""
+    import qw_amd
+
+    _, _, out, ref, f64 = _int8_layer_call(oracle_lib, qw_amd, T_prefix, L, causal,
+                                           seed=31 + T_prefix + L)
+    assert np.isfinite(out).all()
+    assert_close(out, ref, f"int8 T={T_prefix}+{L}")
+    assert_as_exact_as_reference(out, ref, f64, f"int8 T={T_prefix}+{L}")
+
+
+@pytest.mark.gpu
+def test_int8_snapshot_round_trip_and_trim():
+    """Export -> import reproduces the cache (codes, scales, attention); trim
+    then re-append equals never appended."""
+    import qw_amd
+
+    r = rng(1234)
+    k, v = _kv(r, 4, 300, 256)
+    a = qw_amd.KVCache("int8", 4, 256)
+    a.update(_gpu(k[:, :290])[None], _gpu(v[:, :290])[None])
+    snap = a.snapshot_tensors()
+    b = qw_amd.KVCache("int8", 4, 256)
+    b.restore_snapshot(snap)
+    assert b.offset == 290
+    for name, t in b.snapshot_tensors().items():
+        assert torch.equal(t, snap[name]), name
+    q = r.standard_normal((24, 1, 256)).astype(np.float16)
+    oa = a.attention(_gpu(q)[None], 1.0 / 16)
+    ob = b.attention(_gpu(q)[None], 1.0 / 16)
+    assert torch.equal(oa, ob)
+    # trim then re-append the same rows
+    a.update(_gpu(k[:, 290:])[None], _gpu(v[:, 290:])[None])
+    assert a.trim(10) == 10
+    a.update(_gpu(k[:, 290:])[None], _gpu(v[:, 290:])[None])
+    c = qw_amd.KVCache("int8", 4, 256)
+    c.update(_gpu(k)[None], _gpu(v)[None])
+    for name, t in c.snapshot_tensors().items():
+        assert torch.equal(t, a.snapshot_tensors()[name]), name

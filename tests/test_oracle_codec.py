@@ -209,3 +209,66 @@ def test_dequantize_double_rounding(oracle_lib):
     out = oracle_lib.affine_dequantize(codes, s, b, 8)
     assert out[0, 0] == np.float16(766.0)
     assert out[0, 1] == np.float16(0.25)
+
+
+# ----------------------------------------------------------- Int8 per-token
+
+def test_int8_reference_known_answer_round_trip(oracle_lib):
+    """cache.rs:7480-7545 int8_kv_fetch_recovers_values_within_one_quant_step:
+    the reference's own values (two real tokens and an all-zero token per side)
+    come back within one step absmax/127 (x1.05, + 1e-3)."""
+    k = np.array([[0.30, -1.20, 2.50, -0.80], [4.10, -3.30, 0.05, 1.90], [0, 0, 0, 0]],
+                 np.float32)
+    v = np.array([[-5.60, 0.90, 3.10, -2.20], [0.15, -0.45, 0.60, -0.30], [0, 0, 0, 0]],
+                 np.float32)
+    for orig in (k, v):
+        x = orig.astype(np.float16)
+        codes, scales = oracle_lib.int8_quantize(x)
+        deq = oracle_lib.int8_dequantize(codes, scales).astype(np.float32)
+        absmax = np.abs(orig).max(1, keepdims=True)
+        tol = absmax / 127.0 * 1.05 + 1e-3
+        assert (np.abs(orig - deq) <= tol).all()
+        assert scales[2] == np.float16(1.0) and not codes[2].any()  # zero-token guard
+
+
+def test_int8_hand_computed_known_answer(oracle_lib):
+    """absmax 128: scale = f16(128/127 = 1.00787...) = 1.0078125 (1 + 8/1024).
+    127/s = 126.0155 -> f16 126.0 -> 126; -128/s = -127.0077 -> f16 -127.0 ->
+    -127 (the absmax element takes the extreme code); 63.5/s = 63.0078 -> f16
+    63.0 -> 63; 0.25/s = 0.248 -> 0. A scale kept in fp32 would give 63/126
+    differently only through the quotients' fp16 rounding, which this row
+    fixes exactly."""
+    x = np.zeros((1, 128), np.float16)
+    x[0, :4] = [127.0, -128.0, 63.5, 0.25]
+    codes, scales = oracle_lib.int8_quantize(x)
+    assert scales[0] == np.float16(1.0078125)
+    assert list(codes[0, :4]) == [126, -127, 63, 0] and not codes[0, 4:].any()
+    deq = oracle_lib.int8_dequantize(codes, scales)
+    assert deq[0, 0] == np.float16(126 * 1.0078125)  # 126.984375, exact in fp16
+
+
+def test_int8_invariants_and_brute_force(oracle_lib):
+    r = rng(808)
+    x = (r.standard_normal((400, 256)) * r.uniform(0.01, 30, (400, 1))).astype(np.float16)
+    x[7] = 0
+    codes, scales = oracle_lib.int8_quantize(x)
+    xf = x.astype(np.float64)
+    s = scales.astype(np.float64)[:, None]
+    absmax = np.abs(xf).max(1)
+    # scale is the fp16 rounding of absmax / 127 (1 for the zero row)
+    want_s = np.where(absmax == 0, 1.0, (absmax / 127.0).astype(np.float16).astype(np.float64))
+    assert np.array_equal(s[:, 0], want_s)
+    # the absmax element takes code +-127 (or 126/-128 at the fp16 edge)
+    i = np.abs(xf).argmax(1)
+    cm = np.abs(codes[np.arange(400), i].astype(int))
+    assert (cm[absmax > 0] >= 126).all()
+    # codes are the nearest integers to x / s up to the fp16 rounding of x / s
+    q = xf / s
+    c = codes.astype(np.float64)
+    slack = 0.5 + np.abs(q) * 2.0 ** -11 + 1e-12
+    inside = (q >= -128.5) & (q <= 127.5)
+    assert (np.abs(c - q)[inside] <= slack[inside]).all()
+    assert codes.min() >= -128 and codes.max() <= 127
+    # dequantize is the fp16 product
+    deq = oracle_lib.int8_dequantize(codes, scales)
+    assert np.array_equal(deq, (c * s).astype(np.float16))
