@@ -199,6 +199,31 @@ int qw_dlsa_sparse_attention_with(const void* q, const void* k, const void* v,
                                   int n_keys, float scale, int parts, int waves, void* out,
                                   void* stream);
 
+/* D-LSA K1 select: dlsa_select (crates/mlxcel-core/src/dlsa_kernels.rs:57-84)
+ * / dlsa_select_with (:88-117), the device twin of the host select
+ * (crates/runtime/src/dlsa/select.rs:65-115). For each of n_rows query rows:
+ *   scores    [n_rows][score_stride] f32: row r ranks its first
+ *             v = min(floor(positions[r] / window) * buckets_per_block,
+ *             total_rows) columns (when v > score_stride only the columns
+ *             present: status bit 2), score descending, -0 == +0, a NaN below
+ *             every number (status bit 1), ties to the lower bucket;
+ *   members   [n_member_rows][bucket_cap] i32, each bucket's key positions
+ *             ascending, -1 padded; total_rows <= n_member_rows;
+ *   positions [n_rows] i32 >= 0.
+ * Outputs (device, i32): picked [n_rows][top_p] (best first, -1 padded);
+ * lists [n_rows][top_k + window + sink]: the picked buckets' members in
+ * [sink, window_start) (pick order, members ascending, at most top_k), then
+ * the window [window_start, p], then the sinks [0, min(sink, window_start,
+ * p + 1)), -1 padded, with window_start = max(0, p + 1 - window); lengths
+ * [n_rows]; status [n_rows]. top_p <= 2048 (DLSA_TOP_P_MAX). `threads` is the
+ * workgroup size (0 = automatic, else a power of two in [64, 1024]); the
+ * outputs do not depend on it. */
+int qw_dlsa_select(const float* scores, int64_t score_stride, const int32_t* members,
+                   int n_member_rows, int bucket_cap, const int32_t* positions, int n_rows,
+                   int total_rows, int window, int sink, int top_k, int top_p,
+                   int buckets_per_block, int threads, int32_t* lists, int32_t* lengths,
+                   int32_t* picked, int32_t* status, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -323,3 +323,66 @@ class AffineCacheOracle:
             "affine_layer_call")
         self.offset += L
         return out
+
+
+# ------------------------------------------------------------ D-LSA K1 select
+
+SELECT_STATUS_NAN = 1
+SELECT_STATUS_SHORT_SCORES = 2
+
+
+def dlsa_select(scores: np.ndarray, members: np.ndarray, positions: np.ndarray,
+                total_rows: int, window: int, sink: int, top_k: int, top_p: int,
+                buckets_per_block: int):
+    """Read lists from bucket scores (crates/runtime/src/dlsa/select.rs:65-115,
+    the device contract of crates/mlxcel-core/src/dlsa_kernels.rs:57-84).
+
+    scores ``[R, S]`` f32, members ``[N, cap]`` i32 (ascending, -1 padded),
+    positions ``[R]``. Row r ranks its first ``min(floor(p / window) * m,
+    total_rows)`` columns (clipped to S, with status bit 2): score descending,
+    -0 == +0, a NaN below every number (status bit 1), ties to the lower
+    bucket; keeps the best ``top_p``; the list is the picked buckets' members
+    in ``[sink, window_start)`` (pick order, members ascending, at most
+    ``top_k``), then the window ``[window_start, p]``, then the sinks
+    ``[0, min(sink, window_start, p + 1))``, -1 padded.
+    Returns (lists [R, top_k+window+sink], lengths [R], picked [R, top_p],
+    status [R]), all int32."""
+    scores = np.asarray(scores, np.float32)
+    members = np.asarray(members, np.int32)
+    R = len(positions)
+    S = scores.shape[1] if scores.ndim == 2 else 0
+    cap = members.shape[1] if members.ndim == 2 else 0
+    width = top_k + window + sink
+    lists = np.full((R, width), -1, np.int32)
+    lengths = np.zeros(R, np.int32)
+    picked = np.full((R, top_p), -1, np.int32)
+    status = np.zeros(R, np.int32)
+    for r in range(R):
+        p = int(positions[r])
+        v = min(p // window * buckets_per_block, total_rows)
+        if v > S:
+            v = S
+            status[r] |= SELECT_STATUS_SHORT_SCORES
+        row = scores[r, :v]
+        nan = np.isnan(row)
+        if nan.any():
+            status[r] |= SELECT_STATUS_NAN
+        neg = np.where(nan, 0.0, -row.astype(np.float64))
+        neg = np.where(neg == 0.0, 0.0, neg)  # -0 == +0
+        order = np.lexsort((np.arange(v), neg, nan.astype(np.int8)))[:top_p]
+        picked[r, :len(order)] = order
+        ws = max(0, p + 1 - window)
+        out = []
+        for b in order:
+            for x in members[b, :cap]:
+                if x >= 0 and sink <= x < ws:
+                    if len(out) == top_k:
+                        break
+                    out.append(int(x))
+            if len(out) == top_k:
+                break
+        out.extend(range(ws, p + 1))
+        out.extend(range(min(sink, ws, p + 1)))
+        lists[r, :len(out)] = out
+        lengths[r] = len(out)
+    return lists, lengths, picked, status

@@ -64,6 +64,8 @@ _SIGNATURES = {
     "qw_kv_demote": (_i, [_p, _i, _p, ctypes.POINTER(_i)]),
     "qw_kv_export": (_i, [_p, _p, _p, _p, _p, _p, _p, _p]),
     "qw_kv_import": (_i, [_p, _i, _p, _p, _p, _p, _p, _p, _p]),
+    "qw_dlsa_select": (_i, [_p, _i64, _p, _i, _i, _p, _i, _i, _i, _i, _i, _i, _i, _i, _p, _p, _p,
+                            _p, _p]),
     "qw_dlsa_sparse_attention": (_i, [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _i, _i, _i,
                                       _i, _i, _i, _f, _p, _p]),
     "qw_dlsa_sparse_attention_with": (_i, [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _i, _i,
@@ -354,3 +356,60 @@ def sparse_attention_with(q, k, v, lists, lengths, scale: float, parts: int = 0,
 def sparse_attention(q, k, v, lists, lengths, scale: float):
     """D-LSA gathered read with the automatic launch policy (dlsa_attention.rs:31)."""
     return sparse_attention_with(q, k, v, lists, lengths, scale, 0, 0)
+
+
+# ------------------------------------------------------------ D-LSA K1 select
+
+DLSA_SELECT_STATUS_NAN = 1
+DLSA_SELECT_STATUS_SHORT_SCORES = 2
+DLSA_TOP_P_MAX = 2048
+
+
+class DlsaSelectParams:
+    """The flat-design knobs the select reads (dlsa_kernels.rs:24-38)."""
+
+    def __init__(self, window: int, sink: int, top_k: int, top_p: int, bucket_cap: int,
+                 buckets_per_block: int):
+        self.window, self.sink, self.top_k, self.top_p = window, sink, top_k, top_p
+        self.bucket_cap, self.buckets_per_block = bucket_cap, buckets_per_block
+
+    def list_width(self) -> int:
+        return self.top_k + self.window + self.sink
+
+
+def dlsa_select_with(scores, members, positions, total_rows: int, params: DlsaSelectParams,
+                     threads: int = 0):
+    """D-LSA K1 on the device (dlsa_kernels.rs:88 ``dlsa_select_with``): scores
+    ``[R, S]`` f32, members ``[N, bucket_cap]`` i32, positions ``[R]`` i32.
+    Returns ``(lists [R, top_k+window+sink], lengths [R], picked [R, top_p],
+    status [R])``, all int32 device tensors."""
+    torch = _torch()
+    if scores.dim() != 2 or scores.dtype != torch.float32 or not scores.is_cuda:
+        raise QwError(1, "dlsa_select: scores must be a [R, S] f32 device tensor")
+    if members.dim() != 2 or members.dtype != torch.int32 or not members.is_cuda:
+        raise QwError(1, "dlsa_select: members must be a [N, cap] i32 device tensor")
+    if positions.dim() != 1 or positions.dtype != torch.int32 or \
+            positions.shape[0] != scores.shape[0]:
+        raise QwError(1, "dlsa_select: positions must be [R] i32")
+    if members.shape[1] != params.bucket_cap:
+        raise QwError(1, "dlsa_select: members width differs from bucket_cap")
+    sc, mb, pos = scores.contiguous(), members.contiguous(), positions.contiguous()
+    R = sc.shape[0]
+    dev = sc.device
+    lists = torch.empty((R, params.list_width()), dtype=torch.int32, device=dev)
+    lengths = torch.empty((R,), dtype=torch.int32, device=dev)
+    picked = torch.empty((R, params.top_p), dtype=torch.int32, device=dev)
+    status = torch.empty((R,), dtype=torch.int32, device=dev)
+    _check(lib().qw_dlsa_select(sc.data_ptr(), sc.shape[1], mb.data_ptr(), mb.shape[0],
+                                params.bucket_cap, pos.data_ptr(), R, total_rows, params.window,
+                                params.sink, params.top_k, params.top_p,
+                                params.buckets_per_block, threads, lists.data_ptr(),
+                                lengths.data_ptr(), picked.data_ptr(), status.data_ptr(),
+                                _stream(dev)))
+    return lists, lengths, picked, status
+
+
+def dlsa_select(scores, members, positions, total_rows: int, params: DlsaSelectParams):
+    """D-LSA K1 with the automatic workgroup size (dlsa_kernels.rs:73)."""
+    return dlsa_select_with(scores, members, positions, total_rows, params, 0)
+

@@ -22,7 +22,8 @@ OUT = os.path.join(HERE, "libqwattn.so")
 BUILD_DIR = os.path.join(HERE, "_build")
 ARCH = "gfx950"
 
-SOURCES = ["kv_cache.hip", "attend_decode.hip", "attend_block.hip", "dlsa.hip", "abi.hip"]
+SOURCES = ["kv_cache.hip", "attend_decode.hip", "attend_block.hip", "dlsa.hip", "dlsa_select.hip",
+           "abi.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

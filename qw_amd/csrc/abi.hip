@@ -204,4 +204,14 @@ int qw_dlsa_sparse_attention_with(const void* q, const void* k, const void* v,
                                          (hipStream_t)stream));
 }
 
+int qw_dlsa_select(const float* scores, int64_t score_stride, const int32_t* members,
+                   int n_member_rows, int bucket_cap, const int32_t* positions, int n_rows,
+                   int total_rows, int window, int sink, int top_k, int top_p,
+                   int buckets_per_block, int threads, int32_t* lists, int32_t* lengths,
+                   int32_t* picked, int32_t* status, void* stream) {
+    QW_GUARDED(qw::dlsa_select(scores, score_stride, members, n_member_rows, bucket_cap, positions,
+                               n_rows, total_rows, window, sink, top_k, top_p, buckets_per_block,
+                               threads, lists, lengths, picked, status, (hipStream_t)stream));
+}
+
 }  // extern "C"

@@ -111,4 +111,12 @@ int launch_block_attention(KVCache& c, const f16* q, int G, int n_rows, float sc
 int launch_partial_merge(const float* part_o, const float2* part_ml, int nc, int rstride, int row0,
                          int R, int hkv, int D, int G, int Tq, f16* out, hipStream_t stream);
 
+
+// D-LSA K1 select (dlsa_select.hip).
+int dlsa_select(const float* scores, int64_t stride, const int32_t* members, int n_member_rows,
+                int bucket_cap, const int32_t* positions, int n_rows, int total_rows, int window,
+                int sink, int top_k, int top_p, int buckets_per_block, int threads,
+                int32_t* lists, int32_t* lengths, int32_t* picked, int32_t* status,
+                hipStream_t stream);
+
 }  // namespace qw
