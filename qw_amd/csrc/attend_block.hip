@@ -56,6 +56,11 @@ struct BlockArgs {
     uint32_t code_off2; // magic offset pair of the separately rounded dequant
 };
 
+// Register stages of K/V tile loads in flight (1 or 2).
+#ifndef QW_BLOCK_STAGES
+#define QW_BLOCK_STAGES 2
+#endif
+
 // 8 waves, two a SIMD: one wave a SIMD leaves the MFMA, LDS and VALU
 // latencies of a wave exposed (measured ~1.6x slower at equal work).
 constexpr int kBlockWaves = 8;
@@ -385,8 +390,34 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         }
     };
 
-    // ---- main loop: round t dequantizes tile t+1 into buffer (t+1)&1, issues
-    // the loads of tile t+2, computes tile t from buffer t&1; one barrier.
+    // ---- main loop: round t dequantizes tile t+1 into LDS buffer (t+1)&1
+    // from its register stage, reuses that stage for the loads of tile
+    // t + 1 + QW_BLOCK_STAGES, and computes tile t from buffer t&1; one
+    // barrier a round. Two register stages keep two tiles of loads in flight
+    // behind the tile being computed, which the key-split verify launches
+    // (one tile of math a round) need to cover HBM latency.
+#if QW_BLOCK_STAGES == 2
+    Stage s0, s1;
+    if (t0 < t1) {
+        load(s0, t0);
+        store(s0, 0);
+        if (t0 + 1 < t1) load(s0, t0 + 1);
+        if (t0 + 2 < t1) load(s1, t0 + 2);
+    }
+    __syncthreads();
+    auto round = [&](Stage& sa, int t, int b) {
+        if (t + 1 < t1) {
+            store(sa, b ^ 1);
+            if (t + 3 < t1) load(sa, t + 3);
+        }
+        if (wave_live && t * KT <= wave_lim) tile(b, t * KT);
+        __syncthreads();
+    };
+    for (int t = t0; t < t1; t += 2) {
+        round(s0, t, 0);
+        if (t + 1 < t1) round(s1, t + 1, 1);
+    }
+#else
     Stage st;
     if (t0 < t1) {
         load(st, t0);
@@ -403,6 +434,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         if (wave_live && t * KT <= wave_lim) tile(b, t * KT);
         __syncthreads();
     }
+#endif
 
     // ---- epilogue: per column, the row sum over the 4 lane groups.
 #pragma unroll
