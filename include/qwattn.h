@@ -224,6 +224,38 @@ int qw_dlsa_select(const float* scores, int64_t score_stride, const int32_t* mem
                    int buckets_per_block, int threads, int32_t* lists, int32_t* lengths,
                    int32_t* picked, int32_t* status, void* stream);
 
+/* Fused q/k RoPE + append layout: fused_rope_qk_append
+ * (crates/mlxcel-core/src/lib.rs:1462-1476, kernel
+ * crates/mlx-cpp/turbo/fused_rope_append.cpp:80-180, contract :378-420).
+ *   qkv   [batch][seq][(n_q_heads + 2 n_kv_heads) head_dim] fp16, per token
+ *         the q heads, then the k heads, then the v heads;
+ *   q_out [batch][n_q_heads][seq][head_dim] fp16, rotated;
+ *   k_out, v_out [batch][n_kv_heads][seq][head_dim] (dest_layout 0, dense
+ *         slab) or [batch][seq][n_kv_heads][head_dim] (dest_layout 1, paged
+ *         pool rows); k rotated, v copied.
+ * Token t rotates at position positions_base + t: pair p of the first
+ * rope_dims dims of a head ((2p, 2p+1) if traditional, else (p, p +
+ * rope_dims/2)) turns by (rope_scale * position) * exp2(-(p / (rope_dims/2))
+ * * log2(rope_base)); the other dims are copied. head_dim even, rope_dims
+ * even, positive and <= head_dim, else QW_ERR_INVALID_ARGUMENT. */
+int qw_fused_rope_qk_append(const void* qkv, int batch, int seq, int n_q_heads, int n_kv_heads,
+                            int head_dim, int rope_dims, float rope_base, float rope_scale,
+                            int traditional, int positions_base, int dest_layout, void* q_out,
+                            void* k_out, void* v_out, void* stream);
+
+/* The same RoPE with the cache append fused in: what
+ * Attention::forward_fused_rope_append (crates/mlxcel-core/src/layers.rs:
+ * 2852-2905) followed by KVCache::update (cache.rs:922) does, without the
+ * k / v round trip through memory. qkv [n_tokens][(n_q_heads + 2 hkv)
+ * head_dim] fp16 (one sequence; hkv and head_dim are the cache's); the
+ * rotated q goes to q_out [n_q_heads][n_tokens][head_dim]; the rotated k
+ * (rounded to fp16) and v are appended as qw_kv_update appends them, token t
+ * at position position0 + t. Same argument contract as
+ * qw_fused_rope_qk_append. */
+int qw_kv_rope_update(qw_kv_cache* cache, const void* qkv, int n_q_heads, int n_tokens,
+                      int rope_dims, int traditional, float rope_base, float rope_scale,
+                      int position0, void* q_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

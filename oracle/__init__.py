@@ -386,3 +386,60 @@ def dlsa_select(scores: np.ndarray, members: np.ndarray, positions: np.ndarray,
         lists[r, :len(out)] = out
         lengths[r] = len(out)
     return lists, lengths, picked, status
+
+
+# ------------------------------------------------- fused q/k RoPE + append
+
+def rope_theta(rope_dims: int, positions, base: float, scale: float = 1.0) -> np.ndarray:
+    """Angles [len(positions), rope_dims/2] as the reference forms them, all in
+    fp32 (crates/mlx-cpp/turbo/fused_rope_append.cpp:163-168, host log2 at
+    :435-441): inv_freq = exp2(-(p / (R/2)) * log2(base)),
+    theta = (scale * position) * inv_freq."""
+    rhalf = rope_dims // 2
+    log2b = np.float32(np.log2(np.float32(base)))
+    d = np.arange(rhalf, dtype=np.float32) / np.float32(rhalf)
+    inv = np.exp2(-d * log2b).astype(np.float32)
+    pos = np.asarray(positions, dtype=np.float32)
+    return ((np.float32(scale) * pos)[:, None] * inv[None, :]).astype(np.float32)
+
+
+def rope_pairs(rope_dims: int, traditional: bool):
+    """Dim indices (first, second) of each rotated pair p
+    (fused_rope_append.cpp:142-151): (2p, 2p+1) traditional, else (p, p + R/2)."""
+    rhalf = rope_dims // 2
+    p = np.arange(rhalf)
+    return (2 * p, 2 * p + 1) if traditional else (p, p + rhalf)
+
+
+def rope(x: np.ndarray, rope_dims: int, traditional: bool, base: float, scale: float,
+         positions) -> np.ndarray:
+    """RoPE of x [..., T, D] (fp16 or wider) at the given per-row positions,
+    returned unrounded in float64 from the fp32 angles of ``rope_theta``:
+    r1 = x1 cos - x2 sin, r2 = x1 sin + x2 cos on each pair; dims past R are
+    copied (fused_rope_append.cpp:152-178)."""
+    x = np.asarray(x, np.float64)
+    out = x.copy()
+    th = rope_theta(rope_dims, positions, base, scale).astype(np.float64)
+    c, s = np.cos(th), np.sin(th)
+    i1, i2 = rope_pairs(rope_dims, traditional)
+    x1, x2 = x[..., i1], x[..., i2]
+    out[..., i1] = x1 * c - x2 * s
+    out[..., i2] = x1 * s + x2 * c
+    return out
+
+
+def fused_rope_qk_append(qkv: np.ndarray, hq: int, hkv: int, D: int, rope_dims: int,
+                         base: float, scale: float, traditional: bool, positions_base: int,
+                         dest_layout: int = 0):
+    """The reference op end to end (lib.rs:1462-1476): qkv [B, L, (Hq+2Hkv) D]
+    -> q [B, Hq, L, D], k / v [B, Hkv, L, D] (layout 0) or [B, L, Hkv, D]
+    (layout 1), q and k rotated (float64, unrounded), v copied."""
+    B, L, _ = qkv.shape
+    x = np.asarray(qkv).reshape(B, L, hq + 2 * hkv, D).transpose(0, 2, 1, 3)
+    pos = positions_base + np.arange(L)
+    q = rope(x[:, :hq], rope_dims, traditional, base, scale, pos)
+    k = rope(x[:, hq:hq + hkv], rope_dims, traditional, base, scale, pos)
+    v = np.asarray(x[:, hq + hkv:], np.float64)
+    if dest_layout == 1:
+        k, v = k.transpose(0, 2, 1, 3), v.transpose(0, 2, 1, 3)
+    return q, k, v

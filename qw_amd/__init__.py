@@ -23,6 +23,7 @@ import ctypes
 import os
 
 __all__ = ["KVCacheMode", "KVCache", "QwError", "sparse_attention", "sparse_attention_with",
+           "fused_rope_qk_append", "dlsa_select", "dlsa_select_with",
            "lib", "LIB_PATH"]
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libqwattn.so")
@@ -66,6 +67,9 @@ _SIGNATURES = {
     "qw_kv_import": (_i, [_p, _i, _p, _p, _p, _p, _p, _p, _p]),
     "qw_dlsa_select": (_i, [_p, _i64, _p, _i, _i, _p, _i, _i, _i, _i, _i, _i, _i, _i, _p, _p, _p,
                             _p, _p]),
+    "qw_fused_rope_qk_append": (_i, [_p, _i, _i, _i, _i, _i, _i, _f, _f, _i, _i, _i, _p, _p, _p,
+                                     _p]),
+    "qw_kv_rope_update": (_i, [_p, _p, _i, _i, _i, _i, _f, _f, _i, _p, _p]),
     "qw_dlsa_sparse_attention": (_i, [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _i, _i, _i,
                                       _i, _i, _i, _f, _p, _p]),
     "qw_dlsa_sparse_attention_with": (_i, [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _i, _i,
@@ -199,6 +203,29 @@ class KVCache:
             raise QwError(1, "update: keys/values must be [n_kv_heads, L, head_dim]")
         _check(lib().qw_kv_update(self._h, k.data_ptr(), v.data_ptr(), k.shape[1],
                                   _stream(self.device)))
+
+    def rope_update(self, qkv, n_q_heads: int, rope_dims: int, rope_base: float,
+                    rope_scale: float = 1.0, traditional: bool = False,
+                    position0: int | None = None):
+        """q/k RoPE out of the fused QKV projection with the append fused in
+        (reference ``Attention::forward_fused_rope_append``, layers.rs:2852,
+        then ``KVCache::update``): ``qkv`` is [1, L, (Hq + 2 Hkv) D] or
+        [L, (Hq + 2 Hkv) D] fp16; token t rotates at position0 + t (default:
+        the cache offset). Returns the rotated q as [1, Hq, L, D]."""
+        torch = _torch()
+        x = qkv[0] if qkv.dim() == 3 else qkv
+        if x.dim() != 2 or x.dtype != torch.float16 or not x.is_cuda:
+            raise QwError(1, "rope_update: qkv must be a [1, L, W] or [L, W] fp16 device tensor")
+        x = x.contiguous()
+        L, W = x.shape
+        if W != (n_q_heads + 2 * self.n_kv_heads) * self.head_dim:
+            raise QwError(1, "rope_update: qkv width does not match the head geometry")
+        pos = self.offset if position0 is None else position0
+        q = torch.empty((n_q_heads, L, self.head_dim), dtype=torch.float16, device=self.device)
+        _check(lib().qw_kv_rope_update(self._h, x.data_ptr(), n_q_heads, L, rope_dims,
+                                       int(traditional), float(rope_base), float(rope_scale),
+                                       pos, q.data_ptr(), _stream(self.device)))
+        return q.unsqueeze(0)
 
     def dequantize(self, start: int = 0, n: int | None = None):
         torch = _torch()
@@ -413,3 +440,30 @@ def dlsa_select(scores, members, positions, total_rows: int, params: DlsaSelectP
     """D-LSA K1 with the automatic workgroup size (dlsa_kernels.rs:73)."""
     return dlsa_select_with(scores, members, positions, total_rows, params, 0)
 
+
+
+def fused_rope_qk_append(qkv, n_q_heads: int, n_kv_heads: int, head_dim: int, rope_dims: int,
+                         rope_base: float, rope_scale: float = 1.0, traditional: bool = False,
+                         positions_base: int = 0, dest_layout: int = 0):
+    """q/k RoPE + append-layout relayout out of the fused QKV projection
+    (reference ``fused_rope_qk_append``, lib.rs:1462; kernel
+    fused_rope_append.cpp:80-180). ``qkv`` [B, L, (Hq + 2 Hkv) D] fp16 on the
+    device. Returns (q [B, Hq, L, D], k, v) with k / v [B, Hkv, L, D]
+    (dest_layout 0) or [B, L, Hkv, D] (dest_layout 1); q and k rotated."""
+    torch = _torch()
+    if qkv.dim() != 3 or qkv.dtype != torch.float16 or not qkv.is_cuda:
+        raise QwError(1, "fused_rope_qk_append: qkv must be [B, L, W] fp16 on the device")
+    x = qkv.contiguous()
+    B, L, W = x.shape
+    if W != (n_q_heads + 2 * n_kv_heads) * head_dim:
+        raise QwError(1, "fused_rope_qk_append: qkv trailing dim does not match the head geometry")
+    q = torch.empty((B, n_q_heads, L, head_dim), dtype=torch.float16, device=x.device)
+    kv_shape = (B, n_kv_heads, L, head_dim) if dest_layout == 0 else (B, L, n_kv_heads, head_dim)
+    k = torch.empty(kv_shape, dtype=torch.float16, device=x.device)
+    v = torch.empty_like(k)
+    _check(lib().qw_fused_rope_qk_append(x.data_ptr(), B, L, n_q_heads, n_kv_heads, head_dim,
+                                         rope_dims, float(rope_base), float(rope_scale),
+                                         int(traditional), positions_base, dest_layout,
+                                         q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                         _stream(x.device)))
+    return q, k, v

@@ -214,4 +214,23 @@ int qw_dlsa_select(const float* scores, int64_t score_stride, const int32_t* mem
                                threads, lists, lengths, picked, status, (hipStream_t)stream));
 }
 
+int qw_fused_rope_qk_append(const void* qkv, int batch, int seq, int n_q_heads, int n_kv_heads,
+                            int head_dim, int rope_dims, float rope_base, float rope_scale,
+                            int traditional, int positions_base, int dest_layout, void* q_out,
+                            void* k_out, void* v_out, void* stream) {
+    QW_GUARDED(qw::fused_rope_qk_append(qkv, batch, seq, n_q_heads, n_kv_heads, head_dim,
+                                        rope_dims, rope_base, rope_scale, traditional,
+                                        positions_base, dest_layout, q_out, k_out, v_out,
+                                        (hipStream_t)stream));
+}
+
+int qw_kv_rope_update(qw_kv_cache* cache, const void* qkv, int n_q_heads, int n_tokens,
+                      int rope_dims, int traditional, float rope_base, float rope_scale,
+                      int position0, void* q_out, void* stream) {
+    QW_HANDLE(cache);
+    QW_GUARDED(cache->impl.rope_update(qkv, n_q_heads, n_tokens, rope_dims, traditional,
+                                       rope_base, rope_scale, position0, q_out,
+                                       (hipStream_t)stream));
+}
+
 }  // extern "C"

@@ -15,6 +15,7 @@
 
 #include "kv_cache.hpp"
 #include "quant.hpp"
+#include "rope.hpp"
 
 namespace qw {
 
@@ -276,16 +277,27 @@ __device__ inline void quantize_row_int8(const float* x, uint8_t* lds_codes, hal
     }
 }
 
+// The row is read from `src`; with `rope` (K of a fused RoPE-append) each
+// element is rotated first and rounded to fp16, the value the fp16 rotation
+// hands to the cache's quantize-on-append.
 template <int D>
 __device__ inline void quantize_row(const f16* __restrict__ src, int bits, bool int8,
                                     uint8_t* lds_codes,
-                                    half2v* sb_out /* [D/64] (scale, bias) */, int* fast_flag) {
+                                    half2v* sb_out /* [D/64] (scale, bias) */, int* fast_flag,
+                                    const RowSrc* rope = nullptr, int pos = 0) {
     constexpr int VPL = D / 64;         // values per lane
     constexpr int LPG = kGroup / VPL;   // lanes per group
     const int lane = threadIdx.x & 63;
     float x[VPL];
+    if (rope && rope->rope_dims > 0) {
 #pragma unroll
-    for (int i = 0; i < VPL; i++) x[i] = (float)src[lane * VPL + i];
+        for (int i = 0; i < VPL; i++) x[i] = (float)(f16)rope_elem(src, lane * VPL + i, rope->rope_dims,
+                                                  rope->traditional, rope->log2_base,
+                                                  rope->scale, pos);
+    } else {
+#pragma unroll
+        for (int i = 0; i < VPL; i++) x[i] = (float)src[lane * VPL + i];
+    }
     if (int8) {
         quantize_row_int8<D>(x, lds_codes, sb_out);
         return;
@@ -317,7 +329,7 @@ __device__ inline void quantize_row(const f16* __restrict__ src, int bits, bool 
 
 template <int D>
 __global__ __launch_bounds__(256) void append_affine_kernel(
-    const f16* __restrict__ k_new, const f16* __restrict__ v_new, int n_tokens, int t_old,
+    RowSrc rs, int n_tokens, int t_old,
     int bits, int int8, int cap, uint32_t* __restrict__ k_codes, uint32_t* __restrict__ k_params,
     uint32_t* __restrict__ v_codes, f16* __restrict__ v_params, int* __restrict__ fast_flag) {
     constexpr int NG = D / kGroup;
@@ -348,9 +360,10 @@ __global__ __launch_bounds__(256) void append_affine_kernel(
     for (int k = wave; k < 8; k += 4) {
         const int t = blk * 8 + k;
         if (t < t_old || t >= t_end) continue;
-        const int64_t src = ((int64_t)h * n_tokens + (t - t_old)) * D;
-        quantize_row<D>(k_new + src, bits, int8 != 0, kc[k], ksb[k], fast_flag);
-        quantize_row<D>(v_new + src, bits, int8 != 0, vc[k], vsb[k], fast_flag);
+        const int64_t src = (int64_t)(t - t_old) * rs.row_stride + (int64_t)h * rs.head_stride;
+        quantize_row<D>(rs.k + src, bits, int8 != 0, kc[k], ksb[k], fast_flag, &rs,
+                        rs.position0 + (t - t_old));
+        quantize_row<D>(rs.v + src, bits, int8 != 0, vc[k], vsb[k], fast_flag);
     }
     __syncthreads();
     // K: row-major MLX packing, words of 32/bits codes LSB-first.
@@ -406,18 +419,20 @@ __global__ __launch_bounds__(256) void append_affine_kernel(
 
 // fp16 mode append: K rows copied, V scattered into 8-key blocks.
 template <int D>
-__global__ __launch_bounds__(256) void append_fp16_kernel(const f16* __restrict__ k_new,
-                                                          const f16* __restrict__ v_new,
-                                                          int n_tokens, int t_old, int cap,
-                                                          f16* __restrict__ k_data,
+__global__ __launch_bounds__(256) void append_fp16_kernel(RowSrc rs, int n_tokens, int t_old,
+                                                          int cap, f16* __restrict__ k_data,
                                                           f16* __restrict__ v_data) {
     const int h = blockIdx.y;
     const int64_t n = (int64_t)n_tokens * D;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x) {
-        const int t = (int)(i / D) + t_old, d = (int)(i % D);
-        const f16 kv = k_new[(int64_t)h * n + i];
-        const f16 vv = v_new[(int64_t)h * n + i];
+        const int r = (int)(i / D), d = (int)(i % D);
+        const int t = r + t_old;
+        const int64_t src = (int64_t)r * rs.row_stride + (int64_t)h * rs.head_stride;
+        const f16 kv = rs.rope_dims > 0 ? (f16)rope_elem(rs.k + src, d, rs.rope_dims, rs.traditional,
+                                                       rs.log2_base, rs.scale, rs.position0 + r)
+                                        : rs.k[src + d];
+        const f16 vv = rs.v[src + d];
         k_data[((int64_t)h * cap + t) * D + d] = kv;
         v_data[(((int64_t)h * (cap / 8) + t / 8) * D + v_phys_dim(d, D, 16)) * 8 + (t & 7)] = vv;
     }
@@ -427,6 +442,16 @@ int KVCache::update(const void* k_new, const void* v_new, int n_tokens, hipStrea
     QW_REQUIRE(n_tokens >= 0, QW_ERR_INVALID_ARGUMENT, "update: n_tokens must be >= 0");
     if (n_tokens == 0) return QW_OK;
     QW_REQUIRE(k_new && v_new, QW_ERR_INVALID_ARGUMENT, "update: null K/V pointer");
+    RowSrc rs{};
+    rs.k = (const f16*)k_new;
+    rs.v = (const f16*)v_new;
+    rs.row_stride = D;
+    rs.head_stride = (int64_t)n_tokens * D;
+    return update_rows(rs, n_tokens, stream);
+}
+
+int KVCache::update_rows(const RowSrc& rs, int n_tokens, hipStream_t stream) {
+    if (n_tokens == 0) return QW_OK;
     DeviceGuard dg(device);
     QW_REQUIRE(dg.ok, QW_ERR_HIP, "update: hipSetDevice failed");
     const int need = offset + n_tokens;
@@ -440,12 +465,12 @@ int KVCache::update(const void* k_new, const void* v_new, int n_tokens, hipStrea
         dim3 grid(nblk, hkv);
         if (D == 256)
             hipLaunchKernelGGL(append_affine_kernel<256>, grid, dim3(256), 0, stream,
-                               (const f16*)k_new, (const f16*)v_new, n_tokens, offset, bits,
+                               rs, n_tokens, offset, bits,
                                int8() ? 1 : 0, cap, (uint32_t*)k_data, k_params,
                                (uint32_t*)v_data, (f16*)v_params, fast_flag);
         else
             hipLaunchKernelGGL(append_affine_kernel<128>, grid, dim3(256), 0, stream,
-                               (const f16*)k_new, (const f16*)v_new, n_tokens, offset, bits,
+                               rs, n_tokens, offset, bits,
                                int8() ? 1 : 0, cap, (uint32_t*)k_data, k_params,
                                (uint32_t*)v_data, (f16*)v_params, fast_flag);
     } else {
@@ -453,11 +478,11 @@ int KVCache::update(const void* k_new, const void* v_new, int n_tokens, hipStrea
         dim3 grid((unsigned)std::min<int64_t>((n + 255) / 256, 1024), hkv);
         if (D == 256)
             hipLaunchKernelGGL(append_fp16_kernel<256>, grid, dim3(256), 0, stream,
-                               (const f16*)k_new, (const f16*)v_new, n_tokens, offset, cap,
+                               rs, n_tokens, offset, cap,
                                (f16*)k_data, (f16*)v_data);
         else
             hipLaunchKernelGGL(append_fp16_kernel<128>, grid, dim3(256), 0, stream,
-                               (const f16*)k_new, (const f16*)v_new, n_tokens, offset, cap,
+                               rs, n_tokens, offset, cap,
                                (f16*)k_data, (f16*)v_data);
     }
     QW_HIP_CHECK(hipGetLastError());

@@ -11,6 +11,21 @@
 
 namespace qw {
 
+// Where an append reads its new rows: row (h, i) of K at k + i * row_stride +
+// h * head_stride (V alike), and the RoPE applied to K as it is read
+// (rope_dims == 0: none). A plain update reads [hkv][n][D]; the fused
+// RoPE-append reads K and V straight out of the fused QKV projection.
+struct RowSrc {
+    const f16* k;
+    const f16* v;
+    int64_t row_stride, head_stride;
+    int rope_dims;      // rotated prefix of each head (even), 0: no rotation
+    int traditional;    // 1: pairs (2p, 2p+1); 0: pairs (p, p + rope_dims/2)
+    int position0;      // position of row 0
+    float log2_base;    // log2(rope base), formed on the host as MLX does
+    float scale;        // rope scale
+};
+
 struct KVCache {
     int mode = QW_KV_FP16;  // QW_KV_*
     int bits = 16;          // 4, 8 (affine) or 16 (fp16)
@@ -65,6 +80,13 @@ struct KVCache {
 
     // cache.rs:922 `update`
     int update(const void* k_new, const void* v_new, int n_tokens, hipStream_t stream);
+    // Append from a row source (strided rows, optional RoPE on K).
+    int update_rows(const RowSrc& src, int n_tokens, hipStream_t stream);
+    // fused_rope_append.cpp:80-180 + update: q/k RoPE out of the fused QKV
+    // projection, rotated q to q_out, rotated k and v appended.
+    int rope_update(const void* qkv, int n_q_heads, int n_tokens, int rope_dims, int traditional,
+                    float rope_base, float rope_scale, int position0, void* q_out,
+                    hipStream_t stream);
     // cache.rs:2709 `update_and_fetch`
     int update_and_fetch(const void* k_new, const void* v_new, int n_tokens, void* k_out,
                          void* v_out, hipStream_t stream);
@@ -118,5 +140,11 @@ int dlsa_select(const float* scores, int64_t stride, const int32_t* members, int
                 int sink, int top_k, int top_p, int buckets_per_block, int threads,
                 int32_t* lists, int32_t* lengths, int32_t* picked, int32_t* status,
                 hipStream_t stream);
+
+// Fused q/k RoPE + append-layout relayout (rope.hip).
+int fused_rope_qk_append(const void* qkv, int batch, int seq, int hq, int hkv, int head_dim,
+                         int rope_dims, float rope_base, float rope_scale, int traditional,
+                         int positions_base, int dest_layout, void* q_out, void* k_out,
+                         void* v_out, hipStream_t stream);
 
 }  // namespace qw

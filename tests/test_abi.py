@@ -74,3 +74,32 @@ def test_invalid_arguments_fail_before_device_work(qwlib):
     args_bad_w = list(args)
     args_bad_w[10] = 0
     assert f(*args_bad_w) == 1
+
+
+def test_fused_rope_contract_fails_before_device_work(qwlib):
+    """fused_rope_append.cpp:394-418: the argument contract, checked before
+    any launch (status 1, QW_ERR_INVALID_ARGUMENT)."""
+    f = qwlib.qw_fused_rope_qk_append
+    one = ctypes.c_void_p(16)
+
+    def call(**kw):
+        a = dict(batch=1, seq=4, hq=8, hkv=2, D=128, R=64, base=10000.0, scale=1.0, trad=0,
+                 pos=0, layout=0)
+        a.update(kw)
+        return f(one, a["batch"], a["seq"], a["hq"], a["hkv"], a["D"], a["R"], a["base"],
+                 a["scale"], a["trad"], a["pos"], a["layout"], one, one, one, None)
+
+    assert call(R=0) == 1
+    assert b"rope_dims" in qwlib.qw_last_error()
+    assert call(R=63) == 1
+    assert call(R=130) == 1
+    assert call(D=127, R=64) == 1
+    assert b"head_dim must be even" in qwlib.qw_last_error()
+    assert call(hq=0) == 1
+    assert call(hkv=-1) == 1
+    assert call(layout=2) == 1
+    assert b"dest_layout" in qwlib.qw_last_error()
+    assert call(seq=-1) == 1
+    assert call(seq=0) == 0  # nothing to do: no launch
+    assert f(None, 1, 4, 8, 2, 128, 64, 10000.0, 1.0, 0, 0, 0, None, None, None, None) == 1
+    assert qwlib.qw_kv_rope_update(None, one, 8, 4, 64, 0, 10000.0, 1.0, 0, one, None) == 1
