@@ -59,6 +59,16 @@ extern "C" {
  * clip(round(f16(x / scale)), -128, 127) and the fetched value is
  * f16(code * scale). */
 #define QW_KV_INT8 3
+/* The reference's Turbo4 mode (symmetric PolarQuant, the served default,
+ * cache.rs:1438-1597 update_turbo4_sym, turbo/quant.rs:119-769): per
+ * (token, KV head) the row is normalised by its L2 norm, rotated by
+ * signs2 . H . signs1 (H the orthonormal Walsh-Hadamard transform, signs from
+ * a 32-bit LCG on the cache's seed, K and V with independent pairs), and
+ * each coordinate stored as the 4-bit index of its nearest Lloyd-Max
+ * centroid for N(0, 1/head_dim), two per byte (low nibble = even coord),
+ * with fp16 sidecars k_rescale, v_norms and v_rescale (norm / |centroids|).
+ * head_dim 128 or 256. */
+#define QW_KV_TURBO4 4
 
 typedef struct qw_kv_cache qw_kv_cache;
 
@@ -78,6 +88,12 @@ const char* qw_last_error(void);
  * HIP device ordinal. */
 int qw_kv_create(int mode, int group_size, int n_kv_heads, int head_dim, int capacity,
                  int device, qw_kv_cache** out);
+
+/* KVCache::new_with_mode_and_seed (cache.rs:537): as qw_kv_create with the
+ * seed of the Turbo4 sign vectors (qw_kv_create uses the reference's
+ * TURBO_DEFAULT_SEED 0x7B470404, cache.rs:324). Other modes ignore it. */
+int qw_kv_create_seeded(int mode, int group_size, int n_kv_heads, int head_dim, int capacity,
+                        int device, uint32_t turbo_seed, qw_kv_cache** out);
 
 /* Frees the device buffers (KVCache drop). Waits for the device first. */
 int qw_kv_destroy(qw_kv_cache* cache);
@@ -147,6 +163,7 @@ int qw_kv_trim(qw_kv_cache* cache, int n, int* trimmed);
  * fp16 rows are staged in a temporary device buffer of 2*hkv*offset*D*2 bytes.
  * The policy deciding when to call it (qwen3_5.rs:929-986) is host code. */
 int qw_kv_demote(qw_kv_cache* cache, int target_mode, void* stream, int* demoted);
+/* (target_mode may also be QW_KV_TURBO4: the reference's own demote.) */
 
 /* Snapshot export in the reference's tensor layout (the packed-tensor
  * snapshot of cache.rs:570-626): for the affine modes
@@ -166,6 +183,26 @@ int qw_kv_export(const qw_kv_cache* cache, void* k_codes, void* k_scales, void* 
 int qw_kv_import(qw_kv_cache* cache, int n_tokens, const void* k_codes, const void* k_scales,
                  const void* k_biases, const void* v_codes, const void* v_scales,
                  const void* v_biases, void* stream);
+
+/* Turbo4 snapshot tensors (KVCache::turbo4_snapshot_tensors, cache.rs:570):
+ *   k_packed, v_packed [n_kv_heads][offset][head_dim/2] uint8 (two indices a
+ *   byte, low nibble = even coord), k_rescale, v_norms, v_rescale
+ *   [n_kv_heads][offset] fp16. QW_ERR_STATE unless the cache is Turbo4. */
+int qw_kv_export_turbo4(const qw_kv_cache* cache, void* k_packed, void* k_rescale,
+                        void* v_packed, void* v_norms, void* v_rescale, void* stream);
+
+/* restore_turbo4_snapshot (cache.rs:581-626): the cache holds exactly the
+ * given n_tokens > 0 rows in the export layout; no requantization. */
+int qw_kv_import_turbo4(qw_kv_cache* cache, int n_tokens, const void* k_packed,
+                        const void* k_rescale, const void* v_packed, const void* v_norms,
+                        const void* v_rescale, void* stream);
+
+/* Host-only (no device work) tables of the Turbo4 codec, for inspection and
+ * tests. optimal_centroids (turbo/codebook.rs:139): the 2^bits sorted
+ * Lloyd-Max centroids for N(0, 1/head_dim) into centroids (bits 1..8);
+ * generate_signs (turbo/quant.rs:217): len +-1 floats from the LCG on seed. */
+int qw_turbo4_codebook(int bits, int head_dim, float* centroids);
+int qw_turbo4_signs(int len, uint32_t seed, float* signs);
 
 /* ---------------------------------------------------------------- D-LSA */
 

@@ -443,3 +443,152 @@ def fused_rope_qk_append(qkv: np.ndarray, hq: int, hkv: int, D: int, rope_dims: 
     if dest_layout == 1:
         k, v = k.transpose(0, 2, 1, 3), v.transpose(0, 2, 1, 3)
     return q, k, v
+
+
+# ------------------------------------------------------------------ Turbo4
+
+TURBO_DEFAULT_SEED = 0x7B470404   # crates/mlxcel-core/src/cache.rs:324
+TURBO_SUB_SEED = 0x9E3779B9       # turbo/quant.rs:196 (second vector of a pair)
+TURBO_K_SEED_OFFSET = 0x4B5F5345  # turbo/quant.rs:101
+
+
+def turbo4_centroids(bits: int, head_dim: int) -> np.ndarray:
+    """Lloyd-Max centroids for N(0, 1/head_dim), float32 (turbo/codebook.rs:
+    208-361, the published turboquant_plus `optimal_centroids`): b = 1, 2 in
+    closed form; b >= 3 from uniform-quantile boundaries (scipy's norm.ppf),
+    100 rounds of midpoint boundaries and conditional-expectation centroids,
+    in float64."""
+    from scipy import stats
+
+    d = float(head_dim)
+    if bits == 1:
+        c = np.sqrt(2.0 / (np.pi * d))
+        return np.array([-c, c]).astype(np.float32)
+    if bits == 2:
+        return (np.array([-1.51, -0.453, 0.453, 1.51]) / np.sqrt(d)).astype(np.float32)
+    n = 1 << bits
+    sigma = 1.0 / np.sqrt(d)
+    bnd = stats.norm.ppf(np.linspace(0.0, 1.0, n + 1)[1:-1], scale=sigma)
+
+    def cond(bnd):
+        lo = np.concatenate([[-np.inf], bnd]) / sigma
+        hi = np.concatenate([bnd, [np.inf]]) / sigma
+        prob = stats.norm.cdf(hi) - stats.norm.cdf(lo)
+        prob[-1] = stats.norm.sf(lo[-1])
+        return sigma * (stats.norm.pdf(lo) - stats.norm.pdf(hi)) / prob
+
+    c = cond(bnd)
+    for _ in range(100):
+        c = cond((c[:-1] + c[1:]) * 0.5)
+    return c.astype(np.float32)
+
+
+def turbo4_boundaries(c: np.ndarray) -> np.ndarray:
+    """Midpoints in float32 (codebook.rs:84-90)."""
+    c = c.astype(np.float32)
+    return ((c[:-1] + c[1:]) * np.float32(0.5)).astype(np.float32)
+
+
+def lcg_signs(n: int, seed: int) -> np.ndarray:
+    """+-1 from the 32-bit LCG x <- 1664525 x + 1013904223 (mod 2^32), a
+    zero seed starting from 0xDEADBEEF; + when bit 31 of the new state is set
+    (turbo/quant.rs:119-139, :217-236)."""
+    s = seed & 0xFFFFFFFF or 0xDEADBEEF
+    out = np.empty(n, np.float32)
+    for i in range(n):
+        s = (1664525 * s + 1013904223) & 0xFFFFFFFF
+        out[i] = 1.0 if s >> 31 else -1.0
+    return out
+
+
+def turbo4_tables(head_dim: int, seed: int = TURBO_DEFAULT_SEED) -> dict:
+    """The per-cache codec state (TurboQuantParams::new, turbo/quant.rs:188-214)."""
+    ks = (seed + TURBO_K_SEED_OFFSET) & 0xFFFFFFFF
+    cb = turbo4_centroids(4, head_dim)
+    return {
+        "v_s1": lcg_signs(head_dim, seed),
+        "v_s2": lcg_signs(head_dim, (seed + TURBO_SUB_SEED) & 0xFFFFFFFF),
+        "k_s1": lcg_signs(head_dim, ks),
+        "k_s2": lcg_signs(head_dim, (ks + TURBO_SUB_SEED) & 0xFFFFFFFF),
+        "cb": cb,
+        "bnd": turbo4_boundaries(cb),
+    }
+
+
+def hadamard_orthonormal(n: int) -> np.ndarray:
+    """Sylvester Walsh-Hadamard matrix / sqrt(n) (MLX hadamard_transform with
+    its default scale, the reference's `wht`, ops.rs:72-111)."""
+    from scipy.linalg import hadamard
+
+    return hadamard(n).astype(np.float64) / np.sqrt(n)
+
+
+def turbo4_rotate(x: np.ndarray, s1: np.ndarray, s2: np.ndarray) -> np.ndarray:
+    """s2 . H . s1 along the last axis, float64."""
+    H = hadamard_orthonormal(x.shape[-1])
+    return ((np.asarray(x, np.float64) * s1) @ H) * s2
+
+
+def turbo4_quantize(x: np.ndarray, s1: np.ndarray, s2: np.ndarray, tab: dict):
+    """quantize_into_packed (turbo/quant.rs:270-440 with the pack kernel,
+    mlx_cxx_kernels.cpp:186-212) in float64 on fp16 rows x [..., D]: returns
+    (indices uint8 [..., D], norms f16 [...], rescale f16 [...], rotated
+    float64 [..., D])."""
+    x = np.asarray(x, np.float64)
+    norm = np.sqrt((x * x).sum(-1))
+    safe = np.where(norm > 0, norm, 1.0)
+    y = turbo4_rotate(x / safe[..., None], s1, s2)
+    idx = (y[..., None] > tab["bnd"].astype(np.float64)).sum(-1).astype(np.uint8)
+    c = tab["cb"].astype(np.float64)[idx]
+    rn = np.maximum(np.sqrt((c * c).sum(-1)), 1e-10)
+    return idx, norm.astype(np.float16), (norm / rn).astype(np.float16), y
+
+
+def turbo4_pack(idx: np.ndarray) -> np.ndarray:
+    """Two indices a byte, low nibble = even coordinate (turbo/quant.rs:30-33)."""
+    idx = np.asarray(idx, np.uint8)
+    return (idx[..., 0::2] | (idx[..., 1::2] << 4)).astype(np.uint8)
+
+
+def turbo4_unpack(packed: np.ndarray) -> np.ndarray:
+    p = np.asarray(packed, np.uint8)
+    out = np.empty(p.shape[:-1] + (2 * p.shape[-1],), np.uint8)
+    out[..., 0::2] = p & 15
+    out[..., 1::2] = p >> 4
+    return out
+
+
+def turbo4_expand_rotated(packed: np.ndarray, rescale: np.ndarray, tab: dict) -> np.ndarray:
+    """f16(f32(centroid) * f32(rescale)) in the rotated basis (quant.rs:586-600,
+    turbo4_delegated_sdpa.cpp:193-221): an fp32 product, then the fp16 cast."""
+    c = tab["cb"].astype(np.float32)[turbo4_unpack(packed)]
+    r = np.asarray(rescale, np.float16).astype(np.float32).reshape(c.shape[:-1] + (1,))
+    return (c * r).astype(np.float32).astype(np.float16)
+
+
+def turbo4_fetch_k(packed, k_rescale, tab) -> np.ndarray:
+    """dequantize_k_turbo4 (quant.rs:676-691): expansion, then s1 . H . s2, fp16."""
+    rot = turbo4_expand_rotated(packed, k_rescale, tab).astype(np.float64)
+    return turbo4_rotate(rot, tab["k_s2"], tab["k_s1"]).astype(np.float16)
+
+
+def turbo4_fetch_v(packed, v_norms, tab) -> np.ndarray:
+    """dequantize_v_turbo4 (quant.rs:486-546): unit-normalised centroids, the
+    inverse rotation, times the stored norm, fp16."""
+    c = tab["cb"].astype(np.float64)[turbo4_unpack(packed)]
+    u = c / np.maximum(np.sqrt((c * c).sum(-1, keepdims=True)), 1e-10)
+    n = np.asarray(v_norms, np.float16).astype(np.float64).reshape(c.shape[:-1] + (1,))
+    return (turbo4_rotate(u, tab["v_s2"], tab["v_s1"]) * n).astype(np.float16)
+
+
+def turbo4_attention(q, k_packed, k_rescale, v_packed, v_rescale, tab, scale: float,
+                     q_pos=None, threads: int | None = None) -> np.ndarray:
+    """attention_turbo4_dequant_sdpa (turbo/sparse_v.rs:1051-1072): q rotated
+    into the K basis and cast to fp16, rotated K/V expansions, MLX fp16 SDPA,
+    the output rotated back through the V basis and cast to fp16. q [Hq, L, D];
+    the packed tensors [Hkv, T, D/2], rescales [Hkv, T]."""
+    q_rot = turbo4_rotate(np.asarray(q, np.float16), tab["k_s1"], tab["k_s2"]).astype(np.float16)
+    k_rot = turbo4_expand_rotated(k_packed, k_rescale, tab)
+    v_rot = turbo4_expand_rotated(v_packed, v_rescale, tab)
+    o_rot = sdpa_mlx_f16(q_rot, k_rot, v_rot, scale, q_pos, threads)
+    return turbo4_rotate(o_rot.astype(np.float64), tab["v_s2"], tab["v_s1"]).astype(np.float16)

@@ -23,7 +23,8 @@ import ctypes
 import os
 
 __all__ = ["KVCacheMode", "KVCache", "QwError", "sparse_attention", "sparse_attention_with",
-           "fused_rope_qk_append", "dlsa_select", "dlsa_select_with",
+           "fused_rope_qk_append", "dlsa_select", "dlsa_select_with", "turbo4_codebook",
+           "turbo4_signs",
            "lib", "LIB_PATH"]
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libqwattn.so")
@@ -51,6 +52,11 @@ _SIGNATURES = {
     "qw_abi_version": (_i, []),
     "qw_last_error": (ctypes.c_char_p, []),
     "qw_kv_create": (_i, [_i, _i, _i, _i, _i, _i, ctypes.POINTER(_p)]),
+    "qw_kv_create_seeded": (_i, [_i, _i, _i, _i, _i, _i, ctypes.c_uint32, ctypes.POINTER(_p)]),
+    "qw_kv_export_turbo4": (_i, [_p, _p, _p, _p, _p, _p, _p]),
+    "qw_kv_import_turbo4": (_i, [_p, _i, _p, _p, _p, _p, _p, _p]),
+    "qw_turbo4_codebook": (_i, [_i, _i, _p]),
+    "qw_turbo4_signs": (_i, [_i, ctypes.c_uint32, _p]),
     "qw_kv_destroy": (_i, [_p]),
     "qw_kv_reserve": (_i, [_p, _i, _p]),
     "qw_kv_offset": (_i, [_p, ctypes.POINTER(_i)]),
@@ -131,17 +137,19 @@ class KVCacheMode:
     AFFINE8 = 1
     AFFINE4 = 2
     INT8 = 3  # per-token absmax Int8 (cache.rs:262-316)
+    TURBO4 = 4  # symmetric PolarQuant, the reference's served default (cache.rs:1438)
 
-    BITS = {0: 16, 1: 8, 2: 4, 3: 8}
+    BITS = {0: 16, 1: 8, 2: 4, 3: 8, 4: 4}
+    DEFAULT_TURBO_SEED = 0x7B470404  # cache.rs:324
 
     @staticmethod
     def from_str(s: str) -> int:
         key = s.lower()
         table = {"fp16": 0, "float16": 0, "affine8": 1, "uniform8": 1, "affine4": 2,
-                 "uniform4": 2, "int8": 3}
+                 "uniform4": 2, "int8": 3, "turbo4": 4}
         if key not in table:
             raise ValueError(f'unknown kv-cache-mode "{s}"; expected "fp16", "affine8", '
-                             f'"affine4" or "int8"')
+                             f'"affine4", "int8" or "turbo4"')
         return table[key]
 
 
@@ -149,7 +157,7 @@ class KVCache:
     """One layer's KV cache on a GPU (reference ``KVCache``, cache.rs:354)."""
 
     def __init__(self, mode: int | str, n_kv_heads: int, head_dim: int, capacity: int = 0,
-                 group_size: int = 64, device=None):
+                 group_size: int = 64, device=None, turbo_seed: int | None = None):
         torch = _torch()
         if isinstance(mode, str):
             mode = KVCacheMode.from_str(mode)
@@ -159,9 +167,12 @@ class KVCache:
         self.bits = KVCacheMode.BITS[mode]
         self.device = torch.device("cuda", torch.cuda.current_device() if device is None else
                                    torch.device(device).index or 0)
+        self.turbo_seed = (KVCacheMode.DEFAULT_TURBO_SEED if turbo_seed is None
+                           else int(turbo_seed) & 0xFFFFFFFF)
         h = _p()
-        _check(lib().qw_kv_create(mode, group_size, n_kv_heads, head_dim, capacity,
-                                  self.device.index, ctypes.byref(h)))
+        # KVCache::new_with_mode_and_seed (cache.rs:537)
+        _check(lib().qw_kv_create_seeded(mode, group_size, n_kv_heads, head_dim, capacity,
+                                         self.device.index, self.turbo_seed, ctypes.byref(h)))
         self._h = h
 
     def close(self) -> None:
@@ -286,6 +297,10 @@ class KVCache:
             self.bits = KVCacheMode.BITS[target_mode]
         return bool(d.value)
 
+    def demote_fp16_to_turbo4(self) -> bool:
+        """The reference's own demote (cache.rs:3591): fp16 -> Turbo4."""
+        return self.demote_fp16_to_affine(KVCacheMode.TURBO4)
+
     def trim(self, n: int) -> int:
         v = _i()
         _check(lib().qw_kv_trim(self._h, n, ctypes.byref(v)))
@@ -302,6 +317,17 @@ class KVCache:
             _check(lib().qw_kv_export(self._h, k.data_ptr(), None, None, v.data_ptr(), None, None,
                                       st))
             return {"keys": k, "values": v}
+        if self.mode == KVCacheMode.TURBO4:
+            # turbo4_snapshot_tensors (cache.rs:570): packed [H, T, D/2] u8, sidecars [H, T, 1]
+            t = {name: torch.empty((H, n, D // 2), dtype=torch.uint8, device=self.device)
+                 for name in ("k_packed", "v_packed")}
+            for name in ("k_rescale", "v_norms", "v_rescale"):
+                t[name] = torch.empty((H, n, 1), dtype=torch.float16, device=self.device)
+            _check(lib().qw_kv_export_turbo4(self._h, t["k_packed"].data_ptr(),
+                                             t["k_rescale"].data_ptr(), t["v_packed"].data_ptr(),
+                                             t["v_norms"].data_ptr(), t["v_rescale"].data_ptr(),
+                                             st))
+            return t
         if self.mode == KVCacheMode.INT8:
             # the reference's keys, values [H, T, D] int8; key_scales, val_scales [H, T, 1] f16
             t = {name: torch.empty((H, n, D), dtype=torch.int8, device=self.device)
@@ -330,6 +356,14 @@ class KVCache:
                                       None, None, st))
             return
         t = {k2: v2.contiguous() for k2, v2 in tensors.items()}
+        if self.mode == KVCacheMode.TURBO4:
+            # restore_turbo4_snapshot (cache.rs:581)
+            n = t["k_packed"].shape[-2]
+            _check(lib().qw_kv_import_turbo4(self._h, n, t["k_packed"].data_ptr(),
+                                             t["k_rescale"].data_ptr(), t["v_packed"].data_ptr(),
+                                             t["v_norms"].data_ptr(), t["v_rescale"].data_ptr(),
+                                             st))
+            return
         if self.mode == KVCacheMode.INT8:
             n = t["keys"].shape[1]
             _check(lib().qw_kv_import(self._h, n, t["keys"].data_ptr(), t["key_scales"].data_ptr(),
@@ -467,3 +501,22 @@ def fused_rope_qk_append(qkv, n_q_heads: int, n_kv_heads: int, head_dim: int, ro
                                          q.data_ptr(), k.data_ptr(), v.data_ptr(),
                                          _stream(x.device)))
     return q, k, v
+
+
+def turbo4_codebook(bits: int, head_dim: int):
+    """The 2^bits Lloyd-Max centroids for N(0, 1/head_dim) the library builds
+    (reference ``optimal_centroids``, turbo/codebook.rs:139), float32 numpy."""
+    import numpy as np
+
+    out = np.zeros(1 << bits, np.float32)
+    _check(lib().qw_turbo4_codebook(bits, head_dim, out.ctypes.data))
+    return out
+
+
+def turbo4_signs(length: int, seed: int):
+    """The +-1 LCG sign vector (reference ``generate_signs``, turbo/quant.rs:217)."""
+    import numpy as np
+
+    out = np.zeros(length, np.float32)
+    _check(lib().qw_turbo4_signs(length, seed & 0xFFFFFFFF, out.ctypes.data))
+    return out

@@ -23,7 +23,7 @@ BUILD_DIR = os.path.join(HERE, "_build")
 ARCH = "gfx950"
 
 SOURCES = ["kv_cache.hip", "attend_decode.hip", "attend_block.hip", "dlsa.hip", "dlsa_select.hip",
-           "rope.hip", "abi.hip"]
+           "rope.hip", "turbo4.hip", "abi.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

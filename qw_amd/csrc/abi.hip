@@ -44,6 +44,12 @@ const char* qw_last_error(void) { return qw::last_error(); }
 
 int qw_kv_create(int mode, int group_size, int n_kv_heads, int head_dim, int capacity,
                  int device, qw_kv_cache** out) {
+    return qw_kv_create_seeded(mode, group_size, n_kv_heads, head_dim, capacity, device,
+                               qw::turbo4::kDefaultSeed, out);
+}
+
+int qw_kv_create_seeded(int mode, int group_size, int n_kv_heads, int head_dim, int capacity,
+                        int device, uint32_t turbo_seed, qw_kv_cache** out) {
     if (!out) {
         qw::set_error("qw_kv_create: null out pointer");
         return QW_ERR_INVALID_ARGUMENT;
@@ -55,6 +61,7 @@ int qw_kv_create(int mode, int group_size, int n_kv_heads, int head_dim, int cap
         return QW_ERR_OUT_OF_MEMORY;
     }
     int rc;
+    c->impl.turbo_seed = turbo_seed;
     try {
         rc = c->impl.init(mode, group_size, n_kv_heads, head_dim, capacity, device);
     } catch (...) {
@@ -212,6 +219,51 @@ int qw_dlsa_select(const float* scores, int64_t score_stride, const int32_t* mem
     QW_GUARDED(qw::dlsa_select(scores, score_stride, members, n_member_rows, bucket_cap, positions,
                                n_rows, total_rows, window, sink, top_k, top_p, buckets_per_block,
                                threads, lists, lengths, picked, status, (hipStream_t)stream));
+}
+
+int qw_kv_export_turbo4(const qw_kv_cache* cache, void* k_packed, void* k_rescale,
+                        void* v_packed, void* v_norms, void* v_rescale, void* stream) {
+    QW_HANDLE(cache);
+    QW_GUARDED(cache->impl.turbo4_export(k_packed, k_rescale, v_packed, v_norms, v_rescale,
+                                         (hipStream_t)stream));
+}
+
+int qw_kv_import_turbo4(qw_kv_cache* cache, int n_tokens, const void* k_packed,
+                        const void* k_rescale, const void* v_packed, const void* v_norms,
+                        const void* v_rescale, void* stream) {
+    QW_HANDLE(cache);
+    QW_GUARDED(cache->impl.turbo4_import(n_tokens, k_packed, k_rescale, v_packed, v_norms,
+                                         v_rescale, (hipStream_t)stream));
+}
+
+int qw_turbo4_codebook(int bits, int head_dim, float* centroids) {
+    if (bits < 1 || bits > 8 || head_dim <= 0 || !centroids) {
+        qw::set_error("qw_turbo4_codebook: bits must be 1..8, head_dim > 0, non-null output");
+        return QW_ERR_INVALID_ARGUMENT;
+    }
+    try {
+        const std::vector<float> c = qw::turbo4::centroids(bits, head_dim);
+        for (size_t i = 0; i < c.size(); i++) centroids[i] = c[i];
+    } catch (...) {
+        qw::set_error("qw_turbo4_codebook: host allocation failed");
+        return QW_ERR_OUT_OF_MEMORY;
+    }
+    return QW_OK;
+}
+
+int qw_turbo4_signs(int len, uint32_t seed, float* signs) {
+    if (len < 0 || (len > 0 && !signs)) {
+        qw::set_error("qw_turbo4_signs: len must be >= 0 with a non-null output");
+        return QW_ERR_INVALID_ARGUMENT;
+    }
+    try {
+        const std::vector<float> s = qw::turbo4::signs(len, seed);
+        for (int i = 0; i < len; i++) signs[i] = s[i];
+    } catch (...) {
+        qw::set_error("qw_turbo4_signs: host allocation failed");
+        return QW_ERR_OUT_OF_MEMORY;
+    }
+    return QW_OK;
 }
 
 int qw_fused_rope_qk_append(const void* qkv, int batch, int seq, int n_q_heads, int n_kv_heads,

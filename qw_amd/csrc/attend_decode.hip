@@ -708,6 +708,7 @@ int launch_partial_merge(const float* part_o, const float2* part_ml, int nc, int
 
 int launch_attention(KVCache& cc, const void* q, int n_q_heads, int n_rows, float scale,
                      bool causal, void* out, hipStream_t stream) {
+    if (cc.turbo4()) return turbo4_attention(cc, q, n_q_heads, n_rows, scale, causal, out, stream);
     QW_REQUIRE(q && out, QW_ERR_INVALID_ARGUMENT, "attention: null q/out");
     QW_REQUIRE(n_q_heads > 0 && n_q_heads % cc.hkv == 0, QW_ERR_INVALID_ARGUMENT,
                "attention: n_q_heads must be a positive multiple of n_kv_heads");

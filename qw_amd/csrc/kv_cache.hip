@@ -27,10 +27,12 @@ const char* last_error() { return g_last_error.c_str(); }
 
 size_t KVCache::k_data_bytes(int c) const { return (size_t)hkv * c * D * bits / 8; }
 size_t KVCache::k_param_bytes(int c) const {
+    if (turbo4()) return (size_t)hkv * c * 4;
     return affine() ? (size_t)hkv * c * (D / kGroup) * 4 : 0;
 }
 size_t KVCache::v_data_bytes(int c) const { return (size_t)hkv * c * D * bits / 8; }
 size_t KVCache::v_param_bytes(int c) const {
+    if (turbo4()) return (size_t)hkv * (c / 8) * 32;
     return affine() ? (size_t)hkv * (c / 8) * (D / kGroup) * 32 : 0;
 }
 
@@ -63,7 +65,7 @@ static int alloc_zero(void** p, size_t bytes) {
 int KVCache::init(int mode_, int group_size, int n_kv_heads, int head_dim, int capacity,
                   int device_) {
     QW_REQUIRE(mode_ == QW_KV_FP16 || mode_ == QW_KV_AFFINE8 || mode_ == QW_KV_AFFINE4 ||
-                   mode_ == QW_KV_INT8,
+                   mode_ == QW_KV_INT8 || mode_ == QW_KV_TURBO4,
                QW_ERR_INVALID_ARGUMENT, "qw_kv_create: unknown mode");
     QW_REQUIRE(n_kv_heads > 0 && capacity >= 0 && head_dim > 0, QW_ERR_INVALID_ARGUMENT,
                "qw_kv_create: n_kv_heads, head_dim must be > 0 and capacity >= 0");
@@ -73,12 +75,13 @@ int KVCache::init(int mode_, int group_size, int n_kv_heads, int head_dim, int c
         QW_REQUIRE(head_dim == 256 || head_dim == 128, QW_ERR_UNSUPPORTED,
                    "qw_kv_create: affine modes support head_dim 128 or 256");
     } else {
-        // fp16 and the per-token Int8 mode have no group; group_size is ignored
+        // fp16, the per-token Int8 mode and Turbo4 have no group; group_size
+        // is ignored
         QW_REQUIRE(head_dim == 256 || head_dim == 128, QW_ERR_UNSUPPORTED,
-                   "qw_kv_create: fp16 and int8 modes support head_dim 128 or 256");
+                   "qw_kv_create: fp16, int8 and turbo4 modes support head_dim 128 or 256");
     }
     mode = mode_;
-    bits = mode_ == QW_KV_AFFINE4 ? 4 : (mode_ == QW_KV_FP16 ? 16 : 8);
+    bits = (mode_ == QW_KV_AFFINE4 || mode_ == QW_KV_TURBO4) ? 4 : (mode_ == QW_KV_FP16 ? 16 : 8);
     D = head_dim;
     hkv = n_kv_heads;
     device = device_;
@@ -95,16 +98,22 @@ int KVCache::init(int mode_, int group_size, int n_kv_heads, int head_dim, int c
     // Int8 codes always take the separately rounded dequant (offset 1152).
     const int fast0 = int8() ? 0 : 1;
     QW_HIP_CHECK(hipMemcpy(fast_flag, &fast0, sizeof(int), hipMemcpyHostToDevice));
+    if (turbo4()) {
+        int rc = turbo4_setup();
+        if (rc) return rc;
+    }
     return reserve(capacity, nullptr);
 }
 
 int KVCache::release() {
     DeviceGuard dg(device);
     (void)hipDeviceSynchronize();
-    void* ptrs[6] = {k_data, (void*)k_params, v_data, (void*)v_params, ws, (void*)fast_flag};
+    void* ptrs[7] = {k_data, (void*)k_params, v_data, (void*)v_params, ws, (void*)fast_flag,
+                     (void*)t4_tables};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     fast_flag = nullptr;
+    t4_tables = nullptr;
     k_data = v_data = ws = nullptr;
     k_params = v_params = nullptr;
     ws_bytes = 0;
@@ -128,8 +137,12 @@ int KVCache::reserve(int capacity, hipStream_t stream) {
     if (cap > 0) {
         // Per head, the first `cap` rows (K, K params) or cap/8 blocks (V, V
         // params) move to the head's start in the new buffers.
-        const size_t kr = (size_t)D * bits / 8, kpr = affine() ? (size_t)(D / kGroup) * 4 : 0;
-        const size_t vb = (size_t)D * bits, vpb = affine() ? (size_t)(D / kGroup) * 32 : 0;
+        // (Turbo4: row-major packed V, cap/8 blocks of 8 rows are the same
+        // bytes; one 4-byte side record a row.)
+        const size_t kr = (size_t)D * bits / 8;
+        const size_t kpr = turbo4() ? 4 : (affine() ? (size_t)(D / kGroup) * 4 : 0);
+        const size_t vb = (size_t)D * bits;
+        const size_t vpb = turbo4() ? 32 : (affine() ? (size_t)(D / kGroup) * 32 : 0);
         for (int h = 0; h < hkv; h++) {
             QW_HIP_CHECK(hipMemcpyAsync((char*)nk + h * (size_t)nc * kr,
                                         (char*)k_data + h * (size_t)cap * kr, cap * kr,
@@ -137,7 +150,7 @@ int KVCache::reserve(int capacity, hipStream_t stream) {
             QW_HIP_CHECK(hipMemcpyAsync((char*)nv + h * (size_t)(nc / 8) * vb,
                                         (char*)v_data + h * (size_t)(cap / 8) * vb,
                                         (cap / 8) * vb, hipMemcpyDeviceToDevice, stream));
-            if (affine()) {
+            if (kpr) {
                 QW_HIP_CHECK(hipMemcpyAsync((char*)nkp + h * (size_t)nc * kpr,
                                             (char*)k_params + h * (size_t)cap * kpr, cap * kpr,
                                             hipMemcpyDeviceToDevice, stream));
@@ -184,8 +197,9 @@ int KVCache::demote(int target_mode, hipStream_t stream, int* demoted) {
     // in the quantized mode by quantize-appending its rows [0, offset) to an
     // empty cache of that mode; anything else is left alone (returns 0).
     *demoted = 0;
-    QW_REQUIRE(target_mode == QW_KV_AFFINE4 || target_mode == QW_KV_AFFINE8, QW_ERR_INVALID_ARGUMENT,
-               "demote: target mode must be an affine mode");
+    QW_REQUIRE(target_mode == QW_KV_AFFINE4 || target_mode == QW_KV_AFFINE8 ||
+                   target_mode == QW_KV_TURBO4,
+               QW_ERR_INVALID_ARGUMENT, "demote: target mode must be an affine mode or turbo4");
     if (mode != QW_KV_FP16 || offset <= 0) return QW_OK;
     DeviceGuard dg(device);
     QW_REQUIRE(dg.ok, QW_ERR_HIP, "demote: hipSetDevice failed");
@@ -212,8 +226,9 @@ int KVCache::demote(int target_mode, hipStream_t stream, int* demoted) {
     cap = 0;
     offset = 0;
     mode = target_mode;
-    bits = target_mode == QW_KV_AFFINE4 ? 4 : 8;
-    rc = reserve(old_cap, stream);
+    bits = target_mode == QW_KV_AFFINE8 ? 8 : 4;
+    rc = turbo4() ? turbo4_setup() : QW_OK;
+    if (rc == QW_OK) rc = reserve(old_cap, stream);
     if (rc == QW_OK) rc = update(tk, tv, n, stream);
     if (rc == QW_OK) rc = hipStreamSynchronize(stream) == hipSuccess ? QW_OK : QW_ERR_HIP;
     (void)hipFree(tk);
@@ -460,7 +475,10 @@ int KVCache::update_rows(const RowSrc& rs, int n_tokens, hipStream_t stream) {
         int rc = reserve(std::max(need, cap + cap / 2), stream);
         if (rc) return rc;
     }
-    if (affine()) {
+    if (turbo4()) {
+        int rc = turbo4_update(rs, n_tokens, stream);
+        if (rc) return rc;
+    } else if (affine()) {
         const int nblk = (offset + n_tokens - 1) / 8 - offset / 8 + 1;
         dim3 grid(nblk, hkv);
         if (D == 256)
@@ -578,6 +596,7 @@ int KVCache::dequantize(int start, int n, void* k_out, void* v_out, hipStream_t 
     if (n == 0) return QW_OK;
     QW_REQUIRE(k_out && v_out, QW_ERR_INVALID_ARGUMENT, "dequantize: null output");
     DeviceGuard dg(device);
+    if (turbo4()) return turbo4_dequantize(start, n, k_out, v_out, stream);
     const int64_t work = affine() ? (int64_t)hkv * n * (D / 8) : (int64_t)hkv * n * D;
     const unsigned blocks = (unsigned)std::min<int64_t>((work + 255) / 256, 4096);
     if (affine())
@@ -737,6 +756,7 @@ __global__ __launch_bounds__(256) void flip_code_sign_kernel(uint32_t* __restric
 
 int KVCache::export_tensors(void* k_codes, void* k_scales, void* k_biases, void* v_codes,
                             void* v_scales, void* v_biases, hipStream_t stream) const {
+    QW_REQUIRE(!turbo4(), QW_ERR_STATE, "export: a Turbo4 cache exports with qw_kv_export_turbo4");
     QW_REQUIRE(k_codes && v_codes, QW_ERR_INVALID_ARGUMENT, "export: null code pointers");
     QW_REQUIRE(!affine() || (k_scales && v_scales && (int8() || (k_biases && v_biases))),
                QW_ERR_INVALID_ARGUMENT, "export: null scale/bias pointers");
@@ -770,6 +790,7 @@ int KVCache::export_tensors(void* k_codes, void* k_scales, void* k_biases, void*
 int KVCache::import_tensors(int n_tokens, const void* k_codes, const void* k_scales,
                             const void* k_biases, const void* v_codes, const void* v_scales,
                             const void* v_biases, hipStream_t stream) {
+    QW_REQUIRE(!turbo4(), QW_ERR_STATE, "import: a Turbo4 cache imports with qw_kv_import_turbo4");
     QW_REQUIRE(n_tokens >= 0, QW_ERR_INVALID_ARGUMENT, "import: n_tokens must be >= 0");
     QW_REQUIRE(k_codes && v_codes, QW_ERR_INVALID_ARGUMENT, "import: null code pointers");
     QW_REQUIRE(!affine() || (k_scales && v_scales && (int8() || (k_biases && v_biases))),

@@ -8,6 +8,7 @@
 #pragma once
 
 #include "qw_common.hpp"
+#include "turbo4_codec.hpp"
 
 namespace qw {
 
@@ -28,22 +29,31 @@ struct RowSrc {
 
 struct KVCache {
     int mode = QW_KV_FP16;  // QW_KV_*
-    int bits = 16;          // 4, 8 (affine) or 16 (fp16)
+    int bits = 16;          // 4 (affine4, turbo4), 8 (affine8, int8) or 16 (fp16)
     int D = 0;              // head_dim
     int hkv = 0;            // KV heads
     int device = 0;
     int offset = 0;         // cached tokens (cache.rs `offset`)
     int cap = 0;            // allocated rows per head, multiple of 256
 
-    // K plane: affine codes [hkv][cap][D*bits/32] u32 or fp16 [hkv][cap][D].
+    // K plane: affine codes [hkv][cap][D*bits/32] u32 or fp16 [hkv][cap][D];
+    // Turbo4: packed indices [hkv][cap][D/2] bytes (low nibble even coord).
     void* k_data = nullptr;
-    // K params: [hkv][cap][D/64] half2(scale, bias); affine only.
+    // K params: [hkv][cap][D/64] half2(scale, bias) (affine);
+    // Turbo4: [hkv][cap] half2(k_rescale, 0).
     uint32_t* k_params = nullptr;
     // V plane: affine 8-key blocks [hkv][cap/8][D*bits/4 bytes] or fp16
-    // 8-key blocks [hkv][cap/8][D][8] f16 (same transposition, 16 bytes a dim).
+    // 8-key blocks [hkv][cap/8][D][8] f16 (same transposition, 16 bytes a dim);
+    // Turbo4: packed indices [hkv][cap][D/2] bytes, row-major like K.
     void* v_data = nullptr;
-    // V params: [hkv][cap/8][D/64][16] f16 (s0..s7, b0..b7); affine only.
+    // V params: [hkv][cap/8][D/64][16] f16 (s0..s7, b0..b7) (affine);
+    // Turbo4: [hkv][cap] half2(v_norm, v_rescale).
     uint32_t* v_params = nullptr;
+
+    // Turbo4 codec tables on the device (float): V signs1, V signs2, K signs1,
+    // K signs2 (D each), then 16 centroids and 15 boundaries.
+    uint32_t turbo_seed = turbo4::kDefaultSeed;
+    float* t4_tables = nullptr;
 
     // 1 while every stored scale is inside the exact 2-op dequant range of the
     // fused kernels (dequant.hpp); cleared by an append or import that stores
@@ -58,8 +68,11 @@ struct KVCache {
     // Codes and per-group (scale, bias) in the affine layout: the affine modes
     // and Int8 (stored as 8-bit codes biased by 128, the token's scale in
     // every group, bias 0).
-    bool affine() const { return mode != QW_KV_FP16; }
+    bool affine() const {
+        return mode == QW_KV_AFFINE8 || mode == QW_KV_AFFINE4 || mode == QW_KV_INT8;
+    }
     bool int8() const { return mode == QW_KV_INT8; }
+    bool turbo4() const { return mode == QW_KV_TURBO4; }
     // Offset the 8-bit magic-number conversion subtracts to recover a code
     // (fp16 1024 + stored byte): 1024 for unsigned affine codes, 1152 for
     // Int8 codes stored biased by 128.
@@ -71,6 +84,8 @@ struct KVCache {
     size_t v_param_bytes(int c) const;
 
     int init(int mode, int group_size, int n_kv_heads, int head_dim, int capacity, int device);
+    // Builds the Turbo4 tables for turbo_seed and D (turbo4.hip).
+    int turbo4_setup();
     int release();
     int reserve(int capacity, hipStream_t stream);
     int ensure_workspace(size_t bytes);
@@ -106,6 +121,16 @@ struct KVCache {
     int import_tensors(int n_tokens, const void* k_codes, const void* k_scales,
                        const void* k_biases, const void* v_codes, const void* v_scales,
                        const void* v_biases, hipStream_t stream);
+
+    // Turbo4 parts (turbo4.hip): quantize-on-append, fetch, snapshot tensors
+    // (cache.rs:570-626 turbo4_snapshot_tensors / restore_turbo4_snapshot).
+    int turbo4_update(const RowSrc& src, int n_tokens, hipStream_t stream);
+    int turbo4_dequantize(int start, int n, void* k_out, void* v_out, hipStream_t stream) const;
+    int turbo4_export(void* k_packed, void* k_rescale, void* v_packed, void* v_norms,
+                      void* v_rescale, hipStream_t stream) const;
+    int turbo4_import(int n_tokens, const void* k_packed, const void* k_rescale,
+                      const void* v_packed, const void* v_norms, const void* v_rescale,
+                      hipStream_t stream);
 };
 
 // RAII guard that makes `device` current for the duration of a call.
@@ -121,6 +146,11 @@ struct DeviceGuard {
         if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
     }
 };
+
+// Turbo4 attention (turbo4.hip): q rotated into the K basis, the cache's
+// rotated K/V expanded to fp16, the fp16 kernels, the output rotated back.
+int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float scale,
+                     bool causal, void* out, hipStream_t stream);
 
 // Kernel launchers (attend_decode.hip, attend_block.hip).
 int launch_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float scale,

@@ -1,0 +1,559 @@
+// turbo4.hip - the Turbo4 (symmetric PolarQuant) KV mode on gfx950:
+// quantize-on-append, fetch, snapshot tensors and attention.
+//
+// Reference behaviour followed (cr0sh/qw):
+//   quantize: crates/mlxcel-core/src/cache/turbo/quant.rs:270-440
+//     (quantize_into_packed: fp32 norm, x / norm, signs1, Walsh-Hadamard,
+//     signs2, nearest centroid by boundary count, nibble pack) and the pack
+//     kernel crates/mlxcel-core/cpp/mlx_cxx_kernels.cpp:186-212 (index =
+//     #boundaries below the value, rescale = f16(norm / max(|y|, 1e-10)));
+//   fetch: quant.rs:486-546 (V: centroids, unit-normalised, inverse rotation,
+//     times the norm) and :676-691 (K: f16(centroid * k_rescale), inverse
+//     rotation);
+//   attention: crates/mlxcel-core/src/cache/turbo/sparse_v.rs:1051-1072
+//     (attention_turbo4_dequant_sdpa: q rotated into the K basis and cast to
+//     fp16, K and V expanded to f16(centroid * rescale) in their rotated
+//     bases, fp16 SDPA, output rotated back through the V basis), with the
+//     bulk expansion of crates/mlx-cpp/turbo/turbo4_delegated_sdpa.cpp:193-221;
+//   storage and growth: crates/mlxcel-core/src/cache.rs:1438-1597
+//     (update_turbo4_sym).
+//
+// The Walsh-Hadamard transform is the orthonormal Sylvester one
+// (H[i][j] = (-1)^popcount(i & j) / sqrt(D)), done in fp32 registers: a lane
+// holds D/64 consecutive coordinates, the first log2(D/64) butterfly stages
+// run inside the lane and the remaining six across lanes.
+#include <math.h>
+
+#include <algorithm>
+#include <mutex>
+#include <string>
+
+#include "kv_cache.hpp"
+#include "rope.hpp"
+
+namespace qw {
+
+namespace {
+
+// Offsets into the device tables.
+template <int D>
+struct T4Tab {
+    static constexpr int v_s1 = 0, v_s2 = D, k_s1 = 2 * D, k_s2 = 3 * D;
+    static constexpr int cb = 4 * D, bnd = 4 * D + 16;
+    static constexpr int size = 4 * D + 32;
+};
+
+// The transform's scale as MLX forms it: 1 / sqrt(n) in double, cast to fp32.
+__host__ __device__ constexpr float wht_scale(int D) {
+    return D == 256 ? 0.0625f : (D == 128 ? 0.08838834764831845f : 0.0f);
+}
+
+// In-place fp32 Walsh-Hadamard transform of the wave's row (lane holds
+// coordinates lane * VPL .. lane * VPL + VPL - 1), unscaled.
+template <int D>
+__device__ __forceinline__ void wht_wave(float (&y)[D / 64], int lane) {
+    constexpr int VPL = D / 64;
+#pragma unroll
+    for (int s = 1; s < VPL; s <<= 1) {
+#pragma unroll
+        for (int j = 0; j < VPL; j++) {
+            if ((j & s) == 0) {
+                const float a = y[j], b = y[j + s];
+                y[j] = a + b;
+                y[j + s] = a - b;
+            }
+        }
+    }
+#pragma unroll
+    for (int ls = 1; ls < 64; ls <<= 1) {
+        const bool upper = (lane & ls) != 0;
+#pragma unroll
+        for (int j = 0; j < VPL; j++) {
+            const float p = __shfl_xor(y[j], ls);
+            y[j] = upper ? p - y[j] : y[j] + p;
+        }
+    }
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+    return x;
+}
+
+// f16 of an fp32 product, rounded first to fp32 (the reference multiplies in
+// fp32 and then casts); the register pin keeps the compiler from fusing the
+// multiply and the conversion into one singly rounded mixed-precision op.
+__device__ __forceinline__ f16 f16_of_product(float a, float b) {
+    float p = a * b;
+    asm volatile("" : "+v"(p));
+    return (f16)p;
+}
+
+// ------------------------------------------------------------ append
+//
+// grid (n_tokens, hkv), 2 waves: wave 0 quantizes the K row (K signs), wave 1
+// the V row (V signs). K may be rotated by RoPE as it is read (RowSrc).
+template <int D>
+__global__ __launch_bounds__(128) void turbo4_append_kernel(
+    RowSrc rs, int t_old, int cap, const float* __restrict__ tab, uint8_t* __restrict__ k_packed,
+    uint32_t* __restrict__ k_side, uint8_t* __restrict__ v_packed, uint32_t* __restrict__ v_side) {
+    constexpr int VPL = D / 64;
+    using TT = T4Tab<D>;
+    __shared__ float s_cb[16];
+    if (threadIdx.x < 16) s_cb[threadIdx.x] = tab[TT::cb + threadIdx.x];
+    __syncthreads();
+    const int i = blockIdx.x, h = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const bool is_k = wave == 0;
+    const int64_t src = (int64_t)i * rs.row_stride + (int64_t)h * rs.head_stride;
+    const f16* row = (is_k ? rs.k : rs.v) + src;
+
+    float x[VPL];
+    if (is_k && rs.rope_dims > 0) {
+#pragma unroll
+        for (int j = 0; j < VPL; j++)
+            x[j] = (float)(f16)rope_elem(row, lane * VPL + j, rs.rope_dims, rs.traditional,
+                                         rs.log2_base, rs.scale, rs.position0 + i);
+    } else {
+#pragma unroll
+        for (int j = 0; j < VPL; j++) x[j] = (float)row[lane * VPL + j];
+    }
+    // 1. L2 norm in fp32; an all-zero row divides by 1
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPL; j++) ss = __builtin_fmaf(x[j], x[j], ss);
+    const float norm = sqrtf(wave_sum(ss));
+    const float safe = norm > 0.0f ? norm : 1.0f;
+    // 2. signs2 . H . signs1 of the unit row
+    const float* s1 = tab + (is_k ? TT::k_s1 : TT::v_s1);
+    const float* s2 = tab + (is_k ? TT::k_s2 : TT::v_s2);
+    float y[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; j++) y[j] = (x[j] / safe) * s1[lane * VPL + j];
+    wht_wave<D>(y, lane);
+    // 3. nearest centroid: the number of boundaries strictly below the value
+    uint32_t idx[VPL];
+    float csq = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPL; j++) {
+        const float v = (y[j] * wht_scale(D)) * s2[lane * VPL + j];
+        uint32_t n = 0;
+#pragma unroll
+        for (int b = 0; b < 15; b++) n += v > tab[TT::bnd + b] ? 1u : 0u;
+        idx[j] = n;
+        const float c = s_cb[n];
+        csq = __builtin_fmaf(c, c, csq);
+    }
+    const float rn = sqrtf(wave_sum(csq));
+    const f16 rescale = (f16)(norm / fmaxf(rn, 1e-10f));
+    // 4. pack: low nibble = even coordinate
+    const int t = t_old + i;
+    uint8_t* prow = (is_k ? k_packed : v_packed) + ((int64_t)h * cap + t) * (D / 2);
+    if constexpr (VPL == 4) {
+        const uint32_t b0 = idx[0] | (idx[1] << 4), b1 = idx[2] | (idx[3] << 4);
+        *(uint16_t*)(prow + 2 * lane) = (uint16_t)(b0 | (b1 << 8));
+    } else {
+        prow[lane] = (uint8_t)(idx[0] | (idx[1] << 4));
+    }
+    if (lane == 0) {
+        half2v sv;
+        if (is_k) {
+            sv.x = rescale;
+            sv.y = (f16)0.0f;
+            k_side[(int64_t)h * cap + t] = __builtin_bit_cast(uint32_t, sv);
+        } else {
+            sv.x = (f16)norm;
+            sv.y = rescale;
+            v_side[(int64_t)h * cap + t] = __builtin_bit_cast(uint32_t, sv);
+        }
+    }
+}
+
+// ------------------------------------------------------------ fetch
+//
+// Rows [start, start + n) back in the original basis: grid (n, hkv), wave 0
+// K, wave 1 V; out [hkv][n][D].
+template <int D>
+__global__ __launch_bounds__(128) void turbo4_fetch_kernel(
+    const uint8_t* __restrict__ k_packed, const uint32_t* __restrict__ k_side,
+    const uint8_t* __restrict__ v_packed, const uint32_t* __restrict__ v_side,
+    const float* __restrict__ tab, int cap, int start, int n, f16* __restrict__ k_out,
+    f16* __restrict__ v_out) {
+    constexpr int VPL = D / 64;
+    using TT = T4Tab<D>;
+    __shared__ float s_cb[16];
+    if (threadIdx.x < 16) s_cb[threadIdx.x] = tab[TT::cb + threadIdx.x];
+    __syncthreads();
+    const int i = blockIdx.x, h = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const bool is_k = wave == 0;
+    const int t = start + i;
+    const uint8_t* prow = (is_k ? k_packed : v_packed) + ((int64_t)h * cap + t) * (D / 2);
+    uint32_t idx[VPL];
+    if constexpr (VPL == 4) {
+        const uint32_t w = *(const uint16_t*)(prow + 2 * lane);
+#pragma unroll
+        for (int j = 0; j < 4; j++) idx[j] = (w >> (4 * j)) & 15u;
+    } else {
+        const uint32_t w = prow[lane];
+        idx[0] = w & 15u;
+        idx[1] = w >> 4;
+    }
+    const half2v side = __builtin_bit_cast(half2v, (is_k ? k_side : v_side)[(int64_t)h * cap + t]);
+    float y[VPL];
+    float mul;
+    if (is_k) {
+        // K: the rotated values as the fp16 expansion holds them
+        const float r = (float)side.x;
+#pragma unroll
+        for (int j = 0; j < VPL; j++) y[j] = (float)f16_of_product(s_cb[idx[j]], r);
+        mul = 1.0f;
+    } else {
+        // V: unit-normalised centroids, scaled by the stored norm at the end
+        float csq = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VPL; j++) {
+            y[j] = s_cb[idx[j]];
+            csq = __builtin_fmaf(y[j], y[j], csq);
+        }
+        const float yn = fmaxf(sqrtf(wave_sum(csq)), 1e-10f);
+#pragma unroll
+        for (int j = 0; j < VPL; j++) y[j] = y[j] / yn;
+        mul = (float)side.x;
+    }
+    // inverse rotation: signs1 . H . signs2
+    const float* s1 = tab + (is_k ? TT::k_s1 : TT::v_s1);
+    const float* s2 = tab + (is_k ? TT::k_s2 : TT::v_s2);
+#pragma unroll
+    for (int j = 0; j < VPL; j++) y[j] *= s2[lane * VPL + j];
+    wht_wave<D>(y, lane);
+    f16* orow = (is_k ? k_out : v_out) + ((int64_t)h * n + i) * D;
+#pragma unroll
+    for (int j = 0; j < VPL; j++) {
+        const float u = (y[j] * wht_scale(D)) * s1[lane * VPL + j];
+        orow[lane * VPL + j] = is_k ? (f16)u : (f16)(u * mul);
+    }
+}
+
+// ------------------------------------------- rotated fp16 expansion (SDPA)
+//
+// One 8-key block of one head a workgroup of D threads: thread = (key,
+// 8 coordinates). K_rot rows go to kw [hkv][capv][D]; V_rot to the fp16
+// cache's transposed blocks vw [hkv][capv/8][D][8] (dims in lane order)
+// through LDS. Keys past
+// `T` are written as zeros (the fp16 kernels read whole 8-key blocks).
+template <int D>
+__global__ __launch_bounds__(D) void turbo4_expand_kernel(
+    const uint8_t* __restrict__ k_packed, const uint32_t* __restrict__ k_side,
+    const uint8_t* __restrict__ v_packed, const uint32_t* __restrict__ v_side,
+    const float* __restrict__ tab, int cap, int T, int capv, f16* __restrict__ kw,
+    f16* __restrict__ vw) {
+    constexpr int CPK = D / 8;  // 8-coordinate chunks a key
+    using TT = T4Tab<D>;
+    __shared__ float s_cb[16];
+    __shared__ __align__(16) f16 sv[D][8];
+    if (threadIdx.x < 16) s_cb[threadIdx.x] = tab[TT::cb + threadIdx.x];
+    __syncthreads();
+    const int blk = blockIdx.x, h = blockIdx.y;
+    const int k = threadIdx.x / CPK, c = threadIdx.x % CPK;
+    const int t = blk * 8 + k;
+    half8 kv8, vv8;
+    if (t < T) {
+        const int64_t r = (int64_t)h * cap + t;
+        const uint32_t kb = *(const uint32_t*)(k_packed + r * (D / 2) + 4 * c);
+        const uint32_t vb = *(const uint32_t*)(v_packed + r * (D / 2) + 4 * c);
+        const float kr = (float)__builtin_bit_cast(half2v, k_side[r]).x;
+        const float vr = (float)__builtin_bit_cast(half2v, v_side[r]).y;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            kv8[j] = f16_of_product(s_cb[(kb >> (4 * j)) & 15u], kr);
+            vv8[j] = f16_of_product(s_cb[(vb >> (4 * j)) & 15u], vr);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) kv8[j] = vv8[j] = (f16)0.0f;
+    }
+    *(half8*)(kw + ((int64_t)h * capv + t) * D + 8 * c) = kv8;
+    // (the fp16 cache keeps V dims in MFMA lane order, v_phys_dim)
+#pragma unroll
+    for (int j = 0; j < 8; j++) sv[v_phys_dim(8 * c + j, D, 16)][k] = vv8[j];
+    __syncthreads();
+    const int p = threadIdx.x;  // physical dim slot
+    *(half8*)(vw + (((int64_t)h * (capv / 8) + blk) * D + p) * 8) = *(const half8*)&sv[p][0];
+}
+
+// ------------------------------------------------------------ rotation
+//
+// rows of D fp16: out = f16(s_out . (H / sqrt(D)) . s_in . in), one wave a row.
+template <int D>
+__global__ __launch_bounds__(256) void turbo4_rotate_kernel(const f16* __restrict__ in,
+                                                            f16* __restrict__ out, int rows,
+                                                            const float* __restrict__ s_in,
+                                                            const float* __restrict__ s_out) {
+    constexpr int VPL = D / 64;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;  // whole waves leave together
+    const f16* r = in + (int64_t)row * D;
+    float y[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; j++) y[j] = (float)r[lane * VPL + j] * s_in[lane * VPL + j];
+    wht_wave<D>(y, lane);
+    f16* o = out + (int64_t)row * D;
+#pragma unroll
+    for (int j = 0; j < VPL; j++)
+        o[lane * VPL + j] = (f16)((y[j] * wht_scale(D)) * s_out[lane * VPL + j]);
+}
+
+// Snapshot planes <-> the side arrays: [hkv][n] k_rescale, v_norms, v_rescale.
+__global__ void turbo4_side_export_kernel(const uint32_t* __restrict__ k_side,
+                                          const uint32_t* __restrict__ v_side, int hkv, int cap,
+                                          int n, f16* __restrict__ k_rescale,
+                                          f16* __restrict__ v_norms, f16* __restrict__ v_rescale) {
+    const int64_t total = (int64_t)hkv * n;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int h = (int)(i / n), t = (int)(i % n);
+        const half2v ks = __builtin_bit_cast(half2v, k_side[(int64_t)h * cap + t]);
+        const half2v vs = __builtin_bit_cast(half2v, v_side[(int64_t)h * cap + t]);
+        k_rescale[i] = ks.x;
+        v_norms[i] = vs.x;
+        v_rescale[i] = vs.y;
+    }
+}
+
+__global__ void turbo4_side_import_kernel(const f16* __restrict__ k_rescale,
+                                          const f16* __restrict__ v_norms,
+                                          const f16* __restrict__ v_rescale, int hkv, int cap,
+                                          int n, uint32_t* __restrict__ k_side,
+                                          uint32_t* __restrict__ v_side) {
+    const int64_t total = (int64_t)hkv * n;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int h = (int)(i / n), t = (int)(i % n);
+        half2v ks, vs;
+        ks.x = k_rescale[i];
+        ks.y = (f16)0.0f;
+        vs.x = v_norms[i];
+        vs.y = v_rescale[i];
+        k_side[(int64_t)h * cap + t] = __builtin_bit_cast(uint32_t, ks);
+        v_side[(int64_t)h * cap + t] = __builtin_bit_cast(uint32_t, vs);
+    }
+}
+
+static unsigned grid_for(int64_t work) {
+    return (unsigned)std::max<int64_t>(1, std::min<int64_t>((work + 255) / 256, 4096));
+}
+
+// Per-device workspace of the attention route: the rotated fp16 K/V, q and
+// output. Shared by the Turbo4 caches of a device (as MLX's allocator shares
+// its transient buffers); an event orders its users across streams.
+struct T4Workspace {
+    std::mutex m;
+    void* buf = nullptr;
+    size_t bytes = 0;
+    hipEvent_t last = nullptr;
+};
+constexpr int kMaxDevices = 64;
+T4Workspace g_ws[kMaxDevices];
+
+}  // namespace
+
+// ------------------------------------------------------------ host side
+
+int KVCache::turbo4_setup() {
+    QW_REQUIRE(D == 128 || D == 256, QW_ERR_UNSUPPORTED, "turbo4: head_dim must be 128 or 256");
+    std::vector<float> tab(4 * D + 32, 0.0f);
+    const uint32_t ks = turbo_seed + turbo4::kKSeedOffset;
+    const std::vector<float> parts[4] = {
+        turbo4::signs(D, turbo_seed), turbo4::signs(D, turbo_seed + turbo4::kSubSeed),
+        turbo4::signs(D, ks), turbo4::signs(D, ks + turbo4::kSubSeed)};
+    for (int p = 0; p < 4; p++) std::copy(parts[p].begin(), parts[p].end(), tab.begin() + p * D);
+    const std::vector<float> cb = turbo4::centroids(4, D);
+    const std::vector<float> bd = turbo4::boundaries(cb);
+    std::copy(cb.begin(), cb.end(), tab.begin() + 4 * D);
+    std::copy(bd.begin(), bd.end(), tab.begin() + 4 * D + 16);
+    DeviceGuard dg(device);
+    QW_REQUIRE(dg.ok, QW_ERR_HIP, "turbo4: hipSetDevice failed");
+    if (!t4_tables) {
+        if (hipMalloc(&t4_tables, tab.size() * sizeof(float)) != hipSuccess) {
+            (void)hipGetLastError();
+            t4_tables = nullptr;
+            set_error("turbo4: hipMalloc of the codec tables failed");
+            return QW_ERR_OUT_OF_MEMORY;
+        }
+    }
+    QW_HIP_CHECK(hipMemcpy(t4_tables, tab.data(), tab.size() * sizeof(float),
+                           hipMemcpyHostToDevice));
+    return QW_OK;
+}
+
+int KVCache::turbo4_update(const RowSrc& rs, int n_tokens, hipStream_t stream) {
+    dim3 grid(n_tokens, hkv);
+    if (D == 256)
+        hipLaunchKernelGGL(turbo4_append_kernel<256>, grid, dim3(128), 0, stream, rs, offset, cap,
+                           t4_tables, (uint8_t*)k_data, k_params, (uint8_t*)v_data, v_params);
+    else
+        hipLaunchKernelGGL(turbo4_append_kernel<128>, grid, dim3(128), 0, stream, rs, offset, cap,
+                           t4_tables, (uint8_t*)k_data, k_params, (uint8_t*)v_data, v_params);
+    QW_HIP_CHECK(hipGetLastError());
+    return QW_OK;
+}
+
+int KVCache::turbo4_dequantize(int start, int n, void* k_out, void* v_out,
+                               hipStream_t stream) const {
+    dim3 grid(n, hkv);
+    if (D == 256)
+        hipLaunchKernelGGL(turbo4_fetch_kernel<256>, grid, dim3(128), 0, stream,
+                           (const uint8_t*)k_data, k_params, (const uint8_t*)v_data, v_params,
+                           t4_tables, cap, start, n, (f16*)k_out, (f16*)v_out);
+    else
+        hipLaunchKernelGGL(turbo4_fetch_kernel<128>, grid, dim3(128), 0, stream,
+                           (const uint8_t*)k_data, k_params, (const uint8_t*)v_data, v_params,
+                           t4_tables, cap, start, n, (f16*)k_out, (f16*)v_out);
+    QW_HIP_CHECK(hipGetLastError());
+    return QW_OK;
+}
+
+int KVCache::turbo4_export(void* kp, void* kr, void* vp, void* vn, void* vr,
+                           hipStream_t stream) const {
+    QW_REQUIRE(turbo4(), QW_ERR_STATE, "turbo4 snapshot requires a Turbo4 cache");
+    QW_REQUIRE(kp && kr && vp && vn && vr, QW_ERR_INVALID_ARGUMENT,
+               "turbo4 snapshot: null tensor pointer");
+    const int n = offset;
+    if (n == 0) return QW_OK;
+    DeviceGuard dg(device);
+    QW_REQUIRE(dg.ok, QW_ERR_HIP, "turbo4 snapshot: hipSetDevice failed");
+    const size_t rb = (size_t)D / 2;
+    QW_HIP_CHECK(hipMemcpy2DAsync(kp, n * rb, k_data, cap * rb, n * rb, hkv,
+                                  hipMemcpyDeviceToDevice, stream));
+    QW_HIP_CHECK(hipMemcpy2DAsync(vp, n * rb, v_data, cap * rb, n * rb, hkv,
+                                  hipMemcpyDeviceToDevice, stream));
+    hipLaunchKernelGGL(turbo4_side_export_kernel, dim3(grid_for((int64_t)hkv * n)), dim3(256), 0,
+                       stream, k_params, v_params, hkv, cap, n, (f16*)kr, (f16*)vn, (f16*)vr);
+    QW_HIP_CHECK(hipGetLastError());
+    return QW_OK;
+}
+
+int KVCache::turbo4_import(int n, const void* kp, const void* kr, const void* vp, const void* vn,
+                           const void* vr, hipStream_t stream) {
+    QW_REQUIRE(turbo4(), QW_ERR_STATE, "turbo4 snapshot requires a Turbo4 cache");
+    QW_REQUIRE(n > 0, QW_ERR_INVALID_ARGUMENT, "turbo4 snapshot offset must be positive");
+    QW_REQUIRE(kp && kr && vp && vn && vr, QW_ERR_INVALID_ARGUMENT,
+               "turbo4 snapshot: null tensor pointer");
+    DeviceGuard dg(device);
+    QW_REQUIRE(dg.ok, QW_ERR_HIP, "turbo4 snapshot: hipSetDevice failed");
+    offset = 0;
+    int rc = reserve(n, stream);
+    if (rc) return rc;
+    const size_t rb = (size_t)D / 2;
+    QW_HIP_CHECK(hipMemcpy2DAsync(k_data, cap * rb, kp, n * rb, n * rb, hkv,
+                                  hipMemcpyDeviceToDevice, stream));
+    QW_HIP_CHECK(hipMemcpy2DAsync(v_data, cap * rb, vp, n * rb, n * rb, hkv,
+                                  hipMemcpyDeviceToDevice, stream));
+    hipLaunchKernelGGL(turbo4_side_import_kernel, dim3(grid_for((int64_t)hkv * n)), dim3(256), 0,
+                       stream, (const f16*)kr, (const f16*)vn, (const f16*)vr, hkv, cap, n,
+                       k_params, v_params);
+    QW_HIP_CHECK(hipGetLastError());
+    offset = n;
+    return QW_OK;
+}
+
+int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float scale,
+                     bool causal, void* out, hipStream_t stream) {
+    QW_REQUIRE(q && out, QW_ERR_INVALID_ARGUMENT, "attention: null q/out");
+    QW_REQUIRE(n_q_heads > 0 && n_q_heads % c.hkv == 0, QW_ERR_INVALID_ARGUMENT,
+               "attention: n_q_heads must be a positive multiple of n_kv_heads");
+    QW_REQUIRE(n_rows > 0, QW_ERR_INVALID_ARGUMENT, "attention: n_rows must be > 0");
+    QW_REQUIRE(c.offset >= n_rows, QW_ERR_INVALID_ARGUMENT,
+               "attention: fewer cached keys than query rows");
+    QW_REQUIRE(c.device >= 0 && c.device < kMaxDevices, QW_ERR_UNSUPPORTED,
+               "turbo4 attention: device ordinal out of range");
+    DeviceGuard dg(c.device);
+    QW_REQUIRE(dg.ok, QW_ERR_HIP, "attention: hipSetDevice failed");
+    const int D = c.D, T = c.offset;
+    const int capv = (T + 255) / 256 * 256;
+    const size_t kv_bytes = (size_t)c.hkv * capv * D * sizeof(f16);
+    const size_t q_bytes = (size_t)n_q_heads * n_rows * D * sizeof(f16);
+    const size_t need = 2 * kv_bytes + 2 * q_bytes;
+
+    T4Workspace& w = g_ws[c.device];
+    std::lock_guard<std::mutex> lock(w.m);
+    if (!w.last) QW_HIP_CHECK(hipEventCreateWithFlags(&w.last, hipEventDisableTiming));
+    if (need > w.bytes) {
+        if (w.buf) {
+            QW_HIP_CHECK(hipDeviceSynchronize());
+            (void)hipFree(w.buf);
+            w.buf = nullptr;
+            w.bytes = 0;
+        }
+        const size_t nb = need + need / 4;
+        if (hipMalloc(&w.buf, nb) != hipSuccess) {
+            (void)hipGetLastError();
+            w.buf = nullptr;
+            set_error("turbo4 attention: workspace hipMalloc failed");
+            return QW_ERR_OUT_OF_MEMORY;
+        }
+        w.bytes = nb;
+    } else {
+        QW_HIP_CHECK(hipStreamWaitEvent(stream, w.last, 0));
+    }
+    f16* kw = (f16*)w.buf;
+    f16* vw = (f16*)((char*)w.buf + kv_bytes);
+    f16* q_rot = (f16*)((char*)w.buf + 2 * kv_bytes);
+    f16* o_rot = (f16*)((char*)w.buf + 2 * kv_bytes + q_bytes);
+    const int qrows = n_q_heads * n_rows;
+    const float* tab = c.t4_tables;
+    // Every 8-key block up to capv: rows past T become zeros, as the fp16
+    // cache's unused rows are, since the fp16 kernels read whole tiles.
+    dim3 eg(capv / 8, c.hkv);
+    if (D == 256) {
+        using TT = T4Tab<256>;
+        hipLaunchKernelGGL(turbo4_rotate_kernel<256>, dim3((qrows + 3) / 4), dim3(256), 0, stream,
+                           (const f16*)q, q_rot, qrows, tab + TT::k_s1, tab + TT::k_s2);
+        hipLaunchKernelGGL(turbo4_expand_kernel<256>, eg, dim3(256), 0, stream,
+                           (const uint8_t*)c.k_data, c.k_params, (const uint8_t*)c.v_data,
+                           c.v_params, tab, c.cap, T, capv, kw, vw);
+    } else {
+        using TT = T4Tab<128>;
+        hipLaunchKernelGGL(turbo4_rotate_kernel<128>, dim3((qrows + 3) / 4), dim3(256), 0, stream,
+                           (const f16*)q, q_rot, qrows, tab + TT::k_s1, tab + TT::k_s2);
+        hipLaunchKernelGGL(turbo4_expand_kernel<128>, eg, dim3(128), 0, stream,
+                           (const uint8_t*)c.k_data, c.k_params, (const uint8_t*)c.v_data,
+                           c.v_params, tab, c.cap, T, capv, kw, vw);
+    }
+    QW_HIP_CHECK(hipGetLastError());
+    // The rotated K/V seen as an fp16 cache (not owning its planes); it
+    // borrows the Turbo4 cache's split-K workspace.
+    KVCache view;
+    view.mode = QW_KV_FP16;
+    view.bits = 16;
+    view.D = D;
+    view.hkv = c.hkv;
+    view.device = c.device;
+    view.offset = T;
+    view.cap = capv;
+    view.k_data = kw;
+    view.v_data = vw;
+    view.fast_flag = c.fast_flag;
+    view.ws = c.ws;
+    view.ws_bytes = c.ws_bytes;
+    int rc = launch_attention(view, q_rot, n_q_heads, n_rows, scale, causal, o_rot, stream);
+    c.ws = view.ws;
+    c.ws_bytes = view.ws_bytes;
+    if (rc) return rc;
+    if (D == 256) {
+        using TT = T4Tab<256>;
+        hipLaunchKernelGGL(turbo4_rotate_kernel<256>, dim3((qrows + 3) / 4), dim3(256), 0, stream,
+                           o_rot, (f16*)out, qrows, tab + TT::v_s2, tab + TT::v_s1);
+    } else {
+        using TT = T4Tab<128>;
+        hipLaunchKernelGGL(turbo4_rotate_kernel<128>, dim3((qrows + 3) / 4), dim3(256), 0, stream,
+                           o_rot, (f16*)out, qrows, tab + TT::v_s2, tab + TT::v_s1);
+    }
+    QW_HIP_CHECK(hipGetLastError());
+    QW_HIP_CHECK(hipEventRecord(w.last, stream));
+    return QW_OK;
+}
+
+}  // namespace qw
