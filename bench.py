@@ -100,11 +100,11 @@ def _mode(bits: int) -> str:
     return {4: "affine4", 8: "affine8", 16: "fp16"}[bits]
 
 
-def make_caches(torch, qw_amd, g, bits, T_prefix, cap, layers, jitter=True):
+def make_caches(torch, qw_amd, g, bits, T_prefix, cap, layers, jitter=True, mode=None):
     dev = torch.device("cuda:0")
     caches = []
     for _ in range(layers):
-        c = qw_amd.KVCache(_mode(bits), HKV, D, capacity=cap)
+        c = qw_amd.KVCache(mode or _mode(bits), HKV, D, capacity=cap)
         jit = (torch.empty((HKV, 1, 1), device=dev).uniform_(0.5, 2.0, generator=g) if jitter
                else torch.ones((HKV, 1, 1), device=dev))
         chunk = 8192
@@ -134,12 +134,13 @@ class LayerSet:
     """`layers` caches of one configuration plus per-layer q / new K,V / out,
     called through the raw C ABI with prebuilt arguments."""
 
-    def __init__(self, torch, qw_amd, seed, bits, T_prefix, L, layers, causal):
+    def __init__(self, torch, qw_amd, seed, bits, T_prefix, L, layers, causal, mode=None):
         dev = torch.device("cuda:0")
         g = torch.Generator(device=dev)
         g.manual_seed(seed)
         self.torch, self.qw, self.L, self.causal = torch, qw_amd, L, causal
-        self.caches = make_caches(torch, qw_amd, g, bits, T_prefix, T_prefix + L, layers)
+        self.caches = make_caches(torch, qw_amd, g, bits, T_prefix, T_prefix + L, layers,
+                                  mode=mode)
         self.q, self.kn, self.vn, self.out = [], [], [], []
         for _, jit in self.caches:
             self.q.append(torch.randn((1, HQ, L, D), device=dev, generator=g).half())
@@ -223,6 +224,21 @@ def bench_decode(torch, qw_amd, steps: int, warmup: int, bits: int = 4, T_prefix
     bytes_layer = bytes_attn + 2 * HKV * D * 2 + HKV * kv_bytes_per_token_head(bits) // 2
     return {"T": T, "bits": bits, "rounds": rounds, "layer_ms": layer_ms, "eager_layer_ms": eager_ms,
             "attn_ms": attn_ms, "bytes_layer": bytes_layer, "bytes_attn": bytes_attn}
+
+
+def bench_turbo4_decode(torch, qw_amd, steps: int, warmup: int, T_prefix: int = 32768):
+    """The reference's served default KV mode at the config-2 geometry:
+    update_and_attention of one token on a Turbo4 cache (rotate q, expand the
+    rotated K/V to fp16, the fp16 decode kernels, rotate the output back).
+    Timed eagerly: the route's shared workspace orders its users with an
+    event, which a HIP graph capture does not take."""
+    ls = LayerSet(torch, qw_amd, 3, 4, T_prefix, 1, LAYERS, causal=False, mode="turbo4")
+    ls.warm(warmup)
+    rounds = max(1, steps // LAYERS)
+    ms = ls.time_eager(rounds)
+    T = ls.T
+    ls.close()
+    return {"T": T, "layer_ms": ms, "rounds": rounds}
 
 
 def bench_block(torch, qw_amd, steps: int, bits: int, T_prefix: int, L: int, layers: int):
@@ -540,6 +556,11 @@ def main() -> int:
             "us_per_layer": round(c1["layer_ms"] * 1e3, 3),
             "us_attention": round(c1["attn_ms"] * 1e3, 3),
             "GB_s": round(c1["bytes_attn"] / (c1["attn_ms"] * 1e-3) / 1e9, 1)}
+        log("bench: Turbo4 decode (config-2 geometry)")
+        t4 = bench_turbo4_decode(torch, qw_amd, steps, args.warmup)
+        extra["turbo4_decode"] = {
+            "us_per_layer_eager": round(t4["layer_ms"] * 1e3, 2), "keys": t4["T"],
+            "route": "rotate q, expand rotated K/V to fp16, fp16 decode, rotate back"}
         line["extra"] = extra
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)

@@ -3,10 +3,12 @@
 A cache configured for a quantized mode prefills in fp16 and is quantized once,
 when the longest cache passes a threshold: at the end of the initial prefill,
 or before the first forward that would carry it past the threshold. The
-reference applies this to Turbo4; here the configured mode is an affine mode
-and the quantization is ``KVCache.demote_fp16_to_affine``. Caches other than
-attention KV caches (the linear-attention state of hybrid models) are passed
-through untouched.
+reference applies this to Turbo4; here it applies to Turbo4 and, in Turbo4's
+place, to the affine modes, and the quantization is
+``KVCache.demote_fp16_to_affine(configured)`` (for Turbo4 the reference's own
+``demote_fp16_to_turbo4``). Int8 and fp16 caches start in their own mode.
+Caches other than attention KV caches (the linear-attention state of hybrid
+models) are passed through untouched.
 """
 from __future__ import annotations
 
@@ -19,7 +21,7 @@ QUANTIZE_THRESHOLD_TOKENS = 2048
 
 
 def _is_quantized(mode: int) -> bool:
-    return mode in (KVCacheMode.AFFINE4, KVCacheMode.AFFINE8)
+    return mode in (KVCacheMode.TURBO4, KVCacheMode.AFFINE4, KVCacheMode.AFFINE8)
 
 
 def _attention_caches(caches: Iterable):

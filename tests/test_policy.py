@@ -111,7 +111,19 @@ def test_unpopulated_attention_caches_stay_fp16_when_others_demote():
     assert a.mode == A4 and b.mode == KVCacheMode.FP16
 
 
-@pytest.mark.parametrize("bad", [KVCacheMode.FP16])
+def test_turbo4_configuration_follows_the_reference_policy():
+    """The reference's own case (qwen3_5.rs:933-986): Turbo4 starts in fp16 and
+    is demoted to Turbo4 past the threshold; Int8 starts and stays Int8."""
+    T4 = KVCacheMode.TURBO4
+    assert policy.initial_attention_cache_mode(T4) == KVCacheMode.FP16
+    assert policy.initial_attention_cache_mode(KVCacheMode.INT8) == KVCacheMode.INT8
+    c = FakeAttentionCache(KVCacheMode.FP16, THR)
+    assert policy.prepare_attention_forward([c], T4, 1, True) == 1
+    assert c.mode == T4 and c.demotions == 1
+    assert policy.prepare_attention_forward([c], T4, 1, True) == 0
+
+
+@pytest.mark.parametrize("bad", [KVCacheMode.FP16, KVCacheMode.INT8])
 def test_demoting_into_a_non_quantized_mode_is_a_no_op_policy(bad):
     c = FakeAttentionCache(KVCacheMode.FP16, THR + 1)
     assert policy.finish_initial_attention_prefill([c], bad) == 0
