@@ -285,3 +285,34 @@ def test_turbo4_demote_and_rope_update():
         np.testing.assert_array_equal(_np(qa), _np(qr))
     for key, val in _snap(a).items():
         np.testing.assert_array_equal(val, _snap(b)[key], err_msg=key)
+
+
+def test_turbo4_workspace_growth_and_streams():
+    """The shared per-device workspace grows with the context and is ordered
+    across streams by its event: caches attended alternately on two streams
+    (with a growth in between) give the same rows as on one stream."""
+    import qw_amd
+
+    H, D, hq = 4, 256, 24
+    r = rng(51)
+    sizes = (300, 2500, 700, 4000)  # the last is first attended on a side stream (growth)
+    caches, qs, want = [], [], []
+    for T in sizes:
+        k, v = _kv(r, H, T, D)
+        c = qw_amd.KVCache("turbo4", H, D)
+        c.update(_gpu(k), _gpu(v))
+        caches.append(c)
+        qs.append(_gpu(r.standard_normal((hq, 1, D)).astype(np.float16)))
+    torch.cuda.synchronize()
+    for c, q in zip(caches[:3], qs[:3]):  # reference: one stream, in order
+        want.append(_np(c.attention(q, 1.0 / 16)))
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    outs = []
+    for rep in range(3):
+        for i, (c, q) in enumerate(zip(caches, qs)):
+            with torch.cuda.stream(s1 if (i + rep) % 2 == 0 else s2):
+                outs.append((i, c.attention(q, 1.0 / 16)))
+    torch.cuda.synchronize()
+    want.append(_np(caches[3].attention(qs[3], 1.0 / 16)))
+    for i, o in outs:
+        np.testing.assert_array_equal(_np(o), want[i])
