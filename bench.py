@@ -208,9 +208,11 @@ class LayerSet:
         self.torch.cuda.empty_cache()
 
 
-def bench_decode(torch, qw_amd, steps: int, warmup: int, bits: int = 4, T_prefix: int = 32768):
-    """Config 2 (bits 4, 32768 + 1) or config 1 (bits 8, 4095 + 1)."""
-    ls = LayerSet(torch, qw_amd, 2, bits, T_prefix, 1, LAYERS, causal=False)
+def bench_decode(torch, qw_amd, steps: int, warmup: int, bits: int = 4, T_prefix: int = 32768,
+                 mode=None):
+    """Config 2 (bits 4, 32768 + 1) or config 1 (bits 8, 4095 + 1); `mode`
+    overrides the cache mode (e.g. "int8", stored in the 8-bit layout)."""
+    ls = LayerSet(torch, qw_amd, 2, bits, T_prefix, 1, LAYERS, causal=False, mode=mode)
     ls.warm(warmup)
     # one attention-only round too, so the split-K workspace exists before capture
     ls.time_attention(1)
@@ -239,6 +241,91 @@ def bench_turbo4_decode(torch, qw_amd, steps: int, warmup: int, T_prefix: int = 
     T = ls.T
     ls.close()
     return {"T": T, "layer_ms": ms, "rounds": rounds}
+
+
+def bench_select(torch, qw_amd, steps: int, T: int = 131072):
+    """D-LSA K1 select at the served defaults (window 512, sink 4, top-k 4096,
+    top-p 1024, 8-key buckets, 64 buckets a block) for one decode row at
+    context T: synthetic N(0,1) bucket scores. Raw ABI calls with preallocated
+    outputs, graph-replayed."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    n_b = T // 8
+    scores = torch.randn((1, n_b), device=dev, generator=g, dtype=torch.float32)
+    members = torch.full((n_b, 16), -1, dtype=torch.int32, device=dev)
+    members[:, :8] = torch.arange(n_b * 8, dtype=torch.int32, device=dev).view(n_b, 8)
+    pos = torch.tensor([T - 1], dtype=torch.int32, device=dev)
+    window, sink, top_k, top_p, bpb = 512, 4, 4096, 1024, 64
+    W = top_k + window + sink
+    lists = torch.empty((1, W), dtype=torch.int32, device=dev)
+    lengths = torch.empty((1,), dtype=torch.int32, device=dev)
+    picked = torch.empty((1, top_p), dtype=torch.int32, device=dev)
+    status = torch.empty((1,), dtype=torch.int32, device=dev)
+    lib = qw_amd.lib()
+
+    def call():
+        st = torch.cuda.current_stream(dev).cuda_stream
+        rc = lib.qw_dlsa_select(scores.data_ptr(), n_b, members.data_ptr(), n_b, 16,
+                                pos.data_ptr(), 1, n_b, window, sink, top_k, top_p, bpb, 0,
+                                lists.data_ptr(), lengths.data_ptr(), picked.data_ptr(),
+                                status.data_ptr(), st)
+        if rc:
+            raise qw_amd.QwError(rc, lib.qw_last_error().decode())
+
+    for _ in range(5):
+        call()
+    torch.cuda.synchronize()
+    ms = graph_time(torch, lambda: [call() for _ in range(LAYERS)], max(1, steps // LAYERS),
+                    LAYERS)
+    return {"ms": ms, "buckets": n_b, "list_len": int(lengths.item()), "width": W}
+
+
+def bench_rope(torch, qw_amd, steps: int, L: int = 2048):
+    """Fused q/k RoPE: the standalone op over a 2048-token QKV chunk (bytes:
+    the chunk read once, q/k/v written once), and the RoPE-append of one
+    decode token into a 4-bit cache (append then trim, graph-replayed)."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(6)
+    W = (HQ + 2 * HKV) * D
+    qkv = torch.randn((1, L, W), device=dev, generator=g).half()
+    q = torch.empty((1, HQ, L, D), dtype=torch.float16, device=dev)
+    k = torch.empty((1, HKV, L, D), dtype=torch.float16, device=dev)
+    v = torch.empty_like(k)
+    lib = qw_amd.lib()
+
+    def chunk():
+        st = torch.cuda.current_stream(dev).cuda_stream
+        rc = lib.qw_fused_rope_qk_append(qkv.data_ptr(), 1, L, HQ, HKV, D, D, 1e7, 1.0, 0, 1000,
+                                         0, q.data_ptr(), k.data_ptr(), v.data_ptr(), st)
+        if rc:
+            raise qw_amd.QwError(rc, lib.qw_last_error().decode())
+
+    chunk()
+    torch.cuda.synchronize()
+    chunk_ms = graph_time(torch, lambda: [chunk() for _ in range(LAYERS)], max(1, steps // LAYERS),
+                          LAYERS)
+    cache = qw_amd.KVCache("affine4", HKV, D, capacity=4096)
+    cache.update(torch.randn((HKV, 4000, D), device=dev, generator=g).half(),
+                 torch.randn((HKV, 4000, D), device=dev, generator=g).half())
+    tok = qkv[:, :1].contiguous()
+    q1 = torch.empty((HQ, 1, D), dtype=torch.float16, device=dev)
+
+    def one():
+        st = torch.cuda.current_stream(dev).cuda_stream
+        rc = lib.qw_kv_rope_update(cache._h, tok.data_ptr(), HQ, 1, D, 0, 1e7, 1.0, 4000,
+                                   q1.data_ptr(), st)
+        if rc:
+            raise qw_amd.QwError(rc, lib.qw_last_error().decode())
+        cache.trim(1)
+
+    one()
+    torch.cuda.synchronize()
+    one_ms = graph_time(torch, lambda: [one() for _ in range(LAYERS)], max(1, steps // LAYERS),
+                        LAYERS)
+    cache.close()
+    return {"chunk_ms": chunk_ms, "chunk_bytes": 2 * L * W * 2, "token_ms": one_ms}
 
 
 def bench_block(torch, qw_amd, steps: int, bits: int, T_prefix: int, L: int, layers: int):
@@ -556,6 +643,23 @@ def main() -> int:
             "us_per_layer": round(c1["layer_ms"] * 1e3, 3),
             "us_attention": round(c1["attn_ms"] * 1e3, 3),
             "GB_s": round(c1["bytes_attn"] / (c1["attn_ms"] * 1e-3) / 1e9, 1)}
+        log("bench: Int8 decode (config-2 geometry)")
+        i8 = bench_decode(torch, qw_amd, steps, args.warmup, bits=8, T_prefix=32768, mode="int8")
+        extra["int8_decode"] = {
+            "us_per_layer": round(i8["layer_ms"] * 1e3, 2),
+            "us_attention": round(i8["attn_ms"] * 1e3, 2),
+            "GB_s": round(i8["bytes_attn"] / (i8["attn_ms"] * 1e-3) / 1e9, 1)}
+        log("bench: D-LSA K1 select")
+        k1 = bench_select(torch, qw_amd, steps)
+        extra["dlsa_k1_select"] = {
+            "us_per_row": round(k1["ms"] * 1e3, 2), "buckets": k1["buckets"],
+            "list_width": k1["width"], "list_len": k1["list_len"]}
+        log("bench: fused q/k RoPE")
+        rp = bench_rope(torch, qw_amd, steps)
+        extra["rope"] = {
+            "us_chunk_2048": round(rp["chunk_ms"] * 1e3, 2),
+            "GB_s_chunk": round(rp["chunk_bytes"] / (rp["chunk_ms"] * 1e-3) / 1e9, 1),
+            "us_rope_append_1_token": round(rp["token_ms"] * 1e3, 2)}
         log("bench: Turbo4 decode (config-2 geometry)")
         t4 = bench_turbo4_decode(torch, qw_amd, steps, args.warmup)
         extra["turbo4_decode"] = {

@@ -13,14 +13,19 @@
 // [0, min(sink, window_start, p + 1)), -1 padded.
 //
 // One workgroup a row. The rank of column i is the 64-bit key
-// (rank32(score) << 32) | i, unique, smaller = better. The top min(top_p, v)
+// (rank32(score) << 32) | i, unique, smaller = better. The row's rank32 values
+// are staged into LDS once (when they fit, rank_cap of them) so that every
+// later pass reads LDS rather than global memory. The top min(top_p, v)
 // keys are found by a radix select on rank32 (4 passes of 8 bits over the
-// row's scores, histograms in LDS); the keys strictly better than the
-// threshold value are all kept, and of those equal to it the lowest indices
-// (an index-ordered pass, run only when the threshold value is shared by more
-// keys than remain to be taken). The kept keys (<= 2048) are sorted in LDS
-// (bitonic), and a block prefix scan over the picked buckets' member counts
-// places every member of the expansion without a serial walk.
+// row, one LDS histogram a wave, summed per pass); the keys strictly better
+// than the threshold value are all kept, and of those equal to it the lowest
+// indices (an index-ordered pass, run only when the threshold value is shared
+// by more keys than remain to be taken). The kept keys (<= 2048) are sorted
+// bitonically: one key a thread in registers when they fit the workgroup
+// (strides below 64 by wave shuffles, longer ones through LDS), else in LDS.
+// A block prefix scan over the picked buckets' member counts places every
+// member of the expansion without a serial walk; with one pick a thread and
+// small, aligned member rows the members are read once into registers.
 #include "kv_cache.hpp"
 
 namespace qw {
@@ -41,6 +46,8 @@ struct SelectArgs {
     int32_t* lengths;         // [R]
     int32_t* picked;          // [R][top_p]
     int32_t* status;          // [R]
+    int rank_cap;             // rank32 values the dynamic LDS holds (0: none)
+    int vec_members;          // members 16-byte aligned, cap a multiple of 4, <= 16
 };
 
 // Monotone key: smaller = better (score descending), -0 == +0, every NaN
@@ -74,12 +81,23 @@ __device__ __forceinline__ int block_exclusive_scan(int x, int* sm, int& tot) {
     return incl - x;
 }
 
+// Histogram increment of `digit` for the lanes with `take`, aggregated over
+// the wave: one LDS atomic per distinct digit (the first radix pass sees few
+// distinct top bytes, and per-lane atomics on them would serialize).
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int mask) {
+    const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)x, mask);
+    const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(x >> 32), mask);
+    return ((uint64_t)hi << 32) | lo;
+}
+
 __global__ __launch_bounds__(1024) void dlsa_select_kernel(SelectArgs a) {
     __shared__ uint64_t sel[kSelectMax];
     __shared__ int scan[2 * 1024];
     __shared__ int cnt[kSelectMax];
     __shared__ uint32_t hist[256];
+    __shared__ uint32_t whist[16][256];  // one radix histogram a wave
     __shared__ int sh_int[4];
+    extern __shared__ uint32_t rank_lds[];  // [rank_cap] rank32 of the row
     const int r = blockIdx.x;
     const int t = threadIdx.x, T = blockDim.x;
     const int p = a.positions[r];
@@ -91,25 +109,63 @@ __global__ __launch_bounds__(1024) void dlsa_select_kernel(SelectArgs a) {
     }
     const float* row = a.scores + (int64_t)r * a.stride;
     const int n_sel = min(a.top_p, v);
+    const int wave = t >> 6, n_waves = T >> 6;
+
+    // ---- the row's rank32 values into LDS (one global pass, four loads in
+    // flight a thread), with the NaN check
+    const bool cached = v <= a.rank_cap;
+    if (t == 0) sh_int[0] = 0;
+    if (cached) {
+        bool nan = false;
+        int i = t;
+        for (; i + 3 * T < v; i += 4 * T) {
+            float f[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) f[j] = row[i + j * T];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                nan |= f[j] != f[j];
+                rank_lds[i + j * T] = rank32(f[j]);
+            }
+        }
+        for (; i < v; i += T) {
+            const float f = row[i];
+            nan |= f != f;
+            rank_lds[i] = rank32(f);
+        }
+        __syncthreads();
+        if (nan && n_sel > 0) sh_int[0] = 1;  // (no pick, no NaN status, as below)
+    }
+    auto rank_at = [&](int i) -> uint32_t { return cached ? rank_lds[i] : rank32(row[i]); };
 
     // ---- threshold: the n_sel-th smallest rank32 (radix select, 8 bits a pass)
     uint32_t prefix = 0, pmask = 0;
     int k = n_sel;  // rank of the wanted key among those matching `prefix`
     int below = 0;  // keys with rank32 strictly below the final threshold
-    if (t == 0) sh_int[0] = 0;
     __syncthreads();
     if (n_sel > 0 && n_sel < v) {
         for (int shift = 24; shift >= 0; shift -= 8) {
-            for (int i = t; i < 256; i += T) hist[i] = 0;
+            for (int i = t; i < 16 * 256; i += T) (&whist[0][0])[i] = 0;
             __syncthreads();
             bool nan = false;
             for (int i = t; i < v; i += T) {
-                const float f = row[i];
-                nan |= f != f;
-                const uint32_t key = rank32(f);
-                if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 0xFF], 1u);
+                uint32_t key;
+                if (cached) {
+                    key = rank_lds[i];
+                } else {
+                    const float f = row[i];
+                    nan |= f != f;
+                    key = rank32(f);
+                }
+                if ((key & pmask) == prefix) atomicAdd(&whist[wave][(key >> shift) & 0xFF], 1u);
             }
             if (nan) sh_int[0] = 1;
+            __syncthreads();
+            for (int i = t; i < 256; i += T) {
+                uint32_t sum = 0;
+                for (int w = 0; w < n_waves; w++) sum += whist[w][i];
+                hist[i] = sum;
+            }
             __syncthreads();
             // the digit whose cumulative count reaches k (one wave scans)
             if (t < 64) {
@@ -142,7 +198,7 @@ __global__ __launch_bounds__(1024) void dlsa_select_kernel(SelectArgs a) {
             pmask |= 0xFFu << shift;
             __syncthreads();
         }
-    } else if (n_sel > 0) {
+    } else if (n_sel > 0 && !cached) {
         // every visible bucket is picked: just the NaN check
         bool nan = false;
         for (int i = t; i < v; i += T) nan |= row[i] != row[i];
@@ -157,29 +213,26 @@ __global__ __launch_bounds__(1024) void dlsa_select_kernel(SelectArgs a) {
     if (t == 0) sh_int[3] = 0;
     __syncthreads();
     if (n_sel == v) {
-        for (int i = t; i < v; i += T) sel[i] = ((uint64_t)rank32(row[i]) << 32) | (uint32_t)i;
+        for (int i = t; i < v; i += T) sel[i] = ((uint64_t)rank_at(i) << 32) | (uint32_t)i;
     } else if (n_sel > 0) {
         int eq_local = 0;
         for (int i = t; i < v; i += T) {
-            const uint32_t key = rank32(row[i]);
-            if (key < thr) {
-                sel[atomicAdd(&sh_int[3], 1)] = ((uint64_t)key << 32) | (uint32_t)i;
-            } else if (key == thr) {
-                eq_local++;
-            }
+            const uint32_t key = rank_at(i);
+            if (key < thr) sel[atomicAdd(&sh_int[3], 1)] = ((uint64_t)key << 32) | (uint32_t)i;
+            eq_local += key == thr;
         }
         int n_eq;
         (void)block_exclusive_scan(eq_local, scan, n_eq);
         if (n_eq == need) {
             for (int i = t; i < v; i += T)
-                if (rank32(row[i]) == thr)
+                if (rank_at(i) == thr)
                     sel[atomicAdd(&sh_int[3], 1)] = ((uint64_t)thr << 32) | (uint32_t)i;
         } else {
             // ties across the threshold: the `need` lowest indices among them
             int taken = 0;
             for (int base = 0; base < v && taken < need; base += T) {
                 const int i = base + t;
-                const int eq = i < v && rank32(row[i]) == thr ? 1 : 0;
+                const int eq = i < v && rank_at(i) == thr ? 1 : 0;
                 int n_blk;
                 const int pos = taken + block_exclusive_scan(eq, scan, n_blk);
                 if (eq && pos < need) sel[below + pos] = ((uint64_t)thr << 32) | (uint32_t)i;
@@ -192,7 +245,30 @@ __global__ __launch_bounds__(1024) void dlsa_select_kernel(SelectArgs a) {
     // ---- sort the kept keys (bitonic over the next power of two)
     int n_pad = 1;
     while (n_pad < n_sel) n_pad <<= 1;
-    if (n_sel > 0) {
+    if (n_sel > 0 && n_pad <= T) {
+        // one key a thread: strides below 64 exchange within the wave by
+        // shuffles, the longer ones through LDS (two barriers a stage)
+        uint64_t x = t < n_sel ? sel[t] : ~0ull;
+        for (int size = 2; size <= n_pad; size <<= 1) {
+            for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                uint64_t y;
+                if (stride >= 64) {
+                    __syncthreads();
+                    sel[t] = x;
+                    __syncthreads();
+                    y = sel[t ^ stride];
+                } else {
+                    y = shfl_xor_u64(x, stride);
+                }
+                const bool keep_min = ((t & stride) == 0) == ((t & size) == 0);
+                const uint64_t mn = x < y ? x : y, mx = x < y ? y : x;
+                x = keep_min ? mn : mx;
+            }
+        }
+        __syncthreads();
+        sel[t] = x;
+        __syncthreads();
+    } else if (n_sel > 0) {
         for (int i = n_sel + t; i < n_pad; i += T) sel[i] = ~0ull;
         __syncthreads();
         for (int size = 2; size <= n_pad; size <<= 1) {
@@ -221,30 +297,63 @@ __global__ __launch_bounds__(1024) void dlsa_select_kernel(SelectArgs a) {
     const int lo = a.sink, hi = ws;
     const int width = a.top_k + a.window + a.sink;
     int32_t* lrow = a.lists + (int64_t)r * width;
-    // counts per picked bucket, in pick order, then their exclusive prefix
-    for (int i = t; i < n_sel; i += T) {
-        const int32_t* mb = a.members + (int64_t)(uint32_t)sel[i] * a.cap;
-        int c = 0;
-        for (int j = 0; j < a.cap; j++) {
-            const int x = mb[j];
-            c += x >= lo && x < hi && x >= 0;
-        }
-        cnt[i] = c;
-    }
-    __syncthreads();
-    // chunked scan: thread t owns picks [t*per, (t+1)*per)
-    const int per = (n_sel + T - 1) / T;
-    int chunk = 0;
-    for (int i = t * per; i < min(n_sel, (t + 1) * per); i++) chunk += cnt[i];
     int total;
-    int off = block_exclusive_scan(chunk, scan, total);
-    for (int i = t * per; i < min(n_sel, (t + 1) * per); i++) {
-        const int32_t* mb = a.members + (int64_t)(uint32_t)sel[i] * a.cap;
-        for (int j = 0; j < a.cap; j++) {
-            const int x = mb[j];
-            if (x >= lo && x < hi && x >= 0) {
-                if (off < a.top_k) lrow[off] = x;
-                off++;
+    if (a.vec_members && n_sel <= T) {
+        // one pick a thread, its members read once (16-byte loads) and kept in
+        // registers between the count and the write
+        int32_t mem[16];
+        int c = 0;
+        if (t < n_sel) {
+            const int4* mb4 = (const int4*)(a.members + (int64_t)(uint32_t)sel[t] * a.cap);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                if (4 * q < a.cap) {
+                    const int4 w = mb4[q];
+                    mem[4 * q] = w.x;
+                    mem[4 * q + 1] = w.y;
+                    mem[4 * q + 2] = w.z;
+                    mem[4 * q + 3] = w.w;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 16; j++)
+                if (j < a.cap) c += mem[j] >= lo && mem[j] < hi && mem[j] >= 0;
+        }
+        int off = block_exclusive_scan(c, scan, total);
+        if (t < n_sel) {
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                if (j < a.cap && mem[j] >= lo && mem[j] < hi && mem[j] >= 0) {
+                    if (off < a.top_k) lrow[off] = mem[j];
+                    off++;
+                }
+            }
+        }
+    } else {
+        // counts per picked bucket, in pick order, then their exclusive prefix
+        for (int i = t; i < n_sel; i += T) {
+            const int32_t* mb = a.members + (int64_t)(uint32_t)sel[i] * a.cap;
+            int c = 0;
+            for (int j = 0; j < a.cap; j++) {
+                const int x = mb[j];
+                c += x >= lo && x < hi && x >= 0;
+            }
+            cnt[i] = c;
+        }
+        __syncthreads();
+        // chunked scan: thread t owns picks [t*per, (t+1)*per)
+        const int per = (n_sel + T - 1) / T;
+        int chunk = 0;
+        for (int i = t * per; i < min(n_sel, (t + 1) * per); i++) chunk += cnt[i];
+        int off = block_exclusive_scan(chunk, scan, total);
+        for (int i = t * per; i < min(n_sel, (t + 1) * per); i++) {
+            const int32_t* mb = a.members + (int64_t)(uint32_t)sel[i] * a.cap;
+            for (int j = 0; j < a.cap; j++) {
+                const int x = mb[j];
+                if (x >= lo && x < hi && x >= 0) {
+                    if (off < a.top_k) lrow[off] = x;
+                    off++;
+                }
             }
         }
     }
@@ -300,8 +409,22 @@ int dlsa_select(const float* scores, int64_t stride, const int32_t* members, int
     a.lengths = lengths;
     a.picked = picked;
     a.status = status;
-    const int T = threads ? threads : 256;
-    hipLaunchKernelGGL(dlsa_select_kernel, dim3(n_rows), dim3(T), 0, stream, a);
+    // Rows of up to kRankCap visible buckets keep their rank32 values in LDS
+    // (96 KB beside the ~49 KB of static arrays); longer rows read global
+    // memory in every pass.
+    constexpr int kRankCap = 24576;
+    a.rank_cap = kRankCap;
+    a.vec_members = bucket_cap <= 16 && bucket_cap % 4 == 0 &&
+                    ((uintptr_t)members & 15) == 0;
+    const size_t shmem = (size_t)kRankCap * sizeof(uint32_t);
+    static bool attr_set = false;
+    if (!attr_set) {
+        QW_HIP_CHECK(hipFuncSetAttribute((const void*)dlsa_select_kernel,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem));
+        attr_set = true;
+    }
+    const int T = threads ? threads : 1024;
+    hipLaunchKernelGGL(dlsa_select_kernel, dim3(n_rows), dim3(T), shmem, stream, a);
     QW_HIP_CHECK(hipGetLastError());
     return QW_OK;
 }
