@@ -100,12 +100,128 @@ __global__ __launch_bounds__(256) void rope_qkv_kernel(RopeArgs a) {
     }
 }
 
+// The same op four pairs a thread, for D and rope_dims multiples of 8 (a
+// group of four pairs is then wholly rotated or wholly tail): the dims of a
+// group are one 16-byte run (traditional pairs, v, the tail) or two 8-byte
+// runs (half-split pairs p and p + R/2), so a wave moves 0.5-1 KB per access.
+// Each element's value is the scalar kernel's (same rope_pair).
+// One workgroup a token row (grid.x = b * seq + t): the row's cos/sin table
+// (one entry a rotated pair, shared by every head) goes to LDS first, then
+// the threads walk the row's (slot, group) units, 32-bit index math.
+constexpr int kRopeMaxPairs = 256;  // rope_dims / 2 the vector kernel takes
+
+__global__ __launch_bounds__(256) void rope_qkv_vec_kernel(RopeArgs a) {
+    const int groups = a.D >> 3;       // 4-pair groups a head
+    const int rgroups = a.rope_dims >> 3;
+    const int rhalf = a.rope_dims >> 1;
+    const int slots = a.hq + 2 * a.hkv;
+    const int nsl = a.slot_end - a.slot_begin;
+    const int64_t row = blockIdx.x;  // b * seq + t
+    __shared__ float2 cs[kRopeMaxPairs];
+    {
+        const int t = (int)(row % a.seq);
+        for (int p = threadIdx.x; p < rhalf; p += blockDim.x) {
+            float c, sn;
+            rope_cs(p, rhalf, a.log2_base, a.scale, t + a.positions_base, c, sn);
+            cs[p] = float2{c, sn};
+        }
+    }
+    __syncthreads();
+    for (int u = threadIdx.x; u < nsl * groups; u += blockDim.x) {
+        const int gi = u % groups;
+        const int slot = a.slot_begin + u / groups;
+        const int b = (int)(row / a.seq), t = (int)(row % a.seq);
+        const f16* in = a.qkv + row * ((int64_t)slots * a.D) + (int64_t)slot * a.D;
+        int kind, h;  // 0 q, 1 k, 2 v
+        if (slot < a.hq) {
+            kind = 0;
+            h = slot;
+        } else if (slot < a.hq + a.hkv) {
+            kind = 1;
+            h = slot - a.hq;
+        } else {
+            kind = 2;
+            h = slot - a.hq - a.hkv;
+        }
+        int64_t ob;
+        f16* out;
+        if (kind == 0) {
+            ob = (((int64_t)b * a.hq + h) * a.seq + t) * a.D;
+            out = a.q_out;
+        } else {
+            ob = a.dest_layout == 0 ? (((int64_t)b * a.hkv + h) * a.seq + t) * a.D
+                                    : (((int64_t)b * a.seq + t) * a.hkv + h) * a.D;
+            out = kind == 1 ? a.k_out : a.v_out;
+        }
+        // Groups [0, R/8) are rotated, groups [R/8, D/8) are the tail, dims
+        // 8 gi .. 8 gi + 7 (8 (R/8) = R). A rotated group holds pairs 4 gi ..
+        // 4 gi + 3: dims 8 gi .. + 7 when traditional, else dims 4 gi .. + 3
+        // and their partners 4 gi + R/2 .. + 3.
+        if (kind == 2 || gi >= rgroups) {
+            *(u32x4*)(out + ob + 8 * gi) = *(const u32x4*)(in + 8 * gi);
+        } else if (a.traditional) {
+            const u32x4 w = *(const u32x4*)(in + 8 * gi);
+            u32x4 o;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const half2v x = h2(w[j]);
+                float r1, r2;
+                const float2 c2 = cs[4 * gi + j];
+                rope_rot((float)x.x, (float)x.y, c2.x, c2.y, r1, r2);
+                half2v y;
+                y.x = (f16)r1;
+                y.y = (f16)r2;
+                o[j] = __builtin_bit_cast(uint32_t, y);
+            }
+            *(u32x4*)(out + ob + 8 * gi) = o;
+        } else {
+            const int pg = gi;  // pairs 4 pg .. 4 pg + 3
+            const uint2 w1 = *(const uint2*)(in + 4 * pg);
+            const uint2 w2 = *(const uint2*)(in + 4 * pg + rhalf);
+            const half2v a1[2] = {h2(w1.x), h2(w1.y)}, a2[2] = {h2(w2.x), h2(w2.y)};
+            half2v o1[2], o2[2];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float x1 = (float)(j & 1 ? a1[j >> 1].y : a1[j >> 1].x);
+                const float x2 = (float)(j & 1 ? a2[j >> 1].y : a2[j >> 1].x);
+                float r1, r2;
+                const float2 c2 = cs[4 * pg + j];
+                rope_rot(x1, x2, c2.x, c2.y, r1, r2);
+                if (j & 1) {
+                    o1[j >> 1].y = (f16)r1;
+                    o2[j >> 1].y = (f16)r2;
+                } else {
+                    o1[j >> 1].x = (f16)r1;
+                    o2[j >> 1].x = (f16)r2;
+                }
+            }
+            *(uint2*)(out + ob + 4 * pg) =
+                uint2{__builtin_bit_cast(uint32_t, o1[0]), __builtin_bit_cast(uint32_t, o1[1])};
+            *(uint2*)(out + ob + 4 * pg + rhalf) =
+                uint2{__builtin_bit_cast(uint32_t, o2[0]), __builtin_bit_cast(uint32_t, o2[1])};
+        }
+    }
+}
+
 static int rope_launch(const RopeArgs& a, hipStream_t stream) {
-    const int64_t total = (int64_t)a.batch * a.seq * (a.slot_end - a.slot_begin) * (a.D / 2);
-    if (total == 0) return QW_OK;
-    // Grid-stride loop: enough workgroups to fill the chip several times over.
-    const int64_t blocks = std::min<int64_t>((total + 255) / 256, 256 * 32);
-    hipLaunchKernelGGL(rope_qkv_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+    const int64_t rows = (int64_t)a.batch * a.seq * (a.slot_end - a.slot_begin);
+    if (rows == 0) return QW_OK;
+    // the vector form needs 16-byte aligned buffers (the ABI takes any pointers)
+    auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    const bool vec = a.D % 8 == 0 && a.rope_dims % 8 == 0 && a.rope_dims / 2 <= kRopeMaxPairs &&
+                     al16(a.qkv) && al16(a.q_out) && al16(a.k_out) && al16(a.v_out);
+    if (vec) {
+        // one workgroup a token row b * seq + t
+        const int64_t tokens = (int64_t)a.batch * a.seq;
+        QW_REQUIRE(tokens <= 0x7FFFFFFF, QW_ERR_INVALID_ARGUMENT,
+                   "fused_rope_qk_append: too many rows");
+        hipLaunchKernelGGL(rope_qkv_vec_kernel, dim3((unsigned)tokens), dim3(256), 0, stream, a);
+    } else {
+        // Grid-stride loop: enough workgroups to fill the chip several times over.
+        const int64_t total = rows * (a.D / 2);
+        const int64_t blocks = std::min<int64_t>((total + 255) / 256, 256 * 32);
+        hipLaunchKernelGGL(rope_qkv_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+    }
     QW_HIP_CHECK(hipGetLastError());
     return QW_OK;
 }

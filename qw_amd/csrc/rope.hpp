@@ -16,14 +16,21 @@
 
 namespace qw {
 
-// The two products of each output are combined with one explicit fma so the
-// rounding does not depend on how the compiler contracts a given call site.
-__device__ __forceinline__ void rope_pair(float x1, float x2, int p, int rhalf, float log2_base,
-                                          float scale, int pos, float& r1, float& r2) {
+// cos and sin of pair p's angle at `pos`.
+__device__ __forceinline__ void rope_cs(int p, int rhalf, float log2_base, float scale, int pos,
+                                        float& c, float& s) {
     const float dd = (float)p / (float)rhalf;
     const float inv_freq = exp2f(-dd * log2_base);
     const float theta = (scale * (float)pos) * inv_freq;
-    const float c = cosf(theta), s = sinf(theta);
+    c = cosf(theta);
+    s = sinf(theta);
+}
+
+// The rotation of one pair by (c, s). The two products of each output are
+// combined with one explicit fma so the rounding does not depend on how the
+// compiler contracts a given call site.
+__device__ __forceinline__ void rope_rot(float x1, float x2, float c, float s, float& r1,
+                                         float& r2) {
     r1 = __builtin_fmaf(x1, c, -(x2 * s));
     r2 = __builtin_fmaf(x1, s, x2 * c);
     // The results are rounded to fp32 here, as the reference's float
@@ -32,6 +39,13 @@ __device__ __forceinline__ void rope_pair(float x1, float x2, int p, int rhalf, 
     // fma that rounds once, which differs from fp32-then-fp16 in about one
     // element of 10^4 and would make call sites disagree.
     asm volatile("" : "+v"(r1), "+v"(r2));
+}
+
+__device__ __forceinline__ void rope_pair(float x1, float x2, int p, int rhalf, float log2_base,
+                                          float scale, int pos, float& r1, float& r2) {
+    float c, s;
+    rope_cs(p, rhalf, log2_base, scale, pos, c, s);
+    rope_rot(x1, x2, c, s, r1, r2);
 }
 
 // Indices of the pair that holds dim d (d < rope_dims): p, the partner dim,
