@@ -33,6 +33,7 @@ namespace qw {
 namespace {
 
 constexpr int kSelectMax = 2048;  // most buckets a row may pick (top_p)
+constexpr int kKeysPerThread = 16;  // rank keys a thread keeps in registers
 
 struct SelectArgs {
     const float* scores;      // [R][stride]
@@ -111,11 +112,28 @@ __global__ __launch_bounds__(1024) void dlsa_select_kernel(SelectArgs a) {
     const int n_sel = min(a.top_p, v);
     const int wave = t >> 6, n_waves = T >> 6;
 
-    // ---- the row's rank32 values into LDS (one global pass, four loads in
-    // flight a thread), with the NaN check
+    // ---- the row's rank32 values into LDS (one global pass), with the NaN
+    // check; rows of up to kKeysPerThread * T also keep each thread's keys
+    // (columns t, t + T, ...) in registers, so the radix passes and the
+    // compaction load nothing.
     const bool cached = v <= a.rank_cap;
+    const bool in_regs = v <= kKeysPerThread * T;
+    uint32_t kr[kKeysPerThread];
     if (t == 0) sh_int[0] = 0;
-    if (cached) {
+    if (in_regs) {
+        bool nan = false;
+        float f[kKeysPerThread];
+#pragma unroll
+        for (int j = 0; j < kKeysPerThread; j++) f[j] = t + j * T < v ? row[t + j * T] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < kKeysPerThread; j++) {
+            nan |= f[j] != f[j];
+            kr[j] = rank32(f[j]);
+            if (t + j * T < v) rank_lds[t + j * T] = kr[j];
+        }
+        __syncthreads();
+        if (nan && n_sel > 0) sh_int[0] = 1;  // (no pick, no NaN status, as below)
+    } else if (cached) {
         bool nan = false;
         int i = t;
         for (; i + 3 * T < v; i += 4 * T) {
@@ -148,16 +166,24 @@ __global__ __launch_bounds__(1024) void dlsa_select_kernel(SelectArgs a) {
             for (int i = t; i < 16 * 256; i += T) (&whist[0][0])[i] = 0;
             __syncthreads();
             bool nan = false;
-            for (int i = t; i < v; i += T) {
-                uint32_t key;
-                if (cached) {
-                    key = rank_lds[i];
-                } else {
-                    const float f = row[i];
-                    nan |= f != f;
-                    key = rank32(f);
+            if (in_regs) {
+#pragma unroll
+                for (int j = 0; j < kKeysPerThread; j++)
+                    if (t + j * T < v && (kr[j] & pmask) == prefix)
+                        atomicAdd(&whist[wave][(kr[j] >> shift) & 0xFF], 1u);
+            } else {
+                for (int i = t; i < v; i += T) {
+                    uint32_t key;
+                    if (cached) {
+                        key = rank_lds[i];
+                    } else {
+                        const float f = row[i];
+                        nan |= f != f;
+                        key = rank32(f);
+                    }
+                    if ((key & pmask) == prefix)
+                        atomicAdd(&whist[wave][(key >> shift) & 0xFF], 1u);
                 }
-                if ((key & pmask) == prefix) atomicAdd(&whist[wave][(key >> shift) & 0xFF], 1u);
             }
             if (nan) sh_int[0] = 1;
             __syncthreads();
@@ -215,19 +241,49 @@ __global__ __launch_bounds__(1024) void dlsa_select_kernel(SelectArgs a) {
     if (n_sel == v) {
         for (int i = t; i < v; i += T) sel[i] = ((uint64_t)rank_at(i) << 32) | (uint32_t)i;
     } else if (n_sel > 0) {
-        int eq_local = 0;
-        for (int i = t; i < v; i += T) {
-            const uint32_t key = rank_at(i);
-            if (key < thr) sel[atomicAdd(&sh_int[3], 1)] = ((uint64_t)key << 32) | (uint32_t)i;
-            eq_local += key == thr;
-        }
-        int n_eq;
-        (void)block_exclusive_scan(eq_local, scan, n_eq);
-        if (n_eq == need) {
-            for (int i = t; i < v; i += T)
-                if (rank_at(i) == thr)
-                    sel[atomicAdd(&sh_int[3], 1)] = ((uint64_t)thr << 32) | (uint32_t)i;
+        bool eq_placed;  // (workgroup-uniform)
+        if (in_regs) {
+            // keys below thr and equal to it, counted per thread and placed by
+            // one block scan of both counts packed in an int (each <= 2^14)
+            int c_lt = 0, c_eq = 0;
+#pragma unroll
+            for (int j = 0; j < kKeysPerThread; j++) {
+                if (t + j * T < v) {
+                    c_lt += kr[j] < thr;
+                    c_eq += kr[j] == thr;
+                }
+            }
+            int tot;
+            const int ex = block_exclusive_scan(c_lt | (c_eq << 16), scan, tot);
+            eq_placed = (tot >> 16) == need;
+            int o_lt = ex & 0xFFFF, o_eq = below + (ex >> 16);
+#pragma unroll
+            for (int j = 0; j < kKeysPerThread; j++) {
+                const int i = t + j * T;
+                if (i < v) {
+                    if (kr[j] < thr)
+                        sel[o_lt++] = ((uint64_t)kr[j] << 32) | (uint32_t)i;
+                    else if (eq_placed && kr[j] == thr)
+                        sel[o_eq++] = ((uint64_t)thr << 32) | (uint32_t)i;
+                }
+            }
         } else {
+            int eq_local = 0;
+            for (int i = t; i < v; i += T) {
+                const uint32_t key = rank_at(i);
+                if (key < thr) sel[atomicAdd(&sh_int[3], 1)] = ((uint64_t)key << 32) | (uint32_t)i;
+                eq_local += key == thr;
+            }
+            int n_eq;
+            (void)block_exclusive_scan(eq_local, scan, n_eq);
+            eq_placed = n_eq == need;
+            if (eq_placed) {
+                for (int i = t; i < v; i += T)
+                    if (rank_at(i) == thr)
+                        sel[atomicAdd(&sh_int[3], 1)] = ((uint64_t)thr << 32) | (uint32_t)i;
+            }
+        }
+        if (!eq_placed) {
             // ties across the threshold: the `need` lowest indices among them
             int taken = 0;
             for (int base = 0; base < v && taken < need; base += T) {
