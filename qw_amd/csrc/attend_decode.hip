@@ -765,8 +765,14 @@ struct MergeAppendArgs {
     f16* out;               // [hq][1][D]
 };
 
-template <int BITS, int D, int PER>
+// I8: the Int8 mode (cache.rs:270-305): the new K and V rows are quantized
+// per token, scale f16(absmax / 127) (1 for an all-zero row), codes
+// clip(rint(f16(x / scale))) stored plus 128 in the 8-bit layout with the
+// scale in every group slot and bias 0, as the append kernel stores them; the
+// new key is attended as f16(code * scale).
+template <int BITS, int D, int PER, bool I8 = false>
 __global__ __launch_bounds__(256) void merge_append_kernel(MergeAppendArgs a) {
+    static_assert(!I8 || BITS == 8, "Int8 rows use the 8-bit layout");
     constexpr int NG = D / 64;
     const int row = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -801,13 +807,46 @@ __global__ __launch_bounds__(256) void merge_append_kernel(MergeAppendArgs a) {
     const float kx = kdim ? (float)a.k_new[(int64_t)h * D + threadIdx.x] : 0.0f;
     const float qx = kdim ? (float)a.q[(int64_t)qh * D + threadIdx.x] : 0.0f;
     const float vx = (float)a.v_new[(int64_t)h * D + d];
+    // Int8: the whole V row too (thread = dim), for its absmax
+    const float vrow = I8 && kdim ? (float)a.v_new[(int64_t)h * D + threadIdx.x] : 0.0f;
 
     // ---- new key: wave w < NG quantizes K group w and forms its share of
     // q' . k (q' = f16(f16(scale) * q), as MLX scales q)
     __shared__ float sm_s[4];
     float kcode = 0.0f;
     f16 ks = (f16)0.0f, kb = (f16)0.0f;
-    if (wave < NG) {
+    f16 vs = (f16)0.0f, vbias = (f16)0.0f;
+    float vcode = 0.0f, vd = 0.0f;
+    if constexpr (I8) {
+        // row absmax of K and V over the workgroup's four waves
+        __shared__ float sm_am[2][4];
+        const float ka = wave_reduce(fabsf(kx), OpMax()), va = wave_reduce(fabsf(vrow), OpMax());
+        if (lane == 0) {
+            sm_am[0][wave] = ka;
+            sm_am[1][wave] = va;
+        }
+        __syncthreads();
+        auto scale_of = [](float am) {
+            f16 sc = (f16)(am / 127.0f);
+            if ((float)sc == 0.0f) sc = (f16)1.0f;
+            return sc;
+        };
+        ks = scale_of(fmaxf(fmaxf(sm_am[0][0], sm_am[0][1]), fmaxf(sm_am[0][2], sm_am[0][3])));
+        vs = scale_of(fmaxf(fmaxf(sm_am[1][0], sm_am[1][1]), fmaxf(sm_am[1][2], sm_am[1][3])));
+        auto code_of = [](float x, float s) {
+            return fminf(fmaxf(__builtin_rintf((float)(f16)(x / s)), -128.0f), 127.0f);
+        };
+        if (wave < NG) {
+            const float c = code_of(kx, (float)ks);
+            kcode = c + 128.0f;  // stored byte
+            const float qs = (float)(f16)((float)(f16)a.scale_h * qx);
+            const float sp = wave_reduce(qs * (float)(f16)(c * (float)ks), OpSum());
+            if (lane == 0) sm_s[wave] = sp;
+        }
+        const float c = code_of(vx, (float)vs);
+        vcode = c + 128.0f;
+        vd = (float)(f16)(c * (float)vs);
+    } else if (wave < NG) {
         const float mn = wave_reduce(kx, OpMin()), mx = wave_reduce(kx, OpMax());
         const AffineGroup g = affine_group(mn, mx, BITS);
         kcode = affine_code(kx, g, BITS);
@@ -818,11 +857,14 @@ __global__ __launch_bounds__(256) void merge_append_kernel(MergeAppendArgs a) {
         if (lane == 0) sm_s[wave] = sp;
     }
     // ---- new value: group b, every wave (lane = dim d)
-    const float vmn = wave_reduce(vx, OpMin()), vmx = wave_reduce(vx, OpMax());
-    const AffineGroup gv = affine_group(vmn, vmx, BITS);
-    const float vcode = affine_code(vx, gv, BITS);
-    const f16 vs = (f16)gv.scale, vbias = (f16)gv.bias;
-    const float vd = affine_dequant(vcode, vs, vbias);
+    if constexpr (!I8) {
+        const float vmn = wave_reduce(vx, OpMin()), vmx = wave_reduce(vx, OpMax());
+        const AffineGroup gv = affine_group(vmn, vmx, BITS);
+        vcode = affine_code(vx, gv, BITS);
+        vs = (f16)gv.scale;
+        vbias = (f16)gv.bias;
+        vd = affine_dequant(vcode, vs, vbias);
+    }
 
     // ---- merge: M over the partials and the new score
     float m = -INFINITY;
@@ -870,7 +912,7 @@ __global__ __launch_bounds__(256) void merge_append_kernel(MergeAppendArgs a) {
             sb.y = kb;
             a.k_params[((int64_t)h * a.cap + t) * NG + k_param_slot(b, NG)] =
                 __builtin_bit_cast(uint32_t, sb);
-            check_fast_scale(ks, BITS, a.fast_flag);
+            if (!I8) check_fast_scale(ks, BITS, a.fast_flag);
         }
     }
     if (v_writer) {
@@ -887,12 +929,12 @@ __global__ __launch_bounds__(256) void merge_append_kernel(MergeAppendArgs a) {
             f16* vpp = a.v_params + (((int64_t)h * (a.cap / 8) + vblk) * NG + b) * 16;
             vpp[vk] = vs;
             vpp[8 + vk] = vbias;
-            check_fast_scale(vs, BITS, a.fast_flag);
+            if (!I8) check_fast_scale(vs, BITS, a.fast_flag);
         }
     }
 }
 
-template <int BITS, int D>
+template <int BITS, int D, bool I8 = false>
 static int launch_decode_fused(KVCache& cc, const f16* q, int G, const f16* k_new,
                                const f16* v_new, float scale, f16* out, hipStream_t stream) {
     MergeAppendArgs m;
@@ -925,19 +967,19 @@ static int launch_decode_fused(KVCache& cc, const f16* q, int G, const f16* k_ne
     const dim3 grid(G, cc.hkv, D / 64);
     switch (merge_per(m.nc)) {
         case 4:
-            hipLaunchKernelGGL((merge_append_kernel<BITS, D, 4>), grid, dim3(256), 0, stream, m);
+            hipLaunchKernelGGL((merge_append_kernel<BITS, D, 4, I8>), grid, dim3(256), 0, stream, m);
             break;
         case 8:
-            hipLaunchKernelGGL((merge_append_kernel<BITS, D, 8>), grid, dim3(256), 0, stream, m);
+            hipLaunchKernelGGL((merge_append_kernel<BITS, D, 8, I8>), grid, dim3(256), 0, stream, m);
             break;
         case 16:
-            hipLaunchKernelGGL((merge_append_kernel<BITS, D, 16>), grid, dim3(256), 0, stream, m);
+            hipLaunchKernelGGL((merge_append_kernel<BITS, D, 16, I8>), grid, dim3(256), 0, stream, m);
             break;
         case 32:
-            hipLaunchKernelGGL((merge_append_kernel<BITS, D, 32>), grid, dim3(256), 0, stream, m);
+            hipLaunchKernelGGL((merge_append_kernel<BITS, D, 32, I8>), grid, dim3(256), 0, stream, m);
             break;
         default:
-            hipLaunchKernelGGL((merge_append_kernel<BITS, D, kMergeMaxPer>), grid, dim3(256), 0,
+            hipLaunchKernelGGL((merge_append_kernel<BITS, D, kMergeMaxPer, I8>), grid, dim3(256), 0,
                                stream, m);
     }
     QW_HIP_CHECK(hipGetLastError());
@@ -957,7 +999,7 @@ int KVCache::update_and_attention(const void* q, int n_q_heads, int n_rows, cons
     QW_REQUIRE(n_q_heads > 0 && n_q_heads % hkv == 0 && n_rows > 0, QW_ERR_INVALID_ARGUMENT,
                "update_and_attention: bad head or row geometry");
     const int G = n_q_heads / hkv;
-    if (QW_FUSED_DECODE_APPEND && affine() && !int8() && n_rows == 1 && G <= 16) {
+    if (QW_FUSED_DECODE_APPEND && affine() && n_rows == 1 && G <= 16) {
         // decode: the append rides in the split-K merge (one launch fewer)
         DeviceGuard dg(device);
         QW_REQUIRE(dg.ok, QW_ERR_HIP, "update_and_attention: hipSetDevice failed");
@@ -969,6 +1011,9 @@ int KVCache::update_and_attention(const void* q, int n_q_heads, int n_rows, cons
         const f16* kn = (const f16*)k_new;
         const f16* vn = (const f16*)v_new;
         f16* oo = (f16*)out;
+        if (int8())
+            return D == 256 ? launch_decode_fused<8, 256, true>(*this, qq, G, kn, vn, scale, oo, stream)
+                            : launch_decode_fused<8, 128, true>(*this, qq, G, kn, vn, scale, oo, stream);
         if (D == 256)
             return bits == 4 ? launch_decode_fused<4, 256>(*this, qq, G, kn, vn, scale, oo, stream)
                              : launch_decode_fused<8, 256>(*this, qq, G, kn, vn, scale, oo, stream);

@@ -528,3 +528,32 @@ def test_int8_snapshot_round_trip_and_trim():
     c.update(_gpu(k)[None], _gpu(v)[None])
     for name, t in c.snapshot_tensors().items():
         assert torch.equal(t, a.snapshot_tensors()[name]), name
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["affine4", "affine8", "int8"])
+@pytest.mark.parametrize("D", [256, 128])
+def test_decode_layer_call_stores_what_update_stores(mode, D):
+    """A one-row update_and_attention appends inside the split-K merge; the
+    cache it leaves equals update() of the same rows, codes, scales and biases
+    (export bit for bit), over decode steps into a partly filled 8-key V block,
+    and its output equals attention over the updated cache."""
+    import qw_amd
+
+    H, hq = 4, 24
+    r = rng(77 + D)
+    k, v = _kv(r, H, 700, D)
+    a = qw_amd.KVCache(mode, H, D)
+    b = qw_amd.KVCache(mode, H, D)
+    a.update(_gpu(k[:, :697])[None], _gpu(v[:, :697])[None])
+    b.update(_gpu(k[:, :697])[None], _gpu(v[:, :697])[None])
+    for t in (697, 698, 699):
+        q = _gpu(r.standard_normal((1, hq, 1, D)).astype(np.float16))
+        out = _np(a.update_and_attention(q, _gpu(k[:, t:t + 1])[None], _gpu(v[:, t:t + 1])[None],
+                                         1.0 / 16))
+        b.update(_gpu(k[:, t:t + 1])[None], _gpu(v[:, t:t + 1])[None])
+        ref = _np(b.attention(q, 1.0 / 16))
+        assert_close(out, ref, f"{mode} D{D} t{t} fused vs separate")
+    sa, sb = a.snapshot_tensors(), b.snapshot_tensors()
+    for key in sa:
+        np.testing.assert_array_equal(_np(sa[key]), _np(sb[key]), err_msg=f"{mode} {key}")
