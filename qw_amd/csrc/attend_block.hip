@@ -63,7 +63,10 @@ struct BlockArgs {
 
 // 8 waves, two a SIMD: one wave a SIMD leaves the MFMA, LDS and VALU
 // latencies of a wave exposed (measured ~1.6x slower at equal work).
-constexpr int kBlockWaves = 8;
+#ifndef QW_BLOCK_WAVES
+#define QW_BLOCK_WAVES 8
+#endif
+constexpr int kBlockWaves = QW_BLOCK_WAVES;
 
 template <int D>
 struct BlockShape {
@@ -106,6 +109,21 @@ __device__ __forceinline__ int v_logical_dim(int slot, int D, int bits) {
     const int e = bits == 4 ? 4 : (bits == 8 ? 2 : 1);
     const int i = slot % e, n = (slot / e) % 16, j = slot / (16 * e);
     return n * dpl + e * j + i;
+}
+
+// max / sum of v over the lane pair (l, l ^ 16), then over (l, l ^ 32): row
+// swaps in the VALU (v_permlane16/32_swap) instead of LDS permutes.
+__device__ __forceinline__ float wave_max_g(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float wave_sum_g(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 template <int BITS, int D, int RT, bool FAST>
@@ -311,36 +329,45 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
             }
         }
         half8 pop[NSUB][RT];
-        // Scores -> fp16 rounding -> (mask) -> online softmax -> P; MASKED only
-        // for tiles some row of the wave cannot fully see (a scalar branch: the
-        // common case carries no per-score compares).
-        auto softmax = [&](auto masked) {
+        // Scores -> fp16 rounding -> (mask) -> online softmax -> P; the mask
+        // only for tiles some row of the wave cannot fully see (a scalar
+        // branch around the compares: the common case carries none).
+        const bool mask = kt0 + KT - 1 > wave_first_lim;
+        auto softmax = [&]() {
 #pragma unroll
             for (int rt = 0; rt < RT; rt++) {
-                float sc[NSUB][8];
+                // MLX rounds the score matrix to fp16 before the softmax: the
+                // scores stay packed in fp16 pairs (element e of pair j is
+                // score 2j + e: keys 32u + 8g + (idx & 3) + 4 (idx >> 2)).
+                half2v sh[NSUB][4];
 #pragma unroll
                 for (int u = 0; u < NSUB; u++)
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        // MLX rounds the score matrix to fp16 before the softmax.
-                        sc[u][i] = (float)(f16)acc[u][0][rt][i];
-                        sc[u][4 + i] = (float)(f16)acc[u][1][rt][i];
-                        if constexpr (decltype(masked)::value) {
-                            const int ka = kt0 + 32 * u + 8 * g + i, kc = ka + 4;
-                            sc[u][i] = ka <= lim[rt] ? sc[u][i] : -INFINITY;
-                            sc[u][4 + i] = kc <= lim[rt] ? sc[u][4 + i] : -INFINITY;
-                        }
+                    for (int j = 0; j < 4; j++) {
+                        const float4v& av = acc[u][j >> 1][rt];
+                        sh[u][j] = half2v{(f16)av[2 * (j & 1)], (f16)av[2 * (j & 1) + 1]};
                     }
+                if (mask) {
+#pragma unroll
+                    for (int u = 0; u < NSUB; u++)
+#pragma unroll
+                        for (int j = 0; j < 4; j++)
+#pragma unroll
+                            for (int e = 0; e < 2; e++) {
+                                const int idx = 2 * j + e;
+                                const int key = kt0 + 32 * u + 8 * g + (idx & 3) + 4 * (idx >> 2);
+                                if (key > lim[rt]) sh[u][j][e] = (f16)(-INFINITY);
+                            }
+                }
                 // Online softmax with a lazy reference: m_run moves only when a
                 // score exceeds it by more than 5.5 (so p <= e^5.5 stays well
                 // inside fp16).
-                float mx = sc[0][0];
+                half2v m2 = sh[0][0];
 #pragma unroll
                 for (int u = 0; u < NSUB; u++)
 #pragma unroll
-                    for (int e = 0; e < 8; e++) mx = fmaxf(mx, sc[u][e]);
-                mx = fmaxf(mx, __shfl_xor(mx, 16));
-                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                    for (int j = 0; j < 4; j++) m2 = __builtin_elementwise_max(m2, sh[u][j]);
+                const float mx = wave_max_g(fmaxf((float)m2.x, (float)m2.y));
                 if (__any(mx > m_run[rt] + 5.5f)) {
                     const float m_new = fmaxf(m_run[rt], mx);
                     if (__any(m_run[rt] != -INFINITY)) {
@@ -363,17 +390,14 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
                 for (int u = 0; u < NSUB; u++)
 #pragma unroll
                     for (int e = 0; e < 8; e++) {
-                        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[u][e], kLog2e, -mref2));
+                        const float x = (float)sh[u][e >> 1][e & 1];
+                        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(x, kLog2e, -mref2));
                         l_run[rt] += p;
                         pop[u][rt][e] = (f16)p;
                     }
             }
         };
-        // every row of the wave sees the whole tile: no per-score mask
-        if (kt0 + KT - 1 <= wave_first_lim)
-            softmax(std::false_type{});
-        else
-            softmax(std::true_type{});
+        softmax();
         // O += P . V: B = slot 16mm + r16 (column r16 of output tile mm) of
         // V block 4u + g, i.e. keys 32u + 8g .. +7.
 #pragma unroll
@@ -440,8 +464,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
         float lsum = l_run[rt];
-        lsum += __shfl_xor(lsum, 16);
-        lsum += __shfl_xor(lsum, 32);
+        lsum = wave_sum_g(lsum);
         const int rbase = wrow0 + 16 * rt + 4 * g;  // rows of acc_o[rt][.][i] are rbase + i
         if (a.n_split == 1) {
             float inv[4];
