@@ -14,9 +14,11 @@
 //   slice of the row's list; waves take 16-entry tiles of it in turn.
 //   Q.K^T on MFMA (v_mfma_f32_16x16x32_f16): A = 16 gathered K rows (each
 //   lane 16 contiguous bytes of its row per MFMA), B = the G query heads.
-//   Probabilities go through LDS (one 16x16 fp32 tile a wave) and P.V runs on
-//   the VALU with each lane owning D/64 contiguous dims of every head, so a
-//   gathered V row is one coalesced 512-byte wave load.
+//   P.V on MFMA too (v_mfma_f32_16x16x16_f16): the S^T tile already holds P
+//   in the A-operand layout, and V is gathered straight into the B layout as
+//   8-byte row pieces (16 lanes cover 128 contiguous bytes of a row); P goes
+//   in as an fp16 high part plus an fp16 remainder, so every product is exact
+//   and the accumulation is fp32.
 //   Online softmax in the exp2 domain across tiles; the waves merge through
 //   LDS; split-K parts write fp32 partials merged by a second kernel.
 #include <algorithm>
@@ -42,9 +44,9 @@ struct DlsaArgs {
 constexpr int kDlsaNT = 2;  // tiles per batch a wave keeps in flight
 
 template <int D, int GMAX>
-__global__ __launch_bounds__(256) void dlsa_kernel(DlsaArgs a) {
+__global__ __launch_bounds__(256, 2) void dlsa_kernel(DlsaArgs a) {
     constexpr int NM = D / 32;
-    constexpr int DPV = D / 64;  // dims a lane owns in P.V
+    constexpr int NP = D / 64;  // 64-dim groups: P.V output tiles (p, c), c < 4
     const int part = blockIdx.x, r = blockIdx.y, h = blockIdx.z;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r16 = lane & 15, g = lane >> 4;
@@ -64,20 +66,26 @@ __global__ __launch_bounds__(256) void dlsa_kernel(DlsaArgs a) {
         for (int m = 0; m < NM; m++) qop[m] = ok ? *(const half8*)(qrow + 32 * m + 8 * g) : half8{};
     }
 
-    __shared__ float sm_p[4][16][17];  // [wave][entry][head], padded
-    float mrun = -INFINITY;             // running max (log2 domain), column r16
-    float lrun = 0.0f;                  // running sum, this lane's share
-    float acc[GMAX][DPV];
+    // P.V on MFMA (v_mfma_f32_16x16x16_f16, K = the tile's 16 entries): A = P
+    // (row = head r16, entries 4g..4g+3: exactly where the S^T tile leaves
+    // them), B = V (entries 4g..4g+3 of one dim), gathered as 8-byte row
+    // pieces: lane (g, r16) loads dims 64p + 4 r16 .. +3 of entries 4g + j.
+    // Output tile (p, c) holds heads 4g + i x dims 64p + 4 r16 + c. P enters
+    // as an fp16 high part and an fp16 remainder, so p * v is exact and the
+    // sums stay fp32 as in the reference.
+    float mrun = -INFINITY;  // running max (log2 domain), column r16
+    float lrun = 0.0f;       // running sum, this lane's share
+    float4v acc[NP][4];
 #pragma unroll
-    for (int hh = 0; hh < GMAX; hh++)
+    for (int pp = 0; pp < NP; pp++)
 #pragma unroll
-        for (int d = 0; d < DPV; d++) acc[hh][d] = 0.0f;
+        for (int c = 0; c < 4; c++) acc[pp][c] = float4v{0.f, 0.f, 0.f, 0.f};
 
     const int n_tiles = (e_end - e_begin + 15) / 16;
     for (int t0 = wave; t0 < n_tiles; t0 += 4 * kDlsaNT) {
         // ---- gather loads for up to NT tiles
         u32x4 kc[kDlsaNT][NM];
-        u32x2 vr[kDlsaNT][16];
+        u32x2 vq[kDlsaNT][4][NP];
         int key_a[kDlsaNT];  // the key of list entry tile*16 + r16 (A-operand row)
         bool ok_a[kDlsaNT];
 #pragma unroll
@@ -95,16 +103,12 @@ __global__ __launch_bounds__(256) void dlsa_kernel(DlsaArgs a) {
 #pragma unroll
         for (int b = 0; b < kDlsaNT; b++) {
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                // V row of tile entry i: every lane reads its DPV dims.
-                const int key = __builtin_amdgcn_readlane(key_a[b], i);
-                const f16* vrow = a.v + h * a.vhs + (int64_t)key * a.vrs + lane * DPV;
-                if constexpr (DPV == 4)
-                    vr[b][i] = *(const u32x2*)vrow;
-                else if constexpr (DPV == 2)
-                    vr[b][i] = u32x2{*(const uint32_t*)vrow, 0u};
-                else
-                    vr[b][i] = u32x2{(uint32_t) * (const uint16_t*)vrow, 0u};
+            for (int j = 0; j < 4; j++) {
+                // entry 4g + j's key sits in lane 4g + j (lane r16 holds entry r16)
+                const int key = __shfl(key_a[b], 4 * g + j);
+                const f16* vrow = a.v + h * a.vhs + (int64_t)key * a.vrs + 4 * r16;
+#pragma unroll
+                for (int pp = 0; pp < NP; pp++) vq[b][j][pp] = *(const u32x2*)(vrow + 64 * pp);
             }
         }
         // ---- scores: S^T tile, lane holds entries 4g+i for head r16
@@ -130,46 +134,48 @@ __global__ __launch_bounds__(256) void dlsa_kernel(DlsaArgs a) {
         const float alpha = mrun == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mrun - mref);
         mrun = mnew;
         lrun *= alpha;
-        // Rescale the P.V accumulators: head hh's factor lives in column hh.
+        // Rescale the accumulators: row i of a tile is head 4g + i, whose
+        // factor lives in column 4g + i.
+        {
+            float f[4];
 #pragma unroll
-        for (int hh = 0; hh < GMAX; hh++) {
-            const float f = __shfl(alpha, hh);
+            for (int i = 0; i < 4; i++) f[i] = __shfl(alpha, 4 * g + i);
 #pragma unroll
-            for (int d = 0; d < DPV; d++) acc[hh][d] *= f;
+            for (int pp = 0; pp < NP; pp++)
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[pp][c][i] *= f[i];
         }
 #pragma unroll
         for (int b = 0; b < kDlsaNT; b++) {
+            half4v ph, pl;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float p = __builtin_amdgcn_exp2f(s[b][i] - mref);
-                lrun += p;
-                sm_p[wave][4 * g + i][r16] = p;
+                const float pv = __builtin_amdgcn_exp2f(s[b][i] - mref);
+                lrun += pv;
+                ph[i] = (f16)pv;
+                pl[i] = (f16)(pv - (float)ph[i]);
             }
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                float vf[DPV];
-                if constexpr (DPV == 4) {
-                    const half4v hv = __builtin_bit_cast(half4v, vr[b][i]);
+            for (int pp = 0; pp < NP; pp++) {
 #pragma unroll
-                    for (int d = 0; d < 4; d++) vf[d] = (float)hv[d];
-                } else if constexpr (DPV == 2) {
-                    const half2v hv = __builtin_bit_cast(half2v, vr[b][i].x);
-                    vf[0] = (float)hv.x;
-                    vf[1] = (float)hv.y;
-                } else {
-                    vf[0] = (float)__builtin_bit_cast(f16, (uint16_t)vr[b][i].x);
-                }
-#pragma unroll
-                for (int hh = 0; hh < GMAX; hh++) {
-                    const float p = sm_p[wave][i][hh];
-#pragma unroll
-                    for (int d = 0; d < DPV; d++) acc[hh][d] = __builtin_fmaf(p, vf[d], acc[hh][d]);
+                for (int c = 0; c < 4; c++) {
+                    // element c of the four entries' 4-dim pieces
+                    const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+                    uint32_t w0, w1;
+                    if (c < 2) {
+                        w0 = __builtin_amdgcn_perm(vq[b][1][pp].x, vq[b][0][pp].x, sel);
+                        w1 = __builtin_amdgcn_perm(vq[b][3][pp].x, vq[b][2][pp].x, sel);
+                    } else {
+                        w0 = __builtin_amdgcn_perm(vq[b][1][pp].y, vq[b][0][pp].y, sel);
+                        w1 = __builtin_amdgcn_perm(vq[b][3][pp].y, vq[b][2][pp].y, sel);
+                    }
+                    const half4v vb = __builtin_bit_cast(half4v, u32x2{w0, w1});
+                    acc[pp][c] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, vb, acc[pp][c], 0, 0, 0);
+                    acc[pp][c] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, vb, acc[pp][c], 0, 0, 0);
                 }
             }
-            __builtin_amdgcn_wave_barrier();
         }
     }
     lrun += __shfl_xor(lrun, 16);
@@ -177,41 +183,55 @@ __global__ __launch_bounds__(256) void dlsa_kernel(DlsaArgs a) {
 
     // ---- merge the waves: (m, l) per head, then the accumulators
     __shared__ float2 sm_ml[4][16];
-    __shared__ float sm_acc[2][GMAX][D];
+    __shared__ float4v sm_acc[2][GMAX][D / 4];
     if (g == 0) sm_ml[wave][r16] = float2{mrun, lrun};
     __syncthreads();
-    float Mh[GMAX], Lh[GMAX];
+    float Mi[4], Li[4];  // heads 4g + i
 #pragma unroll
-    for (int hh = 0; hh < GMAX; hh++) {
+    for (int i = 0; i < 4; i++) {
+        const int hd = 4 * g + i;
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < 4; w++) M = fmaxf(M, sm_ml[w][hh].x);
+        for (int w = 0; w < 4; w++) M = fmaxf(M, sm_ml[w][hd].x);
         float L = 0.0f, own = 0.0f;
 #pragma unroll
         for (int w = 0; w < 4; w++) {
-            const float mw = sm_ml[w][hh].x;
+            const float mw = sm_ml[w][hd].x;
             const float f = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-            L += f * sm_ml[w][hh].y;
+            L += f * sm_ml[w][hd].y;
             if (w == wave) own = f;
         }
-        Mh[hh] = M;
-        Lh[hh] = L;
+        Mi[i] = M;
+        Li[i] = L;
 #pragma unroll
-        for (int d = 0; d < DPV; d++) acc[hh][d] *= own;
+        for (int pp = 0; pp < NP; pp++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc[pp][c][i] *= own;
     }
+    // head 4g + i, dims 64p + 4 r16 .. +3 as one float4
     auto store = [&](int buf) {
 #pragma unroll
-        for (int hh = 0; hh < GMAX; hh++)
-            if (hh < G)
+        for (int i = 0; i < 4; i++) {
+            const int hd = 4 * g + i;
+            if (hd < G && hd < GMAX)
 #pragma unroll
-                for (int d = 0; d < DPV; d++) sm_acc[buf][hh][lane * DPV + d] = acc[hh][d];
+                for (int pp = 0; pp < NP; pp++)
+                    sm_acc[buf][hd][16 * pp + r16] =
+                        float4v{acc[pp][0][i], acc[pp][1][i], acc[pp][2][i], acc[pp][3][i]};
+        }
     };
     auto add = [&](int buf) {
 #pragma unroll
-        for (int hh = 0; hh < GMAX; hh++)
-            if (hh < G)
+        for (int i = 0; i < 4; i++) {
+            const int hd = 4 * g + i;
+            if (hd < G && hd < GMAX)
 #pragma unroll
-                for (int d = 0; d < DPV; d++) acc[hh][d] += sm_acc[buf][hh][lane * DPV + d];
+                for (int pp = 0; pp < NP; pp++) {
+                    const float4v o = sm_acc[buf][hd][16 * pp + r16];
+#pragma unroll
+                    for (int c = 0; c < 4; c++) acc[pp][c][i] += o[c];
+                }
+        }
     };
     if (wave >= 2) store(wave - 2);
     __syncthreads();
@@ -222,20 +242,27 @@ __global__ __launch_bounds__(256) void dlsa_kernel(DlsaArgs a) {
     if (wave != 0) return;
     add(0);
 #pragma unroll
-    for (int hh = 0; hh < GMAX; hh++) {
-        if (hh >= G) continue;
-        const int qh = h * G + hh;
+    for (int i = 0; i < 4; i++) {
+        const int hd = 4 * g + i;
+        if (hd >= G) continue;
+        const int qh = h * G + hd;
         if (a.parts == 1) {
-            const float inv = Lh[hh] > 0.0f ? 1.0f / Lh[hh] : 0.0f;
-            f16* dst = a.out + ((int64_t)qh * a.L + r) * D + lane * DPV;
+            const float inv = Li[i] > 0.0f ? 1.0f / Li[i] : 0.0f;
+            f16* dst = a.out + ((int64_t)qh * a.L + r) * D + 4 * r16;
 #pragma unroll
-            for (int d = 0; d < DPV; d++) dst[d] = (f16)(acc[hh][d] * inv);
+            for (int pp = 0; pp < NP; pp++) {
+                const half4v o = {(f16)(acc[pp][0][i] * inv), (f16)(acc[pp][1][i] * inv),
+                                  (f16)(acc[pp][2][i] * inv), (f16)(acc[pp][3][i] * inv)};
+                *(half4v*)(dst + 64 * pp) = o;
+            }
         } else {
             const int64_t pr = ((int64_t)r * a.hq + qh) * a.parts + part;
-            float* dst = a.part_o + pr * D + lane * DPV;
+            float* dst = a.part_o + pr * D + 4 * r16;
 #pragma unroll
-            for (int d = 0; d < DPV; d++) dst[d] = acc[hh][d];
-            if (lane == 0) a.part_ml[pr] = float2{Mh[hh], Lh[hh]};
+            for (int pp = 0; pp < NP; pp++)
+                *(float4v*)(dst + 64 * pp) =
+                    float4v{acc[pp][0][i], acc[pp][1][i], acc[pp][2][i], acc[pp][3][i]};
+            if (r16 == 0) a.part_ml[pr] = float2{Mi[i], Li[i]};
         }
     }
 }
@@ -327,9 +354,9 @@ static int dlsa_workspace(int device, size_t need, void** out) {
 // Launch policy (the reference's auto_parts, mlx_cxx_dlsa_attention.cpp:379-400,
 // re-derived for 256 CUs): one pass when rows x kv_heads alone fill the CUs,
 // else split each list so that about one workgroup a CU runs (measured for one
-// row, 4 KV heads, 4612 entries: 64 parts 15.5 us, 48 parts 15.9 us, 96 parts
-// 19.0 us, 128 parts 19.4 us, 32 parts 21 us), keeping at least 16 entries
-// (one tile) a part and at most 128 parts.
+// row, 4 KV heads, 4612 entries: 48 parts 14.2 us, 64 parts 14.3 us, 96 parts
+// 15.3 us, 128 parts 16.3 us), keeping at least 16 entries (one tile) a part
+// and at most 128 parts.
 static int auto_parts(int units, int width) {
     if (units >= 256) return 1;
     int parts = (256 + units - 1) / units;
