@@ -67,6 +67,21 @@ struct BlockArgs {
 #define QW_BLOCK_WAVES 8
 #endif
 constexpr int kBlockWaves = QW_BLOCK_WAVES;
+// LDS reads a wave keeps in flight ahead of its MFMAs (instruction-scheduling
+// groups). Left to itself the compiler issues one or two reads ahead, so each
+// MFMA waited on its own read; four ahead measured c3 1.25 -> 1.19 ms and c4
+// 70 -> 67 us (2, 3, 6 and 8 ahead were slower). 0 leaves the order to the
+// compiler.
+#ifndef QW_BLOCK_SCHED_QK
+#define QW_BLOCK_SCHED_QK 4  // > 0: K reads kept that far ahead of the QK MFMAs
+#endif
+#ifndef QW_BLOCK_SCHED_PV
+#define QW_BLOCK_SCHED_PV 4  // > 0: V reads kept that far ahead of the P.V MFMAs
+#endif
+#ifndef QW_BLOCK_STAGGER
+#define QW_BLOCK_STAGGER 0
+#endif
+constexpr bool kBlockStagger = QW_BLOCK_STAGGER != 0;
 
 template <int D>
 struct BlockShape {
@@ -328,6 +343,18 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
                 }
             }
         }
+#if QW_BLOCK_SCHED_QK
+        if constexpr (RT == 1) {
+            constexpr int NQ = NM * NSUB * 2, AH = QW_BLOCK_SCHED_QK;
+            __builtin_amdgcn_sched_group_barrier(0x100, AH, 0);
+#pragma unroll
+            for (int i = 0; i < NQ - AH; i++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, AH, 0);
+        }
+#endif
         half8 pop[NSUB][RT];
         // Scores -> fp16 rounding -> (mask) -> online softmax -> P; the mask
         // only for tiles some row of the wave cannot fully see (a scalar
@@ -412,6 +439,18 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
                         __builtin_amdgcn_mfma_f32_16x16x32_f16(pop[u][rt], vv, acc_o[rt][mm], 0, 0, 0);
             }
         }
+#if QW_BLOCK_SCHED_PV
+        if constexpr (RT == 1) {
+            constexpr int NQ = NSUB * NT, AH = QW_BLOCK_SCHED_PV;
+            __builtin_amdgcn_sched_group_barrier(0x100, AH, 1);
+#pragma unroll
+            for (int i = 0; i < NQ - AH; i++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, AH, 1);
+        }
+#endif
     };
 
     // ---- main loop: round t dequantizes tile t+1 into LDS buffer (t+1)&1
@@ -429,12 +468,22 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         if (t0 + 2 < t1) load(s1, t0 + 2);
     }
     __syncthreads();
+    // The two waves of a SIMD (w, w + 4) take a round's phases in opposite
+    // order: the first half dequantizes the next tile, then computes; the
+    // second half computes, then dequantizes. The barrier puts them in step
+    // each round, and the swap lets one wave's MFMAs run beside the other's
+    // dequant VALU work instead of both contending for the same unit.
+    const bool late = kBlockStagger && wave >= NW / 2;
     auto round = [&](Stage& sa, int t, int b) {
-        if (t + 1 < t1) {
+        if (!late && t + 1 < t1) {
             store(sa, b ^ 1);
             if (t + 3 < t1) load(sa, t + 3);
         }
         if (wave_live && t * KT <= wave_lim) tile(b, t * KT);
+        if (late && t + 1 < t1) {
+            store(sa, b ^ 1);
+            if (t + 3 < t1) load(sa, t + 3);
+        }
         __syncthreads();
     };
     for (int t = t0; t < t1; t += 2) {
