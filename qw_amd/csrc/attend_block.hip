@@ -78,10 +78,6 @@ constexpr int kBlockWaves = QW_BLOCK_WAVES;
 #ifndef QW_BLOCK_SCHED_PV
 #define QW_BLOCK_SCHED_PV 4  // > 0: V reads kept that far ahead of the P.V MFMAs
 #endif
-#ifndef QW_BLOCK_STAGGER
-#define QW_BLOCK_STAGGER 0
-#endif
-constexpr bool kBlockStagger = QW_BLOCK_STAGGER != 0;
 
 template <int D>
 struct BlockShape {
@@ -468,22 +464,12 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         if (t0 + 2 < t1) load(s1, t0 + 2);
     }
     __syncthreads();
-    // The two waves of a SIMD (w, w + 4) take a round's phases in opposite
-    // order: the first half dequantizes the next tile, then computes; the
-    // second half computes, then dequantizes. The barrier puts them in step
-    // each round, and the swap lets one wave's MFMAs run beside the other's
-    // dequant VALU work instead of both contending for the same unit.
-    const bool late = kBlockStagger && wave >= NW / 2;
     auto round = [&](Stage& sa, int t, int b) {
-        if (!late && t + 1 < t1) {
+        if (t + 1 < t1) {
             store(sa, b ^ 1);
             if (t + 3 < t1) load(sa, t + 3);
         }
         if (wave_live && t * KT <= wave_lim) tile(b, t * KT);
-        if (late && t + 1 < t1) {
-            store(sa, b ^ 1);
-            if (t + 3 < t1) load(sa, t + 3);
-        }
         __syncthreads();
     };
     for (int t = t0; t < t1; t += 2) {
