@@ -238,11 +238,14 @@ __global__ __launch_bounds__(128) void turbo4_fetch_kernel(
 
 // ------------------------------------------- rotated fp16 expansion (SDPA)
 //
-// One 8-key block of one head a workgroup of D threads: thread = (key,
-// 8 coordinates). K_rot rows go to kw [hkv][capv][D]; V_rot to the fp16
+// NB 8-key blocks of one head a workgroup of D threads: thread = (key,
+// 8 coordinates) of each block, the loads of all NB blocks issued before the
+// first is expanded. K_rot rows go to kw [hkv][capv][D]; V_rot to the fp16
 // cache's transposed blocks vw [hkv][capv/8][D][8] (dims in lane order)
-// through LDS. Keys past
-// `T` are written as zeros (the fp16 kernels read whole 8-key blocks).
+// through LDS. Keys past `T` are written as zeros (the fp16 kernels read
+// whole 8-key blocks).
+constexpr int kExpandBlocks = 4;  // 8-key blocks a workgroup (capv / 8 is a multiple of 32)
+
 template <int D>
 __global__ __launch_bounds__(D) void turbo4_expand_kernel(
     const uint8_t* __restrict__ k_packed, const uint32_t* __restrict__ k_side,
@@ -250,37 +253,56 @@ __global__ __launch_bounds__(D) void turbo4_expand_kernel(
     const float* __restrict__ tab, int cap, int T, int capv, f16* __restrict__ kw,
     f16* __restrict__ vw) {
     constexpr int CPK = D / 8;  // 8-coordinate chunks a key
+    constexpr int NB = kExpandBlocks;
     using TT = T4Tab<D>;
     __shared__ float s_cb[16];
-    __shared__ __align__(16) f16 sv[D][8];
+    __shared__ __align__(16) f16 sv[NB][D][8];
     if (threadIdx.x < 16) s_cb[threadIdx.x] = tab[TT::cb + threadIdx.x];
-    __syncthreads();
-    const int blk = blockIdx.x, h = blockIdx.y;
+    const int h = blockIdx.y;
     const int k = threadIdx.x / CPK, c = threadIdx.x % CPK;
-    const int t = blk * 8 + k;
-    half8 kv8, vv8;
-    if (t < T) {
-        const int64_t r = (int64_t)h * cap + t;
-        const uint32_t kb = *(const uint32_t*)(k_packed + r * (D / 2) + 4 * c);
-        const uint32_t vb = *(const uint32_t*)(v_packed + r * (D / 2) + 4 * c);
-        const float kr = (float)__builtin_bit_cast(half2v, k_side[r]).x;
-        const float vr = (float)__builtin_bit_cast(half2v, v_side[r]).y;
+    uint32_t kb[NB], vb[NB], ks[NB], vs[NB];
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            kv8[j] = f16_of_product(s_cb[(kb >> (4 * j)) & 15u], kr);
-            vv8[j] = f16_of_product(s_cb[(vb >> (4 * j)) & 15u], vr);
+    for (int n = 0; n < NB; n++) {
+        const int t = (blockIdx.x * NB + n) * 8 + k;
+        kb[n] = vb[n] = ks[n] = vs[n] = 0u;
+        if (t < T) {
+            const int64_t r = (int64_t)h * cap + t;
+            kb[n] = *(const uint32_t*)(k_packed + r * (D / 2) + 4 * c);
+            vb[n] = *(const uint32_t*)(v_packed + r * (D / 2) + 4 * c);
+            ks[n] = k_side[r];
+            vs[n] = v_side[r];
         }
-    } else {
-#pragma unroll
-        for (int j = 0; j < 8; j++) kv8[j] = vv8[j] = (f16)0.0f;
     }
-    *(half8*)(kw + ((int64_t)h * capv + t) * D + 8 * c) = kv8;
-    // (the fp16 cache keeps V dims in MFMA lane order, v_phys_dim)
+    __syncthreads();  // s_cb
 #pragma unroll
-    for (int j = 0; j < 8; j++) sv[v_phys_dim(8 * c + j, D, 16)][k] = vv8[j];
+    for (int n = 0; n < NB; n++) {
+        const int blk = blockIdx.x * NB + n;
+        const int t = blk * 8 + k;
+        half8 kv8, vv8;
+        if (t < T) {
+            const float kr = (float)__builtin_bit_cast(half2v, ks[n]).x;
+            const float vr = (float)__builtin_bit_cast(half2v, vs[n]).y;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                kv8[j] = f16_of_product(s_cb[(kb[n] >> (4 * j)) & 15u], kr);
+                vv8[j] = f16_of_product(s_cb[(vb[n] >> (4 * j)) & 15u], vr);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) kv8[j] = vv8[j] = (f16)0.0f;
+        }
+        *(half8*)(kw + ((int64_t)h * capv + t) * D + 8 * c) = kv8;
+        // (the fp16 cache keeps V dims in MFMA lane order, v_phys_dim)
+#pragma unroll
+        for (int j = 0; j < 8; j++) sv[n][v_phys_dim(8 * c + j, D, 16)][k] = vv8[j];
+    }
     __syncthreads();
     const int p = threadIdx.x;  // physical dim slot
-    *(half8*)(vw + (((int64_t)h * (capv / 8) + blk) * D + p) * 8) = *(const half8*)&sv[p][0];
+#pragma unroll
+    for (int n = 0; n < NB; n++) {
+        const int blk = blockIdx.x * NB + n;
+        *(half8*)(vw + (((int64_t)h * (capv / 8) + blk) * D + p) * 8) = *(const half8*)&sv[n][p][0];
+    }
 }
 
 // ------------------------------------------------------------ rotation
@@ -506,7 +528,7 @@ int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float
     const float* tab = c.t4_tables;
     // Every 8-key block up to capv: rows past T become zeros, as the fp16
     // cache's unused rows are, since the fp16 kernels read whole tiles.
-    dim3 eg(capv / 8, c.hkv);
+    dim3 eg(capv / (8 * kExpandBlocks), c.hkv);
     if (D == 256) {
         using TT = T4Tab<256>;
         hipLaunchKernelGGL(turbo4_rotate_kernel<256>, dim3((qrows + 3) / 4), dim3(256), 0, stream,
