@@ -581,6 +581,36 @@ def turbo4_fetch_v(packed, v_norms, tab) -> np.ndarray:
     return (turbo4_rotate(u, tab["v_s2"], tab["v_s1"]) * n).astype(np.float16)
 
 
+def turbo4_fused_verify(q, k_packed, k_rescale, v_packed, v_rescale, tab, scale: float,
+                        q_pos) -> np.ndarray:
+    """The reference's fused Turbo4 verify pass (crates/mlx-cpp/turbo/
+    turbo4_attention.cpp:45-193 partial, :198-264 merge; wrapper
+    cache/turbo/fused_attention.rs:119-160): q rotated into the K basis in
+    fp32 (quant.rs:728-744), q' = f16(f32(q_rot * f32(scale * log2 e)))
+    (turbo4_attention.cpp:67-79), K and V expanded as f16(f32(centroid) *
+    f32(rescale)), then the closed form of its fp32 scores / softmax / P.V,
+    here in float64, with each row r seeing keys t <= q_pos[r]; the output
+    rotated back through the V basis (quant.rs:752-769) and cast to fp16.
+    q [Hq, L, D] fp16; packed [Hkv, T, D/2]; rescales [Hkv, T]."""
+    q = np.asarray(q, np.float16)
+    hq, L, D = q.shape
+    sl2e = np.float32(scale) * np.float32(1.4426950408889634)
+    q_rot = turbo4_rotate(q, tab["k_s1"], tab["k_s2"]).astype(np.float32)
+    qs = (q_rot * sl2e).astype(np.float32).astype(np.float16).astype(np.float64)
+    k = turbo4_expand_rotated(k_packed, k_rescale, tab).astype(np.float64)
+    v = turbo4_expand_rotated(v_packed, v_rescale, tab).astype(np.float64)
+    hkv, T, _ = k.shape
+    G = hq // hkv
+    pos = np.asarray(q_pos, np.int64)
+    o = np.empty((hq, L, D), np.float64)
+    for h in range(hq):
+        s = qs[h] @ k[h // G].T                        # [L, T], log2 domain
+        s = np.where(np.arange(T)[None, :] <= pos[:, None], s, -np.inf)
+        p = np.exp2(s - s.max(-1, keepdims=True))
+        o[h] = (p @ v[h // G]) / p.sum(-1, keepdims=True)
+    return turbo4_rotate(o, tab["v_s2"], tab["v_s1"]).astype(np.float16)
+
+
 def turbo4_attention(q, k_packed, k_rescale, v_packed, v_rescale, tab, scale: float,
                      q_pos=None, threads: int | None = None) -> np.ndarray:
     """attention_turbo4_dequant_sdpa (turbo/sparse_v.rs:1051-1072): q rotated

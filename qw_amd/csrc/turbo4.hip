@@ -327,6 +327,321 @@ __global__ __launch_bounds__(256) void turbo4_rotate_kernel(const f16* __restric
         o[lane * VPL + j] = (f16)((y[j] * wht_scale(D)) * s_out[lane * VPL + j]);
 }
 
+// q for the fused verify kernel: out = f16(f32(f32(s_out . (H / sqrt(D)) .
+// s_in . in) * post)), the reference's fp32 rotated q times scale * log2(e),
+// then the kernel's fp16 cast (turbo4_attention.cpp:67-79).
+template <int D>
+__global__ __launch_bounds__(256) void turbo4_rotate_scaled_kernel(
+    const f16* __restrict__ in, f16* __restrict__ out, int rows, const float* __restrict__ s_in,
+    const float* __restrict__ s_out, float post) {
+    constexpr int VPL = D / 64;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;  // whole waves leave together
+    const f16* r = in + (int64_t)row * D;
+    float y[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; j++) y[j] = (float)r[lane * VPL + j] * s_in[lane * VPL + j];
+    wht_wave<D>(y, lane);
+    f16* o = out + (int64_t)row * D;
+#pragma unroll
+    for (int j = 0; j < VPL; j++) {
+        float v = (y[j] * wht_scale(D)) * s_out[lane * VPL + j];
+        asm volatile("" : "+v"(v));
+        o[lane * VPL + j] = f16_of_product(v, post);
+    }
+}
+
+// ------------------------------------------- fused causal verify
+//
+// The reference's fused Turbo4 verify pass (turbo4_attention.cpp:45-193
+// partial, :198-264 merge; gate fused_attention.rs:70-100): causal blocks of
+// 1..5 query rows over a cache of more than 2048 tokens, scored straight from
+// the packed codes. Semantics: q' = f16(q_rot * scale * log2 e), K and V
+// expanded as f16(f32(centroid) * f32(rescale)), fp32 scores in the log2
+// domain, an exact running max, fp32 softmax sums and fp32 P.V.
+//
+// grid (splits, kv_heads), 8 waves. A workgroup walks its key range in
+// stages of 64 keys: the stage's K codes are expanded into LDS rows
+// [key][D], its V codes transposed into [dim][key] (so the P.V B operand is
+// one 8-byte read of 4 consecutive keys), double-buffered, with the codes of
+// two stages ahead held in registers. Wave (rt, kq) takes query rows
+// 16 rt .. 16 rt + 15 (G heads x rows, row = qr * G + head) against keys
+// 16 kq .. 16 kq + 15 of every stage: QK on v_mfma_f32_16x16x32_f16 (A = K
+// rows, B = q'), P.V on v_mfma_f32_16x16x16_f16 with P straight from the
+// score tile as an fp16 high part plus an fp16 remainder (every product
+// exact, sums fp32). The four key quarters merge through LDS at the end and the
+// workgroup writes one fp32 partial per row, merged by the block kernels'
+// merge kernel.
+constexpr int kT4vKeys = 64;     // keys a stage
+constexpr int kT4vRows = 32;     // query rows a workgroup (partial row stride)
+constexpr int kT4vWaves = 8;     // two row tiles x four 16-key quarters of a stage
+constexpr int kT4vThreads = 64 * kT4vWaves;
+
+struct T4VerifyArgs {
+    const uint8_t* k_codes;   // [hkv][cap][D/2]
+    const uint32_t* k_side;   // [hkv][cap] half2(k_rescale, 0)
+    const uint8_t* v_codes;   // [hkv][cap][D/2]
+    const uint32_t* v_side;   // [hkv][cap] half2(v_norm, v_rescale)
+    const float* cb;          // 16 centroids
+    const f16* qs;            // [hq][Tq][D] q' = f16(q_rot * scale * log2 e)
+    float* part_o;            // [hkv][nc][kT4vRows][D]
+    float2* part_ml;          // [hkv][nc][kT4vRows] (m in natural units, l)
+    int cap, T, Tq, G, R, nc, kps;
+};
+
+template <int D>
+struct T4vShape {
+    static constexpr int KROW = D + 8;                 // K row stride in LDS (halves)
+    static constexpr int VROW = kT4vKeys + 4;          // V^T row stride (halves), 8-byte rows
+    static constexpr int KBUF = kT4vKeys * KROW;       // halves a K buffer
+    static constexpr int VBUF = D * VROW;              // halves a V buffer
+    static constexpr size_t lds = (size_t)2 * (KBUF + VBUF) * sizeof(f16) + 16 * sizeof(float);
+};
+
+template <int D>
+__global__ __launch_bounds__(kT4vThreads) void turbo4_verify_kernel(T4VerifyArgs a) {
+    using S = T4vShape<D>;
+    constexpr int NM = D / 32, NT = D / 16, KS = kT4vKeys;
+    constexpr int KROW = S::KROW, VROW = S::VROW;
+    constexpr int CH = D / 32;              // 16-byte code chunks a row (32 coordinates each)
+    constexpr int NTH = kT4vThreads, NKW = kT4vWaves / 2;
+    constexpr int KW = KS / NKW;            // keys a wave a stage (one 16-key MFMA tile)
+    static_assert(KW == 16, "one 16-key tile a wave a stage");
+    constexpr int NCH = KS * CH;            // K (and V) chunks a stage
+    constexpr int NJ = (NCH + NTH - 1) / NTH;  // chunks a thread
+    extern __shared__ __attribute__((aligned(16))) char lds_raw[];
+    f16* const sK = (f16*)lds_raw;                          // [2][KS][KROW]
+    f16* const sV = sK + 2 * S::KBUF;                       // [2][D][VROW]
+    float* const s_cb = (float*)(sV + 2 * S::VBUF);         // [16]
+
+    const int c = blockIdx.x, h = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r16 = lane & 15, g = lane >> 4;
+    const int rt = wave & 1, kq = wave >> 1;
+    if (tid < 16) s_cb[tid] = a.cb[tid];
+    const int k0 = c * a.kps;
+    const int k1 = min(a.T, k0 + a.kps);
+    const int n_st = (k1 - k0 + KS - 1) / KS;
+
+    // q' as the B operand: column r16 = row 16 rt + r16 (head row % G, query
+    // row row / G), dims 32m + 8g .. +7.
+    const int row = 16 * rt + r16;
+    const bool row_ok = row < a.R;
+    const int qr = row_ok ? row / a.G : 0, gh = row_ok ? row % a.G : 0;
+    const int lim = row_ok ? a.T - a.Tq + qr : -1;  // last key the row sees
+    const bool tile_live = 16 * rt < a.R;            // wave-uniform
+    half8 qb[NM];
+    {
+        const f16* qrow = a.qs + ((int64_t)(h * a.G + gh) * a.Tq + qr) * D;
+#pragma unroll
+        for (int m = 0; m < NM; m++)
+            qb[m] = row_ok ? *(const half8*)(qrow + 32 * m + 8 * g) : half8{};
+    }
+
+    // A stage's codes: K chunk j of this thread = key (t / CH), chunk t % CH
+    // (8 lanes a 128-byte row); V chunk j = key t % KS, chunk t / KS (a wave
+    // covers 64 consecutive keys of one chunk, so the transposed writes hit 32
+    // distinct banks). Keys past the range load as zeros.
+    struct Stage {
+        u32x4 kc[NJ], vc[NJ];
+        uint32_t kr[NJ], vr[NJ];
+    };
+    const int64_t hrow = (int64_t)h * a.cap;
+    auto load = [&](Stage& st, int s) {
+        const int base = k0 + s * KS;
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const int t = tid + NTH * j;
+            const int kk = base + t / CH, kc = t % CH;
+            const int vk = base + t % KS, vcn = t / KS;
+            st.kc[j] = u32x4{0u, 0u, 0u, 0u};
+            st.vc[j] = u32x4{0u, 0u, 0u, 0u};
+            st.kr[j] = st.vr[j] = 0u;
+            if (t >= NCH) continue;
+            if (kk < k1) {
+                st.kc[j] = *(const u32x4*)(a.k_codes + (hrow + kk) * (D / 2) + 16 * kc);
+                st.kr[j] = a.k_side[hrow + kk];
+            }
+            if (vk < k1) {
+                st.vc[j] = *(const u32x4*)(a.v_codes + (hrow + vk) * (D / 2) + 16 * vcn);
+                st.vr[j] = a.v_side[hrow + vk];
+            }
+        }
+    };
+    auto store = [&](const Stage& st, int b) {
+        f16* const K = sK + b * S::KBUF;
+        f16* const V = sV + b * S::VBUF;
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const int t = tid + NTH * j;
+            if (t >= NCH) continue;
+            {
+                const int key = t / CH, ch = t % CH;
+                const float r = (float)__builtin_bit_cast(half2v, st.kr[j]).x;
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    half8 o;
+#pragma unroll
+                    for (int n = 0; n < 8; n++) o[n] = f16_of_product(s_cb[(st.kc[j][w] >> (4 * n)) & 15u], r);
+                    *(half8*)(K + key * KROW + 32 * ch + 8 * w) = o;
+                }
+            }
+            {
+                const int key = t % KS, ch = t / KS;
+                const float r = (float)__builtin_bit_cast(half2v, st.vr[j]).y;
+#pragma unroll
+                for (int w = 0; w < 4; w++)
+#pragma unroll
+                    for (int n = 0; n < 8; n++)
+                        V[(32 * ch + 8 * w + n) * VROW + key] =
+                            f16_of_product(s_cb[(st.vc[j][w] >> (4 * n)) & 15u], r);
+            }
+        }
+    };
+
+    float m_run = -INFINITY;  // running max of row r16 (log2 domain)
+    float l_run = 0.0f;       // this lane's share of the row's sum
+    float4v acc[NT];          // rows 4g + i of the tile, dims 16 mm + r16
+#pragma unroll
+    for (int mm = 0; mm < NT; mm++) acc[mm] = float4v{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](int b, int s) {
+        const f16* const K = sK + b * S::KBUF;
+        const f16* const V = sV + b * S::VBUF;
+        const int kb = k0 + s * KS + KW * kq;  // the wave's first key of the stage
+        float sc[1][4];
+        {
+            constexpr int u = 0;
+            float4v sacc = {0.f, 0.f, 0.f, 0.f};
+            const f16* krow = K + (KW * kq + r16) * KROW + 8 * g;
+#pragma unroll
+            for (int m = 0; m < NM; m++)
+                sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const half8*)(krow + 32 * m), qb[m],
+                                                              sacc, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int key = kb + 16 * u + 4 * g + i;
+                sc[u][i] = key < k1 && key <= lim ? sacc[i] : -INFINITY;
+            }
+        }
+        float mx = fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3]));
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx);
+        const float mref = m_new == -INFINITY ? 0.0f : m_new;
+        if (__any(m_new != m_run)) {
+            const float corr = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - mref);
+            l_run *= corr;
+            float f[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) f[i] = __shfl(corr, 4 * g + i);
+#pragma unroll
+            for (int mm = 0; mm < NT; mm++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[mm][i] *= f[i];
+        }
+        m_run = m_new;
+        {
+            constexpr int u = 0;
+            half4v ph, pl;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float p = __builtin_amdgcn_exp2f(sc[u][i] - mref);
+                l_run += p;
+                ph[i] = (f16)p;
+                pl[i] = (f16)(p - (float)ph[i]);
+            }
+            const f16* vcol = V + r16 * VROW + KW * kq + 4 * g;
+#pragma unroll
+            for (int mm = 0; mm < NT; mm++) {
+                const half4v vb = *(const half4v*)(vcol + 16 * mm * VROW);
+                acc[mm] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, vb, acc[mm], 0, 0, 0);
+                acc[mm] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, vb, acc[mm], 0, 0, 0);
+            }
+        }
+    };
+
+    // Codes of stage s + 1 sit in the stage being stored, those of s + 2 / s + 3
+    // are in flight; one barrier a stage.
+    Stage s0, s1;
+    if (n_st > 0) load(s0, 0);
+    if (n_st > 1) load(s1, 1);
+    __syncthreads();  // s_cb
+    if (n_st > 0) {
+        store(s0, 0);
+        if (n_st > 2) load(s0, 2);
+    }
+    __syncthreads();
+    auto round = [&](Stage& nx, int s) {
+        if (s + 1 < n_st) {
+            store(nx, (s + 1) & 1);
+            if (s + 3 < n_st) load(nx, s + 3);
+        }
+        if (tile_live) compute(s & 1, s);
+        __syncthreads();
+    };
+    for (int s = 0; s < n_st; s += 2) {
+        round(s1, s);
+        if (s + 1 < n_st) round(s0, s + 1);
+    }
+
+    // ---- the four key quarters of each row tile: kq > 0 park (m, l, O) in
+    // LDS, kq = 0 folds them in and writes the partial.
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
+    float* const park = (float*)lds_raw;  // [2 row tiles][NKW - 1][NT * 4 + 2][64]
+    constexpr int PS = (NT * 4 + 2) * 64;
+    static_assert((size_t)2 * (NKW - 1) * PS * sizeof(float) <= T4vShape<D>::lds,
+                  "parked quarters fit");
+    if (kq > 0) {
+        float* pw = park + (rt * (NKW - 1) + kq - 1) * PS;
+#pragma unroll
+        for (int mm = 0; mm < NT; mm++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) pw[(mm * 4 + i) * 64 + lane] = acc[mm][i];
+        pw[(NT * 4) * 64 + lane] = m_run;
+        pw[(NT * 4 + 1) * 64 + lane] = l_run;
+    }
+    __syncthreads();
+    if (kq > 0 || !tile_live) return;
+    const float* pws = park + rt * (NKW - 1) * PS;
+    float mq[NKW], fq[NKW];
+    mq[0] = m_run;
+#pragma unroll
+    for (int q = 1; q < NKW; q++) mq[q] = pws[(q - 1) * PS + (NT * 4) * 64 + lane];
+    float M = mq[0];
+#pragma unroll
+    for (int q = 1; q < NKW; q++) M = fmaxf(M, mq[q]);
+    float L = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NKW; q++) {
+        fq[q] = mq[q] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mq[q] - M);
+        L += (q == 0 ? l_run : pws[(q - 1) * PS + (NT * 4 + 1) * 64 + lane]) * fq[q];
+    }
+    float F[NKW][4];
+#pragma unroll
+    for (int q = 0; q < NKW; q++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) F[q][i] = __shfl(fq[q], 4 * g + i);
+    const int64_t pbase = ((int64_t)h * a.nc + c) * kT4vRows;
+    if (g == 0 && row_ok) a.part_ml[pbase + row] = float2{M * kLn2, L};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int orow = 16 * rt + 4 * g + i;
+        if (orow >= a.R) continue;
+        float* prow = a.part_o + (pbase + orow) * D;
+#pragma unroll
+        for (int mm = 0; mm < NT; mm++) {
+            float o = acc[mm][i] * F[0][i];
+#pragma unroll
+            for (int q = 1; q < NKW; q++)
+                o = __builtin_fmaf(pws[(q - 1) * PS + (mm * 4 + i) * 64 + lane], F[q][i], o);
+            prow[16 * mm + r16] = o;
+        }
+    }
+}
+
 // Snapshot planes <-> the side arrays: [hkv][n] k_rescale, v_norms, v_rescale.
 __global__ void turbo4_side_export_kernel(const uint32_t* __restrict__ k_side,
                                           const uint32_t* __restrict__ v_side, int hkv, int cap,
@@ -481,6 +796,109 @@ int KVCache::turbo4_import(int n, const void* kp, const void* kr, const void* vp
     return QW_OK;
 }
 
+// Fused causal verify route: rotate q into the K basis (times scale * log2 e),
+// the fused kernel's split partials, the merge, the rotation back.
+static int turbo4_verify(KVCache& c, const void* q, int n_q_heads, int n_rows, float scale,
+                         void* out, hipStream_t stream) {
+    const int D = c.D, T = c.offset, G = n_q_heads / c.hkv, R = G * n_rows;
+    const int qrows = n_q_heads * n_rows;
+    // about one workgroup a CU: splits of whole 64-key stages
+    const int want = std::max(1, std::min(256 / c.hkv, (T + kT4vKeys - 1) / kT4vKeys));
+    const int kps = ((T + want - 1) / want + kT4vKeys - 1) / kT4vKeys * kT4vKeys;
+    const int nc = (T + kps - 1) / kps;
+    const size_t q_bytes = (size_t)qrows * D * sizeof(f16);
+    const size_t po_bytes = (size_t)c.hkv * nc * kT4vRows * D * sizeof(float);
+    const size_t need = 2 * q_bytes + po_bytes + (size_t)c.hkv * nc * kT4vRows * sizeof(float2);
+
+    T4Workspace& w = g_ws[c.device];
+    std::lock_guard<std::mutex> lock(w.m);
+    if (!w.last) QW_HIP_CHECK(hipEventCreateWithFlags(&w.last, hipEventDisableTiming));
+    if (need > w.bytes) {
+        if (w.buf) {
+            QW_HIP_CHECK(hipDeviceSynchronize());
+            (void)hipFree(w.buf);
+            w.buf = nullptr;
+            w.bytes = 0;
+        }
+        const size_t nb = need + need / 4;
+        if (hipMalloc(&w.buf, nb) != hipSuccess) {
+            (void)hipGetLastError();
+            w.buf = nullptr;
+            set_error("turbo4 attention: workspace hipMalloc failed");
+            return QW_ERR_OUT_OF_MEMORY;
+        }
+        w.bytes = nb;
+    } else {
+        QW_HIP_CHECK(hipStreamWaitEvent(stream, w.last, 0));
+    }
+    f16* q_s = (f16*)w.buf;
+    f16* o_rot = (f16*)((char*)w.buf + q_bytes);
+    float* part_o = (float*)((char*)w.buf + 2 * q_bytes);
+    float2* part_ml = (float2*)((char*)w.buf + 2 * q_bytes + po_bytes);
+    const float* tab = c.t4_tables;
+    const float post = scale * 1.4426950408889634f;  // fp32, as the reference forms it
+
+    T4VerifyArgs a;
+    a.k_codes = (const uint8_t*)c.k_data;
+    a.k_side = c.k_params;
+    a.v_codes = (const uint8_t*)c.v_data;
+    a.v_side = c.v_params;
+    a.qs = q_s;
+    a.part_o = part_o;
+    a.part_ml = part_ml;
+    a.cap = c.cap;
+    a.T = T;
+    a.Tq = n_rows;
+    a.G = G;
+    a.R = R;
+    a.nc = nc;
+    a.kps = kps;
+    const dim3 rg((qrows + 3) / 4), vg(nc, c.hkv);
+    if (D == 256) {
+        using TT = T4Tab<256>;
+        a.cb = tab + TT::cb;
+        hipLaunchKernelGGL(turbo4_rotate_scaled_kernel<256>, rg, dim3(256), 0, stream,
+                           (const f16*)q, q_s, qrows, tab + TT::k_s1, tab + TT::k_s2, post);
+        constexpr size_t sh = T4vShape<256>::lds;
+        static bool attr = false;
+        if (!attr) {
+            QW_HIP_CHECK(hipFuncSetAttribute((const void*)turbo4_verify_kernel<256>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)sh));
+            attr = true;
+        }
+        hipLaunchKernelGGL(turbo4_verify_kernel<256>, vg, dim3(kT4vThreads), sh, stream, a);
+    } else {
+        using TT = T4Tab<128>;
+        a.cb = tab + TT::cb;
+        hipLaunchKernelGGL(turbo4_rotate_scaled_kernel<128>, rg, dim3(256), 0, stream,
+                           (const f16*)q, q_s, qrows, tab + TT::k_s1, tab + TT::k_s2, post);
+        constexpr size_t sh = T4vShape<128>::lds;
+        static bool attr = false;
+        if (!attr) {
+            QW_HIP_CHECK(hipFuncSetAttribute((const void*)turbo4_verify_kernel<128>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)sh));
+            attr = true;
+        }
+        hipLaunchKernelGGL(turbo4_verify_kernel<128>, vg, dim3(kT4vThreads), sh, stream, a);
+    }
+    QW_HIP_CHECK(hipGetLastError());
+    int rc = launch_partial_merge(part_o, part_ml, nc, kT4vRows, 0, R, c.hkv, D, G, n_rows, o_rot,
+                                  stream);
+    if (rc) return rc;
+    if (D == 256) {
+        using TT = T4Tab<256>;
+        hipLaunchKernelGGL(turbo4_rotate_kernel<256>, rg, dim3(256), 0, stream, o_rot, (f16*)out,
+                           qrows, tab + TT::v_s2, tab + TT::v_s1);
+    } else {
+        using TT = T4Tab<128>;
+        hipLaunchKernelGGL(turbo4_rotate_kernel<128>, rg, dim3(256), 0, stream, o_rot, (f16*)out,
+                           qrows, tab + TT::v_s2, tab + TT::v_s1);
+    }
+    QW_HIP_CHECK(hipGetLastError());
+    QW_HIP_CHECK(hipEventRecord(w.last, stream));
+    return QW_OK;
+}
+
 int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float scale,
                      bool causal, void* out, hipStream_t stream) {
     QW_REQUIRE(q && out, QW_ERR_INVALID_ARGUMENT, "attention: null q/out");
@@ -494,6 +912,11 @@ int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float
     DeviceGuard dg(c.device);
     QW_REQUIRE(dg.ok, QW_ERR_HIP, "attention: hipSetDevice failed");
     const int D = c.D, T = c.offset;
+    // The reference's gate for its fused verify pass (fused_attention.rs:
+    // 70-100, cache.rs:3520-3560): causal, 1..5 query rows, more than 2048
+    // cached tokens; here also G * rows <= 32 (one workgroup's rows).
+    if (causal && n_rows <= 5 && T > 2048 && (n_q_heads / c.hkv) * n_rows <= kT4vRows)
+        return turbo4_verify(c, q, n_q_heads, n_rows, scale, out, stream);
     const int capv = (T + 255) / 256 * 256;
     const size_t kv_bytes = (size_t)c.hkv * capv * D * sizeof(f16);
     const size_t q_bytes = (size_t)n_q_heads * n_rows * D * sizeof(f16);

@@ -177,16 +177,34 @@ def _turbo4_layer(qw_amd, T_prefix, L, causal, seed, D=256, hq=24, hkv=4, rows=N
     tab = oracle.turbo4_tables(D)
     sel = np.arange(L) if rows is None else np.asarray(rows)
     pos = oracle.causal_positions(L, T_prefix + L) if causal else None
-    ref = oracle.turbo4_attention(np.ascontiguousarray(q[:, sel]), snap["k_packed"],
-                                  snap["k_rescale"], snap["v_packed"], snap["v_rescale"], tab,
-                                  1.0 / 16, None if pos is None else np.ascontiguousarray(pos[sel]))
+    if fused_verify_route(T_prefix + L, L, causal, hq // hkv):
+        ref = oracle.turbo4_fused_verify(np.ascontiguousarray(q[:, sel]), snap["k_packed"],
+                                         snap["k_rescale"], snap["v_packed"], snap["v_rescale"],
+                                         tab, 1.0 / 16, np.ascontiguousarray(pos[sel]))
+    else:
+        ref = oracle.turbo4_attention(np.ascontiguousarray(q[:, sel]), snap["k_packed"],
+                                      snap["k_rescale"], snap["v_packed"], snap["v_rescale"], tab,
+                                      1.0 / 16,
+                                      None if pos is None else np.ascontiguousarray(pos[sel]))
     return out[:, sel], ref, cache, (q, k, v)
+
+
+def fused_verify_route(T, L, causal, G):
+    """The reference's gate for its fused Turbo4 verify pass (fused_attention.rs:
+    70-100): causal, 1..5 rows, more than 2048 cached tokens (here also
+    G * rows <= 32); everything else takes the dequantize-then-SDPA route."""
+    return causal and L <= 5 and T > 2048 and G * L <= 32
 
 
 @pytest.mark.parametrize("T_prefix,L,causal,D", [
     (4095, 1, False, 256),    # decode (the fp16 decode kernel on the rotated expansion)
-    (2999, 2, True, 256),     # 2-row verify, still the decode kernel (G * L = 12)
-    (4090, 5, True, 256),     # 5-row verify (the reference's fused-kernel case), block kernel
+    (2999, 2, True, 256),     # 2-row verify past 2048 tokens: the fused verify kernel
+    (4090, 5, True, 256),     # 5-row verify (G * L = 30 rows): fused
+    (2046, 3, True, 256),     # 2049 tokens: fused, one partial key stage per split
+    (2040, 3, True, 256),     # 2043 tokens: below the gate, the dequantize route
+    (5000, 1, True, 256),     # causal single row: fused
+    (3333, 4, True, 128),     # head_dim 128: fused
+    (65532, 4, True, 256),    # 65536 tokens, 64 key stages a split
     (1000, 16, True, 256),    # 16-row verify block
     (900, 128, True, 256),    # prefill chunk
     (777, 1, False, 128),     # head_dim 128

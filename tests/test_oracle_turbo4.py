@@ -171,3 +171,51 @@ def test_expand_rotated_is_fp32_product_then_fp16():
     got = oracle.turbo4_expand_rotated(packed, np.array([r]), tab)[0]
     want = np.array([np.float16(np.float32(c) * np.float32(r)) for c in tab["cb"]]).repeat(8)
     np.testing.assert_array_equal(got, want)
+
+
+def _fused_case(seed, hkv=2, G=3, L=3, T=300, D=128):
+    r = rng(seed)
+    tab = oracle.turbo4_tables(D)
+    k = r.standard_normal((hkv, T, D))
+    v = r.standard_normal((hkv, T, D))
+    ki, _, kr, _ = oracle.turbo4_quantize(k, tab["k_s1"], tab["k_s2"], tab)
+    vi, _, vr, _ = oracle.turbo4_quantize(v, tab["v_s1"], tab["v_s2"], tab)
+    q = r.standard_normal((hkv * G, L, D)).astype(np.float16)
+    return q, oracle.turbo4_pack(ki), kr, oracle.turbo4_pack(vi), vr, tab
+
+
+def test_fused_verify_zero_query_is_the_visible_value_mean():
+    """q = 0 makes every visible score 0: each row's output is the plain mean of
+    the V expansions it sees (rows see t <= pos), rotated back -- a closed form
+    that fixes the causal cut and the V rotation."""
+    q, kp, kr, vp, vr, tab = _fused_case(3)
+    q[:] = 0
+    hq, L, D = q.shape
+    T = kp.shape[1]
+    pos = oracle.causal_positions(L, T)
+    out = oracle.turbo4_fused_verify(q, kp, kr, vp, vr, tab, 1.0 / 16, pos).astype(np.float64)
+    v = oracle.turbo4_expand_rotated(vp, vr, tab).astype(np.float64)
+    G = hq // kp.shape[0]
+    for h in range(hq):
+        for r_ in range(L):
+            mean = v[h // G, : pos[r_] + 1].mean(0)
+            want = oracle.turbo4_rotate(mean, tab["v_s2"], tab["v_s1"])
+            np.testing.assert_allclose(out[h, r_], want, atol=2e-3, rtol=2e-3)
+
+
+def test_fused_verify_agrees_with_the_dequantize_route():
+    """The fused pass (fp32 scores, log2 domain) and the dequantize-then-SDPA
+    route (fp16 scores) compute the same attention up to their roundings: a
+    dropped log2(e), a wrong scale or a transposed rotation would move the
+    outputs by far more than this bound."""
+    q, kp, kr, vp, vr, tab = _fused_case(4)
+    hq, L, D = q.shape
+    T = kp.shape[1]
+    pos = oracle.causal_positions(L, T)
+    fused = oracle.turbo4_fused_verify(q, kp, kr, vp, vr, tab, 1.0 / 16, pos).astype(np.float64)
+    route = oracle.turbo4_attention(q, kp, kr, vp, vr, tab, 1.0 / 16, pos).astype(np.float64)
+    err = np.abs(fused - route).max()
+    assert err < 1e-2, err
+    wrong = oracle.turbo4_fused_verify(q, kp, kr, vp, vr, tab, 1.0 / 16 / 1.4426950408889634,
+                                       pos).astype(np.float64)
+    assert np.abs(wrong - route).max() > 3 * err
