@@ -83,10 +83,12 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 // f16 of an fp32 product, rounded first to fp32 (the reference multiplies in
 // fp32 and then casts); the register pin keeps the compiler from fusing the
-// multiply and the conversion into one singly rounded mixed-precision op.
+// multiply and the conversion into one singly rounded mixed-precision op. The
+// pin is not volatile: a volatile one is a scheduling barrier, which
+// serialized every table lookup feeding a product behind the previous one.
 __device__ __forceinline__ f16 f16_of_product(float a, float b) {
     float p = a * b;
-    asm volatile("" : "+v"(p));
+    asm("" : "+v"(p));
     return (f16)p;
 }
 
@@ -346,7 +348,7 @@ __global__ __launch_bounds__(256) void turbo4_rotate_scaled_kernel(
 #pragma unroll
     for (int j = 0; j < VPL; j++) {
         float v = (y[j] * wht_scale(D)) * s_out[lane * VPL + j];
-        asm volatile("" : "+v"(v));
+        asm("" : "+v"(v));
         o[lane * VPL + j] = f16_of_product(v, post);
     }
 }
