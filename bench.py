@@ -228,6 +228,21 @@ def bench_decode(torch, qw_amd, steps: int, warmup: int, bits: int = 4, T_prefix
             "attn_ms": attn_ms, "bytes_layer": bytes_layer, "bytes_attn": bytes_attn}
 
 
+def bench_turbo4_verify(torch, qw_amd, steps: int, warmup: int, T_prefix: int = 32768,
+                        L: int = 4):
+    """A Turbo4 causal verify block (L draft rows, the reference's fused-pass
+    case) at the config-2 geometry: update_and_causal_attention of L tokens,
+    routed to the fused verify kernel (scored straight from the packed codes).
+    Timed eagerly, like the decode route."""
+    ls = LayerSet(torch, qw_amd, 4, 4, T_prefix, L, LAYERS, causal=True, mode="turbo4")
+    ls.warm(warmup)
+    rounds = max(1, steps // LAYERS)
+    ms = ls.time_eager(rounds)
+    T = ls.T
+    ls.close()
+    return {"T": T, "L": L, "layer_ms": ms}
+
+
 def bench_turbo4_decode(torch, qw_amd, steps: int, warmup: int, T_prefix: int = 32768):
     """The reference's served default KV mode at the config-2 geometry:
     update_and_attention of one token on a Turbo4 cache (rotate q, expand the
@@ -665,6 +680,11 @@ def main() -> int:
         extra["turbo4_decode"] = {
             "us_per_layer_eager": round(t4["layer_ms"] * 1e3, 2), "keys": t4["T"],
             "route": "rotate q, expand rotated K/V to fp16, fp16 decode, rotate back"}
+        log("bench: Turbo4 fused causal verify (4 rows, config-2 geometry)")
+        tv = bench_turbo4_verify(torch, qw_amd, steps, args.warmup)
+        extra["turbo4_verify"] = {
+            "us_per_layer_eager": round(tv["layer_ms"] * 1e3, 2), "keys": tv["T"], "rows": tv["L"],
+            "route": "rotate q, fused verify kernel on the packed codes, merge, rotate back"}
         line["extra"] = extra
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
