@@ -139,7 +139,12 @@ int qw_kv_dequantize(const qw_kv_cache* cache, int start, int n, void* k_out, vo
  *   causal: bottom-right, row r sees keys t <= offset_after - n_rows + r;
  *   out [n_q_heads][n_rows][head_dim] fp16.
  * Scores are formed as f16(f16(scale) * q) . k and rounded to fp16 before
- * the fp32 softmax, as MLX's SDPA forms them. */
+ * the fp32 softmax, as MLX's SDPA forms them.
+ * On a Turbo4 cache the reference's routing applies: causal blocks of 1..5
+ * rows over more than 2048 tokens (and G * n_rows <= 32) take its fused
+ * verify pass (turbo4_attention.cpp:45-264: q' = f16(q_rot * scale * log2 e),
+ * fp32 scores from the packed codes); every other call takes its
+ * dequantize-then-SDPA route (turbo/sparse_v.rs:1051-1072). */
 int qw_kv_update_and_attention(qw_kv_cache* cache, const void* q, int n_q_heads, int n_rows,
                                const void* k_new, const void* v_new, float scale, int causal,
                                void* out, void* stream);
