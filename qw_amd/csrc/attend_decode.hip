@@ -66,6 +66,9 @@ struct DecodeShape {
 // holds one sub-chunk's loads at a time and latency is hidden by the other
 // waves of its SIMD: 12 waves (3 a SIMD, <= 168 registers each) where one
 // stage fits that budget, 8 (2 a SIMD) for the larger 8-bit / fp16 stages.
+#ifndef QW_DECODE_QREG
+#define QW_DECODE_QREG 1
+#endif
 #ifndef QW_DECODE_WAVES_4BIT
 #define QW_DECODE_WAVES_4BIT 8
 #endif
@@ -260,6 +263,20 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
         }
     }
     __syncthreads();
+    // 4-bit: the wave keeps its q' fragments in registers (32 VGPRs fit the
+    // budget) instead of reading them from LDS for every 16-key tile.
+    constexpr bool kQReg = BITS == 4 && QW_DECODE_QREG;
+    half8 qreg[NM];
+    if constexpr (kQReg) {
+#pragma unroll
+        for (int m = 0; m < NM; m++) qreg[m] = sm_q[m][lane];
+    }
+    auto qop = [&](int m) -> half8 {
+        if constexpr (kQReg)
+            return qreg[m];
+        else
+            return sm_q[m][lane];
+    };
     const int lim = a.causal ? a.T - a.Tq + (row_ok ? rho / a.G : 0) : a.T - 1;
 
     float m_run = -INFINITY;  // softmax reference of row r16 (natural units)
@@ -287,9 +304,9 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
                 for (int mi = 0; mi < 4; mi++) {
                     const int m = 4 * cc + mi;
                     acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        deq4<FAST>(st.kc[0][cc][mi], p0, magic), sm_q[m][lane], acc0, 0, 0, 0);
+                        deq4<FAST>(st.kc[0][cc][mi], p0, magic), qop(m), acc0, 0, 0, 0);
                     acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        deq4<FAST>(st.kc[1][cc][mi], p1, magic), sm_q[m][lane], acc1, 0, 0, 0);
+                        deq4<FAST>(st.kc[1][cc][mi], p1, magic), qop(m), acc1, 0, 0, 0);
                 }
             }
         } else if constexpr (BITS == 8) {
