@@ -536,7 +536,8 @@ def summarize_pmc(fetch_db: str, write_db: str, out: str) -> int:
 
 def summarize_trace(db_path: str, out: str, command: str) -> int:
     """Per-kernel dispatch count and duration (avg / min / max, µs) from a
-    rocprofv3 --kernel-trace database, as a short text table."""
+    rocprofv3 --kernel-trace database, as a short text table: every kernel of
+    this library, then the others (torch's input generation) by total time."""
     import sqlite3
 
     con = sqlite3.connect(db_path)
@@ -546,7 +547,9 @@ def summarize_trace(db_path: str, out: str, command: str) -> int:
     lines = ["# rocprofv3 kernel trace summary", "", "command:", f"  {command}",
              "  python3 bench.py --summarize-trace <db> --out <this file>", "",
              f"{'kernel':<72} {'n':>6} {'avg_us':>9} {'min_us':>9} {'max_us':>9}"]
-    for name, n, avg, mn, mx, _ in rows[:14]:
+    ours = [r for r in rows if "qw::" in r[0] or "_ZN2qw" in r[0]]
+    rows = ours + [r for r in rows if r not in ours][:4]
+    for name, n, avg, mn, mx, _ in rows:
         short = name if len(name) <= 72 else name[:69] + "..."
         lines.append(f"{short:<72} {n:>6} {avg / 1e3:>9.2f} {mn / 1e3:>9.2f} {mx / 1e3:>9.2f}")
     os.makedirs(os.path.dirname(os.path.abspath(out)), exist_ok=True)
