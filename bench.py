@@ -12,7 +12,9 @@ HBM). The 16 layer calls of a round are replayed as one HIP graph, so the
 figure is device time, not Python launch overhead (the eager figure is
 reported beside it). The other configurations are reported under "extra":
 config 3 (2048-row prefill chunk, TFLOP/s against the MFMA peak), config 4
-(16-row verify block), config 5 (D-LSA gathered read), config 1. The CPU
+(16-row verify block), config 5 (D-LSA gathered read), config 1, and the
+neighbouring paths at the config-2 geometry: Int8 decode, the D-LSA K1 select,
+the fused q/k RoPE, Turbo4 decode and the Turbo4 fused causal verify. The CPU
 baseline is the oracle's restatement of the MLX CPU stream, timed on a bounded
 sample on this host.
 
