@@ -49,7 +49,8 @@ def test_golden_qwen_layer(m):
     out = _np(qw_amd.sparse_attention(q, k, v, lists, lengths, 256 ** -0.5))[0]
     ref = d[f"{m}.attention_out"].transpose(1, 0, 2)
     assert_close(out, ref, f"qwen_layer {m}")
-    for parts in (1, 3, 16):
+    # one pass, ragged splits, and part counts that put one or two workgroups on a CU
+    for parts in (1, 3, 16, 64, 128):
         o2 = _np(qw_amd.sparse_attention_with(q, k, v, lists, lengths, 256 ** -0.5, parts, 0))[0]
         assert_close(o2, ref, f"qwen_layer {m} parts={parts}")
 
