@@ -220,6 +220,21 @@ def test_turbo4_attention_matches_oracle(T_prefix, L, causal, D):
     assert_close(out, ref, f"turbo4 T{T_prefix}+{L} causal={causal} D{D}")
 
 
+@pytest.mark.parametrize("T_prefix,L,hq,hkv,D", [
+    (3000, 4, 32, 4, 256),    # G * L = 32: both row tiles of the fused kernel full
+    (2500, 5, 8, 8, 256),     # no GQA sharing (G = 1), 5 rows
+    (4000, 3, 16, 2, 128),    # head_dim 128, two KV heads
+    (3000, 5, 56, 8, 256),    # G * L = 35 > 32: the dequantize route
+])
+def test_turbo4_verify_geometries(T_prefix, L, hq, hkv, D):
+    import qw_amd
+
+    out, ref, _, _ = _turbo4_layer(qw_amd, T_prefix, L, True, seed=T_prefix + 7 * L + hq,
+                                   D=D, hq=hq, hkv=hkv)
+    assert np.isfinite(out).all()
+    assert_close(out, ref, f"turbo4 verify T{T_prefix}+{L} hq{hq} hkv{hkv} D{D}")
+
+
 def test_turbo4_attention_without_append_and_reuse():
     """attention() over the cache as it is equals update_and_attention's
     output, and repeated calls (shared workspace reuse) repeat it exactly."""
