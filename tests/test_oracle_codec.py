@@ -2,9 +2,11 @@
 
 The reference holds no stored affine-KV vectors (it calls MLX `quantize` as a
 black box), so the codec is pinned by what the algorithm fixes: hand-derived
-known answers on grid-aligned groups, exact invariants (edge decodes exactly,
-codes in range, constant groups), brute force (no other code is nearer), and a
-separate numpy restatement for the packing. CPU only.
+known answers on grid-aligned groups and on groups where MLX's scale refit
+(scale = edge / q0) moves the stored scale, exact invariants (edge decodes
+exactly, codes in range, constant groups), brute force (no other code is
+nearer), a separate numpy restatement for the packing, and a count of the
+exact .5 ties the tie rule decides on the config data. CPU only.
 """
 import numpy as np
 import pytest
@@ -109,7 +111,134 @@ def test_constant_and_zero_groups(oracle_lib, bits):
         assert np.array_equal(oracle_lib.affine_dequantize(codes, s, b, bits), w)
 
 
-def test_rint_ties_to_even(oracle_lib):
+def _codes_of(oracle_lib, vals, fill, bits):
+    w = np.array(list(vals) + [fill[i % len(fill)] for i in range(64 - len(vals))], np.float16)
+    codes, s, b = oracle_lib.affine_quantize(w[None], bits)
+    return w, _unpack(codes[0], bits, 64), s[0, 0], b[0, 0]
+
+
+# Hand-derived known answers on groups that are NOT grid-aligned, so MLX's
+# refit `scale = edge / q0` (q0 = rint(edge / scale0)) moves the stored fp16
+# scale away from f16((max - min) / n_bins). Each docstring carries the
+# arithmetic; fp16 ulps: 2^-14 in [2^-4, 2^-3), 2^-13 in [2^-3, 2^-2),
+# 2^-16 in [2^-6, 2^-5). The codes are chosen away from .5 ties except in the
+# tie case, whose ties are exact.
+
+def test_refit_known_answer_4bit_negative_edge(oracle_lib):
+    """4-bit {-1.0, 0.3, 0, -0.5, 0.1, -0.25, fill 0 / -0.5}.
+    f16(0.3) = 0.2998046875, f16(0.1) = 0.0999755859375. |min| > |max|: edge
+    = -1.0, scale0 = 1.2998046875 / 15 = 0.0866536..., q0 = rint(-11.540) =
+    -12, refit scale = -1 / -12 = 1/12, bias = -1. f16(1/12) = 1365 * 2^-14 =
+    0.08331298828125 (without the refit: f16(0.0866536) = 0.086669921875).
+    Codes (w + 1) * 12: -1 -> 0; 0.2998 -> 15.598 -> 16, clamped to 15;
+    0 -> 12; -0.5 -> 6; 0.09998 -> 13.200 -> 13; -0.25 -> 9."""
+    w, c, s, b = _codes_of(oracle_lib, [-1.0, 0.3, 0.0, -0.5, 0.1, -0.25], [0.0, -0.5], 4)
+    assert s.view(np.uint16) == np.float16(0.08331298828125).view(np.uint16)
+    assert b == np.float16(-1.0)
+    assert c[:8].tolist() == [0, 15, 12, 6, 13, 9, 12, 6]
+    # dequant of code 12 (the zero): 12 * 0.08331298828125 = 0.999755859375
+    # = 2047.5 * 2^-11 is a tie in fp16 and rounds to even, 1.0; + (-1) = 0.
+    # Code 13: 13 * s = 1.08306884765625 -> f16 1.0830078125 (2^-10 ulp),
+    # - 1 = 0.0830078125.
+    deq = oracle_lib.affine_dequantize(*oracle_lib.affine_quantize(w[None], 4), 4)[0]
+    assert deq[2] == np.float16(0.0) and deq[4] == np.float16(0.0830078125)
+
+
+def test_refit_known_answer_4bit_positive_edge(oracle_lib):
+    """4-bit {2.0, -0.7, 0, 0.5, -0.5, 1.5, fill 0.5 / 1.5}. f16(0.7) =
+    0.7001953125. |max| > |min|: edge = 2.0, scale0 = -2.7001953125 / 15 =
+    -0.180013..., q0 = rint(-11.110) = -11, refit scale = 2 / -11 =
+    -0.181818..., bias = 2. f16 = -(1489 * 2^-13) = -0.1817626953125 (without
+    the refit: -(1475 * 2^-13) = -0.1800537109375). Codes (w - 2) / scale =
+    (2 - w) * 5.5: 2 -> 0; -0.7002 -> 14.851 -> 15; 0 -> 11; 0.5 -> 8.25 -> 8;
+    -0.5 -> 13.75 -> 14; 1.5 -> 2.75 -> 3."""
+    _, c, s, b = _codes_of(oracle_lib, [2.0, -0.7, 0.0, 0.5, -0.5, 1.5], [0.5, 1.5], 4)
+    assert s.view(np.uint16) == np.float16(-0.1817626953125).view(np.uint16)
+    assert b == np.float16(2.0)
+    assert c[:8].tolist() == [0, 15, 11, 8, 14, 3, 8, 3]
+
+
+def test_refit_known_answer_8bit_negative_edge(oracle_lib):
+    """8-bit {-3, 1, 0, 0.5, -2, fill 0 / 0.5}. edge = -3, scale0 = 4 / 255 =
+    0.0156863, q0 = rint(-191.25) = -191, refit scale = 3 / 191 = 0.0157068,
+    bias = -3. f16 = 1029 * 2^-16 = 0.0157012939453125 (without the refit:
+    1028 * 2^-16 = 0.01568603515625). Codes (w + 3) * 191 / 3: -3 -> 0;
+    1 -> 254.67 -> 255; 0 -> 191; 0.5 -> 222.83 -> 223; -2 -> 63.67 -> 64."""
+    _, c, s, b = _codes_of(oracle_lib, [-3.0, 1.0, 0.0, 0.5, -2.0], [0.0, 0.5], 8)
+    assert s.view(np.uint16) == np.float16(0.0157012939453125).view(np.uint16)
+    assert b == np.float16(-3.0)
+    assert c[:7].tolist() == [0, 255, 191, 223, 64, 191, 223]
+
+
+def test_refit_known_answer_8bit_positive_edge(oracle_lib):
+    """8-bit {5, -1.3, 0, 2.5, 1, -1, fill 0 / 2.5}. f16(1.3) = 1.2998046875.
+    edge = 5, scale0 = -6.2998046875 / 255 = -0.0247051, q0 = rint(-202.39) =
+    -202, refit scale = 5 / -202 = -0.0247525, bias = 5. f16 = -(1622 *
+    2^-16) = -0.024749755859375 (without the refit: -(1619 * 2^-16) =
+    -0.0247039794921875). Codes (5 - w) * 40.4: 5 -> 0; -1.2998 -> 254.51 ->
+    255; 0 -> 202; 2.5 -> 101; 1 -> 161.6 -> 162; -1 -> 242.4 -> 242."""
+    _, c, s, b = _codes_of(oracle_lib, [5.0, -1.3, 0.0, 2.5, 1.0, -1.0], [0.0, 2.5], 8)
+    assert s.view(np.uint16) == np.float16(-0.024749755859375).view(np.uint16)
+    assert b == np.float16(5.0)
+    assert c[:8].tolist() == [0, 255, 202, 101, 162, 242, 202, 101]
+
+
+def test_refit_known_answer_exact_ties(oracle_lib):
+    """4-bit {-1, 0.8, -0.5625, -0.4375, ...}: f16(0.8) = 0.7998046875,
+    scale0 = 1.7998046875 / 15 = 0.119987, q0 = rint(-8.334) = -8, refit
+    scale = 1/8 exactly (without the refit f16(0.119987) = 0.1199951171875).
+    (w + 1) * 8 is then exact: 0.7998 -> 14.398 -> 14 (15 without the refit);
+    -0.5625 -> 3.5 and -0.4375 -> 4.5 are exact .5 ties, both rounding to the
+    even code 4 (ties away from zero would give 4 and 5; without the refit
+    they would be 3.646 -> 4 and 4.688 -> 5)."""
+    _, c, s, b = _codes_of(oracle_lib, [-1.0, 0.8, -0.5625, -0.4375], [-0.5625, -0.4375], 4)
+    assert s == np.float16(0.125) and b == np.float16(-1.0)
+    assert c[:6].tolist() == [0, 14, 4, 4, 4, 4]
+
+
+def _tie_count(w, bits):
+    """Exact .5 ties of (w - bias) / scale in fp32 under the MLX formulas."""
+    n_bins = np.float32((1 << bits) - 1)
+    x = w.astype(np.float32).reshape(-1, 64)
+    mx, mn = x.max(1), x.min(1)
+    neg = np.abs(mn) > np.abs(mx)
+    scale = np.maximum((mx - mn) / n_bins, np.float32(1e-7)).astype(np.float32)
+    scale = np.where(neg, scale, -scale).astype(np.float32)
+    edge = np.where(neg, mn, mx).astype(np.float32)
+    q0 = np.rint(edge / scale).astype(np.float32)
+    nz = q0 != 0
+    scale = np.where(nz, edge / np.where(nz, q0, 1), scale).astype(np.float32)
+    bias = np.where(nz, edge, 0).astype(np.float32)
+    q = ((x - bias[:, None]) / scale[:, None]).astype(np.float32)
+    tie = (q - np.floor(q)) == np.float32(0.5)
+    return int(tie.sum()), tie, q
+
+
+@pytest.mark.parametrize("case", ["c2", "c3"])
+def test_tie_counts_on_config_data(oracle_lib, case):
+    """Counts the exact .5 ties that the tie rule decides on the seeded
+    config data (c2: K/V [4, 32769, 256] N(0,1) x per-head U(0.5, 2), 4-bit;
+    c3: K/V [4, 18432, 256] N(0,1), 8-bit) and checks that the oracle gives
+    each of them the even code. The counts are recorded so a change of the
+    data or the formulas shows."""
+    want = {"c2": (13361, 13271), "c3": (13168, 12940)}[case]
+    r = np.random.default_rng(2 if case == "c2" else 3)
+    T, bits = (32769, 4) if case == "c2" else (18432, 8)
+    jit = r.uniform(0.5, 2.0, (4, 1, 1)) if case == "c2" else np.ones((4, 1, 1))
+    got = []
+    for _ in range(2):  # K, then V
+        w = (r.standard_normal((4, T, 256)) * jit).astype(np.float16)
+        n, tie, q = _tie_count(w, bits)
+        got.append(n)
+        rows = np.unique(np.nonzero(tie)[0])[:4000]  # groups holding a tie
+        wg = w.reshape(-1, 64)[rows]
+        codes, _, _ = oracle_lib.affine_quantize(wg, bits)
+        c = _unpack(codes.reshape(-1), bits, wg.size).reshape(wg.shape)
+        t = tie[rows]
+        n_bins = (1 << bits) - 1
+        want_c = np.clip(np.floor(q[rows]) + (np.floor(q[rows]) % 2 != 0), 0, n_bins)
+        assert np.array_equal(c[t], want_c[t].astype(np.int64))
+    assert tuple(got) == want, got
     """Exact .5 ties round to even (std::rint, MLX's CPU quantizer). Values
     0, 0.5, 1.5, 2.5, ..., 7.5 with the min as edge and scale 1: codes for the
     half-integers x.5 are the even neighbour."""
