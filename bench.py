@@ -8,19 +8,25 @@ Timed steps rotate over 16 distinct layer caches (16 x 37.7 MB = 604 MB, more
 than the 256 MB Infinity Cache), so every step reads HBM.
 
 value = algorithmic bytes of a layer call / its time, GB/s (inputs resident in
-HBM). The 16 layer calls of a round are replayed as one HIP graph, so the
-figure is device time, not Python launch overhead (the eager figure is
-reported beside it). The other configurations are reported under "extra":
-config 3 (2048-row prefill chunk, TFLOP/s against the MFMA peak), config 4
-(16-row verify block), config 5 (D-LSA gathered read), config 1, and the
-neighbouring paths at the config-2 geometry: Int8 decode, the D-LSA K1 select,
-the fused q/k RoPE, Turbo4 decode and the Turbo4 fused causal verify. The CPU
-baseline is the oracle's restatement of the MLX CPU stream, timed on a bounded
-sample on this host.
+HBM). The timed region of a measurement is exactly K = --steps layer calls,
+cycling over the 16 caches, captured as one HIP graph and replayed between two
+HIP events; --reps (at least 50) such replays are timed and ms_per_step is
+their median (min and max are reported beside it), so the figure is device
+time, not Python launch overhead (the eager figure is reported too). The other
+configurations are reported under "extra", each the median of at least 50
+replays: config 3 (2048-row prefill chunk over 4 rotated caches, 392 MB,
+TFLOP/s against the MFMA peak), config 4 (16-row verify block), the served 4-
+and 5-row verify blocks, config 5 (D-LSA gathered read), config 1, and the
+neighbouring paths at the config-2 geometry: Int8 decode, the D-LSA K1
+select, the fused q/k RoPE, Turbo4 decode and the Turbo4 fused causal
+verify. Counter-derived figures (bytes read from memory, MFMA busy cycles)
+come from the committed profiles/counters_<cfg>.txt summaries. The CPU
+baseline is the oracle's restatement of the MLX CPU stream, timed on a
+bounded sample on this host.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
-    python bench.py --pmc-workload          # short run for rocprofv3 --pmc passes
-    python bench.py --summarize-pmc FETCH_DB WRITE_DB --out profiles/<name>.txt
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--reps R] [--no-cpu] [--no-extra]
+    python bench.py --pmc-workload c2|c3|c4|c5   # short run for rocprofv3 --pmc passes
+    python bench.py --summarize-counters CFG DIR --out profiles/counters_<cfg>.txt
     python bench.py --summarize-trace DB --out profiles/<name>.txt
 """
 from __future__ import annotations
@@ -39,7 +45,6 @@ HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = 2500.0  # dense fp16
 LAYERS = 16
 HQ, HKV, D = 24, 4, 256
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attend_decode_c2_traffic.txt")
 COPY_BYTES = 256 << 20  # the calibration copy of --pmc-workload
 
 
@@ -69,13 +74,14 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--pmc-workload", action="store_true",
-                    help="a 256 MiB copy then 16 config-2 attention calls, for counter runs")
-    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DB", "WRITE_DB"))
+    ap.add_argument("--reps", type=int, default=50, help="timed graph replays (at least 50)")
+    ap.add_argument("--pmc-workload", choices=["c2", "c3", "c4", "c5"],
+                    help="a 256 MiB copy then the configuration's attention calls, for counter runs")
+    ap.add_argument("--summarize-counters", nargs=2, metavar=("CFG", "DIR"))
     ap.add_argument("--summarize-trace", metavar="DB")
     ap.add_argument("--command", default="rocprofv3 --kernel-trace --stats -d gpurun_out/ktrace "
                     "-o run -- python3 bench.py --no-cpu")
-    ap.add_argument("--out", default=TRAFFIC_FILE)
+    ap.add_argument("--out", default=os.path.join(ROOT, "profiles", "summary.txt"))
     return ap.parse_args()
 
 
@@ -119,17 +125,51 @@ def make_caches(torch, qw_amd, g, bits, T_prefix, cap, layers, jitter=True, mode
     return caches
 
 
-def graph_time(torch, body, rounds: int, calls_per_round: int) -> float:
-    """Capture body() (calls_per_round library calls) once as a HIP graph,
-    replay it `rounds` times between events; ms per call."""
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        body()
-    for _ in range(3):
+def _stats(ms):
+    ms = sorted(ms)
+    n = len(ms)
+    med = ms[n // 2] if n % 2 else 0.5 * (ms[n // 2 - 1] + ms[n // 2])
+    return {"median": med, "min": ms[0], "max": ms[-1], "n": n}
+
+
+def replay_stats(torch, call, n_units: int, steps: int, reps: int):
+    """Time `steps` consecutive calls, call(u) for u = j, j+1, ... (mod
+    n_units), as one HIP graph replay between two events; `reps` replays.
+    Graph j starts at unit (j * steps) mod n_units, and the graphs are
+    replayed in turn, so successive replays keep walking the units (every
+    unit's data leaves the 256 MB Infinity Cache before it is read again).
+    Returns ms per call: median, min and max over the replays."""
+    import math
+
+    n_graphs = n_units // math.gcd(steps, n_units)
+    # Capture on a stream of our own, after one eager pass over the units on
+    # it, so split-K workspaces kept per stream exist before the capture.
+    cs = torch.cuda.Stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cs):
+        for u in range(n_units):
+            call(u)
+    torch.cuda.synchronize()
+    graphs = []
+    for j in range(n_graphs):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cs):
+            for i in range(steps):
+                call((j * steps + i) % n_units)
+        graphs.append(g)
+    for g in graphs:  # one untimed replay each
         g.replay()
-    ms = Timer(torch).run(g.replay, rounds) / (rounds * calls_per_round)
-    del g
-    return ms
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(reps)]
+    for k, (s, e) in enumerate(evs):
+        s.record()
+        graphs[k % n_graphs].replay()
+        e.record()
+    torch.cuda.synchronize()
+    out = _stats([s.elapsed_time(e) / steps for s, e in evs])
+    del graphs
+    return out
 
 
 class LayerSet:
@@ -174,33 +214,34 @@ class LayerSet:
     def stream(self):
         return self.torch.cuda.current_stream(self.torch.device("cuda:0")).cuda_stream
 
-    def time_layers(self, rounds):
-        n = len(self.caches)
-        ms = graph_time(self.torch, lambda: [self.layer_call(i, self.stream()) for i in range(n)],
-                        rounds, n)
-        return ms
+    def time_layers(self, steps, reps):
+        """update_and_attention layer calls: `steps` per graph replay, `reps`
+        replays; ms per call (median / min / max)."""
+        return replay_stats(self.torch, lambda i: self.layer_call(i, self.stream()),
+                            len(self.caches), steps, reps)
 
-    def time_eager(self, rounds):
+    def time_eager(self, steps):
+        """`steps` eager layer calls (launch overhead included), bracketed by
+        synchronizations; ms per call."""
         n = len(self.caches)
-        return Timer(self.torch).run(lambda: [self.layer_call(i, self.stream()) for i in range(n)],
-                                     rounds) / (rounds * n)
+        it = iter(range(steps))
+        return Timer(self.torch).run(lambda: self.layer_call(next(it) % n, self.stream()),
+                                     steps) / steps
 
-    def time_attention(self, rounds):
+    def time_attention(self, steps, reps):
+        """Attention-only calls over the caches with the L new rows appended."""
         n = len(self.caches)
         for i in range(n):
-            c = self.caches[i][0]
-            c.update(self.kn[i], self.vn[i])
-        ms = graph_time(self.torch, lambda: [self.attn_call(i, self.stream()) for i in range(n)],
-                        rounds, n)
+            self.caches[i][0].update(self.kn[i], self.vn[i])
+        st = replay_stats(self.torch, lambda i: self.attn_call(i, self.stream()), n, steps, reps)
         for i in range(n):
             self.caches[i][0].trim(self.L)
-        return ms
+        return st
 
     def warm(self, n_calls):
         n = len(self.caches)
-        for j in range(max(1, n_calls // n)):
-            for i in range(n):
-                self.layer_call(i, self.stream())
+        for j in range(max(1, n_calls)):
+            self.layer_call(j % n, self.stream())
         self.torch.cuda.synchronize()
 
     def close(self):
@@ -210,24 +251,22 @@ class LayerSet:
         self.torch.cuda.empty_cache()
 
 
-def bench_decode(torch, qw_amd, steps: int, warmup: int, bits: int = 4, T_prefix: int = 32768,
-                 mode=None):
+def bench_decode(torch, qw_amd, steps: int, warmup: int, reps: int, bits: int = 4,
+                 T_prefix: int = 32768, mode=None):
     """Config 2 (bits 4, 32768 + 1) or config 1 (bits 8, 4095 + 1); `mode`
     overrides the cache mode (e.g. "int8", stored in the 8-bit layout)."""
     ls = LayerSet(torch, qw_amd, 2, bits, T_prefix, 1, LAYERS, causal=False, mode=mode)
     ls.warm(warmup)
-    # one attention-only round too, so the split-K workspace exists before capture
-    ls.time_attention(1)
-    rounds = max(1, steps // LAYERS)
-    eager_ms = ls.time_eager(rounds)
-    layer_ms = ls.time_layers(rounds)
-    attn_ms = ls.time_attention(rounds)
+    eager_ms = ls.time_eager(steps)
+    layer = ls.time_layers(steps, reps)
+    attn = ls.time_attention(steps, reps)
     T = ls.T
     ls.close()
     bytes_attn = T * HKV * kv_bytes_per_token_head(bits) + 2 * HQ * D * 2
     bytes_layer = bytes_attn + 2 * HKV * D * 2 + HKV * kv_bytes_per_token_head(bits) // 2
-    return {"T": T, "bits": bits, "rounds": rounds, "layer_ms": layer_ms, "eager_layer_ms": eager_ms,
-            "attn_ms": attn_ms, "bytes_layer": bytes_layer, "bytes_attn": bytes_attn}
+    return {"T": T, "bits": bits, "layer": layer, "layer_ms": layer["median"],
+            "eager_layer_ms": eager_ms, "attn": attn, "attn_ms": attn["median"],
+            "bytes_layer": bytes_layer, "bytes_attn": bytes_attn}
 
 
 def bench_turbo4_verify(torch, qw_amd, steps: int, warmup: int, T_prefix: int = 32768,
@@ -238,8 +277,7 @@ def bench_turbo4_verify(torch, qw_amd, steps: int, warmup: int, T_prefix: int = 
     Timed eagerly, like the decode route."""
     ls = LayerSet(torch, qw_amd, 4, 4, T_prefix, L, LAYERS, causal=True, mode="turbo4")
     ls.warm(warmup)
-    rounds = max(1, steps // LAYERS)
-    ms = ls.time_eager(rounds)
+    ms = ls.time_eager(steps)
     T = ls.T
     ls.close()
     return {"T": T, "L": L, "layer_ms": ms}
@@ -253,14 +291,13 @@ def bench_turbo4_decode(torch, qw_amd, steps: int, warmup: int, T_prefix: int = 
     event, which a HIP graph capture does not take."""
     ls = LayerSet(torch, qw_amd, 3, 4, T_prefix, 1, LAYERS, causal=False, mode="turbo4")
     ls.warm(warmup)
-    rounds = max(1, steps // LAYERS)
-    ms = ls.time_eager(rounds)
+    ms = ls.time_eager(steps)
     T = ls.T
     ls.close()
-    return {"T": T, "layer_ms": ms, "rounds": rounds}
+    return {"T": T, "layer_ms": ms}
 
 
-def bench_select(torch, qw_amd, steps: int, T: int = 131072):
+def bench_select(torch, qw_amd, reps: int, T: int = 131072):
     """D-LSA K1 select at the served defaults (window 512, sink 4, top-k 4096,
     top-p 1024, 8-key buckets, 64 buckets a block) for one decode row at
     context T: synthetic N(0,1) bucket scores. Raw ABI calls with preallocated
@@ -293,12 +330,11 @@ def bench_select(torch, qw_amd, steps: int, T: int = 131072):
     for _ in range(5):
         call()
     torch.cuda.synchronize()
-    ms = graph_time(torch, lambda: [call() for _ in range(LAYERS)], max(1, steps // LAYERS),
-                    LAYERS)
+    ms = replay_stats(torch, lambda i: call(), 1, LAYERS, reps)["median"]
     return {"ms": ms, "buckets": n_b, "list_len": int(lengths.item()), "width": W}
 
 
-def bench_rope(torch, qw_amd, steps: int, L: int = 2048):
+def bench_rope(torch, qw_amd, reps: int, L: int = 2048):
     """Fused q/k RoPE: the standalone op over a 2048-token QKV chunk (bytes:
     the chunk read once, q/k/v written once), and the RoPE-append of one
     decode token into a 4-bit cache (append then trim, graph-replayed)."""
@@ -321,8 +357,7 @@ def bench_rope(torch, qw_amd, steps: int, L: int = 2048):
 
     chunk()
     torch.cuda.synchronize()
-    chunk_ms = graph_time(torch, lambda: [chunk() for _ in range(LAYERS)], max(1, steps // LAYERS),
-                          LAYERS)
+    chunk_ms = replay_stats(torch, lambda i: chunk(), 1, LAYERS, reps)["median"]
     cache = qw_amd.KVCache("affine4", HKV, D, capacity=4096)
     cache.update(torch.randn((HKV, 4000, D), device=dev, generator=g).half(),
                  torch.randn((HKV, 4000, D), device=dev, generator=g).half())
@@ -339,30 +374,29 @@ def bench_rope(torch, qw_amd, steps: int, L: int = 2048):
 
     one()
     torch.cuda.synchronize()
-    one_ms = graph_time(torch, lambda: [one() for _ in range(LAYERS)], max(1, steps // LAYERS),
-                        LAYERS)
+    one_ms = replay_stats(torch, lambda i: one(), 1, LAYERS, reps)["median"]
     cache.close()
     return {"chunk_ms": chunk_ms, "chunk_bytes": 2 * L * W * 2, "token_ms": one_ms}
 
 
-def bench_block(torch, qw_amd, steps: int, bits: int, T_prefix: int, L: int, layers: int):
-    """Config 3 (prefill chunk) / config 4 (verify block): append L rows and
-    attend them causally; graph-replayed over `layers` caches."""
-    ls = LayerSet(torch, qw_amd, 3 + L, bits, T_prefix, L, layers, causal=True)
-    ls.warm(2 * layers)
-    ls.time_attention(1)
-    rounds = max(2, steps // (4 * layers))
-    layer_ms = ls.time_layers(rounds)
-    attn_ms = ls.time_attention(rounds)
+def bench_block(torch, qw_amd, reps: int, bits: int, T_prefix: int, L: int, layers: int,
+                causal: bool = True):
+    """Config 3 (prefill chunk) / config 4 (verify block) and the served
+    verify blocks: append L rows and attend them causally, graph-replayed over
+    `layers` caches (one call a cache a replay, `reps` replays)."""
+    ls = LayerSet(torch, qw_amd, 3 + L, bits, T_prefix, L, layers, causal=causal)
+    ls.warm(layers)
+    layer = ls.time_layers(layers, reps)
+    attn = ls.time_attention(layers, reps)
     T = ls.T
     ls.close()
-    flops = attn_flops(L, T, True)
+    flops = attn_flops(L, T, causal)
     kv = T * HKV * kv_bytes_per_token_head(bits)
-    return {"T": T, "L": L, "bits": bits, "layer_ms": layer_ms, "attn_ms": attn_ms,
-            "flops": flops, "kv_bytes": kv}
+    return {"T": T, "L": L, "bits": bits, "layer": layer, "layer_ms": layer["median"],
+            "attn": attn, "attn_ms": attn["median"], "flops": flops, "kv_bytes": kv}
 
 
-def bench_dlsa(torch, qw_amd, steps: int, T: int = 131072, layers: int = LAYERS):
+def bench_dlsa(torch, qw_amd, reps: int, T: int = 131072, layers: int = LAYERS):
     """Config 5: one decode row, 4612-entry list (4 sinks + 512 window + 8 whole
     512-key blocks drawn without replacement from the blocks fully inside
     [4, window start)), fp16 KV [4, 131072, 256] per layer, 16 layers rotated."""
@@ -398,13 +432,38 @@ def bench_dlsa(torch, qw_amd, steps: int, T: int = 131072, layers: int = LAYERS)
     for i in range(layers):
         call(i, st)
     torch.cuda.synchronize()
-    rounds = max(1, steps // layers)
-    ms = graph_time(torch, lambda: [call(i, torch.cuda.current_stream(dev).cuda_stream)
-                                    for i in range(layers)], rounds, layers)
+    st = replay_stats(torch, lambda i: call(i, torch.cuda.current_stream(dev).cuda_stream),
+                      layers, layers, reps)
+    ms = st["median"]
     bytes_call = W * HKV * 2 * D * 2 + HQ * D * 2 * 2 + W * 4
     del ks, vs
     torch.cuda.empty_cache()
-    return {"T": T, "W": int(W), "ms": ms, "bytes": bytes_call}
+    return {"T": T, "W": int(W), "ms": ms, "stats": st, "bytes": bytes_call}
+
+
+def cpu_threads():
+    """Threads for the CPU baseline: every core this process may run on,
+    capped by OMP_NUM_THREADS when the environment sets it (the GPU box's
+    harness sets it to the box's CPU share)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_baseline(seconds: float, threads: int):
@@ -435,12 +494,56 @@ def cpu_baseline(seconds: float, threads: int):
 
 
 # ----------------------------------------------------------- counter runs
+#
+# Per configuration, four rocprofv3 --pmc passes of `bench.py --pmc-workload
+# <cfg>` (one pass a counter group; rocprofv3 does not split counters over
+# passes), then `bench.py --summarize-counters <cfg> <dir>` writes
+# profiles/counters_<cfg>.txt:
+#   fetch  FETCH_SIZE                      (KiB read from memory per dispatch)
+#   write  WRITE_SIZE                      (KiB written)
+#   ea     TCC_EA0_RDREQ_{32B,64B,128B,DRAM}_sum (read requests by size, and
+#          those addressed to DRAM: bytes = 32 n32 + 64 n64 + 128 n128)
+#   mfma   SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_INSTS_VALU
+#          SQ_INSTS_MFMA SQ_BUSY_CYCLES GRBM_GUI_ACTIVE
+# Each workload first runs one plain 256 MiB device copy (HIP's copyBuffer):
+# its counter readings for a known byte count calibrate the byte counters.
 
-def pmc_workload() -> int:
+PMC_PASSES = {
+    "fetch": "FETCH_SIZE",
+    "write": "WRITE_SIZE",
+    "ea": "TCC_EA0_RDREQ_32B_sum TCC_EA0_RDREQ_64B_sum TCC_EA0_RDREQ_128B_sum "
+          "TCC_EA0_RDREQ_DRAM_sum",
+    "mfma": "SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_INSTS_VALU SQ_INSTS_MFMA "
+            "SQ_BUSY_CYCLES GRBM_GUI_ACTIVE",
+}
+PMC_CONFIGS = {
+    # cfg: (what the dispatches are, algorithmic bytes a call, algorithmic flops a call)
+    "c2": "config 2: 16 qw_kv_attention calls, 4-bit, 32769 keys, 16 caches",
+    "c3": "config 3: 4 qw_kv_attention calls, 2048 causal rows over 18432 keys, 8-bit, 4 caches",
+    "c4": "config 4: 16 qw_kv_attention calls, 16 causal rows over 65552 keys, 4-bit, 16 caches",
+    "c5": "config 5: 16 qw_dlsa_sparse_attention calls, 4612-entry list, fp16 KV, 16 layers",
+}
+
+
+def pmc_algorithmic(cfg: str):
+    """(bytes, flops) of one call of the configuration's attention."""
+    if cfg == "c2":
+        T = 32769
+        return T * HKV * kv_bytes_per_token_head(4) + 2 * HQ * D * 2, attn_flops(1, T, False)
+    if cfg == "c3":
+        T, L = 18432, 2048
+        return T * HKV * kv_bytes_per_token_head(8) + 2 * HQ * L * D * 2, attn_flops(L, T, True)
+    if cfg == "c4":
+        T, L = 65552, 16
+        return T * HKV * kv_bytes_per_token_head(4) + 2 * HQ * L * D * 2, attn_flops(L, T, True)
+    W = 4612
+    return W * HKV * 2 * D * 2 + HQ * D * 2 * 2 + W * 4, 4 * D * HQ * W
+
+
+def pmc_workload(cfg: str) -> int:
     """What the rocprofv3 --pmc passes profile: one plain 256 MiB device copy
-    (the calibration kernel, HIP's copyBuffer: FETCH_SIZE / WRITE_SIZE of a
-    known byte count; the largest copyBuffer dispatch of the run),
-    then 16 config-2 attention calls over 16 distinct caches."""
+    (the calibration kernel, HIP's copyBuffer), then the configuration's
+    attention calls over distinct caches."""
     import torch
 
     import qw_amd
@@ -453,19 +556,28 @@ def pmc_workload() -> int:
     dst.copy_(src)  # a device-to-device memcpy: HIP's copyBuffer kernel
     torch.cuda.synchronize()
     del src, dst
-    ls = LayerSet(torch, qw_amd, 2, 4, 32768, 1, LAYERS, causal=False)
-    for i in range(LAYERS):
+    if cfg == "c5":
+        bench_dlsa(torch, qw_amd, 1)
+        print("pmc workload c5 done", flush=True)
+        return 0
+    bits, T0, L, n, causal = {"c2": (4, 32768, 1, LAYERS, False),
+                              "c3": (8, 16384, 2048, 4, True),
+                              "c4": (4, 65536, 16, LAYERS, True)}[cfg]
+    ls = LayerSet(torch, qw_amd, 2, bits, T0, L, n, causal=causal)
+    for i in range(n):
         ls.caches[i][0].update(ls.kn[i], ls.vn[i])
     torch.cuda.synchronize()
-    for i in range(LAYERS):
+    for i in range(n):
         ls.attn_call(i, ls.stream())
     torch.cuda.synchronize()
     ls.close()
-    print("pmc workload done", flush=True)
+    print(f"pmc workload {cfg} done", flush=True)
     return 0
 
 
-def _pmc_per_kernel(db_path: str, counter: str):
+def _pmc_per_kernel(db_path: str, counters):
+    """{kernel name: {counter: [value per dispatch]}} from a rocprofv3 --pmc
+    database."""
     import sqlite3
 
     con = sqlite3.connect(db_path)
@@ -477,58 +589,98 @@ def _pmc_per_kernel(db_path: str, counter: str):
     cnt_col = next(c for c in cols if c in ("counter_name", "counter"))
     val_col = next(c for c in cols if c in ("value", "counter_value"))
     disp_col = next((c for c in cols if "dispatch" in c and "id" in c), None)
-    if disp_col:
-        q = (f"select {name_col}, sum({val_col}) from {ctab} where {cnt_col} = ? "
-             f"group by {name_col}, {disp_col}")
-    else:
-        q = f"select {name_col}, {val_col} from {ctab} where {cnt_col} = ?"
     per = {}
-    for name, v in con.execute(q, (counter,)):
-        per.setdefault(name, []).append(float(v))
+    for counter in counters:
+        if disp_col:
+            q = (f"select {name_col}, sum({val_col}) from {ctab} where {cnt_col} = ? "
+                 f"group by {name_col}, {disp_col}")
+        else:
+            q = f"select {name_col}, {val_col} from {ctab} where {cnt_col} = ?"
+        for name, v in con.execute(q, (counter,)):
+            per.setdefault(name, {}).setdefault(counter, []).append(float(v))
     return per
 
 
-def summarize_pmc(fetch_db: str, write_db: str, out: str) -> int:
-    fetch = _pmc_per_kernel(fetch_db, "FETCH_SIZE")
-    write = _pmc_per_kernel(write_db, "WRITE_SIZE")
+def _find_db(root: str):
+    import glob
 
-    def pick(d, key):
-        k = next(n for n in d if key in n)
-        v = d[k]
-        return k, sum(v) / len(v), len(v)
+    hits = sorted(glob.glob(os.path.join(root, "**", "*results.db"), recursive=True))
+    if not hits:
+        raise FileNotFoundError(f"no rocprofv3 results database under {root}")
+    return hits[-1]
 
-    # the calibration copy is the largest copyBuffer dispatch of the run
-    copy_k = next(n for n in fetch if "copyBuffer" in n)
-    copy_fetch = max(fetch[copy_k])
-    copy_write = max(write[next(n for n in write if "copyBuffer" in n)])
-    f_scale = (COPY_BYTES / 1024.0) / copy_fetch    # true KiB per counted KiB
-    w_scale = (COPY_BYTES / 1024.0) / copy_write
-    att_k, att_fetch, n_f = pick(fetch, "attend_decode_kernel")
-    _, att_write, n_w = pick(write, "attend_decode_kernel")
-    mer_key = next(k for k in ("merge_append_kernel", "decode_merge_kernel") if any(k in n for n in fetch))
-    mer_k, mer_fetch, _ = pick(fetch, mer_key)
-    _, mer_write, _ = pick(write, mer_key)
-    traffic = (att_fetch * f_scale + att_write * w_scale) * 1024.0
-    alg = 32769 * HKV * kv_bytes_per_token_head(4) + 2 * HQ * D * 2
-    lines = [
-        "# HBM traffic of the config-2 attention kernel (rocprofv3 --pmc)",
-        "",
-        "commands:",
-        "  rocprofv3 --pmc FETCH_SIZE -d gpurun_out/pmc_fetch -o run -- python3 bench.py --pmc-workload",
-        "  rocprofv3 --pmc WRITE_SIZE -d gpurun_out/pmc_write -o run -- python3 bench.py --pmc-workload",
-        "  python3 bench.py --summarize-pmc <fetch db> <write db>",
-        "",
-        f"calibration kernel: {copy_k[:90]}",
-        f"  copy of {COPY_BYTES} B: FETCH_SIZE {copy_fetch:.1f} KiB, WRITE_SIZE {copy_write:.1f} KiB",
-        f"  scale factors (true / counted): fetch {f_scale:.4f}, write {w_scale:.4f}",
-        f"kernel: {att_k[:90]} ({n_f} / {n_w} dispatches)",
-        f"  FETCH_SIZE {att_fetch:.1f} KiB/dispatch, WRITE_SIZE {att_write:.1f} KiB/dispatch",
-        f"merge kernel: {mer_k[:90]}",
-        f"  FETCH_SIZE {mer_fetch:.1f} KiB/dispatch, WRITE_SIZE {mer_write:.1f} KiB/dispatch",
-        f"algorithmic bytes per dispatch: {alg}",
-        f"traffic_bytes_per_dispatch = {traffic:.0f}",
-        f"traffic / algorithmic = {traffic / alg:.4f}",
-    ]
+
+def _short(name: str) -> str:
+    base = name.split("(")[0]
+    return base.replace("void ", "").replace("qw::", "")[:60]
+
+
+def summarize_counters(cfg: str, root: str, out: str) -> int:
+    """profiles/counters_<cfg>.txt from the four passes under root/<pass>."""
+    per = {}
+    for ps, counters in PMC_PASSES.items():
+        data = _pmc_per_kernel(_find_db(os.path.join(root, ps)), counters.split())
+        for name, cs in data.items():
+            per.setdefault(name, {}).update(cs)
+
+    def avg(name, c):
+        v = per.get(name, {}).get(c)
+        return sum(v) / len(v) if v else float("nan")
+
+    def big(name, c):
+        v = per.get(name, {}).get(c)
+        return max(v) if v else float("nan")
+
+    copy_k = next(n for n in per if "copyBuffer" in n)
+    cf, cw = big(copy_k, "FETCH_SIZE"), big(copy_k, "WRITE_SIZE")
+    n32, n64, n128 = (big(copy_k, f"TCC_EA0_RDREQ_{b}_sum") for b in ("32B", "64B", "128B"))
+    copy_ea = 32 * n32 + 64 * n64 + 128 * n128
+    f_scale = (COPY_BYTES / 1024.0) / cf
+    w_scale = (COPY_BYTES / 1024.0) / cw
+    ea_scale = COPY_BYTES / copy_ea
+    alg_bytes, alg_flops = pmc_algorithmic(cfg)
+    ours = [n for n in per if "qw::" in n or "_ZN2qw" in n]
+    lines = [f"# Counters of {PMC_CONFIGS[cfg]} (rocprofv3 --pmc)", "", "commands:"]
+    for ps, counters in PMC_PASSES.items():
+        lines.append(f"  rocprofv3 --pmc {counters} -d gpurun_out/pmc_{cfg}/{ps} -o run -- "
+                     f"python3 bench.py --pmc-workload {cfg}")
+    lines += [f"  python3 bench.py --summarize-counters {cfg} gpurun_out/pmc_{cfg} "
+              f"--out profiles/counters_{cfg}.txt", "",
+              f"calibration: copy of {COPY_BYTES} B ({_short(copy_k)}):",
+              f"  FETCH_SIZE {cf:.1f} KiB -> scale {f_scale:.4f}; WRITE_SIZE {cw:.1f} KiB -> "
+              f"scale {w_scale:.4f}",
+              f"  EA read requests 32B/64B/128B {n32:.0f}/{n64:.0f}/{n128:.0f} -> "
+              f"{copy_ea:.0f} B (x{ea_scale:.4f} of the true count)", "",
+              f"algorithmic per call: {alg_bytes} B, {alg_flops} flop", ""]
+    tot_read = tot_write = tot_ea = tot_dram = 0.0
+    for name in ours:
+        n = len(per[name].get("FETCH_SIZE", [])) or 1
+        fr = avg(name, "FETCH_SIZE") * f_scale * 1024.0
+        wr = avg(name, "WRITE_SIZE") * w_scale * 1024.0
+        e32, e64, e128 = (avg(name, f"TCC_EA0_RDREQ_{b}_sum") for b in ("32B", "64B", "128B"))
+        ea = 32 * e32 + 64 * e64 + 128 * e128
+        dram = avg(name, "TCC_EA0_RDREQ_DRAM_sum")
+        ereq = e32 + e64 + e128
+        tot_read += fr
+        tot_write += wr
+        tot_ea += ea
+        tot_dram += ea * (dram / ereq if ereq else 0.0)
+        mb = avg(name, "SQ_VALU_MFMA_BUSY_CYCLES")
+        mops = avg(name, "SQ_INSTS_VALU_MFMA_MOPS_F16")
+        gui = avg(name, "GRBM_GUI_ACTIVE")
+        lines += [f"kernel: {_short(name)} ({n} dispatches)",
+                  f"  read {fr:.0f} B (FETCH_SIZE x scale), EA read {ea:.0f} B "
+                  f"({dram / ereq if ereq else 0:.3f} of the requests to DRAM), "
+                  f"write {wr:.0f} B",
+                  f"  SQ_VALU_MFMA_BUSY_CYCLES {mb:.0f}  GRBM_GUI_ACTIVE {gui:.0f}  "
+                  f"SQ_BUSY_CYCLES {avg(name, 'SQ_BUSY_CYCLES'):.0f}",
+                  f"  SQ_INSTS_VALU_MFMA_MOPS_F16 {mops:.0f} (x512 = {mops * 512:.4g} flop)  "
+                  f"SQ_INSTS_MFMA {avg(name, 'SQ_INSTS_MFMA'):.0f}  "
+                  f"SQ_INSTS_VALU {avg(name, 'SQ_INSTS_VALU'):.0f}"]
+    lines += ["",
+              f"traffic_bytes_per_call = {tot_read + tot_write:.0f}",
+              f"dram_read_bytes_per_call = {tot_dram:.0f}",
+              f"traffic / algorithmic = {(tot_read + tot_write) / alg_bytes:.4f}"]
     os.makedirs(os.path.dirname(os.path.abspath(out)), exist_ok=True)
     with open(out, "w") as f:
         f.write("\n".join(lines) + "\n")
@@ -561,21 +713,32 @@ def summarize_trace(db_path: str, out: str, command: str) -> int:
     return 0
 
 
-def read_traffic():
+def read_counters(cfg: str):
+    """The committed counter summary of a configuration, as numbers."""
+    out = {}
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(os.path.join(ROOT, "profiles", f"counters_{cfg}.txt")) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_dispatch"):
-                    return int(float(line.split("=")[1]))
+                for key in ("traffic_bytes_per_call", "dram_read_bytes_per_call"):
+                    if line.startswith(key):
+                        out[key] = int(float(line.split("=")[1]))
+                if "SQ_VALU_MFMA_BUSY_CYCLES" in line and "mfma_busy_cycles" not in out:
+                    out["mfma_busy_cycles"] = float(line.split()[1])
+                    out["grbm_gui_active"] = float(line.split()[3])
     except OSError:
         pass
-    return None
+    return out
+
+
+def _round_stats(st, scale=1e3, nd=3):
+    return {k: (round(v * scale, nd) if k != "n" else v) for k, v in st.items()}
 
 
 def main() -> int:
     args = parse()
-    if args.summarize_pmc:
-        return summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], args.out)
+    if args.summarize_counters:
+        return summarize_counters(args.summarize_counters[0], args.summarize_counters[1],
+                                  args.out)
     if args.summarize_trace:
         return summarize_trace(args.summarize_trace, args.out, args.command)
     if args.gpus != 1:
@@ -583,7 +746,7 @@ def main() -> int:
                           "across GPUs in design, which is not implemented; run with --gpus 1"}))
         return 2
     if args.pmc_workload:
-        return pmc_workload()
+        return pmc_workload(args.pmc_workload)
     import torch
 
     import qw_amd
@@ -593,12 +756,13 @@ def main() -> int:
         print(json.dumps({"error": "no GPU visible"}))
         return 2
     torch.cuda.set_device(0)
-    steps = max(LAYERS, args.steps // LAYERS * LAYERS)
-    log(f"bench: config 2 decode, {steps} steps, warmup {args.warmup}")
-    dec = bench_decode(torch, qw_amd, steps, args.warmup)
+    steps, reps = max(1, args.steps), max(50, args.reps)
+    log(f"bench: config 2 decode, {steps} steps a replay, {reps} replays, warmup {args.warmup}")
+    dec = bench_decode(torch, qw_amd, steps, args.warmup, reps)
     us_layer = dec["layer_ms"] * 1e3
     value = dec["bytes_layer"] / (dec["layer_ms"] * 1e-3) / 1e9
     achieved = dec["bytes_attn"] / (dec["attn_ms"] * 1e-3) / 1e9
+    c2c = read_counters("c2")
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -616,83 +780,107 @@ def main() -> int:
                                "group 64) + fused dequant-SDPA over 32769 keys",
                    "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "context": dec["T"],
                    "kv_bits": 4, "layers_rotated": LAYERS},
+        "timing": {"method": f"HIP graph of exactly {steps} layer calls (cycling the "
+                             f"{LAYERS} caches), {reps} replays, each between its own events; "
+                             "ms_per_step is the median",
+                   "ms_per_step": _round_stats(dec["layer"], 1.0, 6)},
         "us_per_layer": round(us_layer, 3),
         "us_per_layer_eager": round(dec["eager_layer_ms"] * 1e3, 3),
         "us_attention": round(dec["attn_ms"] * 1e3, 3),
+        "us_attention_stats": _round_stats(dec["attn"]),
         "tokens_per_s": round(1.0 / (dec["layer_ms"] * 1e-3), 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": read_traffic(),
+                     "traffic": c2c.get("traffic_bytes_per_call"),
                      "kernel": "qw_kv_attention: attend_decode_kernel + decode_merge_kernel, "
                                "graph-replayed over 16 caches",
-                     "algorithmic_bytes": dec["bytes_attn"]},
+                     "algorithmic_bytes": dec["bytes_attn"],
+                     "dram_read_bytes": c2c.get("dram_read_bytes_per_call")},
     }
     if not args.no_extra:
         extra = {}
         log("bench: config 3 prefill chunk")
-        pf = bench_block(torch, qw_amd, steps, 8, 16384, 2048, 2)
+        pf = bench_block(torch, qw_amd, reps, 8, 16384, 2048, 4)
         tf = pf["flops"] / (pf["attn_ms"] * 1e-3) / 1e12
+        c3c = read_counters("c3")
         extra["config3_prefill"] = {
             "us_per_layer": round(pf["layer_ms"] * 1e3, 1),
             "us_attention": round(pf["attn_ms"] * 1e3, 1),
+            "us_attention_stats": _round_stats(pf["attn"], 1e3, 1),
             "TFLOP_s": round(tf, 1), "frac_mfma": round(tf / MFMA_PEAK_TFLOPS, 4),
             "TFLOP_s_layer": round(pf["flops"] / (pf["layer_ms"] * 1e-3) / 1e12, 1),
             "tokens_per_s": round(2048 / (pf["layer_ms"] * 1e-3), 1),
-            "flops": pf["flops"], "keys": pf["T"], "rows": 2048, "kv_bits": 8}
+            "flops": pf["flops"], "keys": pf["T"], "rows": 2048, "kv_bits": 8,
+            "layers_rotated": 4, "counters": c3c}
         log("bench: config 4 verify block")
-        vf = bench_block(torch, qw_amd, steps, 4, 65536, 16, LAYERS)
+        vf = bench_block(torch, qw_amd, reps, 4, 65536, 16, LAYERS)
         vt = vf["flops"] / (vf["attn_ms"] * 1e-3) / 1e12
         vg = vf["kv_bytes"] / (vf["attn_ms"] * 1e-3) / 1e9
         extra["config4_verify"] = {
             "us_per_layer": round(vf["layer_ms"] * 1e3, 2),
             "us_attention": round(vf["attn_ms"] * 1e3, 2),
+            "us_attention_stats": _round_stats(vf["attn"], 1e3, 2),
             "TFLOP_s": round(vt, 1), "frac_mfma": round(vt / MFMA_PEAK_TFLOPS, 4),
             "GB_s": round(vg, 1), "frac_hbm": round(vg / HBM_PEAK_GBS, 4),
             "flops": vf["flops"], "kv_bytes": vf["kv_bytes"], "keys": vf["T"], "rows": 16,
-            "kv_bits": 4}
+            "kv_bits": 4, "counters": read_counters("c4")}
+        for rows, ctx in ((4, 32768), (5, 65536)):
+            log(f"bench: served verify block, {rows} rows at {ctx} (4-bit)")
+            sv = bench_block(torch, qw_amd, reps, 4, ctx, rows, LAYERS)
+            st = sv["flops"] / (sv["attn_ms"] * 1e-3) / 1e12
+            sg = sv["kv_bytes"] / (sv["attn_ms"] * 1e-3) / 1e9
+            extra[f"verify_{rows}rows_{ctx // 1024}k"] = {
+                "us_per_layer": round(sv["layer_ms"] * 1e3, 2),
+                "us_attention": round(sv["attn_ms"] * 1e3, 2),
+                "TFLOP_s": round(st, 1), "GB_s": round(sg, 1),
+                "frac_hbm": round(sg / HBM_PEAK_GBS, 4), "keys": sv["T"], "rows": rows,
+                "kv_bits": 4}
         log("bench: config 5 D-LSA read")
-        ds = bench_dlsa(torch, qw_amd, steps)
+        ds = bench_dlsa(torch, qw_amd, reps)
         gbs = ds["bytes"] / (ds["ms"] * 1e-3) / 1e9
         extra["config5_dlsa_decode"] = {
             "us_per_layer": round(ds["ms"] * 1e3, 3), "GB_s": round(gbs, 1),
+            "us_stats": _round_stats(ds["stats"]),
             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "list_width": ds["W"],
-            "context": ds["T"], "algorithmic_bytes": ds["bytes"]}
+            "context": ds["T"], "algorithmic_bytes": ds["bytes"],
+            "counters": read_counters("c5")}
         log("bench: config 1 decode (8-bit, 4096 keys)")
-        c1 = bench_decode(torch, qw_amd, steps, args.warmup, bits=8, T_prefix=4095)
+        c1 = bench_decode(torch, qw_amd, LAYERS, args.warmup, reps, bits=8, T_prefix=4095)
         extra["config1_decode"] = {
             "us_per_layer": round(c1["layer_ms"] * 1e3, 3),
             "us_attention": round(c1["attn_ms"] * 1e3, 3),
             "GB_s": round(c1["bytes_attn"] / (c1["attn_ms"] * 1e-3) / 1e9, 1)}
         log("bench: Int8 decode (config-2 geometry)")
-        i8 = bench_decode(torch, qw_amd, steps, args.warmup, bits=8, T_prefix=32768, mode="int8")
+        i8 = bench_decode(torch, qw_amd, LAYERS, args.warmup, reps, bits=8, T_prefix=32768,
+                          mode="int8")
         extra["int8_decode"] = {
             "us_per_layer": round(i8["layer_ms"] * 1e3, 2),
             "us_attention": round(i8["attn_ms"] * 1e3, 2),
             "GB_s": round(i8["bytes_attn"] / (i8["attn_ms"] * 1e-3) / 1e9, 1)}
         log("bench: D-LSA K1 select")
-        k1 = bench_select(torch, qw_amd, steps)
+        k1 = bench_select(torch, qw_amd, reps)
         extra["dlsa_k1_select"] = {
             "us_per_row": round(k1["ms"] * 1e3, 2), "buckets": k1["buckets"],
             "list_width": k1["width"], "list_len": k1["list_len"]}
         log("bench: fused q/k RoPE")
-        rp = bench_rope(torch, qw_amd, steps)
+        rp = bench_rope(torch, qw_amd, reps)
         extra["rope"] = {
             "us_chunk_2048": round(rp["chunk_ms"] * 1e3, 2),
             "GB_s_chunk": round(rp["chunk_bytes"] / (rp["chunk_ms"] * 1e-3) / 1e9, 1),
             "us_rope_append_1_token": round(rp["token_ms"] * 1e3, 2)}
         log("bench: Turbo4 decode (config-2 geometry)")
-        t4 = bench_turbo4_decode(torch, qw_amd, steps, args.warmup)
+        t4 = bench_turbo4_decode(torch, qw_amd, 4 * LAYERS, args.warmup)
         extra["turbo4_decode"] = {
             "us_per_layer_eager": round(t4["layer_ms"] * 1e3, 2), "keys": t4["T"],
             "route": "rotate q, expand rotated K/V to fp16, fp16 decode, rotate back"}
         log("bench: Turbo4 fused causal verify (4 rows, config-2 geometry)")
-        tv = bench_turbo4_verify(torch, qw_amd, steps, args.warmup)
+        tv = bench_turbo4_verify(torch, qw_amd, 4 * LAYERS, args.warmup)
         extra["turbo4_verify"] = {
             "us_per_layer_eager": round(tv["layer_ms"] * 1e3, 2), "keys": tv["T"], "rows": tv["L"],
             "route": "rotate q, fused verify kernel on the packed codes, merge, rotate back"}
         line["extra"] = extra
     if not args.no_cpu:
-        threads = min(16, os.cpu_count() or 1)
+        threads = cpu_threads()
         log(f"bench: CPU baseline ({threads} threads, ~{args.cpu_seconds:.0f} s)")
         cb = cpu_baseline(args.cpu_seconds, threads)
         line["cpu_baseline"] = {
@@ -701,9 +889,12 @@ def main() -> int:
             "cores": threads,
             "kind": "port",
             "us_per_layer": round(cb["s_per_call"] * 1e6, 1),
+            "nproc": os.cpu_count(),
+            "cpu_model": cpu_model(),
             "sample": f"{cb['calls']} config-2 layer calls (quantize 1 token, dequantize 32769 "
                       f"keys, MLX-rounding SDPA) by the C oracle, a restatement of the MLX CPU "
-                      f"stream (not MLX)",
+                      f"stream (not MLX), threaded over (KV head x query head) on every core "
+                      f"this process may use, capped by OMP_NUM_THREADS",
         }
     print(json.dumps(line), flush=True)
     return 0

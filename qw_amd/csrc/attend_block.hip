@@ -547,12 +547,8 @@ __global__ __launch_bounds__(64 * kBlockWaves, 1) void attend_block_kernel(Block
 template <int BITS, int D, int RT>
 static int launch_block_rt(KVCache& cc, BlockArgs& a, int n_qt, hipStream_t stream) {
     const size_t shmem = (size_t)2 * BlockShape<D>::BUF;
-    static bool attr_set = false;
-    if (!attr_set) {
-        QW_HIP_CHECK(hipFuncSetAttribute((const void*)attend_block_kernel<BITS, D, RT>,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem));
-        attr_set = true;
-    }
+    int rc = ensure_dynamic_lds((const void*)attend_block_kernel<BITS, D, RT>, shmem);
+    if (rc) return rc;
     hipLaunchKernelGGL((attend_block_kernel<BITS, D, RT>), dim3(a.n_split, n_qt, cc.hkv),
                        dim3(64 * kBlockWaves), shmem, stream, a);
     QW_HIP_CHECK(hipGetLastError());
@@ -670,10 +666,10 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     if (n_split > 1) {
         const size_t o_bytes = (size_t)cc.hkv * n_split * t.PR * D * sizeof(float);
         const size_t need = o_bytes + (size_t)cc.hkv * n_split * t.PR * sizeof(float2);
-        rc = cc.ensure_workspace(need);
+        rc = cc.ensure_workspace(need, stream);
         if (rc) return rc;
-        t.part_o = (float*)cc.ws;
-        t.part_ml = (float2*)((char*)cc.ws + o_bytes);
+        t.part_o = (float*)cc.ws_ptr;
+        t.part_ml = (float2*)((char*)cc.ws_ptr + o_bytes);
     }
     rc = launch_one<BITS, D>(cc, t, rt, q_tail, stream);
     if (rc) return rc;

@@ -589,7 +589,7 @@ static int launch_decode_partials(KVCache& cc, const f16* q, int G, int Tq, int 
     const int nc = std::max(1, std::min({per_head, (n_sub + NW - 1) / NW, 4 * kMergeMaxPer}));
     const size_t need = (size_t)cc.hkv * nc * 16 * D * sizeof(float) +
                         (size_t)cc.hkv * nc * 16 * sizeof(float2);
-    int rc = cc.ensure_workspace(need);
+    int rc = cc.ensure_workspace(need, stream);
     if (rc) return rc;
     DecodeArgs a;
     a.k_data = (const uint32_t*)cc.k_data;
@@ -598,8 +598,8 @@ static int launch_decode_partials(KVCache& cc, const f16* q, int G, int Tq, int 
     a.v_params = cc.v_params;
     a.fast_flag = cc.fast_flag;
     a.q = q;
-    a.part_o = (float*)cc.ws;
-    a.part_ml = (float2*)((char*)cc.ws + (size_t)cc.hkv * nc * 16 * D * sizeof(float));
+    a.part_o = (float*)cc.ws_ptr;
+    a.part_ml = (float2*)((char*)cc.ws_ptr + (size_t)cc.hkv * nc * 16 * D * sizeof(float));
     a.cap = cc.cap;
     a.T = T;
     a.Tq = Tq;
@@ -611,14 +611,9 @@ static int launch_decode_partials(KVCache& cc, const f16* q, int G, int Tq, int 
     a.scale_h = (float)(f16)scale;
     a.code_off2 = cc.code_offset2();
     size_t shmem = (size_t)NW * (D / 16) * (((a.R + 3) / 4) * 16 + 1) * 16;  // wave-merge sm_o
-    // Dynamic LDS above 64 KB must be allowed per kernel; raise the limit to
-    // what this launch needs (once per size, per template instance).
-    static size_t attr_max = 0;
-    if (shmem > attr_max) {
-        QW_HIP_CHECK(hipFuncSetAttribute((const void*)attend_decode_kernel<BITS, D>,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem));
-        attr_max = shmem;
-    }
+    // Dynamic LDS above 64 KB must be allowed per kernel and device.
+    rc = ensure_dynamic_lds((const void*)attend_decode_kernel<BITS, D>, shmem);
+    if (rc) return rc;
     hipLaunchKernelGGL((attend_decode_kernel<BITS, D>), dim3(nc, cc.hkv), dim3(64 * NW), shmem,
                        stream, a);
     QW_HIP_CHECK(hipGetLastError());

@@ -22,6 +22,9 @@
 //   Online softmax in the exp2 domain across tiles; the waves merge through
 //   LDS; split-K parts write fp32 partials merged by a second kernel.
 #include <algorithm>
+#include <map>
+#include <mutex>
+#include <string>
 
 #include "kv_cache.hpp"
 
@@ -318,37 +321,15 @@ __global__ __launch_bounds__(256) void dlsa_merge_kernel(const float* __restrict
     }
 }
 
-// Split-K workspace shared by the D-LSA calls of a device (grown on demand).
-struct DlsaWorkspace {
-    void* ptr = nullptr;
-    size_t bytes = 0;
-};
-static DlsaWorkspace g_ws[64];
+// Split-K workspace of the D-LSA calls, one per (device, stream): calls on
+// different streams never share partials. Each is a GrowBuffer, so growth
+// never frees memory a captured graph may still read.
+static std::mutex g_ws_mu;
+static std::map<std::pair<int, hipStream_t>, GrowBuffer> g_ws;
 
-static int dlsa_workspace(int device, size_t need, void** out) {
-    if (device < 0 || device >= 64) {
-        set_error("dlsa: device ordinal out of range");
-        return QW_ERR_INVALID_ARGUMENT;
-    }
-    DlsaWorkspace& w = g_ws[device];
-    if (need > w.bytes) {
-        if (w.ptr) {
-            QW_HIP_CHECK(hipDeviceSynchronize());
-            (void)hipFree(w.ptr);
-            w.ptr = nullptr;
-            w.bytes = 0;
-        }
-        const size_t nb = std::max(need, (size_t)1 << 20);
-        if (hipMalloc(&w.ptr, nb) != hipSuccess) {
-            (void)hipGetLastError();
-            w.ptr = nullptr;
-            set_error("dlsa: workspace hipMalloc failed");
-            return QW_ERR_OUT_OF_MEMORY;
-        }
-        w.bytes = nb;
-    }
-    *out = w.ptr;
-    return QW_OK;
+static int dlsa_workspace(int device, hipStream_t stream, size_t need, void** out) {
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    return g_ws[{device, stream}].get(need, stream, out);
 }
 
 // Launch policy (the reference's auto_parts, mlx_cxx_dlsa_attention.cpp:379-400,
@@ -364,11 +345,15 @@ static int auto_parts(int units, int width) {
     return std::max(1, std::min(parts, 128));
 }
 
-int dlsa_sparse_attention(const void* q, const void* k, const void* v, int64_t khs, int64_t krs,
-                          int64_t vhs, int64_t vrs, const int32_t* lists, const int32_t* lengths,
-                          int n_rows, int width, int n_q_heads, int n_kv_heads, int head_dim,
-                          int n_keys, float scale, int parts, int waves, void* out,
-                          hipStream_t stream) {
+// scratch == nullptr: the split-K partials go to the stream's workspace
+// (allocated or grown on demand); else to `scratch` (scratch_bytes), and an
+// automatic part count is lowered until the partials fit it.
+static int dlsa_sparse_attention_impl(const void* q, const void* k, const void* v, int64_t khs,
+                                      int64_t krs, int64_t vhs, int64_t vrs,
+                                      const int32_t* lists, const int32_t* lengths, int n_rows,
+                                      int width, int n_q_heads, int n_kv_heads, int head_dim,
+                                      int n_keys, float scale, int parts, int waves, void* out,
+                                      hipStream_t stream, void* scratch, size_t scratch_bytes) {
     QW_REQUIRE(q && k && v && lists && lengths && out, QW_ERR_INVALID_ARGUMENT,
                "dlsa_sparse_attention: null pointer");
     QW_REQUIRE(n_kv_heads > 0 && n_q_heads > 0 && n_q_heads % n_kv_heads == 0 && n_keys > 0 &&
@@ -389,8 +374,19 @@ int dlsa_sparse_attention(const void* q, const void* k, const void* v, int64_t k
                "dlsa_sparse_attention: K/V/q must be 16-byte aligned with strides % 8 == 0");
     int dev = 0;
     QW_HIP_CHECK(hipGetDevice(&dev));
-    if (parts <= 0) parts = auto_parts(n_rows * n_kv_heads, width);
+    // bytes of one part's partials: an fp32 output row and an (m, l) pair per (row, q head)
+    const size_t part_bytes = (size_t)n_rows * n_q_heads * (head_dim * sizeof(float) + sizeof(float2));
+    if (parts <= 0) {
+        parts = auto_parts(n_rows * n_kv_heads, width);
+        if (scratch) parts = (int)std::min<size_t>((size_t)parts, scratch_bytes / part_bytes);
+    }
     parts = std::max(1, std::min(parts, kDlsaMaxParts));
+    QW_REQUIRE(!scratch || parts == 1 || (size_t)parts * part_bytes <= scratch_bytes,
+               QW_ERR_INVALID_ARGUMENT,
+               "dlsa_sparse_attention_noalloc: the partials of " + std::to_string(parts) +
+                   " parts need " + std::to_string((size_t)parts * part_bytes) +
+                   " bytes, more than the " + std::to_string(scratch_bytes) +
+                   "-byte scratch (use fewer parts or rows)");
     DlsaArgs a;
     a.q = (const f16*)q;
     a.k = (const f16*)k;
@@ -414,9 +410,12 @@ int dlsa_sparse_attention(const void* q, const void* k, const void* v, int64_t k
     a.scale2 = scale * kLog2e;
     if (parts > 1) {
         const size_t no = (size_t)n_rows * n_q_heads * parts;
-        void* ws = nullptr;
-        int rc = dlsa_workspace(dev, no * head_dim * sizeof(float) + no * sizeof(float2), &ws);
-        if (rc) return rc;
+        void* ws = scratch;
+        if (!ws) {
+            int rc = dlsa_workspace(dev, stream, no * head_dim * sizeof(float) + no * sizeof(float2),
+                                    &ws);
+            if (rc) return rc;
+        }
         a.part_o = (float*)ws;
         a.part_ml = (float2*)((char*)ws + no * head_dim * sizeof(float));
     }
@@ -440,6 +439,16 @@ int dlsa_sparse_attention(const void* q, const void* k, const void* v, int64_t k
     }
     (void)waves;  // one 4-wave workgroup shape; the knob is accepted for API parity
     return QW_OK;
+}
+
+int dlsa_sparse_attention(const void* q, const void* k, const void* v, int64_t khs, int64_t krs,
+                          int64_t vhs, int64_t vrs, const int32_t* lists, const int32_t* lengths,
+                          int n_rows, int width, int n_q_heads, int n_kv_heads, int head_dim,
+                          int n_keys, float scale, int parts, int waves, void* out,
+                          hipStream_t stream) {
+    return dlsa_sparse_attention_impl(q, k, v, khs, krs, vhs, vrs, lists, lengths, n_rows, width,
+                                      n_q_heads, n_kv_heads, head_dim, n_keys, scale, parts, waves,
+                                      out, stream, nullptr, 0);
 }
 
 }  // namespace qw

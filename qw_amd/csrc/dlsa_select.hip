@@ -473,12 +473,8 @@ int dlsa_select(const float* scores, int64_t stride, const int32_t* members, int
     a.vec_members = bucket_cap <= 16 && bucket_cap % 4 == 0 &&
                     ((uintptr_t)members & 15) == 0;
     const size_t shmem = (size_t)kRankCap * sizeof(uint32_t);
-    static bool attr_set = false;
-    if (!attr_set) {
-        QW_HIP_CHECK(hipFuncSetAttribute((const void*)dlsa_select_kernel,
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)shmem));
-        attr_set = true;
-    }
+    int rc = ensure_dynamic_lds((const void*)dlsa_select_kernel, shmem);
+    if (rc) return rc;
     const int T = threads ? threads : 1024;
     hipLaunchKernelGGL(dlsa_select_kernel, dim3(n_rows), dim3(T), shmem, stream, a);
     QW_HIP_CHECK(hipGetLastError());

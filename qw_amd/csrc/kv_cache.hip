@@ -11,6 +11,8 @@
 #include <string.h>
 
 #include <algorithm>
+#include <map>
+#include <mutex>
 #include <string>
 
 #include "kv_cache.hpp"
@@ -22,6 +24,69 @@ namespace qw {
 static thread_local std::string g_last_error;
 void set_error(const std::string& msg) { g_last_error = msg; }
 const char* last_error() { return g_last_error.c_str(); }
+
+int GrowBuffer::get(size_t need, hipStream_t stream, void** out) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    QW_HIP_CHECK(hipStreamIsCapturing(stream, &cs));
+    const bool capturing = cs != hipStreamCaptureStatusNone;
+    if (need > bytes) {
+        // HIP refuses allocation inside a global-mode capture, and the refused
+        // call would invalidate the caller's capture: refuse here instead.
+        QW_REQUIRE(!capturing, QW_ERR_STATE,
+                   "split-K workspace: too small for this call and the stream is being captured; "
+                   "run one call of this shape on this stream before capturing");
+        if (ptr) {
+            if (captured) {
+                retired.push_back(ptr);  // a graph may still read it
+            } else {
+                QW_HIP_CHECK(hipDeviceSynchronize());
+                (void)hipFree(ptr);
+            }
+            ptr = nullptr;
+            bytes = 0;
+            captured = false;
+        }
+        const size_t nb = std::max(need + need / 4, (size_t)1 << 20);
+        if (hipMalloc(&ptr, nb) != hipSuccess) {
+            (void)hipGetLastError();
+            ptr = nullptr;
+            set_error("split-K workspace: hipMalloc failed");
+            return QW_ERR_OUT_OF_MEMORY;
+        }
+        bytes = nb;
+    }
+    if (capturing) captured = true;
+    *out = ptr;
+    return QW_OK;
+}
+
+void GrowBuffer::release() {
+    if (ptr) (void)hipFree(ptr);
+    for (void* p : retired) (void)hipFree(p);
+    retired.clear();
+    ptr = nullptr;
+    bytes = 0;
+    captured = false;
+}
+
+// Dynamic-LDS limits already raised, per (kernel, device). The attribute is
+// a property of the kernel on the current device, so it is recorded per
+// device, and the mutex keeps two host threads from interleaving a check and
+// a set (which could leave the limit below what the record says).
+static std::mutex g_lds_mu;
+static std::map<std::pair<const void*, int>, size_t> g_lds_set;
+
+int ensure_dynamic_lds(const void* kernel, size_t bytes) {
+    if (bytes <= 65536) return QW_OK;  // the default limit
+    int dev = 0;
+    QW_HIP_CHECK(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_lds_mu);
+    size_t& cur = g_lds_set[{kernel, dev}];
+    if (bytes <= cur) return QW_OK;
+    QW_HIP_CHECK(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes));
+    cur = bytes;
+    return QW_OK;
+}
 
 // --------------------------------------------------------------- sizes
 
@@ -108,15 +173,16 @@ int KVCache::init(int mode_, int group_size, int n_kv_heads, int head_dim, int c
 int KVCache::release() {
     DeviceGuard dg(device);
     (void)hipDeviceSynchronize();
-    void* ptrs[7] = {k_data, (void*)k_params, v_data, (void*)v_params, ws, (void*)fast_flag,
+    void* ptrs[6] = {k_data, (void*)k_params, v_data, (void*)v_params, (void*)fast_flag,
                      (void*)t4_tables};
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
+    ws.release();
+    ws_ptr = nullptr;
     fast_flag = nullptr;
     t4_tables = nullptr;
-    k_data = v_data = ws = nullptr;
+    k_data = v_data = nullptr;
     k_params = v_params = nullptr;
-    ws_bytes = 0;
     cap = offset = 0;
     return QW_OK;
 }
@@ -172,24 +238,9 @@ int KVCache::reserve(int capacity, hipStream_t stream) {
     return QW_OK;
 }
 
-int KVCache::ensure_workspace(size_t bytes) {
-    if (bytes <= ws_bytes) return QW_OK;
+int KVCache::ensure_workspace(size_t bytes, hipStream_t stream) {
     DeviceGuard dg(device);
-    if (ws) {
-        QW_HIP_CHECK(hipDeviceSynchronize());
-        (void)hipFree(ws);
-        ws = nullptr;
-        ws_bytes = 0;
-    }
-    const size_t nb = std::max(bytes, (size_t)1 << 20);
-    if (hipMalloc(&ws, nb) != hipSuccess) {
-        (void)hipGetLastError();
-        ws = nullptr;
-        set_error("workspace hipMalloc failed");
-        return QW_ERR_OUT_OF_MEMORY;
-    }
-    ws_bytes = nb;
-    return QW_OK;
+    return ws.get(bytes, stream, &ws_ptr);
 }
 
 int KVCache::demote(int target_mode, hipStream_t stream, int* demoted) {

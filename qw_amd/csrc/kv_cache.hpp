@@ -60,9 +60,10 @@ struct KVCache {
     // one outside it. Device int, read by each attention launch.
     int* fast_flag = nullptr;
 
-    // Split-K workspace (partial accumulators), grown on demand.
-    void* ws = nullptr;
-    size_t ws_bytes = 0;
+    // Split-K workspace (partial accumulators), grown on demand; ws_ptr is
+    // the current buffer (valid after ensure_workspace).
+    GrowBuffer ws;
+    void* ws_ptr = nullptr;
 
     KvLayout layout() const { return KvLayout{bits, D, hkv, cap}; }
     // Codes and per-group (scale, bias) in the affine layout: the affine modes
@@ -88,7 +89,7 @@ struct KVCache {
     int turbo4_setup();
     int release();
     int reserve(int capacity, hipStream_t stream);
-    int ensure_workspace(size_t bytes);
+    int ensure_workspace(size_t bytes, hipStream_t stream);
     int64_t nbytes() const;
     // cache.rs:3591 demote_fp16_to_turbo4, to an affine mode
     int demote(int target_mode, hipStream_t stream, int* demoted);

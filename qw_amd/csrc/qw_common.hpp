@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include <string>
+#include <vector>
 
 #include "qwattn.h"
 
@@ -117,6 +118,26 @@ struct OpMin {
 // Thread-local last-error string for the C ABI.
 void set_error(const std::string& msg);
 const char* last_error();
+
+// A device buffer for split-K partials that grows on demand and never frees
+// memory a captured HIP graph may still reference: a buffer handed to work
+// recorded into a graph is retired, not freed, when it grows, and released
+// with the owner. A buffer no graph holds is freed after a device
+// synchronization. It cannot grow while its stream is being captured (HIP
+// allows no allocation there): such a call returns QW_ERR_STATE without
+// touching the capture; one call of that shape before capturing sizes it.
+struct GrowBuffer {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    bool captured = false;
+    std::vector<void*> retired;
+    int get(size_t need, hipStream_t stream, void** out);
+    void release();
+};
+
+// Raises `kernel`'s dynamic-LDS limit on the current device to at least
+// `bytes` (needed above 64 KB); thread safe, once per (kernel, device, size).
+int ensure_dynamic_lds(const void* kernel, size_t bytes);
 
 }  // namespace qw
 

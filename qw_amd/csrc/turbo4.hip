@@ -28,6 +28,8 @@
 #include <mutex>
 #include <string>
 
+#include <utility>
+
 #include "kv_cache.hpp"
 #include "rope.hpp"
 
@@ -859,28 +861,20 @@ static int turbo4_verify(KVCache& c, const void* q, int n_q_heads, int n_rows, f
     if (D == 256) {
         using TT = T4Tab<256>;
         a.cb = tab + TT::cb;
+        constexpr size_t sh = T4vShape<256>::lds;
+        int rc = ensure_dynamic_lds((const void*)turbo4_verify_kernel<256>, sh);
+        if (rc) return rc;
         hipLaunchKernelGGL(turbo4_rotate_scaled_kernel<256>, rg, dim3(256), 0, stream,
                            (const f16*)q, q_s, qrows, tab + TT::k_s1, tab + TT::k_s2, post);
-        constexpr size_t sh = T4vShape<256>::lds;
-        static bool attr = false;
-        if (!attr) {
-            QW_HIP_CHECK(hipFuncSetAttribute((const void*)turbo4_verify_kernel<256>,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)sh));
-            attr = true;
-        }
         hipLaunchKernelGGL(turbo4_verify_kernel<256>, vg, dim3(kT4vThreads), sh, stream, a);
     } else {
         using TT = T4Tab<128>;
         a.cb = tab + TT::cb;
+        constexpr size_t sh = T4vShape<128>::lds;
+        int rc = ensure_dynamic_lds((const void*)turbo4_verify_kernel<128>, sh);
+        if (rc) return rc;
         hipLaunchKernelGGL(turbo4_rotate_scaled_kernel<128>, rg, dim3(256), 0, stream,
                            (const f16*)q, q_s, qrows, tab + TT::k_s1, tab + TT::k_s2, post);
-        constexpr size_t sh = T4vShape<128>::lds;
-        static bool attr = false;
-        if (!attr) {
-            QW_HIP_CHECK(hipFuncSetAttribute((const void*)turbo4_verify_kernel<128>,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)sh));
-            attr = true;
-        }
         hipLaunchKernelGGL(turbo4_verify_kernel<128>, vg, dim3(kT4vThreads), sh, stream, a);
     }
     QW_HIP_CHECK(hipGetLastError());
@@ -983,11 +977,9 @@ int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float
     view.k_data = kw;
     view.v_data = vw;
     view.fast_flag = c.fast_flag;
-    view.ws = c.ws;
-    view.ws_bytes = c.ws_bytes;
+    std::swap(view.ws, c.ws);
     int rc = launch_attention(view, q_rot, n_q_heads, n_rows, scale, causal, o_rot, stream);
-    c.ws = view.ws;
-    c.ws_bytes = view.ws_bytes;
+    std::swap(view.ws, c.ws);
     if (rc) return rc;
     if (D == 256) {
         using TT = T4Tab<256>;

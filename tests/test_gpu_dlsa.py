@@ -99,3 +99,32 @@ def test_ragged_lists_skips_and_empty_rows(oracle_lib, D, G):
                                       D ** -0.5))[0]
     assert_close(out, ref, f"ragged D={D} G={G}")
     assert np.all(out[:, 2] == 0)
+
+
+def test_workspace_per_stream_growth():
+    """Split-K partials live in a workspace per (device, stream): calls
+    alternating on two streams, with a growth of one stream's workspace in
+    between, give the single-stream outputs bit for bit."""
+    import qw_amd
+
+    r = rng(77)
+    T, H, G, D, L, W = 3000, 4, 6, 256, 3, 700
+    k = _gpu(r.standard_normal((H, T, D)).astype(np.float16))
+    v = _gpu(r.standard_normal((H, T, D)).astype(np.float16))
+    q = _gpu(r.standard_normal((H * G, L, D)).astype(np.float16))
+    lists = _gpu(np.stack([r.choice(T, W, replace=False) for _ in range(L)]).astype(np.int32))
+    lengths = _gpu(np.array([W, 500, 650], np.int32))
+    knobs = (16, 128, 32)  # 128 parts need ~9.5 MB of partials: a growth
+    torch.cuda.synchronize()
+    want = [_np(qw_amd.sparse_attention_with(q, k, v, lists, lengths, D ** -0.5, p, 0))
+            for p in knobs]
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    outs = []
+    for rep in range(3):
+        for i, p in enumerate(knobs):
+            with torch.cuda.stream(s1 if (i + rep) % 2 == 0 else s2):
+                outs.append((i, qw_amd.sparse_attention_with(q, k, v, lists, lengths,
+                                                             D ** -0.5, p, 0)))
+    torch.cuda.synchronize()
+    for i, o in outs:
+        np.testing.assert_array_equal(_np(o), want[i])
