@@ -241,6 +241,25 @@ int qw_dlsa_sparse_attention_with(const void* q, const void* k, const void* v,
                                   int n_keys, float scale, int parts, int waves, void* out,
                                   void* stream);
 
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). The same read and arguments as
+ * qw_dlsa_sparse_attention_with, but its split-K partials live in a fixed
+ * 4 MiB device array of the library (each GPU holds its own copy from load
+ * until the process ends), so the call allocates nothing. parts = 0 picks
+ * the automatic count, lowered until the partials, n_rows * n_q_heads *
+ * parts * (head_dim * 4 + 8) bytes, fit the 4 MiB; an explicit parts > 1
+ * whose partials do not fit returns QW_ERR_INVALID_ARGUMENT. Every call on a
+ * GPU shares that GPU's array: two calls that overlap on one GPU (other
+ * streams or threads) race and must be ordered by the caller. */
+int qw_dlsa_sparse_attention_noalloc(const void* q, const void* k, const void* v,
+                                     int64_t k_head_stride, int64_t k_row_stride,
+                                     int64_t v_head_stride, int64_t v_row_stride,
+                                     const int32_t* lists, const int32_t* lengths, int n_rows,
+                                     int width, int n_q_heads, int n_kv_heads, int head_dim,
+                                     int n_keys, float scale, int parts, int waves, void* out,
+                                     void* stream);
+
 /* D-LSA K1 select: dlsa_select (crates/mlxcel-core/src/dlsa_kernels.rs:57-84)
  * / dlsa_select_with (:88-117), the device twin of the host select
  * (crates/runtime/src/dlsa/select.rs:65-115). For each of n_rows query rows:

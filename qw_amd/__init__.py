@@ -80,6 +80,8 @@ _SIGNATURES = {
                                       _i, _i, _i, _f, _p, _p]),
     "qw_dlsa_sparse_attention_with": (_i, [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _i, _i,
                                            _i, _i, _i, _i, _f, _i, _i, _p, _p]),
+    "qw_dlsa_sparse_attention_noalloc": (_i, [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _i, _i,
+                                              _i, _i, _i, _i, _f, _i, _i, _p, _p]),
 }
 
 

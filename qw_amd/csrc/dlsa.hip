@@ -451,4 +451,49 @@ int dlsa_sparse_attention(const void* q, const void* k, const void* v, int64_t k
                                       out, stream, nullptr, 0);
 }
 
+// ------------------------------------------------ the no-allocation variant
+//
+// Split-K partials of qw_dlsa_sparse_attention_noalloc, in a fixed device
+// array the library never allocates: each device that loads the library holds
+// its own copy until the process ends. In host code `scratch` only names the
+// symbol; its device address comes from hipGetSymbolAddress, resolved once
+// per device with that device current and kept in g_scratch_ptr. Every call
+// on a device shares the array (nothing in it must start at zero: each
+// partial is written before it is read), so two calls that overlap on one
+// device race.
+constexpr size_t kDlsaScratchBytes = (size_t)4 << 20;
+static __device__ __align__(256) unsigned char scratch[kDlsaScratchBytes];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[64];
+
+static int scratch_address(int device, void** out) {
+    QW_REQUIRE(device >= 0 && device < 64, QW_ERR_INVALID_ARGUMENT,
+               "dlsa_sparse_attention_noalloc: device ordinal out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void* p = nullptr;
+        QW_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        QW_REQUIRE(p != nullptr, QW_ERR_HIP, "dlsa_sparse_attention_noalloc: no scratch address");
+        g_scratch_ptr[device] = p;
+    }
+    *out = g_scratch_ptr[device];
+    return QW_OK;
+}
+
+int dlsa_sparse_attention_noalloc(const void* q, const void* k, const void* v, int64_t khs,
+                                  int64_t krs, int64_t vhs, int64_t vrs, const int32_t* lists,
+                                  const int32_t* lengths, int n_rows, int width, int n_q_heads,
+                                  int n_kv_heads, int head_dim, int n_keys, float scale, int parts,
+                                  int waves, void* out, hipStream_t stream) {
+    int dev = 0;
+    QW_HIP_CHECK(hipGetDevice(&dev));
+    void* ws = nullptr;
+    int rc = scratch_address(dev, &ws);
+    if (rc) return rc;
+    return dlsa_sparse_attention_impl(q, k, v, khs, krs, vhs, vrs, lists, lengths, n_rows, width,
+                                      n_q_heads, n_kv_heads, head_dim, n_keys, scale, parts, waves,
+                                      out, stream, ws, kDlsaScratchBytes);
+}
+
 }  // namespace qw
