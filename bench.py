@@ -429,9 +429,11 @@ def bench_dlsa(torch, qw_amd, reps: int, T: int = 131072, layers: int = LAYERS):
         assert rc == 0, L.qw_last_error()
 
     st = torch.cuda.current_stream(dev).cuda_stream
-    for i in range(layers):
+    for i in range(layers):  # reps = 0: these `layers` calls only (the counter workload)
         call(i, st)
     torch.cuda.synchronize()
+    if reps == 0:
+        return {"T": T, "W": int(W)}
     st = replay_stats(torch, lambda i: call(i, torch.cuda.current_stream(dev).cuda_stream),
                       layers, layers, reps)
     ms = st["median"]
@@ -557,7 +559,7 @@ def pmc_workload(cfg: str) -> int:
     torch.cuda.synchronize()
     del src, dst
     if cfg == "c5":
-        bench_dlsa(torch, qw_amd, 1)
+        bench_dlsa(torch, qw_amd, 0)
         print("pmc workload c5 done", flush=True)
         return 0
     bits, T0, L, n, causal = {"c2": (4, 32768, 1, LAYERS, False),
@@ -575,39 +577,35 @@ def pmc_workload(cfg: str) -> int:
     return 0
 
 
-def _pmc_per_kernel(db_path: str, counters):
-    """{kernel name: {counter: [value per dispatch]}} from a rocprofv3 --pmc
-    database."""
+PMC_CALLS = {"c2": LAYERS, "c3": 4, "c4": LAYERS, "c5": LAYERS}
+# the kernels a call of the configuration launches (set-up appends excluded)
+PMC_KERNELS = ("attend_decode_kernel", "attend_block_kernel", "decode_merge_kernel",
+               "merge_rows_kernel", "merge_append_kernel", "dlsa_kernel", "dlsa_merge_kernel")
+N_XCD, N_SIMD = 8, 1024  # MI355X: 8 XCDs, 256 CUs x 4 SIMDs
+
+
+def _pmc_rows(root: str, ps: str):
+    """(kernel, dispatch, counter, value, duration_ns) rows of one pass, from a
+    rocprofv3 results database under root/ps, or from root/ps.tsv (the same
+    table's rows dumped as text)."""
+    import csv
+    import glob
     import sqlite3
 
-    con = sqlite3.connect(db_path)
+    tsv = os.path.join(root, f"{ps}.tsv")
+    if os.path.exists(tsv):
+        with open(tsv) as f:
+            rd = csv.DictReader(f, delimiter="\t")
+            return [(r["kernel_name"], r["dispatch_id"], r["counter_name"], float(r["value"]),
+                     float(r["duration"])) for r in rd]
+    hits = sorted(glob.glob(os.path.join(root, ps, "**", "*results.db"), recursive=True))
+    if not hits:
+        raise FileNotFoundError(f"no rocprofv3 results under {root}/{ps}")
+    con = sqlite3.connect(hits[-1])
     tabs = [r[0] for r in con.execute("select name from sqlite_master where type in ('table', 'view')")]
     ctab = next(t for t in tabs if t.startswith("counters_collection"))
-    rows = con.execute(f"select * from {ctab} limit 1")
-    cols = [d[0] for d in rows.description]
-    name_col = next(c for c in cols if c in ("kernel_name", "name"))
-    cnt_col = next(c for c in cols if c in ("counter_name", "counter"))
-    val_col = next(c for c in cols if c in ("value", "counter_value"))
-    disp_col = next((c for c in cols if "dispatch" in c and "id" in c), None)
-    per = {}
-    for counter in counters:
-        if disp_col:
-            q = (f"select {name_col}, sum({val_col}) from {ctab} where {cnt_col} = ? "
-                 f"group by {name_col}, {disp_col}")
-        else:
-            q = f"select {name_col}, {val_col} from {ctab} where {cnt_col} = ?"
-        for name, v in con.execute(q, (counter,)):
-            per.setdefault(name, {}).setdefault(counter, []).append(float(v))
-    return per
-
-
-def _find_db(root: str):
-    import glob
-
-    hits = sorted(glob.glob(os.path.join(root, "**", "*results.db"), recursive=True))
-    if not hits:
-        raise FileNotFoundError(f"no rocprofv3 results database under {root}")
-    return hits[-1]
+    q = f"select kernel_name, dispatch_id, counter_name, value, duration from {ctab}"
+    return [(n, d, c, float(v), float(du)) for n, d, c, v, du in con.execute(q)]
 
 
 def _short(name: str) -> str:
@@ -616,71 +614,85 @@ def _short(name: str) -> str:
 
 
 def summarize_counters(cfg: str, root: str, out: str) -> int:
-    """profiles/counters_<cfg>.txt from the four passes under root/<pass>."""
-    per = {}
-    for ps, counters in PMC_PASSES.items():
-        data = _pmc_per_kernel(_find_db(os.path.join(root, ps)), counters.split())
-        for name, cs in data.items():
-            per.setdefault(name, {}).update(cs)
+    """profiles/counters_<cfg>.txt from the four passes under root: per call
+    of the configuration's attention (every dispatch of its kernels summed and
+    divided by the number of calls), bytes read and written, and MFMA
+    figures."""
+    per = {}   # kernel -> dispatch -> {counter: value, "dur": ns}
+    for ps in PMC_PASSES:
+        for name, disp, counter, value, dur in _pmc_rows(root, ps):
+            d = per.setdefault(name, {}).setdefault((ps, disp), {})
+            d[counter] = d.get(counter, 0.0) + value
+            d["dur"] = dur
 
-    def avg(name, c):
-        v = per.get(name, {}).get(c)
-        return sum(v) / len(v) if v else float("nan")
+    def total(name, counter):
+        return sum(d.get(counter, 0.0) for d in per[name].values())
 
-    def big(name, c):
-        v = per.get(name, {}).get(c)
-        return max(v) if v else float("nan")
+    def biggest(name, counter):
+        return max(d.get(counter, 0.0) for d in per[name].values())
 
     copy_k = next(n for n in per if "copyBuffer" in n)
-    cf, cw = big(copy_k, "FETCH_SIZE"), big(copy_k, "WRITE_SIZE")
-    n32, n64, n128 = (big(copy_k, f"TCC_EA0_RDREQ_{b}_sum") for b in ("32B", "64B", "128B"))
+    cf, cw = biggest(copy_k, "FETCH_SIZE"), biggest(copy_k, "WRITE_SIZE")
+    n32, n64, n128 = (biggest(copy_k, f"TCC_EA0_RDREQ_{b}_sum") for b in ("32B", "64B", "128B"))
     copy_ea = 32 * n32 + 64 * n64 + 128 * n128
     f_scale = (COPY_BYTES / 1024.0) / cf
     w_scale = (COPY_BYTES / 1024.0) / cw
-    ea_scale = COPY_BYTES / copy_ea
     alg_bytes, alg_flops = pmc_algorithmic(cfg)
-    ours = [n for n in per if "qw::" in n or "_ZN2qw" in n]
+    calls = PMC_CALLS[cfg]
+    ours = [n for n in per if any(k in n for k in PMC_KERNELS)]
     lines = [f"# Counters of {PMC_CONFIGS[cfg]} (rocprofv3 --pmc)", "", "commands:"]
     for ps, counters in PMC_PASSES.items():
         lines.append(f"  rocprofv3 --pmc {counters} -d gpurun_out/pmc_{cfg}/{ps} -o run -- "
                      f"python3 bench.py --pmc-workload {cfg}")
     lines += [f"  python3 bench.py --summarize-counters {cfg} gpurun_out/pmc_{cfg} "
               f"--out profiles/counters_{cfg}.txt", "",
-              f"calibration: copy of {COPY_BYTES} B ({_short(copy_k)}):",
-              f"  FETCH_SIZE {cf:.1f} KiB -> scale {f_scale:.4f}; WRITE_SIZE {cw:.1f} KiB -> "
-              f"scale {w_scale:.4f}",
-              f"  EA read requests 32B/64B/128B {n32:.0f}/{n64:.0f}/{n128:.0f} -> "
-              f"{copy_ea:.0f} B (x{ea_scale:.4f} of the true count)", "",
-              f"algorithmic per call: {alg_bytes} B, {alg_flops} flop", ""]
-    tot_read = tot_write = tot_ea = tot_dram = 0.0
-    for name in ours:
-        n = len(per[name].get("FETCH_SIZE", [])) or 1
-        fr = avg(name, "FETCH_SIZE") * f_scale * 1024.0
-        wr = avg(name, "WRITE_SIZE") * w_scale * 1024.0
-        e32, e64, e128 = (avg(name, f"TCC_EA0_RDREQ_{b}_sum") for b in ("32B", "64B", "128B"))
-        ea = 32 * e32 + 64 * e64 + 128 * e128
-        dram = avg(name, "TCC_EA0_RDREQ_DRAM_sum")
-        ereq = e32 + e64 + e128
-        tot_read += fr
-        tot_write += wr
-        tot_ea += ea
-        tot_dram += ea * (dram / ereq if ereq else 0.0)
-        mb = avg(name, "SQ_VALU_MFMA_BUSY_CYCLES")
-        mops = avg(name, "SQ_INSTS_VALU_MFMA_MOPS_F16")
-        gui = avg(name, "GRBM_GUI_ACTIVE")
-        lines += [f"kernel: {_short(name)} ({n} dispatches)",
-                  f"  read {fr:.0f} B (FETCH_SIZE x scale), EA read {ea:.0f} B "
-                  f"({dram / ereq if ereq else 0:.3f} of the requests to DRAM), "
-                  f"write {wr:.0f} B",
-                  f"  SQ_VALU_MFMA_BUSY_CYCLES {mb:.0f}  GRBM_GUI_ACTIVE {gui:.0f}  "
-                  f"SQ_BUSY_CYCLES {avg(name, 'SQ_BUSY_CYCLES'):.0f}",
-                  f"  SQ_INSTS_VALU_MFMA_MOPS_F16 {mops:.0f} (x512 = {mops * 512:.4g} flop)  "
-                  f"SQ_INSTS_MFMA {avg(name, 'SQ_INSTS_MFMA'):.0f}  "
-                  f"SQ_INSTS_VALU {avg(name, 'SQ_INSTS_VALU'):.0f}"]
-    lines += ["",
-              f"traffic_bytes_per_call = {tot_read + tot_write:.0f}",
-              f"dram_read_bytes_per_call = {tot_dram:.0f}",
-              f"traffic / algorithmic = {(tot_read + tot_write) / alg_bytes:.4f}"]
+              f"calibration, a copy of {COPY_BYTES} B ({_short(copy_k)}):",
+              f"  FETCH_SIZE {cf:.1f} KiB -> x{f_scale:.4f} (it counts a 128-byte request as 64); "
+              f"WRITE_SIZE {cw:.1f} KiB -> x{w_scale:.4f}",
+              f"  EA read requests 32B/64B/128B {n32:.0f}/{n64:.0f}/{n128:.0f} = {copy_ea:.0f} B "
+              f"({copy_ea / COPY_BYTES:.4f} of the true count)",
+              f"per call: algorithmic {alg_bytes} B and {alg_flops} flop; {calls} calls profiled",
+              "MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs x 1024 SIMDs); "
+              "clock = GRBM_GUI_ACTIVE / 8 / duration",
+              "(GRBM_GUI_ACTIVE spans the profiler's whole dispatch window: for kernels of a few "
+              "tens of us the clock reads high and MFMA busy low; trust them on long kernels)", ""]
+    tot = {"read": 0.0, "write": 0.0, "ea": 0.0, "dram": 0.0, "flop": 0.0, "busy": 0.0,
+           "simd_cycles": 0.0}
+    for name in sorted(ours):
+        disp = {d for (ps, d) in per[name] if ps == "fetch"}
+        n = max(1, len(disp))
+        rd = total(name, "FETCH_SIZE") * f_scale * 1024.0 / calls
+        wr = total(name, "WRITE_SIZE") * w_scale * 1024.0 / calls
+        e32, e64, e128 = (total(name, f"TCC_EA0_RDREQ_{b}_sum") for b in ("32B", "64B", "128B"))
+        ea = (32 * e32 + 64 * e64 + 128 * e128) / calls
+        req = e32 + e64 + e128
+        dram = ea * (total(name, "TCC_EA0_RDREQ_DRAM_sum") / req if req else 0.0)
+        busy = total(name, "SQ_VALU_MFMA_BUSY_CYCLES") / calls
+        gui = total(name, "GRBM_GUI_ACTIVE") / calls
+        mfd = [d for (ps, _), d in per[name].items() if ps == "mfma"]
+        dur = sum(d["dur"] for d in mfd) / calls
+        flop = total(name, "SQ_INSTS_VALU_MFMA_MOPS_F16") * 512 / calls
+        simd = gui / N_XCD * N_SIMD
+        clk = gui / N_XCD / dur if dur else 0.0
+        for k, v in (("read", rd), ("write", wr), ("ea", ea), ("dram", dram), ("flop", flop),
+                     ("busy", busy), ("simd_cycles", simd)):
+            tot[k] += v
+        lines += [f"kernel {_short(name)}: {n} dispatches, {n / calls:g} a call; per call:",
+                  f"  read {rd:.0f} B (FETCH_SIZE), {ea:.0f} B (EA requests, "
+                  f"{dram / ea if ea else 0:.3f} to DRAM); write {wr:.0f} B",
+                  f"  {dur / 1e3:.2f} us under the profiler, clock {clk:.2f} GHz; MFMA busy "
+                  f"{busy / simd if simd else 0:.4f}, MFMA flop {flop:.4g}, SQ_INSTS_VALU "
+                  f"{total(name, 'SQ_INSTS_VALU') / calls:.0f}, SQ_INSTS_MFMA "
+                  f"{total(name, 'SQ_INSTS_MFMA') / calls:.0f}"]
+    lines += ["", "per call, all of the call's kernels:",
+              f"traffic_bytes_per_call = {tot['read'] + tot['write']:.0f}",
+              f"read_bytes_per_call = {tot['read']:.0f}",
+              f"write_bytes_per_call = {tot['write']:.0f}",
+              f"dram_read_bytes_per_call = {tot['dram']:.0f}",
+              f"traffic / algorithmic = {(tot['read'] + tot['write']) / alg_bytes:.4f}",
+              f"mfma_flop_per_call = {tot['flop']:.0f}",
+              f"mfma_flop / algorithmic = {tot['flop'] / alg_flops:.4f}",
+              f"mfma_busy = {tot['busy'] / tot['simd_cycles'] if tot['simd_cycles'] else 0:.4f}"]
     os.makedirs(os.path.dirname(os.path.abspath(out)), exist_ok=True)
     with open(out, "w") as f:
         f.write("\n".join(lines) + "\n")
@@ -714,17 +726,18 @@ def summarize_trace(db_path: str, out: str, command: str) -> int:
 
 
 def read_counters(cfg: str):
-    """The committed counter summary of a configuration, as numbers."""
+    """The committed counter summary of a configuration, as numbers (per call
+    of its attention): bytes read/written, DRAM read bytes, MFMA busy."""
     out = {}
+    keys = ("traffic_bytes_per_call", "read_bytes_per_call", "write_bytes_per_call",
+            "dram_read_bytes_per_call", "mfma_flop_per_call", "mfma_busy")
     try:
         with open(os.path.join(ROOT, "profiles", f"counters_{cfg}.txt")) as f:
             for line in f:
-                for key in ("traffic_bytes_per_call", "dram_read_bytes_per_call"):
-                    if line.startswith(key):
-                        out[key] = int(float(line.split("=")[1]))
-                if "SQ_VALU_MFMA_BUSY_CYCLES" in line and "mfma_busy_cycles" not in out:
-                    out["mfma_busy_cycles"] = float(line.split()[1])
-                    out["grbm_gui_active"] = float(line.split()[3])
+                for key in keys:
+                    if line.startswith(key + " ="):
+                        v = float(line.split("=")[1])
+                        out[key] = v if key == "mfma_busy" else int(v)
     except OSError:
         pass
     return out
