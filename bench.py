@@ -443,6 +443,46 @@ def bench_dlsa(torch, qw_amd, reps: int, T: int = 131072, layers: int = LAYERS):
     return {"T": T, "W": int(W), "ms": ms, "stats": st, "bytes": bytes_call}
 
 
+def bench_dlsa_cache(torch, qw_amd, reps: int, T: int = 131072, layers: int = LAYERS):
+    """Config 5 through an fp16 KV cache read in place (qw_kv_dlsa_attention):
+    the same lists as bench_dlsa over caches holding the same kind of rows."""
+    import numpy as np
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    rng = np.random.default_rng(5)
+    caches, qs, lists, lens, outs = [], [], [], [], []
+    for layer in range(layers):
+        c = qw_amd.KVCache("fp16", HKV, D, capacity=T)
+        for t0 in range(0, T, 16384):
+            c.update(torch.randn((HKV, 16384, D), device=dev, generator=g).half(),
+                     torch.randn((HKV, 16384, D), device=dev, generator=g).half())
+        caches.append(c)
+        qs.append(torch.randn((HQ, 1, D), device=dev, generator=g).half())
+        blocks = np.sort(rng.choice(np.arange(1, (T - 512) // 512), 8, replace=False))
+        lst = np.concatenate([np.concatenate([np.arange(b * 512, b * 512 + 512) for b in blocks]),
+                              np.arange(T - 512, T), np.arange(4)]).astype(np.int32)
+        lists.append(torch.from_numpy(lst[None]).to(dev))
+        lens.append(torch.tensor([lst.size], dtype=torch.int32, device=dev))
+        outs.append(torch.empty((HQ, 1, D), dtype=torch.float16, device=dev))
+    W = lists[0].shape[1]
+    L = qw_amd.lib()
+
+    def call(i, st):
+        rc = L.qw_kv_dlsa_attention(caches[i]._h, qs[i].data_ptr(), HQ, 1, lists[i].data_ptr(),
+                                    lens[i].data_ptr(), W, D ** -0.5, outs[i].data_ptr(), st)
+        assert rc == 0, L.qw_last_error()
+
+    st = replay_stats(torch, lambda i: call(i, torch.cuda.current_stream(dev).cuda_stream),
+                      layers, layers, reps)
+    for c in caches:
+        c.close()
+    torch.cuda.empty_cache()
+    bytes_call = W * HKV * 2 * D * 2 + HQ * D * 2 * 2 + W * 4
+    return {"T": T, "W": int(W), "ms": st["median"], "stats": st, "bytes": bytes_call}
+
+
 def cpu_threads():
     """Threads for the CPU baseline: every core this process may run on,
     capped by OMP_NUM_THREADS when the environment sets it (the GPU box's
@@ -857,6 +897,13 @@ def main() -> int:
             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "list_width": ds["W"],
             "context": ds["T"], "algorithmic_bytes": ds["bytes"],
             "counters": read_counters("c5")}
+        log("bench: config 5 D-LSA read over fp16 KV caches in place")
+        dc = bench_dlsa_cache(torch, qw_amd, reps)
+        gbc = dc["bytes"] / (dc["ms"] * 1e-3) / 1e9
+        extra["config5_dlsa_from_cache"] = {
+            "us_per_layer": round(dc["ms"] * 1e3, 3), "GB_s": round(gbc, 1),
+            "frac_hbm": round(gbc / HBM_PEAK_GBS, 4), "list_width": dc["W"],
+            "route": "qw_kv_dlsa_attention: K rows and 8-key V blocks of the cache read in place"}
         log("bench: config 1 decode (8-bit, 4096 keys)")
         c1 = bench_decode(torch, qw_amd, LAYERS, args.warmup, reps, bits=8, T_prefix=4095)
         extra["config1_decode"] = {

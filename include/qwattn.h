@@ -229,6 +229,31 @@ int qw_dlsa_sparse_attention(const void* q, const void* k, const void* v, int64_
                              int n_q_heads, int n_kv_heads, int head_dim, int n_keys,
                              float scale, void* out, void* stream);
 
+/* The D-LSA read over a KV cache in place: what the reference's caller
+ * (crates/runtime/src/qwen3_next/dlsa.rs:161-177) does with
+ * KVCache::update_and_fetch (cache.rs:2709) followed by
+ * dlsa_attention::sparse_attention (dlsa_attention.rs:31) on the fetched
+ * views, without the fetch. Keys are the cache's rows [0, offset); the
+ * contract is qw_dlsa_sparse_attention's (q [n_q_heads][n_rows][head_dim],
+ * lists [n_rows][width] int32 device, lengths [n_rows], entries outside
+ * [0, offset) skipped, fp32 softmax, out like q). fp16, affine and Int8
+ * caches are read in place, quantized rows dequantized inside the gather
+ * exactly as the fetch would (f16(f16(code * scale) + bias)); a Turbo4 cache
+ * is fetched to fp16 first (into a buffer the cache keeps), as the
+ * reference's own update_and_fetch does. QW_ERR_INVALID_ARGUMENT on an empty
+ * cache. */
+int qw_kv_dlsa_attention(qw_kv_cache* cache, const void* q, int n_q_heads, int n_rows,
+                         const int32_t* lists, const int32_t* lengths, int width, float scale,
+                         void* out, void* stream);
+
+/* update (quantize-on-append of the n_rows new K/V rows, [n_kv_heads][n_rows]
+ * [head_dim] fp16), then qw_kv_dlsa_attention: the update_and_fetch +
+ * sparse_attention pair of qwen3_next/dlsa.rs:161-177 in one call. */
+int qw_kv_update_and_dlsa_attention(qw_kv_cache* cache, const void* q, int n_q_heads,
+                                    int n_rows, const void* k_new, const void* v_new,
+                                    const int32_t* lists, const int32_t* lengths, int width,
+                                    float scale, void* out, void* stream);
+
 /* dlsa_attention::sparse_attention_with (dlsa_attention.rs:44): the same read
  * with explicit launch knobs; 0 = automatic. parts: split-K partitions of
  * each list (1 = one pass, at most 128); waves: wavefronts per workgroup

@@ -68,6 +68,8 @@ _SIGNATURES = {
     "qw_kv_update_and_attention": (_i, [_p, _p, _i, _i, _p, _p, _f, _i, _p, _p]),
     "qw_kv_attention": (_i, [_p, _p, _i, _i, _f, _i, _p, _p]),
     "qw_kv_trim": (_i, [_p, _i, ctypes.POINTER(_i)]),
+    "qw_kv_dlsa_attention": (_i, [_p, _p, _i, _i, _p, _p, _i, _f, _p, _p]),
+    "qw_kv_update_and_dlsa_attention": (_i, [_p, _p, _i, _i, _p, _p, _p, _p, _i, _f, _p, _p]),
     "qw_kv_demote": (_i, [_p, _i, _p, ctypes.POINTER(_i)]),
     "qw_kv_export": (_i, [_p, _p, _p, _p, _p, _p, _p, _p]),
     "qw_kv_import": (_i, [_p, _i, _p, _p, _p, _p, _p, _p, _p]),
@@ -284,6 +286,40 @@ class KVCache:
     def attention(self, q, scale: float, causal: bool = False):
         """Attend the cache as it is (fused prefix attention, cache.rs:3607)."""
         return self._attn(q, None, None, scale, causal)
+
+    # -- D-LSA read over the cache (qwen3_next/dlsa.rs:161-177)
+    def _dlsa(self, q, keys, values, lists, lengths, scale: float):
+        torch = _torch()
+        qq = _as3(q, "q")
+        hq, L, D = qq.shape
+        if lists.dim() != 2 or lists.dtype != torch.int32 or lengths.dim() != 1 or \
+                lengths.dtype != torch.int32 or lists.shape[0] != L or lengths.shape[0] != L:
+            raise QwError(1, "dlsa_attention: lists [L,W] i32 and lengths [L] i32 expected")
+        lists, lengths = lists.contiguous(), lengths.contiguous()
+        out = torch.empty_like(qq)
+        st = _stream(self.device)
+        if keys is None:
+            _check(lib().qw_kv_dlsa_attention(self._h, qq.data_ptr(), hq, L, lists.data_ptr(),
+                                              lengths.data_ptr(), lists.shape[1], float(scale),
+                                              out.data_ptr(), st))
+        else:
+            k, v = _as3(keys, "keys"), _as3(values, "values")
+            if k.shape != v.shape or k.shape[1] != L:
+                raise QwError(1, "dlsa_attention: new keys/values must have q's row count")
+            _check(lib().qw_kv_update_and_dlsa_attention(
+                self._h, qq.data_ptr(), hq, L, k.data_ptr(), v.data_ptr(), lists.data_ptr(),
+                lengths.data_ptr(), lists.shape[1], float(scale), out.data_ptr(), st))
+        return out.unsqueeze(0)
+
+    def dlsa_attention(self, q, lists, lengths, scale: float):
+        """D-LSA K2 over the cached rows in place: the reference's
+        ``update_and_fetch`` + ``sparse_attention`` read without the fetch
+        (``[1, Hq, L, D]`` q, ``[L, W]`` i32 lists, ``[L]`` i32 lengths)."""
+        return self._dlsa(q, None, None, lists, lengths, scale)
+
+    def update_and_dlsa_attention(self, q, keys, values, lists, lengths, scale: float):
+        """Append the L new rows, then :meth:`dlsa_attention`."""
+        return self._dlsa(q, keys, values, lists, lengths, scale)
 
     # -- lifecycle
     def demote_fp16_to_affine(self, target_mode: int | str) -> bool:

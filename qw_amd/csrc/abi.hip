@@ -160,6 +160,24 @@ int qw_kv_attention(qw_kv_cache* cache, const void* q, int n_q_heads, int n_rows
                                      (hipStream_t)stream));
 }
 
+int qw_kv_dlsa_attention(qw_kv_cache* cache, const void* q, int n_q_heads, int n_rows,
+                         const int32_t* lists, const int32_t* lengths, int width, float scale,
+                         void* out, void* stream) {
+    QW_HANDLE(cache);
+    QW_GUARDED(cache->impl.dlsa_attention(q, n_q_heads, n_rows, lists, lengths, width, scale, out,
+                                          (hipStream_t)stream));
+}
+
+int qw_kv_update_and_dlsa_attention(qw_kv_cache* cache, const void* q, int n_q_heads,
+                                    int n_rows, const void* k_new, const void* v_new,
+                                    const int32_t* lists, const int32_t* lengths, int width,
+                                    float scale, void* out, void* stream) {
+    QW_HANDLE(cache);
+    QW_GUARDED(cache->impl.update_and_dlsa_attention(q, n_q_heads, n_rows, k_new, v_new, lists,
+                                                     lengths, width, scale, out,
+                                                     (hipStream_t)stream));
+}
+
 int qw_kv_trim(qw_kv_cache* cache, int n, int* trimmed) {
     QW_HANDLE(cache);
     const int m = cache->impl.trim(n);

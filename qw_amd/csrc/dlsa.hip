@@ -25,16 +25,15 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <type_traits>
 
+#include "dequant.hpp"
 #include "kv_cache.hpp"
 
 namespace qw {
 
 struct DlsaArgs {
     const f16* q;
-    const f16* k;
-    const f16* v;
-    int64_t khs, krs, vhs, vrs;
     const int32_t* lists;
     const int32_t* lengths;
     f16* out;
@@ -46,8 +45,280 @@ struct DlsaArgs {
 
 constexpr int kDlsaNT = 2;  // tiles per batch a wave keeps in flight
 
-template <int D, int GMAX>
-__global__ __launch_bounds__(256, 2) void dlsa_kernel(DlsaArgs a) {
+// ---------------------------------------------------------- row sources
+//
+// Where the gathered K and V rows come from. A source loads the raw registers
+// of one 16-entry tile for a lane (g, r16) (the K row of entry r16, the QK A
+// operand; entries 4g..4g+3, the P.V B operand) and turns them into MFMA
+// operands:
+//   k_op(m):     A operand of QK MFMA m, 8 dims of entry r16 (which dims, and
+//                in which order, is the source's q layout kQ, shared with the
+//                q operand);
+//   v_op(pp, c): B operand of P.V tile (pp, c), entries 4g..4g+3 of dim
+//                64 pp + 4 r16 + c.
+// `aligned` (wave-uniform) says that every lane group's four entries are four
+// consecutive keys starting at a multiple of 4: they then sit in one half of
+// an 8-key V block, which the cache sources read with whole-word loads.
+
+// q layouts: dims of MFMA m for lane group g
+//   kQNatural: 32 m + 8 g .. +7
+//   kQGroup:   (D/4) g + 8 m .. +7 (a lane group's dims are one contiguous run)
+//   kQGroup4:  as kQGroup, in the pair order (0,4),(1,5),(2,6),(3,7) that the
+//              4-bit magic-number dequant produces
+enum { kQNatural = 0, kQGroup = 1, kQGroup4 = 2 };
+
+// fp16 K/V views with strides: the K2 contract (strided views of a larger
+// cache read in place).
+template <int D>
+struct SrcStrided {
+    static constexpr int kQ = kQNatural;
+    static constexpr bool kHasAligned = false;
+    static constexpr bool kAffine = false;
+    static constexpr int kNT = kDlsaNT;
+    static constexpr int NM = D / 32, NP = D / 64;
+    const f16* k;
+    const f16* v;
+    int64_t khs, krs, vhs, vrs;
+    struct Regs {
+        u32x4 kc[NM];
+        u32x2 vq[4][NP];  // entry 4g + j: dims 64 pp + 4 r16 .. +3
+    };
+    template <bool ALIGNED>
+    __device__ __forceinline__ void load(Regs& r, int h, int key, const int* key4, int r16,
+                                         int g) const {
+        const u32x4* krow = (const u32x4*)(k + h * khs + (int64_t)key * krs);
+#pragma unroll
+        for (int m = 0; m < NM; m++) r.kc[m] = krow[4 * m + g];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const f16* vrow = v + h * vhs + (int64_t)key4[j] * vrs + 4 * r16;
+#pragma unroll
+            for (int pp = 0; pp < NP; pp++) r.vq[j][pp] = *(const u32x2*)(vrow + 64 * pp);
+        }
+    }
+    template <bool FAST>
+    __device__ __forceinline__ half8 k_op(const Regs& r, int m) const {
+        return as_h8(r.kc[m]);
+    }
+    template <bool ALIGNED, bool FAST>
+    __device__ __forceinline__ half4v v_op(const Regs& r, int pp, int c) const {
+        // element c of the four entries' 4-dim pieces
+        const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+        uint32_t w0, w1;
+        if (c < 2) {
+            w0 = __builtin_amdgcn_perm(r.vq[1][pp].x, r.vq[0][pp].x, sel);
+            w1 = __builtin_amdgcn_perm(r.vq[3][pp].x, r.vq[2][pp].x, sel);
+        } else {
+            w0 = __builtin_amdgcn_perm(r.vq[1][pp].y, r.vq[0][pp].y, sel);
+            w1 = __builtin_amdgcn_perm(r.vq[3][pp].y, r.vq[2][pp].y, sel);
+        }
+        return __builtin_bit_cast(half4v, u32x2{w0, w1});
+    }
+};
+
+// An fp16 KV cache in place: K rows [hkv][cap][D]; V in 8-key blocks
+// [hkv][cap/8][D][8] with dims in lane order (v_phys_dim).
+template <int D>
+struct SrcCacheF16 {
+    static constexpr int kQ = kQNatural;
+    static constexpr bool kHasAligned = true;
+    static constexpr bool kAffine = false;
+    static constexpr int kNT = kDlsaNT;
+    static constexpr int NM = D / 32, NP = D / 64;
+    const f16* k;
+    const f16* v;
+    int cap;
+    struct Regs {
+        u32x4 kc[NM];
+        u32x2 vq[NP][4];  // (pp, c): entries 4g..4g+3 of dim 64 pp + 4 r16 + c
+    };
+    template <bool ALIGNED>
+    __device__ __forceinline__ void load(Regs& r, int h, int key, const int* key4, int r16,
+                                         int g) const {
+        const u32x4* krow = (const u32x4*)(k + ((int64_t)h * cap + key) * D);
+#pragma unroll
+        for (int m = 0; m < NM; m++) r.kc[m] = krow[4 * m + g];
+        const f16* vh = v + ((int64_t)h * (cap / 8) * D + v_slot_base(r16, D, 16)) * 8;
+        if constexpr (ALIGNED) {
+            const f16* blk = vh + (int64_t)(key4[0] >> 3) * D * 8 + (key4[0] & 4);
+#pragma unroll
+            for (int pp = 0; pp < NP; pp++)
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    r.vq[pp][c] = *(const u32x2*)(blk + v_slot_off(pp, c, D, 16) * 8);
+        } else {
+#pragma unroll
+            for (int pp = 0; pp < NP; pp++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const int slot = v_slot_off(pp, c, D, 16) * 8;
+                    uint16_t e[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        e[j] = *(const uint16_t*)(vh + (int64_t)(key4[j] >> 3) * D * 8 + slot +
+                                                  (key4[j] & 7));
+                    r.vq[pp][c] = u32x2{e[0] | ((uint32_t)e[1] << 16), e[2] | ((uint32_t)e[3] << 16)};
+                }
+        }
+    }
+    template <bool FAST>
+    __device__ __forceinline__ half8 k_op(const Regs& r, int m) const {
+        return as_h8(r.kc[m]);
+    }
+    template <bool ALIGNED, bool FAST>
+    __device__ __forceinline__ half4v v_op(const Regs& r, int pp, int c) const {
+        return __builtin_bit_cast(half4v, r.vq[pp][c]);
+    }
+};
+
+// An affine (4/8-bit, group 64) or Int8 KV cache in place, dequantized inside
+// the gather exactly as the fetch does it (MLX's composite f16(f16(c s) + b);
+// Int8 codes are stored plus 128 with bias 0 and take the separately rounded
+// dequant with magic offset 1152):
+//   K codes [hkv][cap][D bits/32] u32 (MLX packing), params [hkv][cap][D/64]
+//   half2(scale, bias) in k_param_slot order; V blocks of 8 keys,
+//   [hkv][cap/8][D bits/4] u32 (dims in lane order, v_phys_dim), params
+//   [hkv][cap/8][D/64][16] f16 (s0..s7, b0..b7).
+// A lane group's K dims are one contiguous run (kQGroup), so its codes are
+// KW contiguous words and one (scale, bias) pair.
+template <int D, int BITS>
+struct SrcCacheAffine {
+    static constexpr int kQ = BITS == 4 ? kQGroup4 : kQGroup;
+    static constexpr bool kHasAligned = true;
+    static constexpr bool kAffine = true;
+    // the dequantized operands and their constants fill the register budget
+    // at D = 256 with two tiles in flight: one tile a batch there
+    static constexpr int kNT = D == 256 ? 1 : kDlsaNT;
+    static constexpr int NM = D / 32, NP = D / 64, NG = D / 64;
+    static constexpr int KW = NM * BITS / 4;   // K words of a lane group's D/4 dims
+    static constexpr int RW = D * BITS / 32;   // K words a row
+    static constexpr int VBW = D * BITS / 4;   // words of an 8-key V block
+    const uint32_t* kc;
+    const uint32_t* kp;
+    const uint32_t* vc;
+    const f16* vp;
+    int cap;
+    uint32_t off2;  // magic offset pair of the separately rounded dequant
+    struct Regs {
+        u32x4 kw[KW / 4];
+        uint32_t kpar;         // half2(scale, bias) of the lane group's 64-dim group
+        uint32_t vw[NP][4];    // (pp, c): codes of dim 64 pp + 4 r16 + c (ALIGNED 4-bit:
+                               // the dim's block word; otherwise the four entries' codes,
+                               // one a byte)
+        u32x2 vs[NP], vb[NP];  // the four entries' V scales and biases of group pp
+        int half;              // ALIGNED: keys 4..7 of the block (1) or 0..3 (0)
+    };
+    template <bool ALIGNED>
+    __device__ __forceinline__ void load(Regs& r, int h, int key, const int* key4, int r16,
+                                         int g) const {
+        const u32x4* krow = (const u32x4*)(kc + ((int64_t)h * cap + key) * RW + KW * g);
+#pragma unroll
+        for (int i = 0; i < KW / 4; i++) r.kw[i] = krow[i];
+        const int grp = (D / 4) * g / 64;
+        r.kpar = kp[((int64_t)h * cap + key) * NG + k_param_slot(grp, NG)];
+        // slots are in units of a dim's 8 codes: one word at 4-bit, two at 8-bit
+        const uint32_t* vh =
+            vc + (int64_t)h * (cap / 8) * VBW + v_slot_base(r16, D, BITS) * (BITS / 4);
+        const f16* vph = vp + (int64_t)h * (cap / 8) * NG * 16;
+        if constexpr (ALIGNED) {
+            const int blk = key4[0] >> 3, half = (key4[0] >> 2) & 1;
+            r.half = half;
+            const uint32_t* bw = vh + (int64_t)blk * VBW + (BITS == 8 ? half : 0);
+#pragma unroll
+            for (int pp = 0; pp < NP; pp++) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) r.vw[pp][c] = bw[v_slot_off(pp, c, D, BITS) * (BITS / 4)];
+                const f16* pr = vph + ((int64_t)blk * NG + pp) * 16 + 4 * half;
+                r.vs[pp] = *(const u32x2*)pr;
+                r.vb[pp] = *(const u32x2*)(pr + 8);
+            }
+        } else {
+            r.half = 0;
+#pragma unroll
+            for (int pp = 0; pp < NP; pp++) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const int slot = v_slot_off(pp, c, D, BITS) * (BITS / 4);
+                    uint32_t codes = 0;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int t = key4[j], kk = t & 7;
+                        const uint32_t* bw = vh + (int64_t)(t >> 3) * VBW;
+                        const uint32_t code =
+                            BITS == 4 ? (bw[slot] >> (4 * v4_nibble_pos(kk))) & 0xFu
+                                      : (bw[slot + (kk >> 2)] >> (8 * (kk & 3))) & 0xFFu;
+                        codes |= code << (8 * j);
+                    }
+                    r.vw[pp][c] = codes;
+                }
+                uint32_t sv[4], bv[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int t = key4[j];
+                    const uint16_t* pr =
+                        (const uint16_t*)(vph + ((int64_t)(t >> 3) * NG + pp) * 16 + (t & 7));
+                    sv[j] = pr[0];
+                    bv[j] = pr[8];
+                }
+                r.vs[pp] = u32x2{sv[0] | (sv[1] << 16), sv[2] | (sv[3] << 16)};
+                r.vb[pp] = u32x2{bv[0] | (bv[1] << 16), bv[2] | (bv[3] << 16)};
+            }
+        }
+    }
+    template <bool FAST>
+    __device__ __forceinline__ half8 k_op(const Regs& r, int m) const {
+        const half2v sb = h2(r.kpar);
+        const half2v s = {sb.x, sb.x}, b = {sb.y, sb.y};
+        const PairConsts pc = make_consts<FAST, BITS>(s, s, s, s, b, b, b, b, off2);
+        if constexpr (BITS == 4)
+            return deq4<FAST>(r.kw[m / 4][m % 4], pc, vconst(kMagic));
+        else
+            return deq8<FAST>(r.kw[m / 2][2 * (m % 2)], r.kw[m / 2][2 * (m % 2) + 1], pc);
+    }
+    template <bool ALIGNED, bool FAST>
+    __device__ __forceinline__ half4v v_op(const Regs& r, int pp, int c) const {
+        // keys (0,1) and (2,3) of the four as magic-number pairs, then
+        // f16(f16(code s_k) + b_k) with each key's own scale and bias
+        const half2v s01 = h2(r.vs[pp].x), s23 = h2(r.vs[pp].y);
+        const half2v b01 = h2(r.vb[pp].x), b23 = h2(r.vb[pp].y);
+        const half2v off = h2(off2);
+        const half2v k1024 = {(f16)-1024.0f, (f16)-1024.0f};
+        half2v y01, y23;
+        if constexpr (ALIGNED && BITS == 4) {
+            // the dim's block word: key k at nibble k/2 + 4 (k % 2), keys 4..7
+            // the same after a shift by 8; (k0, k1) come out of the low nibble
+            // fields, (k2, k3) out of the x16 fields
+            const uint32_t w = r.half ? r.vw[pp][c] >> 8 : r.vw[pp][c];
+            const uint32_t magic = vconst(kMagic);
+            const half2v s23x = s23 * (half2v){(f16)0.0625f, (f16)0.0625f};
+            y01 = deq_pair<FAST, false>((w & 0x000F000Fu) | magic, s01, s01 * k1024, b01, off);
+            y23 = deq_pair<FAST, true>((w & 0x00F000F0u) | magic, FAST ? s23x : s23,
+                                       s23x * k1024, b23, off);
+        } else {
+            // four codes, one a byte
+            const uint32_t p01 = __builtin_amdgcn_perm(0x64646464u, r.vw[pp][c], 0x04010400u);
+            const uint32_t p23 = __builtin_amdgcn_perm(0x64646464u, r.vw[pp][c], 0x04030402u);
+            y01 = deq_pair<FAST, false>(p01, s01, s01 * k1024, b01, off);
+            y23 = deq_pair<FAST, false>(p23, s23, s23 * k1024, b23, off);
+        }
+        return half4v{y01.x, y01.y, y23.x, y23.y};
+    }
+};
+
+// ---------------------------------------------------------- the kernel
+//
+// grid (parts, rows, kv_heads), 4 waves a workgroup. A part is a contiguous
+// slice of the row's list; waves take 16-entry tiles of it in turn, kDlsaNT
+// tiles a batch with all their gathers issued before the first use.
+// Q.K^T on MFMA (v_mfma_f32_16x16x32_f16): A = 16 gathered K rows, B = the G
+// query heads. P.V on MFMA too (v_mfma_f32_16x16x16_f16, K = the tile's 16
+// entries): A = P (row = head r16, entries 4g..4g+3: exactly where the S^T
+// tile leaves them), B = V (entries 4g..4g+3 of one dim). Output tile (p, c)
+// holds heads 4g + i x dims 64p + 4 r16 + c. P enters as an fp16 high part
+// and an fp16 remainder, so p * v is exact and the sums stay fp32 as in the
+// reference.
+template <int D, int GMAX, class Src, bool FAST>
+__device__ __forceinline__ void dlsa_body(const DlsaArgs& a, const Src& src) {
     constexpr int NM = D / 32;
     constexpr int NP = D / 64;  // 64-dim groups: P.V output tiles (p, c), c < 4
     const int part = blockIdx.x, r = blockIdx.y, h = blockIdx.z;
@@ -56,26 +327,35 @@ __global__ __launch_bounds__(256, 2) void dlsa_kernel(DlsaArgs a) {
     const int G = a.G;
     int len = a.lengths[r];
     len = len < 0 ? 0 : (len > a.W ? a.W : len);
-    const int e_begin = (int)((int64_t)len * part / a.parts);
-    const int e_end = (int)((int64_t)len * (part + 1) / a.parts);
+    // Parts split the list at multiples of 16 entries, so a list made of
+    // aligned key runs gives aligned 4-entry groups in every part.
+    const int e_begin = (int)((int64_t)len * part / a.parts) & ~15;
+    const int e_end = part + 1 == a.parts ? len : (int)((int64_t)len * (part + 1) / a.parts) & ~15;
     const int32_t* list = a.lists + (int64_t)r * a.W;
 
-    // Q operand: column r16 = head h*G + r16 (zero past G), dims 32m + 8g..+7.
+    // Q operand: column r16 = head h*G + r16 (zero past G), 8 dims per MFMA
+    // in the source's layout.
     half8 qop[NM];
     {
         const bool ok = r16 < G;
         const f16* qrow = a.q + ((int64_t)(h * G + (ok ? r16 : 0)) * a.L + r) * D;
 #pragma unroll
-        for (int m = 0; m < NM; m++) qop[m] = ok ? *(const half8*)(qrow + 32 * m + 8 * g) : half8{};
+        for (int m = 0; m < NM; m++) {
+            const int base = Src::kQ == kQNatural ? 32 * m + 8 * g : (D / 4) * g + 8 * m;
+            half8 x = ok ? *(const half8*)(qrow + base) : half8{};
+            if constexpr (Src::kQ == kQGroup4) {
+                const u32x4 w = __builtin_bit_cast(u32x4, x);
+                u32x4 o;  // dims (0,4),(1,5),(2,6),(3,7)
+                o.x = __builtin_amdgcn_perm(w.z, w.x, 0x05040100u);
+                o.y = __builtin_amdgcn_perm(w.z, w.x, 0x07060302u);
+                o.z = __builtin_amdgcn_perm(w.w, w.y, 0x05040100u);
+                o.w = __builtin_amdgcn_perm(w.w, w.y, 0x07060302u);
+                x = __builtin_bit_cast(half8, o);
+            }
+            qop[m] = x;
+        }
     }
 
-    // P.V on MFMA (v_mfma_f32_16x16x16_f16, K = the tile's 16 entries): A = P
-    // (row = head r16, entries 4g..4g+3: exactly where the S^T tile leaves
-    // them), B = V (entries 4g..4g+3 of one dim), gathered as 8-byte row
-    // pieces: lane (g, r16) loads dims 64p + 4 r16 .. +3 of entries 4g + j.
-    // Output tile (p, c) holds heads 4g + i x dims 64p + 4 r16 + c. P enters
-    // as an fp16 high part and an fp16 remainder, so p * v is exact and the
-    // sums stay fp32 as in the reference.
     float mrun = -INFINITY;  // running max (log2 domain), column r16
     float lrun = 0.0f;       // running sum, this lane's share
     float4v acc[NP][4];
@@ -84,50 +364,42 @@ __global__ __launch_bounds__(256, 2) void dlsa_kernel(DlsaArgs a) {
 #pragma unroll
         for (int c = 0; c < 4; c++) acc[pp][c] = float4v{0.f, 0.f, 0.f, 0.f};
 
-    const int n_tiles = (e_end - e_begin + 15) / 16;
-    for (int t0 = wave; t0 < n_tiles; t0 += 4 * kDlsaNT) {
-        // ---- gather loads for up to NT tiles
-        u32x4 kc[kDlsaNT][NM];
-        u32x2 vq[kDlsaNT][4][NP];
-        int key_a[kDlsaNT];  // the key of list entry tile*16 + r16 (A-operand row)
-        bool ok_a[kDlsaNT];
+    // One batch of kDlsaNT tiles; ALIGNED: every lane group's four entries
+    // are four consecutive keys from a multiple of 4 (checked wave-wide).
+    // The general (unaligned) gathers hold many scattered loads: they take
+    // one tile at a time (NT = 1).
+    auto batch = [&](auto aligned_tag, auto nt_tag, const int* key_a, const bool* ok_a) {
+        constexpr bool ALIGNED = decltype(aligned_tag)::value;
+        constexpr int NT = decltype(nt_tag)::value;
+        typename Src::Regs rg[NT];
 #pragma unroll
-        for (int b = 0; b < kDlsaNT; b++) {
-            const int tile = t0 + 4 * b;
-            const int e = e_begin + 16 * tile + r16;
-            int key = -1;
-            if (tile < n_tiles && e < e_end) key = list[e];
-            ok_a[b] = key >= 0 && key < a.T;
-            key_a[b] = ok_a[b] ? key : 0;
-            const u32x4* krow = (const u32x4*)(a.k + h * a.khs + (int64_t)key_a[b] * a.krs);
+        for (int b = 0; b < NT; b++) {
+            int key4[4];
 #pragma unroll
-            for (int m = 0; m < NM; m++) kc[b][m] = krow[4 * m + g];
+            for (int j = 0; j < 4; j++) key4[j] = __shfl(key_a[b], 4 * g + j);
+            src.template load<ALIGNED>(rg[b], h, key_a[b], key4, r16, g);
         }
-#pragma unroll
-        for (int b = 0; b < kDlsaNT; b++) {
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                // entry 4g + j's key sits in lane 4g + j (lane r16 holds entry r16)
-                const int key = __shfl(key_a[b], 4 * g + j);
-                const f16* vrow = a.v + h * a.vhs + (int64_t)key * a.vrs + 4 * r16;
-#pragma unroll
-                for (int pp = 0; pp < NP; pp++) vq[b][j][pp] = *(const u32x2*)(vrow + 64 * pp);
-            }
-        }
+        // Every gather of a multi-tile batch is issued before the first use:
+        // without the barrier the scheduler sinks the V gathers below the QK
+        // MFMAs, and the batch waits for them there (c5: 17.9 against 14.6 us
+        // a call). The one-tile general gathers are left to the scheduler (their
+        // many scattered loads would not fit the registers all at once).
+        if constexpr (NT > 1) __builtin_amdgcn_sched_barrier(0);
         // ---- scores: S^T tile, lane holds entries 4g+i for head r16
-        float s[kDlsaNT][4];
+        float sv[NT][4];
         float bmax = -INFINITY;
 #pragma unroll
-        for (int b = 0; b < kDlsaNT; b++) {
+        for (int b = 0; b < NT; b++) {
             float4v sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int m = 0; m < NM; m++)
-                sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(kc[b][m]), qop[m], sacc, 0, 0, 0);
+                sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(src.template k_op<FAST>(rg[b], m),
+                                                              qop[m], sacc, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const bool ok = __shfl(ok_a[b] ? 1 : 0, 4 * g + i) != 0 && r16 < G;
-                s[b][i] = ok ? sacc[i] * a.scale2 : -INFINITY;
-                bmax = fmaxf(bmax, s[b][i]);
+                sv[b][i] = ok ? sacc[i] * a.scale2 : -INFINITY;
+                bmax = fmaxf(bmax, sv[b][i]);
             }
         }
         bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
@@ -151,11 +423,11 @@ __global__ __launch_bounds__(256, 2) void dlsa_kernel(DlsaArgs a) {
                     for (int i = 0; i < 4; i++) acc[pp][c][i] *= f[i];
         }
 #pragma unroll
-        for (int b = 0; b < kDlsaNT; b++) {
+        for (int b = 0; b < NT; b++) {
             half4v ph, pl;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float pv = __builtin_amdgcn_exp2f(s[b][i] - mref);
+                const float pv = __builtin_amdgcn_exp2f(sv[b][i] - mref);
                 lrun += pv;
                 ph[i] = (f16)pv;
                 pl[i] = (f16)(pv - (float)ph[i]);
@@ -164,21 +436,45 @@ __global__ __launch_bounds__(256, 2) void dlsa_kernel(DlsaArgs a) {
             for (int pp = 0; pp < NP; pp++) {
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
-                    // element c of the four entries' 4-dim pieces
-                    const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
-                    uint32_t w0, w1;
-                    if (c < 2) {
-                        w0 = __builtin_amdgcn_perm(vq[b][1][pp].x, vq[b][0][pp].x, sel);
-                        w1 = __builtin_amdgcn_perm(vq[b][3][pp].x, vq[b][2][pp].x, sel);
-                    } else {
-                        w0 = __builtin_amdgcn_perm(vq[b][1][pp].y, vq[b][0][pp].y, sel);
-                        w1 = __builtin_amdgcn_perm(vq[b][3][pp].y, vq[b][2][pp].y, sel);
-                    }
-                    const half4v vb = __builtin_bit_cast(half4v, u32x2{w0, w1});
+                    const half4v vb = src.template v_op<ALIGNED, FAST>(rg[b], pp, c);
                     acc[pp][c] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, vb, acc[pp][c], 0, 0, 0);
                     acc[pp][c] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, vb, acc[pp][c], 0, 0, 0);
                 }
             }
+        }
+    };
+
+    constexpr int NTB = Src::kNT;  // tiles a batch
+    const int n_tiles = (e_end - e_begin + 15) / 16;
+    for (int t0 = wave; t0 < n_tiles; t0 += 4 * NTB) {
+        int key_a[NTB];  // the key of list entry tile*16 + r16 (A-operand row)
+        bool ok_a[NTB];
+        bool aligned = true;
+#pragma unroll
+        for (int b = 0; b < NTB; b++) {
+            const int tile = t0 + 4 * b;
+            const int e = e_begin + 16 * tile + r16;
+            int key = -1;
+            if (tile < n_tiles && e < e_end) key = list[e];
+            ok_a[b] = key >= 0 && key < a.T;
+            key_a[b] = ok_a[b] ? key : 0;
+            if constexpr (Src::kHasAligned) {
+                // each lane compares with its group's first entry
+                const int first = __shfl(key_a[b], r16 & ~3);
+                aligned = aligned && (first & 3) == 0 && key_a[b] == first + (r16 & 3);
+            }
+        }
+        using NTall = std::integral_constant<int, NTB>;
+        using NT1 = std::integral_constant<int, 1>;
+        if constexpr (Src::kHasAligned) {
+            if (__all(aligned)) {
+                batch(std::true_type{}, NTall{}, key_a, ok_a);
+            } else {
+#pragma unroll
+                for (int b = 0; b < NTB; b++) batch(std::false_type{}, NT1{}, key_a + b, ok_a + b);
+            }
+        } else {
+            batch(std::false_type{}, NTall{}, key_a, ok_a);
         }
     }
     lrun += __shfl_xor(lrun, 16);
@@ -270,6 +566,22 @@ __global__ __launch_bounds__(256, 2) void dlsa_kernel(DlsaArgs a) {
     }
 }
 
+
+// One kernel per (head dim, heads per group, row source); affine sources pick
+// the exact 2-op dequant when every cached scale allows it (the cache's
+// fast_flag), else the separately rounded one, in one uniform branch.
+template <int D, int GMAX, class Src>
+__global__ __launch_bounds__(256, 2) void dlsa_kernel(DlsaArgs a, Src src, const int* fast_flag) {
+    if constexpr (Src::kAffine) {
+        if (*fast_flag != 0)
+            dlsa_body<D, GMAX, Src, true>(a, src);
+        else
+            dlsa_body<D, GMAX, Src, false>(a, src);
+    } else {
+        dlsa_body<D, GMAX, Src, true>(a, src);
+    }
+}
+
 // out[qh, r] = sum_p e^(m_p - M) O_p / sum_p e^(m_p - M) l_p (m in the log2 domain).
 // grid (q heads, rows, D/64), 4 waves: lane = dim, wave w sums parts w, w+4, ...
 // with every load issued before the first use (one memory round trip).
@@ -345,17 +657,60 @@ static int auto_parts(int units, int width) {
     return std::max(1, std::min(parts, 128));
 }
 
+// What a read gathers from: fp16 K/V views with strides (cache == nullptr),
+// or a KV cache's own storage.
+struct DlsaSource {
+    const KVCache* cache = nullptr;
+    const void* k = nullptr;
+    const void* v = nullptr;
+    int64_t khs = 0, krs = 0, vhs = 0, vrs = 0;
+};
+
+template <int D, int GM, class Src>
+static void launch_dlsa_kernel(const Src& src, const DlsaArgs& a, dim3 grid, const int* fast,
+                               hipStream_t stream) {
+    hipLaunchKernelGGL((dlsa_kernel<D, GM, Src>), grid, dim3(256), 0, stream, a, src, fast);
+}
+
+template <int D, int GM>
+static void launch_dlsa_source(const DlsaSource& s, const DlsaArgs& a, dim3 grid,
+                               hipStream_t stream) {
+    if (!s.cache) {
+        const SrcStrided<D> src{(const f16*)s.k, (const f16*)s.v, s.khs, s.krs, s.vhs, s.vrs};
+        launch_dlsa_kernel<D, GM>(src, a, grid, nullptr, stream);
+        return;
+    }
+    const KVCache& c = *s.cache;
+    if (c.mode == QW_KV_FP16) {
+        const SrcCacheF16<D> src{(const f16*)c.k_data, (const f16*)c.v_data, c.cap};
+        launch_dlsa_kernel<D, GM>(src, a, grid, nullptr, stream);
+        return;
+    }
+    if constexpr (D == 128 || D == 256) {
+        if (c.bits == 4) {
+            const SrcCacheAffine<D, 4> src{(const uint32_t*)c.k_data, c.k_params,
+                                           (const uint32_t*)c.v_data, (const f16*)c.v_params,
+                                           c.cap, c.code_offset2()};
+            launch_dlsa_kernel<D, GM>(src, a, grid, c.fast_flag, stream);
+        } else {
+            const SrcCacheAffine<D, 8> src{(const uint32_t*)c.k_data, c.k_params,
+                                           (const uint32_t*)c.v_data, (const f16*)c.v_params,
+                                           c.cap, c.code_offset2()};
+            launch_dlsa_kernel<D, GM>(src, a, grid, c.fast_flag, stream);
+        }
+    }
+}
+
 // scratch == nullptr: the split-K partials go to the stream's workspace
 // (allocated or grown on demand); else to `scratch` (scratch_bytes), and an
 // automatic part count is lowered until the partials fit it.
-static int dlsa_sparse_attention_impl(const void* q, const void* k, const void* v, int64_t khs,
-                                      int64_t krs, int64_t vhs, int64_t vrs,
+static int dlsa_sparse_attention_impl(const void* q, const DlsaSource& src,
                                       const int32_t* lists, const int32_t* lengths, int n_rows,
                                       int width, int n_q_heads, int n_kv_heads, int head_dim,
                                       int n_keys, float scale, int parts, int waves, void* out,
                                       hipStream_t stream, void* scratch, size_t scratch_bytes) {
-    QW_REQUIRE(q && k && v && lists && lengths && out, QW_ERR_INVALID_ARGUMENT,
-               "dlsa_sparse_attention: null pointer");
+    QW_REQUIRE(q && lists && lengths && out && (src.cache || (src.k && src.v)),
+               QW_ERR_INVALID_ARGUMENT, "dlsa_sparse_attention: null pointer");
     QW_REQUIRE(n_kv_heads > 0 && n_q_heads > 0 && n_q_heads % n_kv_heads == 0 && n_keys > 0 &&
                    n_rows > 0,
                QW_ERR_INVALID_ARGUMENT, "dlsa_sparse_attention: bad head or length geometry");
@@ -367,11 +722,16 @@ static int dlsa_sparse_attention_impl(const void* q, const void* k, const void* 
     QW_REQUIRE(width > 0, QW_ERR_INVALID_ARGUMENT, "dlsa_sparse_attention: empty list width");
     QW_REQUIRE(parts >= 0 && waves >= 0 && waves <= 16, QW_ERR_INVALID_ARGUMENT,
                "dlsa_sparse_attention: bad launch knobs");
-    // 16-byte row loads: row starts and strides must keep 8-element alignment.
-    QW_REQUIRE(((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0 && khs % 8 == 0 &&
-                   krs % 8 == 0 && vhs % 8 == 0 && vrs % 8 == 0 && ((uintptr_t)q % 16) == 0,
-               QW_ERR_UNSUPPORTED,
-               "dlsa_sparse_attention: K/V/q must be 16-byte aligned with strides % 8 == 0");
+    QW_REQUIRE(((uintptr_t)q % 16) == 0, QW_ERR_UNSUPPORTED,
+               "dlsa_sparse_attention: q must be 16-byte aligned");
+    if (!src.cache) {
+        // 16-byte row loads: row starts and strides must keep 8-element alignment.
+        QW_REQUIRE(((uintptr_t)src.k % 16) == 0 && ((uintptr_t)src.v % 16) == 0 &&
+                       src.khs % 8 == 0 && src.krs % 8 == 0 && src.vhs % 8 == 0 &&
+                       src.vrs % 8 == 0,
+                   QW_ERR_UNSUPPORTED,
+                   "dlsa_sparse_attention: K/V/q must be 16-byte aligned with strides % 8 == 0");
+    }
     int dev = 0;
     QW_HIP_CHECK(hipGetDevice(&dev));
     // bytes of one part's partials: an fp32 output row and an (m, l) pair per (row, q head)
@@ -389,12 +749,6 @@ static int dlsa_sparse_attention_impl(const void* q, const void* k, const void* 
                    "-byte scratch (use fewer parts or rows)");
     DlsaArgs a;
     a.q = (const f16*)q;
-    a.k = (const f16*)k;
-    a.v = (const f16*)v;
-    a.khs = khs;
-    a.krs = krs;
-    a.vhs = vhs;
-    a.vrs = vrs;
     a.lists = lists;
     a.lengths = lengths;
     a.out = (f16*)out;
@@ -419,17 +773,17 @@ static int dlsa_sparse_attention_impl(const void* q, const void* k, const void* 
         a.part_o = (float*)ws;
         a.part_ml = (float2*)((char*)ws + no * head_dim * sizeof(float));
     }
-    dim3 grid(parts, n_rows, n_kv_heads);
-#define QW_DLSA_LAUNCH(DD, GM) \
-    hipLaunchKernelGGL((dlsa_kernel<DD, GM>), grid, dim3(256), 0, stream, a)
+    const dim3 grid(parts, n_rows, n_kv_heads);
     if (head_dim == 256) {
-        if (G <= 8) QW_DLSA_LAUNCH(256, 8); else QW_DLSA_LAUNCH(256, 16);
+        if (G <= 8) launch_dlsa_source<256, 8>(src, a, grid, stream);
+        else launch_dlsa_source<256, 16>(src, a, grid, stream);
     } else if (head_dim == 128) {
-        if (G <= 8) QW_DLSA_LAUNCH(128, 8); else QW_DLSA_LAUNCH(128, 16);
+        if (G <= 8) launch_dlsa_source<128, 8>(src, a, grid, stream);
+        else launch_dlsa_source<128, 16>(src, a, grid, stream);
     } else {
-        if (G <= 8) QW_DLSA_LAUNCH(64, 8); else QW_DLSA_LAUNCH(64, 16);
+        if (G <= 8) launch_dlsa_source<64, 8>(src, a, grid, stream);
+        else launch_dlsa_source<64, 16>(src, a, grid, stream);
     }
-#undef QW_DLSA_LAUNCH
     QW_HIP_CHECK(hipGetLastError());
     if (parts > 1) {
         hipLaunchKernelGGL(dlsa_merge_kernel, dim3(n_q_heads, n_rows, head_dim / 64), dim3(256), 0,
@@ -441,14 +795,66 @@ static int dlsa_sparse_attention_impl(const void* q, const void* k, const void* 
     return QW_OK;
 }
 
+static DlsaSource strided(const void* k, const void* v, int64_t khs, int64_t krs, int64_t vhs,
+                          int64_t vrs) {
+    DlsaSource s;
+    s.k = k;
+    s.v = v;
+    s.khs = khs;
+    s.krs = krs;
+    s.vhs = vhs;
+    s.vrs = vrs;
+    return s;
+}
+
 int dlsa_sparse_attention(const void* q, const void* k, const void* v, int64_t khs, int64_t krs,
                           int64_t vhs, int64_t vrs, const int32_t* lists, const int32_t* lengths,
                           int n_rows, int width, int n_q_heads, int n_kv_heads, int head_dim,
                           int n_keys, float scale, int parts, int waves, void* out,
                           hipStream_t stream) {
-    return dlsa_sparse_attention_impl(q, k, v, khs, krs, vhs, vrs, lists, lengths, n_rows, width,
-                                      n_q_heads, n_kv_heads, head_dim, n_keys, scale, parts, waves,
-                                      out, stream, nullptr, 0);
+    return dlsa_sparse_attention_impl(q, strided(k, v, khs, krs, vhs, vrs), lists, lengths, n_rows,
+                                      width, n_q_heads, n_kv_heads, head_dim, n_keys, scale, parts,
+                                      waves, out, stream, nullptr, 0);
+}
+
+// The read over a KV cache (the qwen3_next/dlsa.rs:161-177 pair
+// update_and_fetch + sparse_attention, with the fetch gone): keys are the
+// cache's first `offset` rows. fp16 and affine / Int8 caches are read in
+// place (quantized rows dequantized inside the gather as the fetch would);
+// Turbo4 rows have no in-place form (a rotated codebook basis), so they are
+// fetched to fp16 first, as the reference's update_and_fetch does, into a
+// buffer the cache keeps.
+int KVCache::dlsa_attention(const void* q, int n_q_heads, int n_rows, const int32_t* lists,
+                            const int32_t* lengths, int width, float scale, void* out,
+                            hipStream_t stream) {
+    QW_REQUIRE(offset > 0, QW_ERR_INVALID_ARGUMENT, "dlsa_attention: the cache is empty");
+    DeviceGuard dg(device);
+    QW_REQUIRE(dg.ok, QW_ERR_HIP, "dlsa_attention: hipSetDevice failed");
+    if (turbo4()) {
+        const size_t plane = (size_t)hkv * offset * D * sizeof(f16);
+        void* buf = nullptr;
+        int rc = fetch_ws.get(2 * plane, stream, &buf);
+        if (rc) return rc;
+        rc = dequantize(0, offset, buf, (char*)buf + plane, stream);
+        if (rc) return rc;
+        return dlsa_sparse_attention_impl(
+            q, strided(buf, (char*)buf + plane, (int64_t)offset * D, D, (int64_t)offset * D, D),
+            lists, lengths, n_rows, width, n_q_heads, hkv, D, offset, scale, 0, 0, out, stream,
+            nullptr, 0);
+    }
+    DlsaSource s;
+    s.cache = this;
+    return dlsa_sparse_attention_impl(q, s, lists, lengths, n_rows, width, n_q_heads, hkv, D,
+                                      offset, scale, 0, 0, out, stream, nullptr, 0);
+}
+
+int KVCache::update_and_dlsa_attention(const void* q, int n_q_heads, int n_rows,
+                                       const void* k_new, const void* v_new, const int32_t* lists,
+                                       const int32_t* lengths, int width, float scale, void* out,
+                                       hipStream_t stream) {
+    int rc = update(k_new, v_new, n_rows, stream);
+    if (rc) return rc;
+    return dlsa_attention(q, n_q_heads, n_rows, lists, lengths, width, scale, out, stream);
 }
 
 // ------------------------------------------------ the no-allocation variant
@@ -491,9 +897,9 @@ int dlsa_sparse_attention_noalloc(const void* q, const void* k, const void* v, i
     void* ws = nullptr;
     int rc = scratch_address(dev, &ws);
     if (rc) return rc;
-    return dlsa_sparse_attention_impl(q, k, v, khs, krs, vhs, vrs, lists, lengths, n_rows, width,
-                                      n_q_heads, n_kv_heads, head_dim, n_keys, scale, parts, waves,
-                                      out, stream, ws, kDlsaScratchBytes);
+    return dlsa_sparse_attention_impl(q, strided(k, v, khs, krs, vhs, vrs), lists, lengths, n_rows,
+                                      width, n_q_heads, n_kv_heads, head_dim, n_keys, scale, parts,
+                                      waves, out, stream, ws, kDlsaScratchBytes);
 }
 
 }  // namespace qw

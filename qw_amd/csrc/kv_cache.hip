@@ -178,6 +178,7 @@ int KVCache::release() {
     for (void* p : ptrs)
         if (p) (void)hipFree(p);
     ws.release();
+    fetch_ws.release();
     ws_ptr = nullptr;
     fast_flag = nullptr;
     t4_tables = nullptr;

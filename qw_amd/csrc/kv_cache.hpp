@@ -64,6 +64,8 @@ struct KVCache {
     // the current buffer (valid after ensure_workspace).
     GrowBuffer ws;
     void* ws_ptr = nullptr;
+    // fp16 rows of a Turbo4 cache fetched for the D-LSA read (dlsa.hip)
+    GrowBuffer fetch_ws;
 
     KvLayout layout() const { return KvLayout{bits, D, hkv, cap}; }
     // Codes and per-group (scale, bias) in the affine layout: the affine modes
@@ -114,6 +116,14 @@ struct KVCache {
     // cache.rs:3607 fused prefix attention, no append
     int attention(const void* q, int n_q_heads, int n_rows, float scale, bool causal, void* out,
                   hipStream_t stream);
+    // D-LSA K2 over the cache's rows (qwen3_next/dlsa.rs:161-177:
+    // update_and_fetch, then dlsa_attention::sparse_attention), dlsa.hip
+    int dlsa_attention(const void* q, int n_q_heads, int n_rows, const int32_t* lists,
+                       const int32_t* lengths, int width, float scale, void* out,
+                       hipStream_t stream);
+    int update_and_dlsa_attention(const void* q, int n_q_heads, int n_rows, const void* k_new,
+                                  const void* v_new, const int32_t* lists, const int32_t* lengths,
+                                  int width, float scale, void* out, hipStream_t stream);
     // cache.rs:2251 `trim`
     int trim(int n);
     // cache.rs:570-626 snapshot tensors

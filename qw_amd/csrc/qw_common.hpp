@@ -74,6 +74,22 @@ __host__ __device__ inline int v_phys_dim(int d, int D, int bits) {
     return 16 * e * (r / e) + e * n + (r % e);
 }
 
+// v_phys_dim(64 pp + 4 n + c, D, bits) split into a part that depends only
+// on n (0..15, an MFMA column) and one that depends only on (pp, c), so that a
+// lane's 4 * D/64 slots are one base plus immediates (same values, by algebra:
+// 4n % DPL + c < DPL because DPL = D/16 is a multiple of 4).
+__host__ __device__ inline int v_slot_base(int n, int D, int bits) {
+    const int dpl = D / 16;
+    if (bits == 4) return 64 * (n % (dpl / 4)) + 4 * ((4 * n) / dpl);
+    if (bits == 8) return 16 * ((4 * n) % dpl) + 2 * ((4 * n) / dpl);
+    return 16 * ((4 * n) % dpl) + (4 * n) / dpl;
+}
+__host__ __device__ constexpr int v_slot_off(int pp, int c, int D, int bits) {
+    return bits == 4 ? c + (256 * pp) / (D / 16)
+                     : (bits == 8 ? 32 * (c / 2) + c % 2 + (128 * pp) / (D / 16)
+                                  : 16 * c + (64 * pp) / (D / 16));
+}
+
 __device__ inline half2v h2(uint32_t x) { return __builtin_bit_cast(half2v, x); }
 
 // A 32-bit constant materialized in a VGPR the compiler cannot see through.
