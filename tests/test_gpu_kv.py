@@ -199,6 +199,28 @@ def test_update_and_attention_vs_oracle(oracle_lib, bits, T_prefix, L, causal):
     assert_as_exact_as_reference(out, ref, f64, f"bits={bits} T={T_prefix}+{L}")
 
 
+# The served verify blocks (MTP / DFlash2: 3..5 draft rows, the reference's
+# fused-pass sizes, turbo4_attention.cpp:360, fused_attention.rs:70-100) on the
+# affine codec at the config geometry: 18..30 rows a KV head (the block
+# kernel, key-split), and G = 8 with 32 rows a KV head.
+@pytest.mark.parametrize("bits,T_prefix,L,hq", [
+    (4, 32768, 4, 24),      # 4-row verify at 32k
+    (4, 65536, 5, 24),      # 5-row verify at 64k
+    (4, 2049, 3, 24),       # 3 rows just past the reference's 2048-token gate
+    (8, 5000, 5, 24),       # 8-bit
+    (4, 3000, 4, 32),       # G = 8: exactly 32 rows a KV head
+])
+def test_served_verify_blocks_vs_oracle(oracle_lib, bits, T_prefix, L, hq):
+    import qw_amd
+
+    out, ref, f64 = _layer_call(oracle_lib, qw_amd, bits, T_prefix, L, True,
+                                seed=bits * 13 + T_prefix + L + hq, hq=hq)
+    assert np.isfinite(out).all()
+    what = f"verify bits={bits} T={T_prefix}+{L} hq={hq}"
+    assert_close(out, ref, what)
+    assert_as_exact_as_reference(out, ref, f64, what)
+
+
 # Many query rows per KV head (G * L > 16): the LDS-shared block kernel.
 @pytest.mark.parametrize("bits,T_prefix,L,causal,D,hq,hkv,rows", [
     (4, 65536, 16, True, 256, 24, 4, None),     # config 4: 16-row verify at 64k, 4-bit
@@ -230,6 +252,17 @@ def test_block_causal_rows_are_prefix_independent(oracle_lib):
 
     r = rng(4242)
     hkv, hq, D, T0, L = 4, 24, 256, 3000, 8
+    _rows_equal_decode(qw_amd, r, hkv, hq, D, T0, L)
+
+
+def test_verify_rows_equal_row_by_row_decode():
+    """The same for a served 5-row verify block (30 rows a KV head)."""
+    import qw_amd
+
+    _rows_equal_decode(qw_amd, rng(4343), 4, 24, 256, 5000, 5)
+
+
+def _rows_equal_decode(qw_amd, r, hkv, hq, D, T0, L):
     k, v = _kv(r, hkv, T0 + L, D)
     q = r.standard_normal((hq, L, D)).astype(np.float16)
     a = qw_amd.KVCache("affine4", hkv, D)
