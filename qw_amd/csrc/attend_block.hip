@@ -538,10 +538,15 @@ template <int BITS, int D, int RT>
 __global__ __launch_bounds__(64 * kBlockWaves, 1) void attend_block_kernel(BlockArgs a) {
     // two buffers, each a K and a V tile of KT keys in fp16 (~130 KB)
     extern __shared__ __attribute__((aligned(16))) char lds_buf[];
-    if (BITS == 16 || *a.fast_flag != 0)
-        block_body<BITS, D, RT, true>(a, lds_buf);
-    else
+    // The exact 2-op dequant runs without waiting for the cache's fast flag;
+    // a launch whose cache holds a scale outside its exact range redoes the
+    // workgroup's share with the separately rounded dequant (same threads,
+    // same output elements, so the second pass's writes replace the first's).
+    block_body<BITS, D, RT, true>(a, lds_buf);
+    if (BITS != 16 && *a.fast_flag == 0) {
+        __syncthreads();
         block_body<BITS, D, RT, false>(a, lds_buf);
+    }
 }
 
 template <int BITS, int D, int RT>

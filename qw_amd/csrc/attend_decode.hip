@@ -101,8 +101,8 @@ constexpr int decode_stages() {
 // of its block, added to every dim of that group at the end (the bias is
 // exact in fp32; only MLX's second rounding of each V element is skipped).
 template <int BITS, int D, int NW, bool FAST>
-__device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)[16], float* sm_fw,
-                                            float* sm_o, half8 (*sm_q)[64]) {
+__device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)[16], float* sm_o,
+                                            half8 (*sm_q)[64]) {
     using S = DecodeShape<BITS, D>;
     constexpr int NM = S::NM, DPL = S::DPL, NG = S::NG, KL = S::KL, VL = S::VL;
     constexpr bool AFF = BITS != 16;
@@ -443,11 +443,13 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
     lsum += __shfl_xor(lsum, 32);
     // ---- merge the NW waves. Each wave parks its accumulators in LDS in
     // their MFMA layout (float4 of rows 4g..4g+3 at dim r16*DPL + mm; only
-    // the lane groups holding rows < R), and its (m, l). One thread a row then
-    // forms the factors f_w = e^(m_w - M) and L; every thread sums its output
-    // elements out[row][d] = sum_w f_w O_w[row][d] and writes the partial.
-    // sm_o row stride: G4 * 16 float4 plus one, so the phase-B reads (16
-    // consecutive dims = 16 values of mm) fall on distinct banks.
+    // the lane groups holding rows < R), and its (m, l). After one barrier
+    // every thread forms the factors f_w = e^(m_w - M) of its output row
+    // itself (the (m, l) reads are broadcasts: a row's D consecutive outputs
+    // belong to whole waves), sums out[row][d] = sum_w f_w O_w[row][d] and
+    // writes the partial.
+    // sm_o row stride: G4 * 16 float4 plus one, so the reads (16 consecutive
+    // dims = 16 values of mm) fall on distinct banks.
     const int R = a.R;
     const int G4 = (R + 3) >> 2;          // lane groups holding real rows
     const int RS = G4 * 16 + 1;           // float4 per (wave, mm)
@@ -458,34 +460,24 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
         for (int mm = 0; mm < DPL; mm++) dst[mm * RS] = acc_o[mm] + acc_b;
     }
     __syncthreads();
-    float* sm_f = (float*)sm_fw;  // [NW][16] factors, then [16] L
-    if (threadIdx.x < 16) {
-        const int row = threadIdx.x;
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < NW; w++) M = fmaxf(M, sm_ml[w][row].x);
-        float L = 0.0f;
-#pragma unroll
-        for (int w = 0; w < NW; w++) {
-            const float2 ml = sm_ml[w][row];
-            const float f = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((ml.x - M) * kLog2e);
-            sm_f[w * 16 + row] = f;
-            L = __builtin_fmaf(f, ml.y, L);
-        }
-        sm_f[NW * 16 + row] = L;
-        sm_f[NW * 16 + 16 + row] = M;
-    }
-    __syncthreads();
     const int64_t pbase = ((int64_t)h * a.nc + c) * 16;
     for (int o = threadIdx.x; o < R * D; o += 64 * NW) {
         const int row = o / D, d = o % D;
         const int rg = row >> 2, ri = row & 3, rl = d / DPL, mm = d % DPL;
         const float* src = (const float*)sm_o + ((int64_t)mm * RS + rg * 16 + rl) * 4 + ri;
-        float acc = 0.0f;
+        float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < NW; w++) acc = __builtin_fmaf(sm_f[w * 16 + row], src[(int64_t)w * DPL * RS * 4], acc);
+        for (int w = 0; w < NW; w++) M = fmaxf(M, sm_ml[w][row].x);
+        float acc = 0.0f, L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float2 ml = sm_ml[w][row];
+            const float f = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((ml.x - M) * kLog2e);
+            acc = __builtin_fmaf(f, src[(int64_t)w * DPL * RS * 4], acc);
+            L = __builtin_fmaf(f, ml.y, L);
+        }
         a.part_o[(pbase + row) * D + d] = acc;
-        if (d == 0) a.part_ml[pbase + row] = float2{sm_f[NW * 16 + 16 + row], sm_f[NW * 16 + row]};
+        if (d == 0) a.part_ml[pbase + row] = float2{M, L};
     }
 }
 
@@ -494,16 +486,19 @@ __global__ __launch_bounds__((64 * decode_waves<BITS, D>()), 1) void attend_deco
     DecodeArgs a) {
     constexpr int NW = decode_waves<BITS, D>();
     __shared__ float2 sm_ml[NW][16];
-    __shared__ float sm_fw[NW * 16 + 32];
     __shared__ half8 sm_q[D / 32][64];
     // dynamic LDS: the wave merge's sm_o [NW][DPL][R] float4
     extern __shared__ __attribute__((aligned(16))) float sm_o[];
-    // One uniform branch for the whole launch: the exact 2-op dequant when
-    // every cached scale allows it, else the separately rounded path.
-    if (BITS == 16 || *a.fast_flag != 0)
-        decode_body<BITS, D, NW, true>(a, sm_ml, sm_fw, sm_o, sm_q);
-    else
-        decode_body<BITS, D, NW, false>(a, sm_ml, sm_fw, sm_o, sm_q);
+    // The exact 2-op dequant runs first without waiting for the cache's fast
+    // flag (a memory round trip ahead of every load). In the rare launch whose
+    // cache holds a scale outside that dequant's exact range, the workgroup
+    // then redoes its share with the separately rounded dequant, and that
+    // pass's partial (same threads, same elements) replaces the first.
+    decode_body<BITS, D, NW, true>(a, sm_ml, sm_o, sm_q);
+    if (BITS != 16 && *a.fast_flag == 0) {
+        __syncthreads();
+        decode_body<BITS, D, NW, false>(a, sm_ml, sm_o, sm_q);
+    }
 }
 
 // Combines the per-workgroup partials of one query row (partials of a KV head

@@ -325,13 +325,16 @@ __device__ __forceinline__ void dlsa_body(const DlsaArgs& a, const Src& src) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r16 = lane & 15, g = lane >> 4;
     const int G = a.G;
+    // Parts split the list's width W at multiples of 16 entries, so the list
+    // loads depend on the launch arguments only (not on the row's length, a
+    // memory round trip of its own) and a list made of aligned key runs gives
+    // aligned 4-entry groups in every part. The length, loaded alongside,
+    // masks the entries at or past it.
+    const int e_begin = (int)((int64_t)a.W * part / a.parts) & ~15;
+    const int e_end = part + 1 == a.parts ? a.W : (int)((int64_t)a.W * (part + 1) / a.parts) & ~15;
+    const int32_t* list = a.lists + (int64_t)r * a.W;
     int len = a.lengths[r];
     len = len < 0 ? 0 : (len > a.W ? a.W : len);
-    // Parts split the list at multiples of 16 entries, so a list made of
-    // aligned key runs gives aligned 4-entry groups in every part.
-    const int e_begin = (int)((int64_t)len * part / a.parts) & ~15;
-    const int e_end = part + 1 == a.parts ? len : (int)((int64_t)len * (part + 1) / a.parts) & ~15;
-    const int32_t* list = a.lists + (int64_t)r * a.W;
 
     // Q operand: column r16 = head h*G + r16 (zero past G), 8 dims per MFMA
     // in the source's layout.
@@ -456,7 +459,7 @@ __device__ __forceinline__ void dlsa_body(const DlsaArgs& a, const Src& src) {
             const int e = e_begin + 16 * tile + r16;
             int key = -1;
             if (tile < n_tiles && e < e_end) key = list[e];
-            ok_a[b] = key >= 0 && key < a.T;
+            ok_a[b] = e < len && key >= 0 && key < a.T;
             key_a[b] = ok_a[b] ? key : 0;
             if constexpr (Src::kHasAligned) {
                 // each lane compares with its group's first entry
@@ -480,105 +483,72 @@ __device__ __forceinline__ void dlsa_body(const DlsaArgs& a, const Src& src) {
     lrun += __shfl_xor(lrun, 16);
     lrun += __shfl_xor(lrun, 32);
 
-    // ---- merge the waves: (m, l) per head, then the accumulators
+    // ---- merge the 4 waves through LDS: each wave parks its (m, l) and its
+    // unscaled accumulators (head 4g + i, dims 64p + 4 r16 .. +3 as one
+    // float4, i.e. the dims in order); after one barrier thread t owns dim
+    // t % D of every 256 / D-th head, forms the factors e^(m_w - M) itself
+    // and writes the merged row, so the partial's stores are spread over all
+    // four waves. Up to 32 KB of accumulators a round (8 heads at D = 256):
+    // G <= 8 takes one round.
+    constexpr int HC = GMAX * D <= 2048 ? GMAX : 2048 / D;
     __shared__ float2 sm_ml[4][16];
-    __shared__ float4v sm_acc[2][GMAX][D / 4];
+    __shared__ float4v sm_acc[4][HC][D / 4];
     if (g == 0) sm_ml[wave][r16] = float2{mrun, lrun};
-    __syncthreads();
-    float Mi[4], Li[4];  // heads 4g + i
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int hd = 4 * g + i;
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < 4; w++) M = fmaxf(M, sm_ml[w][hd].x);
-        float L = 0.0f, own = 0.0f;
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-            const float mw = sm_ml[w][hd].x;
-            const float f = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-            L += f * sm_ml[w][hd].y;
-            if (w == wave) own = f;
-        }
-        Mi[i] = M;
-        Li[i] = L;
-#pragma unroll
-        for (int pp = 0; pp < NP; pp++)
-#pragma unroll
-            for (int c = 0; c < 4; c++) acc[pp][c][i] *= own;
-    }
-    // head 4g + i, dims 64p + 4 r16 .. +3 as one float4
-    auto store = [&](int buf) {
+    const float* accf = (const float*)&sm_acc[0][0][0];
+    for (int hc0 = 0; hc0 < G; hc0 += HC) {
+        if (hc0 > 0) __syncthreads();  // the previous round's reads are done
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int hd = 4 * g + i;
-            if (hd < G && hd < GMAX)
+            if (hd >= hc0 && hd < hc0 + HC && hd < G)
 #pragma unroll
                 for (int pp = 0; pp < NP; pp++)
-                    sm_acc[buf][hd][16 * pp + r16] =
+                    sm_acc[wave][hd - hc0][16 * pp + r16] =
                         float4v{acc[pp][0][i], acc[pp][1][i], acc[pp][2][i], acc[pp][3][i]};
         }
-    };
-    auto add = [&](int buf) {
+        __syncthreads();
+        const int nh = min(HC, G - hc0);
+        for (int o = threadIdx.x; o < nh * D; o += 256) {
+            const int hl = o / D, d = o % D, hd = hc0 + hl;
+            float M = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int hd = 4 * g + i;
-            if (hd < G && hd < GMAX)
+            for (int w = 0; w < 4; w++) M = fmaxf(M, sm_ml[w][hd].x);
+            float O = 0.0f, Ls = 0.0f;
 #pragma unroll
-                for (int pp = 0; pp < NP; pp++) {
-                    const float4v o = sm_acc[buf][hd][16 * pp + r16];
-#pragma unroll
-                    for (int c = 0; c < 4; c++) acc[pp][c][i] += o[c];
-                }
-        }
-    };
-    if (wave >= 2) store(wave - 2);
-    __syncthreads();
-    if (wave < 2) add(wave);
-    __syncthreads();
-    if (wave == 1) store(0);
-    __syncthreads();
-    if (wave != 0) return;
-    add(0);
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int hd = 4 * g + i;
-        if (hd >= G) continue;
-        const int qh = h * G + hd;
-        if (a.parts == 1) {
-            const float inv = Li[i] > 0.0f ? 1.0f / Li[i] : 0.0f;
-            f16* dst = a.out + ((int64_t)qh * a.L + r) * D + 4 * r16;
-#pragma unroll
-            for (int pp = 0; pp < NP; pp++) {
-                const half4v o = {(f16)(acc[pp][0][i] * inv), (f16)(acc[pp][1][i] * inv),
-                                  (f16)(acc[pp][2][i] * inv), (f16)(acc[pp][3][i] * inv)};
-                *(half4v*)(dst + 64 * pp) = o;
+            for (int w = 0; w < 4; w++) {
+                const float2 ml = sm_ml[w][hd];
+                const float f = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - M);
+                O = __builtin_fmaf(f, accf[(w * HC + hl) * D + d], O);
+                Ls = __builtin_fmaf(f, ml.y, Ls);
             }
-        } else {
-            const int64_t pr = ((int64_t)r * a.hq + qh) * a.parts + part;
-            float* dst = a.part_o + pr * D + 4 * r16;
-#pragma unroll
-            for (int pp = 0; pp < NP; pp++)
-                *(float4v*)(dst + 64 * pp) =
-                    float4v{acc[pp][0][i], acc[pp][1][i], acc[pp][2][i], acc[pp][3][i]};
-            if (r16 == 0) a.part_ml[pr] = float2{Mi[i], Li[i]};
+            const int qh = h * G + hd;
+            if (a.parts == 1) {
+                a.out[((int64_t)qh * a.L + r) * D + d] = (f16)(Ls > 0.0f ? O / Ls : 0.0f);
+            } else {
+                const int64_t pr = ((int64_t)r * a.hq + qh) * a.parts + part;
+                a.part_o[pr * D + d] = O;
+                if (d == 0) a.part_ml[pr] = float2{M, Ls};
+            }
         }
     }
 }
 
 
-// One kernel per (head dim, heads per group, row source); affine sources pick
+// One kernel per (head dim, heads per group, row source). Affine sources use
 // the exact 2-op dequant when every cached scale allows it (the cache's
-// fast_flag), else the separately rounded one, in one uniform branch.
+// fast_flag), else the separately rounded one.
 template <int D, int GMAX, class Src>
 __global__ __launch_bounds__(256, 2) void dlsa_kernel(DlsaArgs a, Src src, const int* fast_flag) {
+    dlsa_body<D, GMAX, Src, true>(a, src);
     if constexpr (Src::kAffine) {
-        if (*fast_flag != 0)
-            dlsa_body<D, GMAX, Src, true>(a, src);
-        else
+        // The exact 2-op dequant ran without waiting for the cache's fast
+        // flag; a cache holding a scale outside its exact range takes the
+        // separately rounded one in a second pass whose writes (same threads,
+        // same elements) replace the first's.
+        if (*fast_flag == 0) {
+            __syncthreads();
             dlsa_body<D, GMAX, Src, false>(a, src);
-    } else {
-        dlsa_body<D, GMAX, Src, true>(a, src);
+        }
     }
 }
 
@@ -645,14 +615,16 @@ static int dlsa_workspace(int device, hipStream_t stream, size_t need, void** ou
 }
 
 // Launch policy (the reference's auto_parts, mlx_cxx_dlsa_attention.cpp:379-400,
-// re-derived for 256 CUs): one pass when rows x kv_heads alone fill the CUs,
-// else split each list so that about one workgroup a CU runs (measured for one
-// row, 4 KV heads, 4612 entries: 48 parts 14.2 us, 64 parts 14.3 us, 96 parts
-// 15.3 us, 128 parts 16.3 us), keeping at least 16 entries (one tile) a part
-// and at most 128 parts.
+// re-derived for 256 CUs): one pass when rows x kv_heads alone reach 192
+// workgroups, else split each list so that about 192 workgroups run (3/4 of
+// the CUs still saturate HBM with these gathers, and fewer parts make the
+// merge cheaper; measured for one row, 4 KV heads, 4612 entries: 40-48 parts
+// 13.0 us, 56 parts 13.2 us, 64 parts 13.4 us, 72 parts 15.5 us), keeping at
+// least 16 entries (one tile) a part and at most 128 parts.
 static int auto_parts(int units, int width) {
-    if (units >= 256) return 1;
-    int parts = (256 + units - 1) / units;
+    constexpr int kTargetWorkgroups = 192;
+    if (units >= kTargetWorkgroups) return 1;
+    int parts = (kTargetWorkgroups + units - 1) / units;
     parts = std::min(parts, std::max(1, width / 16));
     return std::max(1, std::min(parts, 128));
 }

@@ -56,7 +56,7 @@ def _case(seed, T, H, G, D, L, W):
 def test_noalloc_equals_allocating_entry():
     L = _lib()
     scale = 256 ** -0.5
-    # config-5 shape (one row, 4612 entries, automatic parts: 64), then a
+    # config-5 shape (one row, 4612 entries, automatic parts: 48), then a
     # smaller call (3 rows, 700 entries) reusing the same scratch
     big = _case(1, 131072 // 8, 4, 6, 256, 1, 4612)
     small = _case(2, 3000, 4, 6, 256, 3, 700)
@@ -72,13 +72,15 @@ def test_noalloc_equals_allocating_entry():
 def test_noalloc_scratch_limit():
     L = _lib()
     scale = 256 ** -0.5
-    q, k, v, lists, lens = _case(3, 3000, 4, 16, 256, 2, 900)
-    part_bytes = 2 * 64 * (256 * 4 + 8)            # rows x q heads x (fp32 row + (m, l))
-    fit = SCRATCH_BYTES // part_bytes               # 31 parts fit
-    assert fit == 31
+    # 40 rows x 64 q heads: 2.6 MB of partials a part, so one part fits
+    q, k, v, lists, lens = _case(3, 3000, 4, 16, 256, 40, 100)
+    part_bytes = 40 * 64 * (256 * 4 + 8)           # rows x q heads x (fp32 row + (m, l))
+    fit = SCRATCH_BYTES // part_bytes
+    assert fit == 1
     rc, _ = _call(L, "qw_dlsa_sparse_attention_noalloc", q, k, v, lists, lens, scale, fit + 1)
     assert rc == 1 and b"scratch" in L.qw_last_error()
-    # automatic parts (32 here) are lowered to what fits: equal to 31 explicit parts
+    # automatic parts (2 here: 160 workgroups a part) are lowered to what fits:
+    # equal to one explicit part
     rc_a, a = _call(L, "qw_dlsa_sparse_attention_with", q, k, v, lists, lens, scale, fit)
     rc_b, b = _call(L, "qw_dlsa_sparse_attention_noalloc", q, k, v, lists, lens, scale, 0)
     torch.cuda.synchronize()
@@ -87,4 +89,4 @@ def test_noalloc_scratch_limit():
     rc_c, c = _call(L, "qw_dlsa_sparse_attention_with", q, k, v, lists, lens, scale, 0)
     torch.cuda.synchronize()
     assert rc_c == 0
-    assert_close(_np(b), _np(c), "noalloc auto (31 parts) vs auto (32 parts)")
+    assert_close(_np(b), _np(c), "noalloc auto (1 part) vs auto (2 parts)")
