@@ -89,29 +89,35 @@ struct BlockShape {
     static constexpr int TPR = D / 32;    // 32-dim K slices a row
     static constexpr int LTPR = TPR == 8 ? 3 : 2;
     static constexpr int TPB = D / 4;     // 4-slot V slices a block
-    static constexpr int KROW = D / 8 + 1;  // K row stride in 16-byte chunks (one pad chunk)
-    static constexpr int KBUF = (KT * KROW + 4 * (KT / 16)) * 16;  // K tile bytes in LDS
+    static constexpr int KBUF = (D / 8) * KT * 16;  // K tile bytes in LDS (chunk-major)
     static constexpr int VROW = D + D / 16;  // V block stride in chunks (a pad chunk per 16 slots)
     static constexpr int VBUF = (KT / 8) * VROW * 16;               // V tile bytes in LDS
     static constexpr int BUF = KBUF + VBUF;                         // one buffer
 };
 
-// LDS layouts (16-byte chunks):
-//   K  [key][D/8 + 1 chunks] plus 4 chunks every 16 keys: chunk c of key k
-//      sits at kaddr(k, c) = k * (D/8 + 1) + 4 * (k >> 4) + c. The QK A operand
-//      reads keys 8(r>>2) + 4t + (r&3) (r = lane & 15) at one chunk: k mod 16
-//      takes 0-3 and 8-11 twice, and the (k >> 4) shift moves the second pair
-//      to 4-7 and 12-15, so a 16-lane phase hits 16 distinct bank groups; and
-//      the address of every (sub-block, tile, step) is the lane's base plus an
-//      immediate. The store phase writes 4 keys x 4 slices a phase, also
-//      conflict-free.
+// LDS layouts (16-byte chunks). Measured on gfx950 (ds_read_b128, 8 waves a
+// CU): an instruction runs at full rate (~210 B/clk a CU) when the 16 lanes of
+// each quarter-wave hit 16 distinct bank groups (chunk mod 16) AND lane r of
+// every quarter-wave hits the same bank group; quarter-waves whose bank groups
+// are rotated against each other run at ~125 B/clk, like a 2-way conflict.
+//   K  chunk-major [D/8 chunks][KT keys]: chunk c of key k sits at
+//      kaddr(k, c) = c * KT + swz(k), swz(k) = k ^ (bit 4 of k) << 2. The QK
+//      A operand (lane (g, r), r = lane & 15) reads chunk g + 4m of key
+//      8(r>>2) + 4t + (r&3) + 32u: the chunk stride KT keeps the quarter-waves
+//      g aligned, and swz maps the 16 keys of a quarter-wave (k mod 16 takes
+//      0-3 and 8-11 twice) to 16 distinct bank groups. Every (step, sub-block)
+//      is the lane's base (one a 16-key tile t) plus an immediate. The store
+//      phase gives each quarter-wave 16 consecutive keys of one 32-dim slice
+//      (quarter-waves differ in the slice): also aligned and distinct.
 //   V  [8-key block][D slots + D/16 pad][8 keys], slots in the V plane's
 //      physical dim order, slot s at s + (s >> 4): the P.V B operand reads 16
 //      consecutive slots a phase (slot 16mm + r at 17mm + r, an immediate
 //      per mm), and the store phase's lanes (slots 4j + e) land on 16 distinct
 //      bank groups.
-__device__ __forceinline__ int kaddr(int key, int chunk, int krow) {
-    return key * krow + 4 * (key >> 4) + chunk;
+__device__ __forceinline__ int kswz(int key) { return key ^ (((key >> 4) & 1) << 2); }
+template <int KT>
+__device__ __forceinline__ int kaddr(int key, int chunk) {
+    return chunk * KT + kswz(key);
 }
 
 // Logical dim of physical slot `slot` of a V block (inverse of v_phys_dim).
@@ -142,7 +148,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     using S = BlockShape<D>;
     constexpr int KT = S::KT, NSUB = S::NSUB, NM = S::NM, NT = S::NT, NG = S::NG;
     constexpr int TPR = S::TPR, LTPR = S::LTPR, TPB = S::TPB, BUF = S::BUF, KBUF = S::KBUF;
-    constexpr int KROW = S::KROW, VROW = S::VROW;
+    constexpr int VROW = S::VROW;
     constexpr int NW = kBlockWaves;
     constexpr bool AFF = BITS != 16;
     constexpr int KU = BITS / 4;  // u32x4 loads a 32-dim K slice / a 4-slot V slice
@@ -211,9 +217,11 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     }
 
     // ---- tile loads: thread slice j (of PER) -> (key kk, 32-dim slice q32)
-    // of K and (8-key block vb, 4 physical dim slots from 4 vj) of V. Lanes
-    // 4i..4i+3 take 4 keys of one slice so a 16-lane phase writes 4 keys x 4
-    // slices (distinct bank groups under kaddr).
+    // of K and (8-key block vb, 4 physical dim slots from 4 vj) of V. A
+    // quarter-wave takes 16 consecutive keys of one K slice, the quarter-waves
+    // of a wave 4 consecutive slices of the same keys (the LDS writes then hit
+    // aligned, distinct bank groups under kaddr; each key row is read as
+    // 4-slice runs).
     struct Stage {
         u32x4 kc[PER][KU];
         uint32_t kp[PER];
@@ -224,8 +232,8 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
 #pragma unroll
     for (int j = 0; j < PER; j++) {
         const int tt = tid + 64 * NW * j;
-        q32[j] = (tt >> 2) & (TPR - 1);
-        kk[j] = (tt & 3) | ((tt >> (2 + LTPR)) << 2);
+        q32[j] = (tt >> 4) & (TPR - 1);
+        kk[j] = (tt & 15) | ((tt >> (4 + LTPR)) << 4);
         vb[j] = tt / TPB;
         vj[j] = tt % TPB;
         vgrp[j] = v_logical_dim(4 * vj[j], D, BITS) / 64;
@@ -258,23 +266,24 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         half8* const sV8 = (half8*)(lds + BUF * b + KBUF);
 #pragma unroll
         for (int j = 0; j < PER; j++) {
-            half8* krow = sK8 + kaddr(kk[j], 4 * q32[j], KROW);
+            // chunks 4 q32 + w of key kk: KT chunks apart
+            half8* krow = sK8 + kaddr<KT>(kk[j], 4 * q32[j]);
             if constexpr (BITS == 4) {
                 const half2v sb = h2(st.kp[j]);
                 const half2v s = {sb.x, sb.x}, bb = {sb.y, sb.y};
                 const PairConsts pc = make_consts<FAST, 4>(s, s, s, s, bb, bb, bb, bb);
 #pragma unroll
-                for (int w = 0; w < 4; w++) krow[w] = deq4<FAST>(st.kc[j][0][w], pc, magic);
+                for (int w = 0; w < 4; w++) krow[w * KT] = deq4<FAST>(st.kc[j][0][w], pc, magic);
             } else if constexpr (BITS == 8) {
                 const half2v sb = h2(st.kp[j]);
                 const half2v s = {sb.x, sb.x}, bb = {sb.y, sb.y};
                 const PairConsts pc = make_consts<FAST, 8>(s, s, s, s, bb, bb, bb, bb, a.code_off2);
 #pragma unroll
                 for (int w = 0; w < 4; w++)
-                    krow[w] = deq8<FAST>(st.kc[j][w / 2][2 * (w % 2)], st.kc[j][w / 2][2 * (w % 2) + 1], pc);
+                    krow[w * KT] = deq8<FAST>(st.kc[j][w / 2][2 * (w % 2)], st.kc[j][w / 2][2 * (w % 2) + 1], pc);
             } else {
 #pragma unroll
-                for (int w = 0; w < 4; w++) krow[w] = as_h8(st.kc[j][w]);
+                for (int w = 0; w < 4; w++) krow[w * KT] = as_h8(st.kc[j][w]);
             }
             PairConsts vc;
             if constexpr (AFF)
@@ -317,7 +326,10 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         // 4tt + (r16&3), so lane (g, r16) ends up with keys 32u + 8g + 4tt + i
         // of column r16.
         const int key0 = 8 * (r16 >> 2) + (r16 & 3);
-        const half8* kbase = sK8 + kaddr(key0, g, KROW);
+        // kswz(key0 + 4tt) = key0 + 4 (tt ^ bit 4 of key0): one base a tile tt
+        const int b4 = (key0 >> 4) & 1;
+        const half8* kbase0 = sK8 + g * KT + key0 + 4 * b4;
+        const half8* kbase1 = sK8 + g * KT + key0 + 4 * (b4 ^ 1);
         float4v acc[NSUB][2][RT];
 #pragma unroll
         for (int u = 0; u < NSUB; u++)
@@ -329,9 +341,8 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         for (int m = 0; m < NM; m++) {
 #pragma unroll
             for (int u = 0; u < NSUB; u++) {
-                // key0 + 32u (+4) keeps key0's 16-key band offset: +2u bands
-                const half8* k0 = kbase + 32 * u * KROW + 8 * u;
-                const half8 ka = k0[4 * m], kb2 = k0[4 * KROW + 4 * m];
+                // chunk g + 4m of keys key0 + 32u (+4): kswz leaves bits >= 5 alone
+                const half8 ka = kbase0[4 * m * KT + 32 * u], kb2 = kbase1[4 * m * KT + 32 * u];
 #pragma unroll
                 for (int rt = 0; rt < RT; rt++) {
                     acc[u][0][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[rt][m], acc[u][0][rt], 0, 0, 0);
