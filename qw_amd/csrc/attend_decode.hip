@@ -520,10 +520,12 @@ template <int PER>
 __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restrict__ part_o,
                                                            const float2* __restrict__ part_ml,
                                                            int nc, int rstride, int row0, int D,
-                                                           int G, int Tq, f16* __restrict__ out) {
+                                                           int G, int Tq, int slot_bits,
+                                                           f16* __restrict__ out) {
     const int row = blockIdx.x, h = blockIdx.y, d = blockIdx.z * 64 + (threadIdx.x & 63);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t base = (int64_t)h * nc * rstride + row;
+    const int sd = slot_bits ? v_phys_dim(d, D, slot_bits) : d;  // d's place in a partial row
     // One memory round: every (m, l) and O value this lane needs is loaded
     // first; the max is then exchanged through LDS.
     float v[PER];
@@ -533,7 +535,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
         const int c = wave + 4 * i;
         if (c < nc) {
             ml[i] = part_ml[base + (int64_t)c * rstride];
-            v[i] = part_o[(base + (int64_t)c * rstride) * D + d];
+            v[i] = part_o[(base + (int64_t)c * rstride) * D + sd];
         } else {
             ml[i] = float2{-INFINITY, 0.0f};
             v[i] = 0.0f;
@@ -637,20 +639,21 @@ template <int MAXN>
 __global__ __launch_bounds__(256) void merge_rows_kernel(const float* __restrict__ part_o,
                                                          const float2* __restrict__ part_ml,
                                                          int nc, int rstride, int row0, int R,
-                                                         int D, int G, int Tq,
+                                                         int D, int G, int Tq, int slot_bits,
                                                          f16* __restrict__ out) {
     const int h = blockIdx.y;
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int row = (int)(idx / D), d = (int)(idx % D);
     if (row >= R) return;
     const int64_t base = (int64_t)h * nc * rstride + row;
+    const int sd = slot_bits ? v_phys_dim(d, D, slot_bits) : d;  // d's place in a partial row
     float v[MAXN];
     float2 ml[MAXN];
 #pragma unroll
     for (int c = 0; c < MAXN; c++) {
         if (c < nc) {
             ml[c] = part_ml[base + (int64_t)c * rstride];
-            v[c] = part_o[(base + (int64_t)c * rstride) * D + d];
+            v[c] = part_o[(base + (int64_t)c * rstride) * D + sd];
         } else {
             ml[c] = float2{-INFINITY, 0.0f};
             v[c] = 0.0f;
@@ -672,7 +675,8 @@ __global__ __launch_bounds__(256) void merge_rows_kernel(const float* __restrict
 }
 
 int launch_partial_merge(const float* part_o, const float2* part_ml, int nc, int rstride, int row0,
-                         int R, int hkv, int D, int G, int Tq, f16* out, hipStream_t stream) {
+                         int R, int hkv, int D, int G, int Tq, f16* out, hipStream_t stream,
+                         int slot_bits) {
     QW_REQUIRE(nc >= 1 && nc <= 4 * kMergeMaxPer, QW_ERR_INVALID_ARGUMENT,
                "merge: partial count out of range");
     if (R > 16 && nc <= 64) {
@@ -680,10 +684,10 @@ int launch_partial_merge(const float* part_o, const float2* part_ml, int nc, int
         const dim3 grid((unsigned)((n + 255) / 256), hkv);
         if (nc <= 8)
             hipLaunchKernelGGL(merge_rows_kernel<8>, grid, dim3(256), 0, stream, part_o, part_ml, nc,
-                               rstride, row0, R, D, G, Tq, out);
+                               rstride, row0, R, D, G, Tq, slot_bits, out);
         else
             hipLaunchKernelGGL(merge_rows_kernel<64>, grid, dim3(256), 0, stream, part_o, part_ml,
-                               nc, rstride, row0, R, D, G, Tq, out);
+                               nc, rstride, row0, R, D, G, Tq, slot_bits, out);
         QW_HIP_CHECK(hipGetLastError());
         return QW_OK;
     }
@@ -691,23 +695,23 @@ int launch_partial_merge(const float* part_o, const float2* part_ml, int nc, int
     switch (merge_per(nc)) {
         case 4:
             hipLaunchKernelGGL(decode_merge_kernel<4>, grid, dim3(256), 0, stream, part_o, part_ml,
-                               nc, rstride, row0, D, G, Tq, out);
+                               nc, rstride, row0, D, G, Tq, slot_bits, out);
             break;
         case 8:
             hipLaunchKernelGGL(decode_merge_kernel<8>, grid, dim3(256), 0, stream, part_o, part_ml,
-                               nc, rstride, row0, D, G, Tq, out);
+                               nc, rstride, row0, D, G, Tq, slot_bits, out);
             break;
         case 16:
             hipLaunchKernelGGL(decode_merge_kernel<16>, grid, dim3(256), 0, stream, part_o, part_ml,
-                               nc, rstride, row0, D, G, Tq, out);
+                               nc, rstride, row0, D, G, Tq, slot_bits, out);
             break;
         case 32:
             hipLaunchKernelGGL(decode_merge_kernel<32>, grid, dim3(256), 0, stream, part_o, part_ml,
-                               nc, rstride, row0, D, G, Tq, out);
+                               nc, rstride, row0, D, G, Tq, slot_bits, out);
             break;
         default:
             hipLaunchKernelGGL(decode_merge_kernel<kMergeMaxPer>, grid, dim3(256), 0, stream, part_o,
-                               part_ml, nc, rstride, row0, D, G, Tq, out);
+                               part_ml, nc, rstride, row0, D, G, Tq, slot_bits, out);
     }
     QW_HIP_CHECK(hipGetLastError());
     return QW_OK;
