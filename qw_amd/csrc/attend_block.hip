@@ -121,13 +121,6 @@ __device__ __forceinline__ int kaddr(int key, int chunk) {
     return chunk * KT + kswz(key);
 }
 
-// Logical dim of physical slot `slot` of a V block (inverse of v_phys_dim).
-__device__ __forceinline__ int v_logical_dim(int slot, int D, int bits) {
-    const int dpl = D / 16;
-    const int e = bits == 4 ? 4 : (bits == 8 ? 2 : 1);
-    const int i = slot % e, n = (slot / e) % 16, j = slot / (16 * e);
-    return n * dpl + e * j + i;
-}
 
 // max / sum of v over the lane pair (l, l ^ 16), then over (l, l ^ 32): row
 // swaps in the VALU (v_permlane16/32_swap) instead of LDS permutes.

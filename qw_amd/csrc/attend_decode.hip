@@ -522,10 +522,12 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
                                                            int nc, int rstride, int row0, int D,
                                                            int G, int Tq, int slot_bits,
                                                            f16* __restrict__ out) {
-    const int row = blockIdx.x, h = blockIdx.y, d = blockIdx.z * 64 + (threadIdx.x & 63);
+    // lane = place sd in the partial rows (contiguous loads); it holds dim d
+    // (partial rows in slot order: the dim whose slot sd is)
+    const int row = blockIdx.x, h = blockIdx.y, sd = blockIdx.z * 64 + (threadIdx.x & 63);
+    const int d = slot_bits ? v_logical_dim(sd, D, slot_bits) : sd;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t base = (int64_t)h * nc * rstride + row;
-    const int sd = slot_bits ? v_phys_dim(d, D, slot_bits) : d;  // d's place in a partial row
     // One memory round: every (m, l) and O value this lane needs is loaded
     // first; the max is then exchanged through LDS.
     float v[PER];
@@ -643,10 +645,11 @@ __global__ __launch_bounds__(256) void merge_rows_kernel(const float* __restrict
                                                          f16* __restrict__ out) {
     const int h = blockIdx.y;
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int row = (int)(idx / D), d = (int)(idx % D);
+    // thread = place sd in a partial row (contiguous loads), holding dim d
+    const int row = (int)(idx / D), sd = (int)(idx % D);
     if (row >= R) return;
+    const int d = slot_bits ? v_logical_dim(sd, D, slot_bits) : sd;
     const int64_t base = (int64_t)h * nc * rstride + row;
-    const int sd = slot_bits ? v_phys_dim(d, D, slot_bits) : d;  // d's place in a partial row
     float v[MAXN];
     float2 ml[MAXN];
 #pragma unroll

@@ -74,6 +74,14 @@ __host__ __device__ inline int v_phys_dim(int d, int D, int bits) {
     return 16 * e * (r / e) + e * n + (r % e);
 }
 
+// Logical dim of physical slot `slot` of a V block (inverse of v_phys_dim).
+__host__ __device__ inline int v_logical_dim(int slot, int D, int bits) {
+    const int dpl = D / 16;
+    const int e = bits == 4 ? 4 : (bits == 8 ? 2 : 1);
+    const int i = slot % e, n = (slot / e) % 16, j = slot / (16 * e);
+    return n * dpl + e * j + i;
+}
+
 // v_phys_dim(64 pp + 4 n + c, D, bits) split into a part that depends only
 // on n (0..15, an MFMA column) and one that depends only on (pp, c), so that a
 // lane's 4 * D/64 slots are one base plus immediates (same values, by algebra:
