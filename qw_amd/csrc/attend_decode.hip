@@ -521,7 +521,8 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
                                                            const float2* __restrict__ part_ml,
                                                            int nc, int rstride, int row0, int D,
                                                            int G, int Tq, int slot_bits,
-                                                           f16* __restrict__ out) {
+                                                           f16* __restrict__ out,
+                                                           float* __restrict__ out32) {
     // lane = place sd in the partial rows (contiguous loads); it holds dim d
     // (partial rows in slot order: the dim whose slot sd is)
     const int row = blockIdx.x, h = blockIdx.y, sd = blockIdx.z * 64 + (threadIdx.x & 63);
@@ -567,7 +568,11 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
         const float L = (sm[1][0][lane] + sm[1][1][lane]) + (sm[1][2][lane] + sm[1][3][lane]);
         const int orow = row0 + row;  // row index r * G + head-in-group
         const int qh = h * G + orow % G, qr = orow / G;
-        out[((int64_t)qh * Tq + qr) * D + d] = (f16)(L > 0.0f ? O / L : 0.0f);
+        const float y = L > 0.0f ? O / L : 0.0f;
+        if (out32)
+            out32[((int64_t)qh * Tq + qr) * D + d] = y;
+        else
+            out[((int64_t)qh * Tq + qr) * D + d] = (f16)y;
     }
 }
 
@@ -642,7 +647,8 @@ __global__ __launch_bounds__(256) void merge_rows_kernel(const float* __restrict
                                                          const float2* __restrict__ part_ml,
                                                          int nc, int rstride, int row0, int R,
                                                          int D, int G, int Tq, int slot_bits,
-                                                         f16* __restrict__ out) {
+                                                         f16* __restrict__ out,
+                                                         float* __restrict__ out32) {
     const int h = blockIdx.y;
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
     // thread = place sd in a partial row (contiguous loads), holding dim d
@@ -674,12 +680,16 @@ __global__ __launch_bounds__(256) void merge_rows_kernel(const float* __restrict
     }
     const int orow = row0 + row;
     const int qh = h * G + orow % G, qr = orow / G;
-    out[((int64_t)qh * Tq + qr) * D + d] = (f16)(L > 0.0f ? acc / L : 0.0f);
+    const float y = L > 0.0f ? acc / L : 0.0f;
+    if (out32)
+        out32[((int64_t)qh * Tq + qr) * D + d] = y;
+    else
+        out[((int64_t)qh * Tq + qr) * D + d] = (f16)y;
 }
 
 int launch_partial_merge(const float* part_o, const float2* part_ml, int nc, int rstride, int row0,
                          int R, int hkv, int D, int G, int Tq, f16* out, hipStream_t stream,
-                         int slot_bits) {
+                         int slot_bits, float* out32) {
     QW_REQUIRE(nc >= 1 && nc <= 4 * kMergeMaxPer, QW_ERR_INVALID_ARGUMENT,
                "merge: partial count out of range");
     if (R > 16 && nc <= 64) {
@@ -687,10 +697,10 @@ int launch_partial_merge(const float* part_o, const float2* part_ml, int nc, int
         const dim3 grid((unsigned)((n + 255) / 256), hkv);
         if (nc <= 8)
             hipLaunchKernelGGL(merge_rows_kernel<8>, grid, dim3(256), 0, stream, part_o, part_ml, nc,
-                               rstride, row0, R, D, G, Tq, slot_bits, out);
+                               rstride, row0, R, D, G, Tq, slot_bits, out, out32);
         else
             hipLaunchKernelGGL(merge_rows_kernel<64>, grid, dim3(256), 0, stream, part_o, part_ml,
-                               nc, rstride, row0, R, D, G, Tq, slot_bits, out);
+                               nc, rstride, row0, R, D, G, Tq, slot_bits, out, out32);
         QW_HIP_CHECK(hipGetLastError());
         return QW_OK;
     }
@@ -698,23 +708,23 @@ int launch_partial_merge(const float* part_o, const float2* part_ml, int nc, int
     switch (merge_per(nc)) {
         case 4:
             hipLaunchKernelGGL(decode_merge_kernel<4>, grid, dim3(256), 0, stream, part_o, part_ml,
-                               nc, rstride, row0, D, G, Tq, slot_bits, out);
+                               nc, rstride, row0, D, G, Tq, slot_bits, out, out32);
             break;
         case 8:
             hipLaunchKernelGGL(decode_merge_kernel<8>, grid, dim3(256), 0, stream, part_o, part_ml,
-                               nc, rstride, row0, D, G, Tq, slot_bits, out);
+                               nc, rstride, row0, D, G, Tq, slot_bits, out, out32);
             break;
         case 16:
             hipLaunchKernelGGL(decode_merge_kernel<16>, grid, dim3(256), 0, stream, part_o, part_ml,
-                               nc, rstride, row0, D, G, Tq, slot_bits, out);
+                               nc, rstride, row0, D, G, Tq, slot_bits, out, out32);
             break;
         case 32:
             hipLaunchKernelGGL(decode_merge_kernel<32>, grid, dim3(256), 0, stream, part_o, part_ml,
-                               nc, rstride, row0, D, G, Tq, slot_bits, out);
+                               nc, rstride, row0, D, G, Tq, slot_bits, out, out32);
             break;
         default:
             hipLaunchKernelGGL(decode_merge_kernel<kMergeMaxPer>, grid, dim3(256), 0, stream, part_o,
-                               part_ml, nc, rstride, row0, D, G, Tq, slot_bits, out);
+                               part_ml, nc, rstride, row0, D, G, Tq, slot_bits, out, out32);
     }
     QW_HIP_CHECK(hipGetLastError());
     return QW_OK;

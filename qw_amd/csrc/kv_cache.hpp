@@ -172,10 +172,11 @@ int launch_block_attention(KVCache& c, const f16* q, int G, int n_rows, float sc
 // Split-K merge: out[row0 + row] = sum_c e^(m_c - M) O_c / sum_c e^(m_c - M) l_c
 // over nc partials of [rstride][D] fp32 rows per KV head, rows 0 .. R-1.
 // slot_bits == 0: partial rows in dim order; 4/8/16: in the V plane's slot
-// order of that layout (dim d at v_phys_dim(d, D, slot_bits)).
+// order of that layout (dim d at v_phys_dim(d, D, slot_bits)). out32 != null:
+// the merged rows are written there in fp32 (same indexing) instead of to out.
 int launch_partial_merge(const float* part_o, const float2* part_ml, int nc, int rstride, int row0,
                          int R, int hkv, int D, int G, int Tq, f16* out, hipStream_t stream,
-                         int slot_bits = 0);
+                         int slot_bits = 0, float* out32 = nullptr);
 
 
 // D-LSA K1 select (dlsa_select.hip).

@@ -311,16 +311,17 @@ __global__ __launch_bounds__(D) void turbo4_expand_kernel(
 
 // ------------------------------------------------------------ rotation
 //
-// rows of D fp16: out = f16(s_out . (H / sqrt(D)) . s_in . in), one wave a row.
-template <int D>
-__global__ __launch_bounds__(256) void turbo4_rotate_kernel(const f16* __restrict__ in,
+// rows of D fp16 or fp32: out = f16(s_out . (H / sqrt(D)) . s_in . in) in
+// fp32, one wave a row.
+template <int D, typename TIn = f16>
+__global__ __launch_bounds__(256) void turbo4_rotate_kernel(const TIn* __restrict__ in,
                                                             f16* __restrict__ out, int rows,
                                                             const float* __restrict__ s_in,
                                                             const float* __restrict__ s_out) {
     constexpr int VPL = D / 64;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= rows) return;  // whole waves leave together
-    const f16* r = in + (int64_t)row * D;
+    const TIn* r = in + (int64_t)row * D;
     float y[VPL];
 #pragma unroll
     for (int j = 0; j < VPL; j++) y[j] = (float)r[lane * VPL + j] * s_in[lane * VPL + j];
@@ -811,8 +812,9 @@ static int turbo4_verify(KVCache& c, const void* q, int n_q_heads, int n_rows, f
     const int kps = ((T + want - 1) / want + kT4vKeys - 1) / kT4vKeys * kT4vKeys;
     const int nc = (T + kps - 1) / kps;
     const size_t q_bytes = (size_t)qrows * D * sizeof(f16);
+    const size_t o_bytes = (size_t)qrows * D * sizeof(float);  // merged rows, fp32
     const size_t po_bytes = (size_t)c.hkv * nc * kT4vRows * D * sizeof(float);
-    const size_t need = 2 * q_bytes + po_bytes + (size_t)c.hkv * nc * kT4vRows * sizeof(float2);
+    const size_t need = q_bytes + o_bytes + po_bytes + (size_t)c.hkv * nc * kT4vRows * sizeof(float2);
 
     T4Workspace& w = g_ws[c.device];
     std::lock_guard<std::mutex> lock(w.m);
@@ -835,10 +837,13 @@ static int turbo4_verify(KVCache& c, const void* q, int n_q_heads, int n_rows, f
     } else {
         QW_HIP_CHECK(hipStreamWaitEvent(stream, w.last, 0));
     }
+    // The merge leaves the rotated output in fp32 and the rotation back casts
+    // it to fp16 once, as the reference's merge (fp32, turbo4_attention.cpp:
+    // 438-446) and turbo4_v_inverse_rotate (quant.rs:764-768) do.
     f16* q_s = (f16*)w.buf;
-    f16* o_rot = (f16*)((char*)w.buf + q_bytes);
-    float* part_o = (float*)((char*)w.buf + 2 * q_bytes);
-    float2* part_ml = (float2*)((char*)w.buf + 2 * q_bytes + po_bytes);
+    float* o_rot = (float*)((char*)w.buf + q_bytes);
+    float* part_o = (float*)((char*)w.buf + q_bytes + o_bytes);
+    float2* part_ml = (float2*)((char*)w.buf + q_bytes + o_bytes + po_bytes);
     const float* tab = c.t4_tables;
     const float post = scale * 1.4426950408889634f;  // fp32, as the reference forms it
 
@@ -878,17 +883,17 @@ static int turbo4_verify(KVCache& c, const void* q, int n_q_heads, int n_rows, f
         hipLaunchKernelGGL(turbo4_verify_kernel<128>, vg, dim3(kT4vThreads), sh, stream, a);
     }
     QW_HIP_CHECK(hipGetLastError());
-    int rc = launch_partial_merge(part_o, part_ml, nc, kT4vRows, 0, R, c.hkv, D, G, n_rows, o_rot,
-                                  stream);
+    int rc = launch_partial_merge(part_o, part_ml, nc, kT4vRows, 0, R, c.hkv, D, G, n_rows, nullptr,
+                                  stream, 0, o_rot);
     if (rc) return rc;
     if (D == 256) {
         using TT = T4Tab<256>;
-        hipLaunchKernelGGL(turbo4_rotate_kernel<256>, rg, dim3(256), 0, stream, o_rot, (f16*)out,
-                           qrows, tab + TT::v_s2, tab + TT::v_s1);
+        hipLaunchKernelGGL((turbo4_rotate_kernel<256, float>), rg, dim3(256), 0, stream,
+                           (const float*)o_rot, (f16*)out, qrows, tab + TT::v_s2, tab + TT::v_s1);
     } else {
         using TT = T4Tab<128>;
-        hipLaunchKernelGGL(turbo4_rotate_kernel<128>, rg, dim3(256), 0, stream, o_rot, (f16*)out,
-                           qrows, tab + TT::v_s2, tab + TT::v_s1);
+        hipLaunchKernelGGL((turbo4_rotate_kernel<128, float>), rg, dim3(256), 0, stream,
+                           (const float*)o_rot, (f16*)out, qrows, tab + TT::v_s2, tab + TT::v_s1);
     }
     QW_HIP_CHECK(hipGetLastError());
     QW_HIP_CHECK(hipEventRecord(w.last, stream));
