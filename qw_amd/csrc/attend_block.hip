@@ -550,9 +550,14 @@ __global__ __launch_bounds__(64 * kBlockWaves, 1) void attend_block_kernel(Block
     // a launch whose cache holds a scale outside its exact range redoes the
     // workgroup's share with the separately rounded dequant (same threads,
     // same output elements, so the second pass's writes replace the first's).
-    block_body<BITS, D, RT, true>(a, lds_buf);
-    if (BITS != 16 && *a.fast_flag == 0) {
-        __syncthreads();
+    // A null flag (Int8 caches) takes the separately rounded dequant directly.
+    if (BITS == 16 || a.fast_flag != nullptr) {
+        block_body<BITS, D, RT, true>(a, lds_buf);
+        if (BITS != 16 && *a.fast_flag == 0) {
+            __syncthreads();
+            block_body<BITS, D, RT, false>(a, lds_buf);
+        }
+    } else {
         block_body<BITS, D, RT, false>(a, lds_buf);
     }
 }
@@ -634,7 +639,7 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     a.k_params = cc.k_params;
     a.v_data = (const uint32_t*)cc.v_data;
     a.v_params = cc.v_params;
-    a.fast_flag = cc.fast_flag;
+    a.fast_flag = cc.int8() ? nullptr : cc.fast_flag;  // null: always separately rounded
     a.q = q;
     a.out = out;
     a.part_o = nullptr;

@@ -493,10 +493,16 @@ __global__ __launch_bounds__((64 * decode_waves<BITS, D>()), 1) void attend_deco
     // flag (a memory round trip ahead of every load). In the rare launch whose
     // cache holds a scale outside that dequant's exact range, the workgroup
     // then redoes its share with the separately rounded dequant, and that
-    // pass's partial (same threads, same elements) replaces the first.
-    decode_body<BITS, D, NW, true>(a, sm_ml, sm_o, sm_q);
-    if (BITS != 16 && *a.fast_flag == 0) {
-        __syncthreads();
+    // pass's partial (same threads, same elements) replaces the first. A
+    // null flag (Int8 caches, which always take the separately rounded
+    // dequant) goes to that path directly.
+    if (BITS == 16 || a.fast_flag != nullptr) {
+        decode_body<BITS, D, NW, true>(a, sm_ml, sm_o, sm_q);
+        if (BITS != 16 && *a.fast_flag == 0) {
+            __syncthreads();
+            decode_body<BITS, D, NW, false>(a, sm_ml, sm_o, sm_q);
+        }
+    } else {
         decode_body<BITS, D, NW, false>(a, sm_ml, sm_o, sm_q);
     }
 }
@@ -600,7 +606,7 @@ static int launch_decode_partials(KVCache& cc, const f16* q, int G, int Tq, int 
     a.k_params = cc.k_params;
     a.v_data = (const uint32_t*)cc.v_data;
     a.v_params = cc.v_params;
-    a.fast_flag = cc.fast_flag;
+    a.fast_flag = cc.int8() ? nullptr : cc.fast_flag;  // null: always separately rounded
     a.q = q;
     a.part_o = (float*)cc.ws_ptr;
     a.part_ml = (float2*)((char*)cc.ws_ptr + (size_t)cc.hkv * nc * 16 * D * sizeof(float));

@@ -539,16 +539,23 @@ __device__ __forceinline__ void dlsa_body(const DlsaArgs& a, const Src& src) {
 // fast_flag), else the separately rounded one.
 template <int D, int GMAX, class Src>
 __global__ __launch_bounds__(256, 2) void dlsa_kernel(DlsaArgs a, Src src, const int* fast_flag) {
-    dlsa_body<D, GMAX, Src, true>(a, src);
     if constexpr (Src::kAffine) {
-        // The exact 2-op dequant ran without waiting for the cache's fast
+        // The exact 2-op dequant runs without waiting for the cache's fast
         // flag; a cache holding a scale outside its exact range takes the
         // separately rounded one in a second pass whose writes (same threads,
-        // same elements) replace the first's.
-        if (*fast_flag == 0) {
-            __syncthreads();
+        // same elements) replace the first's. A null flag (Int8 caches) takes
+        // the separately rounded dequant directly.
+        if (fast_flag != nullptr) {
+            dlsa_body<D, GMAX, Src, true>(a, src);
+            if (*fast_flag == 0) {
+                __syncthreads();
+                dlsa_body<D, GMAX, Src, false>(a, src);
+            }
+        } else {
             dlsa_body<D, GMAX, Src, false>(a, src);
         }
+    } else {
+        dlsa_body<D, GMAX, Src, true>(a, src);
     }
 }
 
@@ -663,12 +670,12 @@ static void launch_dlsa_source(const DlsaSource& s, const DlsaArgs& a, dim3 grid
             const SrcCacheAffine<D, 4> src{(const uint32_t*)c.k_data, c.k_params,
                                            (const uint32_t*)c.v_data, (const f16*)c.v_params,
                                            c.cap, c.code_offset2()};
-            launch_dlsa_kernel<D, GM>(src, a, grid, c.fast_flag, stream);
+            launch_dlsa_kernel<D, GM>(src, a, grid, c.int8() ? nullptr : c.fast_flag, stream);
         } else {
             const SrcCacheAffine<D, 8> src{(const uint32_t*)c.k_data, c.k_params,
                                            (const uint32_t*)c.v_data, (const f16*)c.v_params,
                                            c.cap, c.code_offset2()};
-            launch_dlsa_kernel<D, GM>(src, a, grid, c.fast_flag, stream);
+            launch_dlsa_kernel<D, GM>(src, a, grid, c.int8() ? nullptr : c.fast_flag, stream);
         }
     }
 }
