@@ -269,32 +269,34 @@ def bench_decode(torch, qw_amd, steps: int, warmup: int, reps: int, bits: int = 
             "bytes_layer": bytes_layer, "bytes_attn": bytes_attn}
 
 
-def bench_turbo4_verify(torch, qw_amd, steps: int, warmup: int, T_prefix: int = 32768,
-                        L: int = 4):
+def bench_turbo4_verify(torch, qw_amd, steps: int, warmup: int, reps: int,
+                        T_prefix: int = 32768, L: int = 4):
     """A Turbo4 causal verify block (L draft rows, the reference's fused-pass
     case) at the config-2 geometry: update_and_causal_attention of L tokens,
     routed to the fused verify kernel (scored straight from the packed codes).
-    Timed eagerly, like the decode route."""
+    Graph-replayed like the affine paths; the eager figure beside it."""
     ls = LayerSet(torch, qw_amd, 4, 4, T_prefix, L, LAYERS, causal=True, mode="turbo4")
     ls.warm(warmup)
-    ms = ls.time_eager(steps)
+    eager_ms = ls.time_eager(steps)
+    layer = ls.time_layers(steps, reps)
     T = ls.T
     ls.close()
-    return {"T": T, "L": L, "layer_ms": ms}
+    return {"T": T, "L": L, "layer_ms": layer["median"], "eager_layer_ms": eager_ms}
 
 
-def bench_turbo4_decode(torch, qw_amd, steps: int, warmup: int, T_prefix: int = 32768):
+def bench_turbo4_decode(torch, qw_amd, steps: int, warmup: int, reps: int,
+                        T_prefix: int = 32768):
     """The reference's served default KV mode at the config-2 geometry:
     update_and_attention of one token on a Turbo4 cache (rotate q, expand the
     rotated K/V to fp16, the fp16 decode kernels, rotate the output back).
-    Timed eagerly: the route's shared workspace orders its users with an
-    event, which a HIP graph capture does not take."""
+    Graph-replayed like the affine paths; the eager figure beside it."""
     ls = LayerSet(torch, qw_amd, 3, 4, T_prefix, 1, LAYERS, causal=False, mode="turbo4")
     ls.warm(warmup)
-    ms = ls.time_eager(steps)
+    eager_ms = ls.time_eager(steps)
+    layer = ls.time_layers(steps, reps)
     T = ls.T
     ls.close()
-    return {"T": T, "layer_ms": ms}
+    return {"T": T, "layer_ms": layer["median"], "eager_layer_ms": eager_ms}
 
 
 def bench_select(torch, qw_amd, reps: int, T: int = 131072):
@@ -929,14 +931,16 @@ def main() -> int:
             "GB_s_chunk": round(rp["chunk_bytes"] / (rp["chunk_ms"] * 1e-3) / 1e9, 1),
             "us_rope_append_1_token": round(rp["token_ms"] * 1e3, 2)}
         log("bench: Turbo4 decode (config-2 geometry)")
-        t4 = bench_turbo4_decode(torch, qw_amd, 4 * LAYERS, args.warmup)
+        t4 = bench_turbo4_decode(torch, qw_amd, LAYERS, args.warmup, reps)
         extra["turbo4_decode"] = {
-            "us_per_layer_eager": round(t4["layer_ms"] * 1e3, 2), "keys": t4["T"],
+            "us_per_layer": round(t4["layer_ms"] * 1e3, 2),
+            "us_per_layer_eager": round(t4["eager_layer_ms"] * 1e3, 2), "keys": t4["T"],
             "route": "rotate q, expand rotated K/V to fp16, fp16 decode, rotate back"}
         log("bench: Turbo4 fused causal verify (4 rows, config-2 geometry)")
-        tv = bench_turbo4_verify(torch, qw_amd, 4 * LAYERS, args.warmup)
+        tv = bench_turbo4_verify(torch, qw_amd, LAYERS, args.warmup, reps)
         extra["turbo4_verify"] = {
-            "us_per_layer_eager": round(tv["layer_ms"] * 1e3, 2), "keys": tv["T"], "rows": tv["L"],
+            "us_per_layer": round(tv["layer_ms"] * 1e3, 2),
+            "us_per_layer_eager": round(tv["eager_layer_ms"] * 1e3, 2), "keys": tv["T"], "rows": tv["L"],
             "route": "rotate q, fused verify kernel on the packed codes, merge, rotate back"}
         line["extra"] = extra
     if not args.no_cpu:

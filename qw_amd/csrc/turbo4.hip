@@ -25,6 +25,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <map>
 #include <mutex>
 #include <string>
 
@@ -687,17 +688,19 @@ static unsigned grid_for(int64_t work) {
     return (unsigned)std::max<int64_t>(1, std::min<int64_t>((work + 255) / 256, 4096));
 }
 
-// Per-device workspace of the attention route: the rotated fp16 K/V, q and
-// output. Shared by the Turbo4 caches of a device (as MLX's allocator shares
-// its transient buffers); an event orders its users across streams.
-struct T4Workspace {
-    std::mutex m;
-    void* buf = nullptr;
-    size_t bytes = 0;
-    hipEvent_t last = nullptr;
-};
-constexpr int kMaxDevices = 64;
-T4Workspace g_ws[kMaxDevices];
+// Workspace of the attention routes (the rotated fp16 K/V, q, the fp32
+// merged rows and split partials), one per (device, stream), shared by the
+// Turbo4 caches that attend on that stream as MLX's allocator shares its
+// transient buffers: calls on one stream are ordered by the stream, calls on
+// different streams never share it. A GrowBuffer, so a call captured in a HIP
+// graph keeps its buffer when a later call grows the workspace.
+std::mutex g_t4_mu;
+std::map<std::pair<int, hipStream_t>, GrowBuffer> g_t4_ws;
+
+int t4_workspace(int device, hipStream_t stream, size_t need, void** out) {
+    std::lock_guard<std::mutex> lock(g_t4_mu);
+    return g_t4_ws[{device, stream}].get(need, stream, out);
+}
 
 }  // namespace
 
@@ -816,34 +819,15 @@ static int turbo4_verify(KVCache& c, const void* q, int n_q_heads, int n_rows, f
     const size_t po_bytes = (size_t)c.hkv * nc * kT4vRows * D * sizeof(float);
     const size_t need = q_bytes + o_bytes + po_bytes + (size_t)c.hkv * nc * kT4vRows * sizeof(float2);
 
-    T4Workspace& w = g_ws[c.device];
-    std::lock_guard<std::mutex> lock(w.m);
-    if (!w.last) QW_HIP_CHECK(hipEventCreateWithFlags(&w.last, hipEventDisableTiming));
-    if (need > w.bytes) {
-        if (w.buf) {
-            QW_HIP_CHECK(hipDeviceSynchronize());
-            (void)hipFree(w.buf);
-            w.buf = nullptr;
-            w.bytes = 0;
-        }
-        const size_t nb = need + need / 4;
-        if (hipMalloc(&w.buf, nb) != hipSuccess) {
-            (void)hipGetLastError();
-            w.buf = nullptr;
-            set_error("turbo4 attention: workspace hipMalloc failed");
-            return QW_ERR_OUT_OF_MEMORY;
-        }
-        w.bytes = nb;
-    } else {
-        QW_HIP_CHECK(hipStreamWaitEvent(stream, w.last, 0));
-    }
+    void* wbuf = nullptr;
+    if (int rc0 = t4_workspace(c.device, stream, need, &wbuf)) return rc0;
     // The merge leaves the rotated output in fp32 and the rotation back casts
     // it to fp16 once, as the reference's merge (fp32, turbo4_attention.cpp:
     // 438-446) and turbo4_v_inverse_rotate (quant.rs:764-768) do.
-    f16* q_s = (f16*)w.buf;
-    float* o_rot = (float*)((char*)w.buf + q_bytes);
-    float* part_o = (float*)((char*)w.buf + q_bytes + o_bytes);
-    float2* part_ml = (float2*)((char*)w.buf + q_bytes + o_bytes + po_bytes);
+    f16* q_s = (f16*)wbuf;
+    float* o_rot = (float*)((char*)wbuf + q_bytes);
+    float* part_o = (float*)((char*)wbuf + q_bytes + o_bytes);
+    float2* part_ml = (float2*)((char*)wbuf + q_bytes + o_bytes + po_bytes);
     const float* tab = c.t4_tables;
     const float post = scale * 1.4426950408889634f;  // fp32, as the reference forms it
 
@@ -896,7 +880,6 @@ static int turbo4_verify(KVCache& c, const void* q, int n_q_heads, int n_rows, f
                            (const float*)o_rot, (f16*)out, qrows, tab + TT::v_s2, tab + TT::v_s1);
     }
     QW_HIP_CHECK(hipGetLastError());
-    QW_HIP_CHECK(hipEventRecord(w.last, stream));
     return QW_OK;
 }
 
@@ -908,8 +891,6 @@ int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float
     QW_REQUIRE(n_rows > 0, QW_ERR_INVALID_ARGUMENT, "attention: n_rows must be > 0");
     QW_REQUIRE(c.offset >= n_rows, QW_ERR_INVALID_ARGUMENT,
                "attention: fewer cached keys than query rows");
-    QW_REQUIRE(c.device >= 0 && c.device < kMaxDevices, QW_ERR_UNSUPPORTED,
-               "turbo4 attention: device ordinal out of range");
     DeviceGuard dg(c.device);
     QW_REQUIRE(dg.ok, QW_ERR_HIP, "attention: hipSetDevice failed");
     const int D = c.D, T = c.offset;
@@ -923,31 +904,12 @@ int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float
     const size_t q_bytes = (size_t)n_q_heads * n_rows * D * sizeof(f16);
     const size_t need = 2 * kv_bytes + 2 * q_bytes;
 
-    T4Workspace& w = g_ws[c.device];
-    std::lock_guard<std::mutex> lock(w.m);
-    if (!w.last) QW_HIP_CHECK(hipEventCreateWithFlags(&w.last, hipEventDisableTiming));
-    if (need > w.bytes) {
-        if (w.buf) {
-            QW_HIP_CHECK(hipDeviceSynchronize());
-            (void)hipFree(w.buf);
-            w.buf = nullptr;
-            w.bytes = 0;
-        }
-        const size_t nb = need + need / 4;
-        if (hipMalloc(&w.buf, nb) != hipSuccess) {
-            (void)hipGetLastError();
-            w.buf = nullptr;
-            set_error("turbo4 attention: workspace hipMalloc failed");
-            return QW_ERR_OUT_OF_MEMORY;
-        }
-        w.bytes = nb;
-    } else {
-        QW_HIP_CHECK(hipStreamWaitEvent(stream, w.last, 0));
-    }
-    f16* kw = (f16*)w.buf;
-    f16* vw = (f16*)((char*)w.buf + kv_bytes);
-    f16* q_rot = (f16*)((char*)w.buf + 2 * kv_bytes);
-    f16* o_rot = (f16*)((char*)w.buf + 2 * kv_bytes + q_bytes);
+    void* wbuf = nullptr;
+    if (int rc0 = t4_workspace(c.device, stream, need, &wbuf)) return rc0;
+    f16* kw = (f16*)wbuf;
+    f16* vw = (f16*)((char*)wbuf + kv_bytes);
+    f16* q_rot = (f16*)((char*)wbuf + 2 * kv_bytes);
+    f16* o_rot = (f16*)((char*)wbuf + 2 * kv_bytes + q_bytes);
     const int qrows = n_q_heads * n_rows;
     const float* tab = c.t4_tables;
     // Every 8-key block up to capv: rows past T become zeros, as the fp16
@@ -996,7 +958,6 @@ int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float
                            o_rot, (f16*)out, qrows, tab + TT::v_s2, tab + TT::v_s1);
     }
     QW_HIP_CHECK(hipGetLastError());
-    QW_HIP_CHECK(hipEventRecord(w.last, stream));
     return QW_OK;
 }
 

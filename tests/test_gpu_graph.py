@@ -147,3 +147,49 @@ def test_graph_dlsa_first_use_inside_capture():
         g.replay()
         torch.cuda.synchronize()
         np.testing.assert_array_equal(_np(out), want, err_msg=f"replay {rep}")
+
+
+def test_graph_turbo4_routes():
+    """Turbo4 attention captured in a HIP graph: the expansion route (one
+    decode row) and the fused verify route (4 causal rows past 2048 tokens).
+    The route's workspace is per stream, so both capture; replays equal the
+    eager outputs, with eager work between the replays, also after a larger
+    call grows the stream's workspace."""
+    r = rng(14)
+    H, G, D, T = 4, 6, 256, 3000
+    c = _cache("turbo4", r, H, T, D)
+    q1 = _gpu(r.standard_normal((H * G, 1, D)).astype(np.float16))
+    q4 = _gpu(r.standard_normal((H * G, 4, D)).astype(np.float16))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):  # size the stream's workspaces before capturing
+        want1 = _np(c.attention(q1, 1 / 16))
+        want4 = _np(c.attention(q4, 1 / 16, causal=True))
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        o1 = c.attention(q1, 1 / 16)
+        o4 = c.attention(q4, 1 / 16, causal=True)
+    for rep in range(3):
+        o1.zero_()
+        o4.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(_np(o1), want1, err_msg=f"decode replay {rep}")
+        np.testing.assert_array_equal(_np(o4), want4, err_msg=f"verify replay {rep}")
+        _ = (q1.float() * 2).sum().item()
+    # a 64-row block on the same stream needs a larger workspace: it grows
+    q64 = _gpu(r.standard_normal((H * G, 64, D)).astype(np.float16))
+    with torch.cuda.stream(s):
+        big = _np(c.attention(q64, 1 / 16, causal=True))
+    torch.cuda.synchronize()
+    assert np.isfinite(big).all()
+    for rep in range(2):
+        o1.zero_()
+        o4.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(_np(o1), want1, err_msg=f"after growth, decode replay {rep}")
+        np.testing.assert_array_equal(_np(o4), want4, err_msg=f"after growth, verify replay {rep}")
+    del g
+    c.close()
