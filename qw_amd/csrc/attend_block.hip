@@ -234,20 +234,34 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     }
     const int64_t krow_words = (int64_t)D * BITS / 32;
     const int64_t vblk_words = (int64_t)D * BITS / 4;
+    // the thread's tile-0 addresses; tile t is a scalar multiple of the tile
+    // strides further on (one 64-bit add a pointer a tile)
+    const u32x4* ksrc0[PER];
+    const uint32_t* kpsrc0[PER];
+    const u32x4* vsrc0[PER];
+    const u32x4* vpsrc0[PER];
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int64_t row = (int64_t)h * a.cap + kk[j];
+        ksrc0[j] = (const u32x4*)(a.k_data + row * krow_words) + KU * q32[j];
+        kpsrc0[j] = a.k_params + row * NG + k_param_slot(q32[j] >> 1, NG);
+        const int64_t blk = (int64_t)h * (a.cap / 8) + vb[j];
+        vsrc0[j] = (const u32x4*)(a.v_data + blk * vblk_words) + KU * vj[j];
+        vpsrc0[j] = (const u32x4*)(a.v_params + (blk * NG + vgrp[j]) * 8);
+    }
     auto load = [&](Stage& st, int t) {
+        const int64_t t_rows = (int64_t)t * KT, t_blks = (int64_t)t * (KT / 8);
 #pragma unroll
         for (int j = 0; j < PER; j++) {
-            const int64_t row = (int64_t)h * a.cap + (int64_t)t * KT + kk[j];
-            const u32x4* ksrc = (const u32x4*)(a.k_data + row * krow_words) + KU * q32[j];
+            const u32x4* ksrc = ksrc0[j] + t_rows * (krow_words / 4);
 #pragma unroll
             for (int u = 0; u < KU; u++) st.kc[j][u] = ksrc[u];
-            if constexpr (AFF) st.kp[j] = a.k_params[row * NG + k_param_slot(q32[j] >> 1, NG)];
-            const int64_t blk = (int64_t)h * (a.cap / 8) + (int64_t)t * (KT / 8) + vb[j];
-            const u32x4* vsrc = (const u32x4*)(a.v_data + blk * vblk_words) + KU * vj[j];
+            if constexpr (AFF) st.kp[j] = kpsrc0[j][t_rows * NG];
+            const u32x4* vsrc = vsrc0[j] + t_blks * (vblk_words / 4);
 #pragma unroll
             for (int u = 0; u < KU; u++) st.vc[j][u] = vsrc[u];
             if constexpr (AFF) {
-                const u32x4* psrc = (const u32x4*)(a.v_params + (blk * NG + vgrp[j]) * 8);
+                const u32x4* psrc = vpsrc0[j] + t_blks * (NG * 2);
                 st.vp[j][0] = psrc[0];
                 st.vp[j][1] = psrc[1];
             }
@@ -395,9 +409,12 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
                 for (int u = 0; u < NSUB; u++)
 #pragma unroll
                     for (int j = 0; j < 4; j++) m2 = __builtin_elementwise_max(m2, sh[u][j]);
-                const float mx = wave_max_g(fmaxf((float)m2.x, (float)m2.y));
-                if (__any(mx > m_run[rt] + 5.5f)) {
-                    const float m_new = fmaxf(m_run[rt], mx);
+                // the lane's own maximum decides (m_run is the same in the
+                // four lanes of a column); the column reduction runs only when
+                // the reference moves
+                const float mx_lane = fmaxf((float)m2.x, (float)m2.y);
+                if (__any(mx_lane > m_run[rt] + 5.5f)) {
+                    const float m_new = fmaxf(m_run[rt], wave_max_g(mx_lane));
                     if (__any(m_run[rt] != -INFINITY)) {
                         const float alpha = m_run[rt] == -INFINITY
                                                 ? 0.0f

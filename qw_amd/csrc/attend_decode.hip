@@ -371,12 +371,16 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
         // ---- online softmax with a lazy reference: the row reference m_run
         // only moves when a score exceeds it by more than 5.5 (p <= e^5.5 fits
         // fp16 easily), so the accumulators are rarely rescaled.
+        // The check uses the lane's own maximum: m_run is the same in the four
+        // lanes of a row, so some lane's maximum exceeds m_run + 5.5 exactly
+        // when some row's does, and the row reduction (two LDS permutes) runs
+        // only when the reference moves.
         float mx = sc[0];
 #pragma unroll
         for (int e = 1; e < 8; e++) mx = fmaxf(mx, sc[e]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
         if (__any(mx > m_run + 5.5f)) {
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
             const float m_new = fmaxf(m_run, mx);
             if (__any(m_run != -INFINITY)) {
                 const float alpha =
