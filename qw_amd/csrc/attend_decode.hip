@@ -50,6 +50,7 @@ struct DecodeArgs {
     int cap, T, Tq, G, R, causal, n_sub, nc;
     float scale_h;     // f16(scale) as float
     uint32_t code_off2;  // magic offset pair of the separately rounded dequant
+    const float* t4_cb;  // Turbo4 caches: the 16 fp32 centroids (else null)
 };
 
 template <int BITS, int D>
@@ -90,6 +91,22 @@ constexpr int decode_stages() {
     return BITS == 4 ? 2 : 1;
 }
 
+// Turbo4: centroid idx from the register table (lane i holds centroid i % 16)
+// and its expansion f16(centroid * rescale), the product rounded to fp32 first
+// as the expansion kernel forms it.
+__device__ __forceinline__ f16 t4_expand(uint32_t idx, float r, int cbv) {
+    float p = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((int)(idx << 2), cbv)) * r;
+    asm("" : "+v"(p));
+    return (f16)p;
+}
+// 8 consecutive dims (the word's nibbles, LSB first) of one row
+__device__ __forceinline__ half8 t4_expand8(uint32_t w, float r, int cbv) {
+    half8 y;
+#pragma unroll
+    for (int j = 0; j < 8; j++) y[j] = t4_expand((w >> (4 * j)) & 15u, r, cbv);
+    return y;
+}
+
 // FAST: every scale in the cache is inside the 2-op dequant's exact range
 // (the cache's fast_flag, maintained by the append and import kernels).
 //
@@ -100,12 +117,25 @@ constexpr int decode_stages() {
 // O_b += P * Vb with B = the biases of the lane's dim group for the 8 keys
 // of its block, added to every dim of that group at the end (the bias is
 // exact in fp32; only MLX's second rounding of each V element is skipped).
-template <int BITS, int D, int NW, bool FAST>
+//
+// T4 (Turbo4 caches, BITS = 4): K and V rows of D/2 bytes of 4-bit centroid
+// indices, row-major, and one side word a row (K rescale in .x of the K side
+// plane, V rescale in .y of the V side plane). Every element is formed as the
+// fp16 expansion stores it, f16(centroid * rescale) with the product rounded
+// to fp32 first, and the attention arithmetic is the fp16 cache's (MLX's SDPA
+// on the expansion). Lane group g of a K tile reads dims (D/4) g .. +D/4 - 1 of
+// its key (q is laid out to match); the P.V lane (g, r16) reads dims
+// DPL r16 .. +DPL - 1 of keys 8g .. 8g+7 (16 lanes cover a row's D/2 bytes).
+// The centroid comes from a register table (lane i holds centroid i % 16)
+// through ds_bpermute.
+template <int BITS, int D, int NW, bool FAST, bool T4 = false>
 __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)[16], float* sm_o,
                                             half8 (*sm_q)[64]) {
     using S = DecodeShape<BITS, D>;
-    constexpr int NM = S::NM, DPL = S::DPL, NG = S::NG, KL = S::KL, VL = S::VL;
-    constexpr bool AFF = BITS != 16;
+    constexpr int NM = S::NM, DPL = S::DPL, NG = S::NG, VL = S::VL;
+    static_assert(!T4 || BITS == 4, "Turbo4 indices are 4-bit");
+    constexpr bool AFF = BITS != 16 && !T4;
+    constexpr int KL = T4 ? D / 128 : S::KL;  // 128-bit K loads a lane a tile
     const int c = blockIdx.x, h = blockIdx.y;
     // wave index as a scalar: sub-chunk indices, and so the buffer offsets
     // below, stay in SGPRs
@@ -120,14 +150,19 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
     const int SS = a.nc * NW;  // stride between a wave's sub-chunks
     const int s_end = a.n_sub;
     const uint32_t magic = vconst(kMagic);
+    const int cbv = T4 ? __builtin_bit_cast(int, a.t4_cb[lane & 15]) : 0;  // Turbo4 centroid table
 
     // One 32-key sub-chunk's loads; a wave walks its sub-chunks
     // c + nc * (wave + NW * k) through one of these.
+    // T4: vc holds the DPL/2-byte row pieces of keys 8g..8g+7 (two keys a
+    // u32x4 at D = 256, four at D = 128), vp the 8 keys' V side words, kp[t].x
+    // the K side word of the lane's key.
+    constexpr int VLS = T4 ? (D == 256 ? 4 : 2) : VL;
     struct Stage {
         u32x4 kc[2][KL];  // K codes of tiles 0/1 (16 keys each)
         u32x4 kp[2];      // K (scale, bias) of the lane's key, tiles 0/1 (4-bit: the
                           // lane's groups g/2 and 2+g/2 in .x/.y)
-        u32x4 vc[VL];     // V block of keys 8g..8g+7, the lane's DPL dims
+        u32x4 vc[VLS];    // V block of keys 8g..8g+7, the lane's DPL dims
         u32x4 vp[2];      // V scales / biases of that block and dim group
     };
     // Raw buffer loads over this KV head's rows of each plane: the lane's
@@ -136,21 +171,22 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
     // the chunk's end gets num_records = 0, so its loads are issued
     // unconditionally but return zeros without touching memory.
     constexpr int KRB = D * BITS / 8;          // K row bytes
-    constexpr int KPB = AFF ? NG * 4 : 0;      // K param bytes a row
-    constexpr int VBB = D * BITS;              // V block bytes (8 keys: D*BITS/4 words)
-    constexpr int VPB = NG * 32;               // V param bytes a block
+    constexpr int KPB = T4 ? 4 : AFF ? NG * 4 : 0;  // K param bytes a row
+    constexpr int VBB = D * BITS;              // V block bytes (8 keys: D*BITS/4 words; T4: 8 rows)
+    constexpr int VPB = T4 ? 32 : NG * 32;     // V param bytes a block (T4: 8 side words)
     const int64_t hrow = (int64_t)h * a.cap;
     const char* kbase = (const char*)a.k_data + hrow * KRB;
     const char* kpbase = (const char*)a.k_params + hrow * KPB;
     const char* vbase = (const char*)a.v_data + hrow / 8 * VBB;
     const char* vpbase = (const char*)a.v_params + hrow / 8 * VPB;
     const int kkey = 8 * (r16 >> 2) + (r16 & 3);  // the lane's K row in tile 0
-    const int off_k = kkey * KRB + 16 * g;
-    const int off_kp = BITS == 4 && NG == 4 ? kkey * KPB + 8 * (g >> 1)
+    const int off_k = T4 ? kkey * KRB + (KRB / 4) * g : kkey * KRB + 16 * g;
+    const int off_kp = T4                   ? kkey * KPB
+                       : BITS == 4 && NG == 4 ? kkey * KPB + 8 * (g >> 1)
                        : BITS == 4          ? kkey * KPB + 4 * (g >> 1)
                                             : kkey * KPB;
-    const int off_v = g * VBB + 16 * r16;
-    const int off_vp = (g * NG + (r16 * DPL) / 64) * 32;
+    const int off_v = T4 ? g * VBB + (DPL / 2) * r16 : g * VBB + 16 * r16;
+    const int off_vp = T4 ? g * VPB : (g * NG + (r16 * DPL) / 64) * 32;
     // K half of a stage (codes + params: 2*KL + 2 loads) and V half (VL + 2).
     auto load_k = [&](Stage& st, int s) {
         const bool ok = s < s_end;
@@ -163,7 +199,16 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
             for (int cc = 0; cc < KL; cc++)
                 st.kc[tile][cc] = __builtin_bit_cast(
                     u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                               rk, off_k + tile * 4 * KRB + 64 * cc, 32 * si * KRB, 0));
+                               rk, off_k + tile * 4 * KRB + (T4 ? 16 : 64) * cc, 32 * si * KRB, 0));
+        }
+        if constexpr (T4) {
+            const __amdgpu_buffer_rsrc_t rkp =
+                __builtin_amdgcn_make_buffer_rsrc((void*)kpbase, 0, ok ? a.cap * KPB : 0, kBufWord3);
+#pragma unroll
+            for (int tile = 0; tile < 2; tile++)
+                st.kp[tile] = u32x4{__builtin_amdgcn_raw_buffer_load_b32(rkp, off_kp + tile * 4 * KPB,
+                                                                         32 * si * KPB, 0),
+                                    0u, 0u, 0u};
         }
         if constexpr (AFF) {
             const __amdgpu_buffer_rsrc_t rkp =
@@ -192,10 +237,30 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
         const int si = ok ? s : 0;
         const __amdgpu_buffer_rsrc_t rv =
             __builtin_amdgcn_make_buffer_rsrc((void*)vbase, 0, ok ? a.cap / 8 * VBB : 0, kBufWord3);
+        if constexpr (T4) {
+            // key 8g + j: the lane's DPL/2 bytes of that row (row stride KRB)
 #pragma unroll
-        for (int jj = 0; jj < VL; jj++)
-            st.vc[jj] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, off_v + 256 * jj, 4 * si * VBB, 0));
+            for (int j = 0; j < 8; j++) {
+                if constexpr (D == 256) {
+                    const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(rv, off_v + j * KRB, 4 * si * VBB, 0);
+                    st.vc[j / 2][2 * (j % 2)] = t2[0];
+                    st.vc[j / 2][2 * (j % 2) + 1] = t2[1];
+                } else {
+                    st.vc[j / 4][j % 4] = __builtin_amdgcn_raw_buffer_load_b32(rv, off_v + j * KRB, 4 * si * VBB, 0);
+                }
+            }
+            const __amdgpu_buffer_rsrc_t rvp =
+                __builtin_amdgcn_make_buffer_rsrc((void*)vpbase, 0, ok ? a.cap / 8 * VPB : 0, kBufWord3);
+            st.vp[0] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rvp, off_vp, 4 * si * VPB, 0));
+            st.vp[1] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rvp, off_vp + 16, 4 * si * VPB, 0));
+        } else {
+#pragma unroll
+            for (int jj = 0; jj < VL; jj++)
+                st.vc[jj] = __builtin_bit_cast(
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, off_v + 256 * jj, 4 * si * VBB, 0));
+        }
         if constexpr (AFF) {
             const __amdgpu_buffer_rsrc_t rvp =
                 __builtin_amdgcn_make_buffer_rsrc((void*)vpbase, 0, ok ? a.cap / 8 * VPB : 0, kBufWord3);
@@ -223,7 +288,9 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
         const f16* qrow = a.q + ((int64_t)(h * a.G + rr % a.G) * a.Tq + rr / a.G) * D;
         const int m = wave % NM;
         int base;
-        if constexpr (BITS == 4)
+        if constexpr (T4)
+            base = (D / 4) * g + 8 * m;
+        else if constexpr (BITS == 4)
             base = 8 * (16 * (m / 4) + 4 * g + (m % 4));
         else if constexpr (BITS == 8)
             base = 4 * (16 * (m / 2) + 4 * g + 2 * (m % 2));
@@ -245,7 +312,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
             const int m = wave;
             const u32x4 w = __builtin_bit_cast(u32x4, x);
             u32x4 o;
-            if constexpr (BITS == 4) {
+            if constexpr (BITS == 4 && !T4) {
                 // 4-bit K pairs come out as dims (0,4),(1,5),(2,6),(3,7).
                 o.x = __builtin_amdgcn_perm(w.z, w.x, 0x05040100u);
                 o.y = __builtin_amdgcn_perm(w.z, w.x, 0x07060302u);
@@ -291,7 +358,17 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
     auto qk = [&](const Stage& st, float4v& acc0, float4v& acc1) {
         acc0 = float4v{0.f, 0.f, 0.f, 0.f};
         acc1 = float4v{0.f, 0.f, 0.f, 0.f};
-        if constexpr (BITS == 4) {
+        if constexpr (T4) {
+            // step m: dims (D/4) g + 8m .. +7 of the lane's key, word m of its codes
+            const float kr0 = (float)h2(st.kp[0][0]).x, kr1 = (float)h2(st.kp[1][0]).x;
+#pragma unroll
+            for (int m = 0; m < NM; m++) {
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(t4_expand8(st.kc[0][m / 4][m % 4], kr0, cbv),
+                                                              qop(m), acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(t4_expand8(st.kc[1][m / 4][m % 4], kr1, cbv),
+                                                              qop(m), acc1, 0, 0, 0);
+            }
+        } else if constexpr (BITS == 4) {
             // load cc covers words 16cc + 4g .. +3, all in group 2cc + g/2
 #pragma unroll
             for (int cc = 0; cc < KL; cc++) {
@@ -336,6 +413,24 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
         }
     };
     auto pv = [&](const Stage& st, const half8& pop) {
+        if constexpr (T4) {
+            // B of output tile mm: dim DPL r16 + mm of keys 8g..8g+7 (nibble mm
+            // of each key's row piece)
+            float vr[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) vr[j] = (float)h2(st.vp[j / 4][j % 4]).y;
+#pragma unroll
+            for (int mm = 0; mm < DPL; mm++) {
+                half8 bv;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const uint32_t w = D == 256 ? st.vc[j / 2][2 * (j % 2) + mm / 8] : st.vc[j / 4][j % 4];
+                    bv[j] = t4_expand((w >> (4 * (mm % 8))) & 15u, vr[j], cbv);
+                }
+                acc_o[mm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop, bv, acc_o[mm], 0, 0, 0);
+            }
+            return;
+        }
         PairConsts pc;
         if constexpr (AFF)
             pc = make_consts<FAST, BITS>(h2(st.vp[0][0]), h2(st.vp[0][1]), h2(st.vp[0][2]),
@@ -416,21 +511,25 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
         // as the stage's K half is in, so about one stage of a wave is in
         // flight at a time (measured faster than both stages in flight from
         // the start, and than waiting for whole stages).
-        constexpr int NK = 2 * KL + (AFF ? 2 : 0), NV = VL + (AFF ? 2 : 0);
-        static_assert(NK == NV && NK < 16, "equal K and V halves: one vmcnt value");
-        constexpr int kWaitHalf = 0x0F70 | NK;  // vmcnt(NK), expcnt/lgkmcnt untouched
+        // loads a K half and a V half of a stage issue
+        constexpr int NK = 2 * KL + (AFF || T4 ? 2 : 0), NV = (T4 ? 8 : VL) + (AFF || T4 ? 2 : 0);
+        static_assert(NK < 16 && NV < 16, "vmcnt field");
+        // vmcnt(n), expcnt/lgkmcnt untouched: a stage's K half is in while its
+        // V half (NV loads) may be in flight; its V half while the next
+        // stage's K half (NK loads) may be
+        constexpr int kWaitK = 0x0F70 | NV, kWaitV = 0x0F70 | NK;
         for (; s < s_end; s += 2 * SS) {
-            __builtin_amdgcn_s_waitcnt(kWaitHalf);  // K(A) in; V(A) may be in flight
+            __builtin_amdgcn_s_waitcnt(kWaitK);  // K(A) in; V(A) may be in flight
             load_k(B, s + SS);
             const half8 pa = scores(A, s);
-            __builtin_amdgcn_s_waitcnt(kWaitHalf);  // V(A) in; K(B) may be in flight
+            __builtin_amdgcn_s_waitcnt(kWaitV);  // V(A) in; K(B) may be in flight
             load_v(B, s + SS);
             pv(A, pa);
             if (s + SS >= s_end) break;
-            __builtin_amdgcn_s_waitcnt(kWaitHalf);
+            __builtin_amdgcn_s_waitcnt(kWaitK);
             load_k(A, s + 2 * SS);
             const half8 pb = scores(B, s + SS);
-            __builtin_amdgcn_s_waitcnt(kWaitHalf);
+            __builtin_amdgcn_s_waitcnt(kWaitV);
             load_v(A, s + 2 * SS);
             pv(B, pb);
         }
@@ -485,7 +584,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
     }
 }
 
-template <int BITS, int D>
+template <int BITS, int D, bool T4 = false>
 __global__ __launch_bounds__((64 * decode_waves<BITS, D>()), 1) void attend_decode_kernel(
     DecodeArgs a) {
     constexpr int NW = decode_waves<BITS, D>();
@@ -500,14 +599,15 @@ __global__ __launch_bounds__((64 * decode_waves<BITS, D>()), 1) void attend_deco
     // pass's partial (same threads, same elements) replaces the first. A
     // null flag (Int8 caches, which always take the separately rounded
     // dequant) goes to that path directly.
-    if (BITS == 16 || a.fast_flag != nullptr) {
+    // Turbo4 caches have one dequant (a null flag).
+    if (!T4 && (BITS == 16 || a.fast_flag != nullptr)) {
         decode_body<BITS, D, NW, true>(a, sm_ml, sm_o, sm_q);
         if (BITS != 16 && *a.fast_flag == 0) {
             __syncthreads();
             decode_body<BITS, D, NW, false>(a, sm_ml, sm_o, sm_q);
         }
     } else {
-        decode_body<BITS, D, NW, false>(a, sm_ml, sm_o, sm_q);
+        decode_body<BITS, D, NW, false, T4>(a, sm_ml, sm_o, sm_q);
     }
 }
 
@@ -588,10 +688,10 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
 
 // Split-K attention of the Tq rows over the first T cached keys: launches the
 // decode kernel and returns its partials (nc per KV head, 16 rows apart).
-template <int BITS, int D>
+template <int BITS, int D, bool T4 = false>
 static int launch_decode_partials(KVCache& cc, const f16* q, int G, int Tq, int T, float scale,
                                   bool causal, int* nc_out, float** po, float2** pml,
-                                  hipStream_t stream) {
+                                  hipStream_t stream, const float* t4_cb = nullptr) {
     const int n_sub = (T + 31) / 32;
     // Sub-chunks a wave owns: 4-bit rows are small enough to keep 4 in flight.
     // Sub-chunks a wave keeps in flight per round, and workgroups per KV head:
@@ -610,7 +710,8 @@ static int launch_decode_partials(KVCache& cc, const f16* q, int G, int Tq, int 
     a.k_params = cc.k_params;
     a.v_data = (const uint32_t*)cc.v_data;
     a.v_params = cc.v_params;
-    a.fast_flag = cc.int8() ? nullptr : cc.fast_flag;  // null: always separately rounded
+    a.fast_flag = cc.int8() || T4 ? nullptr : cc.fast_flag;  // null: always separately rounded
+    a.t4_cb = t4_cb;
     a.q = q;
     a.part_o = (float*)cc.ws_ptr;
     a.part_ml = (float2*)((char*)cc.ws_ptr + (size_t)cc.hkv * nc * 16 * D * sizeof(float));
@@ -626,9 +727,9 @@ static int launch_decode_partials(KVCache& cc, const f16* q, int G, int Tq, int 
     a.code_off2 = cc.code_offset2();
     size_t shmem = (size_t)NW * (D / 16) * (((a.R + 3) / 4) * 16 + 1) * 16;  // wave-merge sm_o
     // Dynamic LDS above 64 KB must be allowed per kernel and device.
-    rc = ensure_dynamic_lds((const void*)attend_decode_kernel<BITS, D>, shmem);
+    rc = ensure_dynamic_lds((const void*)attend_decode_kernel<BITS, D, T4>, shmem);
     if (rc) return rc;
-    hipLaunchKernelGGL((attend_decode_kernel<BITS, D>), dim3(nc, cc.hkv), dim3(64 * NW), shmem,
+    hipLaunchKernelGGL((attend_decode_kernel<BITS, D, T4>), dim3(nc, cc.hkv), dim3(64 * NW), shmem,
                        stream, a);
     QW_HIP_CHECK(hipGetLastError());
     *nc_out = nc;
@@ -647,6 +748,19 @@ static int launch_decode_bits(KVCache& cc, const f16* q, int G, int Tq, float sc
                                              &pml, stream);
     if (rc) return rc;
     return launch_partial_merge(po, pml, nc, 16, 0, G * Tq, cc.hkv, D, G, Tq, out, stream);
+}
+
+int launch_turbo4_decode(KVCache& cc, const f16* q_rot, int G, int Tq, float scale, bool causal,
+                         const float* cb, f16* o_rot, hipStream_t stream) {
+    int nc = 0;
+    float* po = nullptr;
+    float2* pml = nullptr;
+    int rc = cc.D == 256 ? launch_decode_partials<4, 256, true>(cc, q_rot, G, Tq, cc.offset, scale,
+                                                                causal, &nc, &po, &pml, stream, cb)
+                         : launch_decode_partials<4, 128, true>(cc, q_rot, G, Tq, cc.offset, scale,
+                                                                causal, &nc, &po, &pml, stream, cb);
+    if (rc) return rc;
+    return launch_partial_merge(po, pml, nc, 16, 0, G * Tq, cc.hkv, cc.D, G, Tq, o_rot, stream);
 }
 
 // The same merge for many rows (block kernels' key splits): one thread an

@@ -249,6 +249,11 @@ __global__ __launch_bounds__(128) void turbo4_fetch_kernel(
 // cache's transposed blocks vw [hkv][capv/8][D][8] (dims in lane order)
 // through LDS. Keys past `T` are written as zeros (the fp16 kernels read
 // whole 8-key blocks).
+// 1: Turbo4 calls of up to 16 rows a KV head (decode) read the packed cache in
+// the decode kernel; 0: they expand it to fp16 first, as longer blocks do.
+#ifndef QW_T4_FUSED_DECODE
+#define QW_T4_FUSED_DECODE 1
+#endif
 constexpr int kExpandBlocks = 4;  // 8-key blocks a workgroup (capv / 8 is a multiple of 32)
 
 template <int D>
@@ -899,6 +904,46 @@ int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float
     // cached tokens; here also G * rows <= 32 (one workgroup's rows).
     if (causal && n_rows <= 5 && T > 2048 && (n_q_heads / c.hkv) * n_rows <= kT4vRows)
         return turbo4_verify(c, q, n_q_heads, n_rows, scale, out, stream);
+    const int qrows = n_q_heads * n_rows;
+    const float* tab = c.t4_tables;
+#if QW_T4_FUSED_DECODE
+    if ((n_q_heads / c.hkv) * n_rows <= 16) {
+        // Up to 16 rows a KV head: the decode kernel reads the packed indices
+        // in place (the values the fp16 expansion would hold, the fp16 SDPA
+        // arithmetic on them) between the two rotations.
+        const size_t q_bytes = (size_t)qrows * D * sizeof(f16);
+        void* wbuf = nullptr;
+        if (int rc0 = t4_workspace(c.device, stream, 2 * q_bytes, &wbuf)) return rc0;
+        f16* q_rot = (f16*)wbuf;
+        f16* o_rot = (f16*)((char*)wbuf + q_bytes);
+        const dim3 rg((qrows + 3) / 4);
+        if (D == 256) {
+            using TT = T4Tab<256>;
+            hipLaunchKernelGGL(turbo4_rotate_kernel<256>, rg, dim3(256), 0, stream, (const f16*)q,
+                               q_rot, qrows, tab + TT::k_s1, tab + TT::k_s2);
+        } else {
+            using TT = T4Tab<128>;
+            hipLaunchKernelGGL(turbo4_rotate_kernel<128>, rg, dim3(256), 0, stream, (const f16*)q,
+                               q_rot, qrows, tab + TT::k_s1, tab + TT::k_s2);
+        }
+        QW_HIP_CHECK(hipGetLastError());
+        const float* cb = tab + (D == 256 ? T4Tab<256>::cb : T4Tab<128>::cb);
+        int rc = launch_turbo4_decode(c, q_rot, n_q_heads / c.hkv, n_rows, scale, causal, cb, o_rot,
+                                      stream);
+        if (rc) return rc;
+        if (D == 256) {
+            using TT = T4Tab<256>;
+            hipLaunchKernelGGL(turbo4_rotate_kernel<256>, rg, dim3(256), 0, stream, o_rot, (f16*)out,
+                               qrows, tab + TT::v_s2, tab + TT::v_s1);
+        } else {
+            using TT = T4Tab<128>;
+            hipLaunchKernelGGL(turbo4_rotate_kernel<128>, rg, dim3(256), 0, stream, o_rot, (f16*)out,
+                               qrows, tab + TT::v_s2, tab + TT::v_s1);
+        }
+        QW_HIP_CHECK(hipGetLastError());
+        return QW_OK;
+    }
+#endif
     const int capv = (T + 255) / 256 * 256;
     const size_t kv_bytes = (size_t)c.hkv * capv * D * sizeof(f16);
     const size_t q_bytes = (size_t)n_q_heads * n_rows * D * sizeof(f16);
@@ -910,8 +955,6 @@ int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float
     f16* vw = (f16*)((char*)wbuf + kv_bytes);
     f16* q_rot = (f16*)((char*)wbuf + 2 * kv_bytes);
     f16* o_rot = (f16*)((char*)wbuf + 2 * kv_bytes + q_bytes);
-    const int qrows = n_q_heads * n_rows;
-    const float* tab = c.t4_tables;
     // Every 8-key block up to capv: rows past T become zeros, as the fp16
     // cache's unused rows are, since the fp16 kernels read whole tiles.
     dim3 eg(capv / (8 * kExpandBlocks), c.hkv);

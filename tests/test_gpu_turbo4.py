@@ -216,7 +216,9 @@ def fused_verify_route(T, L, causal, G):
 
 
 @pytest.mark.parametrize("T_prefix,L,causal,D", [
-    (4095, 1, False, 256),    # decode (the fp16 decode kernel on the rotated expansion)
+    (4095, 1, False, 256),    # decode: the decode kernel on the packed indices, rotated basis
+    (12286, 1, False, 256),   # decode over 12287 keys (a partial last 32-key sub-chunk)
+    (1500, 2, True, 256),     # 2 causal rows below the gate (G * L = 12): the decode kernel
     (2999, 2, True, 256),     # 2-row verify past 2048 tokens: the fused verify kernel
     (4090, 5, True, 256),     # 5-row verify (G * L = 30 rows): fused
     (2046, 3, True, 256),     # 2049 tokens: fused, one partial key stage per split
@@ -225,8 +227,8 @@ def fused_verify_route(T, L, causal, G):
     (3333, 4, True, 128),     # head_dim 128: fused
     (65532, 4, True, 256),    # 65536 tokens, 64 key stages a split
     (1000, 16, True, 256),    # 16-row verify block
-    (900, 128, True, 256),    # prefill chunk
-    (777, 1, False, 128),     # head_dim 128
+    (900, 128, True, 256),    # prefill chunk (expansion + block kernel)
+    (777, 1, False, 128),     # head_dim 128 decode
     (0, 1, False, 256),       # first token
 ])
 def test_turbo4_attention_matches_oracle(T_prefix, L, causal, D):
