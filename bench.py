@@ -287,9 +287,10 @@ def bench_turbo4_verify(torch, qw_amd, steps: int, warmup: int, reps: int,
 def bench_turbo4_decode(torch, qw_amd, steps: int, warmup: int, reps: int,
                         T_prefix: int = 32768):
     """The reference's served default KV mode at the config-2 geometry:
-    update_and_attention of one token on a Turbo4 cache (rotate q, expand the
-    rotated K/V to fp16, the fp16 decode kernels, rotate the output back).
-    Graph-replayed like the affine paths; the eager figure beside it."""
+    update_and_attention of one token on a Turbo4 cache (append the token; the
+    decode kernel rotates q and reads the packed indices in place; the merge
+    rotates the output back). Graph-replayed like the affine paths; the eager
+    figure beside it."""
     ls = LayerSet(torch, qw_amd, 3, 4, T_prefix, 1, LAYERS, causal=False, mode="turbo4")
     ls.warm(warmup)
     eager_ms = ls.time_eager(steps)

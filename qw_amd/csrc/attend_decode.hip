@@ -35,6 +35,7 @@
 #include "dequant.hpp"
 #include "quant.hpp"
 #include "kv_cache.hpp"
+#include "turbo4_device.hpp"
 
 namespace qw {
 
@@ -50,7 +51,7 @@ struct DecodeArgs {
     int cap, T, Tq, G, R, causal, n_sub, nc;
     float scale_h;     // f16(scale) as float
     uint32_t code_off2;  // magic offset pair of the separately rounded dequant
-    const float* t4_cb;  // Turbo4 caches: the 16 fp32 centroids (else null)
+    const float* t4_tab;  // Turbo4 caches: the device tables (signs, centroids); else null
 };
 
 template <int BITS, int D>
@@ -91,19 +92,25 @@ constexpr int decode_stages() {
     return BITS == 4 ? 2 : 1;
 }
 
-// Turbo4: centroid idx from the register table (lane i holds centroid i % 16)
-// and its expansion f16(centroid * rescale), the product rounded to fp32 first
-// as the expansion kernel forms it.
-__device__ __forceinline__ f16 t4_expand(uint32_t idx, float r, int cbv) {
-    float p = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((int)(idx << 2), cbv)) * r;
+// Turbo4: the 256-entry LDS table of centroid pairs (entry b = (centroid of
+// the low nibble of b, centroid of its high nibble)) turns one byte of codes
+// into two centroids with one 8-byte read (measured ~1.9x the throughput of a
+// ds_bpermute per element); the expansion f16(centroid * rescale) rounds the
+// product to fp32 first, as the expansion kernel forms it.
+__device__ __forceinline__ f16 t4_product(float c, float r) {
+    float p = c * r;
     asm("" : "+v"(p));
     return (f16)p;
 }
 // 8 consecutive dims (the word's nibbles, LSB first) of one row
-__device__ __forceinline__ half8 t4_expand8(uint32_t w, float r, int cbv) {
+__device__ __forceinline__ half8 t4_expand8(uint32_t w, float r, const float2* pt) {
     half8 y;
 #pragma unroll
-    for (int j = 0; j < 8; j++) y[j] = t4_expand((w >> (4 * j)) & 15u, r, cbv);
+    for (int k = 0; k < 4; k++) {
+        const float2 c = pt[(w >> (8 * k)) & 0xFFu];
+        y[2 * k] = t4_product(c.x, r);
+        y[2 * k + 1] = t4_product(c.y, r);
+    }
     return y;
 }
 
@@ -130,7 +137,7 @@ __device__ __forceinline__ half8 t4_expand8(uint32_t w, float r, int cbv) {
 // through ds_bpermute.
 template <int BITS, int D, int NW, bool FAST, bool T4 = false>
 __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)[16], float* sm_o,
-                                            half8 (*sm_q)[64]) {
+                                            half8 (*sm_q)[64], float2* sm_t4 = nullptr) {
     using S = DecodeShape<BITS, D>;
     constexpr int NM = S::NM, DPL = S::DPL, NG = S::NG, VL = S::VL;
     static_assert(!T4 || BITS == 4, "Turbo4 indices are 4-bit");
@@ -150,7 +157,6 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
     const int SS = a.nc * NW;  // stride between a wave's sub-chunks
     const int s_end = a.n_sub;
     const uint32_t magic = vconst(kMagic);
-    const int cbv = T4 ? __builtin_bit_cast(int, a.t4_cb[lane & 15]) : 0;  // Turbo4 centroid table
 
     // One 32-key sub-chunk's loads; a wave walks its sub-chunks
     // c + nc * (wave + NW * k) through one of these.
@@ -282,10 +288,33 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
     const int rho = r16;
     const bool row_ok = rho < a.R;
     static_assert(NW >= NM, "one Q slice per wave");
+    // Turbo4: the rows are rotated into the K basis here (as the rotation
+    // kernel does it, one wave a row) and staged as fp16 in the wave merge's
+    // LDS area, which is free until the main loop ends.
+    f16* const sm_qr = (f16*)sm_o;
+    if constexpr (T4) {
+        constexpr int VPL = D / 64;
+        for (int b = threadIdx.x; b < 256; b += 64 * NW) {
+            const float* cb = a.t4_tab + T4Tab<D>::cb;
+            sm_t4[b] = float2{cb[b & 15], cb[b >> 4]};
+        }
+        for (int row = wave; row < a.R; row += NW) {
+            const f16* qrow = a.q + ((int64_t)(h * a.G + row % a.G) * a.Tq + row / a.G) * D;
+            float y[VPL];
+            f16 o[VPL];
+#pragma unroll
+            for (int j = 0; j < VPL; j++) y[j] = (float)qrow[lane * VPL + j];
+            t4_rotate_row<D>(y, lane, a.t4_tab + T4Tab<D>::k_s1, a.t4_tab + T4Tab<D>::k_s2, o);
+#pragma unroll
+            for (int j = 0; j < VPL; j++) sm_qr[row * D + lane * VPL + j] = o[j];
+        }
+        __syncthreads();
+    }
     half8 x;
     {
         const int rr = row_ok ? rho : 0;
-        const f16* qrow = a.q + ((int64_t)(h * a.G + rr % a.G) * a.Tq + rr / a.G) * D;
+        const f16* qrow = T4 ? sm_qr + rr * D
+                             : a.q + ((int64_t)(h * a.G + rr % a.G) * a.Tq + rr / a.G) * D;
         const int m = wave % NM;
         int base;
         if constexpr (T4)
@@ -363,9 +392,9 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
             const float kr0 = (float)h2(st.kp[0][0]).x, kr1 = (float)h2(st.kp[1][0]).x;
 #pragma unroll
             for (int m = 0; m < NM; m++) {
-                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(t4_expand8(st.kc[0][m / 4][m % 4], kr0, cbv),
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(t4_expand8(st.kc[0][m / 4][m % 4], kr0, sm_t4),
                                                               qop(m), acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(t4_expand8(st.kc[1][m / 4][m % 4], kr1, cbv),
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(t4_expand8(st.kc[1][m / 4][m % 4], kr1, sm_t4),
                                                               qop(m), acc1, 0, 0, 0);
             }
         } else if constexpr (BITS == 4) {
@@ -419,15 +448,20 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
             float vr[8];
 #pragma unroll
             for (int j = 0; j < 8; j++) vr[j] = (float)h2(st.vp[j / 4][j % 4]).y;
+            // output tiles 2e, 2e+1: byte e of each key's piece (one pair lookup
+            // a key for both)
 #pragma unroll
-            for (int mm = 0; mm < DPL; mm++) {
-                half8 bv;
+            for (int e = 0; e < DPL / 2; e++) {
+                half8 b0, b1;
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
-                    const uint32_t w = D == 256 ? st.vc[j / 2][2 * (j % 2) + mm / 8] : st.vc[j / 4][j % 4];
-                    bv[j] = t4_expand((w >> (4 * (mm % 8))) & 15u, vr[j], cbv);
+                    const uint32_t w = D == 256 ? st.vc[j / 2][2 * (j % 2) + e / 4] : st.vc[j / 4][j % 4];
+                    const float2 c = sm_t4[(w >> (8 * (e % 4))) & 0xFFu];
+                    b0[j] = t4_product(c.x, vr[j]);
+                    b1[j] = t4_product(c.y, vr[j]);
                 }
-                acc_o[mm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop, bv, acc_o[mm], 0, 0, 0);
+                acc_o[2 * e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop, b0, acc_o[2 * e], 0, 0, 0);
+                acc_o[2 * e + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop, b1, acc_o[2 * e + 1], 0, 0, 0);
             }
             return;
         }
@@ -590,6 +624,7 @@ __global__ __launch_bounds__((64 * decode_waves<BITS, D>()), 1) void attend_deco
     constexpr int NW = decode_waves<BITS, D>();
     __shared__ float2 sm_ml[NW][16];
     __shared__ half8 sm_q[D / 32][64];
+    __shared__ float2 sm_t4[T4 ? 256 : 1];  // Turbo4 centroid-pair table
     // dynamic LDS: the wave merge's sm_o [NW][DPL][R] float4
     extern __shared__ __attribute__((aligned(16))) float sm_o[];
     // The exact 2-op dequant runs first without waiting for the cache's fast
@@ -607,7 +642,7 @@ __global__ __launch_bounds__((64 * decode_waves<BITS, D>()), 1) void attend_deco
             decode_body<BITS, D, NW, false>(a, sm_ml, sm_o, sm_q);
         }
     } else {
-        decode_body<BITS, D, NW, false, T4>(a, sm_ml, sm_o, sm_q);
+        decode_body<BITS, D, NW, false, T4>(a, sm_ml, sm_o, sm_q, sm_t4);
     }
 }
 
@@ -691,7 +726,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
 template <int BITS, int D, bool T4 = false>
 static int launch_decode_partials(KVCache& cc, const f16* q, int G, int Tq, int T, float scale,
                                   bool causal, int* nc_out, float** po, float2** pml,
-                                  hipStream_t stream, const float* t4_cb = nullptr) {
+                                  hipStream_t stream, const float* t4_tab = nullptr) {
     const int n_sub = (T + 31) / 32;
     // Sub-chunks a wave owns: 4-bit rows are small enough to keep 4 in flight.
     // Sub-chunks a wave keeps in flight per round, and workgroups per KV head:
@@ -700,7 +735,9 @@ static int launch_decode_partials(KVCache& cc, const f16* q, int G, int Tq, int 
     // One workgroup a CU (256 CUs), at least a wave's worth of sub-chunks each.
     constexpr int NW = decode_waves<BITS, D>();
     const int per_head = std::max(1, 256 / cc.hkv);
-    const int nc = std::max(1, std::min({per_head, (n_sub + NW - 1) / NW, 4 * kMergeMaxPer}));
+    // Turbo4: at most 128 partials a head (its merge kernel sums up to 32 a thread)
+    const int nc_cap = T4 ? 128 : 4 * kMergeMaxPer;
+    const int nc = std::max(1, std::min({per_head, (n_sub + NW - 1) / NW, nc_cap}));
     const size_t need = (size_t)cc.hkv * nc * 16 * D * sizeof(float) +
                         (size_t)cc.hkv * nc * 16 * sizeof(float2);
     int rc = cc.ensure_workspace(need, stream);
@@ -711,7 +748,7 @@ static int launch_decode_partials(KVCache& cc, const f16* q, int G, int Tq, int 
     a.v_data = (const uint32_t*)cc.v_data;
     a.v_params = cc.v_params;
     a.fast_flag = cc.int8() || T4 ? nullptr : cc.fast_flag;  // null: always separately rounded
-    a.t4_cb = t4_cb;
+    a.t4_tab = t4_tab;
     a.q = q;
     a.part_o = (float*)cc.ws_ptr;
     a.part_ml = (float2*)((char*)cc.ws_ptr + (size_t)cc.hkv * nc * 16 * D * sizeof(float));
@@ -750,17 +787,116 @@ static int launch_decode_bits(KVCache& cc, const f16* q, int G, int Tq, float sc
     return launch_partial_merge(po, pml, nc, 16, 0, G * Tq, cc.hkv, D, G, Tq, out, stream);
 }
 
-int launch_turbo4_decode(KVCache& cc, const f16* q_rot, int G, int Tq, float scale, bool causal,
-                         const float* cb, f16* o_rot, hipStream_t stream) {
+// Turbo4 decode merge: one workgroup a query row, D/64 x 4 waves (wave w sums
+// partials c = w % 4, w % 4 + 4, ... of dims 64 (w / 4) .. +63, every load
+// issued first). The merged row is rounded to fp16 (the rotated-basis SDPA
+// output) and rotated back through the V basis by wave 0, as the rotation
+// kernel forms it.
+template <int D, int PER>
+__global__ __launch_bounds__(D * 4) void t4_merge_rotate_kernel(const float* __restrict__ part_o,
+                                                              const float2* __restrict__ part_ml,
+                                                              int nc, int rstride, int G, int Tq,
+                                                              const float* __restrict__ tab,
+                                                              f16* __restrict__ out) {
+    constexpr int NDG = D / 64;
+    const int row = blockIdx.x, h = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int pg = wave & 3, d = 64 * (wave >> 2) + lane;
+    const int64_t base = (int64_t)h * nc * rstride + row;
+    float v[PER];
+    float2 ml[PER];
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int c = pg + 4 * i;
+        if (c < nc) {
+            ml[i] = part_ml[base + (int64_t)c * rstride];
+            v[i] = part_o[(base + (int64_t)c * rstride) * D + d];
+        } else {
+            ml[i] = float2{-INFINITY, 0.0f};
+            v[i] = 0.0f;
+        }
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PER; i++) m = fmaxf(m, ml[i].x);
+    __shared__ float sm_m[4];
+    __shared__ float sm[2][4][D];
+    __shared__ f16 sm_y[D];
+    if (wave < 4 && lane == 0) sm_m[pg] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(sm_m[0], sm_m[1]), fmaxf(sm_m[2], sm_m[3]));
+    float o = 0.0f, l = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const float w = ml[i].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((ml[i].x - m) * kLog2e);
+        o = __builtin_fmaf(w, v[i], o);
+        l = __builtin_fmaf(w, ml[i].y, l);
+    }
+    sm[0][pg][d] = o;
+    sm[1][pg][d] = l;
+    __syncthreads();
+    if (pg == 0) {
+        const float O = (sm[0][0][d] + sm[0][1][d]) + (sm[0][2][d] + sm[0][3][d]);
+        const float L = (sm[1][0][d] + sm[1][1][d]) + (sm[1][2][d] + sm[1][3][d]);
+        sm_y[d] = (f16)(L > 0.0f ? O / L : 0.0f);
+    }
+    __syncthreads();
+    if (wave == 0) {
+        constexpr int VPL = D / 64;
+        float y[VPL];
+        f16 r[VPL];
+#pragma unroll
+        for (int j = 0; j < VPL; j++) y[j] = (float)sm_y[lane * VPL + j];
+        t4_rotate_row<D>(y, lane, tab + T4Tab<D>::v_s2, tab + T4Tab<D>::v_s1, r);
+        const int qh = h * G + row % G, qr = row / G;
+        f16* orow = out + ((int64_t)qh * Tq + qr) * D;
+#pragma unroll
+        for (int j = 0; j < VPL; j++) orow[lane * VPL + j] = r[j];
+    }
+    (void)NDG;
+}
+
+template <int D>
+static int launch_t4_merge_rotate(const float* po, const float2* pml, int nc, int R, int hkv, int G,
+                                  int Tq, const float* tab, f16* out, hipStream_t stream) {
+    QW_REQUIRE(nc >= 1 && nc <= 128, QW_ERR_INVALID_ARGUMENT, "merge: partial count out of range");
+    const dim3 grid(R, hkv), block(D * 4);
+    switch (merge_per(nc)) {
+        case 4:
+            hipLaunchKernelGGL((t4_merge_rotate_kernel<D, 4>), grid, block, 0, stream, po, pml, nc, 16, G,
+                               Tq, tab, out);
+            break;
+        case 8:
+            hipLaunchKernelGGL((t4_merge_rotate_kernel<D, 8>), grid, block, 0, stream, po, pml, nc, 16, G,
+                               Tq, tab, out);
+            break;
+        case 16:
+            hipLaunchKernelGGL((t4_merge_rotate_kernel<D, 16>), grid, block, 0, stream, po, pml, nc, 16,
+                               G, Tq, tab, out);
+            break;
+        default:  // nc <= 128
+            hipLaunchKernelGGL((t4_merge_rotate_kernel<D, 32>), grid, block, 0, stream, po, pml, nc, 16,
+                               G, Tq, tab, out);
+    }
+    QW_HIP_CHECK(hipGetLastError());
+    return QW_OK;
+}
+
+int launch_turbo4_decode(KVCache& cc, const f16* q, int G, int Tq, float scale, bool causal,
+                         const float* tab, f16* out, hipStream_t stream) {
     int nc = 0;
     float* po = nullptr;
     float2* pml = nullptr;
-    int rc = cc.D == 256 ? launch_decode_partials<4, 256, true>(cc, q_rot, G, Tq, cc.offset, scale,
-                                                                causal, &nc, &po, &pml, stream, cb)
-                         : launch_decode_partials<4, 128, true>(cc, q_rot, G, Tq, cc.offset, scale,
-                                                                causal, &nc, &po, &pml, stream, cb);
+    if (cc.D == 256) {
+        int rc = launch_decode_partials<4, 256, true>(cc, q, G, Tq, cc.offset, scale, causal, &nc,
+                                                      &po, &pml, stream, tab);
+        if (rc) return rc;
+        return launch_t4_merge_rotate<256>(po, pml, nc, G * Tq, cc.hkv, G, Tq, tab, out, stream);
+    }
+    int rc = launch_decode_partials<4, 128, true>(cc, q, G, Tq, cc.offset, scale, causal, &nc, &po,
+                                                  &pml, stream, tab);
     if (rc) return rc;
-    return launch_partial_merge(po, pml, nc, 16, 0, G * Tq, cc.hkv, cc.D, G, Tq, o_rot, stream);
+    return launch_t4_merge_rotate<128>(po, pml, nc, G * Tq, cc.hkv, G, Tq, tab, out, stream);
 }
 
 // The same merge for many rows (block kernels' key splits): one thread an

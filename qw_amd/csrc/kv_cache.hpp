@@ -169,11 +169,12 @@ int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float
 // Kernel launchers (attend_decode.hip, attend_block.hip).
 int launch_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float scale,
                      bool causal, void* out, hipStream_t stream);
-// Turbo4 caches, G * n_rows <= 16: the decode kernel reads the packed indices
-// in place and forms f16(centroid * rescale) as the fp16 expansion holds it;
-// q_rot / o_rot are in the rotated basis, cb the 16 fp32 centroids.
-int launch_turbo4_decode(KVCache& c, const f16* q_rot, int G, int n_rows, float scale,
-                         bool causal, const float* cb, f16* o_rot, hipStream_t stream);
+// Turbo4 caches, G * n_rows <= 16: the decode kernel rotates q into the K
+// basis, reads the packed indices in place and forms f16(centroid * rescale)
+// as the fp16 expansion holds it; the merge rotates the output back. tab: the
+// cache's device tables.
+int launch_turbo4_decode(KVCache& c, const f16* q, int G, int n_rows, float scale, bool causal,
+                         const float* tab, f16* out, hipStream_t stream);
 // G * n_rows > 16 query rows per KV head (verify blocks, prefill chunks).
 int launch_block_attention(KVCache& c, const f16* q, int G, int n_rows, float scale, bool causal,
                            f16* out, hipStream_t stream);

@@ -33,50 +33,12 @@
 
 #include "kv_cache.hpp"
 #include "rope.hpp"
+#include "turbo4_device.hpp"
 
 namespace qw {
 
 namespace {
 
-// Offsets into the device tables.
-template <int D>
-struct T4Tab {
-    static constexpr int v_s1 = 0, v_s2 = D, k_s1 = 2 * D, k_s2 = 3 * D;
-    static constexpr int cb = 4 * D, bnd = 4 * D + 16;
-    static constexpr int size = 4 * D + 32;
-};
-
-// The transform's scale as MLX forms it: 1 / sqrt(n) in double, cast to fp32.
-__host__ __device__ constexpr float wht_scale(int D) {
-    return D == 256 ? 0.0625f : (D == 128 ? 0.08838834764831845f : 0.0f);
-}
-
-// In-place fp32 Walsh-Hadamard transform of the wave's row (lane holds
-// coordinates lane * VPL .. lane * VPL + VPL - 1), unscaled.
-template <int D>
-__device__ __forceinline__ void wht_wave(float (&y)[D / 64], int lane) {
-    constexpr int VPL = D / 64;
-#pragma unroll
-    for (int s = 1; s < VPL; s <<= 1) {
-#pragma unroll
-        for (int j = 0; j < VPL; j++) {
-            if ((j & s) == 0) {
-                const float a = y[j], b = y[j + s];
-                y[j] = a + b;
-                y[j + s] = a - b;
-            }
-        }
-    }
-#pragma unroll
-    for (int ls = 1; ls < 64; ls <<= 1) {
-        const bool upper = (lane & ls) != 0;
-#pragma unroll
-        for (int j = 0; j < VPL; j++) {
-            const float p = __shfl_xor(y[j], ls);
-            y[j] = upper ? p - y[j] : y[j] + p;
-        }
-    }
-}
 
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
@@ -907,42 +869,13 @@ int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float
     const int qrows = n_q_heads * n_rows;
     const float* tab = c.t4_tables;
 #if QW_T4_FUSED_DECODE
-    if ((n_q_heads / c.hkv) * n_rows <= 16) {
-        // Up to 16 rows a KV head: the decode kernel reads the packed indices
-        // in place (the values the fp16 expansion would hold, the fp16 SDPA
-        // arithmetic on them) between the two rotations.
-        const size_t q_bytes = (size_t)qrows * D * sizeof(f16);
-        void* wbuf = nullptr;
-        if (int rc0 = t4_workspace(c.device, stream, 2 * q_bytes, &wbuf)) return rc0;
-        f16* q_rot = (f16*)wbuf;
-        f16* o_rot = (f16*)((char*)wbuf + q_bytes);
-        const dim3 rg((qrows + 3) / 4);
-        if (D == 256) {
-            using TT = T4Tab<256>;
-            hipLaunchKernelGGL(turbo4_rotate_kernel<256>, rg, dim3(256), 0, stream, (const f16*)q,
-                               q_rot, qrows, tab + TT::k_s1, tab + TT::k_s2);
-        } else {
-            using TT = T4Tab<128>;
-            hipLaunchKernelGGL(turbo4_rotate_kernel<128>, rg, dim3(256), 0, stream, (const f16*)q,
-                               q_rot, qrows, tab + TT::k_s1, tab + TT::k_s2);
-        }
-        QW_HIP_CHECK(hipGetLastError());
-        const float* cb = tab + (D == 256 ? T4Tab<256>::cb : T4Tab<128>::cb);
-        int rc = launch_turbo4_decode(c, q_rot, n_q_heads / c.hkv, n_rows, scale, causal, cb, o_rot,
-                                      stream);
-        if (rc) return rc;
-        if (D == 256) {
-            using TT = T4Tab<256>;
-            hipLaunchKernelGGL(turbo4_rotate_kernel<256>, rg, dim3(256), 0, stream, o_rot, (f16*)out,
-                               qrows, tab + TT::v_s2, tab + TT::v_s1);
-        } else {
-            using TT = T4Tab<128>;
-            hipLaunchKernelGGL(turbo4_rotate_kernel<128>, rg, dim3(256), 0, stream, o_rot, (f16*)out,
-                               qrows, tab + TT::v_s2, tab + TT::v_s1);
-        }
-        QW_HIP_CHECK(hipGetLastError());
-        return QW_OK;
-    }
+    if ((n_q_heads / c.hkv) * n_rows <= 16)
+        // Up to 16 rows a KV head: the decode kernel rotates q, reads the
+        // packed indices in place (the values the fp16 expansion would hold,
+        // the fp16 SDPA arithmetic on them) and its merge rotates the output
+        // back.
+        return launch_turbo4_decode(c, (const f16*)q, n_q_heads / c.hkv, n_rows, scale, causal, tab,
+                                    (f16*)out, stream);
 #endif
     const int capv = (T + 255) / 256 * 256;
     const size_t kv_bytes = (size_t)c.hkv * capv * D * sizeof(f16);
