@@ -101,6 +101,48 @@ def test_ragged_lists_skips_and_empty_rows(oracle_lib, D, G):
     assert np.all(out[:, 2] == 0)
 
 
+def prefill_lists(T0, L, seed, sinks=4, window=512, block=512, n_blocks=4):
+    """Lists of an L-row prefill chunk at positions T0 .. T0 + L - 1: the sinks,
+    the row's own trailing window (ending at its position) and n_blocks whole
+    512-key blocks drawn once for the chunk from below the first row's window
+    (the rows of a chunk pick mostly the same clusters). Width sinks + window +
+    n_blocks * block; every entry is visible to its row."""
+    r = rng(seed)
+    last = (T0 - window) // block - 1
+    blocks = np.sort(r.choice(np.arange(1, last + 1), n_blocks, replace=False))
+    exp = np.concatenate([np.arange(b * block, (b + 1) * block) for b in blocks])
+    lists = np.empty((L, sinks + window + exp.size), np.int32)
+    for row in range(L):
+        pos = T0 + row
+        lists[row] = np.concatenate([exp, np.arange(pos - window + 1, pos + 1), np.arange(sinks)])
+    return lists
+
+
+@pytest.mark.parametrize("L", [256, 24])
+def test_prefill_rows_vs_oracle(oracle_lib, L):
+    """K2 at prefill row counts: 256 rows x 4 KV heads take one pass (one
+    workgroup a row and head, mlx_cxx_dlsa_attention.cpp:379-418 switches at
+    L * Hkv >= 160), 24 rows split each list; checked against the oracle on a
+    spread of rows (first, last, and between)."""
+    import qw_amd
+
+    T0, H, G, D = 8192, 4, 6, 256
+    T = T0 + L
+    r = rng(9000 + L)
+    k = r.standard_normal((H, T, D)).astype(np.float16)
+    v = r.standard_normal((H, T, D)).astype(np.float16)
+    q = r.standard_normal((H * G, L, D)).astype(np.float16)
+    lists = prefill_lists(T0, L, 77 + L)
+    lengths = np.full(L, lists.shape[1], np.int32)
+    out = _np(qw_amd.sparse_attention(_gpu(q), _gpu(k), _gpu(v), _gpu(lists), _gpu(lengths),
+                                      D ** -0.5))[0]
+    sel = np.unique(np.array([0, 1, L // 3, L // 2, L - 2, L - 1]))
+    ref = oracle_lib.dlsa_attention(np.ascontiguousarray(q[:, sel]), k, v,
+                                    np.ascontiguousarray(lists[sel]), lengths[sel], D ** -0.5)
+    assert np.isfinite(out).all()
+    assert_close(out[:, sel], ref, f"prefill rows L={L}")
+
+
 def test_workspace_per_stream_growth():
     """Split-K partials live in a workspace per (device, stream): calls
     alternating on two streams, with a growth of one stream's workspace in
