@@ -51,8 +51,15 @@ struct BlockArgs {
     float* part_o;      // [hkv][n_split][PR][D], rows from prow0
     float2* part_ml;    // [hkv][n_split][PR]
     int cap, T, Tq, G, R, causal, n_split, tiles_per_split;
-    int qt0;            // first query tile of this launch
+    int qt0;            // first query tile of this launch (of its split segment)
     int prow0, PR;      // first row and row count of this launch's partials
+    // n_main > 0: a one-dimensional grid whose first n_main workgroups are
+    // unsplit query tiles 0 .. n_main / hkv - 1 (unit u: tile u / hkv, head
+    // u % hkv, all main_tiles key tiles, rows written directly) and whose
+    // others are the split segment described by the fields above (unit t:
+    // split t % n_split, head (t / n_split) % hkv, tile qt0 + t / (n_split hkv)).
+    // The dispatcher starts the split workgroups as the first ones finish.
+    int n_main, main_tiles, hkv;
     float scale_h;      // f16(scale) as float
     uint32_t code_off2; // magic offset pair of the separately rounded dequant
 };
@@ -149,7 +156,30 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     constexpr int PER = KT * TPR / (64 * NW);  // slices of each kind a thread owns
     static_assert(PER * 64 * NW == KT * TPR && (KT / 8) * TPB == KT * TPR, "slices a thread");
 
-    const int sp = blockIdx.x, qt = blockIdx.y + a.qt0, h = blockIdx.z;
+    int sp, qt, h, n_split, tiles_per_split;
+    if (a.n_main > 0) {
+        const int lin = blockIdx.x;
+        if (lin < a.n_main) {
+            sp = 0;
+            qt = lin / a.hkv;
+            h = lin % a.hkv;
+            n_split = 1;
+            tiles_per_split = a.main_tiles;
+        } else {
+            const int t = lin - a.n_main;
+            sp = t % a.n_split;
+            h = (t / a.n_split) % a.hkv;
+            qt = a.qt0 + t / (a.n_split * a.hkv);
+            n_split = a.n_split;
+            tiles_per_split = a.tiles_per_split;
+        }
+    } else {
+        sp = blockIdx.x;
+        qt = blockIdx.y + a.qt0;
+        h = blockIdx.z;
+        n_split = a.n_split;
+        tiles_per_split = a.tiles_per_split;
+    }
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: wave-uniform branches
     const int r16 = lane & 15, g = lane >> 4;
@@ -162,8 +192,8 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     const int row_last = min(a.R, row0 + WROWS * NW) - 1;
     const int wg_lim = a.causal ? a.T - a.Tq + row_last / a.G : a.T - 1;
     const int n_tiles = (a.T + KT - 1) / KT;
-    const int t0 = sp * a.tiles_per_split;
-    const int t1 = min(min(n_tiles, t0 + a.tiles_per_split), wg_lim / KT + 1);
+    const int t0 = sp * tiles_per_split;
+    const int t1 = min(min(n_tiles, t0 + tiles_per_split), wg_lim / KT + 1);
 
     // ---- the wave's RT x 16 query rows as the B operand of S^T = K . Q'^T
     // (col = query row r16 of row tile rt, k-group g = dims 32m + 8g .. +7 of
@@ -523,7 +553,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         float lsum = l_run[rt];
         lsum = wave_sum_g(lsum);
         const int rbase = wrow0 + 16 * rt + 4 * g;  // rows of acc_o[rt][.][i] are rbase + i
-        if (a.n_split == 1) {
+        if (n_split == 1) {
             float inv[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -540,7 +570,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
                     orow[v_logical_dim(16 * mm + r16, D, BITS)] = (f16)(acc_o[rt][mm][i] * inv[i]);
             }
         } else {
-            const int64_t pbase = ((int64_t)h * a.n_split + sp) * a.PR - a.prow0;
+            const int64_t pbase = ((int64_t)h * n_split + sp) * a.PR - a.prow0;
             const int rho = wrow0 + 16 * rt + r16;
             if (g == 0 && rho < a.R) a.part_ml[pbase + rho] = float2{m_run[rt], lsum};
 #pragma unroll
@@ -584,8 +614,10 @@ static int launch_block_rt(KVCache& cc, BlockArgs& a, int n_qt, hipStream_t stre
     const size_t shmem = (size_t)2 * BlockShape<D>::BUF;
     int rc = ensure_dynamic_lds((const void*)attend_block_kernel<BITS, D, RT>, shmem);
     if (rc) return rc;
-    hipLaunchKernelGGL((attend_block_kernel<BITS, D, RT>), dim3(a.n_split, n_qt, cc.hkv),
-                       dim3(64 * kBlockWaves), shmem, stream, a);
+    const dim3 grid = a.n_main > 0 ? dim3(a.n_main + n_qt * cc.hkv * a.n_split)
+                                   : dim3(a.n_split, n_qt, cc.hkv);
+    hipLaunchKernelGGL((attend_block_kernel<BITS, D, RT>), grid, dim3(64 * kBlockWaves), shmem,
+                       stream, a);
     QW_HIP_CHECK(hipGetLastError());
     return QW_OK;
 }
@@ -632,6 +664,12 @@ static int launch_one(KVCache& cc, BlockArgs a, int rt, int n_qt, hipStream_t st
     return rc;
 }
 
+// 1: unsplit and split query tiles of a call in one launch (see
+// launch_block_bits); 0: two launches.
+#ifndef QW_BLOCK_ONE_LAUNCH
+#define QW_BLOCK_ONE_LAUNCH 1
+#endif
+
 // Splits `n_tiles` key tiles into about `want` parts of at least 4 tiles.
 static void split_keys(int n_tiles, int want, int* n_split, int* tps) {
     int ns = std::max(1, std::min({want, (n_tiles + 3) / 4, 256}));
@@ -672,27 +710,35 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     a.qt0 = 0;
     a.prow0 = 0;
     a.PR = R;
+    a.n_main = 0;
+    a.main_tiles = n_tiles;
+    a.hkv = cc.hkv;
 
     // Plan (one workgroup a CU, 256 CUs): query tiles that fill whole rounds
     // run unsplit and write their rows; the rest (all of them when fewer than
     // 256 units) split the keys so that about 256 workgroups run, and go
     // through fp32 partials and the merge kernel.
+    // With both parts, one launch: the unsplit tiles first, the split ones
+    // behind them, so a CU whose unsplit tile ends early starts a split one
+    // (the unsplit tiles' lengths differ with the causal cut) and no kernel
+    // boundary separates them.
     int q_main = 0;
     if (units >= 256 && 256 % cc.hkv == 0) q_main = (units / 256) * (256 / cc.hkv);
     q_main = std::min(q_main, n_qt);
+    const int q_tail = n_qt - q_main;
     int rc;
-    if (q_main > 0) {
+    if (q_main > 0 && (q_tail == 0 || !QW_BLOCK_ONE_LAUNCH)) {
         BlockArgs m = a;
         m.n_split = 1;
         m.tiles_per_split = n_tiles;
         rc = launch_one<BITS, D>(cc, m, rt, q_main, stream);
         if (rc) return rc;
     }
-    const int q_tail = n_qt - q_main;
     if (q_tail == 0) return QW_OK;
     int n_split, tps;
     split_keys(n_tiles, std::max(1, 256 / (q_tail * cc.hkv)), &n_split, &tps);
     BlockArgs t = a;
+    if (q_main > 0 && QW_BLOCK_ONE_LAUNCH) t.n_main = q_main * cc.hkv;
     t.qt0 = q_main;
     t.n_split = n_split;
     t.tiles_per_split = tps;
