@@ -37,6 +37,7 @@
 
 #include "dequant.hpp"
 #include "kv_cache.hpp"
+#include "turbo4_device.hpp"
 
 namespace qw {
 
@@ -60,6 +61,8 @@ struct BlockArgs {
     // split t % n_split, head (t / n_split) % hkv, tile qt0 + t / (n_split hkv)).
     // The dispatcher starts the split workgroups as the first ones finish.
     int n_main, main_tiles, hkv;
+    const float* t4_tab;  // Turbo4 caches: the device tables (signs, centroids: T4Tab<D>)
+    float t4_post;        // Turbo4 fused pass: scale * log2(e) in fp32
     float scale_h;      // f16(scale) as float
     uint32_t code_off2; // magic offset pair of the separately rounded dequant
 };
@@ -144,14 +147,28 @@ __device__ __forceinline__ float wave_sum_g(float v) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-template <int BITS, int D, int RT, bool FAST>
+// T4M: 0 the affine / Int8 / fp16 caches; 1 and 2 a Turbo4 cache (BITS = 4:
+// K rows of D/2 bytes of centroid indices, row-major like the 4-bit K plane,
+// one side word a row; V row-major too). The store forms f16(centroid *
+// rescale) as the fp16 expansion holds it (centroid pairs from an LDS table,
+// one 8-byte read a byte of codes) and places V in the fp16 cache's slot
+// order. T4M = 1 keeps the fp16 SDPA arithmetic (the reference's
+// dequantize-then-SDPA route); T4M = 2 is the reference's fused verify pass
+// (turbo4_attention.cpp:45-197): q arrives rotated and scaled by scale *
+// log2(e), scores stay fp32 in the log2 domain, P enters P.V as an fp16 high
+// part plus an fp16 remainder (fp32-exact products), and the partial maxima are
+// stored in natural units for the shared merge.
+template <int BITS, int D, int RT, bool FAST, int T4M = 0>
 __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     using S = BlockShape<D>;
     constexpr int KT = S::KT, NSUB = S::NSUB, NM = S::NM, NT = S::NT, NG = S::NG;
     constexpr int TPR = S::TPR, LTPR = S::LTPR, TPB = S::TPB, BUF = S::BUF, KBUF = S::KBUF;
     constexpr int VROW = S::VROW;
     constexpr int NW = kBlockWaves;
-    constexpr bool AFF = BITS != 16;
+    constexpr bool T4 = T4M != 0, FUSED = T4M == 2;
+    static_assert(!T4 || BITS == 4, "Turbo4 indices are 4-bit");
+    constexpr bool AFF = BITS != 16 && !T4;
+    constexpr int VB = T4 ? 16 : BITS;  // the V slot order in LDS (and of the partial rows)
     constexpr int KU = BITS / 4;  // u32x4 loads a 32-dim K slice / a 4-slot V slice
     constexpr int PER = KT * TPR / (64 * NW);  // slices of each kind a thread owns
     static_assert(PER * 64 * NW == KT * TPR && (KT / 8) * TPB == KT * TPR, "slices a thread");
@@ -208,20 +225,65 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     int lim[RT];
     bool row_ok[RT];
     half8 qb[RT][NM];
+    // Turbo4: the workgroup's rows are rotated into the K basis (the rotation
+    // kernels' arithmetic; wave w takes rows w, w + NW, ..., four at a time
+    // with their loads issued first) and staged as fp16 in the second tile
+    // buffer, which the prologue leaves alone; the centroid-pair table goes
+    // behind the two buffers. One barrier covers both.
+    f16* const sq = (f16*)(lds + BUF);
+    if constexpr (T4) {
+        static_assert(NW * WROWS * D * sizeof(f16) <= BUF, "staged q rows exceed a tile buffer");
+        float2* const cp = (float2*)(lds + 2 * BUF);
+        const float* cb = a.t4_tab + T4Tab<D>::cb;
+        for (int bb = tid; bb < 256; bb += 64 * NW) cp[bb] = float2{cb[bb & 15], cb[bb >> 4]};
+        constexpr int VPL = D / 64, NB = 4;
+        using HV = std::conditional_t<VPL == 4, half4v, half2v>;
+        float si[VPL], so[VPL];
+        t4_lane_signs<D>(a.t4_tab + T4Tab<D>::k_s1, lane, si);
+        t4_lane_signs<D>(a.t4_tab + T4Tab<D>::k_s2, lane, so);
+        for (int k0 = 0; k0 < WROWS; k0 += NB) {
+            if (row0 + wave + NW * k0 >= a.R) break;  // wave-uniform
+            float y[NB][VPL];
+#pragma unroll
+            for (int kk = 0; kk < NB; kk++) {
+                const int rho = min(row0 + wave + NW * (k0 + kk), a.R - 1);
+                const f16* qrow = a.q + ((int64_t)(h * a.G + rho % a.G) * a.Tq + rho / a.G) * D;
+                const HV w = *(const HV*)(qrow + lane * VPL);
+#pragma unroll
+                for (int jj = 0; jj < VPL; jj++) y[kk][jj] = (float)w[jj];
+            }
+#pragma unroll
+            for (int kk = 0; kk < NB; kk++) {
+                f16 o[VPL];
+                if constexpr (FUSED)
+                    t4_rotate_row_scaled<D>(y[kk], lane, si, so, a.t4_post, o);
+                else
+                    t4_rotate_row<D>(y[kk], lane, si, so, o);
+                const int lr = wave + NW * (k0 + kk);
+                HV ov;
+#pragma unroll
+                for (int jj = 0; jj < VPL; jj++) ov[jj] = o[jj];
+                if (row0 + lr < a.R) *(HV*)(sq + lr * D + lane * VPL) = ov;
+            }
+        }
+        __syncthreads();
+    }
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
         const int rho = wrow0 + 16 * rt + r16;
         row_ok[rt] = rho < a.R;
         lim[rt] = row_ok[rt] ? (a.causal ? a.T - a.Tq + rho / a.G : a.T - 1) : -1;
         const int rr = row_ok[rt] ? rho : 0;
-        const f16* qrow = a.q + ((int64_t)(h * a.G + rr % a.G) * a.Tq + rr / a.G) * D;
-        const f16 sc = row_ok[rt] ? (f16)a.scale_h : (f16)0.0f;
+        // (Turbo4 padding rows read the workgroup's first staged row; their scale is 0)
+        const f16* qrow = T4 ? sq + (row_ok[rt] ? WROWS * wave + 16 * rt + r16 : 0) * D
+                             : a.q + ((int64_t)(h * a.G + rr % a.G) * a.Tq + rr / a.G) * D;
+        const f16 sc = row_ok[rt] ? (FUSED ? (f16)1.0f : (f16)a.scale_h) : (f16)0.0f;
         const half2v sc2 = {sc, sc};
 #pragma unroll
         for (int m = 0; m < NM; m++) {
             const u32x4 w = *(const u32x4*)(qrow + 32 * m + 8 * g);
             u32x4 o;
-            if constexpr (BITS == 4) {
+            if constexpr (BITS == 4 && !T4) {
                 // 4-bit K rows sit in LDS as dim pairs (0,4),(1,5),(2,6),(3,7).
                 o.x = __builtin_amdgcn_perm(w.z, w.x, 0x05040100u);
                 o.y = __builtin_amdgcn_perm(w.z, w.x, 0x07060302u);
@@ -251,6 +313,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         uint32_t kp[PER];
         u32x4 vc[PER][KU];
         u32x4 vp[PER][2];
+        uint32_t vt[PER][T4 ? 8 : 1];  // Turbo4: keys 8 vb + i, the 2 bytes of dims 4 vj .. +3
     };
     int kk[PER], q32[PER], vb[PER], vj[PER], vgrp[PER];
 #pragma unroll
@@ -260,7 +323,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         kk[j] = (tt & 15) | ((tt >> (4 + LTPR)) << 4);
         vb[j] = tt / TPB;
         vj[j] = tt % TPB;
-        vgrp[j] = v_logical_dim(4 * vj[j], D, BITS) / 64;
+        vgrp[j] = v_logical_dim(4 * vj[j], D, VB) / 64;
     }
     const int64_t krow_words = (int64_t)D * BITS / 32;
     const int64_t vblk_words = (int64_t)D * BITS / 4;
@@ -274,10 +337,12 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     for (int j = 0; j < PER; j++) {
         const int64_t row = (int64_t)h * a.cap + kk[j];
         ksrc0[j] = (const u32x4*)(a.k_data + row * krow_words) + KU * q32[j];
-        kpsrc0[j] = a.k_params + row * NG + k_param_slot(q32[j] >> 1, NG);
+        kpsrc0[j] = T4 ? a.k_params + row : a.k_params + row * NG + k_param_slot(q32[j] >> 1, NG);
         const int64_t blk = (int64_t)h * (a.cap / 8) + vb[j];
-        vsrc0[j] = (const u32x4*)(a.v_data + blk * vblk_words) + KU * vj[j];
-        vpsrc0[j] = (const u32x4*)(a.v_params + (blk * NG + vgrp[j]) * 8);
+        vsrc0[j] = T4 ? (const u32x4*)((const uint16_t*)a.v_data + (8 * blk) * (D / 4) + vj[j])
+                      : (const u32x4*)(a.v_data + blk * vblk_words) + KU * vj[j];
+        vpsrc0[j] = T4 ? (const u32x4*)(a.v_params + 8 * blk)
+                       : (const u32x4*)(a.v_params + (blk * NG + vgrp[j]) * 8);
     }
     auto load = [&](Stage& st, int t) {
         const int64_t t_rows = (int64_t)t * KT, t_blks = (int64_t)t * (KT / 8);
@@ -287,9 +352,20 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
 #pragma unroll
             for (int u = 0; u < KU; u++) st.kc[j][u] = ksrc[u];
             if constexpr (AFF) st.kp[j] = kpsrc0[j][t_rows * NG];
-            const u32x4* vsrc = vsrc0[j] + t_blks * (vblk_words / 4);
+            if constexpr (T4) {
+                st.kp[j] = kpsrc0[j][t_rows];
+                // V: 2 bytes of each of the block's 8 rows (row stride D/4 halfwords)
+                const uint16_t* vsrc = (const uint16_t*)vsrc0[j] + t_rows * (D / 4);
 #pragma unroll
-            for (int u = 0; u < KU; u++) st.vc[j][u] = vsrc[u];
+                for (int i = 0; i < 8; i++) st.vt[j][i] = vsrc[i * (D / 4)];
+                const u32x4* psrc = vpsrc0[j] + t_blks * 2;
+                st.vp[j][0] = psrc[0];
+                st.vp[j][1] = psrc[1];
+            } else {
+                const u32x4* vsrc = vsrc0[j] + t_blks * (vblk_words / 4);
+#pragma unroll
+                for (int u = 0; u < KU; u++) st.vc[j][u] = vsrc[u];
+            }
             if constexpr (AFF) {
                 const u32x4* psrc = vpsrc0[j] + t_blks * (NG * 2);
                 st.vp[j][0] = psrc[0];
@@ -306,6 +382,39 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         for (int j = 0; j < PER; j++) {
             // chunks 4 q32 + w of key kk: KT chunks apart
             half8* krow = sK8 + kaddr<KT>(kk[j], 4 * q32[j]);
+            if constexpr (T4) {
+                const float2* cp = (const float2*)(lds + 2 * BUF);
+                const float kr = (float)h2(st.kp[j]).x;
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    half8 y;
+#pragma unroll
+                    for (int n = 0; n < 4; n++) {
+                        const float2 c = cp[(st.kc[j][0][w] >> (8 * n)) & 0xFFu];
+                        y[2 * n] = t4_f16_product(c.x, kr);
+                        y[2 * n + 1] = t4_f16_product(c.y, kr);
+                    }
+                    krow[w * KT] = y;
+                }
+                // V: key i of the block, dims 4 vj + e at the fp16 layout's slot
+                half8 yv[4];
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const float vr = (float)h2(st.vp[j][i / 4][i % 4]).y;
+                    const float2 c0 = cp[st.vt[j][i] & 0xFFu], c1 = cp[(st.vt[j][i] >> 8) & 0xFFu];
+                    yv[0][i] = t4_f16_product(c0.x, vr);
+                    yv[1][i] = t4_f16_product(c0.y, vr);
+                    yv[2][i] = t4_f16_product(c1.x, vr);
+                    yv[3][i] = t4_f16_product(c1.y, vr);
+                }
+                half8* vblk = sV8 + vb[j] * VROW;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int sl = v_phys_dim(4 * vj[j] + e, D, 16);
+                    vblk[sl + (sl >> 4)] = yv[e];
+                }
+                continue;
+            }
             if constexpr (BITS == 4) {
                 const half2v sb = h2(st.kp[j]);
                 const half2v s = {sb.x, sb.x}, bb = {sb.y, sb.y};
@@ -405,6 +514,60 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         // only for tiles some row of the wave cannot fully see (a scalar
         // branch around the compares: the common case carries none).
         const bool mask = kt0 + KT - 1 > wave_first_lim;
+        half8 popl[FUSED ? NSUB : 1][RT];  // fused pass: the remainders p - f16(p)
+        auto softmax_fused = [&]() {
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) {
+                // fp32 scores in the log2 domain (q carries scale * log2 e)
+                float sf[NSUB][8];
+#pragma unroll
+                for (int u = 0; u < NSUB; u++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) sf[u][e] = acc[u][e >> 2][rt][e & 3];
+                if (mask) {
+#pragma unroll
+                    for (int u = 0; u < NSUB; u++)
+#pragma unroll
+                        for (int e = 0; e < 8; e++) {
+                            const int key = kt0 + 32 * u + 8 * g + (e & 3) + 4 * (e >> 2);
+                            if (key > lim[rt]) sf[u][e] = -INFINITY;
+                        }
+                }
+                float mx_lane = sf[0][0];
+#pragma unroll
+                for (int u = 0; u < NSUB; u++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) mx_lane = fmaxf(mx_lane, sf[u][e]);
+                // lazy reference in log2 units (p <= 2^5.5)
+                if (__any(mx_lane > m_run[rt] + 5.5f)) {
+                    const float m_new = fmaxf(m_run[rt], wave_max_g(mx_lane));
+                    if (__any(m_run[rt] != -INFINITY)) {
+                        const float alpha =
+                            m_run[rt] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run[rt] - m_new);
+                        l_run[rt] *= alpha;
+                        float f[4];
+#pragma unroll
+                        for (int i = 0; i < 4; i++) f[i] = __shfl(alpha, 4 * g + i);
+#pragma unroll
+                        for (int mm = 0; mm < NT; mm++)
+#pragma unroll
+                            for (int i = 0; i < 4; i++) acc_o[rt][mm][i] *= f[i];
+                    }
+                    m_run[rt] = m_new;
+                }
+                const float mref = m_run[rt] == -INFINITY ? 0.0f : m_run[rt];
+#pragma unroll
+                for (int u = 0; u < NSUB; u++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        const float p = __builtin_amdgcn_exp2f(sf[u][e] - mref);
+                        l_run[rt] += p;
+                        const f16 ph = (f16)p;
+                        pop[u][rt][e] = ph;
+                        if constexpr (FUSED) popl[u][rt][e] = (f16)(p - (float)ph);
+                    }
+            }
+        };
         auto softmax = [&]() {
 #pragma unroll
             for (int rt = 0; rt < RT; rt++) {
@@ -472,7 +635,10 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
                     }
             }
         };
-        softmax();
+        if constexpr (FUSED)
+            softmax_fused();
+        else
+            softmax();
         // O += P . V: B = slot 16mm + r16 (column r16 of output tile mm) of
         // V block 4u + g, i.e. keys 32u + 8g .. +7.
 #pragma unroll
@@ -482,9 +648,13 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
             for (int mm = 0; mm < NT; mm++) {
                 const half8 vv = vb8[17 * mm];  // slot 16mm + r16
 #pragma unroll
-                for (int rt = 0; rt < RT; rt++)
+                for (int rt = 0; rt < RT; rt++) {
                     acc_o[rt][mm] =
                         __builtin_amdgcn_mfma_f32_16x16x32_f16(pop[u][rt], vv, acc_o[rt][mm], 0, 0, 0);
+                    if constexpr (FUSED)
+                        acc_o[rt][mm] =
+                            __builtin_amdgcn_mfma_f32_16x16x32_f16(popl[u][rt], vv, acc_o[rt][mm], 0, 0, 0);
+                }
             }
         }
 #if QW_BLOCK_SCHED_PV
@@ -564,15 +734,18 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
             for (int i = 0; i < 4; i++) {
                 const int row = rbase + i;
                 if (row >= a.R) continue;
-                f16* orow = a.out + ((int64_t)(h * a.G + row % a.G) * a.Tq + row / a.G) * D;
+                const int64_t obase = ((int64_t)(h * a.G + row % a.G) * a.Tq + row / a.G) * D;
 #pragma unroll
-                for (int mm = 0; mm < NT; mm++)
-                    orow[v_logical_dim(16 * mm + r16, D, BITS)] = (f16)(acc_o[rt][mm][i] * inv[i]);
+                for (int mm = 0; mm < NT; mm++) {
+                    const int d = v_logical_dim(16 * mm + r16, D, VB);
+                    a.out[obase + d] = (f16)(acc_o[rt][mm][i] * inv[i]);
+                }
             }
         } else {
             const int64_t pbase = ((int64_t)h * n_split + sp) * a.PR - a.prow0;
             const int rho = wrow0 + 16 * rt + r16;
-            if (g == 0 && rho < a.R) a.part_ml[pbase + rho] = float2{m_run[rt], lsum};
+            // (the fused pass's maxima are in log2 units; the merge takes natural ones)
+            if (g == 0 && rho < a.R) a.part_ml[pbase + rho] = float2{FUSED ? m_run[rt] * kLn2 : m_run[rt], lsum};
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int row = rbase + i;
@@ -589,7 +762,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     }
 }
 
-template <int BITS, int D, int RT>
+template <int BITS, int D, int RT, int T4M = 0>
 __global__ __launch_bounds__(64 * kBlockWaves, 1) void attend_block_kernel(BlockArgs a) {
     // two buffers, each a K and a V tile of KT keys in fp16 (~130 KB)
     extern __shared__ __attribute__((aligned(16))) char lds_buf[];
@@ -598,25 +771,27 @@ __global__ __launch_bounds__(64 * kBlockWaves, 1) void attend_block_kernel(Block
     // workgroup's share with the separately rounded dequant (same threads,
     // same output elements, so the second pass's writes replace the first's).
     // A null flag (Int8 caches) takes the separately rounded dequant directly.
-    if (BITS == 16 || a.fast_flag != nullptr) {
+    // Turbo4 caches have one expansion (a null flag).
+    if (T4M == 0 && (BITS == 16 || a.fast_flag != nullptr)) {
         block_body<BITS, D, RT, true>(a, lds_buf);
         if (BITS != 16 && *a.fast_flag == 0) {
             __syncthreads();
             block_body<BITS, D, RT, false>(a, lds_buf);
         }
     } else {
-        block_body<BITS, D, RT, false>(a, lds_buf);
+        block_body<BITS, D, RT, false, T4M>(a, lds_buf);
     }
 }
 
-template <int BITS, int D, int RT>
+template <int BITS, int D, int RT, int T4M>
 static int launch_block_rt(KVCache& cc, BlockArgs& a, int n_qt, hipStream_t stream) {
-    const size_t shmem = (size_t)2 * BlockShape<D>::BUF;
-    int rc = ensure_dynamic_lds((const void*)attend_block_kernel<BITS, D, RT>, shmem);
+    // two tile buffers (+ the Turbo4 centroid-pair table)
+    const size_t shmem = (size_t)2 * BlockShape<D>::BUF + (T4M ? 256 * sizeof(float2) : 0);
+    int rc = ensure_dynamic_lds((const void*)attend_block_kernel<BITS, D, RT, T4M>, shmem);
     if (rc) return rc;
     const dim3 grid = a.n_main > 0 ? dim3(a.n_main + n_qt * cc.hkv * a.n_split)
                                    : dim3(a.n_split, n_qt, cc.hkv);
-    hipLaunchKernelGGL((attend_block_kernel<BITS, D, RT>), grid, dim3(64 * kBlockWaves), shmem,
+    hipLaunchKernelGGL((attend_block_kernel<BITS, D, RT, T4M>), grid, dim3(64 * kBlockWaves), shmem,
                        stream, a);
     QW_HIP_CHECK(hipGetLastError());
     return QW_OK;
@@ -651,16 +826,16 @@ static int pick_rt(int R, int hkv) {
     return best;
 }
 
-template <int BITS, int D>
+template <int BITS, int D, int T4M>
 static int launch_one(KVCache& cc, BlockArgs a, int rt, int n_qt, hipStream_t stream) {
     int rc = QW_OK;
     if constexpr (QW_BLOCK_MAX_RT >= 3 || QW_BLOCK_RT == 3) {
-        if (rt == 3) rc = launch_block_rt<BITS, D, 3>(cc, a, n_qt, stream);
+        if (rt == 3) rc = launch_block_rt<BITS, D, 3, T4M>(cc, a, n_qt, stream);
     }
     if constexpr (QW_BLOCK_MAX_RT >= 2 || QW_BLOCK_RT == 2) {
-        if (rt == 2) rc = launch_block_rt<BITS, D, 2>(cc, a, n_qt, stream);
+        if (rt == 2) rc = launch_block_rt<BITS, D, 2, T4M>(cc, a, n_qt, stream);
     }
-    if (rt == 1) rc = launch_block_rt<BITS, D, 1>(cc, a, n_qt, stream);
+    if (rt == 1) rc = launch_block_rt<BITS, D, 1, T4M>(cc, a, n_qt, stream);
     return rc;
 }
 
@@ -677,9 +852,9 @@ static void split_keys(int n_tiles, int want, int* n_split, int* tps) {
     *n_split = (n_tiles + *tps - 1) / *tps;
 }
 
-template <int BITS, int D>
+template <int BITS, int D, int T4M = 0>
 static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float scale, bool causal,
-                             f16* out, hipStream_t stream) {
+                             f16* out, hipStream_t stream, const float* t4_tab = nullptr) {
     using S = BlockShape<D>;
     const int T = cc.offset;
     const int R = G * Tq;
@@ -694,9 +869,11 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     a.k_params = cc.k_params;
     a.v_data = (const uint32_t*)cc.v_data;
     a.v_params = cc.v_params;
-    a.fast_flag = cc.int8() ? nullptr : cc.fast_flag;  // null: always separately rounded
+    a.fast_flag = cc.int8() || T4M ? nullptr : cc.fast_flag;  // null: always separately rounded
     a.q = q;
     a.out = out;
+    a.t4_tab = t4_tab;
+    a.t4_post = scale * 1.4426950408889634f;
     a.part_o = nullptr;
     a.part_ml = nullptr;
     a.cap = cc.cap;
@@ -722,8 +899,9 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     // behind them, so a CU whose unsplit tile ends early starts a split one
     // (the unsplit tiles' lengths differ with the causal cut) and no kernel
     // boundary separates them.
+    // The Turbo4 fused pass splits every row (its merge rotates them back).
     int q_main = 0;
-    if (units >= 256 && 256 % cc.hkv == 0) q_main = (units / 256) * (256 / cc.hkv);
+    if (units >= 256 && 256 % cc.hkv == 0 && T4M != 2) q_main = (units / 256) * (256 / cc.hkv);
     q_main = std::min(q_main, n_qt);
     const int q_tail = n_qt - q_main;
     int rc;
@@ -731,12 +909,15 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
         BlockArgs m = a;
         m.n_split = 1;
         m.tiles_per_split = n_tiles;
-        rc = launch_one<BITS, D>(cc, m, rt, q_main, stream);
+        rc = launch_one<BITS, D, T4M>(cc, m, rt, q_main, stream);
         if (rc) return rc;
     }
     if (q_tail == 0) return QW_OK;
     int n_split, tps;
-    split_keys(n_tiles, std::max(1, 256 / (q_tail * cc.hkv)), &n_split, &tps);
+    const int want = std::max(1, 256 / (q_tail * cc.hkv));
+    split_keys(n_tiles, T4M == 2 ? std::min(std::max(want, 2), 128) : want, &n_split, &tps);
+    QW_REQUIRE(T4M != 2 || n_split > 1, QW_ERR_INVALID_ARGUMENT,
+               "block attention: fused Turbo4 pass needs at least 5 key tiles");
     BlockArgs t = a;
     if (q_main > 0 && QW_BLOCK_ONE_LAUNCH) t.n_main = q_main * cc.hkv;
     t.qt0 = q_main;
@@ -752,12 +933,26 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
         t.part_o = (float*)cc.ws_ptr;
         t.part_ml = (float2*)((char*)cc.ws_ptr + o_bytes);
     }
-    rc = launch_one<BITS, D>(cc, t, rt, q_tail, stream);
+    rc = launch_one<BITS, D, T4M>(cc, t, rt, q_tail, stream);
     if (rc) return rc;
+    if (n_split > 1 && T4M == 2)
+        return launch_t4_merge_rotate(t.part_o, t.part_ml, n_split, t.PR, R, cc.hkv, D, G, Tq, 16,
+                                      true, t4_tab, out, stream);
     if (n_split > 1)
         return launch_partial_merge(t.part_o, t.part_ml, n_split, t.PR, t.prow0, t.PR, cc.hkv, D,
-                                    G, Tq, out, stream, BITS);
+                                    G, Tq, out, stream, T4M ? 16 : BITS);
     return QW_OK;
+}
+
+int launch_block_attention_t4(KVCache& cc, const f16* q, int G, int n_rows, float scale,
+                              bool causal, bool fused, const float* tab, f16* out,
+                              hipStream_t stream) {
+    QW_REQUIRE(cc.turbo4() && cc.bits == 4, QW_ERR_INVALID_ARGUMENT, "block attention: not Turbo4");
+    if (cc.D == 256)
+        return fused ? launch_block_bits<4, 256, 2>(cc, q, G, n_rows, scale, causal, out, stream, tab)
+                     : launch_block_bits<4, 256, 1>(cc, q, G, n_rows, scale, causal, out, stream, tab);
+    return fused ? launch_block_bits<4, 128, 2>(cc, q, G, n_rows, scale, causal, out, stream, tab)
+                 : launch_block_bits<4, 128, 1>(cc, q, G, n_rows, scale, causal, out, stream, tab);
 }
 
 int launch_block_attention(KVCache& cc, const f16* q, int G, int n_rows, float scale, bool causal,

@@ -96,20 +96,15 @@ constexpr int decode_stages() {
 // the low nibble of b, centroid of its high nibble)) turns one byte of codes
 // into two centroids with one 8-byte read (measured ~1.9x the throughput of a
 // ds_bpermute per element); the expansion f16(centroid * rescale) rounds the
-// product to fp32 first, as the expansion kernel forms it.
-__device__ __forceinline__ f16 t4_product(float c, float r) {
-    float p = c * r;
-    asm("" : "+v"(p));
-    return (f16)p;
-}
+// product to fp32 first, as the expansion kernel forms it (t4_f16_product).
 // 8 consecutive dims (the word's nibbles, LSB first) of one row
 __device__ __forceinline__ half8 t4_expand8(uint32_t w, float r, const float2* pt) {
     half8 y;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         const float2 c = pt[(w >> (8 * k)) & 0xFFu];
-        y[2 * k] = t4_product(c.x, r);
-        y[2 * k + 1] = t4_product(c.y, r);
+        y[2 * k] = t4_f16_product(c.x, r);
+        y[2 * k + 1] = t4_f16_product(c.y, r);
     }
     return y;
 }
@@ -457,8 +452,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
                 for (int j = 0; j < 8; j++) {
                     const uint32_t w = D == 256 ? st.vc[j / 2][2 * (j % 2) + e / 4] : st.vc[j / 4][j % 4];
                     const float2 c = sm_t4[(w >> (8 * (e % 4))) & 0xFFu];
-                    b0[j] = t4_product(c.x, vr[j]);
-                    b1[j] = t4_product(c.y, vr[j]);
+                    b0[j] = t4_f16_product(c.x, vr[j]);
+                    b1[j] = t4_f16_product(c.y, vr[j]);
                 }
                 acc_o[2 * e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop, b0, acc_o[2 * e], 0, 0, 0);
                 acc_o[2 * e + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop, b1, acc_o[2 * e + 1], 0, 0, 0);
@@ -787,21 +782,24 @@ static int launch_decode_bits(KVCache& cc, const f16* q, int G, int Tq, float sc
     return launch_partial_merge(po, pml, nc, 16, 0, G * Tq, cc.hkv, D, G, Tq, out, stream);
 }
 
-// Turbo4 decode merge: one workgroup a query row, D/64 x 4 waves (wave w sums
-// partials c = w % 4, w % 4 + 4, ... of dims 64 (w / 4) .. +63, every load
-// issued first). The merged row is rounded to fp16 (the rotated-basis SDPA
-// output) and rotated back through the V basis by wave 0, as the rotation
-// kernel forms it.
-template <int D, int PER>
+// Turbo4 merge: one workgroup a query row, D/64 x 4 waves (wave w sums
+// partials c = w % 4, w % 4 + 4, ... of places 64 (w / 4) .. +63 of the partial
+// rows, every load issued first; slot_bits != 0: the rows are in that V
+// layout's slot order). The merged row is rounded to fp16 (the rotated-basis
+// SDPA output; KEEP32: kept in fp32, the fused verify pass) and rotated back
+// through the V basis by wave 0, as the rotation kernels form it.
+template <int D, int PER, bool KEEP32>
 __global__ __launch_bounds__(D * 4) void t4_merge_rotate_kernel(const float* __restrict__ part_o,
                                                               const float2* __restrict__ part_ml,
                                                               int nc, int rstride, int G, int Tq,
+                                                              int slot_bits,
                                                               const float* __restrict__ tab,
                                                               f16* __restrict__ out) {
     constexpr int NDG = D / 64;
     const int row = blockIdx.x, h = blockIdx.y;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int pg = wave & 3, d = 64 * (wave >> 2) + lane;
+    const int pg = wave & 3, sd = 64 * (wave >> 2) + lane;
+    const int d = slot_bits ? v_logical_dim(sd, D, slot_bits) : sd;
     const int64_t base = (int64_t)h * nc * rstride + row;
     float v[PER];
     float2 ml[PER];
@@ -810,7 +808,7 @@ __global__ __launch_bounds__(D * 4) void t4_merge_rotate_kernel(const float* __r
         const int c = pg + 4 * i;
         if (c < nc) {
             ml[i] = part_ml[base + (int64_t)c * rstride];
-            v[i] = part_o[(base + (int64_t)c * rstride) * D + d];
+            v[i] = part_o[(base + (int64_t)c * rstride) * D + sd];
         } else {
             ml[i] = float2{-INFINITY, 0.0f};
             v[i] = 0.0f;
@@ -821,7 +819,7 @@ __global__ __launch_bounds__(D * 4) void t4_merge_rotate_kernel(const float* __r
     for (int i = 0; i < PER; i++) m = fmaxf(m, ml[i].x);
     __shared__ float sm_m[4];
     __shared__ float sm[2][4][D];
-    __shared__ f16 sm_y[D];
+    __shared__ std::conditional_t<KEEP32, float, f16> sm_y[D];
     if (wave < 4 && lane == 0) sm_m[pg] = m;
     __syncthreads();
     m = fmaxf(fmaxf(sm_m[0], sm_m[1]), fmaxf(sm_m[2], sm_m[3]));
@@ -838,7 +836,11 @@ __global__ __launch_bounds__(D * 4) void t4_merge_rotate_kernel(const float* __r
     if (pg == 0) {
         const float O = (sm[0][0][d] + sm[0][1][d]) + (sm[0][2][d] + sm[0][3][d]);
         const float L = (sm[1][0][d] + sm[1][1][d]) + (sm[1][2][d] + sm[1][3][d]);
-        sm_y[d] = (f16)(L > 0.0f ? O / L : 0.0f);
+        const float y = L > 0.0f ? O / L : 0.0f;
+        if constexpr (KEEP32)
+            sm_y[d] = y;
+        else
+            sm_y[d] = (f16)y;
     }
     __syncthreads();
     if (wave == 0) {
@@ -856,30 +858,45 @@ __global__ __launch_bounds__(D * 4) void t4_merge_rotate_kernel(const float* __r
     (void)NDG;
 }
 
-template <int D>
-static int launch_t4_merge_rotate(const float* po, const float2* pml, int nc, int R, int hkv, int G,
-                                  int Tq, const float* tab, f16* out, hipStream_t stream) {
+template <int D, bool KEEP32>
+static int launch_t4_merge_rotate_d(const float* po, const float2* pml, int nc, int rstride, int R,
+                                    int hkv, int G, int Tq, int slot_bits, const float* tab,
+                                    f16* out, hipStream_t stream) {
     QW_REQUIRE(nc >= 1 && nc <= 128, QW_ERR_INVALID_ARGUMENT, "merge: partial count out of range");
     const dim3 grid(R, hkv), block(D * 4);
     switch (merge_per(nc)) {
         case 4:
-            hipLaunchKernelGGL((t4_merge_rotate_kernel<D, 4>), grid, block, 0, stream, po, pml, nc, 16, G,
-                               Tq, tab, out);
+            hipLaunchKernelGGL((t4_merge_rotate_kernel<D, 4, KEEP32>), grid, block, 0, stream, po, pml,
+                               nc, rstride, G, Tq, slot_bits, tab, out);
             break;
         case 8:
-            hipLaunchKernelGGL((t4_merge_rotate_kernel<D, 8>), grid, block, 0, stream, po, pml, nc, 16, G,
-                               Tq, tab, out);
+            hipLaunchKernelGGL((t4_merge_rotate_kernel<D, 8, KEEP32>), grid, block, 0, stream, po, pml,
+                               nc, rstride, G, Tq, slot_bits, tab, out);
             break;
         case 16:
-            hipLaunchKernelGGL((t4_merge_rotate_kernel<D, 16>), grid, block, 0, stream, po, pml, nc, 16,
-                               G, Tq, tab, out);
+            hipLaunchKernelGGL((t4_merge_rotate_kernel<D, 16, KEEP32>), grid, block, 0, stream, po, pml,
+                               nc, rstride, G, Tq, slot_bits, tab, out);
             break;
         default:  // nc <= 128
-            hipLaunchKernelGGL((t4_merge_rotate_kernel<D, 32>), grid, block, 0, stream, po, pml, nc, 16,
-                               G, Tq, tab, out);
+            hipLaunchKernelGGL((t4_merge_rotate_kernel<D, 32, KEEP32>), grid, block, 0, stream, po, pml,
+                               nc, rstride, G, Tq, slot_bits, tab, out);
     }
     QW_HIP_CHECK(hipGetLastError());
     return QW_OK;
+}
+
+int launch_t4_merge_rotate(const float* po, const float2* pml, int nc, int rstride, int R, int hkv,
+                           int D, int G, int Tq, int slot_bits, bool keep32, const float* tab,
+                           f16* out, hipStream_t stream) {
+    if (D == 256)
+        return keep32 ? launch_t4_merge_rotate_d<256, true>(po, pml, nc, rstride, R, hkv, G, Tq,
+                                                            slot_bits, tab, out, stream)
+                      : launch_t4_merge_rotate_d<256, false>(po, pml, nc, rstride, R, hkv, G, Tq,
+                                                             slot_bits, tab, out, stream);
+    return keep32 ? launch_t4_merge_rotate_d<128, true>(po, pml, nc, rstride, R, hkv, G, Tq, slot_bits,
+                                                        tab, out, stream)
+                  : launch_t4_merge_rotate_d<128, false>(po, pml, nc, rstride, R, hkv, G, Tq,
+                                                         slot_bits, tab, out, stream);
 }
 
 int launch_turbo4_decode(KVCache& cc, const f16* q, int G, int Tq, float scale, bool causal,
@@ -891,12 +908,14 @@ int launch_turbo4_decode(KVCache& cc, const f16* q, int G, int Tq, float scale, 
         int rc = launch_decode_partials<4, 256, true>(cc, q, G, Tq, cc.offset, scale, causal, &nc,
                                                       &po, &pml, stream, tab);
         if (rc) return rc;
-        return launch_t4_merge_rotate<256>(po, pml, nc, G * Tq, cc.hkv, G, Tq, tab, out, stream);
+        return launch_t4_merge_rotate(po, pml, nc, 16, G * Tq, cc.hkv, 256, G, Tq, 0, false, tab, out,
+                                      stream);
     }
     int rc = launch_decode_partials<4, 128, true>(cc, q, G, Tq, cc.offset, scale, causal, &nc, &po,
                                                   &pml, stream, tab);
     if (rc) return rc;
-    return launch_t4_merge_rotate<128>(po, pml, nc, G * Tq, cc.hkv, G, Tq, tab, out, stream);
+    return launch_t4_merge_rotate(po, pml, nc, 16, G * Tq, cc.hkv, 128, G, Tq, 0, false, tab, out,
+                                  stream);
 }
 
 // The same merge for many rows (block kernels' key splits): one thread an

@@ -175,6 +175,20 @@ int launch_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float
 // cache's device tables.
 int launch_turbo4_decode(KVCache& c, const f16* q, int G, int n_rows, float scale, bool causal,
                          const float* tab, f16* out, hipStream_t stream);
+// Turbo4 caches through the block kernel, which rotates q into the K basis
+// itself and reads the packed cache in place. fused = false keeps the fp16
+// SDPA arithmetic on the expansion's values and writes the rotated-basis rows
+// (fp16) to out; fused = true is the reference's fused verify pass (q scaled
+// by scale * log2 e, fp32 scores; every row key-split) and its merge writes
+// the rows rotated back to out. tab: the cache's device tables.
+int launch_block_attention_t4(KVCache& c, const f16* q, int G, int n_rows, float scale, bool causal,
+                              bool fused, const float* tab, f16* out, hipStream_t stream);
+// Turbo4 merge of split partials ([hkv][nc][rstride][D], slot_bits as
+// launch_partial_merge): each row merged, rounded to fp16 (keep32: kept fp32),
+// rotated back through the V basis and written to out.
+int launch_t4_merge_rotate(const float* part_o, const float2* part_ml, int nc, int rstride, int R,
+                           int hkv, int D, int G, int Tq, int slot_bits, bool keep32,
+                           const float* tab, f16* out, hipStream_t stream);
 // G * n_rows > 16 query rows per KV head (verify blocks, prefill chunks).
 int launch_block_attention(KVCache& c, const f16* q, int G, int n_rows, float scale, bool causal,
                            f16* out, hipStream_t stream);

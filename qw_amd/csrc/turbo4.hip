@@ -216,6 +216,13 @@ __global__ __launch_bounds__(128) void turbo4_fetch_kernel(
 #ifndef QW_T4_FUSED_DECODE
 #define QW_T4_FUSED_DECODE 1
 #endif
+// 1: longer Turbo4 blocks (the fused verify pass, and the dequantize-then-SDPA
+// route from 17 to kT4BlockRows rows a KV head) run in the block kernel, which
+// reads the packed cache in place; 0: the verify kernel and the fp16 expansion.
+#ifndef QW_T4_BLOCK
+#define QW_T4_BLOCK 1
+#endif
+constexpr int kT4BlockRows = 1024;
 constexpr int kExpandBlocks = 4;  // 8-key blocks a workgroup (capv / 8 is a multiple of 32)
 
 template <int D>
@@ -850,6 +857,40 @@ static int turbo4_verify(KVCache& c, const void* q, int n_q_heads, int n_rows, f
     return QW_OK;
 }
 
+// The same two routes through the block kernel, which rotates q into the K
+// basis itself and reads the packed cache in place: fused = true, the fused
+// verify pass (q rotated and scaled by scale * log2 e in fp32 then cast to
+// fp16, fp32 merged rows rotated back and cast once, by the merge);
+// fused = false, the dequantize-then-SDPA route (q rotated to fp16, the fp16
+// SDPA arithmetic on the expansion's values, the fp16 rows rotated back here).
+static int turbo4_block(KVCache& c, const void* q, int n_q_heads, int n_rows, float scale,
+                        bool causal, bool fused, void* out, hipStream_t stream) {
+    const int D = c.D, G = n_q_heads / c.hkv;
+    const float* tab = c.t4_tables;
+    if (fused)
+        return launch_block_attention_t4(c, (const f16*)q, G, n_rows, scale, causal, true, tab,
+                                         (f16*)out, stream);
+    const int qrows = n_q_heads * n_rows;
+    void* wbuf = nullptr;
+    if (int rc0 = t4_workspace(c.device, stream, (size_t)qrows * D * sizeof(f16), &wbuf)) return rc0;
+    f16* o_r = (f16*)wbuf;
+    int rc = launch_block_attention_t4(c, (const f16*)q, G, n_rows, scale, causal, false, tab, o_r,
+                                       stream);
+    if (rc) return rc;
+    const dim3 rg((qrows + 3) / 4);
+    if (D == 256) {
+        using TT = T4Tab<256>;
+        hipLaunchKernelGGL(turbo4_rotate_kernel<256>, rg, dim3(256), 0, stream, (const f16*)o_r,
+                           (f16*)out, qrows, tab + TT::v_s2, tab + TT::v_s1);
+    } else {
+        using TT = T4Tab<128>;
+        hipLaunchKernelGGL(turbo4_rotate_kernel<128>, rg, dim3(256), 0, stream, (const f16*)o_r,
+                           (f16*)out, qrows, tab + TT::v_s2, tab + TT::v_s1);
+    }
+    QW_HIP_CHECK(hipGetLastError());
+    return QW_OK;
+}
+
 int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float scale,
                      bool causal, void* out, hipStream_t stream) {
     QW_REQUIRE(q && out, QW_ERR_INVALID_ARGUMENT, "attention: null q/out");
@@ -865,7 +906,8 @@ int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float
     // 70-100, cache.rs:3520-3560): causal, 1..5 query rows, more than 2048
     // cached tokens; here also G * rows <= 32 (one workgroup's rows).
     if (causal && n_rows <= 5 && T > 2048 && (n_q_heads / c.hkv) * n_rows <= kT4vRows)
-        return turbo4_verify(c, q, n_q_heads, n_rows, scale, out, stream);
+        return QW_T4_BLOCK ? turbo4_block(c, q, n_q_heads, n_rows, scale, causal, true, out, stream)
+                           : turbo4_verify(c, q, n_q_heads, n_rows, scale, out, stream);
     const int qrows = n_q_heads * n_rows;
     const float* tab = c.t4_tables;
 #if QW_T4_FUSED_DECODE
@@ -877,6 +919,13 @@ int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float
         return launch_turbo4_decode(c, (const f16*)q, n_q_heads / c.hkv, n_rows, scale, causal, tab,
                                     (f16*)out, stream);
 #endif
+    // Up to 8 query tiles a KV head, the block kernel reads the packed cache in
+    // place; past that, its per-tile dequantization (repeated for every query
+    // tile) costs more than expanding the cache once for the fp16 kernel
+    // (measured at 4 q heads a KV head, depth 8k and 32k: 1024 rows a head
+    // 320 against 329 us, 2048 rows 651 against 599 us).
+    if (QW_T4_BLOCK && (n_q_heads / c.hkv) * n_rows <= kT4BlockRows)
+        return turbo4_block(c, q, n_q_heads, n_rows, scale, causal, false, out, stream);
     const int capv = (T + 255) / 256 * 256;
     const size_t kv_bytes = (size_t)c.hkv * capv * D * sizeof(f16);
     const size_t q_bytes = (size_t)n_q_heads * n_rows * D * sizeof(f16);

@@ -49,19 +49,66 @@ __device__ __forceinline__ void wht_wave(float (&y)[D / 64], int lane) {
     }
 }
 
+// f16 of an fp32 product, rounded first to fp32 (the expansion's
+// f16(centroid * rescale)); the register pin keeps the compiler from fusing
+// the multiply and the conversion into one singly rounded mixed-precision op.
+__device__ __forceinline__ f16 t4_f16_product(float c, float r) {
+    float p = c * r;
+    asm("" : "+v"(p));
+    return (f16)p;
+}
+
 // One row through a rotation, as the rotation kernel forms it:
 // out = f16((H x (s_in . in)) * (1/sqrt(D)) * s_out) in fp32, the wave's lane
-// holding coordinates lane * VPL .. + VPL - 1 of `in` (fp32 values).
+// holding coordinates lane * VPL .. + VPL - 1 of `in` (fp32 values) and of
+// the signs si, so.
+template <int D>
+__device__ __forceinline__ void t4_rotate_row(float (&y)[D / 64], int lane,
+                                              const float (&si)[D / 64], const float (&so)[D / 64],
+                                              f16 (&o)[D / 64]) {
+    constexpr int VPL = D / 64;
+#pragma unroll
+    for (int j = 0; j < VPL; j++) y[j] *= si[j];
+    wht_wave<D>(y, lane);
+#pragma unroll
+    for (int j = 0; j < VPL; j++) o[j] = (f16)((y[j] * wht_scale(D)) * so[j]);
+}
+
+// The fused verify pass's q: out = f16(f32(f32(s_out . (H / sqrt(D)) . s_in .
+// in) * post)) (post = scale * log2 e), as the scaled rotation kernel forms it.
+template <int D>
+__device__ __forceinline__ void t4_rotate_row_scaled(float (&y)[D / 64], int lane,
+                                                     const float (&si)[D / 64],
+                                                     const float (&so)[D / 64], float post,
+                                                     f16 (&o)[D / 64]) {
+    constexpr int VPL = D / 64;
+#pragma unroll
+    for (int j = 0; j < VPL; j++) y[j] *= si[j];
+    wht_wave<D>(y, lane);
+#pragma unroll
+    for (int j = 0; j < VPL; j++) {
+        float v = (y[j] * wht_scale(D)) * so[j];
+        asm("" : "+v"(v));
+        o[j] = t4_f16_product(v, post);
+    }
+}
+
+// The lane's coordinates of a sign vector (D floats).
+template <int D>
+__device__ __forceinline__ void t4_lane_signs(const float* __restrict__ s, int lane,
+                                              float (&r)[D / 64]) {
+#pragma unroll
+    for (int j = 0; j < D / 64; j++) r[j] = s[lane * (D / 64) + j];
+}
+
 template <int D>
 __device__ __forceinline__ void t4_rotate_row(float (&y)[D / 64], int lane,
                                               const float* __restrict__ s_in,
                                               const float* __restrict__ s_out, f16 (&o)[D / 64]) {
-    constexpr int VPL = D / 64;
-#pragma unroll
-    for (int j = 0; j < VPL; j++) y[j] *= s_in[lane * VPL + j];
-    wht_wave<D>(y, lane);
-#pragma unroll
-    for (int j = 0; j < VPL; j++) o[j] = (f16)((y[j] * wht_scale(D)) * s_out[lane * VPL + j]);
+    float si[D / 64], so[D / 64];
+    t4_lane_signs<D>(s_in, lane, si);
+    t4_lane_signs<D>(s_out, lane, so);
+    t4_rotate_row<D>(y, lane, si, so, o);
 }
 
 }  // namespace qw

@@ -227,14 +227,16 @@ def fused_verify_route(T, L, causal, G):
     (3333, 4, True, 128),     # head_dim 128: fused
     (65532, 4, True, 256),    # 65536 tokens, 64 key stages a split
     (1000, 16, True, 256),    # 16-row verify block
-    (900, 128, True, 256),    # prefill chunk (expansion + block kernel)
+    (900, 128, True, 256),    # prefill chunk, 768 rows a KV head: block kernel on the packed cache
+    (700, 200, True, 256),    # 1200 rows a KV head: fp16 expansion + fp16 block kernel
+    (2000, 40, False, 128),   # non-causal 240 rows a KV head, head_dim 128: block kernel
     (777, 1, False, 128),     # head_dim 128 decode
     (0, 1, False, 256),       # first token
 ])
 def test_turbo4_attention_matches_oracle(T_prefix, L, causal, D):
     import qw_amd
 
-    rows = None if L <= 16 else np.array([0, 1, 63, 64, 100, L - 1])
+    rows = None if L <= 16 else np.unique([r for r in (0, 1, 63, 64, 100, L - 1) if r < L])
     out, ref, _, _ = _turbo4_layer(qw_amd, T_prefix, L, causal, seed=T_prefix + L + D,
                                    D=D, rows=rows)
     assert np.isfinite(out).all()
