@@ -35,6 +35,7 @@
 #include <algorithm>
 #include <type_traits>
 
+#include "append.hpp"
 #include "dequant.hpp"
 #include "kv_cache.hpp"
 #include "turbo4_device.hpp"
@@ -61,6 +62,13 @@ struct BlockArgs {
     // split t % n_split, head (t / n_split) % hkv, tile qt0 + t / (n_split hkv)).
     // The dispatcher starts the split workgroups as the first ones finish.
     int n_main, main_tiles, hkv;
+    // n_app > 0: a verify block that appends its own rows in this launch
+    // (affine and Int8 caches, one query tile). Workgroup h < n_app (= hkv)
+    // quantizes-and-appends head h's new rows (read through app) and attends
+    // them, keys T_pre .. T - 1, as the last of the n_split partial slots; the
+    // others are splits 0 .. n_split - 2 of the cached prefix, keys < T_pre.
+    int n_app, T_pre, app_int8;
+    RowSrc app;
     const float* t4_tab;  // Turbo4 caches: the device tables (signs, centroids: T4Tab<D>)
     float t4_post;        // Turbo4 fused pass: scale * log2(e) in fp32
     float scale_h;      // f16(scale) as float
@@ -174,7 +182,23 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     static_assert(PER * 64 * NW == KT * TPR && (KT / 8) * TPB == KT * TPR, "slices a thread");
 
     int sp, qt, h, n_split, tiles_per_split;
-    if (a.n_main > 0) {
+    int key_lo = 0, key_hi = a.T;  // the keys this workgroup may see: [key_lo, key_hi)
+    if (a.n_app > 0) {
+        const int lin = blockIdx.x;
+        qt = 0;
+        n_split = a.n_split;
+        tiles_per_split = a.tiles_per_split;
+        if (lin < a.n_app) {
+            h = lin;
+            sp = a.n_split - 1;
+            key_lo = a.T_pre;
+        } else {
+            const int t = lin - a.n_app;
+            sp = t % (a.n_split - 1);
+            h = t / (a.n_split - 1);
+            key_hi = a.T_pre;
+        }
+    } else if (a.n_main > 0) {
         const int lin = blockIdx.x;
         if (lin < a.n_main) {
             sp = 0;
@@ -207,10 +231,10 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     constexpr int WROWS = 16 * RT;
     const int row0 = qt * WROWS * NW;
     const int row_last = min(a.R, row0 + WROWS * NW) - 1;
-    const int wg_lim = a.causal ? a.T - a.Tq + row_last / a.G : a.T - 1;
+    const int wg_lim = min(a.causal ? a.T - a.Tq + row_last / a.G : a.T - 1, key_hi - 1);
     const int n_tiles = (a.T + KT - 1) / KT;
-    const int t0 = sp * tiles_per_split;
-    const int t1 = min(min(n_tiles, t0 + tiles_per_split), wg_lim / KT + 1);
+    const int t0 = key_lo > 0 ? key_lo / KT : sp * tiles_per_split;
+    const int t1 = key_lo > 0 ? wg_lim / KT + 1 : min(min(n_tiles, t0 + tiles_per_split), wg_lim / KT + 1);
 
     // ---- the wave's RT x 16 query rows as the B operand of S^T = K . Q'^T
     // (col = query row r16 of row tile rt, k-group g = dims 32m + 8g .. +7 of
@@ -218,10 +242,10 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     const int wrow0 = row0 + WROWS * wave;
     const bool wave_live = wrow0 < a.R;
     const int wave_last = min(a.R, wrow0 + WROWS) - 1;
-    const int wave_lim = a.causal ? a.T - a.Tq + wave_last / a.G : a.T - 1;
+    const int wave_lim = min(a.causal ? a.T - a.Tq + wave_last / a.G : a.T - 1, key_hi - 1);
     // the smallest key limit of the wave's live rows (padding rows see nothing
     // and are never written, so they do not count)
-    const int wave_first_lim = a.causal ? a.T - a.Tq + wrow0 / a.G : a.T - 1;
+    const int wave_first_lim = min(a.causal ? a.T - a.Tq + wrow0 / a.G : a.T - 1, key_hi - 1);
     int lim[RT];
     bool row_ok[RT];
     half8 qb[RT][NM];
@@ -272,7 +296,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     for (int rt = 0; rt < RT; rt++) {
         const int rho = wrow0 + 16 * rt + r16;
         row_ok[rt] = rho < a.R;
-        lim[rt] = row_ok[rt] ? (a.causal ? a.T - a.Tq + rho / a.G : a.T - 1) : -1;
+        lim[rt] = row_ok[rt] ? min(a.causal ? a.T - a.Tq + rho / a.G : a.T - 1, key_hi - 1) : -1;
         const int rr = row_ok[rt] ? rho : 0;
         // (Turbo4 padding rows read the workgroup's first staged row; their scale is 0)
         const f16* qrow = T4 ? sq + (row_ok[rt] ? WROWS * wave + 16 * rt + r16 : 0) * D
@@ -513,7 +537,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         // Scores -> fp16 rounding -> (mask) -> online softmax -> P; the mask
         // only for tiles some row of the wave cannot fully see (a scalar
         // branch around the compares: the common case carries none).
-        const bool mask = kt0 + KT - 1 > wave_first_lim;
+        const bool mask = kt0 + KT - 1 > wave_first_lim || kt0 < key_lo;
         half8 popl[FUSED ? NSUB : 1][RT];  // fused pass: the remainders p - f16(p)
         auto softmax_fused = [&]() {
 #pragma unroll
@@ -530,7 +554,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
 #pragma unroll
                         for (int e = 0; e < 8; e++) {
                             const int key = kt0 + 32 * u + 8 * g + (e & 3) + 4 * (e >> 2);
-                            if (key > lim[rt]) sf[u][e] = -INFINITY;
+                            if (key > lim[rt] || key < key_lo) sf[u][e] = -INFINITY;
                         }
                 }
                 float mx_lane = sf[0][0];
@@ -591,7 +615,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
                             for (int e = 0; e < 2; e++) {
                                 const int idx = 2 * j + e;
                                 const int key = kt0 + 32 * u + 8 * g + (idx & 3) + 4 * (idx >> 2);
-                                if (key > lim[rt]) sh[u][j][e] = (f16)(-INFINITY);
+                                if (key > lim[rt] || key < key_lo) sh[u][j][e] = (f16)(-INFINITY);
                             }
                 }
                 // Online softmax with a lazy reference: m_run moves only when a
@@ -772,6 +796,23 @@ __global__ __launch_bounds__(64 * kBlockWaves, 1) void attend_block_kernel(Block
     // same output elements, so the second pass's writes replace the first's).
     // A null flag (Int8 caches) takes the separately rounded dequant directly.
     // Turbo4 caches have one expansion (a null flag).
+    if constexpr (BITS != 16 && T4M == 0) {
+        if (a.n_app > 0 && (int)blockIdx.x < a.n_app) {
+            // the new rows of head blockIdx.x go into the cache first (the
+            // append kernel's work, 8-token V block by block); this
+            // workgroup's tiles then read them back, and its fast-flag check
+            // below sees its own rows' scales
+            const int L = a.T - a.T_pre;
+            auto& sc = *reinterpret_cast<AppendScratch<D>*>(lds_buf);
+            for (int blk = a.T_pre / 8; blk <= (a.T - 1) / 8; blk++) {
+                append_block<D>(a.app, L, a.T_pre, BITS, a.app_int8 != 0, a.cap,
+                                (uint32_t*)a.k_data, (uint32_t*)a.k_params, (uint32_t*)a.v_data,
+                                (f16*)a.v_params, (int*)a.fast_flag, blk, blockIdx.x, threadIdx.x,
+                                64 * kBlockWaves, sc);
+                __syncthreads();
+            }
+        }
+    }
     if (T4M == 0 && (BITS == 16 || a.fast_flag != nullptr)) {
         block_body<BITS, D, RT, true>(a, lds_buf);
         if (BITS != 16 && *a.fast_flag == 0) {
@@ -789,13 +830,20 @@ static int launch_block_rt(KVCache& cc, BlockArgs& a, int n_qt, hipStream_t stre
     const size_t shmem = (size_t)2 * BlockShape<D>::BUF + (T4M ? 256 * sizeof(float2) : 0);
     int rc = ensure_dynamic_lds((const void*)attend_block_kernel<BITS, D, RT, T4M>, shmem);
     if (rc) return rc;
-    const dim3 grid = a.n_main > 0 ? dim3(a.n_main + n_qt * cc.hkv * a.n_split)
-                                   : dim3(a.n_split, n_qt, cc.hkv);
+    const dim3 grid = a.n_app > 0    ? dim3(a.n_app + cc.hkv * (a.n_split - 1))
+                      : a.n_main > 0 ? dim3(a.n_main + n_qt * cc.hkv * a.n_split)
+                                     : dim3(a.n_split, n_qt, cc.hkv);
     hipLaunchKernelGGL((attend_block_kernel<BITS, D, RT, T4M>), grid, dim3(64 * kBlockWaves), shmem,
                        stream, a);
     QW_HIP_CHECK(hipGetLastError());
     return QW_OK;
 }
+
+// 1: verify blocks on affine and Int8 caches append their rows inside the
+// attention launch (launch_block_append_attention); 0: a separate append.
+#ifndef QW_BLOCK_APPEND
+#define QW_BLOCK_APPEND 1
+#endif
 
 // Row tiles a wave owns: the fewest workgroup rounds on 256 CUs (one
 // workgroup a CU), weighing the larger RT's longer rounds.
@@ -890,6 +938,10 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     a.n_main = 0;
     a.main_tiles = n_tiles;
     a.hkv = cc.hkv;
+    a.n_app = 0;
+    a.T_pre = T;
+    a.app_int8 = 0;
+    a.app = RowSrc{};
 
     // Plan (one workgroup a CU, 256 CUs): query tiles that fill whole rounds
     // run unsplit and write their rows; the rest (all of them when fewer than
@@ -953,6 +1005,86 @@ int launch_block_attention_t4(KVCache& cc, const f16* q, int G, int n_rows, floa
                      : launch_block_bits<4, 256, 1>(cc, q, G, n_rows, scale, causal, out, stream, tab);
     return fused ? launch_block_bits<4, 128, 2>(cc, q, G, n_rows, scale, causal, out, stream, tab)
                  : launch_block_bits<4, 128, 1>(cc, q, G, n_rows, scale, causal, out, stream, tab);
+}
+
+// Verify blocks on affine and Int8 caches: the append rides in the attention
+// launch (see BlockArgs::n_app). The prefix splits are planned for the CUs the
+// append workgroups leave free; every row sees the whole prefix, so the
+// prefix splits need no causal cut and the partial slot of the new keys
+// carries it.
+template <int BITS, int D>
+static int launch_block_append_bits(KVCache& cc, const f16* q, int G, int L, const f16* k_new,
+                                    const f16* v_new, float scale, bool causal, f16* out,
+                                    hipStream_t stream) {
+    using S = BlockShape<D>;
+    const int T_pre = cc.offset, T = T_pre + L, R = G * L;
+    BlockArgs a;
+    a.k_data = (const uint32_t*)cc.k_data;
+    a.k_params = cc.k_params;
+    a.v_data = (const uint32_t*)cc.v_data;
+    a.v_params = cc.v_params;
+    a.fast_flag = cc.int8() ? nullptr : cc.fast_flag;
+    a.q = q;
+    a.out = out;
+    a.t4_tab = nullptr;
+    a.t4_post = 0.0f;
+    a.cap = cc.cap;
+    a.T = T;
+    a.Tq = L;
+    a.G = G;
+    a.R = R;
+    a.causal = causal ? 1 : 0;
+    a.scale_h = (float)(f16)scale;
+    a.code_off2 = cc.code_offset2();
+    a.qt0 = 0;
+    a.prow0 = 0;
+    a.PR = R;
+    a.n_main = 0;
+    a.main_tiles = 0;
+    a.hkv = cc.hkv;
+    a.n_app = cc.hkv;
+    a.T_pre = T_pre;
+    a.app_int8 = cc.int8() ? 1 : 0;
+    a.app = RowSrc{};
+    a.app.k = k_new;
+    a.app.v = v_new;
+    a.app.row_stride = D;
+    a.app.head_stride = (int64_t)L * D;
+    int n_pre, tps;
+    split_keys((T_pre + S::KT - 1) / S::KT, std::max(1, (256 - cc.hkv) / cc.hkv), &n_pre, &tps);
+    a.n_split = n_pre + 1;
+    a.tiles_per_split = tps;
+    const size_t o_bytes = (size_t)cc.hkv * a.n_split * R * D * sizeof(float);
+    int rc = cc.ensure_workspace(o_bytes + (size_t)cc.hkv * a.n_split * R * sizeof(float2), stream);
+    if (rc) return rc;
+    a.part_o = (float*)cc.ws_ptr;
+    a.part_ml = (float2*)((char*)cc.ws_ptr + o_bytes);
+    rc = launch_one<BITS, D, 0>(cc, a, 1, 1, stream);
+    if (rc) return rc;
+    cc.offset = T;
+    return launch_partial_merge(a.part_o, a.part_ml, a.n_split, R, 0, R, cc.hkv, D, G, L, out,
+                                stream, BITS);
+}
+
+bool block_append_fits(const KVCache& cc, int G, int L) {
+    return QW_BLOCK_APPEND && cc.affine() && (cc.D == 128 || cc.D == 256) && L >= 2 &&
+           G * L > 16 && G * L <= 16 * kBlockWaves && cc.offset >= 256;
+}
+
+int launch_block_append_attention(KVCache& cc, const f16* q, int G, int L, const f16* k_new,
+                                  const f16* v_new, float scale, bool causal, f16* out,
+                                  hipStream_t stream) {
+    QW_REQUIRE(block_append_fits(cc, G, L) && cc.offset + L <= cc.cap, QW_ERR_INVALID_ARGUMENT,
+               "block attention: verify block outside the fused-append shapes");
+    if (cc.D == 256)
+        return cc.bits == 4 ? launch_block_append_bits<4, 256>(cc, q, G, L, k_new, v_new, scale,
+                                                               causal, out, stream)
+                            : launch_block_append_bits<8, 256>(cc, q, G, L, k_new, v_new, scale,
+                                                               causal, out, stream);
+    return cc.bits == 4 ? launch_block_append_bits<4, 128>(cc, q, G, L, k_new, v_new, scale, causal,
+                                                           out, stream)
+                        : launch_block_append_bits<8, 128>(cc, q, G, L, k_new, v_new, scale, causal,
+                                                           out, stream);
 }
 
 int launch_block_attention(KVCache& cc, const f16* q, int G, int n_rows, float scale, bool causal,

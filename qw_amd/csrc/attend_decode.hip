@@ -1323,6 +1323,17 @@ int KVCache::update_and_attention(const void* q, int n_q_heads, int n_rows, cons
         return bits == 4 ? launch_decode_fused<4, 128>(*this, qq, G, kn, vn, scale, oo, stream)
                          : launch_decode_fused<8, 128>(*this, qq, G, kn, vn, scale, oo, stream);
     }
+    if (block_append_fits(*this, G, n_rows)) {
+        // verify blocks: the append rides in the block kernel's launch
+        DeviceGuard dg(device);
+        QW_REQUIRE(dg.ok, QW_ERR_HIP, "update_and_attention: hipSetDevice failed");
+        if (offset + n_rows > cap) {
+            int rc = reserve(std::max(offset + n_rows, cap + cap / 2), stream);
+            if (rc) return rc;
+        }
+        return launch_block_append_attention(*this, (const f16*)q, G, n_rows, (const f16*)k_new,
+                                             (const f16*)v_new, scale, causal, (f16*)out, stream);
+    }
     int rc = update(k_new, v_new, n_rows, stream);
     if (rc) return rc;
     return launch_attention(*this, q, n_q_heads, n_rows, scale, causal, out, stream);

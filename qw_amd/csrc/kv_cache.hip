@@ -16,6 +16,7 @@
 #include <string>
 
 #include "kv_cache.hpp"
+#include "append.hpp"
 #include "quant.hpp"
 #include "rope.hpp"
 
@@ -301,187 +302,16 @@ int KVCache::trim(int n) {
     return m;
 }
 
-// ------------------------------------------------ quantize-on-append (A.1)
-//
-// One workgroup (4 waves) per (KV head, 8-token V block touched by the
-// append). Each wave quantizes whole rows (one token of K or V): a lane
-// holds D/64 consecutive dims, a 64-dim group is 64/(D/64) lanes and its
-// min/max are wave shuffles. The group math is MLX's, in fp32 with IEEE
-// division and rint (ties to even):
-//   scale = max((max - min) / n_bins, 1e-7), negated unless |min| > |max|
-//   edge = larger-magnitude extreme; q0 = rint(edge / scale)
-//   if q0 != 0: scale = edge / q0, bias = edge, else bias = 0
-//   code = clamp(rint((w - bias) / scale), 0, n_bins)
-// Codes go through LDS so the V block words (8 keys per dim) are assembled
-// by one thread each: no two threads write the same word.
-
-// Int8 (cache.rs:270-305 quantize_per_token, MLX fp16 ops): absmax over the
-// row; scale = f16(absmax / 127), 1 where that is 0; code = clip(round(
-// f16(x / scale)), -128, 127), stored as code + 128 with (scale, 0) in every
-// group slot. fp16 division rounded once from the fp32 quotient equals the
-// correctly rounded fp16 division (24 >= 2*11 + 2 bits).
-template <int D>
-__device__ inline void quantize_row_int8(const float* x, uint8_t* lds_codes, half2v* sb_out) {
-    constexpr int VPL = D / 64;
-    const int lane = threadIdx.x & 63;
-    float am = 0.0f;
-#pragma unroll
-    for (int i = 0; i < VPL; i++) am = fmaxf(am, fabsf(x[i]));
-    am = wave_reduce(am, OpMax());
-    f16 sc = (f16)(am / 127.0f);
-    if ((float)sc == 0.0f) sc = (f16)1.0f;
-    const float s = (float)sc;
-#pragma unroll
-    for (int i = 0; i < VPL; i++) {
-        const float c = __builtin_rintf((float)(f16)(x[i] / s));
-        lds_codes[lane * VPL + i] = (uint8_t)((int)fminf(fmaxf(c, -128.0f), 127.0f) + 128);
-    }
-    if (lane < D / kGroup) {
-        half2v sb;
-        sb.x = sc;
-        sb.y = (f16)0.0f;
-        sb_out[lane] = sb;
-    }
-}
-
-// The row is read from `src`; with `rope` (K of a fused RoPE-append) each
-// element is rotated first and rounded to fp16, the value the fp16 rotation
-// hands to the cache's quantize-on-append.
-template <int D>
-__device__ inline void quantize_row(const f16* __restrict__ src, int bits, bool int8,
-                                    uint8_t* lds_codes,
-                                    half2v* sb_out /* [D/64] (scale, bias) */, int* fast_flag,
-                                    const RowSrc* rope = nullptr, int pos = 0) {
-    constexpr int VPL = D / 64;         // values per lane
-    constexpr int LPG = kGroup / VPL;   // lanes per group
-    const int lane = threadIdx.x & 63;
-    float x[VPL];
-    if (rope && rope->rope_dims > 0) {
-#pragma unroll
-        for (int i = 0; i < VPL; i++) x[i] = (float)(f16)rope_elem(src, lane * VPL + i, rope->rope_dims,
-                                                  rope->traditional, rope->log2_base,
-                                                  rope->scale, pos);
-    } else {
-#pragma unroll
-        for (int i = 0; i < VPL; i++) x[i] = (float)src[lane * VPL + i];
-    }
-    if (int8) {
-        quantize_row_int8<D>(x, lds_codes, sb_out);
-        return;
-    }
-    float mx = x[0], mn = x[0];
-#pragma unroll
-    for (int i = 1; i < VPL; i++) {
-        mx = mx < x[i] ? x[i] : mx;
-        mn = x[i] < mn ? x[i] : mn;
-    }
-#pragma unroll
-    for (int off = 1; off < LPG; off <<= 1) {
-        const float omx = __shfl_xor(mx, off);
-        const float omn = __shfl_xor(mn, off);
-        mx = mx < omx ? omx : mx;
-        mn = omn < mn ? omn : mn;
-    }
-    const AffineGroup q = affine_group(mn, mx, bits);
-#pragma unroll
-    for (int i = 0; i < VPL; i++) lds_codes[lane * VPL + i] = (uint8_t)affine_code(x[i], q, bits);
-    if ((lane % LPG) == 0) {
-        half2v sb;
-        sb.x = (f16)q.scale;
-        sb.y = (f16)q.bias;
-        sb_out[lane / LPG] = sb;
-        check_fast_scale(sb.x, bits, fast_flag);
-    }
-}
-
+// Quantize-on-append: one workgroup (4 waves) per (8-token V block touched by
+// the append, KV head).
 template <int D>
 __global__ __launch_bounds__(256) void append_affine_kernel(
     RowSrc rs, int n_tokens, int t_old,
     int bits, int int8, int cap, uint32_t* __restrict__ k_codes, uint32_t* __restrict__ k_params,
     uint32_t* __restrict__ v_codes, f16* __restrict__ v_params, int* __restrict__ fast_flag) {
-    constexpr int NG = D / kGroup;
-    __shared__ uint8_t kc[8][D];
-    __shared__ uint8_t vc[8][D];
-    __shared__ half2v ksb[8][NG];
-    __shared__ half2v vsb[8][NG];
-    const int h = blockIdx.y;
-    const int blk = t_old / 8 + blockIdx.x;
-    const int wave = threadIdx.x >> 6;
-    const int t_end = t_old + n_tokens;
-    // Codes of earlier tokens in a partly filled block are kept: fetch those
-    // words now so their latency overlaps the quantization.
-    const int bw = D * bits / 4;  // words per V block (8 keys x D dims)
-    uint32_t* vb = v_codes + ((int64_t)h * (cap / 8) + blk) * bw;
-    const bool keep_old = blk * 8 < t_old;
-    uint32_t old0 = 0, old1 = 0;
-    const int d_own = threadIdx.x;  // blockDim.x == 256 >= D
-    const int p_own = d_own < D ? v_phys_dim(d_own, D, bits) : 0;
-    if (keep_old && d_own < D) {
-        if (bits == 4) {
-            old0 = vb[p_own];
-        } else {
-            old0 = vb[2 * p_own];
-            old1 = vb[2 * p_own + 1];
-        }
-    }
-    for (int k = wave; k < 8; k += 4) {
-        const int t = blk * 8 + k;
-        if (t < t_old || t >= t_end) continue;
-        const int64_t src = (int64_t)(t - t_old) * rs.row_stride + (int64_t)h * rs.head_stride;
-        quantize_row<D>(rs.k + src, bits, int8 != 0, kc[k], ksb[k], fast_flag, &rs,
-                        rs.position0 + (t - t_old));
-        quantize_row<D>(rs.v + src, bits, int8 != 0, vc[k], vsb[k], fast_flag);
-    }
-    __syncthreads();
-    // K: row-major MLX packing, words of 32/bits codes LSB-first.
-    const int epw = 32 / bits;
-    const int nw = D / epw;
-    for (int i = threadIdx.x; i < 8 * nw; i += blockDim.x) {
-        const int k = i / nw, w = i % nw;
-        const int t = blk * 8 + k;
-        if (t < t_old || t >= t_end) continue;
-        uint32_t word = 0;
-        for (int e = 0; e < epw; e++) word |= (uint32_t)kc[k][w * epw + e] << (e * bits);
-        k_codes[((int64_t)h * cap + t) * nw + w] = word;
-    }
-    for (int i = threadIdx.x; i < 8 * NG; i += blockDim.x) {
-        const int k = i / NG, g = i % NG;
-        const int t = blk * 8 + k;
-        if (t < t_old || t >= t_end) continue;
-        k_params[((int64_t)h * cap + t) * NG + k_param_slot(g, NG)] =
-            __builtin_bit_cast(uint32_t, ksb[k][g]);
-        f16* vp = v_params + (((int64_t)h * (cap / 8) + blk) * NG + g) * 16;
-        vp[k] = vsb[k][g].x;
-        vp[8 + k] = vsb[k][g].y;
-    }
-    // V: one thread per dim assembles the block word(s), keeping the codes of
-    // slots before this append (earlier tokens of a partly filled block).
-    if (d_own < D) {
-        const int d = d_own, p = p_own;
-        if (bits == 4) {
-            uint32_t word = old0;
-            for (int k = 0; k < 8; k++) {
-                const int t = blk * 8 + k;
-                if (t < t_old || t >= t_end) continue;
-                const int sh = 4 * v4_nibble_pos(k);
-                word = (word & ~(0xFu << sh)) | ((uint32_t)vc[k][d] << sh);
-            }
-            vb[p] = word;
-        } else {
-            uint32_t w0 = old0, w1 = old1;
-            for (int k = 0; k < 8; k++) {
-                const int t = blk * 8 + k;
-                if (t < t_old || t >= t_end) continue;
-                const int sh = 8 * (k & 3);
-                if (k < 4)
-                    w0 = (w0 & ~(0xFFu << sh)) | ((uint32_t)vc[k][d] << sh);
-                else
-                    w1 = (w1 & ~(0xFFu << sh)) | ((uint32_t)vc[k][d] << sh);
-            }
-            vb[2 * p] = w0;
-            vb[2 * p + 1] = w1;
-        }
-    }
+    __shared__ AppendScratch<D> sc;
+    append_block<D>(rs, n_tokens, t_old, bits, int8 != 0, cap, k_codes, k_params, v_codes, v_params,
+                    fast_flag, t_old / 8 + blockIdx.x, blockIdx.y, threadIdx.x, blockDim.x, sc);
 }
 
 // fp16 mode append: K rows copied, V scattered into 8-key blocks.

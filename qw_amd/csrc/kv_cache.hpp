@@ -192,6 +192,14 @@ int launch_t4_merge_rotate(const float* part_o, const float2* part_ml, int nc, i
 // G * n_rows > 16 query rows per KV head (verify blocks, prefill chunks).
 int launch_block_attention(KVCache& c, const f16* q, int G, int n_rows, float scale, bool causal,
                            f16* out, hipStream_t stream);
+// A verify block on an affine or Int8 cache whose append runs inside the block
+// kernel's launch: appends n_rows new rows ([hkv][n_rows][D]) and attends q
+// over the cache including them, as update + launch_block_attention would.
+// block_append_fits: the shapes it takes; the caller reserves the capacity.
+bool block_append_fits(const KVCache& c, int G, int n_rows);
+int launch_block_append_attention(KVCache& c, const f16* q, int G, int n_rows, const f16* k_new,
+                                  const f16* v_new, float scale, bool causal, f16* out,
+                                  hipStream_t stream);
 // Split-K merge: out[row0 + row] = sum_c e^(m_c - M) O_c / sum_c e^(m_c - M) l_c
 // over nc partials of [rstride][D] fp32 rows per KV head, rows 0 .. R-1.
 // slot_bits == 0: partial rows in dim order; 4/8/16: in the V plane's slot

@@ -299,6 +299,39 @@ def test_attention_without_append_equals_fused_call(oracle_lib, bits):
     assert_close(o2, o1, f"bits={bits} fused append vs cached")
 
 
+@pytest.mark.parametrize("mode,D,T0,L,hq,causal,cap", [
+    ("affine4", 256, 3000, 4, 24, True, 0),     # served 4-row verify
+    ("affine8", 256, 2045, 5, 24, True, 0),     # new rows across an 8-key block and a 64-key tile
+    ("int8", 256, 4093, 3, 24, True, 0),        # Int8 per-token rows
+    ("affine4", 128, 1000, 16, 32, True, 0),    # head_dim 128, 128 rows a KV head
+    ("affine4", 256, 700, 6, 24, False, 0),     # non-causal block: every row sees every new key
+    ("affine8", 256, 512, 4, 24, True, 512),    # the call grows the capacity first
+])
+def test_verify_append_in_launch_equals_separate_append(oracle_lib, mode, D, T0, L, hq, causal, cap):
+    """A verify block on an affine or Int8 cache appends its rows inside the
+    attention launch. The cache then holds exactly what one bulk update of the
+    same rows stores (every snapshot tensor equal bit for bit), and the output
+    equals attending the updated cache, within the stated tolerance."""
+    import qw_amd
+
+    r = rng(7000 + T0 + L + D)
+    k, v = _kv(r, 4, T0 + L, D)
+    q = r.standard_normal((hq, L, D)).astype(np.float16)
+    a = qw_amd.KVCache(mode, 4, D, capacity=cap)
+    a.update(_gpu(k[:, :T0])[None], _gpu(v[:, :T0])[None])
+    fn = a.update_and_causal_attention if causal else a.update_and_attention
+    o1 = _np(fn(_gpu(q)[None], _gpu(k[:, T0:])[None], _gpu(v[:, T0:])[None], 1.0 / 16))[0]
+    b = qw_amd.KVCache(mode, 4, D)
+    b.update(_gpu(k)[None], _gpu(v)[None])
+    o2 = _np(b.attention(_gpu(q)[None], 1.0 / 16, causal))[0]
+    assert a.offset == b.offset == T0 + L
+    sa, sb = a.snapshot_tensors(), b.snapshot_tensors()
+    for name, t in sa.items():
+        assert torch.equal(t, sb[name]), name
+    assert np.isfinite(o1).all()
+    assert_close(o1, o2, f"{mode} D{D} T{T0}+{L} causal={causal}: append in launch vs cached")
+
+
 @pytest.mark.parametrize("bits,D", [(4, 256), (8, 256), (4, 128), (8, 128)])
 def test_decode_steps_store_the_same_codes_as_a_bulk_append(oracle_lib, bits, D):
     """Token-by-token decode (append fused into the attention call), across
