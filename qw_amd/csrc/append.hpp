@@ -6,6 +6,7 @@
 #include "kv_cache.hpp"
 #include "quant.hpp"
 #include "rope.hpp"
+#include "turbo4_device.hpp"
 
 namespace qw {
 
@@ -196,6 +197,82 @@ __device__ inline void append_block(const RowSrc& rs, int n_tokens, int t_old, i
             }
             vb[2 * p] = w0;
             vb[2 * p + 1] = w1;
+        }
+    }
+}
+
+// Turbo4 quantize-on-append of one row by one wave (lane holds D/64
+// consecutive coordinates): row i of head h, K (is_k: K signs, RoPE as RowSrc
+// asks) or V (V signs), stored as cache row t_old + i. The steps: fp32 L2 norm
+// (an all-zero row divides by 1); signs2 . H . signs1 of the unit row (H the
+// Walsh-Hadamard transform scaled 1/sqrt(D)); the index = the number of the
+// 15 boundaries strictly below the value; rescale = f16(norm / max(|centroid
+// vector|, 1e-10)); nibbles packed low = even coordinate; side word K
+// (rescale, 0), V (f16 norm, rescale). cb: the 16 centroids.
+template <int D>
+__device__ inline void turbo4_append_row(const RowSrc& rs, int i, int h, bool is_k, int lane,
+                                         int t_old, int cap, const float* __restrict__ tab,
+                                         const float* cb, uint8_t* __restrict__ k_packed,
+                                         uint32_t* __restrict__ k_side,
+                                         uint8_t* __restrict__ v_packed,
+                                         uint32_t* __restrict__ v_side) {
+    constexpr int VPL = D / 64;
+    using TT = T4Tab<D>;
+    const int64_t src = (int64_t)i * rs.row_stride + (int64_t)h * rs.head_stride;
+    const f16* row = (is_k ? rs.k : rs.v) + src;
+    float x[VPL];
+    if (is_k && rs.rope_dims > 0) {
+#pragma unroll
+        for (int j = 0; j < VPL; j++)
+            x[j] = (float)(f16)rope_elem(row, lane * VPL + j, rs.rope_dims, rs.traditional,
+                                         rs.log2_base, rs.scale, rs.position0 + i);
+    } else {
+#pragma unroll
+        for (int j = 0; j < VPL; j++) x[j] = (float)row[lane * VPL + j];
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPL; j++) ss = __builtin_fmaf(x[j], x[j], ss);
+    const float norm = sqrtf(t4_wave_sum(ss));
+    const float safe = norm > 0.0f ? norm : 1.0f;
+    const float* s1 = tab + (is_k ? TT::k_s1 : TT::v_s1);
+    const float* s2 = tab + (is_k ? TT::k_s2 : TT::v_s2);
+    float y[VPL];
+#pragma unroll
+    for (int j = 0; j < VPL; j++) y[j] = (x[j] / safe) * s1[lane * VPL + j];
+    wht_wave<D>(y, lane);
+    uint32_t idx[VPL];
+    float csq = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPL; j++) {
+        const float v = (y[j] * wht_scale(D)) * s2[lane * VPL + j];
+        uint32_t n = 0;
+#pragma unroll
+        for (int b = 0; b < 15; b++) n += v > tab[TT::bnd + b] ? 1u : 0u;
+        idx[j] = n;
+        const float c = cb[n];
+        csq = __builtin_fmaf(c, c, csq);
+    }
+    const float rn = sqrtf(t4_wave_sum(csq));
+    const f16 rescale = (f16)(norm / fmaxf(rn, 1e-10f));
+    const int t = t_old + i;
+    uint8_t* prow = (is_k ? k_packed : v_packed) + ((int64_t)h * cap + t) * (D / 2);
+    if constexpr (VPL == 4) {
+        const uint32_t b0 = idx[0] | (idx[1] << 4), b1 = idx[2] | (idx[3] << 4);
+        *(uint16_t*)(prow + 2 * lane) = (uint16_t)(b0 | (b1 << 8));
+    } else {
+        prow[lane] = (uint8_t)(idx[0] | (idx[1] << 4));
+    }
+    if (lane == 0) {
+        half2v sv;
+        if (is_k) {
+            sv.x = rescale;
+            sv.y = (f16)0.0f;
+            k_side[(int64_t)h * cap + t] = __builtin_bit_cast(uint32_t, sv);
+        } else {
+            sv.x = (f16)norm;
+            sv.y = rescale;
+            v_side[(int64_t)h * cap + t] = __builtin_bit_cast(uint32_t, sv);
         }
     }
 }

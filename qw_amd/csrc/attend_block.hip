@@ -166,7 +166,7 @@ __device__ __forceinline__ float wave_sum_g(float v) {
 // log2(e), scores stay fp32 in the log2 domain, P enters P.V as an fp16 high
 // part plus an fp16 remainder (fp32-exact products), and the partial maxima are
 // stored in natural units for the shared merge.
-template <int BITS, int D, int RT, bool FAST, int T4M = 0>
+template <int BITS, int D, int RT, bool FAST, int T4M = 0, bool APP = false>
 __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     using S = BlockShape<D>;
     constexpr int KT = S::KT, NSUB = S::NSUB, NM = S::NM, NT = S::NT, NG = S::NG;
@@ -182,8 +182,10 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     static_assert(PER * 64 * NW == KT * TPR && (KT / 8) * TPB == KT * TPR, "slices a thread");
 
     int sp, qt, h, n_split, tiles_per_split;
-    int key_lo = 0, key_hi = a.T;  // the keys this workgroup may see: [key_lo, key_hi)
-    if (a.n_app > 0) {
+    // APP (launches with n_app > 0): the keys this workgroup may see are
+    // [key_lo, key_hi); other launches compile without the bounds
+    int key_lo = 0, key_hi = a.T;
+    if (APP) {
         const int lin = blockIdx.x;
         qt = 0;
         n_split = a.n_split;
@@ -231,10 +233,12 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     constexpr int WROWS = 16 * RT;
     const int row0 = qt * WROWS * NW;
     const int row_last = min(a.R, row0 + WROWS * NW) - 1;
-    const int wg_lim = min(a.causal ? a.T - a.Tq + row_last / a.G : a.T - 1, key_hi - 1);
+    auto cut = [&](int lim_) { return APP ? min(lim_, key_hi - 1) : lim_; };
+    const bool app_unit = APP && key_lo > 0;
+    const int wg_lim = cut(a.causal ? a.T - a.Tq + row_last / a.G : a.T - 1);
     const int n_tiles = (a.T + KT - 1) / KT;
-    const int t0 = key_lo > 0 ? key_lo / KT : sp * tiles_per_split;
-    const int t1 = key_lo > 0 ? wg_lim / KT + 1 : min(min(n_tiles, t0 + tiles_per_split), wg_lim / KT + 1);
+    const int t0 = app_unit ? key_lo / KT : sp * tiles_per_split;
+    const int t1 = app_unit ? wg_lim / KT + 1 : min(min(n_tiles, t0 + tiles_per_split), wg_lim / KT + 1);
 
     // ---- the wave's RT x 16 query rows as the B operand of S^T = K . Q'^T
     // (col = query row r16 of row tile rt, k-group g = dims 32m + 8g .. +7 of
@@ -242,10 +246,10 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     const int wrow0 = row0 + WROWS * wave;
     const bool wave_live = wrow0 < a.R;
     const int wave_last = min(a.R, wrow0 + WROWS) - 1;
-    const int wave_lim = min(a.causal ? a.T - a.Tq + wave_last / a.G : a.T - 1, key_hi - 1);
+    const int wave_lim = cut(a.causal ? a.T - a.Tq + wave_last / a.G : a.T - 1);
     // the smallest key limit of the wave's live rows (padding rows see nothing
     // and are never written, so they do not count)
-    const int wave_first_lim = min(a.causal ? a.T - a.Tq + wrow0 / a.G : a.T - 1, key_hi - 1);
+    const int wave_first_lim = cut(a.causal ? a.T - a.Tq + wrow0 / a.G : a.T - 1);
     int lim[RT];
     bool row_ok[RT];
     half8 qb[RT][NM];
@@ -296,7 +300,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     for (int rt = 0; rt < RT; rt++) {
         const int rho = wrow0 + 16 * rt + r16;
         row_ok[rt] = rho < a.R;
-        lim[rt] = row_ok[rt] ? min(a.causal ? a.T - a.Tq + rho / a.G : a.T - 1, key_hi - 1) : -1;
+        lim[rt] = row_ok[rt] ? cut(a.causal ? a.T - a.Tq + rho / a.G : a.T - 1) : -1;
         const int rr = row_ok[rt] ? rho : 0;
         // (Turbo4 padding rows read the workgroup's first staged row; their scale is 0)
         const f16* qrow = T4 ? sq + (row_ok[rt] ? WROWS * wave + 16 * rt + r16 : 0) * D
@@ -537,7 +541,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         // Scores -> fp16 rounding -> (mask) -> online softmax -> P; the mask
         // only for tiles some row of the wave cannot fully see (a scalar
         // branch around the compares: the common case carries none).
-        const bool mask = kt0 + KT - 1 > wave_first_lim || kt0 < key_lo;
+        const bool mask = kt0 + KT - 1 > wave_first_lim || (APP && kt0 < key_lo);
         half8 popl[FUSED ? NSUB : 1][RT];  // fused pass: the remainders p - f16(p)
         auto softmax_fused = [&]() {
 #pragma unroll
@@ -554,7 +558,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
 #pragma unroll
                         for (int e = 0; e < 8; e++) {
                             const int key = kt0 + 32 * u + 8 * g + (e & 3) + 4 * (e >> 2);
-                            if (key > lim[rt] || key < key_lo) sf[u][e] = -INFINITY;
+                            if (key > lim[rt] || (APP && key < key_lo)) sf[u][e] = -INFINITY;
                         }
                 }
                 float mx_lane = sf[0][0];
@@ -615,7 +619,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
                             for (int e = 0; e < 2; e++) {
                                 const int idx = 2 * j + e;
                                 const int key = kt0 + 32 * u + 8 * g + (idx & 3) + 4 * (idx >> 2);
-                                if (key > lim[rt] || key < key_lo) sh[u][j][e] = (f16)(-INFINITY);
+                                if (key > lim[rt] || (APP && key < key_lo)) sh[u][j][e] = (f16)(-INFINITY);
                             }
                 }
                 // Online softmax with a lazy reference: m_run moves only when a
@@ -786,7 +790,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     }
 }
 
-template <int BITS, int D, int RT, int T4M = 0>
+template <int BITS, int D, int RT, int T4M = 0, bool APP = false>
 __global__ __launch_bounds__(64 * kBlockWaves, 1) void attend_block_kernel(BlockArgs a) {
     // two buffers, each a K and a V tile of KT keys in fp16 (~130 KB)
     extern __shared__ __attribute__((aligned(16))) char lds_buf[];
@@ -796,8 +800,8 @@ __global__ __launch_bounds__(64 * kBlockWaves, 1) void attend_block_kernel(Block
     // same output elements, so the second pass's writes replace the first's).
     // A null flag (Int8 caches) takes the separately rounded dequant directly.
     // Turbo4 caches have one expansion (a null flag).
-    if constexpr (BITS != 16 && T4M == 0) {
-        if (a.n_app > 0 && (int)blockIdx.x < a.n_app) {
+    if constexpr (APP && BITS != 16 && T4M == 0) {
+        if ((int)blockIdx.x < a.n_app) {
             // the new rows of head blockIdx.x go into the cache first (the
             // append kernel's work, 8-token V block by block); this
             // workgroup's tiles then read them back, and its fast-flag check
@@ -813,27 +817,40 @@ __global__ __launch_bounds__(64 * kBlockWaves, 1) void attend_block_kernel(Block
             }
         }
     }
+    if constexpr (APP && T4M != 0) {
+        if ((int)blockIdx.x < a.n_app) {
+            // Turbo4: the 2L row appends (K and V of each new token) of head
+            // blockIdx.x, a wave a row
+            const int L = a.T - a.T_pre;
+            for (int job = (int)threadIdx.x >> 6; job < 2 * L; job += kBlockWaves)
+                turbo4_append_row<D>(a.app, job >> 1, blockIdx.x, (job & 1) == 0, threadIdx.x & 63,
+                                     a.T_pre, a.cap, a.t4_tab, a.t4_tab + T4Tab<D>::cb,
+                                     (uint8_t*)a.k_data, (uint32_t*)a.k_params, (uint8_t*)a.v_data,
+                                     (uint32_t*)a.v_params);
+            __syncthreads();
+        }
+    }
     if (T4M == 0 && (BITS == 16 || a.fast_flag != nullptr)) {
-        block_body<BITS, D, RT, true>(a, lds_buf);
+        block_body<BITS, D, RT, true, 0, APP>(a, lds_buf);
         if (BITS != 16 && *a.fast_flag == 0) {
             __syncthreads();
-            block_body<BITS, D, RT, false>(a, lds_buf);
+            block_body<BITS, D, RT, false, 0, APP>(a, lds_buf);
         }
     } else {
-        block_body<BITS, D, RT, false, T4M>(a, lds_buf);
+        block_body<BITS, D, RT, false, T4M, APP>(a, lds_buf);
     }
 }
 
-template <int BITS, int D, int RT, int T4M>
+template <int BITS, int D, int RT, int T4M, bool APP = false>
 static int launch_block_rt(KVCache& cc, BlockArgs& a, int n_qt, hipStream_t stream) {
     // two tile buffers (+ the Turbo4 centroid-pair table)
     const size_t shmem = (size_t)2 * BlockShape<D>::BUF + (T4M ? 256 * sizeof(float2) : 0);
-    int rc = ensure_dynamic_lds((const void*)attend_block_kernel<BITS, D, RT, T4M>, shmem);
+    int rc = ensure_dynamic_lds((const void*)attend_block_kernel<BITS, D, RT, T4M, APP>, shmem);
     if (rc) return rc;
     const dim3 grid = a.n_app > 0    ? dim3(a.n_app + cc.hkv * (a.n_split - 1))
                       : a.n_main > 0 ? dim3(a.n_main + n_qt * cc.hkv * a.n_split)
                                      : dim3(a.n_split, n_qt, cc.hkv);
-    hipLaunchKernelGGL((attend_block_kernel<BITS, D, RT, T4M>), grid, dim3(64 * kBlockWaves), shmem,
+    hipLaunchKernelGGL((attend_block_kernel<BITS, D, RT, T4M, APP>), grid, dim3(64 * kBlockWaves), shmem,
                        stream, a);
     QW_HIP_CHECK(hipGetLastError());
     return QW_OK;
@@ -1012,10 +1029,10 @@ int launch_block_attention_t4(KVCache& cc, const f16* q, int G, int n_rows, floa
 // append workgroups leave free; every row sees the whole prefix, so the
 // prefix splits need no causal cut and the partial slot of the new keys
 // carries it.
-template <int BITS, int D>
+template <int BITS, int D, int T4M = 0>
 static int launch_block_append_bits(KVCache& cc, const f16* q, int G, int L, const f16* k_new,
                                     const f16* v_new, float scale, bool causal, f16* out,
-                                    hipStream_t stream) {
+                                    hipStream_t stream, const float* t4_tab = nullptr) {
     using S = BlockShape<D>;
     const int T_pre = cc.offset, T = T_pre + L, R = G * L;
     BlockArgs a;
@@ -1023,11 +1040,11 @@ static int launch_block_append_bits(KVCache& cc, const f16* q, int G, int L, con
     a.k_params = cc.k_params;
     a.v_data = (const uint32_t*)cc.v_data;
     a.v_params = cc.v_params;
-    a.fast_flag = cc.int8() ? nullptr : cc.fast_flag;
+    a.fast_flag = cc.int8() || T4M ? nullptr : cc.fast_flag;
     a.q = q;
     a.out = out;
-    a.t4_tab = nullptr;
-    a.t4_post = 0.0f;
+    a.t4_tab = t4_tab;
+    a.t4_post = scale * 1.4426950408889634f;
     a.cap = cc.cap;
     a.T = T;
     a.Tq = L;
@@ -1051,7 +1068,9 @@ static int launch_block_append_bits(KVCache& cc, const f16* q, int G, int L, con
     a.app.row_stride = D;
     a.app.head_stride = (int64_t)L * D;
     int n_pre, tps;
-    split_keys((T_pre + S::KT - 1) / S::KT, std::max(1, (256 - cc.hkv) / cc.hkv), &n_pre, &tps);
+    // (the Turbo4 fused pass's merge takes up to 128 partials)
+    const int want = std::max(1, (256 - cc.hkv) / cc.hkv);
+    split_keys((T_pre + S::KT - 1) / S::KT, T4M == 2 ? std::min(want, 127) : want, &n_pre, &tps);
     a.n_split = n_pre + 1;
     a.tiles_per_split = tps;
     const size_t o_bytes = (size_t)cc.hkv * a.n_split * R * D * sizeof(float);
@@ -1059,11 +1078,14 @@ static int launch_block_append_bits(KVCache& cc, const f16* q, int G, int L, con
     if (rc) return rc;
     a.part_o = (float*)cc.ws_ptr;
     a.part_ml = (float2*)((char*)cc.ws_ptr + o_bytes);
-    rc = launch_one<BITS, D, 0>(cc, a, 1, 1, stream);
+    rc = launch_block_rt<BITS, D, 1, T4M, true>(cc, a, 1, stream);
     if (rc) return rc;
     cc.offset = T;
+    if (T4M == 2)
+        return launch_t4_merge_rotate(a.part_o, a.part_ml, a.n_split, R, R, cc.hkv, D, G, L, 16, true,
+                                      t4_tab, out, stream);
     return launch_partial_merge(a.part_o, a.part_ml, a.n_split, R, 0, R, cc.hkv, D, G, L, out,
-                                stream, BITS);
+                                stream, T4M ? 16 : BITS);
 }
 
 bool block_append_fits(const KVCache& cc, int G, int L) {
@@ -1085,6 +1107,23 @@ int launch_block_append_attention(KVCache& cc, const f16* q, int G, int L, const
                                                            out, stream)
                         : launch_block_append_bits<8, 128>(cc, q, G, L, k_new, v_new, scale, causal,
                                                            out, stream);
+}
+
+int launch_block_append_attention_t4(KVCache& cc, const f16* q, int G, int L, const f16* k_new,
+                                     const f16* v_new, float scale, bool causal, bool fused,
+                                     const float* tab, f16* out, hipStream_t stream) {
+    QW_REQUIRE(cc.turbo4() && G * L <= 16 * kBlockWaves && cc.offset >= 256 &&
+                   cc.offset + L <= cc.cap,
+               QW_ERR_INVALID_ARGUMENT, "block attention: Turbo4 block outside the fused-append shapes");
+    if (cc.D == 256)
+        return fused ? launch_block_append_bits<4, 256, 2>(cc, q, G, L, k_new, v_new, scale, causal,
+                                                           out, stream, tab)
+                     : launch_block_append_bits<4, 256, 1>(cc, q, G, L, k_new, v_new, scale, causal,
+                                                           out, stream, tab);
+    return fused ? launch_block_append_bits<4, 128, 2>(cc, q, G, L, k_new, v_new, scale, causal, out,
+                                                       stream, tab)
+                 : launch_block_append_bits<4, 128, 1>(cc, q, G, L, k_new, v_new, scale, causal, out,
+                                                       stream, tab);
 }
 
 int launch_block_attention(KVCache& cc, const f16* q, int G, int n_rows, float scale, bool causal,

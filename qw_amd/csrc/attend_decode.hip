@@ -1302,6 +1302,9 @@ int KVCache::update_and_attention(const void* q, int n_q_heads, int n_rows, cons
     QW_REQUIRE(n_q_heads > 0 && n_q_heads % hkv == 0 && n_rows > 0, QW_ERR_INVALID_ARGUMENT,
                "update_and_attention: bad head or row geometry");
     const int G = n_q_heads / hkv;
+    if (turbo4())
+        return turbo4_update_and_attention(*this, q, n_q_heads, n_rows, k_new, v_new, scale, causal,
+                                           out, stream);
     if (QW_FUSED_DECODE_APPEND && affine() && n_rows == 1 && G <= 16) {
         // decode: the append rides in the split-K merge (one launch fewer)
         DeviceGuard dg(device);

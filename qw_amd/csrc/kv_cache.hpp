@@ -197,6 +197,17 @@ int launch_block_attention(KVCache& c, const f16* q, int G, int n_rows, float sc
 // over the cache including them, as update + launch_block_attention would.
 // block_append_fits: the shapes it takes; the caller reserves the capacity.
 bool block_append_fits(const KVCache& c, int G, int n_rows);
+// The same for a Turbo4 cache (one query tile, at least 256 cached rows,
+// capacity reserved): fused as launch_block_attention_t4's fused pass (out:
+// the rows rotated back), else its fp16 arithmetic (out: rotated-basis rows).
+int launch_block_append_attention_t4(KVCache& c, const f16* q, int G, int n_rows, const f16* k_new,
+                                     const f16* v_new, float scale, bool causal, bool fused,
+                                     const float* tab, f16* out, hipStream_t stream);
+// Turbo4 update-and-attention: the append in the block kernel's launch where
+// the call takes the block kernel, else turbo4_update then turbo4_attention.
+int turbo4_update_and_attention(KVCache& c, const void* q, int n_q_heads, int n_rows,
+                                const void* k_new, const void* v_new, float scale, bool causal,
+                                void* out, hipStream_t stream);
 int launch_block_append_attention(KVCache& c, const f16* q, int G, int n_rows, const f16* k_new,
                                   const f16* v_new, float scale, bool causal, f16* out,
                                   hipStream_t stream);

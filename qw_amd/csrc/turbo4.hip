@@ -31,6 +31,7 @@
 
 #include <utility>
 
+#include "append.hpp"
 #include "kv_cache.hpp"
 #include "rope.hpp"
 #include "turbo4_device.hpp"
@@ -39,12 +40,6 @@ namespace qw {
 
 namespace {
 
-
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
-    return x;
-}
 
 // f16 of an fp32 product, rounded first to fp32 (the reference multiplies in
 // fp32 and then casts); the register pin keeps the compiler from fusing the
@@ -60,81 +55,16 @@ __device__ __forceinline__ f16 f16_of_product(float a, float b) {
 // ------------------------------------------------------------ append
 //
 // grid (n_tokens, hkv), 2 waves: wave 0 quantizes the K row (K signs), wave 1
-// the V row (V signs). K may be rotated by RoPE as it is read (RowSrc).
+// the V row (V signs); turbo4_append_row holds the steps.
 template <int D>
 __global__ __launch_bounds__(128) void turbo4_append_kernel(
     RowSrc rs, int t_old, int cap, const float* __restrict__ tab, uint8_t* __restrict__ k_packed,
     uint32_t* __restrict__ k_side, uint8_t* __restrict__ v_packed, uint32_t* __restrict__ v_side) {
-    constexpr int VPL = D / 64;
-    using TT = T4Tab<D>;
     __shared__ float s_cb[16];
-    if (threadIdx.x < 16) s_cb[threadIdx.x] = tab[TT::cb + threadIdx.x];
+    if (threadIdx.x < 16) s_cb[threadIdx.x] = tab[T4Tab<D>::cb + threadIdx.x];
     __syncthreads();
-    const int i = blockIdx.x, h = blockIdx.y;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const bool is_k = wave == 0;
-    const int64_t src = (int64_t)i * rs.row_stride + (int64_t)h * rs.head_stride;
-    const f16* row = (is_k ? rs.k : rs.v) + src;
-
-    float x[VPL];
-    if (is_k && rs.rope_dims > 0) {
-#pragma unroll
-        for (int j = 0; j < VPL; j++)
-            x[j] = (float)(f16)rope_elem(row, lane * VPL + j, rs.rope_dims, rs.traditional,
-                                         rs.log2_base, rs.scale, rs.position0 + i);
-    } else {
-#pragma unroll
-        for (int j = 0; j < VPL; j++) x[j] = (float)row[lane * VPL + j];
-    }
-    // 1. L2 norm in fp32; an all-zero row divides by 1
-    float ss = 0.0f;
-#pragma unroll
-    for (int j = 0; j < VPL; j++) ss = __builtin_fmaf(x[j], x[j], ss);
-    const float norm = sqrtf(wave_sum(ss));
-    const float safe = norm > 0.0f ? norm : 1.0f;
-    // 2. signs2 . H . signs1 of the unit row
-    const float* s1 = tab + (is_k ? TT::k_s1 : TT::v_s1);
-    const float* s2 = tab + (is_k ? TT::k_s2 : TT::v_s2);
-    float y[VPL];
-#pragma unroll
-    for (int j = 0; j < VPL; j++) y[j] = (x[j] / safe) * s1[lane * VPL + j];
-    wht_wave<D>(y, lane);
-    // 3. nearest centroid: the number of boundaries strictly below the value
-    uint32_t idx[VPL];
-    float csq = 0.0f;
-#pragma unroll
-    for (int j = 0; j < VPL; j++) {
-        const float v = (y[j] * wht_scale(D)) * s2[lane * VPL + j];
-        uint32_t n = 0;
-#pragma unroll
-        for (int b = 0; b < 15; b++) n += v > tab[TT::bnd + b] ? 1u : 0u;
-        idx[j] = n;
-        const float c = s_cb[n];
-        csq = __builtin_fmaf(c, c, csq);
-    }
-    const float rn = sqrtf(wave_sum(csq));
-    const f16 rescale = (f16)(norm / fmaxf(rn, 1e-10f));
-    // 4. pack: low nibble = even coordinate
-    const int t = t_old + i;
-    uint8_t* prow = (is_k ? k_packed : v_packed) + ((int64_t)h * cap + t) * (D / 2);
-    if constexpr (VPL == 4) {
-        const uint32_t b0 = idx[0] | (idx[1] << 4), b1 = idx[2] | (idx[3] << 4);
-        *(uint16_t*)(prow + 2 * lane) = (uint16_t)(b0 | (b1 << 8));
-    } else {
-        prow[lane] = (uint8_t)(idx[0] | (idx[1] << 4));
-    }
-    if (lane == 0) {
-        half2v sv;
-        if (is_k) {
-            sv.x = rescale;
-            sv.y = (f16)0.0f;
-            k_side[(int64_t)h * cap + t] = __builtin_bit_cast(uint32_t, sv);
-        } else {
-            sv.x = (f16)norm;
-            sv.y = rescale;
-            v_side[(int64_t)h * cap + t] = __builtin_bit_cast(uint32_t, sv);
-        }
-    }
+    turbo4_append_row<D>(rs, blockIdx.x, blockIdx.y, (threadIdx.x >> 6) == 0, threadIdx.x & 63, t_old,
+                         cap, tab, s_cb, k_packed, k_side, v_packed, v_side);
 }
 
 // ------------------------------------------------------------ fetch
@@ -184,7 +114,7 @@ __global__ __launch_bounds__(128) void turbo4_fetch_kernel(
             y[j] = s_cb[idx[j]];
             csq = __builtin_fmaf(y[j], y[j], csq);
         }
-        const float yn = fmaxf(sqrtf(wave_sum(csq)), 1e-10f);
+        const float yn = fmaxf(sqrtf(t4_wave_sum(csq)), 1e-10f);
 #pragma unroll
         for (int j = 0; j < VPL; j++) y[j] = y[j] / yn;
         mul = (float)side.x;
@@ -223,6 +153,11 @@ __global__ __launch_bounds__(128) void turbo4_fetch_kernel(
 #define QW_T4_BLOCK 1
 #endif
 constexpr int kT4BlockRows = 1024;
+// 1: update-and-attention calls that take the block kernel with one query tile
+// append their rows inside its launch; 0: the append kernel first.
+#ifndef QW_T4_APPEND
+#define QW_T4_APPEND 1
+#endif
 constexpr int kExpandBlocks = 4;  // 8-key blocks a workgroup (capv / 8 is a multiple of 32)
 
 template <int D>
@@ -876,6 +811,50 @@ static int turbo4_block(KVCache& c, const void* q, int n_q_heads, int n_rows, fl
     f16* o_r = (f16*)wbuf;
     int rc = launch_block_attention_t4(c, (const f16*)q, G, n_rows, scale, causal, false, tab, o_r,
                                        stream);
+    if (rc) return rc;
+    const dim3 rg((qrows + 3) / 4);
+    if (D == 256) {
+        using TT = T4Tab<256>;
+        hipLaunchKernelGGL(turbo4_rotate_kernel<256>, rg, dim3(256), 0, stream, (const f16*)o_r,
+                           (f16*)out, qrows, tab + TT::v_s2, tab + TT::v_s1);
+    } else {
+        using TT = T4Tab<128>;
+        hipLaunchKernelGGL(turbo4_rotate_kernel<128>, rg, dim3(256), 0, stream, (const f16*)o_r,
+                           (f16*)out, qrows, tab + TT::v_s2, tab + TT::v_s1);
+    }
+    QW_HIP_CHECK(hipGetLastError());
+    return QW_OK;
+}
+
+int turbo4_update_and_attention(KVCache& c, const void* q, int n_q_heads, int n_rows,
+                                const void* k_new, const void* v_new, float scale, bool causal,
+                                void* out, hipStream_t stream) {
+    const int G = n_q_heads / c.hkv, T = c.offset + n_rows;
+    // the routes of turbo4_attention below that take the block kernel
+    const bool fused = causal && n_rows <= 5 && T > 2048 && G * n_rows <= kT4vRows;
+    const bool block = fused || (G * n_rows > 16 && G * n_rows <= 16 * 8);
+    if (!(QW_T4_APPEND && QW_T4_BLOCK && block && c.offset >= 256)) {
+        int rc = c.update(k_new, v_new, n_rows, stream);
+        if (rc) return rc;
+        return turbo4_attention(c, q, n_q_heads, n_rows, scale, causal, out, stream);
+    }
+    DeviceGuard dg(c.device);
+    QW_REQUIRE(dg.ok, QW_ERR_HIP, "attention: hipSetDevice failed");
+    if (T > c.cap) {
+        int rc = c.reserve(std::max(T, c.cap + c.cap / 2), stream);
+        if (rc) return rc;
+    }
+    const float* tab = c.t4_tables;
+    const f16 *qq = (const f16*)q, *kn = (const f16*)k_new, *vn = (const f16*)v_new;
+    if (fused)
+        return launch_block_append_attention_t4(c, qq, G, n_rows, kn, vn, scale, causal, true, tab,
+                                                (f16*)out, stream);
+    const int D = c.D, qrows = n_q_heads * n_rows;
+    void* wbuf = nullptr;
+    if (int rc0 = t4_workspace(c.device, stream, (size_t)qrows * D * sizeof(f16), &wbuf)) return rc0;
+    f16* o_r = (f16*)wbuf;
+    int rc = launch_block_append_attention_t4(c, qq, G, n_rows, kn, vn, scale, causal, false, tab,
+                                              o_r, stream);
     if (rc) return rc;
     const dim3 rg((qrows + 3) / 4);
     if (D == 256) {

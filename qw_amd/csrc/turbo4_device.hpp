@@ -21,6 +21,14 @@ __host__ __device__ constexpr float wht_scale(int D) {
     return D == 256 ? 0.0625f : (D == 128 ? 0.08838834764831845f : 0.0f);
 }
 
+// Sum over the wave by an xor butterfly (offsets 32, 16, ..., 1): the order
+// every Turbo4 norm is formed in, so all kernels store the same rescales.
+__device__ __forceinline__ float t4_wave_sum(float x) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+    return x;
+}
+
 // In-place fp32 Walsh-Hadamard transform of the wave's row (lane holds
 // coordinates lane * VPL .. lane * VPL + VPL - 1), unscaled: log2(VPL)
 // butterfly stages inside the lane, then six across lanes.

@@ -277,6 +277,37 @@ def test_turbo4_attention_without_append_and_reuse():
     np.testing.assert_array_equal(_np(cache.attention(_gpu(q), 1.0 / 16))[0], out)
 
 
+@pytest.mark.parametrize("T0,L,causal,D", [
+    (3000, 4, True, 256),     # the fused verify pass, its rows appended in the block launch
+    (2040, 3, True, 256),     # below the gate: the fp16 arithmetic in the block kernel, likewise
+    (1000, 16, True, 128),    # 96 rows a KV head at head_dim 128
+    (600, 5, False, 256),     # non-causal block
+])
+def test_turbo4_append_in_launch_equals_separate_update(T0, L, causal, D):
+    """Update-and-attention calls that take the block kernel append their rows
+    inside its launch: the cache then holds exactly what one bulk update
+    stores (every snapshot tensor equal bit for bit), and the output equals
+    attending the updated cache, within the stated tolerance."""
+    import qw_amd
+
+    r = rng(8100 + T0 + L + D)
+    k, v = _kv(r, 4, T0 + L, D)
+    q = r.standard_normal((24, L, D)).astype(np.float16)
+    a = qw_amd.KVCache("turbo4", 4, D)
+    a.update(_gpu(k[:, :T0]), _gpu(v[:, :T0]))
+    fn = a.update_and_causal_attention if causal else a.update_and_attention
+    o1 = _np(fn(_gpu(q), _gpu(k[:, T0:]), _gpu(v[:, T0:]), 1.0 / 16))[0]
+    b = qw_amd.KVCache("turbo4", 4, D)
+    b.update(_gpu(k), _gpu(v))
+    o2 = _np(b.attention(_gpu(q), 1.0 / 16, causal))[0]
+    assert a.offset == b.offset == T0 + L
+    sa, sb = a.snapshot_tensors(), b.snapshot_tensors()
+    for name, t in sa.items():
+        assert torch.equal(t, sb[name]), name
+    assert np.isfinite(o1).all()
+    assert_close(o1, o2, f"turbo4 D{D} T{T0}+{L} causal={causal}: append in launch vs cached")
+
+
 def test_turbo4_snapshot_trim_and_seed():
     import qw_amd
 
