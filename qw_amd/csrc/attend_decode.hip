@@ -32,6 +32,7 @@
 #include <algorithm>
 #include <type_traits>
 
+#include "append.hpp"
 #include "dequant.hpp"
 #include "quant.hpp"
 #include "kv_cache.hpp"
@@ -52,6 +53,12 @@ struct DecodeArgs {
     float scale_h;     // f16(scale) as float
     uint32_t code_off2;  // magic offset pair of the separately rounded dequant
     const float* t4_tab;  // Turbo4 caches: the device tables (signs, centroids); else null
+    // ns: workgroups that split the T cached keys (= nc, or nc - 1 with an
+    // append unit). app_L > 0: workgroup (ns, h) is the append unit of head h:
+    // it appends the app_L new rows read through app (keys T .. T + app_L - 1)
+    // and writes their partial, slot ns, with the causal cut when app_causal.
+    int ns, app_L, app_causal, app_int8;
+    RowSrc app;
 };
 
 template <int BITS, int D>
@@ -145,16 +152,16 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
     const int lane = threadIdx.x & 63;
     const int r16 = lane & 15, g = lane >> 4;
     // Sub-chunks are dealt round-robin: workgroup c, wave w, round k owns
-    // sub-chunk c + nc * (w + NW * k). At any moment the workgroups of a head
+    // sub-chunk c + ns * (w + NW * k). At any moment the workgroups of a head
     // stream adjacent 4 KB blocks, spreading the reads over all HBM channels
     // (contiguous per-workgroup ranges put the 64 workgroups of a head on a
     // few channel phases at once).
-    const int SS = a.nc * NW;  // stride between a wave's sub-chunks
+    const int SS = a.ns * NW;  // stride between a wave's sub-chunks
     const int s_end = a.n_sub;
     const uint32_t magic = vconst(kMagic);
 
     // One 32-key sub-chunk's loads; a wave walks its sub-chunks
-    // c + nc * (wave + NW * k) through one of these.
+    // c + ns * (wave + NW * k) through one of these.
     // T4: vc holds the DPL/2-byte row pieces of keys 8g..8g+7 (two keys a
     // u32x4 at D = 256, four at D = 128), vp the 8 keys' V side words, kp[t].x
     // the K side word of the lane's key.
@@ -322,7 +329,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
             base = 32 * m + 8 * g;
         x = *(const half8*)(qrow + base);
     }
-    int s = c + a.nc * wave;
+    int s = c + a.ns * wave;
     Stage A, B;
     // The first sub-chunk's loads go out right behind Q (loads return in
     // issue order, so the Q conversion below waits for Q only).
@@ -613,7 +620,132 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
     }
 }
 
-template <int BITS, int D, bool T4 = false>
+// LDS the append unit needs: an 8-token block's append scratch, then the new
+// keys' K and V values (fp16, [app_L][D] each).
+template <int D>
+constexpr size_t decode_append_lds(int L) {
+    return (sizeof(AppendScratch<D>) + 15) / 16 * 16 + (size_t)4 * L * D;
+}
+
+// The append unit of a decode launch (DecodeArgs::app_L > 0), workgroup
+// (ns, h). It appends head h's new rows (the append kernels' work), reads
+// them back as the decode kernel would (affine and Int8: f16(f16(c s) + b)
+// and f16(c s); Turbo4: f16(centroid rescale) in the rotated basis), and
+// writes the new keys' partial for every row of the launch in the decode
+// kernel's arithmetic: q' = f16(f16(scale) q) (Turbo4: q rotated first), the
+// score rounded to fp16, the weights exp(s - m) summed in fp32 and rounded to
+// fp16 for P.V. Wave w takes rows w, w + NW, ...
+template <int BITS, int D, bool T4>
+__device__ void decode_append_unit(const DecodeArgs& a, char* lds) {
+    constexpr int NW = decode_waves<BITS, D>();
+    constexpr int VPL = D / 64, NG = D / 64;
+    const int h = blockIdx.y, L = a.app_L, T0 = a.T;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    if constexpr (T4) {
+        for (int job = wave; job < 2 * L; job += NW)
+            turbo4_append_row<D>(a.app, job >> 1, h, (job & 1) == 0, lane, T0, a.cap, a.t4_tab,
+                                 a.t4_tab + T4Tab<D>::cb, (uint8_t*)a.k_data, (uint32_t*)a.k_params,
+                                 (uint8_t*)a.v_data, (uint32_t*)a.v_params);
+    } else {
+        auto& sc = *reinterpret_cast<AppendScratch<D>*>(lds);
+        for (int blk = T0 / 8; blk <= (T0 + L - 1) / 8; blk++) {
+            append_block<D>(a.app, L, T0, BITS, a.app_int8 != 0, a.cap, (uint32_t*)a.k_data,
+                            (uint32_t*)a.k_params, (uint32_t*)a.v_data, (f16*)a.v_params,
+                            (int*)a.fast_flag, blk, h, tid, 64 * NW, sc);
+            __syncthreads();
+        }
+    }
+    __syncthreads();
+    // the new keys' values, read back from the cache
+    f16* sk = (f16*)(lds + (sizeof(AppendScratch<D>) + 15) / 16 * 16);
+    f16* sv = sk + L * D;
+    for (int i = tid; i < L * D; i += 64 * NW) {
+        const int j = i / D, d = i % D, t = T0 + j;
+        const int64_t kr = (int64_t)h * a.cap + t;
+        const int blk = t / 8, k = t % 8;
+        f16 kv, vv;
+        if constexpr (T4) {
+            using TT = T4Tab<D>;
+            const uint8_t kb = ((const uint8_t*)a.k_data)[kr * (D / 2) + d / 2];
+            const uint8_t vb = ((const uint8_t*)a.v_data)[kr * (D / 2) + d / 2];
+            const half2v ks = __builtin_bit_cast(half2v, a.k_params[kr]);
+            const half2v vs = __builtin_bit_cast(half2v, a.v_params[kr]);
+            const int sh = 4 * (d & 1);
+            kv = t4_f16_product(a.t4_tab[TT::cb + ((kb >> sh) & 15)], (float)ks.x);
+            vv = t4_f16_product(a.t4_tab[TT::cb + ((vb >> sh) & 15)], (float)vs.y);
+        } else {
+            constexpr int EPW = 32 / BITS;
+            constexpr uint32_t MASK = (1u << BITS) - 1;
+            const uint32_t kw = a.k_data[kr * (D * BITS / 32) + d / EPW];
+            const float kc = (float)((kw >> (BITS * (d % EPW))) & MASK);
+            const half2v ksb = __builtin_bit_cast(half2v, a.k_params[kr * NG + k_param_slot(d / 64, NG)]);
+            const int p = v_phys_dim(d, D, BITS);
+            const uint32_t* vbw = a.v_data + ((int64_t)h * (a.cap / 8) + blk) * (D * BITS / 4);
+            const float vc = BITS == 4 ? (float)((vbw[p] >> (4 * v4_nibble_pos(k))) & 15u)
+                                       : (float)((vbw[2 * p + (k >> 2)] >> (8 * (k & 3))) & 255u);
+            const f16* vpp = (const f16*)a.v_params + (((int64_t)h * (a.cap / 8) + blk) * NG + d / 64) * 16;
+            if (a.app_int8) {
+                kv = (f16)((kc - 128.0f) * (float)ksb.x);
+                vv = (f16)((vc - 128.0f) * (float)vpp[k]);
+            } else {
+                kv = (f16)affine_dequant(kc, ksb.x, ksb.y);
+                vv = (f16)affine_dequant(vc, vpp[k], vpp[8 + k]);
+            }
+        }
+        sk[i] = kv;
+        sv[i] = vv;
+    }
+    __syncthreads();
+    const int64_t pbase = ((int64_t)h * a.nc + a.ns) * 16;
+    for (int rho = wave; rho < a.R; rho += NW) {
+        const int l = rho / a.G;
+        const f16* qrow = a.q + ((int64_t)(h * a.G + rho % a.G) * a.Tq + l) * D;
+        float qv[VPL];
+#pragma unroll
+        for (int i = 0; i < VPL; i++) qv[i] = (float)qrow[lane * VPL + i];
+        if constexpr (T4) {
+            f16 o[VPL];
+            t4_rotate_row<D>(qv, lane, a.t4_tab + T4Tab<D>::k_s1, a.t4_tab + T4Tab<D>::k_s2, o);
+#pragma unroll
+            for (int i = 0; i < VPL; i++) qv[i] = (float)o[i];
+        }
+#pragma unroll
+        for (int i = 0; i < VPL; i++) qv[i] = (float)(f16)(a.scale_h * qv[i]);
+        const int n_vis = a.app_causal ? l + 1 : L;
+        float sc[16];
+        float m = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            sc[j] = -INFINITY;
+            if (j < n_vis) {
+                float dot = 0.0f;
+#pragma unroll
+                for (int i = 0; i < VPL; i++)
+                    dot = __builtin_fmaf(qv[i], (float)sk[j * D + lane * VPL + i], dot);
+                sc[j] = (float)(f16)t4_wave_sum(dot);
+                m = fmaxf(m, sc[j]);
+            }
+        }
+        float o[VPL] = {};
+        float lsum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            if (j < n_vis) {
+                const float pj = __builtin_amdgcn_exp2f((sc[j] - m) * kLog2e);
+                lsum += pj;
+                const float ph = (float)(f16)pj;
+#pragma unroll
+                for (int i = 0; i < VPL; i++)
+                    o[i] = __builtin_fmaf(ph, (float)sv[j * D + lane * VPL + i], o[i]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < VPL; i++) a.part_o[(pbase + rho) * D + lane * VPL + i] = o[i];
+        if (lane == 0) a.part_ml[pbase + rho] = float2{m, lsum};
+    }
+}
+
+template <int BITS, int D, bool T4 = false, bool APP = false>
 __global__ __launch_bounds__((64 * decode_waves<BITS, D>()), 1) void attend_decode_kernel(
     DecodeArgs a) {
     constexpr int NW = decode_waves<BITS, D>();
@@ -630,6 +762,12 @@ __global__ __launch_bounds__((64 * decode_waves<BITS, D>()), 1) void attend_deco
     // null flag (Int8 caches, which always take the separately rounded
     // dequant) goes to that path directly.
     // Turbo4 caches have one dequant (a null flag).
+    if constexpr (APP && BITS != 16) {
+        if ((int)blockIdx.x == a.ns) {
+            decode_append_unit<BITS, D, T4>(a, (char*)sm_o);
+            return;
+        }
+    }
     if (!T4 && (BITS == 16 || a.fast_flag != nullptr)) {
         decode_body<BITS, D, NW, true>(a, sm_ml, sm_o, sm_q);
         if (BITS != 16 && *a.fast_flag == 0) {
@@ -721,7 +859,9 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
 template <int BITS, int D, bool T4 = false>
 static int launch_decode_partials(KVCache& cc, const f16* q, int G, int Tq, int T, float scale,
                                   bool causal, int* nc_out, float** po, float2** pml,
-                                  hipStream_t stream, const float* t4_tab = nullptr) {
+                                  hipStream_t stream, const float* t4_tab = nullptr,
+                                  const f16* k_new = nullptr, const f16* v_new = nullptr,
+                                  int app_L = 0, bool app_causal = false) {
     const int n_sub = (T + 31) / 32;
     // Sub-chunks a wave owns: 4-bit rows are small enough to keep 4 in flight.
     // Sub-chunks a wave keeps in flight per round, and workgroups per KV head:
@@ -729,10 +869,13 @@ static int launch_decode_partials(KVCache& cc, const f16* q, int G, int Tq, int 
     // context allows, at most 1024 partials per head.
     // One workgroup a CU (256 CUs), at least a wave's worth of sub-chunks each.
     constexpr int NW = decode_waves<BITS, D>();
-    const int per_head = std::max(1, 256 / cc.hkv);
+    // an append unit (app_L > 0) takes one workgroup slot a head
+    const int app = app_L > 0 ? 1 : 0;
+    const int per_head = std::max(1, 256 / cc.hkv - app);
     // Turbo4: at most 128 partials a head (its merge kernel sums up to 32 a thread)
-    const int nc_cap = T4 ? 128 : 4 * kMergeMaxPer;
-    const int nc = std::max(1, std::min({per_head, (n_sub + NW - 1) / NW, nc_cap}));
+    const int nc_cap = (T4 ? 128 : 4 * kMergeMaxPer) - app;
+    const int ns = std::max(1, std::min({per_head, (n_sub + NW - 1) / NW, nc_cap}));
+    const int nc = ns + app;
     const size_t need = (size_t)cc.hkv * nc * 16 * D * sizeof(float) +
                         (size_t)cc.hkv * nc * 16 * sizeof(float2);
     int rc = cc.ensure_workspace(need, stream);
@@ -755,14 +898,31 @@ static int launch_decode_partials(KVCache& cc, const f16* q, int G, int Tq, int 
     a.causal = causal ? 1 : 0;
     a.n_sub = n_sub;
     a.nc = nc;
+    a.ns = ns;
     a.scale_h = (float)(f16)scale;
     a.code_off2 = cc.code_offset2();
+    a.app_L = app_L;
+    a.app_causal = app_causal ? 1 : 0;
+    a.app_int8 = cc.int8() ? 1 : 0;
+    a.app = RowSrc{};
+    a.app.k = k_new;
+    a.app.v = v_new;
+    a.app.row_stride = D;
+    a.app.head_stride = (int64_t)app_L * D;
     size_t shmem = (size_t)NW * (D / 16) * (((a.R + 3) / 4) * 16 + 1) * 16;  // wave-merge sm_o
     // Dynamic LDS above 64 KB must be allowed per kernel and device.
-    rc = ensure_dynamic_lds((const void*)attend_decode_kernel<BITS, D, T4>, shmem);
-    if (rc) return rc;
-    hipLaunchKernelGGL((attend_decode_kernel<BITS, D, T4>), dim3(nc, cc.hkv), dim3(64 * NW), shmem,
-                       stream, a);
+    if (app) {
+        shmem = std::max(shmem, decode_append_lds<D>(app_L));
+        rc = ensure_dynamic_lds((const void*)attend_decode_kernel<BITS, D, T4, true>, shmem);
+        if (rc) return rc;
+        hipLaunchKernelGGL((attend_decode_kernel<BITS, D, T4, true>), dim3(nc, cc.hkv), dim3(64 * NW),
+                           shmem, stream, a);
+    } else {
+        rc = ensure_dynamic_lds((const void*)attend_decode_kernel<BITS, D, T4>, shmem);
+        if (rc) return rc;
+        hipLaunchKernelGGL((attend_decode_kernel<BITS, D, T4>), dim3(nc, cc.hkv), dim3(64 * NW),
+                           shmem, stream, a);
+    }
     QW_HIP_CHECK(hipGetLastError());
     *nc_out = nc;
     *po = a.part_o;
@@ -897,6 +1057,43 @@ int launch_t4_merge_rotate(const float* po, const float2* pml, int nc, int rstri
                                                         tab, out, stream)
                   : launch_t4_merge_rotate_d<128, false>(po, pml, nc, rstride, R, hkv, G, Tq,
                                                          slot_bits, tab, out, stream);
+}
+
+// Decode-route calls (G * L <= 16 rows a KV head) that append L rows first:
+// the decode launch's append unit appends them and attends the new keys, the
+// other workgroups split the cached prefix (every row sees all of it).
+template <int BITS, int D>
+static int launch_decode_append(KVCache& cc, const f16* q, int G, int L, const f16* k_new,
+                                const f16* v_new, float scale, bool causal, f16* out,
+                                hipStream_t stream) {
+    int nc = 0;
+    float* po = nullptr;
+    float2* pml = nullptr;
+    int rc = launch_decode_partials<BITS, D>(cc, q, G, L, cc.offset, scale, false, &nc, &po, &pml,
+                                             stream, nullptr, k_new, v_new, L, causal);
+    if (rc) return rc;
+    cc.offset += L;
+    return launch_partial_merge(po, pml, nc, 16, 0, G * L, cc.hkv, D, G, L, out, stream);
+}
+
+int launch_turbo4_decode_append(KVCache& cc, const f16* q, int G, int L, const f16* k_new,
+                                const f16* v_new, float scale, bool causal, const float* tab,
+                                f16* out, hipStream_t stream) {
+    QW_REQUIRE(cc.turbo4() && G * L <= 16 && cc.offset >= 64 && cc.offset + L <= cc.cap,
+               QW_ERR_INVALID_ARGUMENT, "decode: Turbo4 append outside the decode-route shapes");
+    int nc = 0;
+    float* po = nullptr;
+    float2* pml = nullptr;
+    int rc = cc.D == 256 ? launch_decode_partials<4, 256, true>(cc, q, G, L, cc.offset, scale, false,
+                                                                &nc, &po, &pml, stream, tab, k_new,
+                                                                v_new, L, causal)
+                         : launch_decode_partials<4, 128, true>(cc, q, G, L, cc.offset, scale, false,
+                                                                &nc, &po, &pml, stream, tab, k_new,
+                                                                v_new, L, causal);
+    if (rc) return rc;
+    cc.offset += L;
+    return launch_t4_merge_rotate(po, pml, nc, 16, G * L, cc.hkv, cc.D, G, L, 0, false, tab, out,
+                                  stream);
 }
 
 int launch_turbo4_decode(KVCache& cc, const f16* q, int G, int Tq, float scale, bool causal,
@@ -1293,6 +1490,11 @@ static int launch_decode_fused(KVCache& cc, const f16* q, int G, const f16* k_ne
 #ifndef QW_FUSED_DECODE_APPEND
 #define QW_FUSED_DECODE_APPEND 1
 #endif
+// 1: decode-route calls of 2+ rows (and Turbo4 decode-route calls) append
+// their rows in the decode launch's append unit; 0: a separate append first.
+#ifndef QW_DECODE_APPEND
+#define QW_DECODE_APPEND 1
+#endif
 
 int KVCache::update_and_attention(const void* q, int n_q_heads, int n_rows, const void* k_new,
                                   const void* v_new, float scale, bool causal, void* out,
@@ -1325,6 +1527,22 @@ int KVCache::update_and_attention(const void* q, int n_q_heads, int n_rows, cons
                              : launch_decode_fused<8, 256>(*this, qq, G, kn, vn, scale, oo, stream);
         return bits == 4 ? launch_decode_fused<4, 128>(*this, qq, G, kn, vn, scale, oo, stream)
                          : launch_decode_fused<8, 128>(*this, qq, G, kn, vn, scale, oo, stream);
+    }
+    if (QW_DECODE_APPEND && affine() && n_rows >= 2 && G * n_rows <= 16 && offset >= 64) {
+        // short verify blocks: the append unit rides in the decode launch
+        DeviceGuard dg(device);
+        QW_REQUIRE(dg.ok, QW_ERR_HIP, "update_and_attention: hipSetDevice failed");
+        if (offset + n_rows > cap) {
+            int rc = reserve(std::max(offset + n_rows, cap + cap / 2), stream);
+            if (rc) return rc;
+        }
+        const f16 *qq = (const f16*)q, *kn = (const f16*)k_new, *vn = (const f16*)v_new;
+        f16* oo = (f16*)out;
+        if (D == 256)
+            return bits == 4 ? launch_decode_append<4, 256>(*this, qq, G, n_rows, kn, vn, scale, causal, oo, stream)
+                             : launch_decode_append<8, 256>(*this, qq, G, n_rows, kn, vn, scale, causal, oo, stream);
+        return bits == 4 ? launch_decode_append<4, 128>(*this, qq, G, n_rows, kn, vn, scale, causal, oo, stream)
+                         : launch_decode_append<8, 128>(*this, qq, G, n_rows, kn, vn, scale, causal, oo, stream);
     }
     if (block_append_fits(*this, G, n_rows)) {
         // verify blocks: the append rides in the block kernel's launch

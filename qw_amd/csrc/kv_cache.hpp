@@ -203,6 +203,13 @@ bool block_append_fits(const KVCache& c, int G, int n_rows);
 int launch_block_append_attention_t4(KVCache& c, const f16* q, int G, int n_rows, const f16* k_new,
                                      const f16* v_new, float scale, bool causal, bool fused,
                                      const float* tab, f16* out, hipStream_t stream);
+// A Turbo4 decode-route call (G * n_rows <= 16, at least 64 cached rows,
+// capacity reserved) that appends its n_rows rows in the decode launch (its
+// append unit) and attends them with the cached prefix; out as
+// launch_turbo4_decode.
+int launch_turbo4_decode_append(KVCache& c, const f16* q, int G, int n_rows, const f16* k_new,
+                                const f16* v_new, float scale, bool causal, const float* tab,
+                                f16* out, hipStream_t stream);
 // Turbo4 update-and-attention: the append in the block kernel's launch where
 // the call takes the block kernel, else turbo4_update then turbo4_attention.
 int turbo4_update_and_attention(KVCache& c, const void* q, int n_q_heads, int n_rows,

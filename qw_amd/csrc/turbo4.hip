@@ -153,8 +153,9 @@ __global__ __launch_bounds__(128) void turbo4_fetch_kernel(
 #define QW_T4_BLOCK 1
 #endif
 constexpr int kT4BlockRows = 1024;
-// 1: update-and-attention calls that take the block kernel with one query tile
-// append their rows inside its launch; 0: the append kernel first.
+// 1: update-and-attention calls that take the block kernel with one query tile,
+// or the decode kernel, append their rows inside its launch; 0: the append
+// kernel first.
 #ifndef QW_T4_APPEND
 #define QW_T4_APPEND 1
 #endif
@@ -830,10 +831,13 @@ int turbo4_update_and_attention(KVCache& c, const void* q, int n_q_heads, int n_
                                 const void* k_new, const void* v_new, float scale, bool causal,
                                 void* out, hipStream_t stream) {
     const int G = n_q_heads / c.hkv, T = c.offset + n_rows;
-    // the routes of turbo4_attention below that take the block kernel
+    // the routes of turbo4_attention below: the fused pass and the block
+    // kernel's one-tile blocks append in the block launch, the decode route
+    // in the decode launch's append unit
     const bool fused = causal && n_rows <= 5 && T > 2048 && G * n_rows <= kT4vRows;
-    const bool block = fused || (G * n_rows > 16 && G * n_rows <= 16 * 8);
-    if (!(QW_T4_APPEND && QW_T4_BLOCK && block && c.offset >= 256)) {
+    const bool block = QW_T4_BLOCK && c.offset >= 256 && (fused || (G * n_rows > 16 && G * n_rows <= 16 * 8));
+    const bool decode = !fused && QW_T4_FUSED_DECODE && G * n_rows <= 16 && c.offset >= 64;
+    if (!(QW_T4_APPEND && (block || decode))) {
         int rc = c.update(k_new, v_new, n_rows, stream);
         if (rc) return rc;
         return turbo4_attention(c, q, n_q_heads, n_rows, scale, causal, out, stream);
@@ -846,6 +850,9 @@ int turbo4_update_and_attention(KVCache& c, const void* q, int n_q_heads, int n_
     }
     const float* tab = c.t4_tables;
     const f16 *qq = (const f16*)q, *kn = (const f16*)k_new, *vn = (const f16*)v_new;
+    if (decode)
+        return launch_turbo4_decode_append(c, qq, G, n_rows, kn, vn, scale, causal, tab, (f16*)out,
+                                           stream);
     if (fused)
         return launch_block_append_attention_t4(c, qq, G, n_rows, kn, vn, scale, causal, true, tab,
                                                 (f16*)out, stream);

@@ -306,12 +306,20 @@ def test_attention_without_append_equals_fused_call(oracle_lib, bits):
     ("affine4", 128, 1000, 16, 32, True, 0),    # head_dim 128, 128 rows a KV head
     ("affine4", 256, 700, 6, 24, False, 0),     # non-causal block: every row sees every new key
     ("affine8", 256, 512, 4, 24, True, 512),    # the call grows the capacity first
+    # decode route (<= 16 rows a KV head): the decode launch's append unit
+    ("affine4", 256, 3000, 2, 24, True, 0),     # 2-row verify (one draft), 12 rows a KV head
+    ("affine8", 256, 2045, 2, 32, True, 0),     # 16 rows a KV head, across an 8-key block
+    ("int8", 256, 1000, 2, 24, True, 0),
+    ("affine4", 128, 500, 4, 16, True, 0),      # head_dim 128 (12-wave decode kernel)
+    ("affine4", 256, 777, 3, 20, False, 0),     # non-causal, 15 rows a KV head
+    ("affine8", 256, 256, 2, 24, True, 256),    # the call grows the capacity first
 ])
 def test_verify_append_in_launch_equals_separate_append(oracle_lib, mode, D, T0, L, hq, causal, cap):
     """A verify block on an affine or Int8 cache appends its rows inside the
-    attention launch. The cache then holds exactly what one bulk update of the
-    same rows stores (every snapshot tensor equal bit for bit), and the output
-    equals attending the updated cache, within the stated tolerance."""
+    attention launch (the block kernel's, or the decode kernel's append unit).
+    The cache then holds exactly what one bulk update of the same rows stores
+    (every snapshot tensor equal bit for bit), and the output equals attending
+    the updated cache, within the stated tolerance."""
     import qw_amd
 
     r = rng(7000 + T0 + L + D)

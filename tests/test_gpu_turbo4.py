@@ -264,17 +264,19 @@ def test_turbo4_verify_geometries(T_prefix, L, hq, hkv, D):
 
 def test_turbo4_attention_without_append_and_reuse():
     """attention() over the cache as it is equals update_and_attention's
-    output, and repeated calls (shared workspace reuse) repeat it exactly."""
+    output (which attends the new key in the decode launch's append unit, so
+    within the stated tolerance), and repeated calls (shared workspace reuse)
+    repeat it exactly."""
     import qw_amd
 
     out, _, cache, (q, k, v) = _turbo4_layer(qw_amd, 2000, 1, False, seed=9)
     again = _np(cache.attention(_gpu(q), 1.0 / 16))[0]
-    np.testing.assert_array_equal(again, out)
+    assert_close(again, out, "turbo4 attention() vs update_and_attention")
     # a second, smaller cache in between uses the same device workspace
     other = qw_amd.KVCache("turbo4", 4, 256)
     other.update(_gpu(k[:, :300]), _gpu(v[:, :300]))
     _np(other.attention(_gpu(q), 1.0 / 16))
-    np.testing.assert_array_equal(_np(cache.attention(_gpu(q), 1.0 / 16))[0], out)
+    np.testing.assert_array_equal(_np(cache.attention(_gpu(q), 1.0 / 16))[0], again)
 
 
 @pytest.mark.parametrize("T0,L,causal,D", [
@@ -282,12 +284,17 @@ def test_turbo4_attention_without_append_and_reuse():
     (2040, 3, True, 256),     # below the gate: the fp16 arithmetic in the block kernel, likewise
     (1000, 16, True, 128),    # 96 rows a KV head at head_dim 128
     (600, 5, False, 256),     # non-causal block
+    (4095, 1, False, 256),    # the decode step: the decode launch's append unit
+    (12286, 1, False, 256),
+    (1500, 2, True, 256),     # 2 causal rows below the fused gate: decode route
+    (777, 1, False, 128),     # head_dim 128 decode
 ])
 def test_turbo4_append_in_launch_equals_separate_update(T0, L, causal, D):
-    """Update-and-attention calls that take the block kernel append their rows
-    inside its launch: the cache then holds exactly what one bulk update
-    stores (every snapshot tensor equal bit for bit), and the output equals
-    attending the updated cache, within the stated tolerance."""
+    """Update-and-attention calls append their rows inside the attention
+    launch (the block kernel's, or the decode kernel's append unit): the cache
+    then holds exactly what one bulk update stores (every snapshot tensor
+    equal bit for bit), and the output equals attending the updated cache,
+    within the stated tolerance."""
     import qw_amd
 
     r = rng(8100 + T0 + L + D)
