@@ -1079,7 +1079,7 @@ static int launch_decode_append(KVCache& cc, const f16* q, int G, int L, const f
 int launch_turbo4_decode_append(KVCache& cc, const f16* q, int G, int L, const f16* k_new,
                                 const f16* v_new, float scale, bool causal, const float* tab,
                                 f16* out, hipStream_t stream) {
-    QW_REQUIRE(cc.turbo4() && G * L <= 16 && cc.offset >= 64 && cc.offset + L <= cc.cap,
+    QW_REQUIRE(cc.turbo4() && G * L <= 16 && cc.offset >= 1 && cc.offset + L <= cc.cap,
                QW_ERR_INVALID_ARGUMENT, "decode: Turbo4 append outside the decode-route shapes");
     int nc = 0;
     float* po = nullptr;
@@ -1236,262 +1236,8 @@ int KVCache::attention(const void* q, int n_q_heads, int n_rows, float scale, bo
     return launch_attention(*this, q, n_q_heads, n_rows, scale, causal, out, stream);
 }
 
-// ---------------------------------------------------- fused decode append
-//
-// One decode row on an affine cache: the decode kernel attends the cached
-// prefix (t keys) and this kernel quantizes-and-appends the new token (MLX
-// quantize, quant.hpp) while merging the split-K partials, folding the new key
-// in as one more partial: (m, l, O) = (f16(q'.k), 1, v), k and v in their
-// dequantized form (the reference attends appended rows dequantized,
-// cache.rs:2723, :3508). This replaces the separate append launch on the
-// decode path; the cache contents it writes equal the append kernel's.
-// grid (G, kv_heads, D/64), 4 waves: workgroup (g, h, b) writes out[h*G + g]
-// dims [64b, 64b+64); the g == 0 workgroups also write group b of the new
-// K row (wave b) and of the new V block slot (wave 0).
-struct MergeAppendArgs {
-    const float* part_o;
-    const float2* part_ml;
-    int nc;                 // partials a KV head (0: empty prefix)
-    const f16* q;           // [hq][1][D]
-    const f16* k_new;       // [hkv][1][D]
-    const f16* v_new;
-    int G, t, cap;          // t: index of the new token
-    float scale_h;          // f16(scale)
-    uint32_t* k_codes;
-    uint32_t* k_params;
-    uint32_t* v_codes;
-    f16* v_params;
-    int* fast_flag;
-    f16* out;               // [hq][1][D]
-};
-
-// I8: the Int8 mode (cache.rs:270-305): the new K and V rows are quantized
-// per token, scale f16(absmax / 127) (1 for an all-zero row), codes
-// clip(rint(f16(x / scale))) stored plus 128 in the 8-bit layout with the
-// scale in every group slot and bias 0, as the append kernel stores them; the
-// new key is attended as f16(code * scale).
-template <int BITS, int D, int PER, bool I8 = false>
-__global__ __launch_bounds__(256) void merge_append_kernel(MergeAppendArgs a) {
-    static_assert(!I8 || BITS == 8, "Int8 rows use the 8-bit layout");
-    constexpr int NG = D / 64;
-    const int row = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int d = b * 64 + lane;
-    const int qh = h * a.G + row;
-    const int t = a.t;
-    // ---- every load first: the V word the new code goes into (row-0
-    // workgroups, wave 0: read-modify-write of the 8-key block slot), the
-    // partials (wave w: c = w, w+4, ...), the new K row and q (thread = dim),
-    // the new V group b (lane = dim)
-    const int vblk = t / 8, vk = t % 8;
-    const int vp = v_phys_dim(d, D, BITS);
-    uint32_t* vbp = a.v_codes + ((int64_t)h * (a.cap / 8) + vblk) * (D * BITS / 4);
-    const int vidx = BITS == 4 ? vp : 2 * vp + (vk >> 2);
-    const bool v_writer = row == 0 && wave == 0;
-    const uint32_t vword = v_writer ? vbp[vidx] : 0u;
-    const int64_t base = (int64_t)h * a.nc * 16 + row;
-    float v[PER];
-    float2 ml[PER];
-#pragma unroll
-    for (int i = 0; i < PER; i++) {
-        const int c = wave + 4 * i;
-        if (c < a.nc) {
-            ml[i] = a.part_ml[base + (int64_t)c * 16];
-            v[i] = a.part_o[(base + (int64_t)c * 16) * D + d];
-        } else {
-            ml[i] = float2{-INFINITY, 0.0f};
-            v[i] = 0.0f;
-        }
-    }
-    const bool kdim = (int)threadIdx.x < D;
-    const float kx = kdim ? (float)a.k_new[(int64_t)h * D + threadIdx.x] : 0.0f;
-    const float qx = kdim ? (float)a.q[(int64_t)qh * D + threadIdx.x] : 0.0f;
-    const float vx = (float)a.v_new[(int64_t)h * D + d];
-    // Int8: the whole V row too (thread = dim), for its absmax
-    const float vrow = I8 && kdim ? (float)a.v_new[(int64_t)h * D + threadIdx.x] : 0.0f;
-
-    // ---- new key: wave w < NG quantizes K group w and forms its share of
-    // q' . k (q' = f16(f16(scale) * q), as MLX scales q)
-    __shared__ float sm_s[4];
-    float kcode = 0.0f;
-    f16 ks = (f16)0.0f, kb = (f16)0.0f;
-    f16 vs = (f16)0.0f, vbias = (f16)0.0f;
-    float vcode = 0.0f, vd = 0.0f;
-    if constexpr (I8) {
-        // row absmax of K and V over the workgroup's four waves
-        __shared__ float sm_am[2][4];
-        const float ka = wave_reduce(fabsf(kx), OpMax()), va = wave_reduce(fabsf(vrow), OpMax());
-        if (lane == 0) {
-            sm_am[0][wave] = ka;
-            sm_am[1][wave] = va;
-        }
-        __syncthreads();
-        auto scale_of = [](float am) {
-            f16 sc = (f16)(am / 127.0f);
-            if ((float)sc == 0.0f) sc = (f16)1.0f;
-            return sc;
-        };
-        ks = scale_of(fmaxf(fmaxf(sm_am[0][0], sm_am[0][1]), fmaxf(sm_am[0][2], sm_am[0][3])));
-        vs = scale_of(fmaxf(fmaxf(sm_am[1][0], sm_am[1][1]), fmaxf(sm_am[1][2], sm_am[1][3])));
-        auto code_of = [](float x, float s) {
-            return fminf(fmaxf(__builtin_rintf((float)(f16)(x / s)), -128.0f), 127.0f);
-        };
-        if (wave < NG) {
-            const float c = code_of(kx, (float)ks);
-            kcode = c + 128.0f;  // stored byte
-            const float qs = (float)(f16)((float)(f16)a.scale_h * qx);
-            const float sp = wave_reduce(qs * (float)(f16)(c * (float)ks), OpSum());
-            if (lane == 0) sm_s[wave] = sp;
-        }
-        const float c = code_of(vx, (float)vs);
-        vcode = c + 128.0f;
-        vd = (float)(f16)(c * (float)vs);
-    } else if (wave < NG) {
-        const float mn = wave_reduce(kx, OpMin()), mx = wave_reduce(kx, OpMax());
-        const AffineGroup g = affine_group(mn, mx, BITS);
-        kcode = affine_code(kx, g, BITS);
-        ks = (f16)g.scale;
-        kb = (f16)g.bias;
-        const float qs = (float)(f16)((float)(f16)a.scale_h * qx);
-        const float sp = wave_reduce(qs * affine_dequant(kcode, ks, kb), OpSum());
-        if (lane == 0) sm_s[wave] = sp;
-    }
-    // ---- new value: group b, every wave (lane = dim d)
-    if constexpr (!I8) {
-        const float vmn = wave_reduce(vx, OpMin()), vmx = wave_reduce(vx, OpMax());
-        const AffineGroup gv = affine_group(vmn, vmx, BITS);
-        vcode = affine_code(vx, gv, BITS);
-        vs = (f16)gv.scale;
-        vbias = (f16)gv.bias;
-        vd = affine_dequant(vcode, vs, vbias);
-    }
-
-    // ---- merge: M over the partials and the new score
-    float m = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < PER; i++) m = fmaxf(m, ml[i].x);
-    __shared__ float sm_m[4];
-    __shared__ float sm[2][4][64];
-    if (lane == 0) sm_m[wave] = m;
-    __syncthreads();
-    float S = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NG; w++) S += sm_s[w];
-    const float s_new = (float)(f16)S;  // MLX rounds the score to fp16
-    m = fmaxf(fmaxf(fmaxf(sm_m[0], sm_m[1]), fmaxf(sm_m[2], sm_m[3])), s_new);
-    float o = 0.0f, l = 0.0f;
-#pragma unroll
-    for (int i = 0; i < PER; i++) {
-        const float w = ml[i].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((ml[i].x - m) * kLog2e);
-        o = __builtin_fmaf(w, v[i], o);
-        l = __builtin_fmaf(w, ml[i].y, l);
-    }
-    sm[0][wave][lane] = o;
-    sm[1][wave][lane] = l;
-    __syncthreads();
-    if (wave == 0) {
-        const float wn = __builtin_amdgcn_exp2f((s_new - m) * kLog2e);
-        const float O = (sm[0][0][lane] + sm[0][1][lane]) + (sm[0][2][lane] + sm[0][3][lane]) + wn * vd;
-        const float L = (sm[1][0][lane] + sm[1][1][lane]) + (sm[1][2][lane] + sm[1][3][lane]) + wn;
-        a.out[(int64_t)qh * D + d] = (f16)(O / L);
-    }
-
-    // ---- append: the g == 0 workgroups write group b of the new row
-    if (row != 0) return;
-    if (wave == b && wave < NG) {
-        // K: MLX packing, 32/BITS codes a word, LSB first
-        constexpr int EPW = 32 / BITS;
-        uint32_t piece = (uint32_t)kcode << (BITS * (lane % EPW));
-#pragma unroll
-        for (int off = 1; off < EPW; off <<= 1) piece |= __shfl_xor(piece, off);
-        const int64_t krow = ((int64_t)h * a.cap + t) * (D * BITS / 32);
-        if (lane % EPW == 0) a.k_codes[krow + (64 * b) / EPW + lane / EPW] = piece;
-        if (lane == 0) {
-            half2v sb;
-            sb.x = ks;
-            sb.y = kb;
-            a.k_params[((int64_t)h * a.cap + t) * NG + k_param_slot(b, NG)] =
-                __builtin_bit_cast(uint32_t, sb);
-            if (!I8) check_fast_scale(ks, BITS, a.fast_flag);
-        }
-    }
-    if (v_writer) {
-        // V: key slot t % 8 of block t / 8, dim d at its lane-order slot
-        const uint32_t code = (uint32_t)vcode;
-        if constexpr (BITS == 4) {
-            const int sh = 4 * v4_nibble_pos(vk);
-            vbp[vidx] = (vword & ~(0xFu << sh)) | (code << sh);
-        } else {
-            const int sh = 8 * (vk & 3);
-            vbp[vidx] = (vword & ~(0xFFu << sh)) | (code << sh);
-        }
-        if (lane == 0) {
-            f16* vpp = a.v_params + (((int64_t)h * (a.cap / 8) + vblk) * NG + b) * 16;
-            vpp[vk] = vs;
-            vpp[8 + vk] = vbias;
-            if (!I8) check_fast_scale(vs, BITS, a.fast_flag);
-        }
-    }
-}
-
-template <int BITS, int D, bool I8 = false>
-static int launch_decode_fused(KVCache& cc, const f16* q, int G, const f16* k_new,
-                               const f16* v_new, float scale, f16* out, hipStream_t stream) {
-    MergeAppendArgs m;
-    m.nc = 0;
-    m.part_o = nullptr;
-    m.part_ml = nullptr;
-    const int t = cc.offset;
-    if (t > 0) {
-        float* po = nullptr;
-        float2* pml = nullptr;
-        int rc = launch_decode_partials<BITS, D>(cc, q, G, 1, t, scale, false, &m.nc, &po, &pml,
-                                                 stream);
-        if (rc) return rc;
-        m.part_o = po;
-        m.part_ml = pml;
-    }
-    m.q = q;
-    m.k_new = k_new;
-    m.v_new = v_new;
-    m.G = G;
-    m.t = t;
-    m.cap = cc.cap;
-    m.scale_h = (float)(f16)scale;
-    m.k_codes = (uint32_t*)cc.k_data;
-    m.k_params = cc.k_params;
-    m.v_codes = (uint32_t*)cc.v_data;
-    m.v_params = (f16*)cc.v_params;
-    m.fast_flag = cc.fast_flag;
-    m.out = out;
-    const dim3 grid(G, cc.hkv, D / 64);
-    switch (merge_per(m.nc)) {
-        case 4:
-            hipLaunchKernelGGL((merge_append_kernel<BITS, D, 4, I8>), grid, dim3(256), 0, stream, m);
-            break;
-        case 8:
-            hipLaunchKernelGGL((merge_append_kernel<BITS, D, 8, I8>), grid, dim3(256), 0, stream, m);
-            break;
-        case 16:
-            hipLaunchKernelGGL((merge_append_kernel<BITS, D, 16, I8>), grid, dim3(256), 0, stream, m);
-            break;
-        case 32:
-            hipLaunchKernelGGL((merge_append_kernel<BITS, D, 32, I8>), grid, dim3(256), 0, stream, m);
-            break;
-        default:
-            hipLaunchKernelGGL((merge_append_kernel<BITS, D, kMergeMaxPer, I8>), grid, dim3(256), 0,
-                               stream, m);
-    }
-    QW_HIP_CHECK(hipGetLastError());
-    cc.offset = t + 1;
-    return QW_OK;
-}
-
-#ifndef QW_FUSED_DECODE_APPEND
-#define QW_FUSED_DECODE_APPEND 1
-#endif
-// 1: decode-route calls of 2+ rows (and Turbo4 decode-route calls) append
-// their rows in the decode launch's append unit; 0: a separate append first.
+// 1: decode-route calls (and Turbo4 decode-route calls) append their rows in
+// the decode launch's append unit; 0: a separate append first.
 #ifndef QW_DECODE_APPEND
 #define QW_DECODE_APPEND 1
 #endif
@@ -1507,29 +1253,8 @@ int KVCache::update_and_attention(const void* q, int n_q_heads, int n_rows, cons
     if (turbo4())
         return turbo4_update_and_attention(*this, q, n_q_heads, n_rows, k_new, v_new, scale, causal,
                                            out, stream);
-    if (QW_FUSED_DECODE_APPEND && affine() && n_rows == 1 && G <= 16) {
-        // decode: the append rides in the split-K merge (one launch fewer)
-        DeviceGuard dg(device);
-        QW_REQUIRE(dg.ok, QW_ERR_HIP, "update_and_attention: hipSetDevice failed");
-        if (offset + 1 > cap) {
-            int rc = reserve(std::max(offset + 1, cap + cap / 2), stream);
-            if (rc) return rc;
-        }
-        const f16* qq = (const f16*)q;
-        const f16* kn = (const f16*)k_new;
-        const f16* vn = (const f16*)v_new;
-        f16* oo = (f16*)out;
-        if (int8())
-            return D == 256 ? launch_decode_fused<8, 256, true>(*this, qq, G, kn, vn, scale, oo, stream)
-                            : launch_decode_fused<8, 128, true>(*this, qq, G, kn, vn, scale, oo, stream);
-        if (D == 256)
-            return bits == 4 ? launch_decode_fused<4, 256>(*this, qq, G, kn, vn, scale, oo, stream)
-                             : launch_decode_fused<8, 256>(*this, qq, G, kn, vn, scale, oo, stream);
-        return bits == 4 ? launch_decode_fused<4, 128>(*this, qq, G, kn, vn, scale, oo, stream)
-                         : launch_decode_fused<8, 128>(*this, qq, G, kn, vn, scale, oo, stream);
-    }
-    if (QW_DECODE_APPEND && affine() && n_rows >= 2 && G * n_rows <= 16 && offset >= 64) {
-        // short verify blocks: the append unit rides in the decode launch
+    if (QW_DECODE_APPEND && affine() && G * n_rows <= 16 && offset >= 1) {
+        // decode and short verify blocks: the append unit rides in the decode launch
         DeviceGuard dg(device);
         QW_REQUIRE(dg.ok, QW_ERR_HIP, "update_and_attention: hipSetDevice failed");
         if (offset + n_rows > cap) {

@@ -203,7 +203,7 @@ bool block_append_fits(const KVCache& c, int G, int n_rows);
 int launch_block_append_attention_t4(KVCache& c, const f16* q, int G, int n_rows, const f16* k_new,
                                      const f16* v_new, float scale, bool causal, bool fused,
                                      const float* tab, f16* out, hipStream_t stream);
-// A Turbo4 decode-route call (G * n_rows <= 16, at least 64 cached rows,
+// A Turbo4 decode-route call (G * n_rows <= 16, at least one cached row,
 // capacity reserved) that appends its n_rows rows in the decode launch (its
 // append unit) and attends them with the cached prefix; out as
 // launch_turbo4_decode.

@@ -836,7 +836,7 @@ int turbo4_update_and_attention(KVCache& c, const void* q, int n_q_heads, int n_
     // in the decode launch's append unit
     const bool fused = causal && n_rows <= 5 && T > 2048 && G * n_rows <= kT4vRows;
     const bool block = QW_T4_BLOCK && c.offset >= 256 && (fused || (G * n_rows > 16 && G * n_rows <= 16 * 8));
-    const bool decode = !fused && QW_T4_FUSED_DECODE && G * n_rows <= 16 && c.offset >= 64;
+    const bool decode = !fused && QW_T4_FUSED_DECODE && G * n_rows <= 16 && c.offset >= 1;
     if (!(QW_T4_APPEND && (block || decode))) {
         int rc = c.update(k_new, v_new, n_rows, stream);
         if (rc) return rc;
