@@ -208,14 +208,16 @@ __device__ inline void append_block(const RowSrc& rs, int n_tokens, int t_old, i
 // Walsh-Hadamard transform scaled 1/sqrt(D)); the index = the number of the
 // 15 boundaries strictly below the value; rescale = f16(norm / max(|centroid
 // vector|, 1e-10)); nibbles packed low = even coordinate; side word K
-// (rescale, 0), V (f16 norm, rescale). cb: the 16 centroids.
+// (rescale, 0), V (f16 norm, rescale). cb: the 16 centroids. expand (if not
+// null, D values): the row's stored values in the rotated basis, f16(centroid
+// * rescale), as the attention kernels form them from the cache.
 template <int D>
 __device__ inline void turbo4_append_row(const RowSrc& rs, int i, int h, bool is_k, int lane,
                                          int t_old, int cap, const float* __restrict__ tab,
                                          const float* cb, uint8_t* __restrict__ k_packed,
                                          uint32_t* __restrict__ k_side,
                                          uint8_t* __restrict__ v_packed,
-                                         uint32_t* __restrict__ v_side) {
+                                         uint32_t* __restrict__ v_side, f16* expand = nullptr) {
     constexpr int VPL = D / 64;
     using TT = T4Tab<D>;
     const int64_t src = (int64_t)i * rs.row_stride + (int64_t)h * rs.head_stride;
@@ -255,6 +257,10 @@ __device__ inline void turbo4_append_row(const RowSrc& rs, int i, int h, bool is
     }
     const float rn = sqrtf(t4_wave_sum(csq));
     const f16 rescale = (f16)(norm / fmaxf(rn, 1e-10f));
+    if (expand) {
+#pragma unroll
+        for (int j = 0; j < VPL; j++) expand[lane * VPL + j] = t4_f16_product(cb[idx[j]], (float)rescale);
+    }
     const int t = t_old + i;
     uint8_t* prow = (is_k ? k_packed : v_packed) + ((int64_t)h * cap + t) * (D / 2);
     if constexpr (VPL == 4) {

@@ -626,6 +626,8 @@ template <int D>
 constexpr size_t decode_append_lds(int L) {
     return (sizeof(AppendScratch<D>) + 15) / 16 * 16 + (size_t)4 * L * D;
 }
+// (Turbo4 uses the scratch's first 64 bytes for the centroids)
+static_assert(sizeof(AppendScratch<128>) >= 16 * sizeof(float), "centroid table fits the scratch");
 
 // The append unit of a decode launch (DecodeArgs::app_L > 0), workgroup
 // (ns, h). It appends head h's new rows (the append kernels' work), reads
@@ -634,18 +636,41 @@ constexpr size_t decode_append_lds(int L) {
 // writes the new keys' partial for every row of the launch in the decode
 // kernel's arithmetic: q' = f16(f16(scale) q) (Turbo4: q rotated first), the
 // score rounded to fp16, the weights exp(s - m) summed in fp32 and rounded to
-// fp16 for P.V. Wave w takes rows w, w + NW, ...
+// fp16 for P.V. Wave w takes rows w, w + NW, ... The unit runs while the
+// prefix splits keep HBM busy, so its loads are issued up front (q rows and
+// rotation signs with the appended rows) and Turbo4 expands the new keys
+// from the quantizer's registers: each dependent memory round trip here costs
+// microseconds.
 template <int BITS, int D, bool T4>
 __device__ void decode_append_unit(const DecodeArgs& a, char* lds) {
     constexpr int NW = decode_waves<BITS, D>();
     constexpr int VPL = D / 64, NG = D / 64;
+    constexpr int RPW = (16 + NW - 1) / NW;  // rows a wave (R <= 16)
     const int h = blockIdx.y, L = a.app_L, T0 = a.T;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    f16* sk = (f16*)(lds + (sizeof(AppendScratch<D>) + 15) / 16 * 16);
+    f16* sv = sk + L * D;
+    float qv[RPW][VPL];
+#pragma unroll
+    for (int k = 0; k < RPW; k++) {
+        const int rho = min(wave + NW * k, a.R - 1);
+        const f16* qrow = a.q + ((int64_t)(h * a.G + rho % a.G) * a.Tq + rho / a.G) * D;
+#pragma unroll
+        for (int i = 0; i < VPL; i++) qv[k][i] = (float)qrow[lane * VPL + i];
+    }
+    float si[VPL], so[VPL];
     if constexpr (T4) {
-        for (int job = wave; job < 2 * L; job += NW)
-            turbo4_append_row<D>(a.app, job >> 1, h, (job & 1) == 0, lane, T0, a.cap, a.t4_tab,
-                                 a.t4_tab + T4Tab<D>::cb, (uint8_t*)a.k_data, (uint32_t*)a.k_params,
-                                 (uint8_t*)a.v_data, (uint32_t*)a.v_params);
+        t4_lane_signs<D>(a.t4_tab + T4Tab<D>::k_s1, lane, si);
+        t4_lane_signs<D>(a.t4_tab + T4Tab<D>::k_s2, lane, so);
+        float* s_cb = (float*)lds;
+        if (tid < 16) s_cb[tid] = a.t4_tab[T4Tab<D>::cb + tid];
+        __syncthreads();
+        for (int job = wave; job < 2 * L; job += NW) {
+            const int j = job >> 1;
+            turbo4_append_row<D>(a.app, j, h, (job & 1) == 0, lane, T0, a.cap, a.t4_tab, s_cb,
+                                 (uint8_t*)a.k_data, (uint32_t*)a.k_params, (uint8_t*)a.v_data,
+                                 (uint32_t*)a.v_params, ((job & 1) == 0 ? sk : sv) + j * D);
+        }
     } else {
         auto& sc = *reinterpret_cast<AppendScratch<D>*>(lds);
         for (int blk = T0 / 8; blk <= (T0 + L - 1) / 8; blk++) {
@@ -656,24 +681,13 @@ __device__ void decode_append_unit(const DecodeArgs& a, char* lds) {
         }
     }
     __syncthreads();
-    // the new keys' values, read back from the cache
-    f16* sk = (f16*)(lds + (sizeof(AppendScratch<D>) + 15) / 16 * 16);
-    f16* sv = sk + L * D;
-    for (int i = tid; i < L * D; i += 64 * NW) {
+    // affine and Int8: the new keys' values, read back from the cache
+    for (int i = tid; i < (T4 ? 0 : L * D); i += 64 * NW) {
         const int j = i / D, d = i % D, t = T0 + j;
         const int64_t kr = (int64_t)h * a.cap + t;
         const int blk = t / 8, k = t % 8;
-        f16 kv, vv;
-        if constexpr (T4) {
-            using TT = T4Tab<D>;
-            const uint8_t kb = ((const uint8_t*)a.k_data)[kr * (D / 2) + d / 2];
-            const uint8_t vb = ((const uint8_t*)a.v_data)[kr * (D / 2) + d / 2];
-            const half2v ks = __builtin_bit_cast(half2v, a.k_params[kr]);
-            const half2v vs = __builtin_bit_cast(half2v, a.v_params[kr]);
-            const int sh = 4 * (d & 1);
-            kv = t4_f16_product(a.t4_tab[TT::cb + ((kb >> sh) & 15)], (float)ks.x);
-            vv = t4_f16_product(a.t4_tab[TT::cb + ((vb >> sh) & 15)], (float)vs.y);
-        } else {
+        f16 kv = (f16)0.0f, vv = (f16)0.0f;
+        if constexpr (!T4) {
             constexpr int EPW = 32 / BITS;
             constexpr uint32_t MASK = (1u << BITS) - 1;
             const uint32_t kw = a.k_data[kr * (D * BITS / 32) + d / EPW];
@@ -697,20 +711,20 @@ __device__ void decode_append_unit(const DecodeArgs& a, char* lds) {
     }
     __syncthreads();
     const int64_t pbase = ((int64_t)h * a.nc + a.ns) * 16;
-    for (int rho = wave; rho < a.R; rho += NW) {
-        const int l = rho / a.G;
-        const f16* qrow = a.q + ((int64_t)(h * a.G + rho % a.G) * a.Tq + l) * D;
-        float qv[VPL];
 #pragma unroll
-        for (int i = 0; i < VPL; i++) qv[i] = (float)qrow[lane * VPL + i];
+    for (int k = 0; k < RPW; k++) {
+        const int rho = wave + NW * k;
+        if (rho >= a.R) break;  // wave-uniform
+        const int l = rho / a.G;
+        float(&q)[VPL] = qv[k];
         if constexpr (T4) {
             f16 o[VPL];
-            t4_rotate_row<D>(qv, lane, a.t4_tab + T4Tab<D>::k_s1, a.t4_tab + T4Tab<D>::k_s2, o);
+            t4_rotate_row<D>(q, lane, si, so, o);
 #pragma unroll
-            for (int i = 0; i < VPL; i++) qv[i] = (float)o[i];
+            for (int i = 0; i < VPL; i++) q[i] = (float)o[i];
         }
 #pragma unroll
-        for (int i = 0; i < VPL; i++) qv[i] = (float)(f16)(a.scale_h * qv[i]);
+        for (int i = 0; i < VPL; i++) q[i] = (float)(f16)(a.scale_h * q[i]);
         const int n_vis = a.app_causal ? l + 1 : L;
         float sc[16];
         float m = -INFINITY;
@@ -721,7 +735,7 @@ __device__ void decode_append_unit(const DecodeArgs& a, char* lds) {
                 float dot = 0.0f;
 #pragma unroll
                 for (int i = 0; i < VPL; i++)
-                    dot = __builtin_fmaf(qv[i], (float)sk[j * D + lane * VPL + i], dot);
+                    dot = __builtin_fmaf(q[i], (float)sk[j * D + lane * VPL + i], dot);
                 sc[j] = (float)(f16)t4_wave_sum(dot);
                 m = fmaxf(m, sc[j]);
             }
