@@ -33,6 +33,8 @@
 //   fp32 partials (m, l, O; rows in V slot order) and the shared split-K
 //   merge kernel.
 #include <algorithm>
+#include <map>
+#include <mutex>
 #include <type_traits>
 
 #include "append.hpp"
@@ -69,6 +71,12 @@ struct BlockArgs {
     // others are splits 0 .. n_split - 2 of the cached prefix, keys < T_pre.
     int n_app, T_pre, app_int8;
     RowSrc app;
+    // Tile images (affine and Int8 prefill): img_w / img hold each key tile's
+    // dequantized LDS buffer, [hkv][img_tiles][BUF bytes]; the expansion
+    // launch writes them and the attention launch copies them into LDS.
+    char* img_w;
+    const char* img;
+    int img_tiles;
     const float* t4_tab;  // Turbo4 caches: the device tables (signs, centroids: T4Tab<D>)
     float t4_post;        // Turbo4 fused pass: scale * log2(e) in fp32
     float scale_h;      // f16(scale) as float
@@ -86,6 +94,16 @@ struct BlockArgs {
 #define QW_BLOCK_WAVES 8
 #endif
 constexpr int kBlockWaves = QW_BLOCK_WAVES;
+// Waves of the launches that attend from tile images (no register staging:
+// three waves a SIMD fit the register budget).
+#ifndef QW_IMAGE_WAVES
+#define QW_IMAGE_WAVES 12
+#endif
+constexpr int kImageWaves = QW_IMAGE_WAVES;
+template <int PM>
+constexpr int block_waves() {
+    return PM == 2 ? kImageWaves : kBlockWaves;
+}
 // LDS reads a wave keeps in flight ahead of its MFMAs (instruction-scheduling
 // groups). Left to itself the compiler issues one or two reads ahead, so each
 // MFMA waited on its own read; four ahead measured c3 1.25 -> 1.19 ms and c4
@@ -166,26 +184,33 @@ __device__ __forceinline__ float wave_sum_g(float v) {
 // log2(e), scores stay fp32 in the log2 domain, P enters P.V as an fp16 high
 // part plus an fp16 remainder (fp32-exact products), and the partial maxima are
 // stored in natural units for the shared merge.
-template <int BITS, int D, int RT, bool FAST, int T4M = 0, bool APP = false>
+// PM (tile images): 0 none; 1 the expansion launch (workgroup (t, h) writes
+// the image of key tile t of head h and returns); 2 attention from the images
+// (each tile's LDS buffer copied in by LDS-DMA, no dequant in the loop).
+template <int BITS, int D, int RT, bool FAST, int T4M = 0, bool APP = false, int PM = 0>
 __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     using S = BlockShape<D>;
     constexpr int KT = S::KT, NSUB = S::NSUB, NM = S::NM, NT = S::NT, NG = S::NG;
     constexpr int TPR = S::TPR, LTPR = S::LTPR, TPB = S::TPB, BUF = S::BUF, KBUF = S::KBUF;
     constexpr int VROW = S::VROW;
-    constexpr int NW = kBlockWaves;
+    constexpr int NW = block_waves<PM>();
     constexpr bool T4 = T4M != 0, FUSED = T4M == 2;
     static_assert(!T4 || BITS == 4, "Turbo4 indices are 4-bit");
     constexpr bool AFF = BITS != 16 && !T4;
     constexpr int VB = T4 ? 16 : BITS;  // the V slot order in LDS (and of the partial rows)
     constexpr int KU = BITS / 4;  // u32x4 loads a 32-dim K slice / a 4-slot V slice
-    constexpr int PER = KT * TPR / (64 * NW);  // slices of each kind a thread owns
-    static_assert(PER * 64 * NW == KT * TPR && (KT / 8) * TPB == KT * TPR, "slices a thread");
+    // slices of each kind a thread owns (the image launches stage nothing)
+    constexpr int PER = PM == 2 ? 1 : KT * TPR / (64 * NW);
+    static_assert(PM == 2 || (PER * 64 * NW == KT * TPR && (KT / 8) * TPB == KT * TPR),
+                  "slices a thread");
 
-    int sp, qt, h, n_split, tiles_per_split;
+    int sp = 0, qt = 0, h = 0, n_split = 1, tiles_per_split = 1;
     // APP (launches with n_app > 0): the keys this workgroup may see are
     // [key_lo, key_hi); other launches compile without the bounds
     int key_lo = 0, key_hi = a.T;
-    if (APP) {
+    if constexpr (PM == 1) {
+        h = blockIdx.y;
+    } else if (APP) {
         const int lin = blockIdx.x;
         qt = 0;
         n_split = a.n_split;
@@ -297,7 +322,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         __syncthreads();
     }
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++) {
+    for (int rt = 0; rt < (PM == 1 ? 0 : RT); rt++) {
         const int rho = wrow0 + 16 * rt + r16;
         row_ok[rt] = rho < a.R;
         lim[rt] = row_ok[rt] ? cut(a.causal ? a.T - a.Tq + rho / a.G : a.T - 1) : -1;
@@ -699,6 +724,42 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
 #endif
     };
 
+    if constexpr (PM == 1) {
+        // the expansion: tile blockIdx.x's buffer, as the main loop stores
+        // it, copied out to its image
+        Stage st;
+        load(st, blockIdx.x);
+        store(st, 0);
+        __syncthreads();
+        char* dst = a.img_w + ((int64_t)h * a.img_tiles + blockIdx.x) * BUF;
+        for (int i = 16 * tid; i < BUF; i += 16 * 64 * NW) *(u32x4*)(dst + i) = *(const u32x4*)(lds + i);
+        return;
+    }
+    if constexpr (PM == 2) {
+        // tile t's image into buffer b: 1 KB a wave instruction (lane i its
+        // 16 bytes), the LDS address from M0; waited for before the barrier
+        const char* img0 = a.img + (int64_t)h * a.img_tiles * BUF;
+        const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds;
+        auto dma = [&](int t, int b) {
+            const char* src = img0 + (int64_t)t * BUF + 16 * lane;
+            for (int c = wave; c < BUF / 1024; c += NW)
+                asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                             ::"v"(src + 1024 * c),
+                             "s"(__builtin_amdgcn_readfirstlane(lds0 + BUF * b + 1024 * c))
+                             : "memory", "m0");
+        };
+        static_assert(BUF % 1024 == 0, "a tile buffer is whole 1 KB DMA instructions");
+        if (t0 < t1) dma(t0, 0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        for (int t = t0; t < t1; t++) {
+            const int b = (t - t0) & 1;
+            if (t + 1 < t1) dma(t + 1, b ^ 1);
+            if (wave_live && t * KT <= wave_lim) tile(b, t * KT);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+        }
+    } else {
     // ---- main loop: round t dequantizes tile t+1 into LDS buffer (t+1)&1
     // from its register stage, reuses that stage for the loads of tile
     // t + 1 + QW_BLOCK_STAGES, and computes tile t from buffer t&1; one
@@ -744,6 +805,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         __syncthreads();
     }
 #endif
+    }
 
     // ---- epilogue: per column, the row sum over the 4 lane groups.
 #pragma unroll
@@ -790,8 +852,8 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     }
 }
 
-template <int BITS, int D, int RT, int T4M = 0, bool APP = false>
-__global__ __launch_bounds__(64 * kBlockWaves, 1) void attend_block_kernel(BlockArgs a) {
+template <int BITS, int D, int RT, int T4M = 0, bool APP = false, int PM = 0>
+__global__ __launch_bounds__(64 * block_waves<PM>(), 1) void attend_block_kernel(BlockArgs a) {
     // two buffers, each a K and a V tile of KT keys in fp16 (~130 KB)
     extern __shared__ __attribute__((aligned(16))) char lds_buf[];
     // The exact 2-op dequant runs without waiting for the cache's fast flag;
@@ -830,27 +892,30 @@ __global__ __launch_bounds__(64 * kBlockWaves, 1) void attend_block_kernel(Block
             __syncthreads();
         }
     }
-    if (T4M == 0 && (BITS == 16 || a.fast_flag != nullptr)) {
-        block_body<BITS, D, RT, true, 0, APP>(a, lds_buf);
+    if constexpr (PM == 2) {
+        // the images hold the dequantized tiles: no dequant, no fast flag
+        block_body<BITS, D, RT, false, 0, APP, 2>(a, lds_buf);
+    } else if (T4M == 0 && (BITS == 16 || a.fast_flag != nullptr)) {
+        block_body<BITS, D, RT, true, 0, APP, PM>(a, lds_buf);
         if (BITS != 16 && *a.fast_flag == 0) {
             __syncthreads();
-            block_body<BITS, D, RT, false, 0, APP>(a, lds_buf);
+            block_body<BITS, D, RT, false, 0, APP, PM>(a, lds_buf);
         }
     } else {
-        block_body<BITS, D, RT, false, T4M, APP>(a, lds_buf);
+        block_body<BITS, D, RT, false, T4M, APP, PM>(a, lds_buf);
     }
 }
 
-template <int BITS, int D, int RT, int T4M, bool APP = false>
+template <int BITS, int D, int RT, int T4M, bool APP = false, int PM = 0>
 static int launch_block_rt(KVCache& cc, BlockArgs& a, int n_qt, hipStream_t stream) {
     // two tile buffers (+ the Turbo4 centroid-pair table)
     const size_t shmem = (size_t)2 * BlockShape<D>::BUF + (T4M ? 256 * sizeof(float2) : 0);
-    int rc = ensure_dynamic_lds((const void*)attend_block_kernel<BITS, D, RT, T4M, APP>, shmem);
+    int rc = ensure_dynamic_lds((const void*)attend_block_kernel<BITS, D, RT, T4M, APP, PM>, shmem);
     if (rc) return rc;
     const dim3 grid = a.n_app > 0    ? dim3(a.n_app + cc.hkv * (a.n_split - 1))
                       : a.n_main > 0 ? dim3(a.n_main + n_qt * cc.hkv * a.n_split)
                                      : dim3(a.n_split, n_qt, cc.hkv);
-    hipLaunchKernelGGL((attend_block_kernel<BITS, D, RT, T4M, APP>), grid, dim3(64 * kBlockWaves), shmem,
+    hipLaunchKernelGGL((attend_block_kernel<BITS, D, RT, T4M, APP, PM>), grid, dim3(64 * block_waves<PM>()), shmem,
                        stream, a);
     QW_HIP_CHECK(hipGetLastError());
     return QW_OK;
@@ -891,16 +956,16 @@ static int pick_rt(int R, int hkv) {
     return best;
 }
 
-template <int BITS, int D, int T4M>
+template <int BITS, int D, int T4M, int PM = 0>
 static int launch_one(KVCache& cc, BlockArgs a, int rt, int n_qt, hipStream_t stream) {
     int rc = QW_OK;
     if constexpr (QW_BLOCK_MAX_RT >= 3 || QW_BLOCK_RT == 3) {
-        if (rt == 3) rc = launch_block_rt<BITS, D, 3, T4M>(cc, a, n_qt, stream);
+        if (rt == 3) rc = launch_block_rt<BITS, D, 3, T4M, false, PM>(cc, a, n_qt, stream);
     }
     if constexpr (QW_BLOCK_MAX_RT >= 2 || QW_BLOCK_RT == 2) {
-        if (rt == 2) rc = launch_block_rt<BITS, D, 2, T4M>(cc, a, n_qt, stream);
+        if (rt == 2) rc = launch_block_rt<BITS, D, 2, T4M, false, PM>(cc, a, n_qt, stream);
     }
-    if (rt == 1) rc = launch_block_rt<BITS, D, 1, T4M>(cc, a, n_qt, stream);
+    if (rt == 1) rc = launch_block_rt<BITS, D, 1, T4M, false, PM>(cc, a, n_qt, stream);
     return rc;
 }
 
@@ -909,6 +974,28 @@ static int launch_one(KVCache& cc, BlockArgs a, int rt, int n_qt, hipStream_t st
 #ifndef QW_BLOCK_ONE_LAUNCH
 #define QW_BLOCK_ONE_LAUNCH 1
 #endif
+
+// 1: prefill calls with at least kImageMinRows query rows a KV head (affine
+// and Int8 caches) dequantize each key tile once into an image of its LDS
+// buffer and attend from the images; 0: every query tile dequantizes its key
+// tiles. The expansion costs about as much as 2200 rows a KV head gain
+// (measured at 8k and 18k keys: 512 rows of 6 heads 146 -> 136 us, config 3
+// 942 -> 826 us).
+#ifndef QW_BLOCK_IMAGES
+#define QW_BLOCK_IMAGES 1
+#endif
+constexpr int kImageMinRows = 3072;
+
+namespace {
+std::mutex g_img_mu;
+std::map<std::pair<int, hipStream_t>, GrowBuffer> g_img_ws;
+// The tile images' buffer, one per (device, stream) like the other
+// transient workspaces (stream-ordered reuse; capture-safe growth).
+int image_workspace(int device, hipStream_t stream, size_t need, void** out) {
+    std::lock_guard<std::mutex> lock(g_img_mu);
+    return g_img_ws[{device, stream}].get(need, stream, out);
+}
+}  // namespace
 
 // Splits `n_tiles` key tiles into about `want` parts of at least 4 tiles.
 static void split_keys(int n_tiles, int want, int* n_split, int* tps) {
@@ -923,10 +1010,15 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     using S = BlockShape<D>;
     const int T = cc.offset;
     const int R = G * Tq;
-    const int rt = pick_rt(R, cc.hkv);
-    const int wg_rows = 16 * kBlockWaves * rt;
-    const int n_qt = (R + wg_rows - 1) / wg_rows;
     const int n_tiles = (T + S::KT - 1) / S::KT;
+    // long prefill calls (affine and Int8) dequantize each key tile once into
+    // an image of its LDS buffer and attend from the images, in query tiles
+    // of 16 kImageWaves rows
+    const bool images = QW_BLOCK_IMAGES && (BITS == 4 || BITS == 8) && T4M == 0 &&
+                        R >= kImageMinRows && n_tiles > 0;
+    const int rt = images ? 1 : pick_rt(R, cc.hkv);
+    const int wg_rows = 16 * (images ? kImageWaves : kBlockWaves) * rt;
+    const int n_qt = (R + wg_rows - 1) / wg_rows;
     const int units = n_qt * cc.hkv;
 
     BlockArgs a;
@@ -959,6 +1051,25 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     a.T_pre = T;
     a.app_int8 = 0;
     a.app = RowSrc{};
+    a.img_w = nullptr;
+    a.img = nullptr;
+    a.img_tiles = n_tiles;
+    int rc;
+    if constexpr ((BITS == 4 || BITS == 8) && T4M == 0) {
+        if (images) {
+            void* img = nullptr;
+            rc = image_workspace(cc.device, stream, (size_t)cc.hkv * n_tiles * S::BUF, &img);
+            if (rc) return rc;
+            a.img_w = (char*)img;
+            a.img = (const char*)img;
+            const size_t shmem = S::BUF;
+            rc = ensure_dynamic_lds((const void*)attend_block_kernel<BITS, D, 1, 0, false, 1>, shmem);
+            if (rc) return rc;
+            hipLaunchKernelGGL((attend_block_kernel<BITS, D, 1, 0, false, 1>), dim3(n_tiles, cc.hkv),
+                               dim3(64 * kBlockWaves), shmem, stream, a);
+            QW_HIP_CHECK(hipGetLastError());
+        }
+    }
 
     // Plan (one workgroup a CU, 256 CUs): query tiles that fill whole rounds
     // run unsplit and write their rows; the rest (all of them when fewer than
@@ -973,12 +1084,17 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     if (units >= 256 && 256 % cc.hkv == 0 && T4M != 2) q_main = (units / 256) * (256 / cc.hkv);
     q_main = std::min(q_main, n_qt);
     const int q_tail = n_qt - q_main;
-    int rc;
+    auto launch = [&](BlockArgs& x, int n_qt_) {
+        if constexpr ((BITS == 4 || BITS == 8) && T4M == 0) {
+            if (images) return launch_one<BITS, D, 0, 2>(cc, x, rt, n_qt_, stream);
+        }
+        return launch_one<BITS, D, T4M>(cc, x, rt, n_qt_, stream);
+    };
     if (q_main > 0 && (q_tail == 0 || !QW_BLOCK_ONE_LAUNCH)) {
         BlockArgs m = a;
         m.n_split = 1;
         m.tiles_per_split = n_tiles;
-        rc = launch_one<BITS, D, T4M>(cc, m, rt, q_main, stream);
+        rc = launch(m, q_main);
         if (rc) return rc;
     }
     if (q_tail == 0) return QW_OK;
@@ -1002,7 +1118,7 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
         t.part_o = (float*)cc.ws_ptr;
         t.part_ml = (float2*)((char*)cc.ws_ptr + o_bytes);
     }
-    rc = launch_one<BITS, D, T4M>(cc, t, rt, q_tail, stream);
+    rc = launch(t, q_tail);
     if (rc) return rc;
     if (n_split > 1 && T4M == 2)
         return launch_t4_merge_rotate(t.part_o, t.part_ml, n_split, t.PR, R, cc.hkv, D, G, Tq, 16,
@@ -1067,6 +1183,9 @@ static int launch_block_append_bits(KVCache& cc, const f16* q, int G, int L, con
     a.app.v = v_new;
     a.app.row_stride = D;
     a.app.head_stride = (int64_t)L * D;
+    a.img_w = nullptr;
+    a.img = nullptr;
+    a.img_tiles = 0;
     int n_pre, tps;
     // (the Turbo4 fused pass's merge takes up to 128 partials)
     const int want = std::max(1, (256 - cc.hkv) / cc.hkv);

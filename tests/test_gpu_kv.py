@@ -232,6 +232,10 @@ def test_served_verify_blocks_vs_oracle(oracle_lib, bits, T_prefix, L, hq):
     (4, 0, 100, True, 256, 24, 4, None),        # prefill into an empty cache
     (4, 777, 5, True, 128, 32, 8, None),        # head_dim 128, G = 4
     (8, 4000, 17, True, 128, 8, 8, None),       # no GQA sharing (G = 1), 17 rows
+    # 3072+ rows a KV head: key tiles dequantized once into LDS images
+    (4, 3000, 520, True, 256, 24, 4, [0, 1, 63, 64, 300, 519]),   # 3120 rows a KV head
+    (4, 500, 400, False, 128, 16, 2, [0, 5, 128, 399]),           # head_dim 128, no mask
+    (8, 0, 520, True, 256, 24, 4, [0, 1, 200, 519]),              # into an empty cache
 ])
 def test_block_attention_vs_oracle(oracle_lib, bits, T_prefix, L, causal, D, hq, hkv, rows):
     import qw_amd
@@ -561,6 +565,7 @@ def test_int8_append_and_fetch_bit_exact(oracle_lib, D):
     (1000, 2, True),     # 2-row verify block (decode kernel)
     (3000, 16, True),    # 16-row verify block (block kernel)
     (300, 64, False),    # block kernel, no mask
+    (2000, 520, True),   # 3120 rows a KV head: key tiles dequantized once into LDS images
 ])
 def test_int8_attention_vs_oracle(oracle_lib, T_prefix, L, causal):
     """Attention on an Int8 cache equals the reference's fetch-then-SDPA
@@ -608,8 +613,8 @@ def test_int8_snapshot_round_trip_and_trim():
 @pytest.mark.parametrize("mode", ["affine4", "affine8", "int8"])
 @pytest.mark.parametrize("D", [256, 128])
 def test_decode_layer_call_stores_what_update_stores(mode, D):
-    """A one-row update_and_attention appends inside the split-K merge; the
-    cache it leaves equals update() of the same rows, codes, scales and biases
+    """A one-row update_and_attention appends in the decode launch's append
+    unit; the cache it leaves equals update() of the same rows, codes, scales and biases
     (export bit for bit), over decode steps into a partly filled 8-key V block,
     and its output equals attention over the updated cache."""
     import qw_amd
