@@ -282,19 +282,24 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     // kernels' arithmetic; wave w takes rows w, w + NW, ..., four at a time
     // with their loads issued first) and staged as fp16 in the second tile
     // buffer, which the prologue leaves alone; the centroid-pair table goes
-    // behind the two buffers. One barrier covers both.
-    f16* const sq = (f16*)(lds + BUF);
+    // behind the two buffers. One barrier covers both. (The image launches
+    // stage q from the start of the two buffers, one barrier more before the
+    // first tile's copy; they need no pair table, the expansion launch no q.)
+    f16* const sq = (f16*)(lds + (PM == 2 ? 0 : BUF));
     if constexpr (T4) {
-        static_assert(NW * WROWS * D * sizeof(f16) <= BUF, "staged q rows exceed a tile buffer");
-        float2* const cp = (float2*)(lds + 2 * BUF);
-        const float* cb = a.t4_tab + T4Tab<D>::cb;
-        for (int bb = tid; bb < 256; bb += 64 * NW) cp[bb] = float2{cb[bb & 15], cb[bb >> 4]};
+        static_assert(NW * WROWS * D * sizeof(f16) <= (PM == 2 ? 2 : 1) * BUF,
+                      "staged q rows exceed the tile buffers");
+        if constexpr (PM != 2) {
+            float2* const cp = (float2*)(lds + 2 * BUF);
+            const float* cb = a.t4_tab + T4Tab<D>::cb;
+            for (int bb = tid; bb < 256; bb += 64 * NW) cp[bb] = float2{cb[bb & 15], cb[bb >> 4]};
+        }
         constexpr int VPL = D / 64, NB = 4;
         using HV = std::conditional_t<VPL == 4, half4v, half2v>;
         float si[VPL], so[VPL];
         t4_lane_signs<D>(a.t4_tab + T4Tab<D>::k_s1, lane, si);
         t4_lane_signs<D>(a.t4_tab + T4Tab<D>::k_s2, lane, so);
-        for (int k0 = 0; k0 < WROWS; k0 += NB) {
+        for (int k0 = 0; k0 < (PM == 1 ? 0 : WROWS); k0 += NB) {
             if (row0 + wave + NW * k0 >= a.R) break;  // wave-uniform
             float y[NB][VPL];
 #pragma unroll
@@ -354,6 +359,8 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
             qb[rt][m] = __builtin_bit_cast(half8, y);
         }
     }
+
+    if constexpr (T4 && PM == 2) __syncthreads();  // staged q read before the first copy
 
     // ---- tile loads: thread slice j (of PER) -> (key kk, 32-dim slice q32)
     // of K and (8-key block vb, 4 physical dim slots from 4 vj) of V. A
@@ -894,7 +901,7 @@ __global__ __launch_bounds__(64 * block_waves<PM>(), 1) void attend_block_kernel
     }
     if constexpr (PM == 2) {
         // the images hold the dequantized tiles: no dequant, no fast flag
-        block_body<BITS, D, RT, false, 0, APP, 2>(a, lds_buf);
+        block_body<BITS, D, RT, false, T4M, APP, 2>(a, lds_buf);
     } else if (T4M == 0 && (BITS == 16 || a.fast_flag != nullptr)) {
         block_body<BITS, D, RT, true, 0, APP, PM>(a, lds_buf);
         if (BITS != 16 && *a.fast_flag == 0) {
@@ -1014,7 +1021,7 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     // long prefill calls (affine and Int8) dequantize each key tile once into
     // an image of its LDS buffer and attend from the images, in query tiles
     // of 16 kImageWaves rows
-    const bool images = QW_BLOCK_IMAGES && (BITS == 4 || BITS == 8) && T4M == 0 &&
+    const bool images = QW_BLOCK_IMAGES && (BITS == 4 || BITS == 8) && T4M != 2 &&
                         R >= kImageMinRows && n_tiles > 0;
     const int rt = images ? 1 : pick_rt(R, cc.hkv);
     const int wg_rows = 16 * (images ? kImageWaves : kBlockWaves) * rt;
@@ -1055,17 +1062,18 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     a.img = nullptr;
     a.img_tiles = n_tiles;
     int rc;
-    if constexpr ((BITS == 4 || BITS == 8) && T4M == 0) {
+    if constexpr ((BITS == 4 || BITS == 8) && T4M != 2) {
         if (images) {
             void* img = nullptr;
             rc = image_workspace(cc.device, stream, (size_t)cc.hkv * n_tiles * S::BUF, &img);
             if (rc) return rc;
             a.img_w = (char*)img;
             a.img = (const char*)img;
-            const size_t shmem = S::BUF;
-            rc = ensure_dynamic_lds((const void*)attend_block_kernel<BITS, D, 1, 0, false, 1>, shmem);
+            // (Turbo4: the store's centroid-pair table sits behind two buffers)
+            const size_t shmem = T4M ? 2 * S::BUF + 256 * sizeof(float2) : S::BUF;
+            rc = ensure_dynamic_lds((const void*)attend_block_kernel<BITS, D, 1, T4M, false, 1>, shmem);
             if (rc) return rc;
-            hipLaunchKernelGGL((attend_block_kernel<BITS, D, 1, 0, false, 1>), dim3(n_tiles, cc.hkv),
+            hipLaunchKernelGGL((attend_block_kernel<BITS, D, 1, T4M, false, 1>), dim3(n_tiles, cc.hkv),
                                dim3(64 * kBlockWaves), shmem, stream, a);
             QW_HIP_CHECK(hipGetLastError());
         }
@@ -1085,8 +1093,8 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     q_main = std::min(q_main, n_qt);
     const int q_tail = n_qt - q_main;
     auto launch = [&](BlockArgs& x, int n_qt_) {
-        if constexpr ((BITS == 4 || BITS == 8) && T4M == 0) {
-            if (images) return launch_one<BITS, D, 0, 2>(cc, x, rt, n_qt_, stream);
+        if constexpr ((BITS == 4 || BITS == 8) && T4M != 2) {
+            if (images) return launch_one<BITS, D, T4M, 2>(cc, x, rt, n_qt_, stream);
         }
         return launch_one<BITS, D, T4M>(cc, x, rt, n_qt_, stream);
     };
@@ -1206,6 +1214,8 @@ static int launch_block_append_bits(KVCache& cc, const f16* q, int G, int L, con
     return launch_partial_merge(a.part_o, a.part_ml, a.n_split, R, 0, R, cc.hkv, D, G, L, out,
                                 stream, T4M ? 16 : BITS);
 }
+
+int block_image_min_rows() { return QW_BLOCK_IMAGES ? kImageMinRows : 1 << 30; }
 
 bool block_append_fits(const KVCache& cc, int G, int L) {
     return QW_BLOCK_APPEND && cc.affine() && (cc.D == 128 || cc.D == 256) && L >= 2 &&

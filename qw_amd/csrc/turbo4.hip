@@ -909,8 +909,11 @@ int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float
     // place; past that, its per-tile dequantization (repeated for every query
     // tile) costs more than expanding the cache once for the fp16 kernel
     // (measured at 4 q heads a KV head, depth 8k and 32k: 1024 rows a head
-    // 320 against 329 us, 2048 rows 651 against 599 us).
-    if (QW_T4_BLOCK && (n_q_heads / c.hkv) * n_rows <= kT4BlockRows)
+    // 320 against 329 us, 2048 rows 651 against 599 us). From
+    // block_image_min_rows() on, the block kernel expands the tiles once into
+    // LDS images itself.
+    if (QW_T4_BLOCK && ((n_q_heads / c.hkv) * n_rows <= kT4BlockRows ||
+                        (n_q_heads / c.hkv) * n_rows >= block_image_min_rows()))
         return turbo4_block(c, q, n_q_heads, n_rows, scale, causal, false, out, stream);
     const int capv = (T + 255) / 256 * 256;
     const size_t kv_bytes = (size_t)c.hkv * capv * D * sizeof(f16);
