@@ -992,6 +992,10 @@ static int launch_one(KVCache& cc, BlockArgs a, int rt, int n_qt, hipStream_t st
 #define QW_BLOCK_IMAGES 1
 #endif
 constexpr int kImageMinRows = 3072;
+// Turbo4 (the block kernel's fp16 arithmetic on the expansion's values): from
+// 1025 rows a KV head, where the alternative expands the cache to fp16 rows
+// at about the images' cost.
+constexpr int kT4ImageMinRows = 1025;
 
 namespace {
 std::mutex g_img_mu;
@@ -1022,7 +1026,7 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     // an image of its LDS buffer and attend from the images, in query tiles
     // of 16 kImageWaves rows
     const bool images = QW_BLOCK_IMAGES && (BITS == 4 || BITS == 8) && T4M != 2 &&
-                        R >= kImageMinRows && n_tiles > 0;
+                        R >= (T4M ? kT4ImageMinRows : kImageMinRows) && n_tiles > 0;
     const int rt = images ? 1 : pick_rt(R, cc.hkv);
     const int wg_rows = 16 * (images ? kImageWaves : kBlockWaves) * rt;
     const int n_qt = (R + wg_rows - 1) / wg_rows;
@@ -1215,7 +1219,9 @@ static int launch_block_append_bits(KVCache& cc, const f16* q, int G, int L, con
                                 stream, T4M ? 16 : BITS);
 }
 
-int block_image_min_rows() { return QW_BLOCK_IMAGES ? kImageMinRows : 1 << 30; }
+int block_image_min_rows(bool turbo4) {
+    return QW_BLOCK_IMAGES ? (turbo4 ? kT4ImageMinRows : kImageMinRows) : 1 << 30;
+}
 
 bool block_append_fits(const KVCache& cc, int G, int L) {
     return QW_BLOCK_APPEND && cc.affine() && (cc.D == 128 || cc.D == 256) && L >= 2 &&

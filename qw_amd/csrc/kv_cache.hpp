@@ -197,9 +197,9 @@ int launch_block_attention(KVCache& c, const f16* q, int G, int n_rows, float sc
 // over the cache including them, as update + launch_block_attention would.
 // block_append_fits: the shapes it takes; the caller reserves the capacity.
 bool block_append_fits(const KVCache& c, int G, int n_rows);
-// Query rows a KV head from which block attention on an affine, Int8 or Turbo4
-// cache expands the key tiles once into LDS images.
-int block_image_min_rows();
+// Query rows a KV head from which block attention on an affine or Int8
+// (turbo4: a Turbo4) cache expands the key tiles once into LDS images.
+int block_image_min_rows(bool turbo4);
 // The same for a Turbo4 cache (one query tile, at least 256 cached rows,
 // capacity reserved): fused as launch_block_attention_t4's fused pass (out:
 // the rows rotated back), else its fp16 arithmetic (out: rotated-basis rows).

@@ -913,7 +913,7 @@ int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float
     // block_image_min_rows() on, the block kernel expands the tiles once into
     // LDS images itself.
     if (QW_T4_BLOCK && ((n_q_heads / c.hkv) * n_rows <= kT4BlockRows ||
-                        (n_q_heads / c.hkv) * n_rows >= block_image_min_rows()))
+                        (n_q_heads / c.hkv) * n_rows >= block_image_min_rows(true)))
         return turbo4_block(c, q, n_q_heads, n_rows, scale, causal, false, out, stream);
     const int capv = (T + 255) / 256 * 256;
     const size_t kv_bytes = (size_t)c.hkv * capv * D * sizeof(f16);

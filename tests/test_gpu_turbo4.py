@@ -228,8 +228,8 @@ def fused_verify_route(T, L, causal, G):
     (65532, 4, True, 256),    # 65536 tokens, 64 key stages a split
     (1000, 16, True, 256),    # 16-row verify block
     (900, 128, True, 256),    # prefill chunk, 768 rows a KV head: block kernel on the packed cache
-    (700, 200, True, 256),    # 1200 rows a KV head: fp16 expansion + fp16 block kernel
-    (600, 520, True, 256),    # 3120 rows a KV head: the block kernel from LDS tile images
+    (700, 200, True, 256),    # 1200 rows a KV head: the block kernel from LDS tile images
+    (600, 520, True, 256),    # 3120 rows a KV head, likewise
     (400, 520, False, 128),   # the same at head_dim 128, non-causal
     (2000, 40, False, 128),   # non-causal 240 rows a KV head, head_dim 128: block kernel
     (777, 1, False, 128),     # head_dim 128 decode
