@@ -982,10 +982,10 @@ static int launch_one(KVCache& cc, BlockArgs a, int rt, int n_qt, hipStream_t st
 #define QW_BLOCK_ONE_LAUNCH 1
 #endif
 
-// 1: prefill calls with at least kImageMinRows query rows a KV head (affine
-// and Int8 caches) dequantize each key tile once into an image of its LDS
-// buffer and attend from the images; 0: every query tile dequantizes its key
-// tiles. The expansion costs about as much as 2200 rows a KV head gain
+// 1: prefill calls with at least kImageMinRows query rows a KV head (affine,
+// Int8 and fp16 caches) dequantize (fp16: lay out) each key tile once into an
+// image of its LDS buffer and attend from the images; 0: every query tile
+// does that work again. The expansion costs about as much as 2200 rows a KV head gain
 // (measured at 8k and 18k keys: 512 rows of 6 heads 146 -> 136 us, config 3
 // 942 -> 826 us).
 #ifndef QW_BLOCK_IMAGES
@@ -1022,10 +1022,10 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     const int T = cc.offset;
     const int R = G * Tq;
     const int n_tiles = (T + S::KT - 1) / S::KT;
-    // long prefill calls (affine and Int8) dequantize each key tile once into
-    // an image of its LDS buffer and attend from the images, in query tiles
-    // of 16 kImageWaves rows
-    const bool images = QW_BLOCK_IMAGES && (BITS == 4 || BITS == 8) && T4M != 2 &&
+    // long prefill calls dequantize (fp16: lay out) each key tile once into an
+    // image of its LDS buffer and attend from the images, in query tiles of
+    // 16 kImageWaves rows
+    const bool images = QW_BLOCK_IMAGES && T4M != 2 &&
                         R >= (T4M ? kT4ImageMinRows : kImageMinRows) && n_tiles > 0;
     const int rt = images ? 1 : pick_rt(R, cc.hkv);
     const int wg_rows = 16 * (images ? kImageWaves : kBlockWaves) * rt;
@@ -1066,7 +1066,7 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     a.img = nullptr;
     a.img_tiles = n_tiles;
     int rc;
-    if constexpr ((BITS == 4 || BITS == 8) && T4M != 2) {
+    if constexpr (T4M != 2) {
         if (images) {
             void* img = nullptr;
             rc = image_workspace(cc.device, stream, (size_t)cc.hkv * n_tiles * S::BUF, &img);
@@ -1097,7 +1097,7 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     q_main = std::min(q_main, n_qt);
     const int q_tail = n_qt - q_main;
     auto launch = [&](BlockArgs& x, int n_qt_) {
-        if constexpr ((BITS == 4 || BITS == 8) && T4M != 2) {
+        if constexpr (T4M != 2) {
             if (images) return launch_one<BITS, D, T4M, 2>(cc, x, rt, n_qt_, stream);
         }
         return launch_one<BITS, D, T4M>(cc, x, rt, n_qt_, stream);

@@ -236,6 +236,7 @@ def test_served_verify_blocks_vs_oracle(oracle_lib, bits, T_prefix, L, hq):
     (4, 3000, 520, True, 256, 24, 4, [0, 1, 63, 64, 300, 519]),   # 3120 rows a KV head
     (4, 500, 400, False, 128, 16, 2, [0, 5, 128, 399]),           # head_dim 128, no mask
     (8, 0, 520, True, 256, 24, 4, [0, 1, 200, 519]),              # into an empty cache
+    (16, 2000, 520, True, 256, 24, 4, [0, 1, 300, 519]),          # fp16 cache (layout images)
 ])
 def test_block_attention_vs_oracle(oracle_lib, bits, T_prefix, L, causal, D, hq, hkv, rows):
     import qw_amd
