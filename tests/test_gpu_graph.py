@@ -150,8 +150,8 @@ def test_graph_dlsa_first_use_inside_capture():
 
 
 def test_graph_turbo4_routes():
-    """Turbo4 attention captured in a HIP graph: the expansion route (one
-    decode row) and the fused verify route (4 causal rows past 2048 tokens).
+    """Turbo4 attention captured in a HIP graph: the decode route (one row)
+    and the fused verify route (4 causal rows past 2048 tokens).
     The route's workspace is per stream, so both capture; replays equal the
     eager outputs, with eager work between the replays, also after a larger
     call grows the stream's workspace."""
@@ -193,3 +193,46 @@ def test_graph_turbo4_routes():
         np.testing.assert_array_equal(_np(o4), want4, err_msg=f"after growth, verify replay {rep}")
     del g
     c.close()
+
+
+@pytest.mark.parametrize("mode,L", [("affine8", 600), ("turbo4", 200)])
+def test_graph_tile_image_route(mode, L):
+    """A long prefill call (the key tiles expanded once into LDS images, then
+    copied into LDS by the attention launch) captured in a HIP graph: replays
+    equal the eager output, with eager work between them, also after a larger
+    call grows the stream's image workspace."""
+    r = rng(21)
+    H, G, D, T = 4, 6, 256, 1500
+    c = _cache(mode, r, H, T, D)
+    q = _gpu(r.standard_normal((H * G, L, D)).astype(np.float16))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):  # size the stream's workspaces before capturing
+        want = _np(c.attention(q, 1 / 16, causal=True))
+    torch.cuda.synchronize()
+    assert np.isfinite(want).all()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        o = c.attention(q, 1 / 16, causal=True)
+    for rep in range(3):
+        o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(_np(o), want, err_msg=f"replay {rep}")
+        _ = (q.float() * 2).sum().item()  # eager work between replays
+    # more keys: a larger image workspace on the same stream
+    k = _gpu(r.standard_normal((H, 2000, D)).astype(np.float16))
+    big_c = _cache(mode, r, H, 1, D)
+    big_c.update(k, k)
+    with torch.cuda.stream(s):
+        big = _np(big_c.attention(q, 1 / 16, causal=True))
+    torch.cuda.synchronize()
+    assert np.isfinite(big).all()
+    for rep in range(2):
+        o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(_np(o), want, err_msg=f"after growth, replay {rep}")
+    del g
+    c.close()
+    big_c.close()
