@@ -82,9 +82,26 @@ __device__ __forceinline__ int block_exclusive_scan(int x, int* sm, int& tot) {
     return incl - x;
 }
 
-// Histogram increment of `digit` for the lanes with `take`, aggregated over
-// the wave: one LDS atomic per distinct digit (the first radix pass sees few
-// distinct top bytes, and per-lane atomics on them would serialize).
+// Ascending sort of a thread's N register values (bitonic network, N a power
+// of two).
+template <int N>
+__device__ __forceinline__ void sort_regs(uint32_t (&x)[N]) {
+#pragma unroll
+    for (int k = 2; k <= N; k <<= 1)
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1)
+#pragma unroll
+            for (int i = 0; i < N; i++) {
+                const int l = i ^ j;
+                if (l > i) {
+                    const uint32_t lo = min(x[i], x[l]), hi = max(x[i], x[l]);
+                    const bool up = (i & k) == 0;
+                    x[i] = up ? lo : hi;
+                    x[l] = up ? hi : lo;
+                }
+            }
+}
+
 __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int mask) {
     const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)x, mask);
     const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(x >> 32), mask);
@@ -166,7 +183,25 @@ __global__ __launch_bounds__(1024) void dlsa_select_kernel(SelectArgs a) {
             for (int i = t; i < 16 * 256; i += T) (&whist[0][0])[i] = 0;
             __syncthreads();
             bool nan = false;
-            if (in_regs) {
+            if (in_regs && shift == 24) {
+                // The first digit (sign and top exponent bits) takes few
+                // values: the thread sorts its keys' digits and adds one count
+                // a run, about 3x fewer atomics on the few busy bins.
+                uint32_t d[kKeysPerThread];
+#pragma unroll
+                for (int j = 0; j < kKeysPerThread; j++) d[j] = t + j * T < v ? kr[j] >> 24 : 256u;
+                sort_regs(d);
+                uint32_t run = 1;
+#pragma unroll
+                for (int j = 0; j < kKeysPerThread; j++) {
+                    if (j + 1 < kKeysPerThread && d[j] == d[j + 1]) {
+                        run++;
+                    } else {
+                        if (d[j] < 256u) atomicAdd(&whist[wave][d[j]], run);
+                        run = 1;
+                    }
+                }
+            } else if (in_regs) {
 #pragma unroll
                 for (int j = 0; j < kKeysPerThread; j++)
                     if (t + j * T < v && (kr[j] & pmask) == prefix)
