@@ -110,7 +110,7 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t x, int mask) {
 
 __global__ __launch_bounds__(1024) void dlsa_select_kernel(SelectArgs a) {
     __shared__ uint64_t sel[kSelectMax];
-    __shared__ int scan[2 * 1024];
+    __shared__ __attribute__((aligned(16))) int scan[2 * 1024];
     __shared__ int cnt[kSelectMax];
     __shared__ uint32_t hist[256];
     __shared__ uint32_t whist[16][256];  // one radix histogram a wave
@@ -337,27 +337,48 @@ __global__ __launch_bounds__(1024) void dlsa_select_kernel(SelectArgs a) {
     int n_pad = 1;
     while (n_pad < n_sel) n_pad <<= 1;
     if (n_sel > 0 && n_pad <= T) {
-        // one key a thread: strides below 64 exchange within the wave by
-        // shuffles, the longer ones through LDS (two barriers a stage)
+        // One key a thread. Each wave sorts its 64 keys ascending (bitonic
+        // by shuffles), then runs of 64, 128, ... merge pairwise: a key's
+        // place in the merged run is its place in its own run plus the count
+        // of the partner run's keys before it (a branch-free binary search in
+        // LDS; keys are unique but for the padding, whose ties break left run
+        // first). One barrier a merge round, none inside a wave's sort.
+        const int lane = t & 63;
         uint64_t x = t < n_sel ? sel[t] : ~0ull;
-        for (int size = 2; size <= n_pad; size <<= 1) {
+        for (int size = 2; size <= 64; size <<= 1) {
             for (int stride = size >> 1; stride > 0; stride >>= 1) {
-                uint64_t y;
-                if (stride >= 64) {
-                    __syncthreads();
-                    sel[t] = x;
-                    __syncthreads();
-                    y = sel[t ^ stride];
-                } else {
-                    y = shfl_xor_u64(x, stride);
-                }
-                const bool keep_min = ((t & stride) == 0) == ((t & size) == 0);
+                const uint64_t y = shfl_xor_u64(x, stride);
+                const bool keep_min = ((lane & stride) == 0) == ((lane & size) == 0);
                 const uint64_t mn = x < y ? x : y, mx = x < y ? y : x;
                 x = keep_min ? mn : mx;
             }
         }
+        uint64_t* cur = sel;
+        uint64_t* nxt = reinterpret_cast<uint64_t*>(scan);  // free during the sort
+        if (t < n_pad) cur[t] = x;
         __syncthreads();
-        sel[t] = x;
+        for (int run = 64; run < n_pad; run <<= 1) {
+            if (t < n_pad) {
+                const int base = t & ~(2 * run - 1);
+                const bool left = (t & run) == 0;
+                const uint64_t* other = cur + base + (left ? run : 0);
+                int c = 0;
+                for (int step = run >> 1; step > 0; step >>= 1) {
+                    const uint64_t o = other[c + step - 1];
+                    if (left ? o < x : o <= x) c += step;
+                }
+                const uint64_t o = other[c];
+                if (left ? o < x : o <= x) c += 1;
+                nxt[base + (t & (run - 1)) + c] = x;
+            }
+            __syncthreads();
+            if (t < n_pad) x = nxt[t];
+            uint64_t* const tmp = cur;
+            cur = nxt;
+            nxt = tmp;
+        }
+        __syncthreads();
+        if (t < n_pad) sel[t] = x;
         __syncthreads();
     } else if (n_sel > 0) {
         for (int i = n_sel + t; i < n_pad; i += T) sel[i] = ~0ull;
