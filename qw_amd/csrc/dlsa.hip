@@ -75,6 +75,7 @@ struct SrcStrided {
     static constexpr bool kHasAligned = false;
     static constexpr bool kAffine = false;
     static constexpr int kNT = kDlsaNT;
+    static constexpr bool kPairs = true;  // the two-row form fits the registers
     static constexpr int NM = D / 32, NP = D / 64;
     const f16* k;
     const f16* v;
@@ -124,6 +125,7 @@ struct SrcCacheF16 {
     static constexpr bool kHasAligned = true;
     static constexpr bool kAffine = false;
     static constexpr int kNT = kDlsaNT;
+    static constexpr bool kPairs = D <= 128;  // (at D = 256 the two-row form spills)
     static constexpr int NM = D / 32, NP = D / 64;
     const f16* k;
     const f16* v;
@@ -189,6 +191,7 @@ struct SrcCacheAffine {
     // the dequantized operands and their constants fill the register budget
     // at D = 256 with two tiles in flight: one tile a batch there
     static constexpr int kNT = D == 256 ? 1 : kDlsaNT;
+    static constexpr bool kPairs = D <= 128;  // (at D = 256 the two-row form spills)
     static constexpr int NM = D / 32, NP = D / 64, NG = D / 64;
     static constexpr int KW = NM * BITS / 4;   // K words of a lane group's D/4 dims
     static constexpr int RW = D * BITS / 32;   // K words a row
@@ -317,14 +320,23 @@ struct SrcCacheAffine {
 // holds heads 4g + i x dims 64p + 4 r16 + c. P enters as an fp16 high part
 // and an fp16 remainder, so p * v is exact and the sums stay fp32 as in the
 // reference.
-template <int D, int GMAX, class Src, bool FAST>
+// RP rows a workgroup (2: one-pass prefill calls, 2G <= 16): MFMA column c
+// is query head c % G of row r0 + c / G. A tile index whose 16 entries are the
+// same keys for both rows (sinks, shared blocks) is gathered once for both;
+// otherwise each row's tile runs with the other row's columns masked.
+template <int D, int GMAX, class Src, bool FAST, int RP = 1>
 __device__ __forceinline__ void dlsa_body(const DlsaArgs& a, const Src& src) {
     constexpr int NM = D / 32;
     constexpr int NP = D / 64;  // 64-dim groups: P.V output tiles (p, c), c < 4
-    const int part = blockIdx.x, r = blockIdx.y, h = blockIdx.z;
+    const int part = blockIdx.x, r0 = blockIdx.y * RP, h = blockIdx.z;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r16 = lane & 15, g = lane >> 4;
     const int G = a.G;
+    const int nrow = RP == 1 ? 1 : min(RP, a.L - r0);  // rows this workgroup owns
+    const int NC = RP == 1 ? G : nrow * G;              // live columns
+    const int crow = RP == 1 ? 0 : r16 / G;             // the lane's column's row
+    const int chead = RP == 1 ? r16 : r16 - crow * G;   // and its head in the group
+    const bool col_ok = r16 < NC;
     // Parts split the list's width W at multiples of 16 entries, so the list
     // loads depend on the launch arguments only (not on the row's length, a
     // memory round trip of its own) and a list made of aligned key runs gives
@@ -332,16 +344,23 @@ __device__ __forceinline__ void dlsa_body(const DlsaArgs& a, const Src& src) {
     // masks the entries at or past it.
     const int e_begin = (int)((int64_t)a.W * part / a.parts) & ~15;
     const int e_end = part + 1 == a.parts ? a.W : (int)((int64_t)a.W * (part + 1) / a.parts) & ~15;
-    const int32_t* list = a.lists + (int64_t)r * a.W;
-    int len = a.lengths[r];
-    len = len < 0 ? 0 : (len > a.W ? a.W : len);
+    const int32_t* list[RP];
+    int len[RP];
+#pragma unroll
+    for (int k = 0; k < RP; k++) {
+        const int rk = min(r0 + k, a.L - 1);
+        list[k] = a.lists + (int64_t)rk * a.W;
+        const int l = a.lengths[rk];
+        len[k] = l < 0 ? 0 : (l > a.W ? a.W : l);
+    }
 
-    // Q operand: column r16 = head h*G + r16 (zero past G), 8 dims per MFMA
-    // in the source's layout.
+    // Q operand: column r16 = head h*G + r16 % G of row r0 + r16 / G (zero
+    // past the live columns), 8 dims per MFMA in the source's layout.
     half8 qop[NM];
     {
-        const bool ok = r16 < G;
-        const f16* qrow = a.q + ((int64_t)(h * G + (ok ? r16 : 0)) * a.L + r) * D;
+        const bool ok = col_ok;
+        const f16* qrow =
+            a.q + ((int64_t)(h * G + (ok ? chead : 0)) * a.L + r0 + (ok ? crow : 0)) * D;
 #pragma unroll
         for (int m = 0; m < NM; m++) {
             const int base = Src::kQ == kQNatural ? 32 * m + 8 * g : (D / 4) * g + 8 * m;
@@ -371,7 +390,8 @@ __device__ __forceinline__ void dlsa_body(const DlsaArgs& a, const Src& src) {
     // are four consecutive keys from a multiple of 4 (checked wave-wide).
     // The general (unaligned) gathers hold many scattered loads: they take
     // one tile at a time (NT = 1).
-    auto batch = [&](auto aligned_tag, auto nt_tag, const int* key_a, const bool* ok_a) {
+    auto batch = [&](auto aligned_tag, auto nt_tag, const int* key_a, const bool* ok_a, int colmask) {
+        const bool my_col = RP == 1 ? col_ok : col_ok && ((colmask >> crow) & 1) != 0;
         constexpr bool ALIGNED = decltype(aligned_tag)::value;
         constexpr int NT = decltype(nt_tag)::value;
         typename Src::Regs rg[NT];
@@ -400,7 +420,7 @@ __device__ __forceinline__ void dlsa_body(const DlsaArgs& a, const Src& src) {
                                                               qop[m], sacc, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const bool ok = __shfl(ok_a[b] ? 1 : 0, 4 * g + i) != 0 && r16 < G;
+                const bool ok = __shfl(ok_a[b] ? 1 : 0, 4 * g + i) != 0 && my_col;
                 sv[b][i] = ok ? sacc[i] * a.scale2 : -INFINITY;
                 bmax = fmaxf(bmax, sv[b][i]);
             }
@@ -447,37 +467,64 @@ __device__ __forceinline__ void dlsa_body(const DlsaArgs& a, const Src& src) {
         }
     };
 
-    constexpr int NTB = Src::kNT;  // tiles a batch
+    // tiles a batch (the two-row form stages one: its three batch forms would
+    // not fit the registers with two)
+    constexpr int NTB = RP == 2 ? 1 : Src::kNT;
     const int n_tiles = (e_end - e_begin + 15) / 16;
     for (int t0 = wave; t0 < n_tiles; t0 += 4 * NTB) {
-        int key_a[NTB];  // the key of list entry tile*16 + r16 (A-operand row)
-        bool ok_a[NTB];
-        bool aligned = true;
+        int key_a[RP][NTB];  // the key of list entry tile*16 + r16 (A-operand row), row k
+        bool ok_a[RP][NTB];
 #pragma unroll
-        for (int b = 0; b < NTB; b++) {
-            const int tile = t0 + 4 * b;
-            const int e = e_begin + 16 * tile + r16;
-            int key = -1;
-            if (tile < n_tiles && e < e_end) key = list[e];
-            ok_a[b] = e < len && key >= 0 && key < a.T;
-            key_a[b] = ok_a[b] ? key : 0;
-            if constexpr (Src::kHasAligned) {
-                // each lane compares with its group's first entry
-                const int first = __shfl(key_a[b], r16 & ~3);
-                aligned = aligned && (first & 3) == 0 && key_a[b] == first + (r16 & 3);
+        for (int k = 0; k < RP; k++)
+#pragma unroll
+            for (int b = 0; b < NTB; b++) {
+                const int tile = t0 + 4 * b;
+                const int e = e_begin + 16 * tile + r16;
+                int key = -1;
+                if (tile < n_tiles && e < e_end) key = list[k][e];
+                ok_a[k][b] = e < len[k] && key >= 0 && key < a.T;
+                key_a[k][b] = ok_a[k][b] ? key : 0;
             }
-        }
         using NTall = std::integral_constant<int, NTB>;
         using NT1 = std::integral_constant<int, 1>;
-        if constexpr (Src::kHasAligned) {
-            if (__all(aligned)) {
-                batch(std::true_type{}, NTall{}, key_a, ok_a);
-            } else {
+        // row k's tiles for the columns in colmask (k a compile-time tag: the
+        // key arrays stay in registers)
+        auto run = [&](auto k_tag, int colmask) {
+            constexpr int k = decltype(k_tag)::value;
+            if constexpr (Src::kHasAligned) {
+                bool aligned = true;
 #pragma unroll
-                for (int b = 0; b < NTB; b++) batch(std::false_type{}, NT1{}, key_a + b, ok_a + b);
+                for (int b = 0; b < NTB; b++) {
+                    // each lane compares with its group's first entry
+                    const int first = __shfl(key_a[k][b], r16 & ~3);
+                    aligned = aligned && (first & 3) == 0 && key_a[k][b] == first + (r16 & 3);
+                }
+                if (__all(aligned)) {
+                    batch(std::true_type{}, NTall{}, key_a[k], ok_a[k], colmask);
+                } else {
+#pragma unroll
+                    for (int b = 0; b < NTB; b++)
+                        batch(std::false_type{}, NT1{}, key_a[k] + b, ok_a[k] + b, colmask);
+                }
+            } else {
+                batch(std::false_type{}, NTall{}, key_a[k], ok_a[k], colmask);
             }
+        };
+        using K0 = std::integral_constant<int, 0>;
+        using K1 = std::integral_constant<int, RP - 1>;
+        if constexpr (RP == 1) {
+            run(K0{}, 1);
         } else {
-            batch(std::false_type{}, NTall{}, key_a, ok_a);
+            bool same = true;
+#pragma unroll
+            for (int b = 0; b < NTB; b++)
+                same = same && key_a[0][b] == key_a[1][b] && ok_a[0][b] == ok_a[1][b];
+            if (nrow == 1 || __all(same)) {
+                run(K0{}, 3);
+            } else {
+                run(K0{}, 1);
+                run(K1{}, 2);
+            }
         }
     }
     lrun += __shfl_xor(lrun, 16);
@@ -495,19 +542,19 @@ __device__ __forceinline__ void dlsa_body(const DlsaArgs& a, const Src& src) {
     __shared__ float4v sm_acc[4][HC][D / 4];
     if (g == 0) sm_ml[wave][r16] = float2{mrun, lrun};
     const float* accf = (const float*)&sm_acc[0][0][0];
-    for (int hc0 = 0; hc0 < G; hc0 += HC) {
+    for (int hc0 = 0; hc0 < NC; hc0 += HC) {
         if (hc0 > 0) __syncthreads();  // the previous round's reads are done
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int hd = 4 * g + i;
-            if (hd >= hc0 && hd < hc0 + HC && hd < G)
+            if (hd >= hc0 && hd < hc0 + HC && hd < NC)
 #pragma unroll
                 for (int pp = 0; pp < NP; pp++)
                     sm_acc[wave][hd - hc0][16 * pp + r16] =
                         float4v{acc[pp][0][i], acc[pp][1][i], acc[pp][2][i], acc[pp][3][i]};
         }
         __syncthreads();
-        const int nh = min(HC, G - hc0);
+        const int nh = min(HC, NC - hc0);
         for (int o = threadIdx.x; o < nh * D; o += 256) {
             const int hl = o / D, d = o % D, hd = hc0 + hl;
             float M = -INFINITY;
@@ -521,7 +568,8 @@ __device__ __forceinline__ void dlsa_body(const DlsaArgs& a, const Src& src) {
                 O = __builtin_fmaf(f, accf[(w * HC + hl) * D + d], O);
                 Ls = __builtin_fmaf(f, ml.y, Ls);
             }
-            const int qh = h * G + hd;
+            const int hr = RP == 1 ? 0 : hd / G;  // the column's row
+            const int qh = h * G + hd - hr * G, r = r0 + hr;
             if (a.parts == 1) {
                 a.out[((int64_t)qh * a.L + r) * D + d] = (f16)(Ls > 0.0f ? O / Ls : 0.0f);
             } else {
@@ -537,7 +585,7 @@ __device__ __forceinline__ void dlsa_body(const DlsaArgs& a, const Src& src) {
 // One kernel per (head dim, heads per group, row source). Affine sources use
 // the exact 2-op dequant when every cached scale allows it (the cache's
 // fast_flag), else the separately rounded one.
-template <int D, int GMAX, class Src>
+template <int D, int GMAX, class Src, int RP = 1>
 __global__ __launch_bounds__(256, 2) void dlsa_kernel(DlsaArgs a, Src src, const int* fast_flag) {
     if constexpr (Src::kAffine) {
         // The exact 2-op dequant runs without waiting for the cache's fast
@@ -546,16 +594,16 @@ __global__ __launch_bounds__(256, 2) void dlsa_kernel(DlsaArgs a, Src src, const
         // same elements) replace the first's. A null flag (Int8 caches) takes
         // the separately rounded dequant directly.
         if (fast_flag != nullptr) {
-            dlsa_body<D, GMAX, Src, true>(a, src);
+            dlsa_body<D, GMAX, Src, true, RP>(a, src);
             if (*fast_flag == 0) {
                 __syncthreads();
-                dlsa_body<D, GMAX, Src, false>(a, src);
+                dlsa_body<D, GMAX, Src, false, RP>(a, src);
             }
         } else {
-            dlsa_body<D, GMAX, Src, false>(a, src);
+            dlsa_body<D, GMAX, Src, false, RP>(a, src);
         }
     } else {
-        dlsa_body<D, GMAX, Src, true>(a, src);
+        dlsa_body<D, GMAX, Src, true, RP>(a, src);
     }
 }
 
@@ -645,9 +693,20 @@ struct DlsaSource {
     int64_t khs = 0, krs = 0, vhs = 0, vrs = 0;
 };
 
+constexpr int kPairMinWorkgroups = 192;
+
 template <int D, int GM, class Src>
 static void launch_dlsa_kernel(const Src& src, const DlsaArgs& a, dim3 grid, const int* fast,
                                hipStream_t stream) {
+    // one-pass calls with rows to spare: two rows a workgroup (the grid keeps
+    // at least kPairMinWorkgroups workgroups)
+    if constexpr (Src::kPairs) {
+        if (a.parts == 1 && 2 * a.G <= 16 && (int64_t)a.L * a.hkv >= 2 * kPairMinWorkgroups) {
+            hipLaunchKernelGGL((dlsa_kernel<D, GM, Src, 2>), dim3(grid.x, (a.L + 1) / 2, grid.z),
+                               dim3(256), 0, stream, a, src, fast);
+            return;
+        }
+    }
     hipLaunchKernelGGL((dlsa_kernel<D, GM, Src>), grid, dim3(256), 0, stream, a, src, fast);
 }
 

@@ -143,6 +143,35 @@ def test_prefill_rows_vs_oracle(oracle_lib, L):
     assert_close(out[:, sel], ref, f"prefill rows L={L}")
 
 
+@pytest.mark.parametrize("D,H,G", [(256, 4, 6), (128, 2, 8)])
+def test_prefill_row_pairs_vs_oracle(oracle_lib, D, H, G):
+    """One-pass prefill calls take two rows a workgroup: a tile whose 16
+    entries are the same keys for both rows (sinks, the chunk's blocks) is
+    gathered once for both, other tiles once a row. An odd row count leaves
+    the last workgroup one row; the rows' lengths differ (so some tiles split
+    inside the shared part) and some entries are -1 or past the keys (skipped)."""
+    import qw_amd
+
+    T0, L = 4096, 203
+    T = T0 + L
+    r = rng(9100 + D)
+    k = r.standard_normal((H, T, D)).astype(np.float16)
+    v = r.standard_normal((H, T, D)).astype(np.float16)
+    q = r.standard_normal((H * G, L, D)).astype(np.float16)
+    lists = prefill_lists(T0, L, 81 + D, n_blocks=2)
+    W = lists.shape[1]
+    lengths = (W - (np.arange(L) % 5) * 37).astype(np.int32)
+    lists[::11, 5] = -1
+    lists[::13, 9] = T + 5
+    out = _np(qw_amd.sparse_attention(_gpu(q), _gpu(k), _gpu(v), _gpu(lists), _gpu(lengths),
+                                      D ** -0.5))[0]
+    sel = np.array([0, 1, 2, 11, 13, 100, 101, 200, 201, 202])
+    ref = oracle_lib.dlsa_attention(np.ascontiguousarray(q[:, sel]), k, v,
+                                    np.ascontiguousarray(lists[sel]), lengths[sel], D ** -0.5)
+    assert np.isfinite(out).all()
+    assert_close(out[:, sel], ref, f"prefill row pairs D={D} G={G}")
+
+
 def test_workspace_per_stream_growth():
     """Split-K partials live in a workspace per (device, stream): calls
     alternating on two streams, with a growth of one stream's workspace in
