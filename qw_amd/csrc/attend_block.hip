@@ -77,6 +77,11 @@ struct BlockArgs {
     char* img_w;
     const char* img;
     int img_tiles;
+    // pair_h > 0 (causal image launches whose units fill whole rounds): the
+    // rows come in pair_h half tiles of NW / 2 waves' rows; unit qt holds half
+    // tile qt in waves [0, NW/2) and half tile pair_h - 1 - qt in the others,
+    // so every workgroup sees about the same number of (row, key) pairs.
+    int pair_h;
     const float* t4_tab;  // Turbo4 caches: the device tables (signs, centroids: T4Tab<D>)
     float t4_post;        // Turbo4 fused pass: scale * log2(e) in fp32
     float scale_h;      // f16(scale) as float
@@ -256,8 +261,23 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     // ---- key range of this workgroup: its split, cut at the last key any of
     // its rows can see.
     constexpr int WROWS = 16 * RT;
-    const int row0 = qt * WROWS * NW;
-    const int row_last = min(a.R, row0 + WROWS * NW) - 1;
+    int row0 = qt * WROWS * NW;
+    int row_last = min(a.R, row0 + WROWS * NW) - 1;
+    int wrow0 = row0 + WROWS * wave;
+    if constexpr (PM == 2 && !T4 && NW % 2 == 0) {
+        if (a.pair_h > 0) {
+            // causal balance: an early half tile and its mirror (a padding
+            // wave gets wrow0 = R and no rows)
+            constexpr int HR = WROWS * NW / 2;
+            const int hb = a.pair_h - 1 - qt;
+            const bool b_live = hb > qt;
+            row0 = qt * HR;
+            row_last = min(a.R, (b_live ? hb : qt) * HR + HR) - 1;
+            wrow0 = wave < NW / 2 ? qt * HR + WROWS * wave
+                                  : (b_live ? hb * HR + WROWS * (wave - NW / 2) : a.R);
+            wrow0 = min(wrow0, a.R);
+        }
+    }
     auto cut = [&](int lim_) { return APP ? min(lim_, key_hi - 1) : lim_; };
     const bool app_unit = APP && key_lo > 0;
     const int wg_lim = cut(a.causal ? a.T - a.Tq + row_last / a.G : a.T - 1);
@@ -268,7 +288,6 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     // ---- the wave's RT x 16 query rows as the B operand of S^T = K . Q'^T
     // (col = query row r16 of row tile rt, k-group g = dims 32m + 8g .. +7 of
     // MFMA step m, in the order the LDS K row holds them).
-    const int wrow0 = row0 + WROWS * wave;
     const bool wave_live = wrow0 < a.R;
     const int wave_last = min(a.R, wrow0 + WROWS) - 1;
     const int wave_lim = cut(a.causal ? a.T - a.Tq + wave_last / a.G : a.T - 1);
@@ -995,6 +1014,11 @@ static int launch_one(KVCache& cc, BlockArgs a, int rt, int n_qt, hipStream_t st
 #define QW_BLOCK_IMAGES 1
 #endif
 constexpr int kImageMinRows = 3072;
+// 1: causal image launches whose query tiles fill whole rounds pair an early
+// and a late half tile in each workgroup (equal work a CU); 0: one tile each.
+#ifndef QW_BLOCK_PAIR
+#define QW_BLOCK_PAIR 1
+#endif
 // Turbo4 (the block kernel's fp16 arithmetic on the expansion's values): from
 // 1025 rows a KV head, where the alternative expands the cache to fp16 rows
 // at about the images' cost.
@@ -1068,6 +1092,7 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     a.img_w = nullptr;
     a.img = nullptr;
     a.img_tiles = n_tiles;
+    a.pair_h = 0;
     int rc;
     if constexpr (T4M != 2) {
         if (images) {
@@ -1108,6 +1133,9 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     if (q_main > 0 && (q_tail == 0 || !QW_BLOCK_ONE_LAUNCH)) {
         BlockArgs m = a;
         m.n_split = 1;
+        // causal image launches of whole rounds: balanced half-tile pairs
+        if (QW_BLOCK_PAIR && images && causal && T4M == 0 && q_tail == 0 && Tq > 1)
+            m.pair_h = (R + wg_rows / 2 - 1) / (wg_rows / 2);
         m.tiles_per_split = n_tiles;
         rc = launch(m, q_main);
         if (rc) return rc;
@@ -1201,6 +1229,7 @@ static int launch_block_append_bits(KVCache& cc, const f16* q, int G, int L, con
     a.img_w = nullptr;
     a.img = nullptr;
     a.img_tiles = 0;
+    a.pair_h = 0;
     int n_pre, tps;
     // (the Turbo4 fused pass's merge takes up to 128 partials)
     const int want = std::max(1, (256 - cc.hkv) / cc.hkv);
