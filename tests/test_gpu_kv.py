@@ -237,6 +237,10 @@ def test_served_verify_blocks_vs_oracle(oracle_lib, bits, T_prefix, L, hq):
     (4, 500, 400, False, 128, 16, 2, [0, 5, 128, 399]),           # head_dim 128, no mask
     (8, 0, 520, True, 256, 24, 4, [0, 1, 200, 519]),              # into an empty cache
     (16, 2000, 520, True, 256, 24, 4, [0, 1, 300, 519]),          # fp16 cache (layout images)
+    # causal image launch of whole rounds with paired half tiles: 12144 rows a
+    # KV head make 127 half tiles of 96 rows, so unit 63 holds half tile 63
+    # alone and unit 0 pairs half tile 0 with the partial half tile 126
+    (8, 1000, 2024, True, 256, 24, 4, [0, 15, 16, 1007, 1008, 1023, 1024, 2015, 2016, 2023]),
 ])
 def test_block_attention_vs_oracle(oracle_lib, bits, T_prefix, L, causal, D, hq, hkv, rows):
     import qw_amd
