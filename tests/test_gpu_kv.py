@@ -241,6 +241,9 @@ def test_served_verify_blocks_vs_oracle(oracle_lib, bits, T_prefix, L, hq):
     # KV head make 127 half tiles of 96 rows, so unit 63 holds half tile 63
     # alone and unit 0 pairs half tile 0 with the partial half tile 126
     (8, 1000, 2024, True, 256, 24, 4, [0, 15, 16, 1007, 1008, 1023, 1024, 2015, 2016, 2023]),
+    # the same at head_dim 128, 8 KV heads: 6000 rows a KV head, 32 units a
+    # head, 63 half tiles (the last one partial)
+    (4, 200, 1500, True, 128, 32, 8, [0, 23, 24, 743, 744, 767, 768, 1487, 1488, 1499]),
 ])
 def test_block_attention_vs_oracle(oracle_lib, bits, T_prefix, L, causal, D, hq, hkv, rows):
     import qw_amd
