@@ -536,6 +536,118 @@ def bench_dlsa_cache(torch, qw_amd, reps: int, T: int = 131072, layers: int = LA
     return {"T": T, "W": int(W), "ms": st["median"], "stats": st, "bytes": bytes_call}
 
 
+def _ceil_lib(qw_amd):
+    import ctypes
+
+    path = os.path.join(os.path.dirname(os.path.abspath(qw_amd.__file__)), "libqwceil.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: run `python -m qw_amd.build`")
+    L = ctypes.CDLL(path)
+    L.qwc_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
+                           ctypes.c_int, ctypes.c_void_p]
+    L.qwc_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+                           ctypes.c_void_p]
+    return L
+
+
+def bench_ceilings(torch, qw_amd, reps: int):
+    """The box's ceilings, measured:
+    - a 2 GiB device-to-device copy (a 128-bit grid-stride copy kernel, and
+      torch's copy_), reported as bytes moved (read + write) per second;
+    - the config-2 read floor: every byte of 16 rotated 37.8 MB buffers (the
+      size of one config-2 attention call's KV, 604 MB in all, more than the
+      256 MB MALL) read once by a plain load-and-XOR kernel, graph-replayed
+      like the headline; the best of a sweep of grids and loads in flight;
+    - the same read kernel over one 2 GiB buffer (the stream rate);
+    - torch.matmul fp16 8192^3 (hipBLASLt), TFLOP/s."""
+    dev = torch.device("cuda:0")
+    L = _ceil_lib(qw_amd)
+    out = {}
+
+    def st():
+        return torch.cuda.current_stream(dev).cuda_stream
+
+    def time_fn(fn, iters):
+        fn()
+        torch.cuda.synchronize()
+        ms = []
+        for _ in range(iters):
+            s = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            s.record()
+            fn()
+            e.record()
+            torch.cuda.synchronize()
+            ms.append(s.elapsed_time(e))
+        return _stats(ms)
+
+    nb = 2 << 30
+    src = torch.empty(nb, dtype=torch.uint8, device=dev)
+    dst = torch.empty(nb, dtype=torch.uint8, device=dev)
+    src.fill_(1)
+    sink = torch.zeros(2048 * 512, dtype=torch.int32, device=dev)
+
+    def copy_k():
+        rc = L.qwc_copy(dst.data_ptr(), src.data_ptr(), nb, 4096, st())
+        assert rc == 0, rc
+
+    ck = time_fn(copy_k, 20)
+    ct = time_fn(lambda: dst.copy_(src), 20)
+    out["copy_2GiB"] = {
+        "GB_s_kernel": round(2 * nb / (ck["median"] * 1e-3) / 1e9, 1),
+        "GB_s_torch_copy": round(2 * nb / (ct["median"] * 1e-3) / 1e9, 1),
+        "ms_kernel": round(ck["median"], 4), "bytes_moved": 2 * nb,
+        "note": "GB/s counts the bytes read plus the bytes written"}
+
+    def read_big(blocks, unroll):
+        rc = L.qwc_read(src.data_ptr(), nb, sink.data_ptr(), blocks, unroll, st())
+        assert rc == 0, rc
+
+    best = None
+    for blocks in (1024, 2048):
+        for unroll in (2, 4, 8):
+            r = time_fn(lambda: read_big(blocks, unroll), 10)
+            gbs = nb / (r["median"] * 1e-3) / 1e9
+            if best is None or gbs > best[0]:
+                best = (gbs, blocks, unroll)
+    out["read_2GiB"] = {"GB_s": round(best[0], 1), "blocks": best[1], "unroll": best[2]}
+    del src, dst
+    torch.cuda.empty_cache()
+
+    # the config-2-sized read floor
+    c2_bytes = 32769 * HKV * kv_bytes_per_token_head(4) + 2 * HQ * D * 2
+    rb = (c2_bytes + 1023) // 1024 * 1024
+    bufs = [torch.empty(rb, dtype=torch.uint8, device=dev).fill_(i + 1) for i in range(LAYERS)]
+    sweep = {}
+    best = None
+    for blocks in (256, 512, 1024):
+        for unroll in (1, 2, 4):
+            def call(i, blocks=blocks, unroll=unroll):
+                rc = L.qwc_read(bufs[i].data_ptr(), rb, sink.data_ptr(), blocks, unroll, st())
+                assert rc == 0, rc
+            r = replay_stats(torch, call, LAYERS, LAYERS, reps)
+            sweep[f"{blocks}x{unroll}"] = round(r["median"] * 1e3, 3)
+            if best is None or r["median"] < best[0]["median"]:
+                best = (r, blocks, unroll)
+    r, blocks, unroll = best
+    out["read_c2_size"] = {
+        "us": round(r["median"] * 1e3, 3), "GB_s": round(rb / (r["median"] * 1e-3) / 1e9, 1),
+        "bytes": rb, "blocks": blocks, "unroll": unroll, "sweep_us": sweep,
+        "note": "16 rotated buffers, one graph of 16 reads, median of the replays"}
+    del bufs
+    torch.cuda.empty_cache()
+
+    n = 8192
+    a = torch.randn((n, n), device=dev, dtype=torch.float16)
+    b = torch.randn((n, n), device=dev, dtype=torch.float16)
+    r = time_fn(lambda: torch.matmul(a, b), 20)
+    out["gemm_fp16_8192"] = {"TFLOP_s": round(2 * n ** 3 / (r["median"] * 1e-3) / 1e12, 1),
+                             "ms": round(r["median"], 4), "route": "torch.matmul (hipBLASLt)"}
+    del a, b
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_threads():
     """Threads for the CPU baseline: every core this process may run on,
     capped by OMP_NUM_THREADS when the environment sets it (the GPU box's

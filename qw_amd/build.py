@@ -24,6 +24,9 @@ ARCH = "gfx950"
 
 SOURCES = ["kv_cache.hip", "attend_decode.hip", "attend_block.hip", "dlsa.hip", "dlsa_select.hip",
            "rope.hip", "turbo4.hip", "abi.hip"]
+# The measurement library (read-floor and copy kernels), loaded by bench.py only.
+CEIL_SOURCES = ["ceiling.hip"]
+CEIL_OUT = os.path.join(HERE, "libqwceil.so")
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -57,20 +60,27 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every source and link libqwattn.so; always rebuilds."""
-    os.makedirs(BUILD_DIR, exist_ok=True)
-    jobs = min(len(SOURCES), max(1, (os.cpu_count() or 2)))
-    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = OUT + ".tmp"
+def _link(objs, out: str) -> None:
+    tmp = out + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
-    os.replace(tmp, OUT)
+    os.replace(tmp, out)
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every source and link libqwattn.so (and the measurement library
+    libqwceil.so); always rebuilds."""
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    srcs = SOURCES + CEIL_SOURCES
+    jobs = min(len(srcs), max(1, (os.cpu_count() or 2)))
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = dict(zip(srcs, ex.map(_compile, srcs)))
+    _link([objs[s] for s in SOURCES], OUT)
+    _link([objs[s] for s in CEIL_SOURCES], CEIL_OUT)
     if verbose:
-        print(f"built {OUT}")
+        print(f"built {OUT} and {CEIL_OUT}")
     return OUT
 
 

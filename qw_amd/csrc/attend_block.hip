@@ -763,19 +763,15 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     }
     if constexpr (PM == 2) {
         // tile t's image into buffer b: 1 KB a wave instruction (lane i its
-        // 16 bytes), the LDS address from M0; waited for before the barrier.
-        // (The asm clobbers M0, which these kernels use for nothing else: no
-        // LDS-direct, movrel or message instructions; the nop keeps one wait
-        // state between the M0 write and the copy that reads it.)
+        // 16 bytes at the wave-uniform LDS address + 16 i; the compiler sets
+        // M0 and its wait state); waited for before the barrier.
         const char* img0 = a.img + (int64_t)h * a.img_tiles * BUF;
-        const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds;
         auto dma = [&](int t, int b) {
             const char* src = img0 + (int64_t)t * BUF + 16 * lane;
             for (int c = wave; c < BUF / 1024; c += NW)
-                asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-                             ::"v"(src + 1024 * c),
-                             "s"(__builtin_amdgcn_readfirstlane(lds0 + BUF * b + 1024 * c))
-                             : "memory", "m0");
+                __builtin_amdgcn_global_load_lds(
+                    (const void*)(src + 1024 * c),
+                    (__attribute__((address_space(3))) void*)(lds + BUF * b + 1024 * c), 16, 0, 0);
         };
         static_assert(BUF % 1024 == 0, "a tile buffer is whole 1 KB DMA instructions");
         if (t0 < t1) dma(t0, 0);

@@ -51,6 +51,7 @@ struct DecodeArgs {
     float2* part_ml;   // [hkv][nc][16]
     int cap, T, Tq, G, R, causal, n_sub, nc;
     float scale_h;     // f16(scale) as float
+    float inv_g;       // 1 / G
     uint32_t code_off2;  // magic offset pair of the separately rounded dequant
     const float* t4_tab;  // Turbo4 caches: the device tables (signs, centroids); else null
     // ns: workgroups that split the T cached keys (= nc, or nc - 1 with an
@@ -89,6 +90,15 @@ constexpr int decode_waves() {
 // Word 3 of a raw buffer resource on gfx9-family parts (CDNA): 32-bit data
 // format, no swizzle, no index stride.
 constexpr int kBufWord3 = 0x00020000;
+
+// Cache policy of the decode kernel's K/V loads (the instruction's sc0 / nt /
+// sc1 bits: 1, 2, 16). Non-temporal (2): the streamed cache leaves the L2 and
+// the MALL to what is reused (code, arguments, q, partials); config 2's layer
+// call measured 16.67 -> 16.10 us against the default policy.
+#ifndef QW_DECODE_KV_AUX
+#define QW_DECODE_KV_AUX 2
+#endif
+constexpr int kKvAux = QW_DECODE_KV_AUX;
 
 // Register stages a wave streams through (1: load the next sub-chunk after
 // the current one's math; 2: wait-then-prefetch ping-pong, a stage's
@@ -138,7 +148,7 @@ __device__ __forceinline__ half8 t4_expand8(uint32_t w, float r, const float2* p
 // The centroid comes from a register table (lane i holds centroid i % 16)
 // through ds_bpermute.
 template <int BITS, int D, int NW, bool FAST, bool T4 = false>
-__device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)[16], float* sm_o,
+__device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)[NW], float* sm_o,
                                             half8 (*sm_q)[64], float2* sm_t4 = nullptr) {
     using S = DecodeShape<BITS, D>;
     constexpr int NM = S::NM, DPL = S::DPL, NG = S::NG, VL = S::VL;
@@ -159,6 +169,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
     const int SS = a.ns * NW;  // stride between a wave's sub-chunks
     const int s_end = a.n_sub;
     const uint32_t magic = vconst(kMagic);
+    float* const part_o = a.part_o;
+    float2* const part_ml = a.part_ml;
 
     // One 32-key sub-chunk's loads; a wave walks its sub-chunks
     // c + ns * (wave + NW * k) through one of these.
@@ -207,7 +219,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
             for (int cc = 0; cc < KL; cc++)
                 st.kc[tile][cc] = __builtin_bit_cast(
                     u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                               rk, off_k + tile * 4 * KRB + (T4 ? 16 : 64) * cc, 32 * si * KRB, 0));
+                               rk, off_k + tile * 4 * KRB + (T4 ? 16 : 64) * cc, 32 * si * KRB, kKvAux));
         }
         if constexpr (T4) {
             const __amdgpu_buffer_rsrc_t rkp =
@@ -215,7 +227,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
 #pragma unroll
             for (int tile = 0; tile < 2; tile++)
                 st.kp[tile] = u32x4{__builtin_amdgcn_raw_buffer_load_b32(rkp, off_kp + tile * 4 * KPB,
-                                                                         32 * si * KPB, 0),
+                                                                         32 * si * KPB, kKvAux),
                                     0u, 0u, 0u};
         }
         if constexpr (AFF) {
@@ -225,16 +237,16 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
             for (int tile = 0; tile < 2; tile++) {
                 const int o = off_kp + tile * 4 * KPB;
                 if constexpr (BITS == 4 && NG == 4) {
-                    const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(rkp, o, 32 * si * KPB, 0);
+                    const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(rkp, o, 32 * si * KPB, kKvAux);
                     st.kp[tile] = u32x4{t2[0], t2[1], 0u, 0u};
                 } else if constexpr (BITS == 4) {
-                    st.kp[tile] = u32x4{__builtin_amdgcn_raw_buffer_load_b32(rkp, o, 32 * si * KPB, 0),
+                    st.kp[tile] = u32x4{__builtin_amdgcn_raw_buffer_load_b32(rkp, o, 32 * si * KPB, kKvAux),
                                         0u, 0u, 0u};
                 } else if constexpr (NG == 4) {
                     st.kp[tile] = __builtin_bit_cast(
-                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rkp, o, 32 * si * KPB, 0));
+                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rkp, o, 32 * si * KPB, kKvAux));
                 } else {
-                    const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(rkp, o, 32 * si * KPB, 0);
+                    const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(rkp, o, 32 * si * KPB, kKvAux);
                     st.kp[tile] = u32x4{t2[0], t2[1], 0u, 0u};
                 }
             }
@@ -250,32 +262,32 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 if constexpr (D == 256) {
-                    const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(rv, off_v + j * KRB, 4 * si * VBB, 0);
+                    const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(rv, off_v + j * KRB, 4 * si * VBB, kKvAux);
                     st.vc[j / 2][2 * (j % 2)] = t2[0];
                     st.vc[j / 2][2 * (j % 2) + 1] = t2[1];
                 } else {
-                    st.vc[j / 4][j % 4] = __builtin_amdgcn_raw_buffer_load_b32(rv, off_v + j * KRB, 4 * si * VBB, 0);
+                    st.vc[j / 4][j % 4] = __builtin_amdgcn_raw_buffer_load_b32(rv, off_v + j * KRB, 4 * si * VBB, kKvAux);
                 }
             }
             const __amdgpu_buffer_rsrc_t rvp =
                 __builtin_amdgcn_make_buffer_rsrc((void*)vpbase, 0, ok ? a.cap / 8 * VPB : 0, kBufWord3);
             st.vp[0] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rvp, off_vp, 4 * si * VPB, 0));
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rvp, off_vp, 4 * si * VPB, kKvAux));
             st.vp[1] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rvp, off_vp + 16, 4 * si * VPB, 0));
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rvp, off_vp + 16, 4 * si * VPB, kKvAux));
         } else {
 #pragma unroll
             for (int jj = 0; jj < VL; jj++)
                 st.vc[jj] = __builtin_bit_cast(
-                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, off_v + 256 * jj, 4 * si * VBB, 0));
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, off_v + 256 * jj, 4 * si * VBB, kKvAux));
         }
         if constexpr (AFF) {
             const __amdgpu_buffer_rsrc_t rvp =
                 __builtin_amdgcn_make_buffer_rsrc((void*)vpbase, 0, ok ? a.cap / 8 * VPB : 0, kBufWord3);
             st.vp[0] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rvp, off_vp, 4 * si * VPB, 0));
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rvp, off_vp, 4 * si * VPB, kKvAux));
             st.vp[1] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rvp, off_vp + 16, 4 * si * VPB, 0));
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rvp, off_vp + 16, 4 * si * VPB, kKvAux));
         }
     };
     auto load = [&](Stage& st, int s) {
@@ -315,8 +327,10 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
     half8 x;
     {
         const int rr = row_ok ? rho : 0;
-        const f16* qrow = T4 ? sm_qr + rr * D
-                             : a.q + ((int64_t)(h * a.G + rr % a.G) * a.Tq + rr / a.G) * D;
+        // rr / G and rr % G for rr < 16 from a float reciprocal (exact here:
+        // (rr + 0.5) / G is at least 0.5 / G from an integer)
+        const int rq = (int)(((float)rr + 0.5f) * a.inv_g), rg_ = rr - rq * a.G;
+        const f16* qrow = T4 ? sm_qr + rr * D : a.q + ((int64_t)(h * a.G + rg_) * a.Tq + rq) * D;
         const int m = wave % NM;
         int base;
         if constexpr (T4)
@@ -332,7 +346,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
     int s = c + a.ns * wave;
     Stage A, B;
     // The first sub-chunk's loads go out right behind Q (loads return in
-    // issue order, so the Q conversion below waits for Q only).
+    // issue order, so the Q conversion below waits for Q only: the Q barrier
+    // holds every wave of the workgroup until the last one's q is in).
     load(A, s);
     {
         // q' = f16(f16(scale) * q): one packed fp16 multiply rounds exactly
@@ -572,6 +587,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
     } else {
         for (; s < s_end; s += SS) {
             compute(A, s);
+            if (s + SS >= s_end) break;
             // keep the next sub-chunk's loads behind this one's math
             __builtin_amdgcn_sched_barrier(0);
             load(A, s + SS);
@@ -580,43 +596,69 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
     float lsum = l_run;
     lsum += __shfl_xor(lsum, 16);
     lsum += __shfl_xor(lsum, 32);
-    // ---- merge the NW waves. Each wave parks its accumulators in LDS in
-    // their MFMA layout (float4 of rows 4g..4g+3 at dim r16*DPL + mm; only
-    // the lane groups holding rows < R), and its (m, l). After one barrier
-    // every thread forms the factors f_w = e^(m_w - M) of its output row
-    // itself (the (m, l) reads are broadcasts: a row's D consecutive outputs
-    // belong to whole waves), sums out[row][d] = sum_w f_w O_w[row][d] and
-    // writes the partial.
-    // sm_o row stride: G4 * 16 float4 plus one, so the reads (16 consecutive
-    // dims = 16 values of mm) fall on distinct banks.
+    // ---- merge the NW waves into the workgroup's partial. The VALU work of
+    // a merge is what sits on the critical path after the last data (two
+    // waves a SIMD run it at once), so each step does as little as it can:
+    //  1. each wave parks its raw accumulators (lanes g < G4: rows 4g..4g+3
+    //     of dims r16*DPL .. +DPL-1, a float4 a dim), its P.V-bias sums
+    //     (rows 4g..4g+3, the dim group of column r16) and (m, l) of its
+    //     rows; barrier;
+    //  2. wave 0 forms each row's M = max m_w, L = sum e^(m_w - M) l_w and
+    //     the factors f_w = e^(m_w - M) (lane (g, r16): row r16, waves
+    //     g, g+4, ...), and writes (M, L) of the partial; barrier;
+    //  3. each thread sums f_w (acc_w + b_w) over the waves for one dim of
+    //     four rows and stores them (consecutive threads, consecutive dims).
     const int R = a.R;
-    const int G4 = (R + 3) >> 2;          // lane groups holding real rows
-    const int RS = G4 * 16 + 1;           // float4 per (wave, mm)
-    if (g == 0) sm_ml[wave][r16] = float2{m_run, lsum};
+    const int G4 = (R + 3) >> 2;  // lane groups holding real rows
+    float4v* const sm_acc = (float4v*)sm_o;                    // [NW][G4][16][DPL]
+    float4v* const sm_b = sm_acc + (int64_t)NW * G4 * 16 * DPL;  // [NW][G4][16]
+    float* const sm_f = (float*)(sm_b + NW * G4 * 16);         // [4 row groups][NW][4 rows]
+    if (g == 0) sm_ml[r16][wave] = float2{m_run, lsum};
     if (g < G4) {
-        float4v* dst = (float4v*)sm_o + (int64_t)wave * DPL * RS + g * 16 + r16;
+        // dim r16*DPL + mm at slot mm ^ (r16 % DPL) of the lane's DPL-slot run:
+        // the 16 lanes of a store land in 16 distinct bank groups, and step 3
+        // reads whole runs
+        float4v* dst = sm_acc + (((int64_t)wave * G4 + g) * 16 + r16) * DPL;
 #pragma unroll
-        for (int mm = 0; mm < DPL; mm++) dst[mm * RS] = acc_o[mm] + acc_b;
+        for (int mm = 0; mm < DPL; mm++) dst[mm ^ (r16 % DPL)] = acc_o[mm];
+        sm_b[(wave * G4 + g) * 16 + r16] = acc_b;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; w++) M = fmaxf(M, sm_ml[r16][w].x);
+        const float Ms = M == -INFINITY ? 0.0f : M;  // a row with no visible key
+        float L = 0.0f;
+        for (int w = g; w < NW; w += 4) {
+            const float2 ml = sm_ml[r16][w];
+            const float f = __builtin_amdgcn_exp2f((ml.x - Ms) * kLog2e);
+            sm_f[((r16 >> 2) * NW + w) * 4 + (r16 & 3)] = f;
+            L = __builtin_fmaf(f, ml.y, L);
+        }
+        L += __shfl_xor(L, 16);
+        L += __shfl_xor(L, 32);
+        if (g == 0 && r16 < R) part_ml[((int64_t)h * a.nc + c) * 16 + r16] = float2{M, L};
     }
     __syncthreads();
     const int64_t pbase = ((int64_t)h * a.nc + c) * 16;
-    for (int o = threadIdx.x; o < R * D; o += 64 * NW) {
-        const int row = o / D, d = o % D;
-        const int rg = row >> 2, ri = row & 3, rl = d / DPL, mm = d % DPL;
-        const float* src = (const float*)sm_o + ((int64_t)mm * RS + rg * 16 + rl) * 4 + ri;
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < NW; w++) M = fmaxf(M, sm_ml[w][row].x);
-        float acc = 0.0f, L = 0.0f;
-#pragma unroll
+    for (int t = threadIdx.x; t < G4 * D; t += 64 * NW) {
+        // t = (rg, d): dim d of rows 4rg..4rg+3
+        const int rg = t / D, d = t % D, rl = d / DPL, mm = d % DPL;
+        const float4v* src = sm_acc + ((int64_t)rg * 16 + rl) * DPL + (mm ^ (rl % DPL));
+        const float4v* bsrc = sm_b + rg * 16 + rl;
+        const float4v* fsrc = (const float4v*)sm_f + rg * NW;
+        float4v y = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
         for (int w = 0; w < NW; w++) {
-            const float2 ml = sm_ml[w][row];
-            const float f = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((ml.x - M) * kLog2e);
-            acc = __builtin_fmaf(f, src[(int64_t)w * DPL * RS * 4], acc);
-            L = __builtin_fmaf(f, ml.y, L);
+            const float4v x = src[(int64_t)w * G4 * 16 * DPL] + bsrc[w * G4 * 16];
+            const float4v f = fsrc[w];
+#pragma unroll
+            for (int i = 0; i < 4; i++) y[i] = __builtin_fmaf(f[i], x[i], y[i]);
         }
-        a.part_o[(pbase + row) * D + d] = acc;
-        if (d == 0) a.part_ml[pbase + row] = float2{M, L};
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (4 * rg + i < R) part_o[(pbase + 4 * rg + i) * D + d] = y[i];
     }
 }
 
@@ -763,10 +805,10 @@ template <int BITS, int D, bool T4 = false, bool APP = false>
 __global__ __launch_bounds__((64 * decode_waves<BITS, D>()), 1) void attend_decode_kernel(
     DecodeArgs a) {
     constexpr int NW = decode_waves<BITS, D>();
-    __shared__ float2 sm_ml[NW][16];
+    __shared__ __attribute__((aligned(16))) float2 sm_ml[16][NW];
     __shared__ half8 sm_q[D / 32][64];
     __shared__ float2 sm_t4[T4 ? 256 : 1];  // Turbo4 centroid-pair table
-    // dynamic LDS: the wave merge's sm_o [NW][DPL][R] float4
+    // dynamic LDS: the wave merge's accumulators, bias sums and factors
     extern __shared__ __attribute__((aligned(16))) float sm_o[];
     // The exact 2-op dequant runs first without waiting for the cache's fast
     // flag (a memory round trip ahead of every load). In the rare launch whose
@@ -914,6 +956,7 @@ static int launch_decode_partials(KVCache& cc, const f16* q, int G, int Tq, int 
     a.nc = nc;
     a.ns = ns;
     a.scale_h = (float)(f16)scale;
+    a.inv_g = 1.0f / (float)G;
     a.code_off2 = cc.code_offset2();
     a.app_L = app_L;
     a.app_causal = app_causal ? 1 : 0;
@@ -923,7 +966,9 @@ static int launch_decode_partials(KVCache& cc, const f16* q, int G, int Tq, int 
     a.app.v = v_new;
     a.app.row_stride = D;
     a.app.head_stride = (int64_t)app_L * D;
-    size_t shmem = (size_t)NW * (D / 16) * (((a.R + 3) / 4) * 16 + 1) * 16;  // wave-merge sm_o
+    // wave merge: accumulators NW x G4 x D float4, bias sums NW x G4 x 16
+    // float4, factors 4 x NW float4
+    size_t shmem = (size_t)NW * ((a.R + 3) / 4) * (D + 16) * 16 + 4 * NW * 16;
     // Dynamic LDS above 64 KB must be allowed per kernel and device.
     if (app) {
         shmem = std::max(shmem, decode_append_lds<D>(app_L));
