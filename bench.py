@@ -75,7 +75,7 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--reps", type=int, default=50, help="timed graph replays (at least 50)")
-    ap.add_argument("--pmc-workload", choices=["c2", "c3", "c4", "c5"],
+    ap.add_argument("--pmc-workload", choices=["c2", "c3", "c4", "c5", "gemm"],
                     help="a 256 MiB copy then the configuration's attention calls, for counter runs")
     ap.add_argument("--summarize-counters", nargs=2, metavar=("CFG", "DIR"))
     ap.add_argument("--summarize-trace", metavar="DB")
@@ -729,7 +729,9 @@ PMC_CONFIGS = {
     "c3": "config 3: 4 qw_kv_attention calls, 2048 causal rows over 18432 keys, 8-bit, 4 caches",
     "c4": "config 4: 16 qw_kv_attention calls, 16 causal rows over 65552 keys, 4-bit, 16 caches",
     "c5": "config 5: 16 qw_dlsa_sparse_attention calls, 4612-entry list, fp16 KV, 16 layers",
+    "gemm": "the MFMA ceiling: 3 torch.matmul calls, fp16 8192 x 8192 x 8192 (hipBLASLt)",
 }
+GEMM_N = 8192
 
 
 def pmc_algorithmic(cfg: str):
@@ -743,6 +745,8 @@ def pmc_algorithmic(cfg: str):
     if cfg == "c4":
         T, L = 65552, 16
         return T * HKV * kv_bytes_per_token_head(4) + 2 * HQ * L * D * 2, attn_flops(L, T, True)
+    if cfg == "gemm":
+        return 3 * GEMM_N * GEMM_N * 2, 2 * GEMM_N ** 3
     W = 4612
     return W * HKV * 2 * D * 2 + HQ * D * 2 * 2 + W * 4, 4 * D * HQ * W
 
@@ -763,6 +767,14 @@ def pmc_workload(cfg: str) -> int:
     dst.copy_(src)  # a device-to-device memcpy: HIP's copyBuffer kernel
     torch.cuda.synchronize()
     del src, dst
+    if cfg == "gemm":
+        a = torch.randn((GEMM_N, GEMM_N), device="cuda:0", dtype=torch.float16)
+        b = torch.randn((GEMM_N, GEMM_N), device="cuda:0", dtype=torch.float16)
+        for _ in range(PMC_CALLS["gemm"]):
+            torch.matmul(a, b)
+        torch.cuda.synchronize()
+        print("pmc workload gemm done", flush=True)
+        return 0
     if cfg == "c5":
         bench_dlsa(torch, qw_amd, 0)
         print("pmc workload c5 done", flush=True)
@@ -782,7 +794,7 @@ def pmc_workload(cfg: str) -> int:
     return 0
 
 
-PMC_CALLS = {"c2": LAYERS, "c3": 4, "c4": LAYERS, "c5": LAYERS}
+PMC_CALLS = {"c2": LAYERS, "c3": 4, "c4": LAYERS, "c5": LAYERS, "gemm": 3}
 # the kernels a call of the configuration launches (set-up appends excluded)
 PMC_KERNELS = ("attend_decode_kernel", "attend_block_kernel", "decode_merge_kernel",
                "merge_rows_kernel", "t4_merge_rotate_kernel", "dlsa_kernel", "dlsa_merge_kernel")
@@ -844,7 +856,9 @@ def summarize_counters(cfg: str, root: str, out: str) -> int:
     w_scale = (COPY_BYTES / 1024.0) / cw
     alg_bytes, alg_flops = pmc_algorithmic(cfg)
     calls = PMC_CALLS[cfg]
-    ours = [n for n in per if any(k in n for k in PMC_KERNELS)]
+    ours = [n for n in per if any(k in n for k in PMC_KERNELS)] if cfg != "gemm" else \
+        [n for n in per if "copyBuffer" not in n and "elementwise" not in n.lower()
+         and "distribution" not in n.lower()]
     lines = [f"# Counters of {PMC_CONFIGS[cfg]} (rocprofv3 --pmc)", "", "commands:"]
     for ps, counters in PMC_PASSES.items():
         lines.append(f"  rocprofv3 --pmc {counters} -d gpurun_out/pmc_{cfg}/{ps} -o run -- "
@@ -975,6 +989,8 @@ def main() -> int:
         return 2
     torch.cuda.set_device(0)
     steps, reps = max(1, args.steps), max(50, args.reps)
+    log("bench: measured ceilings (copy, config-2-sized read floor, fp16 GEMM)")
+    ceil = bench_ceilings(torch, qw_amd, reps)
     log(f"bench: config 2 decode, {steps} steps a replay, {reps} replays, warmup {args.warmup}")
     dec = bench_decode(torch, qw_amd, steps, args.warmup, reps)
     us_layer = dec["layer_ms"] * 1e3
@@ -1006,9 +1022,15 @@ def main() -> int:
         "us_per_layer_eager": round(dec["eager_layer_ms"] * 1e3, 3),
         "us_attention": round(dec["attn_ms"] * 1e3, 3),
         "us_attention_stats": _round_stats(dec["attn"]),
-        "tokens_per_s": round(1.0 / (dec["layer_ms"] * 1e-3), 1),
+        "layer_calls_per_s": round(1.0 / (dec["layer_ms"] * 1e-3), 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "peak_measured": ceil["read_2GiB"]["GB_s"],
+                     "frac_measured": round(achieved / ceil["read_2GiB"]["GB_s"], 4),
+                     "read_floor_us": ceil["read_c2_size"]["us"],
+                     "peak_measured_note": "peak_measured: a plain read kernel over 2 GiB on this "
+                                           "box; read_floor_us: the same kernel reading 16 rotated "
+                                           "config-2-sized buffers, timed like the headline",
                      "traffic": c2c.get("traffic_bytes_per_call"),
                      "kernel": "qw_kv_attention: attend_decode_kernel + decode_merge_kernel, "
                                "graph-replayed over 16 caches",
@@ -1016,7 +1038,7 @@ def main() -> int:
                      "dram_read_bytes": c2c.get("dram_read_bytes_per_call")},
     }
     if not args.no_extra:
-        extra = {}
+        extra = {"ceilings": ceil}
         log("bench: config 3 prefill chunk")
         pf = bench_block(torch, qw_amd, reps, 8, 16384, 2048, 4)
         tf = pf["flops"] / (pf["attn_ms"] * 1e-3) / 1e12
@@ -1026,8 +1048,9 @@ def main() -> int:
             "us_attention": round(pf["attn_ms"] * 1e3, 1),
             "us_attention_stats": _round_stats(pf["attn"], 1e3, 1),
             "TFLOP_s": round(tf, 1), "frac_mfma": round(tf / MFMA_PEAK_TFLOPS, 4),
+            "frac_mfma_measured": round(tf / ceil["gemm_fp16_8192"]["TFLOP_s"], 4),
             "TFLOP_s_layer": round(pf["flops"] / (pf["layer_ms"] * 1e-3) / 1e12, 1),
-            "tokens_per_s": round(2048 / (pf["layer_ms"] * 1e-3), 1),
+            "chunk_rows_per_s_one_layer": round(2048 / (pf["layer_ms"] * 1e-3), 1),
             "flops": pf["flops"], "keys": pf["T"], "rows": 2048, "kv_bits": 8,
             "layers_rotated": 4, "counters": c3c}
         log("bench: config 4 verify block")

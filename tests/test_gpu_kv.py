@@ -256,6 +256,59 @@ def test_block_attention_vs_oracle(oracle_lib, bits, T_prefix, L, causal, D, hq,
     assert_as_exact_as_reference(out, ref, f64, what)
 
 
+# Every row of the paired-half-tile image launches, at full size: config 3
+# (2048 rows, 8-bit, 16384 cached keys), the 2024-row chunk (an odd half-tile
+# count, a lone middle half tile, a partial last one) and the 1500-row chunk
+# at head_dim 128 with 8 KV heads. A half tile is 96 rows a KV head, i.e.
+# 96 / G query rows; the launch pairs half tile j with half tile n - 1 - j.
+#  - The first and last query row of every half tile (both members of every
+#    pair) are checked against the oracle.
+#  - All rows x heads are checked against the decode route row by row: the
+#    cache is trimmed back to each row's last visible key and attended with
+#    that row alone (bottom-right causal = all cached keys). The decode route
+#    is a separate kernel whose config-2-size oracle test is green.
+@pytest.mark.parametrize("bits,T_prefix,L,D,hq,hkv", [
+    (8, 16384, 2048, 256, 24, 4),   # config 3
+    (8, 1000, 2024, 256, 24, 4),    # 127 half tiles
+    (4, 200, 1500, 128, 32, 8),     # head_dim 128, 63 half tiles
+])
+def test_paired_half_tiles_every_row(oracle_lib, bits, T_prefix, L, D, hq, hkv):
+    import qw_amd
+
+    G = hq // hkv
+    per_half = 96 // G
+    n_half = -(-L // per_half)
+    sel = np.array(sorted({x for j in range(n_half)
+                           for x in (j * per_half, min(L, (j + 1) * per_half) - 1)}))
+    r = rng(7000 + bits + T_prefix + L + D)
+    k, v = _kv(r, hkv, T_prefix + L, D)
+    q = r.standard_normal((hq, L, D)).astype(np.float16)
+    cache = qw_amd.KVCache(_mode(bits), hkv, D, capacity=T_prefix + L)
+    cache.update(_gpu(k[:, :T_prefix])[None], _gpu(v[:, :T_prefix])[None])
+    qg = _gpu(q)[None]
+    out = _np(cache.update_and_causal_attention(qg, _gpu(k[:, T_prefix:])[None],
+                                                _gpu(v[:, T_prefix:])[None], 1.0 / 16))[0]
+    assert np.isfinite(out).all()
+    what = f"paired half tiles bits={bits} D={D} T={T_prefix}+{L}"
+
+    orc = oracle_lib.AffineCacheOracle(hkv, D, T_prefix + L, bits)
+    orc.update(k[:, :T_prefix], v[:, :T_prefix])
+    ref = orc.update_and_attention(q, k[:, T_prefix:], v[:, T_prefix:], 1.0 / 16, True, rows=sel)
+    kd, vd = orc.fetch()
+    pos = np.ascontiguousarray(oracle_lib.causal_positions(L, T_prefix + L)[sel])
+    f64 = oracle_lib.sdpa_f64(np.ascontiguousarray(q[:, sel]), kd, vd, 1.0 / 16, q_pos=pos)
+    assert_close(out[:, sel], ref, f"{what}: {len(sel)} half-tile edge rows vs oracle")
+    assert_as_exact_as_reference(out[:, sel], ref, f64, what)
+
+    rows = []
+    for i in reversed(range(L)):
+        rows.append(cache.attention(qg[:, :, i:i + 1], 1.0 / 16)[0])
+        cache.trim(1)
+    dec = _np(torch.cat(rows[::-1], dim=1))
+    assert dec.shape == out.shape
+    assert_close(out, dec, f"{what}: all {L} rows x {hq} heads vs the decode route")
+
+
 def test_block_causal_rows_are_prefix_independent(oracle_lib):
     """Bottom-right causal: query row r of an L-row block sees exactly the keys
     a single-row call at the same position sees, so appending the block in one
