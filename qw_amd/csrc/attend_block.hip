@@ -1027,7 +1027,9 @@ std::map<std::pair<int, hipStream_t>, GrowBuffer> g_img_ws;
 // transient workspaces (stream-ordered reuse; capture-safe growth).
 int image_workspace(int device, hipStream_t stream, size_t need, void** out) {
     std::lock_guard<std::mutex> lock(g_img_mu);
-    return g_img_ws[{device, stream}].get(need, stream, out);
+    GrowBuffer& b = g_img_ws[{device, stream}];
+    b.stream_owned = true;  // only calls on `stream` use it
+    return b.get(need, stream, out);
 }
 }  // namespace
 
@@ -1272,11 +1274,14 @@ int launch_block_append_attention(KVCache& cc, const f16* q, int G, int L, const
                                                            out, stream);
 }
 
+bool block_append_fits_t4(const KVCache& cc, int G, int L) {
+    return cc.turbo4() && G * L <= 16 * kBlockWaves && cc.offset >= 256;
+}
+
 int launch_block_append_attention_t4(KVCache& cc, const f16* q, int G, int L, const f16* k_new,
                                      const f16* v_new, float scale, bool causal, bool fused,
                                      const float* tab, f16* out, hipStream_t stream) {
-    QW_REQUIRE(cc.turbo4() && G * L <= 16 * kBlockWaves && cc.offset >= 256 &&
-                   cc.offset + L <= cc.cap,
+    QW_REQUIRE(block_append_fits_t4(cc, G, L) && cc.offset + L <= cc.cap,
                QW_ERR_INVALID_ARGUMENT, "block attention: Turbo4 block outside the fused-append shapes");
     if (cc.D == 256)
         return fused ? launch_block_append_bits<4, 256, 2>(cc, q, G, L, k_new, v_new, scale, causal,

@@ -666,7 +666,9 @@ static std::map<std::pair<int, hipStream_t>, GrowBuffer> g_ws;
 
 static int dlsa_workspace(int device, hipStream_t stream, size_t need, void** out) {
     std::lock_guard<std::mutex> lock(g_ws_mu);
-    return g_ws[{device, stream}].get(need, stream, out);
+    GrowBuffer& b = g_ws[{device, stream}];
+    b.stream_owned = true;  // only calls on `stream` use it
+    return b.get(need, stream, out);
 }
 
 // Launch policy (the reference's auto_parts, mlx_cxx_dlsa_attention.cpp:379-400,

@@ -40,7 +40,10 @@ int GrowBuffer::get(size_t need, hipStream_t stream, void** out) {
             if (captured) {
                 retired.push_back(ptr);  // a graph may still read it
             } else {
-                QW_HIP_CHECK(hipDeviceSynchronize());
+                if (stream_owned)
+                    QW_HIP_CHECK(hipStreamSynchronize(stream));
+                else
+                    QW_HIP_CHECK(hipDeviceSynchronize());
                 (void)hipFree(ptr);
             }
             ptr = nullptr;

@@ -200,6 +200,9 @@ bool block_append_fits(const KVCache& c, int G, int n_rows);
 // Query rows a KV head from which block attention on an affine or Int8
 // (turbo4: a Turbo4) cache expands the key tiles once into LDS images.
 int block_image_min_rows(bool turbo4);
+// The shapes the Turbo4 form below takes (one query tile, at least 256 cached
+// rows; the caller reserves the capacity).
+bool block_append_fits_t4(const KVCache& c, int G, int n_rows);
 // The same for a Turbo4 cache (one query tile, at least 256 cached rows,
 // capacity reserved): fused as launch_block_attention_t4's fused pass (out:
 // the rows rotated back), else its fp16 arithmetic (out: rotated-basis rows).

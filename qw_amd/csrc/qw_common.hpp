@@ -146,14 +146,19 @@ const char* last_error();
 // A device buffer for split-K partials that grows on demand and never frees
 // memory a captured HIP graph may still reference: a buffer handed to work
 // recorded into a graph is retired, not freed, when it grows, and released
-// with the owner. A buffer no graph holds is freed after a device
-// synchronization. It cannot grow while its stream is being captured (HIP
-// allows no allocation there): such a call returns QW_ERR_STATE without
-// touching the capture; one call of that shape before capturing sizes it.
+// with the owner. A buffer no graph holds is freed after a synchronization:
+// of the one stream that uses it (stream_owned: the per-(device, stream)
+// workspaces), else of the device. It cannot grow while its stream is being
+// captured (HIP allows no allocation there): such a call returns
+// QW_ERR_STATE without touching the capture; one call of that shape before
+// capturing sizes it. Growth allocates and frees device memory, which HIP
+// forbids while any stream of the process is under a global-mode capture:
+// size the buffers (one call of each shape) before such a capture begins.
 struct GrowBuffer {
     void* ptr = nullptr;
     size_t bytes = 0;
     bool captured = false;
+    bool stream_owned = false;
     std::vector<void*> retired;
     int get(size_t need, hipStream_t stream, void** out);
     void release();

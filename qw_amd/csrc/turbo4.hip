@@ -609,7 +609,9 @@ std::map<std::pair<int, hipStream_t>, GrowBuffer> g_t4_ws;
 
 int t4_workspace(int device, hipStream_t stream, size_t need, void** out) {
     std::lock_guard<std::mutex> lock(g_t4_mu);
-    return g_t4_ws[{device, stream}].get(need, stream, out);
+    GrowBuffer& b = g_t4_ws[{device, stream}];
+    b.stream_owned = true;  // only calls on `stream` use it
+    return b.get(need, stream, out);
 }
 
 }  // namespace
@@ -835,7 +837,7 @@ int turbo4_update_and_attention(KVCache& c, const void* q, int n_q_heads, int n_
     // kernel's one-tile blocks append in the block launch, the decode route
     // in the decode launch's append unit
     const bool fused = causal && n_rows <= 5 && T > 2048 && G * n_rows <= kT4vRows;
-    const bool block = QW_T4_BLOCK && c.offset >= 256 && (fused || (G * n_rows > 16 && G * n_rows <= 16 * 8));
+    const bool block = QW_T4_BLOCK && block_append_fits_t4(c, G, n_rows) && (fused || G * n_rows > 16);
     const bool decode = !fused && QW_T4_FUSED_DECODE && G * n_rows <= 16 && c.offset >= 1;
     if (!(QW_T4_APPEND && (block || decode))) {
         int rc = c.update(k_new, v_new, n_rows, stream);

@@ -203,3 +203,66 @@ def test_empty_cache_is_an_error():
         c.dlsa_attention(q, lists, lengths, 1 / 16)
     assert ei.value.status == 1 and "empty" in str(ei.value)
     c.close()
+
+
+# The two-rows-a-workgroup D-LSA kernel (RP = 2) on cache sources: one-pass
+# calls (rows x kv_heads >= 192), 2G <= 16 and rows x kv_heads >= 384, at
+# head_dim 128 (the cache sources' pair form). 203 rows over 2 KV heads
+# (406 units, an odd row count so the last workgroup holds one row),
+# unequal lengths with -1 padding and past-the-end entries. Both list kinds:
+# whole aligned runs (the aligned block gathers, the pair's shared tiles)
+# and random entries (the unaligned gathers). One affine case holds scales
+# outside the 2-op dequant's exact range, so the separately rounded second
+# pass runs under the pair form too.
+@pytest.mark.parametrize("mode,extreme", [("fp16", False), ("affine4", False),
+                                          ("affine8", False), ("int8", False),
+                                          ("affine4", True)])
+@pytest.mark.parametrize("lists_kind", ["runs", "random"])
+def test_row_pairs_over_cache_sources_vs_oracle(oracle_lib, mode, extreme, lists_kind):
+    import qw_amd
+
+    H, G, D, T, L, W = 2, 6, 128, 3000, 203, 400
+    r = rng(8100 + 10 * ["fp16", "affine4", "affine8", "int8"].index(mode) + extreme
+            + 2 * (lists_kind == "runs"))
+    jit = r.uniform(0.5, 2.0, (H, 1, 1))
+    k = (r.standard_normal((H, T, D)) * jit).astype(np.float32)
+    v = (r.standard_normal((H, T, D)) * jit).astype(np.float32)
+    if extreme:
+        k[:, 100:140, :64] *= 1e-3       # |scale| < 2^-10
+        k[:, 900:905, 64:] *= 300.0      # |scale| >= 64
+        v[:, 200:260, 64:] *= 1e-3
+    k, v = k.astype(np.float16), v.astype(np.float16)
+    q = r.standard_normal((H * G, L, D)).astype(np.float16)
+    lists = np.full((L, W), -1, np.int32)
+    lengths = r.integers(1, W + 1, L).astype(np.int32)
+    lengths[::7] = W
+    lengths[5] = 0
+    for row in range(L):
+        n = int(lengths[row])
+        if lists_kind == "runs":
+            # whole aligned 16-key runs, then a ragged tail; the two rows of a
+            # workgroup (2j, 2j + 1) draw from the same runs, so their tiles
+            # are shared (gathered and multiplied once) up to the shorter list
+            if row % 2 == 0:
+                blocks = np.sort(r.choice(np.arange(T // 16 - 1), W // 16, replace=False))
+            lst = np.concatenate([np.arange(b * 16, b * 16 + 16) for b in blocks[:n // 16]]
+                                 + [np.arange(T - (n % 16), T)])[:n]
+        else:
+            lst = r.choice(T, n, replace=False)
+        lists[row, :n] = lst
+    lists[3, 1] = T + 7      # past the cached rows: skipped
+    lists[8, 0] = T + 100
+    c = _cache(mode, k, v)
+    assert (lengths.size * H) >= 384
+    out = _np(c.dlsa_attention(_gpu(q), _gpu(lists), _gpu(lengths), D ** -0.5))[0]
+    if mode == "fp16":
+        kf, vf = k, v
+    else:
+        orc = (oracle_lib.Int8CacheOracle(H, D, T) if mode == "int8"
+               else oracle_lib.AffineCacheOracle(H, D, T, 4 if mode == "affine4" else 8))
+        orc.update(k, v)
+        kf, vf = orc.fetch()
+    ref = oracle_lib.dlsa_attention(q, kf, vf, lists, lengths, D ** -0.5)
+    assert_close(out, ref, f"row pairs {mode}{' extreme' if extreme else ''} {lists_kind}")
+    assert np.all(out[:, 5] == 0)  # the empty row
+    c.close()
