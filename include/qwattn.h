@@ -254,6 +254,29 @@ int qw_kv_update_and_dlsa_attention(qw_kv_cache* cache, const void* q, int n_q_h
                                     const int32_t* lists, const int32_t* lengths, int width,
                                     float scale, void* out, void* stream);
 
+/* Element types of the typed D-LSA read. */
+#define QW_DTYPE_F16 0
+#define QW_DTYPE_BF16 1
+#define QW_DTYPE_F32 2
+
+/* dlsa_attention::sparse_attention_with (dlsa_attention.rs:44) with the
+ * reference's full dtype and head-dim contract (mlx_cxx_dlsa_attention.cpp:
+ * 429-470): q in q_dtype, K and V alike in kv_dtype, each of QW_DTYPE_F16 /
+ * _BF16 / _F32; head_dim 32, 64, 128 or 256; n_q_heads / n_kv_heads <= 8;
+ * out [n_q_heads][n_rows][head_dim] in q_dtype. Strides, lists, lengths and
+ * the launch knobs as qw_dlsa_sparse_attention_with (waves above 8 run as 8
+ * at head_dim 256). Scores, softmax and P.V
+ * are fp32 (inputs widened exactly); only the output is rounded. fp16 q with
+ * fp16 K/V at head_dim >= 64 is the fp16 read itself (the same result as
+ * qw_dlsa_sparse_attention_with, bit for bit). */
+int qw_dlsa_sparse_attention_typed(const void* q, int q_dtype, const void* k, const void* v,
+                                   int kv_dtype, int64_t k_head_stride, int64_t k_row_stride,
+                                   int64_t v_head_stride, int64_t v_row_stride,
+                                   const int32_t* lists, const int32_t* lengths, int n_rows,
+                                   int width, int n_q_heads, int n_kv_heads, int head_dim,
+                                   int n_keys, float scale, int parts, int waves, void* out,
+                                   void* stream);
+
 /* dlsa_attention::sparse_attention_with (dlsa_attention.rs:44): the same read
  * with explicit launch knobs; 0 = automatic. parts: split-K partitions of
  * each list (1 = one pass, at most 128); waves: wavefronts per workgroup

@@ -204,6 +204,35 @@ def sdpa_f64(q, k, v, scale: float, q_pos=None, threads: int | None = None):
     return out
 
 
+def dlsa_attention_f64(q, k, v, lists, lengths, scale: float):
+    """The K2 contract in fp64 for inputs of any float dtype (numpy; the
+    reference's own host check, dlsa_attention.rs:140-170): for row r and
+    head h, the valid entries p of lists[r, :lengths[r]] (0 <= p < T) give
+    s_p = scale * q[h, r] . k[h / G, p] and out = sum_p softmax(s)_p v[h / G, p];
+    a row without a valid entry is zeros. q [Hq,L,D]; k, v [Hkv,T,D];
+    returns fp64 [Hq,L,D]."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    lists = np.asarray(lists, np.int64)
+    lengths = np.asarray(lengths, np.int64)
+    hq, L, D = q.shape
+    hkv, T, _ = k.shape
+    G = hq // hkv
+    out = np.zeros((hq, L, D))
+    for r in range(L):
+        lst = lists[r, :max(0, min(int(lengths[r]), lists.shape[1]))]
+        lst = lst[(lst >= 0) & (lst < T)]
+        if lst.size == 0:
+            continue
+        for h in range(hq):
+            kh = k[h // G, lst]
+            s = (kh @ q[h, r]) * float(scale)
+            w = np.exp(s - s.max())
+            out[h, r] = (w @ v[h // G, lst]) / w.sum()
+    return out
+
+
 def dlsa_attention(q, k, v, lists, lengths, scale: float, threads: int | None = None):
     """D-LSA gathered read (K2 contract). q [Hq,L,D] f16; k/v [Hkv,T,D] f16
     (any element strides with a unit last stride); lists [L,W] i32;

@@ -84,6 +84,8 @@ _SIGNATURES = {
                                            _i, _i, _i, _i, _f, _i, _i, _p, _p]),
     "qw_dlsa_sparse_attention_noalloc": (_i, [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _i, _i,
                                               _i, _i, _i, _i, _f, _i, _i, _p, _p]),
+    "qw_dlsa_sparse_attention_typed": (_i, [_p, _i, _p, _p, _i, _i64, _i64, _i64, _i64, _p, _p, _i,
+                                            _i, _i, _i, _i, _i, _f, _i, _i, _p, _p]),
 }
 
 
@@ -455,6 +457,54 @@ def sparse_attention_with(q, k, v, lists, lengths, scale: float, parts: int = 0,
 def sparse_attention(q, k, v, lists, lengths, scale: float):
     """D-LSA gathered read with the automatic launch policy (dlsa_attention.rs:31)."""
     return sparse_attention_with(q, k, v, lists, lengths, scale, 0, 0)
+
+
+def _dtype_code(t, name: str) -> int:
+    torch = _torch()
+    codes = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+    if t.dtype not in codes:
+        raise QwError(1, f"{name}: f16/bf16/f32 expected, got {t.dtype}")
+    return codes[t.dtype]
+
+
+def sparse_attention_typed(q, k, v, lists, lengths, scale: float, parts: int = 0,
+                           waves: int = 0):
+    """The D-LSA read over the reference's whole dtype and head-dim contract
+    (mlx_cxx_dlsa_attention.cpp:429-470): q f16/bf16/f32, K and V alike in one
+    of the three, head_dim 32..256, at most 8 query heads a KV head; the output
+    has q's dtype (dlsa_attention.rs:5-9). fp32 arithmetic throughout."""
+    torch = _torch()
+
+    def as3(t, name, any_stride=False):
+        if t.dim() == 4:
+            if t.shape[0] != 1:
+                raise QwError(1, f"{name}: batch must be 1")
+            t = t[0]
+        if t.dim() != 3 or not t.is_cuda:
+            raise QwError(1, f"{name}: device tensor [1, H, L, D] expected")
+        return t if (any_stride and t.stride(2) == 1) else t.contiguous()
+
+    qq = as3(q, "q")
+    kk, vv = as3(k, "k", True), as3(v, "v", True)
+    qd, kd = _dtype_code(qq, "q"), _dtype_code(kk, "k")
+    if vv.dtype != kk.dtype:
+        raise QwError(1, "sparse_attention: k and v must share a dtype")
+    if kk.shape != vv.shape or kk.shape[2] != qq.shape[2]:
+        raise QwError(1, "sparse_attention: k/v shapes disagree with q")
+    if lists.dim() != 2 or lists.dtype != torch.int32 or lengths.dim() != 1 or \
+            lengths.dtype != torch.int32 or lists.shape[0] != qq.shape[1] or \
+            lengths.shape[0] != qq.shape[1]:
+        raise QwError(1, "sparse_attention: lists [L,W] i32 and lengths [L] i32 expected")
+    lists = lists.contiguous()
+    lengths = lengths.contiguous()
+    out = torch.empty_like(qq)
+    hq, L, D = qq.shape
+    hkv, T, _ = kk.shape
+    _check(lib().qw_dlsa_sparse_attention_typed(
+        qq.data_ptr(), qd, kk.data_ptr(), vv.data_ptr(), kd, kk.stride(0), kk.stride(1),
+        vv.stride(0), vv.stride(1), lists.data_ptr(), lengths.data_ptr(), L, lists.shape[1], hq,
+        hkv, D, T, float(scale), parts, waves, out.data_ptr(), _stream(qq.device)))
+    return out.unsqueeze(0)
 
 
 # ------------------------------------------------------------ D-LSA K1 select

@@ -9,20 +9,6 @@ struct qw_kv_cache {
     qw::KVCache impl;
 };
 
-namespace qw {
-int dlsa_sparse_attention(const void* q, const void* k, const void* v, int64_t k_head_stride,
-                          int64_t k_row_stride, int64_t v_head_stride, int64_t v_row_stride,
-                          const int32_t* lists, const int32_t* lengths, int n_rows, int width,
-                          int n_q_heads, int n_kv_heads, int head_dim, int n_keys, float scale,
-                          int parts, int waves, void* out, hipStream_t stream);
-int dlsa_sparse_attention_noalloc(const void* q, const void* k, const void* v,
-                                  int64_t k_head_stride, int64_t k_row_stride,
-                                  int64_t v_head_stride, int64_t v_row_stride,
-                                  const int32_t* lists, const int32_t* lengths, int n_rows,
-                                  int width, int n_q_heads, int n_kv_heads, int head_dim,
-                                  int n_keys, float scale, int parts, int waves, void* out,
-                                  hipStream_t stream);
-}
 
 #define QW_HANDLE(c)                                                          \
     do {                                                                      \
@@ -221,6 +207,20 @@ int qw_dlsa_sparse_attention(const void* q, const void* k, const void* v, int64_
                                          v_row_stride, lists, lengths, n_rows, width, n_q_heads,
                                          n_kv_heads, head_dim, n_keys, scale, 0, 0, out,
                                          (hipStream_t)stream));
+}
+
+int qw_dlsa_sparse_attention_typed(const void* q, int q_dtype, const void* k, const void* v,
+                                   int kv_dtype, int64_t k_head_stride, int64_t k_row_stride,
+                                   int64_t v_head_stride, int64_t v_row_stride,
+                                   const int32_t* lists, const int32_t* lengths, int n_rows,
+                                   int width, int n_q_heads, int n_kv_heads, int head_dim,
+                                   int n_keys, float scale, int parts, int waves, void* out,
+                                   void* stream) {
+    QW_GUARDED(qw::dlsa_sparse_attention_typed(q, q_dtype, k, v, kv_dtype, k_head_stride,
+                                               k_row_stride, v_head_stride, v_row_stride, lists,
+                                               lengths, n_rows, width, n_q_heads, n_kv_heads,
+                                               head_dim, n_keys, scale, parts, waves, out,
+                                               (hipStream_t)stream));
 }
 
 int qw_dlsa_sparse_attention_with(const void* q, const void* k, const void* v,

@@ -203,6 +203,27 @@ int block_image_min_rows(bool turbo4);
 // The shapes the Turbo4 form below takes (one query tile, at least 256 cached
 // rows; the caller reserves the capacity).
 bool block_append_fits_t4(const KVCache& c, int G, int n_rows);
+
+// The D-LSA reads (dlsa.hip, dlsa_typed.hip).
+int dlsa_sparse_attention(const void* q, const void* k, const void* v, int64_t k_head_stride,
+                          int64_t k_row_stride, int64_t v_head_stride, int64_t v_row_stride,
+                          const int32_t* lists, const int32_t* lengths, int n_rows, int width,
+                          int n_q_heads, int n_kv_heads, int head_dim, int n_keys, float scale,
+                          int parts, int waves, void* out, hipStream_t stream);
+int dlsa_sparse_attention_noalloc(const void* q, const void* k, const void* v,
+                                  int64_t k_head_stride, int64_t k_row_stride,
+                                  int64_t v_head_stride, int64_t v_row_stride,
+                                  const int32_t* lists, const int32_t* lengths, int n_rows,
+                                  int width, int n_q_heads, int n_kv_heads, int head_dim,
+                                  int n_keys, float scale, int parts, int waves, void* out,
+                                  hipStream_t stream);
+int dlsa_sparse_attention_typed(const void* q, int q_dtype, const void* k, const void* v,
+                                int kv_dtype, int64_t k_head_stride, int64_t k_row_stride,
+                                int64_t v_head_stride, int64_t v_row_stride,
+                                const int32_t* lists, const int32_t* lengths, int n_rows,
+                                int width, int n_q_heads, int n_kv_heads, int head_dim,
+                                int n_keys, float scale, int parts, int waves, void* out,
+                                hipStream_t stream);
 // The same for a Turbo4 cache (one query tile, at least 256 cached rows,
 // capacity reserved): fused as launch_block_attention_t4's fused pass (out:
 // the rows rotated back), else its fp16 arithmetic (out: rotated-basis rows).

@@ -159,3 +159,66 @@ def test_dlsa_skips_and_empty_rows(oracle_lib):
     b = oracle_lib.dlsa_attention(q, k, v, dirty, lengths, 0.125)
     assert np.array_equal(a, b)
     assert np.all(a[:, 2] == 0)
+
+
+# dlsa_attention_f64: the typed read's checker (any input dtype, fp64). Pinned
+# by the reference's golden outputs, by the fp32 C restatement on the same
+# inputs, by the dense-causal identity and by hand-computed answers.
+@pytest.mark.parametrize("m", ["real", "random"])
+def test_dlsa_f64_qwen_layer_golden(oracle_lib, m):
+    d = _golden("qwen_layer")
+    q = d["q_rows"].transpose(1, 0, 2)
+    k = d["k"].transpose(1, 0, 2)
+    v = d["v"].transpose(1, 0, 2)
+    out = oracle_lib.dlsa_attention_f64(q, k, v, d[f"{m}.selected"], d[f"{m}.selected_lengths"],
+                                        256 ** -0.5)
+    assert np.abs(out - d[f"{m}.attention_out"].transpose(1, 0, 2)).max() < 1e-5
+
+
+def test_dlsa_f64_matches_the_fp32_restatement(oracle_lib):
+    r = rng(13)
+    q = r.standard_normal((8, 5, 128)).astype(np.float16)
+    k = r.standard_normal((2, 300, 128)).astype(np.float16)
+    v = r.standard_normal((2, 300, 128)).astype(np.float16)
+    lists = np.full((5, 120), -1, np.int32)
+    lengths = np.array([120, 1, 60, 0, 99], np.int32)
+    for row in range(5):
+        lists[row, :lengths[row]] = r.choice(300, lengths[row], replace=False)
+    lists[2, 3] = 300  # past the end: skipped
+    a = oracle_lib.dlsa_attention_f64(q, k, v, lists, lengths, 128 ** -0.5)
+    b = oracle_lib.dlsa_attention(q, k, v, lists, lengths, 128 ** -0.5)
+    assert np.abs(a - b).max() < 1e-5
+    assert np.all(a[:, 3] == 0)
+
+
+def test_dlsa_f64_known_answers(oracle_lib):
+    # one entry: that key's value row exactly; two keys with equal scores:
+    # their mean; a key scored log(3) above another: weights 3/4, 1/4
+    k = np.zeros((1, 4, 32))
+    v = np.arange(4 * 32, dtype=np.float64).reshape(1, 4, 32)
+    k[0, 2, 0] = np.log(3.0)
+    q = np.zeros((2, 1, 32))
+    q[:, 0, 0] = 1.0
+    lists = np.array([[1, 3, -1]], np.int32)
+    one = oracle_lib.dlsa_attention_f64(q, k, v, lists, np.array([1], np.int32), 1.0)
+    assert np.array_equal(one[0, 0], v[0, 1])
+    two = oracle_lib.dlsa_attention_f64(q, k, v, lists, np.array([2], np.int32), 1.0)
+    assert np.allclose(two[1, 0], (v[0, 1] + v[0, 3]) / 2, rtol=0, atol=1e-12)
+    w = oracle_lib.dlsa_attention_f64(q, k, v, np.array([[2, 0]], np.int32),
+                                      np.array([2], np.int32), 1.0)
+    assert np.allclose(w[0, 0], 0.75 * v[0, 2] + 0.25 * v[0, 0], rtol=0, atol=1e-12)
+
+
+def test_dlsa_f64_full_list_equals_dense_causal(oracle_lib):
+    r = rng(14)
+    T, D = 50, 32
+    q = r.standard_normal((6, T, D)).astype(np.float32)
+    k = r.standard_normal((2, T, D)).astype(np.float32)
+    v = r.standard_normal((2, T, D)).astype(np.float32)
+    lists = np.full((T, T), -1, np.int32)
+    for p in range(T):
+        lists[p, :p + 1] = r.permutation(p + 1)
+    out = oracle_lib.dlsa_attention_f64(q, k, v, lists, np.arange(1, T + 1, dtype=np.int32),
+                                        D ** -0.5)
+    pos = np.arange(T)
+    assert np.abs(out - _np_attention(q, k, v, D ** -0.5, pos)).max() < 1e-12
