@@ -864,7 +864,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t base = (int64_t)h * nc * rstride + row;
     // One memory round: every (m, l) and O value this lane needs is loaded
-    // first; the max is then exchanged through LDS.
+    // first.
     float v[PER];
     float2 ml[PER];
 #pragma unroll
@@ -878,14 +878,11 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
             v[i] = 0.0f;
         }
     }
+    // each wave reduces its partials against its own maximum; the four
+    // (m, l, O) then meet in LDS behind one barrier
     float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < PER; i++) m = fmaxf(m, ml[i].x);
-    __shared__ float sm_m[4];
-    __shared__ float sm[2][4][64];
-    if (lane == 0) sm_m[wave] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(sm_m[0], sm_m[1]), fmaxf(sm_m[2], sm_m[3]));
     float o = 0.0f, l = 0.0f;
 #pragma unroll
     for (int i = 0; i < PER; i++) {
@@ -894,12 +891,22 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(const float* __restri
         o = __builtin_fmaf(w, v[i], o);
         l = __builtin_fmaf(w, ml[i].y, l);
     }
-    sm[0][wave][lane] = o;
-    sm[1][wave][lane] = l;
+    __shared__ float2 sm_ml[4];
+    __shared__ float sm_o[4][64];
+    if (lane == 0) sm_ml[wave] = float2{m, l};
+    sm_o[wave][lane] = o;
     __syncthreads();
     if (wave == 0) {
-        const float O = (sm[0][0][lane] + sm[0][1][lane]) + (sm[0][2][lane] + sm[0][3][lane]);
-        const float L = (sm[1][0][lane] + sm[1][1][lane]) + (sm[1][2][lane] + sm[1][3][lane]);
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; w++) M = fmaxf(M, sm_ml[w].x);
+        float O = 0.0f, L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float f = sm_ml[w].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((sm_ml[w].x - M) * kLog2e);
+            O = __builtin_fmaf(f, sm_o[w][lane], O);
+            L = __builtin_fmaf(f, sm_ml[w].y, L);
+        }
         const int orow = row0 + row;  // row index r * G + head-in-group
         const int qh = h * G + orow % G, qr = orow / G;
         const float y = L > 0.0f ? O / L : 0.0f;
