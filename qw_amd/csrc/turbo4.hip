@@ -801,6 +801,16 @@ static int turbo4_verify(KVCache& c, const void* q, int n_q_heads, int n_rows, f
 // fp16, fp32 merged rows rotated back and cast once, by the merge);
 // fused = false, the dequantize-then-SDPA route (q rotated to fp16, the fp16
 // SDPA arithmetic on the expansion's values, the fp16 rows rotated back here).
+// The reference's gate for its fused verify pass (fused_attention.rs:69-110,
+// cache.rs:3520-3560): causal, 1..5 query rows, more than 2048 cached tokens,
+// at most 32 query heads a KV head. The block kernel runs it for any of those
+// shapes (G * rows <= 160: one or two 128-row query tiles, every key split);
+// the standalone verify kernel (QW_T4_BLOCK = 0) holds G * rows <= 32.
+static bool t4_fused_route(bool causal, int n_rows, int T, int G) {
+    return causal && n_rows >= 1 && n_rows <= 5 && T > 2048 && G <= 32 &&
+           (QW_T4_BLOCK || G * n_rows <= kT4vRows);
+}
+
 static int turbo4_block(KVCache& c, const void* q, int n_q_heads, int n_rows, float scale,
                         bool causal, bool fused, void* out, hipStream_t stream) {
     const int D = c.D, G = n_q_heads / c.hkv;
@@ -836,7 +846,7 @@ int turbo4_update_and_attention(KVCache& c, const void* q, int n_q_heads, int n_
     // the routes of turbo4_attention below: the fused pass and the block
     // kernel's one-tile blocks append in the block launch, the decode route
     // in the decode launch's append unit
-    const bool fused = causal && n_rows <= 5 && T > 2048 && G * n_rows <= kT4vRows;
+    const bool fused = t4_fused_route(causal, n_rows, T, G);
     const bool block = QW_T4_BLOCK && block_append_fits_t4(c, G, n_rows) && (fused || G * n_rows > 16);
     const bool decode = !fused && QW_T4_FUSED_DECODE && G * n_rows <= 16 && c.offset >= 1;
     if (!(QW_T4_APPEND && (block || decode))) {
@@ -890,10 +900,7 @@ int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float
     DeviceGuard dg(c.device);
     QW_REQUIRE(dg.ok, QW_ERR_HIP, "attention: hipSetDevice failed");
     const int D = c.D, T = c.offset;
-    // The reference's gate for its fused verify pass (fused_attention.rs:
-    // 70-100, cache.rs:3520-3560): causal, 1..5 query rows, more than 2048
-    // cached tokens; here also G * rows <= 32 (one workgroup's rows).
-    if (causal && n_rows <= 5 && T > 2048 && (n_q_heads / c.hkv) * n_rows <= kT4vRows)
+    if (t4_fused_route(causal, n_rows, T, n_q_heads / c.hkv))
         return QW_T4_BLOCK ? turbo4_block(c, q, n_q_heads, n_rows, scale, causal, true, out, stream)
                            : turbo4_verify(c, q, n_q_heads, n_rows, scale, out, stream);
     const int qrows = n_q_heads * n_rows;

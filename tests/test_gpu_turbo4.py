@@ -210,9 +210,9 @@ def assert_fused_exact(out, ref, what=""):
 
 def fused_verify_route(T, L, causal, G):
     """The reference's gate for its fused Turbo4 verify pass (fused_attention.rs:
-    70-100): causal, 1..5 rows, more than 2048 cached tokens (here also
-    G * rows <= 32); everything else takes the dequantize-then-SDPA route."""
-    return causal and L <= 5 and T > 2048 and G * L <= 32
+    69-110): causal, 1..5 rows, more than 2048 cached tokens, at most 32 query
+    heads a KV head; everything else takes the dequantize-then-SDPA route."""
+    return causal and 1 <= L <= 5 and T > 2048 and G <= 32
 
 
 @pytest.mark.parametrize("T_prefix,L,causal,D", [
@@ -251,7 +251,11 @@ def test_turbo4_attention_matches_oracle(T_prefix, L, causal, D):
     (3000, 4, 32, 4, 256),    # G * L = 32: both row tiles of the fused kernel full
     (2500, 5, 8, 8, 256),     # no GQA sharing (G = 1), 5 rows
     (4000, 3, 16, 2, 128),    # head_dim 128, two KV heads
-    (3000, 5, 56, 8, 256),    # G * L = 35 > 32: the dequantize route
+    (3000, 5, 56, 8, 256),    # G * L = 35: fused (one 128-row query tile)
+    (2600, 5, 64, 8, 256),    # G = 8 with 5 rows (40)
+    (4000, 4, 64, 2, 128),    # G = 32 with 4 rows: exactly one query tile, head_dim 128
+    (2500, 5, 128, 4, 256),   # G = 32 with 5 rows (160): two query tiles, every key split
+    (3000, 3, 132, 4, 256),   # G = 33 > 32: the dequantize route
 ])
 def test_turbo4_verify_geometries(T_prefix, L, hq, hkv, D):
     import qw_amd
