@@ -30,8 +30,8 @@
 //   One barrier a tile. RT is chosen per launch so the workgroup count fills
 //   the 256 CUs in whole rounds where the row count allows.
 //   One key split: the workgroup writes normalized fp16 rows. Several:
-//   fp32 partials (m, l, O; rows in V slot order) and the shared split-K
-//   merge kernel.
+//   partials (fp32 m and l, the row O / l in fp16; the fused Turbo4 pass
+//   keeps O in fp32) and a split-K merge kernel.
 #include <algorithm>
 #include <map>
 #include <mutex>
@@ -120,6 +120,29 @@ constexpr int block_waves() {
 #ifndef QW_BLOCK_SCHED_PV
 #define QW_BLOCK_SCHED_PV 4  // > 0: V reads kept that far ahead of the P.V MFMAs
 #endif
+
+// Split partials of the non-fused launches in fp16 (each row O / l rounded
+// once, (m, l) in fp32), as the reference's split-K passes keep them
+// (turbo4_attention.cpp:180-200); 0: fp32 O and l. Measured (A/B in one
+// run): config 4 48.3 -> 46.0 us, served 4-row verify 22.7 -> 21.8 us,
+// 5-row 33.6 -> 32.5 us; parity unchanged within the bar.
+#ifndef QW_BLOCK_PART16
+#define QW_BLOCK_PART16 1
+#endif
+constexpr bool kPart16 = QW_BLOCK_PART16;
+
+// Wave priority raised over the MFMA phases of a tile (QK and P.V), so a
+// SIMD's waves drift apart and one wave's softmax and dequant VALU issue under
+// another's MFMAs: 0 never, 1 the launches that dequantize in the loop, 2
+// every launch. Measured (A/B in one run): served 4- and 5-row verify blocks
+// -0.15 to -0.35 us, config 4 unchanged, the image launches of config 3
+// +0.5 % (their three waves a SIMD already overlap).
+#ifndef QW_BLOCK_SETPRIO
+#define QW_BLOCK_SETPRIO 1
+#endif
+constexpr bool kSetprio(int pm) {
+    return QW_BLOCK_SETPRIO == 2 || (QW_BLOCK_SETPRIO == 1 && pm != 2);
+}
 
 template <int D>
 struct BlockShape {
@@ -563,6 +586,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
             for (int tt = 0; tt < 2; tt++)
 #pragma unroll
                 for (int rt = 0; rt < RT; rt++) acc[u][tt][rt] = float4v{0.f, 0.f, 0.f, 0.f};
+        if constexpr (kSetprio(PM)) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int m = 0; m < NM; m++) {
 #pragma unroll
@@ -588,6 +612,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
             __builtin_amdgcn_sched_group_barrier(0x008, AH, 0);
         }
 #endif
+        if constexpr (kSetprio(PM)) __builtin_amdgcn_s_setprio(0);
         half8 pop[NSUB][RT];
         // Scores -> fp16 rounding -> (mask) -> online softmax -> P; the mask
         // only for tiles some row of the wave cannot fully see (a scalar
@@ -720,6 +745,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
             softmax();
         // O += P . V: B = slot 16mm + r16 (column r16 of output tile mm) of
         // V block 4u + g, i.e. keys 32u + 8g .. +7.
+        if constexpr (kSetprio(PM)) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int u = 0; u < NSUB; u++) {
             const half8* vb8 = sV8 + (4 * u + g) * VROW + r16;
@@ -748,6 +774,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
             __builtin_amdgcn_sched_group_barrier(0x008, AH, 1);
         }
 #endif
+        if constexpr (kSetprio(PM)) __builtin_amdgcn_s_setprio(0);
     };
 
     if constexpr (PM == 1) {
@@ -854,6 +881,32 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
                 for (int mm = 0; mm < NT; mm++) {
                     const int d = v_logical_dim(16 * mm + r16, D, VB);
                     a.out[obase + d] = (f16)(acc_o[rt][mm][i] * inv[i]);
+                }
+            }
+        } else if constexpr (kPart16 && !FUSED) {
+            // fp16 partials: row O / l rounded once, lane r16's NT slots
+            // 16 mm + r16 at places NT r16 + mm (whole 16-byte stores), and
+            // (m, l) in fp32
+            const int64_t pbase = ((int64_t)h * n_split + sp) * a.PR - a.prow0;
+            const int rho = wrow0 + 16 * rt + r16;
+            if (g == 0 && rho < a.R) a.part_ml[pbase + rho] = float2{m_run[rt], lsum};
+            float inv[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float l = __shfl(lsum, 4 * g + i);
+                inv[i] = l > 0.0f ? 1.0f / l : 0.0f;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int row = rbase + i;
+                if (row >= a.R) continue;
+                f16* prow = (f16*)a.part_o + (pbase + row) * D + NT * r16;
+#pragma unroll
+                for (int c = 0; c < NT / 8; c++) {
+                    half8 y;
+#pragma unroll
+                    for (int j = 0; j < 8; j++) y[j] = (f16)(acc_o[rt][8 * c + j][i] * inv[i]);
+                    *(half8*)(prow + 8 * c) = y;
                 }
             }
         } else {
@@ -1164,6 +1217,9 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     if (n_split > 1 && T4M == 2)
         return launch_t4_merge_rotate(t.part_o, t.part_ml, n_split, t.PR, R, cc.hkv, D, G, Tq, 16,
                                       true, t4_tab, out, stream);
+    if (n_split > 1 && kPart16)
+        return launch_partial_merge_h((const f16*)t.part_o, t.part_ml, n_split, t.PR, t.prow0, t.PR,
+                                      cc.hkv, D, G, Tq, out, stream, T4M ? 16 : BITS);
     if (n_split > 1)
         return launch_partial_merge(t.part_o, t.part_ml, n_split, t.PR, t.prow0, t.PR, cc.hkv, D,
                                     G, Tq, out, stream, T4M ? 16 : BITS);
@@ -1245,6 +1301,9 @@ static int launch_block_append_bits(KVCache& cc, const f16* q, int G, int L, con
     if (T4M == 2)
         return launch_t4_merge_rotate(a.part_o, a.part_ml, a.n_split, R, R, cc.hkv, D, G, L, 16, true,
                                       t4_tab, out, stream);
+    if (kPart16)
+        return launch_partial_merge_h((const f16*)a.part_o, a.part_ml, a.n_split, R, 0, R, cc.hkv, D,
+                                      G, L, out, stream, T4M ? 16 : BITS);
     return launch_partial_merge(a.part_o, a.part_ml, a.n_split, R, 0, R, cc.hkv, D, G, L, out,
                                 stream, T4M ? 16 : BITS);
 }

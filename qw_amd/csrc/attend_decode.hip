@@ -1331,6 +1331,125 @@ static void launch_merge_rows_vec(const float* part_o, const float2* part_ml, in
     }
 }
 
+// The merge of the block kernel's fp16 partials (normalized rows, place
+// NT * r + mm = slot 16 mm + r): one workgroup a (row, KV head), 4 waves; lane
+// n owns places SPL*n .. +SPL-1 (one 4- or 8-byte load a partial), wave w
+// sums partials w, w + 4, ... weighted by e^(m_c - m) l_c, and the waves
+// combine through LDS.
+template <int D, int PER>
+__global__ __launch_bounds__(256) void merge_rows_h_kernel(const f16* __restrict__ part_o,
+                                                           const float2* __restrict__ part_ml,
+                                                           int nc, int rstride, int row0, int G,
+                                                           int Tq, int slot_bits,
+                                                           f16* __restrict__ out) {
+    constexpr int SPL = D / 64, NT = D / 16;
+    typedef _Float16 hvec __attribute__((ext_vector_type(SPL)));
+    typedef float vec __attribute__((ext_vector_type(SPL)));
+    const int row = blockIdx.x, h = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t base = (int64_t)h * nc * rstride + row;
+    hvec v[PER];
+    float2 ml[PER];
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int c = wave + 4 * i;
+        if (c < nc) {
+            ml[i] = part_ml[base + (int64_t)c * rstride];
+            v[i] = *(const hvec*)(part_o + (base + (int64_t)c * rstride) * D + SPL * lane);
+        } else {
+            ml[i] = float2{-INFINITY, 0.0f};
+            v[i] = hvec{};
+        }
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < PER; i++) m = fmaxf(m, ml[i].x);
+    vec o = vec{};
+    float l = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const float w = ml[i].x == -INFINITY
+                            ? 0.0f
+                            : __builtin_amdgcn_exp2f((ml[i].x - m) * kLog2e) * ml[i].y;
+#pragma unroll
+        for (int j = 0; j < SPL; j++) o[j] = __builtin_fmaf(w, (float)v[i][j], o[j]);
+        l += w;
+    }
+    __shared__ float2 sm_ml[4];
+    __shared__ vec sm_o[4][64];
+    if (lane == 0) sm_ml[wave] = float2{m, l};
+    sm_o[wave][lane] = o;
+    __syncthreads();
+    if (wave == 0) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; w++) M = fmaxf(M, sm_ml[w].x);
+        vec O = vec{};
+        float L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float f = sm_ml[w].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((sm_ml[w].x - M) * kLog2e);
+            O += f * sm_o[w][lane];
+            L = __builtin_fmaf(f, sm_ml[w].y, L);
+        }
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        const int orow = row0 + row;
+        const int qh = h * G + orow % G, qr = orow / G;
+        const int64_t obase = ((int64_t)qh * Tq + qr) * D;
+#pragma unroll
+        for (int j = 0; j < SPL; j++) {
+            const int p = SPL * lane + j;
+            const int sd = 16 * (p % NT) + p / NT;
+            const int d = slot_bits ? v_logical_dim(sd, D, slot_bits) : sd;
+            out[obase + d] = (f16)(O[j] * inv);
+        }
+    }
+}
+
+template <int D>
+static void launch_merge_rows_h(const f16* part_o, const float2* part_ml, int nc, int rstride,
+                                int row0, int R, int hkv, int G, int Tq, int slot_bits, f16* out,
+                                hipStream_t stream) {
+    const dim3 grid(R, hkv);
+    switch (merge_per(nc)) {
+        case 4:
+            hipLaunchKernelGGL((merge_rows_h_kernel<D, 4>), grid, dim3(256), 0, stream, part_o,
+                               part_ml, nc, rstride, row0, G, Tq, slot_bits, out);
+            break;
+        case 8:
+            hipLaunchKernelGGL((merge_rows_h_kernel<D, 8>), grid, dim3(256), 0, stream, part_o,
+                               part_ml, nc, rstride, row0, G, Tq, slot_bits, out);
+            break;
+        case 16:
+            hipLaunchKernelGGL((merge_rows_h_kernel<D, 16>), grid, dim3(256), 0, stream, part_o,
+                               part_ml, nc, rstride, row0, G, Tq, slot_bits, out);
+            break;
+        case 32:
+            hipLaunchKernelGGL((merge_rows_h_kernel<D, 32>), grid, dim3(256), 0, stream, part_o,
+                               part_ml, nc, rstride, row0, G, Tq, slot_bits, out);
+            break;
+        default:
+            hipLaunchKernelGGL((merge_rows_h_kernel<D, kMergeMaxPer>), grid, dim3(256), 0, stream,
+                               part_o, part_ml, nc, rstride, row0, G, Tq, slot_bits, out);
+    }
+}
+
+int launch_partial_merge_h(const f16* part_o, const float2* part_ml, int nc, int rstride, int row0,
+                           int R, int hkv, int D, int G, int Tq, f16* out, hipStream_t stream,
+                           int slot_bits) {
+    QW_REQUIRE(nc >= 1 && nc <= 4 * kMergeMaxPer, QW_ERR_INVALID_ARGUMENT,
+               "merge: partial count out of range");
+    QW_REQUIRE(D == 128 || D == 256, QW_ERR_INVALID_ARGUMENT, "merge: fp16 partials need D 128/256");
+    if (D == 256)
+        launch_merge_rows_h<256>(part_o, part_ml, nc, rstride, row0, R, hkv, G, Tq, slot_bits, out,
+                                 stream);
+    else
+        launch_merge_rows_h<128>(part_o, part_ml, nc, rstride, row0, R, hkv, G, Tq, slot_bits, out,
+                                 stream);
+    QW_HIP_CHECK(hipGetLastError());
+    return QW_OK;
+}
+
 #ifndef QW_MERGE_VEC
 #define QW_MERGE_VEC 1
 #endif

@@ -253,6 +253,13 @@ int launch_block_append_attention(KVCache& c, const f16* q, int G, int n_rows, c
 int launch_partial_merge(const float* part_o, const float2* part_ml, int nc, int rstride, int row0,
                          int R, int hkv, int D, int G, int Tq, f16* out, hipStream_t stream,
                          int slot_bits = 0, float* out32 = nullptr);
+// The same merge over the block kernel's fp16 partials: each partial row is
+// O_c / l_c rounded to fp16, place NT * r + mm holding slot 16 mm + r
+// (NT = D / 16), with (m_c, l_c) in part_ml; out[row0 + row] =
+// sum_c e^(m_c - M) l_c O_c / sum_c e^(m_c - M) l_c.
+int launch_partial_merge_h(const f16* part_o, const float2* part_ml, int nc, int rstride, int row0,
+                           int R, int hkv, int D, int G, int Tq, f16* out, hipStream_t stream,
+                           int slot_bits);
 
 
 // D-LSA K1 select (dlsa_select.hip).
