@@ -1131,13 +1131,13 @@ def main() -> int:
         extra["turbo4_decode"] = {
             "us_per_layer": round(t4["layer_ms"] * 1e3, 2),
             "us_per_layer_eager": round(t4["eager_layer_ms"] * 1e3, 2), "keys": t4["T"],
-            "route": "rotate q, expand rotated K/V to fp16, fp16 decode, rotate back"}
+            "route": "decode kernel: q rotated in the kernel, packed indices read in place, the new token appended in its launch; merge kernel rotates the rows back"}
         log("bench: Turbo4 fused causal verify (4 rows, config-2 geometry)")
         tv = bench_turbo4_verify(torch, qw_amd, LAYERS, args.warmup, reps)
         extra["turbo4_verify"] = {
             "us_per_layer": round(tv["layer_ms"] * 1e3, 2),
             "us_per_layer_eager": round(tv["eager_layer_ms"] * 1e3, 2), "keys": tv["T"], "rows": tv["L"],
-            "route": "rotate q, fused verify kernel on the packed codes, merge, rotate back"}
+            "route": "fused verify pass in the block kernel on the packed indices (q rotated in the kernel, rows appended in its launch); merge kernel rotates the rows back"}
         line["extra"] = extra
     if not args.no_cpu:
         threads = cpu_threads()

@@ -141,7 +141,7 @@ int qw_kv_dequantize(const qw_kv_cache* cache, int start, int n, void* k_out, vo
  * Scores are formed as f16(f16(scale) * q) . k and rounded to fp16 before
  * the fp32 softmax, as MLX's SDPA forms them.
  * On a Turbo4 cache the reference's routing applies: causal blocks of 1..5
- * rows over more than 2048 tokens (and G * n_rows <= 32) take its fused
+ * rows over more than 2048 tokens (at most 32 query heads a KV head) take its fused
  * verify pass (turbo4_attention.cpp:45-264: q' = f16(q_rot * scale * log2 e),
  * fp32 scores from the packed codes); every other call takes its
  * dequantize-then-SDPA route (turbo/sparse_v.rs:1051-1072). */
@@ -154,6 +154,51 @@ int qw_kv_update_and_attention(qw_kv_cache* cache, const void* q, int n_q_heads,
  * r of n_rows sees keys t <= offset - n_rows + r. */
 int qw_kv_attention(qw_kv_cache* cache, const void* q, int n_q_heads, int n_rows, float scale,
                     int causal, void* out, void* stream);
+
+/* Attention with the reference's general options over fp16 K/V views:
+ * layers::attention(q, k, v, scale, mask, softcap, window) (layers.rs:4010)
+ * and causal_attention(q, k, v, scale, softcap, window) (lib.rs:3185).
+ *   q [n_q_heads][n_rows][head_dim] fp16, head_dim 64 / 128 / 256; K and V
+ *   rows [n_kv_heads][n_keys][head_dim] with element strides (% 8 == 0);
+ *   causal: bottom-right, row r sees keys t <= n_keys - n_rows + r;
+ *   window > 0 (causal required): also t >= n_keys - n_rows + r - window + 1,
+ *     the windowed causal mask causal_attention builds (utils.rs:95-140);
+ *   softcap > 0: the softcap composite (mlx_cxx_bridge.cpp:1573-1590):
+ *     S = f16(q . k), s = tanh(S * scale / softcap) * softcap in fp32, fp32
+ *     softmax and P.V; softcap == 0: MLX's SDPA, S = f16(f16(f16(scale) q) . k);
+ *   mask (null: none) [n_q_heads or broadcast][n_rows][n_keys], key stride 1,
+ *     element strides mask_head_stride (0: one mask for every head) and
+ *     mask_row_stride: QW_MASK_BOOL (uint8, nonzero attends), or additive
+ *     QW_DTYPE_F16 / BF16 / F32, cast to fp16 as the reference casts float
+ *     masks to q's dtype (mlx_cxx_bridge.cpp:3466-3497) and added to the
+ *     scores (in fp16 without softcap); a bool mask with softcap is refused
+ *     (QW_ERR_UNSUPPORTED: the reference would cast it to 0/1 offsets);
+ *   out [n_q_heads][n_rows][head_dim] fp16; a row with no visible key is 0.
+ * A generic kernel (sdpa_general.hip), not the tuned fused paths. */
+int qw_sdpa(const void* q, int n_q_heads, int n_rows, const void* k, const void* v,
+            int n_kv_heads, int n_keys, int head_dim, int64_t k_head_stride, int64_t k_row_stride,
+            int64_t v_head_stride, int64_t v_row_stride, float scale, int causal, int window,
+            float softcap, const void* mask, int mask_dtype, int64_t mask_head_stride,
+            int64_t mask_row_stride, void* out, void* stream);
+
+/* The same over a cache (n_keys = its offset): without mask, softcap or
+ * window it is qw_kv_attention; otherwise the cache's rows are dequantized
+ * into a per-stream workspace and attended as qw_sdpa does, the route of the
+ * runtime's masked branch (update_and_fetch + layers::attention,
+ * qwen3_next.rs:316-324). On a Turbo4 cache: the rotated expansion, q rotated
+ * in and the output rotated back (update_and_turbo4_attention with a mask,
+ * cache.rs:3495 -> turbo/sparse_v.rs:1051-1072). The update form appends
+ * k_new / v_new ([n_kv_heads][n_rows][head_dim]) first; invalid options are
+ * refused before the append. */
+int qw_kv_attention_general(qw_kv_cache* cache, const void* q, int n_q_heads, int n_rows,
+                            float scale, int causal, int window, float softcap, const void* mask,
+                            int mask_dtype, int64_t mask_head_stride, int64_t mask_row_stride,
+                            void* out, void* stream);
+int qw_kv_update_and_attention_general(qw_kv_cache* cache, const void* q, int n_q_heads,
+                                       int n_rows, const void* k_new, const void* v_new,
+                                       float scale, int causal, int window, float softcap,
+                                       const void* mask, int mask_dtype, int64_t mask_head_stride,
+                                       int64_t mask_row_stride, void* out, void* stream);
 
 /* KVCache::trim (cache.rs:2251): drop the last n tokens (clamped to the
  * cached length); *trimmed receives the number removed. No device work. */
@@ -258,6 +303,8 @@ int qw_kv_update_and_dlsa_attention(qw_kv_cache* cache, const void* q, int n_q_h
 #define QW_DTYPE_F16 0
 #define QW_DTYPE_BF16 1
 #define QW_DTYPE_F32 2
+/* Mask dtype of the general attention calls: uint8, nonzero = attend. */
+#define QW_MASK_BOOL 3
 
 /* dlsa_attention::sparse_attention_with (dlsa_attention.rs:44) with the
  * reference's full dtype and head-dim contract (mlx_cxx_dlsa_attention.cpp:

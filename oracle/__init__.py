@@ -204,6 +204,72 @@ def sdpa_f64(q, k, v, scale: float, q_pos=None, threads: int | None = None):
     return out
 
 
+def sdpa_general(q, k, v, scale: float, causal: bool = False, window: int = 0,
+                 softcap: float = 0.0, mask=None) -> np.ndarray:
+    """Attention with the reference's general options (numpy): layers::attention
+    (layers.rs:4010-4060) and causal_attention (lib.rs:3185-3275) reduce to
+    MLX's SDPA with an array mask, or with softcap to the composite of
+    mlx_cxx_bridge.cpp:1573-1590.
+
+    q [Hq, L, D] fp16, k / v [Hkv, T, D] fp16. Position of row r:
+    p = T - L + r. causal keeps keys t <= p; window > 0 also t >= p - window + 1
+    (create_causal_mask_with_window, utils.rs:95-140). mask broadcastable to
+    [Hq, L, T]: bool / uint8 keeps the scores where nonzero; a float mask is
+    cast to fp16 (mlx_cxx_bridge.cpp:3466-3497) and added.
+      softcap == 0: S = f16(f16(f16(scale) q) . k); S = f16(S + mask);
+        P = f16(softmax_fp32(S)); out = f16(P . V).
+      softcap > 0: S = f16(q . k); s = tanh(S scale / cap) cap, + mask, in
+        fp32; P = softmax_fp32(s) (not rounded); out = f16(P . V).
+    Dot products and P . V accumulate in fp64 (MLX accumulates in fp32; the
+    two differ only at fp16 rounding ties of S). A row with no visible key is
+    zeros. Returns fp16 [Hq, L, D]."""
+    q = np.asarray(q, np.float16)
+    k = np.asarray(k, np.float16)
+    v = np.asarray(v, np.float16)
+    hq, L, D = q.shape
+    hkv, T, _ = k.shape
+    G = hq // hkv
+    kk = np.repeat(k.astype(np.float64), G, axis=0)
+    vv = np.repeat(v.astype(np.float64), G, axis=0)
+    t = np.arange(T)
+    p = T - L + np.arange(L)
+    vis = np.ones((L, T), bool)
+    if causal:
+        vis &= t[None, :] <= p[:, None]
+    if window > 0:
+        vis &= t[None, :] >= (p - window + 1)[:, None]
+    vis = np.broadcast_to(vis, (hq, L, T)).copy()
+    add = None
+    if mask is not None:
+        m = np.asarray(mask)
+        m = np.broadcast_to(m.reshape((-1, L, T)), (hq, L, T))
+        if m.dtype == np.bool_ or m.dtype == np.uint8:
+            vis &= m != 0
+        else:
+            add = m.astype(np.float16).astype(np.float32)
+    if softcap <= 0:
+        sh = np.float32(np.float16(scale))
+        qs = (sh * q.astype(np.float32)).astype(np.float16).astype(np.float64)
+        s = np.matmul(qs, kk.transpose(0, 2, 1)).astype(np.float16).astype(np.float32)
+        if add is not None:
+            s = (s + add).astype(np.float16).astype(np.float32)
+    else:
+        S = np.matmul(q.astype(np.float64), kk.transpose(0, 2, 1)).astype(np.float16)
+        s = S.astype(np.float32) * np.float32(scale)
+        s = np.tanh(s / np.float32(softcap)).astype(np.float32) * np.float32(softcap)
+        if add is not None:
+            s = s + add
+    s = np.where(vis, s, np.float32(-np.inf)).astype(np.float32)
+    mx = s.max(axis=-1, keepdims=True)
+    any_vis = np.isfinite(mx)
+    e = np.exp(s - np.where(any_vis, mx, np.float32(0.0))).astype(np.float32)
+    den = e.sum(axis=-1, keepdims=True, dtype=np.float32)
+    P = np.where(any_vis, e / np.where(den > 0, den, np.float32(1.0)), np.float32(0.0))
+    if softcap <= 0:
+        P = P.astype(np.float16)
+    return np.matmul(P.astype(np.float64), vv).astype(np.float16)
+
+
 def dlsa_attention_f64(q, k, v, lists, lengths, scale: float):
     """The K2 contract in fp64 for inputs of any float dtype (numpy; the
     reference's own host check, dlsa_attention.rs:140-170): for row r and

@@ -11,6 +11,11 @@ and the tests use the reference's names:
   ``trim`` :2251, ``offset``, ``nbytes`` :3063, snapshot tensors :570-626).
 * :func:`sparse_attention` / :func:`sparse_attention_with` mirror
   ``crates/mlxcel-core/src/dlsa_attention.rs:31`` / ``:44``.
+* :func:`attention` / :func:`causal_attention` mirror ``layers::attention(q, k,
+  v, scale, mask, softcap, window)`` (``layers.rs:4010``) and
+  ``causal_attention(q, k, v, scale, softcap, window)`` (``lib.rs:3185``);
+  ``KVCache.update_and_attention(..., mask)`` and
+  :meth:`KVCache.attention_general` take the same options over a cache.
 
 Torch is used only to hold device memory and to name the current stream.
 Tensors follow the reference's layouts: ``[1, H, L, D]`` (the batch of 1 may
@@ -22,7 +27,8 @@ from __future__ import annotations
 import ctypes
 import os
 
-__all__ = ["KVCacheMode", "KVCache", "QwError", "sparse_attention", "sparse_attention_with",
+__all__ = ["KVCacheMode", "KVCache", "QwError", "attention", "causal_attention",
+           "sparse_attention", "sparse_attention_with",
            "fused_rope_qk_append", "dlsa_select", "dlsa_select_with", "turbo4_codebook",
            "turbo4_signs",
            "lib", "LIB_PATH"]
@@ -67,6 +73,12 @@ _SIGNATURES = {
     "qw_kv_dequantize": (_i, [_p, _i, _i, _p, _p, _p]),
     "qw_kv_update_and_attention": (_i, [_p, _p, _i, _i, _p, _p, _f, _i, _p, _p]),
     "qw_kv_attention": (_i, [_p, _p, _i, _i, _f, _i, _p, _p]),
+    "qw_sdpa": (_i, [_p, _i, _i, _p, _p, _i, _i, _i, _i64, _i64, _i64, _i64, _f, _i, _i, _f,
+                     _p, _i, _i64, _i64, _p, _p]),
+    "qw_kv_attention_general": (_i, [_p, _p, _i, _i, _f, _i, _i, _f, _p, _i, _i64, _i64, _p,
+                                     _p]),
+    "qw_kv_update_and_attention_general": (_i, [_p, _p, _i, _i, _p, _p, _f, _i, _i, _f, _p, _i,
+                                                _i64, _i64, _p, _p]),
     "qw_kv_trim": (_i, [_p, _i, ctypes.POINTER(_i)]),
     "qw_kv_dlsa_attention": (_i, [_p, _p, _i, _i, _p, _p, _i, _f, _p, _p]),
     "qw_kv_update_and_dlsa_attention": (_i, [_p, _p, _i, _i, _p, _p, _p, _p, _i, _f, _p, _p]),
@@ -277,9 +289,13 @@ class KVCache:
                                                     out.data_ptr(), st))
         return out.unsqueeze(0)
 
-    def update_and_attention(self, q, keys, values, scale: float):
-        """Append, then attend without a mask (reference ``update_and_turbo4_attention``)."""
-        return self._attn(q, keys, values, scale, False)
+    def update_and_attention(self, q, keys, values, scale: float, mask=None):
+        """Append, then attend (reference ``update_and_turbo4_attention(q, k, v,
+        scale, mask)``, cache.rs:3495). With a mask (bool, or additive f16 /
+        bf16 / f32, broadcastable to [1, Hq, L, T]) the general route runs."""
+        if mask is None:
+            return self._attn(q, keys, values, scale, False)
+        return self._general(q, keys, values, scale, False, 0, 0.0, mask)
 
     def update_and_causal_attention(self, q, keys, values, scale: float):
         """Append, then bottom-right causal attention (``update_and_turbo4_causal_attention``)."""
@@ -288,6 +304,38 @@ class KVCache:
     def attention(self, q, scale: float, causal: bool = False):
         """Attend the cache as it is (fused prefix attention, cache.rs:3607)."""
         return self._attn(q, None, None, scale, causal)
+
+    def attention_general(self, q, scale: float, causal: bool = False, window: int = 0,
+                          softcap: float = 0.0, mask=None):
+        """Attend the cache as it is with the general options (``layers::attention``'s
+        mask and softcap, ``causal_attention``'s window) over its dequantized rows."""
+        return self._general(q, None, None, scale, causal, window, softcap, mask)
+
+    def update_and_attention_general(self, q, keys, values, scale: float, causal: bool = False,
+                                     window: int = 0, softcap: float = 0.0, mask=None):
+        """Append, then :meth:`attention_general`."""
+        return self._general(q, keys, values, scale, causal, window, softcap, mask)
+
+    def _general(self, q, keys, values, scale, causal, window, softcap, mask):
+        torch = _torch()
+        qq = _as3(q, "q")
+        hq, L, D = qq.shape
+        out = torch.empty_like(qq)
+        T = self.offset + (0 if keys is None else L)
+        m, md, mhs, mrs, _keep = _mask_args(mask, hq, L, T)
+        st = _stream(self.device)
+        if keys is None:
+            _check(lib().qw_kv_attention_general(self._h, qq.data_ptr(), hq, L, float(scale),
+                                                 int(causal), int(window), float(softcap), m, md,
+                                                 mhs, mrs, out.data_ptr(), st))
+        else:
+            k, v = _as3(keys, "keys"), _as3(values, "values")
+            if k.shape != v.shape or k.shape[1] != L:
+                raise QwError(1, "attention: new keys/values must have q's row count")
+            _check(lib().qw_kv_update_and_attention_general(
+                self._h, qq.data_ptr(), hq, L, k.data_ptr(), v.data_ptr(), float(scale),
+                int(causal), int(window), float(softcap), m, md, mhs, mrs, out.data_ptr(), st))
+        return out.unsqueeze(0)
 
     # -- D-LSA read over the cache (qwen3_next/dlsa.rs:161-177)
     def _dlsa(self, q, keys, values, lists, lengths, scale: float):
@@ -452,6 +500,64 @@ def sparse_attention_with(q, k, v, lists, lengths, scale: float, parts: int = 0,
         vv.stride(1), lists.data_ptr(), lengths.data_ptr(), L, lists.shape[1], hq, hkv, D, T,
         float(scale), parts, waves, out.data_ptr(), _stream(qq.device)))
     return out.unsqueeze(0)
+
+
+QW_MASK_BOOL = 3
+
+
+def _mask_args(mask, hq: int, L: int, T: int):
+    """(pointer, dtype code, head stride, row stride, tensor kept alive) of a
+    mask broadcastable to [1, hq, L, T]: bool / uint8 (nonzero attends) or an
+    additive f16 / bf16 / f32 mask."""
+    if mask is None:
+        return None, 0, 0, 0, None
+    torch = _torch()
+    m = mask
+    while m.dim() > 3:
+        if m.shape[0] != 1:
+            raise QwError(1, "mask: batch must be 1")
+        m = m[0]
+    if m.dim() == 2:
+        m = m.unsqueeze(0)
+    if m.dim() != 3 or m.shape[0] not in (1, hq) or m.shape[1] != L or m.shape[2] != T:
+        raise QwError(1, f"mask: shape {tuple(mask.shape)} does not broadcast to [1, {hq}, {L}, {T}]")
+    if not m.is_cuda:
+        raise QwError(1, "mask: device tensor expected")
+    codes = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2, torch.bool: QW_MASK_BOOL,
+             torch.uint8: QW_MASK_BOOL}
+    if m.dtype not in codes:
+        raise QwError(1, f"mask: bool or f16/bf16/f32 expected, got {m.dtype}")
+    if m.stride(2) != 1:
+        m = m.contiguous()
+    hs = 0 if m.shape[0] == 1 else m.stride(0)
+    return m.data_ptr(), codes[m.dtype], hs, m.stride(1), m
+
+
+def attention(q, k, v, scale: float, mask=None, softcap: float = 0.0, window: int = 0,
+              causal: bool = False):
+    """``layers::attention(q, k, v, scale, mask, softcap, window)`` (layers.rs:4010)
+    over fp16 K/V [1, Hkv, T, D] (any head/row strides); ``causal`` and
+    ``window`` give ``causal_attention``'s masks (lib.rs:3185)."""
+    torch = _torch()
+    qq = _as3(q, "q")
+    kk, vv = _kv_view(k, "k"), _kv_view(v, "v")
+    if kk.shape != vv.shape or kk.shape[2] != qq.shape[2]:
+        raise QwError(1, "attention: k/v shapes disagree with q")
+    hq, L, D = qq.shape
+    hkv, T, _ = kk.shape
+    m, md, mhs, mrs, _keep = _mask_args(mask, hq, L, T)
+    out = torch.empty_like(qq)
+    _check(lib().qw_sdpa(qq.data_ptr(), hq, L, kk.data_ptr(), vv.data_ptr(), hkv, T, D,
+                         kk.stride(0), kk.stride(1), vv.stride(0), vv.stride(1), float(scale),
+                         int(causal), int(window), float(softcap), m, md, mhs, mrs,
+                         out.data_ptr(), _stream(qq.device)))
+    return out.unsqueeze(0)
+
+
+def causal_attention(q, k, v, scale: float, softcap: float = 0.0, window: int = 0):
+    """``causal_attention(q, k, v, scale, softcap, window)`` (lib.rs:3185):
+    bottom-right causal, with the sliding window when ``window`` > 0."""
+    return attention(q, k, v, scale, None, softcap, window, True)
 
 
 def sparse_attention(q, k, v, lists, lengths, scale: float):

@@ -23,7 +23,7 @@ BUILD_DIR = os.path.join(HERE, "_build")
 ARCH = "gfx950"
 
 SOURCES = ["kv_cache.hip", "attend_decode.hip", "attend_block.hip", "dlsa.hip", "dlsa_typed.hip",
-           "dlsa_select.hip", "rope.hip", "turbo4.hip", "abi.hip"]
+           "sdpa_general.hip", "dlsa_select.hip", "rope.hip", "turbo4.hip", "abi.hip"]
 # The measurement library (read-floor and copy kernels), loaded by bench.py only.
 CEIL_SOURCES = ["ceiling.hip"]
 CEIL_OUT = os.path.join(HERE, "libqwceil.so")

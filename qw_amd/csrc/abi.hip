@@ -146,6 +146,78 @@ int qw_kv_attention(qw_kv_cache* cache, const void* q, int n_q_heads, int n_rows
                                      (hipStream_t)stream));
 }
 
+static qw::SdpaOptions sdpa_options(int causal, int window, float softcap, const void* mask,
+                                    int mask_dtype, int64_t mask_head_stride,
+                                    int64_t mask_row_stride) {
+    qw::SdpaOptions o;
+    o.causal = causal != 0;
+    o.window = window;
+    o.softcap = softcap;
+    o.mask = mask;
+    o.mask_dtype = mask_dtype;
+    o.mask_head_stride = mask_head_stride;
+    o.mask_row_stride = mask_row_stride;
+    return o;
+}
+
+// Append, then the general attention (update_and_fetch + layers::attention,
+// qwen3_next.rs:316-324; update_and_turbo4_attention, cache.rs:3495). The
+// options are checked before the append, so a rejected call leaves the cache
+// as it was.
+static int update_and_general(qw::KVCache& c, const void* q, int n_q_heads, int n_rows,
+                              const void* k_new, const void* v_new, float scale,
+                              const qw::SdpaOptions& o, void* out, hipStream_t stream) {
+    const bool bad_mask = o.mask && (o.mask_dtype < QW_DTYPE_F16 || o.mask_dtype > QW_MASK_BOOL ||
+                                     (o.mask_dtype == QW_MASK_BOOL && o.softcap > 0.0f) ||
+                                     o.mask_head_stride < 0 || o.mask_row_stride < 0);
+    QW_REQUIRE(q && out && n_rows > 0 && n_q_heads > 0 && n_q_heads % c.hkv == 0,
+               QW_ERR_INVALID_ARGUMENT, "attention: bad q geometry");
+    QW_REQUIRE(!(o.softcap < 0.0f) && o.softcap == o.softcap && (o.window <= 0 || o.causal) &&
+                   !bad_mask,
+               QW_ERR_INVALID_ARGUMENT, "attention: invalid general options (see qw_sdpa)");
+    int rc = c.update(k_new, v_new, n_rows, stream);
+    if (rc) return rc;
+    return qw::cache_attention_general(c, q, n_q_heads, n_rows, scale, o, out, stream);
+}
+
+int qw_sdpa(const void* q, int n_q_heads, int n_rows, const void* k, const void* v,
+            int n_kv_heads, int n_keys, int head_dim, int64_t k_head_stride, int64_t k_row_stride,
+            int64_t v_head_stride, int64_t v_row_stride, float scale, int causal, int window,
+            float softcap, const void* mask, int mask_dtype, int64_t mask_head_stride,
+            int64_t mask_row_stride, void* out, void* stream) {
+    QW_GUARDED(qw::sdpa_general(q, n_q_heads, n_rows, k, v, n_kv_heads, n_keys, head_dim,
+                                k_head_stride, k_row_stride, v_head_stride, v_row_stride, scale,
+                                sdpa_options(causal, window, softcap, mask, mask_dtype,
+                                             mask_head_stride, mask_row_stride),
+                                out, (hipStream_t)stream));
+}
+
+int qw_kv_attention_general(qw_kv_cache* cache, const void* q, int n_q_heads, int n_rows,
+                            float scale, int causal, int window, float softcap, const void* mask,
+                            int mask_dtype, int64_t mask_head_stride, int64_t mask_row_stride,
+                            void* out, void* stream) {
+    QW_HANDLE(cache);
+    QW_GUARDED(qw::cache_attention_general(
+        cache->impl, q, n_q_heads, n_rows, scale,
+        sdpa_options(causal, window, softcap, mask, mask_dtype, mask_head_stride, mask_row_stride),
+        out, (hipStream_t)stream));
+}
+
+int qw_kv_update_and_attention_general(qw_kv_cache* cache, const void* q, int n_q_heads,
+                                       int n_rows, const void* k_new, const void* v_new,
+                                       float scale, int causal, int window, float softcap,
+                                       const void* mask, int mask_dtype, int64_t mask_head_stride,
+                                       int64_t mask_row_stride, void* out, void* stream) {
+    QW_HANDLE(cache);
+    if (!mask && softcap == 0.0f && window <= 0)
+        QW_GUARDED(cache->impl.update_and_attention(q, n_q_heads, n_rows, k_new, v_new, scale,
+                                                    causal != 0, out, (hipStream_t)stream));
+    QW_GUARDED(update_and_general(cache->impl, q, n_q_heads, n_rows, k_new, v_new, scale,
+                                  sdpa_options(causal, window, softcap, mask, mask_dtype,
+                                               mask_head_stride, mask_row_stride),
+                                  out, (hipStream_t)stream));
+}
+
 int qw_kv_dlsa_attention(qw_kv_cache* cache, const void* q, int n_q_heads, int n_rows,
                          const int32_t* lists, const int32_t* lengths, int width, float scale,
                          void* out, void* stream) {

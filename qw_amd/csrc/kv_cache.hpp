@@ -253,6 +253,29 @@ int launch_block_append_attention(KVCache& c, const f16* q, int G, int n_rows, c
 int launch_partial_merge(const float* part_o, const float2* part_ml, int nc, int rstride, int row0,
                          int R, int hkv, int D, int G, int Tq, f16* out, hipStream_t stream,
                          int slot_bits = 0, float* out32 = nullptr);
+// Attention with the reference's general options (sdpa_general.hip):
+// layers::attention's mask and softcap and causal_attention's sliding window.
+struct SdpaOptions {
+    bool causal = false;
+    int window = 0;           // > 0 (with causal): keys p - window + 1 .. p
+    float softcap = 0.0f;     // > 0: tanh(s / softcap) * softcap on the scores
+    const void* mask = nullptr;  // [hq or broadcast][n_rows][n_keys], key stride 1
+    int mask_dtype = 0;       // QW_MASK_BOOL or QW_DTYPE_F16 / BF16 / F32 (additive)
+    int64_t mask_head_stride = 0, mask_row_stride = 0;  // elements; head stride 0 broadcasts
+};
+// Over fp16 K/V rows [hkv][n_keys][D] with element strides; q and out
+// [hq][n_rows][D] fp16.
+int sdpa_general(const void* q, int n_q_heads, int n_rows, const void* k, const void* v,
+                 int n_kv_heads, int n_keys, int head_dim, int64_t khs, int64_t krs, int64_t vhs,
+                 int64_t vrs, float scale, const SdpaOptions& o, void* out, hipStream_t stream);
+// Over a cache: without mask, softcap or window the cache's own fused
+// attention; else its rows dequantized (Turbo4: expanded in the rotated basis,
+// q rotated in and the output rotated back) and sdpa_general.
+int cache_attention_general(KVCache& c, const void* q, int n_q_heads, int n_rows, float scale,
+                            const SdpaOptions& o, void* out, hipStream_t stream);
+int turbo4_attention_general(KVCache& c, const void* q, int n_q_heads, int n_rows, float scale,
+                             const SdpaOptions& opts, void* out, hipStream_t stream);
+
 // The same merge over the block kernel's fp16 partials: each partial row is
 // O_c / l_c rounded to fp16, place NT * r + mm holding slot 16 mm + r
 // (NT = D / 16), with (m_c, l_c) in part_ml; out[row0 + row] =

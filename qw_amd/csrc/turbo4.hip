@@ -161,7 +161,9 @@ constexpr int kT4BlockRows = 1024;
 #endif
 constexpr int kExpandBlocks = 4;  // 8-key blocks a workgroup (capv / 8 is a multiple of 32)
 
-template <int D>
+// VROWS: V rows too ([hkv][capv][D], for the general SDPA); else V in the fp16
+// cache's 8-key blocks.
+template <int D, bool VROWS = false>
 __global__ __launch_bounds__(D) void turbo4_expand_kernel(
     const uint8_t* __restrict__ k_packed, const uint32_t* __restrict__ k_side,
     const uint8_t* __restrict__ v_packed, const uint32_t* __restrict__ v_side,
@@ -207,10 +209,15 @@ __global__ __launch_bounds__(D) void turbo4_expand_kernel(
             for (int j = 0; j < 8; j++) kv8[j] = vv8[j] = (f16)0.0f;
         }
         *(half8*)(kw + ((int64_t)h * capv + t) * D + 8 * c) = kv8;
-        // (the fp16 cache keeps V dims in MFMA lane order, v_phys_dim)
+        if constexpr (VROWS) {
+            *(half8*)(vw + ((int64_t)h * capv + t) * D + 8 * c) = vv8;
+        } else {
+            // (the fp16 cache keeps V dims in MFMA lane order, v_phys_dim)
 #pragma unroll
-        for (int j = 0; j < 8; j++) sv[n][v_phys_dim(8 * c + j, D, 16)][k] = vv8[j];
+            for (int j = 0; j < 8; j++) sv[n][v_phys_dim(8 * c + j, D, 16)][k] = vv8[j];
+        }
     }
+    if constexpr (VROWS) return;
     __syncthreads();
     const int p = threadIdx.x;  // physical dim slot
 #pragma unroll
@@ -889,6 +896,17 @@ int turbo4_update_and_attention(KVCache& c, const void* q, int n_q_heads, int n_
     return QW_OK;
 }
 
+static int turbo4_expansion_route(KVCache& c, const void* q, int n_q_heads, int n_rows,
+                                  float scale, bool causal, const SdpaOptions* opts, void* out,
+                                  hipStream_t stream);
+
+int turbo4_attention_general(KVCache& c, const void* q, int n_q_heads, int n_rows, float scale,
+                             const SdpaOptions& opts, void* out, hipStream_t stream) {
+    DeviceGuard dg(c.device);
+    QW_REQUIRE(dg.ok, QW_ERR_HIP, "attention: hipSetDevice failed");
+    return turbo4_expansion_route(c, q, n_q_heads, n_rows, scale, opts.causal, &opts, out, stream);
+}
+
 int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float scale,
                      bool causal, void* out, hipStream_t stream) {
     QW_REQUIRE(q && out, QW_ERR_INVALID_ARGUMENT, "attention: null q/out");
@@ -899,11 +917,10 @@ int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float
                "attention: fewer cached keys than query rows");
     DeviceGuard dg(c.device);
     QW_REQUIRE(dg.ok, QW_ERR_HIP, "attention: hipSetDevice failed");
-    const int D = c.D, T = c.offset;
+    const int T = c.offset;
     if (t4_fused_route(causal, n_rows, T, n_q_heads / c.hkv))
         return QW_T4_BLOCK ? turbo4_block(c, q, n_q_heads, n_rows, scale, causal, true, out, stream)
                            : turbo4_verify(c, q, n_q_heads, n_rows, scale, out, stream);
-    const int qrows = n_q_heads * n_rows;
     const float* tab = c.t4_tables;
 #if QW_T4_FUSED_DECODE
     if ((n_q_heads / c.hkv) * n_rows <= 16)
@@ -924,6 +941,20 @@ int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float
     if (QW_T4_BLOCK && ((n_q_heads / c.hkv) * n_rows <= kT4BlockRows ||
                         (n_q_heads / c.hkv) * n_rows >= block_image_min_rows(true)))
         return turbo4_block(c, q, n_q_heads, n_rows, scale, causal, false, out, stream);
+    return turbo4_expansion_route(c, q, n_q_heads, n_rows, scale, causal, nullptr, out, stream);
+}
+
+// The expansion route: q rotated into the K basis (fp16), the rotated K/V
+// expanded to fp16 rows once, attention over them in the rotated basis (the
+// fp16 cache's kernels, or with opts the general SDPA: mask, softcap,
+// window), and the output rotated back through the V basis
+// (attention_turbo4_dequant_sdpa, turbo/sparse_v.rs:1051-1072).
+static int turbo4_expansion_route(KVCache& c, const void* q, int n_q_heads, int n_rows,
+                                  float scale, bool causal, const SdpaOptions* opts, void* out,
+                                  hipStream_t stream) {
+    const int D = c.D, T = c.offset;
+    const int qrows = n_q_heads * n_rows;
+    const float* tab = c.t4_tables;
     const int capv = (T + 255) / 256 * 256;
     const size_t kv_bytes = (size_t)c.hkv * capv * D * sizeof(f16);
     const size_t q_bytes = (size_t)n_q_heads * n_rows * D * sizeof(f16);
@@ -942,34 +973,51 @@ int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float
         using TT = T4Tab<256>;
         hipLaunchKernelGGL(turbo4_rotate_kernel<256>, dim3((qrows + 3) / 4), dim3(256), 0, stream,
                            (const f16*)q, q_rot, qrows, tab + TT::k_s1, tab + TT::k_s2);
-        hipLaunchKernelGGL(turbo4_expand_kernel<256>, eg, dim3(256), 0, stream,
-                           (const uint8_t*)c.k_data, c.k_params, (const uint8_t*)c.v_data,
-                           c.v_params, tab, c.cap, T, capv, kw, vw);
+        if (opts)
+            hipLaunchKernelGGL((turbo4_expand_kernel<256, true>), eg, dim3(256), 0, stream,
+                               (const uint8_t*)c.k_data, c.k_params, (const uint8_t*)c.v_data,
+                               c.v_params, tab, c.cap, T, capv, kw, vw);
+        else
+            hipLaunchKernelGGL(turbo4_expand_kernel<256>, eg, dim3(256), 0, stream,
+                               (const uint8_t*)c.k_data, c.k_params, (const uint8_t*)c.v_data,
+                               c.v_params, tab, c.cap, T, capv, kw, vw);
     } else {
         using TT = T4Tab<128>;
         hipLaunchKernelGGL(turbo4_rotate_kernel<128>, dim3((qrows + 3) / 4), dim3(256), 0, stream,
                            (const f16*)q, q_rot, qrows, tab + TT::k_s1, tab + TT::k_s2);
-        hipLaunchKernelGGL(turbo4_expand_kernel<128>, eg, dim3(128), 0, stream,
-                           (const uint8_t*)c.k_data, c.k_params, (const uint8_t*)c.v_data,
-                           c.v_params, tab, c.cap, T, capv, kw, vw);
+        if (opts)
+            hipLaunchKernelGGL((turbo4_expand_kernel<128, true>), eg, dim3(128), 0, stream,
+                               (const uint8_t*)c.k_data, c.k_params, (const uint8_t*)c.v_data,
+                               c.v_params, tab, c.cap, T, capv, kw, vw);
+        else
+            hipLaunchKernelGGL(turbo4_expand_kernel<128>, eg, dim3(128), 0, stream,
+                               (const uint8_t*)c.k_data, c.k_params, (const uint8_t*)c.v_data,
+                               c.v_params, tab, c.cap, T, capv, kw, vw);
     }
     QW_HIP_CHECK(hipGetLastError());
-    // The rotated K/V seen as an fp16 cache (not owning its planes); it
-    // borrows the Turbo4 cache's split-K workspace.
-    KVCache view;
-    view.mode = QW_KV_FP16;
-    view.bits = 16;
-    view.D = D;
-    view.hkv = c.hkv;
-    view.device = c.device;
-    view.offset = T;
-    view.cap = capv;
-    view.k_data = kw;
-    view.v_data = vw;
-    view.fast_flag = c.fast_flag;
-    std::swap(view.ws, c.ws);
-    int rc = launch_attention(view, q_rot, n_q_heads, n_rows, scale, causal, o_rot, stream);
-    std::swap(view.ws, c.ws);
+    int rc;
+    if (opts) {
+        // rotated K and V rows, [hkv][capv][D]
+        rc = sdpa_general(q_rot, n_q_heads, n_rows, kw, vw, c.hkv, T, D, (int64_t)capv * D, D,
+                          (int64_t)capv * D, D, scale, *opts, o_rot, stream);
+    } else {
+        // The rotated K/V seen as an fp16 cache (not owning its planes); it
+        // borrows the Turbo4 cache's split-K workspace.
+        KVCache view;
+        view.mode = QW_KV_FP16;
+        view.bits = 16;
+        view.D = D;
+        view.hkv = c.hkv;
+        view.device = c.device;
+        view.offset = T;
+        view.cap = capv;
+        view.k_data = kw;
+        view.v_data = vw;
+        view.fast_flag = c.fast_flag;
+        std::swap(view.ws, c.ws);
+        rc = launch_attention(view, q_rot, n_q_heads, n_rows, scale, causal, o_rot, stream);
+        std::swap(view.ws, c.ws);
+    }
     if (rc) return rc;
     if (D == 256) {
         using TT = T4Tab<256>;

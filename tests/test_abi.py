@@ -103,3 +103,32 @@ def test_fused_rope_contract_fails_before_device_work(qwlib):
     assert call(seq=0) == 0  # nothing to do: no launch
     assert f(None, 1, 4, 8, 2, 128, 64, 10000.0, 1.0, 0, 0, 0, None, None, None, None) == 1
     assert qwlib.qw_kv_rope_update(None, one, 8, 4, 64, 0, 10000.0, 1.0, 0, one, None) == 1
+
+
+def test_general_attention_contract_fails_before_device_work(qwlib):
+    """qw_sdpa's argument contract (mask, softcap and window as the reference's
+    layers::attention / causal_attention take them), checked before any HIP
+    call."""
+    f = qwlib.qw_sdpa
+    one = ctypes.c_void_p(16)
+
+    def call(**kw):
+        a = dict(hq=8, L=4, hkv=2, T=100, D=128, causal=1, window=0, softcap=0.0, mask=None,
+                 md=0, mhs=0, mrs=100)
+        a.update(kw)
+        return f(one, a["hq"], a["L"], one, one, a["hkv"], a["T"], a["D"], a["T"] * a["D"],
+                 a["D"], a["T"] * a["D"], a["D"], 0.1, a["causal"], a["window"], a["softcap"],
+                 a["mask"], a["md"], a["mhs"], a["mrs"], one, None)
+
+    assert call(D=96) == 1
+    assert call(hq=9) == 1                     # not a multiple of the KV heads
+    assert call(T=3) == 1                      # causal with fewer keys than rows
+    assert call(causal=0, window=8) == 1       # a window is the windowed causal mask
+    assert b"window" in qwlib.qw_last_error()
+    assert call(softcap=-1.0) == 1
+    assert call(mask=one, md=7) == 1           # unknown mask dtype
+    assert call(mask=one, md=3, softcap=5.0) == 2  # bool mask with softcap
+    assert b"bool mask" in qwlib.qw_last_error()
+    assert call(mask=one, md=0, mrs=-1) == 1
+    assert f(None, 8, 4, one, one, 2, 100, 128, 0, 128, 0, 128, 0.1, 1, 0, 0.0, None, 0, 0, 0,
+             one, None) == 1

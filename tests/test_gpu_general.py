@@ -1,0 +1,194 @@
+"""GPU parity of the general attention options (qw_sdpa, qw_kv_attention_general,
+qw_kv_update_and_attention_general, through the C ABI) against
+oracle.sdpa_general: layers::attention's mask and softcap (layers.rs:4010),
+causal_attention's sliding window (lib.rs:3185), the masked cache route
+(update_and_fetch + attention, qwen3_next.rs:316-324) and the masked Turbo4
+route (update_and_turbo4_attention, cache.rs:3495 -> sparse_v.rs:1051-1072).
+
+Bar: 2e-3 max-abs and 1e-3 relative L2 (the attention tolerance); the cache
+routes are checked against the oracle fed the cache's own dequantized rows
+(whose bit-exactness the KV tests pin)."""
+import numpy as np
+import pytest
+
+import oracle
+from conftest import rng
+from test_gpu_kv import _gpu, _np, assert_close
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+
+def _mask(r, kind, hq, L, T):
+    """(numpy mask for the oracle, torch mask for the library)."""
+    if kind is None:
+        return None, None
+    if kind == "bool":
+        m = r.random((L, T)) < 0.7
+        m[:, 0] = True
+        return m, _gpu(m)
+    if kind == "f32":
+        m = (r.standard_normal((1, L, T)) * 2).astype(np.float32)
+        m[0, :, 1::7] = -np.inf
+        return m, _gpu(m)
+    if kind == "f16_heads":
+        m = (r.standard_normal((hq, L, T)) * 3).astype(np.float16)
+        return m, _gpu(m)
+    if kind == "bf16":
+        m = (r.standard_normal((L, T)) * 2).astype(np.float32)
+        t = _gpu(m).to(torch.bfloat16)
+        return t.float().cpu().numpy(), t  # the values the device holds
+    raise ValueError(kind)
+
+
+CASES = [
+    # hq, hkv, D, L, T, causal, window, softcap, mask
+    (24, 4, 256, 1, 3000, False, 0, 0.0, None),
+    (24, 4, 256, 5, 4100, True, 0, 0.0, "bool"),
+    (24, 4, 256, 16, 2049, True, 512, 0.0, None),
+    (8, 8, 128, 37, 700, True, 100, 30.0, None),
+    (16, 2, 64, 64, 900, False, 0, 50.0, "f32"),
+    (6, 1, 128, 3, 1000, False, 0, 0.0, "f16_heads"),
+    (24, 4, 256, 200, 1500, True, 0, 0.0, "bf16"),
+    (12, 4, 256, 1, 9000, True, 4096, 0.0, None),
+    (24, 4, 256, 2048, 2048, True, 0, 0.0, None),
+    (16, 2, 128, 2, 777, True, 0, 0.0, "bool"),      # 16 rows a KV head: one-wave launch
+    (4, 4, 64, 1, 50, False, 0, 5.0, "f32"),         # shorter than a tile
+]
+
+
+@pytest.mark.parametrize("hq,hkv,D,L,T,causal,window,softcap,mkind", CASES)
+def test_sdpa_matches_oracle(hq, hkv, D, L, T, causal, window, softcap, mkind):
+    import qw_amd
+
+    print(f"case hq={hq} hkv={hkv} D={D} L={L} T={T} causal={causal} window={window} "
+          f"softcap={softcap} mask={mkind}", flush=True)
+    r = rng(hq * 7 + D + L + T)
+    q = r.standard_normal((hq, L, D)).astype(np.float16)
+    k = r.standard_normal((hkv, T, D)).astype(np.float16)
+    v = r.standard_normal((hkv, T, D)).astype(np.float16)
+    m_np, m_t = _mask(r, mkind, hq, L, T)
+    # K/V as views of larger buffers (head and row strides of a cache)
+    kb = torch.zeros((hkv, T + 40, D + 64), dtype=torch.float16, device="cuda:0")
+    vb = torch.zeros_like(kb)
+    kb[:, :T, :D] = _gpu(k)
+    vb[:, :T, :D] = _gpu(v)
+    out = _np(qw_amd.attention(_gpu(q), kb[:, :T, :D], vb[:, :T, :D], D ** -0.5, m_t, softcap,
+                               window, causal))[0]
+    ref = oracle.sdpa_general(q, k, v, D ** -0.5, causal, window, softcap, m_np)
+    assert np.isfinite(out).all()
+    assert_close(out, ref, f"sdpa {mkind} sc={softcap} w={window}")
+
+
+def test_causal_attention_and_plain_route_agree():
+    """causal_attention with no softcap or window is the plain causal SDPA: the
+    general kernel within the bar of the fused fp16-cache kernel."""
+    import qw_amd
+
+    r = rng(77)
+    hq, hkv, D, L, T = 24, 4, 256, 4, 3000
+    q = r.standard_normal((hq, L, D)).astype(np.float16)
+    k = r.standard_normal((hkv, T, D)).astype(np.float16)
+    v = r.standard_normal((hkv, T, D)).astype(np.float16)
+    a = _np(qw_amd.causal_attention(_gpu(q), _gpu(k), _gpu(v), 1 / 16))[0]
+    cache = qw_amd.KVCache("fp16", hkv, D)
+    cache.update(_gpu(k), _gpu(v))
+    b = _np(cache.attention(_gpu(q), 1 / 16, causal=True))[0]
+    assert_close(a, b, "causal_attention vs fp16 cache")
+
+
+def test_rows_without_visible_keys_are_zero():
+    import qw_amd
+
+    r = rng(78)
+    hq, hkv, D, L, T = 4, 2, 128, 3, 500
+    q = r.standard_normal((hq, L, D)).astype(np.float16)
+    k = r.standard_normal((hkv, T, D)).astype(np.float16)
+    v = r.standard_normal((hkv, T, D)).astype(np.float16)
+    m = np.ones((L, T), bool)
+    m[1] = False
+    out = _np(qw_amd.attention(_gpu(q), _gpu(k), _gpu(v), 0.1, _gpu(m)))[0]
+    assert np.all(out[:, 1] == 0)
+    assert_close(out, oracle.sdpa_general(q, k, v, 0.1, mask=m), "empty row")
+
+
+@pytest.mark.parametrize("mode", ["affine4", "affine8", "int8", "fp16"])
+def test_cache_general_routes(mode):
+    import qw_amd
+
+    print(f"case cache {mode}", flush=True)
+    r = rng(80 + len(mode))
+    hq, hkv, D, T0, L = 24, 4, 256, 3000, 4
+    k = r.standard_normal((hkv, T0 + L, D)).astype(np.float16)
+    v = r.standard_normal((hkv, T0 + L, D)).astype(np.float16)
+    q = r.standard_normal((hq, L, D)).astype(np.float16)
+    cache = qw_amd.KVCache(mode, hkv, D)
+    cache.update(_gpu(k[:, :T0]), _gpu(v[:, :T0]))
+    m_np, m_t = _mask(r, "bool", hq, L, T0 + L)
+    # update_and_turbo4_attention(q, k, v, scale, mask) form
+    out = _np(cache.update_and_attention(_gpu(q), _gpu(k[:, T0:]), _gpu(v[:, T0:]), 1 / 16,
+                                         mask=m_t))[0]
+    assert cache.offset == T0 + L
+    kd, vd = (_np(x)[0] for x in cache.dequantize())
+    assert_close(out, oracle.sdpa_general(q, kd, vd, 1 / 16, mask=m_np), f"{mode} masked update")
+    # window and softcap over the cache as it is
+    out2 = _np(cache.attention_general(_gpu(q), 1 / 16, causal=True, window=300,
+                                       softcap=20.0))[0]
+    assert_close(out2, oracle.sdpa_general(q, kd, vd, 1 / 16, True, 300, 20.0),
+                 f"{mode} window+softcap")
+    # no options: the cache's own fused attention, exactly
+    np.testing.assert_array_equal(_np(cache.attention_general(_gpu(q), 1 / 16, causal=True))[0],
+                                  _np(cache.attention(_gpu(q), 1 / 16, causal=True))[0])
+
+
+def test_turbo4_masked_route():
+    """Turbo4 with a mask: q rotated into the K basis, the rotated expansion,
+    SDPA with the mask, the output rotated back (the reference's
+    attention_turbo4_dequant_sdpa with its mask argument)."""
+    import qw_amd
+
+    r = rng(90)
+    hq, hkv, D, T0, L = 24, 4, 256, 2500, 3
+    k = r.standard_normal((hkv, T0 + L, D)).astype(np.float16)
+    v = r.standard_normal((hkv, T0 + L, D)).astype(np.float16)
+    q = r.standard_normal((hq, L, D)).astype(np.float16)
+    cache = qw_amd.KVCache("turbo4", hkv, D)
+    cache.update(_gpu(k[:, :T0]), _gpu(v[:, :T0]))
+    m = (r.standard_normal((L, T0 + L)) * 2).astype(np.float16)
+    out = _np(cache.update_and_attention(_gpu(q), _gpu(k[:, T0:]), _gpu(v[:, T0:]), 1 / 16,
+                                         mask=_gpu(m)))[0]
+    t = cache.snapshot_tensors()
+    snap = {n: _np(x) for n, x in t.items()}
+    for n in ("k_rescale", "v_rescale"):
+        snap[n] = snap[n][..., 0]
+    tab = oracle.turbo4_tables(D)
+    q_rot = oracle.turbo4_rotate(q.astype(np.float64), tab["k_s1"], tab["k_s2"]).astype(np.float16)
+    k_rot = oracle.turbo4_expand_rotated(snap["k_packed"], snap["k_rescale"], tab)
+    v_rot = oracle.turbo4_expand_rotated(snap["v_packed"], snap["v_rescale"], tab)
+    o_rot = oracle.sdpa_general(q_rot, k_rot, v_rot, 1 / 16, mask=m)
+    ref = oracle.turbo4_rotate(o_rot.astype(np.float64), tab["v_s2"], tab["v_s1"]).astype(np.float16)
+    assert_close(out, ref, "turbo4 masked")
+
+
+def test_general_contract_errors():
+    import qw_amd
+
+    q = torch.zeros((4, 2, 128), dtype=torch.float16, device="cuda:0")
+    k = torch.zeros((2, 50, 128), dtype=torch.float16, device="cuda:0")
+    m = torch.ones((2, 50), dtype=torch.bool, device="cuda:0")
+    with pytest.raises(qw_amd.QwError) as e:  # bool mask with softcap
+        qw_amd.attention(q, k, k, 0.1, m, 10.0)
+    assert e.value.status == 2
+    with pytest.raises(qw_amd.QwError):  # a window needs causal
+        qw_amd.attention(q, k, k, 0.1, None, 0.0, 16, False)
+    with pytest.raises(qw_amd.QwError):  # mask shape
+        qw_amd.attention(q, k, k, 0.1, torch.ones((3, 50), dtype=torch.bool, device="cuda:0"))
+    with pytest.raises(qw_amd.QwError):  # head dim 96
+        qw_amd.attention(q[..., :96].contiguous(), k[..., :96].contiguous(),
+                         k[..., :96].contiguous(), 0.1)
+    # a rejected update leaves the cache as it was
+    cache = qw_amd.KVCache("affine4", 2, 128)
+    cache.update(k, k)
+    with pytest.raises(qw_amd.QwError):
+        cache.update_and_attention_general(q, k[:, :2], k[:, :2], 0.1, False, 8, 0.0, None)
+    assert cache.offset == 50
