@@ -306,19 +306,38 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
     // kernel does it, one wave a row) and staged as fp16 in the wave merge's
     // LDS area, which is free until the main loop ends.
     f16* const sm_qr = (f16*)sm_o;
+    int s = c + a.ns * wave;
+    Stage A, B;
     if constexpr (T4) {
+        // Every global read of the prologue (the wave's q rows, the lane's
+        // signs, a centroid pair a thread) is issued first and the first
+        // sub-chunk's loads right behind them, so their latencies overlap;
+        // the rotations and the table then wait for the prologue's reads only.
         constexpr int VPL = D / 64;
-        for (int b = threadIdx.x; b < 256; b += 64 * NW) {
-            const float* cb = a.t4_tab + T4Tab<D>::cb;
-            sm_t4[b] = float2{cb[b & 15], cb[b >> 4]};
-        }
-        for (int row = wave; row < a.R; row += NW) {
-            const f16* qrow = a.q + ((int64_t)(h * a.G + row % a.G) * a.Tq + row / a.G) * D;
-            float y[VPL];
-            f16 o[VPL];
+        static_assert(2 * NW >= 16 && 64 * NW >= 256, "two q rows a wave, a table entry a thread");
+        float yq[2][VPL];
 #pragma unroll
-            for (int j = 0; j < VPL; j++) y[j] = (float)qrow[lane * VPL + j];
-            t4_rotate_row<D>(y, lane, a.t4_tab + T4Tab<D>::k_s1, a.t4_tab + T4Tab<D>::k_s2, o);
+        for (int k = 0; k < 2; k++) {
+            const int row = wave + k * NW;
+            const int rr = row < a.R ? row : 0;
+            const f16* qrow = a.q + ((int64_t)(h * a.G + rr % a.G) * a.Tq + rr / a.G) * D;
+#pragma unroll
+            for (int j = 0; j < VPL; j++) yq[k][j] = (float)qrow[lane * VPL + j];
+        }
+        float si[VPL], so[VPL];
+        t4_lane_signs<D>(a.t4_tab + T4Tab<D>::k_s1, lane, si);
+        t4_lane_signs<D>(a.t4_tab + T4Tab<D>::k_s2, lane, so);
+        const int tb = threadIdx.x & 255;
+        const float* cb = a.t4_tab + T4Tab<D>::cb;
+        const float2 pair = float2{cb[tb & 15], cb[tb >> 4]};
+        load(A, s);
+        if (threadIdx.x < 256) sm_t4[threadIdx.x] = pair;
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int row = wave + k * NW;
+            if (row >= a.R) break;
+            f16 o[VPL];
+            t4_rotate_row<D>(yq[k], lane, si, so, o);
 #pragma unroll
             for (int j = 0; j < VPL; j++) sm_qr[row * D + lane * VPL + j] = o[j];
         }
@@ -343,12 +362,11 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
             base = 32 * m + 8 * g;
         x = *(const half8*)(qrow + base);
     }
-    int s = c + a.ns * wave;
-    Stage A, B;
     // The first sub-chunk's loads go out right behind Q (loads return in
     // issue order, so the Q conversion below waits for Q only: the Q barrier
-    // holds every wave of the workgroup until the last one's q is in).
-    load(A, s);
+    // holds every wave of the workgroup until the last one's q is in);
+    // Turbo4 issued them in its prologue above.
+    if constexpr (!T4) load(A, s);
     {
         // q' = f16(f16(scale) * q): one packed fp16 multiply rounds exactly
         // like MLX's fp16 `multiply`. Padding rows get scale 0.
