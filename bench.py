@@ -797,8 +797,7 @@ def pmc_workload(cfg: str) -> int:
 PMC_CALLS = {"c2": LAYERS, "c3": 4, "c4": LAYERS, "c5": LAYERS, "gemm": 3}
 # the kernels a call of the configuration launches (set-up appends excluded)
 PMC_KERNELS = ("attend_decode_kernel", "attend_block_kernel", "decode_merge_kernel",
-               "merge_rows_kernel", "merge_rows_vec_kernel", "t4_merge_rotate_kernel",
-               "dlsa_kernel", "dlsa_merge_kernel")
+               "merge_rows_", "t4_merge_rotate_kernel", "dlsa_kernel", "dlsa_merge_kernel")
 N_XCD, N_SIMD = 8, 1024  # MI355X: 8 XCDs, 256 CUs x 4 SIMDs
 
 
