@@ -92,13 +92,17 @@ constexpr int decode_waves() {
 constexpr int kBufWord3 = 0x00020000;
 
 // Cache policy of the decode kernel's K/V loads (the instruction's sc0 / nt /
-// sc1 bits: 1, 2, 16). Non-temporal (2): the streamed cache leaves the L2 and
-// the MALL to what is reused (code, arguments, q, partials); config 2's layer
-// call measured 16.67 -> 16.10 us against the default policy.
-#ifndef QW_DECODE_KV_AUX
-#define QW_DECODE_KV_AUX 2
+// sc1 bits: 1, 2, 16). Non-temporal (2) when a call reads at least
+// QW_DECODE_NT_MIN_MB of cache: the streamed cache then leaves the L2 and the
+// MALL to what is reused (code, arguments, q, partials); a whole layer stack
+// of such calls cannot stay in the 256 MB MALL anyway. Smaller calls keep the
+// default policy, so a stack of short caches can stay resident there. A/B in
+// one run: config 2 (37.8 MB) 15.9 -> 15.3 us and Int8 at its geometry 21.5
+// -> 20.7 us with nt; config 1 (8.9 MB, sixteen caches that fit the MALL)
+// 11.4 us without against 12.4 us with.
+#ifndef QW_DECODE_NT_MIN_MB
+#define QW_DECODE_NT_MIN_MB 16
 #endif
-constexpr int kKvAux = QW_DECODE_KV_AUX;
 
 // Register stages a wave streams through (1: load the next sub-chunk after
 // the current one's math; 2: wait-then-prefetch ping-pong, a stage's
@@ -147,7 +151,7 @@ __device__ __forceinline__ half8 t4_expand8(uint32_t w, float r, const float2* p
 // DPL r16 .. +DPL - 1 of keys 8g .. 8g+7 (16 lanes cover a row's D/2 bytes).
 // The centroid comes from a register table (lane i holds centroid i % 16)
 // through ds_bpermute.
-template <int BITS, int D, int NW, bool FAST, bool T4 = false>
+template <int BITS, int D, int NW, bool FAST, bool T4 = false, int AUX = 0>
 __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)[NW], float* sm_o,
                                             half8 (*sm_q)[64], float2* sm_t4 = nullptr) {
     using S = DecodeShape<BITS, D>;
@@ -219,7 +223,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
             for (int cc = 0; cc < KL; cc++)
                 st.kc[tile][cc] = __builtin_bit_cast(
                     u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                               rk, off_k + tile * 4 * KRB + (T4 ? 16 : 64) * cc, 32 * si * KRB, kKvAux));
+                               rk, off_k + tile * 4 * KRB + (T4 ? 16 : 64) * cc, 32 * si * KRB, AUX));
         }
         if constexpr (T4) {
             const __amdgpu_buffer_rsrc_t rkp =
@@ -227,7 +231,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
 #pragma unroll
             for (int tile = 0; tile < 2; tile++)
                 st.kp[tile] = u32x4{__builtin_amdgcn_raw_buffer_load_b32(rkp, off_kp + tile * 4 * KPB,
-                                                                         32 * si * KPB, kKvAux),
+                                                                         32 * si * KPB, AUX),
                                     0u, 0u, 0u};
         }
         if constexpr (AFF) {
@@ -237,16 +241,16 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
             for (int tile = 0; tile < 2; tile++) {
                 const int o = off_kp + tile * 4 * KPB;
                 if constexpr (BITS == 4 && NG == 4) {
-                    const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(rkp, o, 32 * si * KPB, kKvAux);
+                    const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(rkp, o, 32 * si * KPB, AUX);
                     st.kp[tile] = u32x4{t2[0], t2[1], 0u, 0u};
                 } else if constexpr (BITS == 4) {
-                    st.kp[tile] = u32x4{__builtin_amdgcn_raw_buffer_load_b32(rkp, o, 32 * si * KPB, kKvAux),
+                    st.kp[tile] = u32x4{__builtin_amdgcn_raw_buffer_load_b32(rkp, o, 32 * si * KPB, AUX),
                                         0u, 0u, 0u};
                 } else if constexpr (NG == 4) {
                     st.kp[tile] = __builtin_bit_cast(
-                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rkp, o, 32 * si * KPB, kKvAux));
+                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(rkp, o, 32 * si * KPB, AUX));
                 } else {
-                    const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(rkp, o, 32 * si * KPB, kKvAux);
+                    const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(rkp, o, 32 * si * KPB, AUX);
                     st.kp[tile] = u32x4{t2[0], t2[1], 0u, 0u};
                 }
             }
@@ -262,32 +266,32 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 if constexpr (D == 256) {
-                    const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(rv, off_v + j * KRB, 4 * si * VBB, kKvAux);
+                    const auto t2 = __builtin_amdgcn_raw_buffer_load_b64(rv, off_v + j * KRB, 4 * si * VBB, AUX);
                     st.vc[j / 2][2 * (j % 2)] = t2[0];
                     st.vc[j / 2][2 * (j % 2) + 1] = t2[1];
                 } else {
-                    st.vc[j / 4][j % 4] = __builtin_amdgcn_raw_buffer_load_b32(rv, off_v + j * KRB, 4 * si * VBB, kKvAux);
+                    st.vc[j / 4][j % 4] = __builtin_amdgcn_raw_buffer_load_b32(rv, off_v + j * KRB, 4 * si * VBB, AUX);
                 }
             }
             const __amdgpu_buffer_rsrc_t rvp =
                 __builtin_amdgcn_make_buffer_rsrc((void*)vpbase, 0, ok ? a.cap / 8 * VPB : 0, kBufWord3);
             st.vp[0] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rvp, off_vp, 4 * si * VPB, kKvAux));
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rvp, off_vp, 4 * si * VPB, AUX));
             st.vp[1] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rvp, off_vp + 16, 4 * si * VPB, kKvAux));
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rvp, off_vp + 16, 4 * si * VPB, AUX));
         } else {
 #pragma unroll
             for (int jj = 0; jj < VL; jj++)
                 st.vc[jj] = __builtin_bit_cast(
-                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, off_v + 256 * jj, 4 * si * VBB, kKvAux));
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, off_v + 256 * jj, 4 * si * VBB, AUX));
         }
         if constexpr (AFF) {
             const __amdgpu_buffer_rsrc_t rvp =
                 __builtin_amdgcn_make_buffer_rsrc((void*)vpbase, 0, ok ? a.cap / 8 * VPB : 0, kBufWord3);
             st.vp[0] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rvp, off_vp, 4 * si * VPB, kKvAux));
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rvp, off_vp, 4 * si * VPB, AUX));
             st.vp[1] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rvp, off_vp + 16, 4 * si * VPB, kKvAux));
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rvp, off_vp + 16, 4 * si * VPB, AUX));
         }
     };
     auto load = [&](Stage& st, int s) {
@@ -819,10 +823,11 @@ __device__ void decode_append_unit(const DecodeArgs& a, char* lds) {
     }
 }
 
-template <int BITS, int D, bool T4 = false, bool APP = false>
+template <int BITS, int D, bool T4 = false, bool APP = false, bool NT = false>
 __global__ __launch_bounds__((64 * decode_waves<BITS, D>()), 1) void attend_decode_kernel(
     DecodeArgs a) {
     constexpr int NW = decode_waves<BITS, D>();
+    constexpr int AUX = NT ? 2 : 0;  // the K/V loads' cache policy
     __shared__ __attribute__((aligned(16))) float2 sm_ml[16][NW];
     __shared__ half8 sm_q[D / 32][64];
     __shared__ float2 sm_t4[T4 ? 256 : 1];  // Turbo4 centroid-pair table
@@ -843,13 +848,13 @@ __global__ __launch_bounds__((64 * decode_waves<BITS, D>()), 1) void attend_deco
         }
     }
     if (!T4 && (BITS == 16 || a.fast_flag != nullptr)) {
-        decode_body<BITS, D, NW, true>(a, sm_ml, sm_o, sm_q);
+        decode_body<BITS, D, NW, true, false, AUX>(a, sm_ml, sm_o, sm_q);
         if (BITS != 16 && *a.fast_flag == 0) {
             __syncthreads();
-            decode_body<BITS, D, NW, false>(a, sm_ml, sm_o, sm_q);
+            decode_body<BITS, D, NW, false, false, AUX>(a, sm_ml, sm_o, sm_q);
         }
     } else {
-        decode_body<BITS, D, NW, false, T4>(a, sm_ml, sm_o, sm_q, sm_t4);
+        decode_body<BITS, D, NW, false, T4, AUX>(a, sm_ml, sm_o, sm_q, sm_t4);
     }
 }
 
@@ -995,18 +1000,24 @@ static int launch_decode_partials(KVCache& cc, const f16* q, int G, int Tq, int 
     // float4, factors 4 x NW float4
     size_t shmem = (size_t)NW * ((a.R + 3) / 4) * (D + 16) * 16 + 4 * NW * 16;
     // Dynamic LDS above 64 KB must be allowed per kernel and device.
+    // KV bytes the call reads: K and V codes plus their params, a key and head
+    constexpr int kKeyBytes = 2 * (D * BITS / 8) + (T4 ? 8 : BITS == 16 ? 0 : 2 * (D / 64) * 4);
+    const bool nt = (size_t)cc.hkv * T * kKeyBytes >= ((size_t)QW_DECODE_NT_MIN_MB << 20);
+    auto go = [&](auto kernel) -> int {
+        int rc1 = ensure_dynamic_lds((const void*)kernel, shmem);
+        if (rc1) return rc1;
+        hipLaunchKernelGGL(kernel, dim3(nc, cc.hkv), dim3(64 * NW), shmem, stream, a);
+        return QW_OK;
+    };
     if (app) {
         shmem = std::max(shmem, decode_append_lds<D>(app_L));
-        rc = ensure_dynamic_lds((const void*)attend_decode_kernel<BITS, D, T4, true>, shmem);
-        if (rc) return rc;
-        hipLaunchKernelGGL((attend_decode_kernel<BITS, D, T4, true>), dim3(nc, cc.hkv), dim3(64 * NW),
-                           shmem, stream, a);
+        rc = nt ? go(attend_decode_kernel<BITS, D, T4, true, true>)
+                : go(attend_decode_kernel<BITS, D, T4, true, false>);
     } else {
-        rc = ensure_dynamic_lds((const void*)attend_decode_kernel<BITS, D, T4>, shmem);
-        if (rc) return rc;
-        hipLaunchKernelGGL((attend_decode_kernel<BITS, D, T4>), dim3(nc, cc.hkv), dim3(64 * NW),
-                           shmem, stream, a);
+        rc = nt ? go(attend_decode_kernel<BITS, D, T4, false, true>)
+                : go(attend_decode_kernel<BITS, D, T4, false, false>);
     }
+    if (rc) return rc;
     QW_HIP_CHECK(hipGetLastError());
     *nc_out = nc;
     *po = a.part_o;
