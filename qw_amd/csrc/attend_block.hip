@@ -790,15 +790,34 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     }
     if constexpr (PM == 2) {
         // tile t's image into buffer b: 1 KB a wave instruction (lane i its
-        // 16 bytes at the wave-uniform LDS address + 16 i; the compiler sets
-        // M0 and its wait state); waited for before the barrier.
+        // 16 bytes at the wave-uniform LDS address + 16 i, which the
+        // instruction takes from M0); waited for before the barrier.
+        // Issued from asm that saves M0 first and restores it after (each
+        // write followed by one wait state), so the compiler's view of M0
+        // holds across it. The compiler builtin for this copy
+        // (__builtin_amdgcn_global_load_lds) compiles the same instruction,
+        // but around it the tile's LDS reads lose their lookahead (21
+        // lgkmcnt(0) waits in the kernel against 7, and 4 lgkmcnt(3) against
+        // 63): config 3 827 us against 819 us here (A/B in one run; 814 us
+        // with an asm that clobbers M0 without restoring it).
         const char* img0 = a.img + (int64_t)h * a.img_tiles * BUF;
+        const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds;
         auto dma = [&](int t, int b) {
             const char* src = img0 + (int64_t)t * BUF + 16 * lane;
-            for (int c = wave; c < BUF / 1024; c += NW)
-                __builtin_amdgcn_global_load_lds(
-                    (const void*)(src + 1024 * c),
-                    (__attribute__((address_space(3))) void*)(lds + BUF * b + 1024 * c), 16, 0, 0);
+            for (int c = wave; c < BUF / 1024; c += NW) {
+                uint32_t saved;
+                asm volatile(
+                    "s_mov_b32 %0, m0\n\t"
+                    "s_mov_b32 m0, %2\n\t"
+                    "s_nop 0\n\t"
+                    "global_load_lds_dwordx4 %1, off\n\t"
+                    "s_nop 0\n\t"
+                    "s_mov_b32 m0, %0"
+                    : "=&s"(saved)
+                    : "v"(src + 1024 * c),
+                      "s"(__builtin_amdgcn_readfirstlane(lds0 + BUF * b + 1024 * c))
+                    : "memory");
+            }
         };
         static_assert(BUF % 1024 == 0, "a tile buffer is whole 1 KB DMA instructions");
         if (t0 < t1) dma(t0, 0);
