@@ -199,6 +199,31 @@ def test_update_and_attention_vs_oracle(oracle_lib, bits, T_prefix, L, causal):
     assert_as_exact_as_reference(out, ref, f64, f"bits={bits} T={T_prefix}+{L}")
 
 
+@pytest.mark.parametrize("bits,T", [(4, 32769), (8, 4096)])
+def test_headline_call_vs_oracle(oracle_lib, bits, T):
+    """The call the headline roofline times, qw_kv_attention over a cache that
+    already holds every key (the decode kernel without its append unit, with
+    non-temporal loads at config 2's 37.8 MB), against the oracle at config 2
+    (and config 1) size."""
+    import qw_amd
+
+    r = rng(300 + bits)
+    hq, hkv, D = 24, 4, 256
+    k, v = _kv(r, hkv, T, D)
+    q = r.standard_normal((hq, 1, D)).astype(np.float16)
+    cache = qw_amd.KVCache(_mode(bits), hkv, D)
+    cache.update(_gpu(k)[None], _gpu(v)[None])
+    out = _np(cache.attention(_gpu(q)[None], 1.0 / 16))[0]
+    orc = oracle_lib.AffineCacheOracle(hkv, D, T, bits)
+    orc.update(k, v)
+    kd, vd = orc.fetch()
+    ref = oracle_lib.sdpa_mlx_f16(q, kd, vd, 1.0 / 16)
+    f64 = oracle_lib.sdpa_f64(q, kd, vd, 1.0 / 16)
+    assert np.isfinite(out).all()
+    assert_close(out, ref, f"headline call bits={bits} T={T} vs oracle")
+    assert_as_exact_as_reference(out, ref, f64, f"headline call bits={bits} T={T}")
+
+
 # The served verify blocks (MTP / DFlash2: 3..5 draft rows, the reference's
 # fused-pass sizes, turbo4_attention.cpp:360, fused_attention.rs:70-100) on the
 # affine codec at the config geometry: 18..30 rows a KV head (the block
