@@ -159,10 +159,12 @@ struct DeviceGuard {
 };
 
 // Turbo4 attention (turbo4.hip): q rotated into the K basis, attention in the
-// rotated basis, the output rotated back. Up to 16 rows a KV head the decode
-// kernel reads the packed indices in place; causal blocks of 1-5 rows past
-// 2048 tokens take the fused verify pass; anything else expands the rotated
-// K/V to fp16 for the fp16 kernels.
+// rotated basis, the output rotated back. Causal blocks of 1-5 rows past 2048
+// tokens with at most 32 query heads a KV head take the fused verify pass (in
+// the block kernel); other calls of up to 16 rows a KV head the decode kernel
+// reads from the packed indices in place, up to 1024 the block kernel, and
+// from block_image_min_rows(true) on the block kernel's tile images; the rest
+// expand the rotated K/V to fp16 for the fp16 kernels.
 int turbo4_attention(KVCache& c, const void* q, int n_q_heads, int n_rows, float scale,
                      bool causal, void* out, hipStream_t stream);
 
