@@ -236,3 +236,44 @@ def test_graph_tile_image_route(mode, L):
     del g
     c.close()
     big_c.close()
+
+
+def test_graph_general_options_replay():
+    """The general options captured in a graph: a masked SDPA over K/V views,
+    a softcap-and-window call, and a masked call over an affine cache (its
+    rows dequantized into the stream's workspace inside the graph); every
+    replay equals the eager output, with eager work between replays."""
+    import qw_amd
+
+    r = rng(13)
+    H, G, D, T, L = 4, 6, 256, 3000, 5
+    k = _gpu(r.standard_normal((H, T, D)).astype(np.float16))
+    v = _gpu(r.standard_normal((H, T, D)).astype(np.float16))
+    q = _gpu(r.standard_normal((H * G, L, D)).astype(np.float16))
+    m = _gpu(r.random((L, T)) < 0.6)
+    madd = _gpu((r.standard_normal((L, T)) * 2).astype(np.float16))
+    c = _cache("affine4", r, H, T, D)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+
+    def calls():
+        return (qw_amd.attention(q, k, v, 1 / 16, m),
+                qw_amd.causal_attention(q, k, v, 1 / 16, 30.0, 700),
+                c.attention_general(q, 1 / 16, mask=madd))
+
+    with torch.cuda.stream(s):  # size the stream's workspaces first
+        want = [_np(x) for x in calls()]
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        outs = calls()
+    for rep in range(3):
+        for o in outs:
+            o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, w in zip(outs, want):
+            np.testing.assert_array_equal(_np(o), w, err_msg=f"replay {rep}")
+        _ = (q.float() * 3).sum().item()  # eager work between replays
+    del g
+    c.close()
