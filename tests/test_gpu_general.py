@@ -192,3 +192,61 @@ def test_general_contract_errors():
     with pytest.raises(qw_amd.QwError):
         cache.update_and_attention_general(q, k[:, :2], k[:, :2], 0.1, False, 8, 0.0, None)
     assert cache.offset == 50
+
+
+def _torch_fp32_attention(q, k, v, scale, causal, window, softcap, mask):
+    """Plain PyTorch fp32 attention of the same op (on the CPU): no fp16
+    roundings of the scores or probabilities."""
+    qf, kf, vf = (torch.from_numpy(np.asarray(x, np.float32)) for x in (q, k, v))
+    hq, L, D = qf.shape
+    hkv, T, _ = kf.shape
+    G = hq // hkv
+    kf = kf.repeat_interleave(G, dim=0)
+    vf = vf.repeat_interleave(G, dim=0)
+    s = torch.matmul(qf, kf.transpose(1, 2).contiguous()) * scale
+    if softcap > 0:
+        s = torch.tanh(s / softcap) * softcap
+    t = torch.arange(T)[None, :]
+    p = (T - L + torch.arange(L))[:, None]
+    vis = torch.ones((L, T), dtype=torch.bool)
+    if causal:
+        vis &= t <= p
+    if window > 0:
+        vis &= t >= p - window + 1
+    vis = vis[None].expand(hq, L, T).clone()
+    if mask is not None:
+        m = torch.from_numpy(np.ascontiguousarray(mask))
+        m = m.reshape(-1, L, T).expand(hq, L, T)
+        if m.dtype == torch.bool:
+            vis &= m
+        else:
+            s = s + m.float()
+    s = s.masked_fill(~vis, float("-inf"))
+    return torch.matmul(torch.softmax(s, dim=-1), vf).numpy()
+
+
+@pytest.mark.parametrize("causal,window,softcap,mkind", [
+    (True, 0, 0.0, None), (True, 300, 0.0, "bool"), (False, 0, 25.0, "f32"), (True, 0, 40.0, None)])
+def test_sdpa_against_torch_fp32(causal, window, softcap, mkind):
+    """An independent check of the general kernel: PyTorch fp32 attention of
+    the same op, which skips MLX's fp16 roundings of S (and of P without
+    softcap), so the bar is the fp16 budget those roundings leave: 5e-3
+    max-abs, 3e-3 relative L2."""
+    import qw_amd
+
+    r = rng(501 + int(softcap) + window)
+    hq, hkv, D, L, T = 12, 2, 128, 6, 1500
+    q = r.standard_normal((hq, L, D)).astype(np.float16)
+    k = r.standard_normal((hkv, T, D)).astype(np.float16)
+    v = r.standard_normal((hkv, T, D)).astype(np.float16)
+    m_np, m_t = _mask(r, mkind, hq, L, T)
+    if m_np is not None and m_np.dtype != np.bool_:
+        m_np = m_np.astype(np.float16).astype(np.float32)  # the cast the reference applies
+    out = _np(qw_amd.attention(_gpu(q), _gpu(k), _gpu(v), D ** -0.5, m_t, softcap, window,
+                               causal))[0].astype(np.float64)
+    ref = _torch_fp32_attention(q, k, v, D ** -0.5, causal, window, softcap, m_np)
+    err = np.abs(out - ref)
+    rel = np.linalg.norm(out - ref) / np.linalg.norm(ref)
+    print(f"torch fp32 {mkind} sc={softcap} w={window}: max_abs={err.max():.3e} rel_l2={rel:.3e}",
+          flush=True)
+    assert err.max() < 5e-3 and rel < 3e-3
