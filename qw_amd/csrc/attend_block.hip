@@ -134,7 +134,8 @@ constexpr bool kPart16 = QW_BLOCK_PART16;
 // Wave priority raised over the MFMA phases of a tile (QK and P.V), so a
 // SIMD's waves drift apart and one wave's softmax and dequant VALU issue under
 // another's MFMAs: 0 never, 1 the launches that dequantize in the loop, 2
-// every launch. Measured (A/B in one run): served 4- and 5-row verify blocks
+// every launch (the fused Turbo4 pass never: 39.25 against 39.39 us at 4 rows
+// @ 32k). Measured (A/B in one run): served 4- and 5-row verify blocks
 // -0.15 to -0.35 us, config 4 unchanged, the image launches of config 3
 // +0.5 % (their three waves a SIMD already overlap).
 #ifndef QW_BLOCK_SETPRIO
@@ -586,7 +587,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
             for (int tt = 0; tt < 2; tt++)
 #pragma unroll
                 for (int rt = 0; rt < RT; rt++) acc[u][tt][rt] = float4v{0.f, 0.f, 0.f, 0.f};
-        if constexpr (kSetprio(PM)) __builtin_amdgcn_s_setprio(1);
+        if constexpr (kSetprio(PM) && !FUSED) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int m = 0; m < NM; m++) {
 #pragma unroll
@@ -612,7 +613,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
             __builtin_amdgcn_sched_group_barrier(0x008, AH, 0);
         }
 #endif
-        if constexpr (kSetprio(PM)) __builtin_amdgcn_s_setprio(0);
+        if constexpr (kSetprio(PM) && !FUSED) __builtin_amdgcn_s_setprio(0);
         half8 pop[NSUB][RT];
         // Scores -> fp16 rounding -> (mask) -> online softmax -> P; the mask
         // only for tiles some row of the wave cannot fully see (a scalar
@@ -745,7 +746,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
             softmax();
         // O += P . V: B = slot 16mm + r16 (column r16 of output tile mm) of
         // V block 4u + g, i.e. keys 32u + 8g .. +7.
-        if constexpr (kSetprio(PM)) __builtin_amdgcn_s_setprio(1);
+        if constexpr (kSetprio(PM) && !FUSED) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int u = 0; u < NSUB; u++) {
             const half8* vb8 = sV8 + (4 * u + g) * VROW + r16;
@@ -774,7 +775,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
             __builtin_amdgcn_sched_group_barrier(0x008, AH, 1);
         }
 #endif
-        if constexpr (kSetprio(PM)) __builtin_amdgcn_s_setprio(0);
+        if constexpr (kSetprio(PM) && !FUSED) __builtin_amdgcn_s_setprio(0);
     };
 
     if constexpr (PM == 1) {
