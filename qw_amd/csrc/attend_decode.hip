@@ -1050,12 +1050,19 @@ __global__ __launch_bounds__(D * 4) void t4_merge_rotate_kernel(const float* __r
                                                               int slot_bits,
                                                               const float* __restrict__ tab,
                                                               f16* __restrict__ out) {
-    constexpr int NDG = D / 64;
     const int row = blockIdx.x, h = blockIdx.y;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int pg = wave & 3, sd = 64 * (wave >> 2) + lane;
     const int d = slot_bits ? v_logical_dim(sd, D, slot_bits) : sd;
     const int64_t base = (int64_t)h * nc * rstride + row;
+    // the rotation's signs (wave 0 rotates the merged row): loaded with the
+    // partials, so no memory round trip follows the merge
+    constexpr int VPL = D / 64;
+    float s_in[VPL], s_out[VPL];
+    if (wave == 0) {
+        t4_lane_signs<D>(tab + T4Tab<D>::v_s2, lane, s_in);
+        t4_lane_signs<D>(tab + T4Tab<D>::v_s1, lane, s_out);
+    }
     float v[PER];
     float2 ml[PER];
 #pragma unroll
@@ -1069,15 +1076,12 @@ __global__ __launch_bounds__(D * 4) void t4_merge_rotate_kernel(const float* __r
             v[i] = 0.0f;
         }
     }
+    // each partial group pg reduces against its own maximum; wave 0 then
+    // combines the four groups for the lane's D/64 dims (the rotation's
+    // layout), so one barrier separates the loads from the rotation
     float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < PER; i++) m = fmaxf(m, ml[i].x);
-    __shared__ float sm_m[4];
-    __shared__ float sm[2][4][D];
-    __shared__ std::conditional_t<KEEP32, float, f16> sm_y[D];
-    if (wave < 4 && lane == 0) sm_m[pg] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(sm_m[0], sm_m[1]), fmaxf(sm_m[2], sm_m[3]));
     float o = 0.0f, l = 0.0f;
 #pragma unroll
     for (int i = 0; i < PER; i++) {
@@ -1085,32 +1089,40 @@ __global__ __launch_bounds__(D * 4) void t4_merge_rotate_kernel(const float* __r
         o = __builtin_fmaf(w, v[i], o);
         l = __builtin_fmaf(w, ml[i].y, l);
     }
-    sm[0][pg][d] = o;
-    sm[1][pg][d] = l;
-    __syncthreads();
-    if (pg == 0) {
-        const float O = (sm[0][0][d] + sm[0][1][d]) + (sm[0][2][d] + sm[0][3][d]);
-        const float L = (sm[1][0][d] + sm[1][1][d]) + (sm[1][2][d] + sm[1][3][d]);
-        const float y = L > 0.0f ? O / L : 0.0f;
-        if constexpr (KEEP32)
-            sm_y[d] = y;
-        else
-            sm_y[d] = (f16)y;
-    }
+    __shared__ float2 sm_ml[4];
+    __shared__ float sm_o[4][D];
+    if (wave < 4 && lane == 0) sm_ml[pg] = float2{m, l};
+    sm_o[pg][d] = o;
     __syncthreads();
     if (wave == 0) {
-        constexpr int VPL = D / 64;
+        float M = -INFINITY;
+#pragma unroll
+        for (int p = 0; p < 4; p++) M = fmaxf(M, sm_ml[p].x);
+        float f[4], L = 0.0f;
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const float2 gl = sm_ml[p];
+            f[p] = gl.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((gl.x - M) * kLog2e);
+            L = __builtin_fmaf(f[p], gl.y, L);
+        }
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
         float y[VPL];
         f16 r[VPL];
 #pragma unroll
-        for (int j = 0; j < VPL; j++) y[j] = (float)sm_y[lane * VPL + j];
-        t4_rotate_row<D>(y, lane, tab + T4Tab<D>::v_s2, tab + T4Tab<D>::v_s1, r);
+        for (int j = 0; j < VPL; j++) {
+            const int dd = lane * VPL + j;
+            float O = 0.0f;
+#pragma unroll
+            for (int p = 0; p < 4; p++) O = __builtin_fmaf(f[p], sm_o[p][dd], O);
+            const float yy = L > 0.0f ? O * inv : 0.0f;
+            y[j] = KEEP32 ? yy : (float)(f16)yy;
+        }
+        t4_rotate_row<D>(y, lane, s_in, s_out, r);
         const int qh = h * G + row % G, qr = row / G;
         f16* orow = out + ((int64_t)qh * Tq + qr) * D;
 #pragma unroll
         for (int j = 0; j < VPL; j++) orow[lane * VPL + j] = r[j];
     }
-    (void)NDG;
 }
 
 template <int D, bool KEEP32>
