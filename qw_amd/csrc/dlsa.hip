@@ -609,9 +609,11 @@ __global__ __launch_bounds__(256, 2) void dlsa_kernel(DlsaArgs a, Src src, const
 
 // out[qh, r] = sum_p e^(m_p - M) O_p / sum_p e^(m_p - M) l_p (m in the log2 domain).
 // grid (q heads, rows, D/64), 4 waves: lane = dim, wave w sums parts w, w+4, ...
-// with every load issued before the first use (one memory round trip).
+// (at most PER of them) with every load issued before the first use (one
+// memory round trip).
 constexpr int kDlsaMaxParts = 128;
 
+template <int PER>
 __global__ __launch_bounds__(256) void dlsa_merge_kernel(const float* __restrict__ part_o,
                                                          const float2* __restrict__ part_ml,
                                                          int parts, int D, int L, int hq,
@@ -619,7 +621,6 @@ __global__ __launch_bounds__(256) void dlsa_merge_kernel(const float* __restrict
     const int qh = blockIdx.x, r = blockIdx.y, d = blockIdx.z * 64 + (threadIdx.x & 63);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t base = ((int64_t)r * hq + qh) * parts;
-    constexpr int PER = kDlsaMaxParts / 4;
     float v[PER];
     float2 ml[PER];
 #pragma unroll
@@ -633,14 +634,11 @@ __global__ __launch_bounds__(256) void dlsa_merge_kernel(const float* __restrict
             v[i] = 0.0f;
         }
     }
+    // each wave reduces its parts against its own maximum (log2 units); the
+    // four (m, l, O) meet in LDS behind one barrier
     float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < PER; i++) m = fmaxf(m, ml[i].x);
-    __shared__ float sm_m[4];
-    __shared__ float sm[2][4][64];
-    if (lane == 0) sm_m[wave] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(sm_m[0], sm_m[1]), fmaxf(sm_m[2], sm_m[3]));
     float o = 0.0f, l = 0.0f;
 #pragma unroll
     for (int i = 0; i < PER; i++) {
@@ -648,12 +646,23 @@ __global__ __launch_bounds__(256) void dlsa_merge_kernel(const float* __restrict
         o = __builtin_fmaf(f, v[i], o);
         l = __builtin_fmaf(f, ml[i].y, l);
     }
-    sm[0][wave][lane] = o;
-    sm[1][wave][lane] = l;
+    __shared__ float2 sm_ml[4];
+    __shared__ float sm_o[4][64];
+    if (lane == 0) sm_ml[wave] = float2{m, l};
+    sm_o[wave][lane] = o;
     __syncthreads();
     if (wave == 0) {
-        const float O = (sm[0][0][lane] + sm[0][1][lane]) + (sm[0][2][lane] + sm[0][3][lane]);
-        const float Ls = (sm[1][0][lane] + sm[1][1][lane]) + (sm[1][2][lane] + sm[1][3][lane]);
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; w++) M = fmaxf(M, sm_ml[w].x);
+        float O = 0.0f, Ls = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const float2 gl = sm_ml[w];
+            const float f = gl.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(gl.x - M);
+            O = __builtin_fmaf(f, sm_o[w][lane], O);
+            Ls = __builtin_fmaf(f, gl.y, Ls);
+        }
         out[((int64_t)qh * L + r) * D + d] = (f16)(Ls > 0.0f ? O / Ls : 0.0f);
     }
 }
@@ -826,9 +835,20 @@ static int dlsa_sparse_attention_impl(const void* q, const DlsaSource& src,
     }
     QW_HIP_CHECK(hipGetLastError());
     if (parts > 1) {
-        hipLaunchKernelGGL(dlsa_merge_kernel, dim3(n_q_heads, n_rows, head_dim / 64), dim3(256), 0,
-                           stream, a.part_o, a.part_ml, parts, head_dim, n_rows, n_q_heads,
-                           (f16*)out);
+        // parts a wave sums, rounded up to a power of two (parts <= kDlsaMaxParts)
+        const dim3 mg(n_q_heads, n_rows, head_dim / 64);
+        auto merge = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, mg, dim3(256), 0, stream, a.part_o, a.part_ml, parts, head_dim,
+                               n_rows, n_q_heads, (f16*)out);
+        };
+        if (parts <= 16)
+            merge(dlsa_merge_kernel<4>);
+        else if (parts <= 32)
+            merge(dlsa_merge_kernel<8>);
+        else if (parts <= 64)
+            merge(dlsa_merge_kernel<16>);
+        else
+            merge(dlsa_merge_kernel<kDlsaMaxParts / 4>);
         QW_HIP_CHECK(hipGetLastError());
     }
     (void)waves;  // one 4-wave workgroup shape; the knob is accepted for API parity
