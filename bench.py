@@ -269,6 +269,61 @@ def bench_decode(torch, qw_amd, steps: int, warmup: int, reps: int, bits: int = 
             "bytes_layer": bytes_layer, "bytes_attn": bytes_attn}
 
 
+def bench_rope_decode(torch, qw_amd, reps: int, mode=None, T_prefix: int = 32768,
+                      rope_dims: int = 64):
+    """The served decode step from the QKV projection at the config-2
+    geometry (4-bit unless `mode`): RoPE of one token (a quarter of the dims
+    rotated, Qwen3-Next's partial rotary), its append and the attention.
+    Three forms, graph-replayed over 16 caches, each call then trimmed:
+    qw_kv_rope_update_and_attention (one decode launch plus the merge); the
+    reference's two calls (qw_fused_rope_qk_append, then
+    qw_kv_update_and_attention on its q, k, v); qw_kv_rope_update then
+    qw_kv_attention."""
+    ls = LayerSet(torch, qw_amd, 7, 4, T_prefix, 1, LAYERS, causal=False, mode=mode)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(8)
+    W = (HQ + 2 * HKV) * D
+    qkv = [torch.randn((1, 1, W), device=dev, generator=g).half() for _ in ls.caches]
+    qo = [torch.empty((HQ, 1, D), dtype=torch.float16, device=dev) for _ in ls.caches]
+    kr = [torch.empty((HKV, 1, D), dtype=torch.float16, device=dev) for _ in ls.caches]
+    vr = [torch.empty((HKV, 1, D), dtype=torch.float16, device=dev) for _ in ls.caches]
+    L = ls.lib
+    base, pos = 1e7, T_prefix
+
+    def one(i, st):
+        c = ls.caches[i][0]
+        ls._check(L.qw_kv_rope_update_and_attention(c._h, qkv[i].data_ptr(), HQ, 1, rope_dims, 0,
+                                                    base, 1.0, pos, 1.0 / 16, 0, qo[i].data_ptr(),
+                                                    ls.out[i].data_ptr(), st))
+        c.trim(1)
+
+    def two(i, st):
+        c = ls.caches[i][0]
+        ls._check(L.qw_fused_rope_qk_append(qkv[i].data_ptr(), 1, 1, HQ, HKV, D, rope_dims, base,
+                                            1.0, 0, pos, 0, qo[i].data_ptr(), kr[i].data_ptr(),
+                                            vr[i].data_ptr(), st))
+        ls._check(L.qw_kv_update_and_attention(c._h, qo[i].data_ptr(), HQ, 1, kr[i].data_ptr(),
+                                               vr[i].data_ptr(), 1.0 / 16, 0,
+                                               ls.out[i].data_ptr(), st))
+        c.trim(1)
+
+    def split(i, st):
+        c = ls.caches[i][0]
+        ls._check(L.qw_kv_rope_update(c._h, qkv[i].data_ptr(), HQ, 1, rope_dims, 0, base, 1.0, pos,
+                                      qo[i].data_ptr(), st))
+        ls._check(L.qw_kv_attention(c._h, qo[i].data_ptr(), HQ, 1, 1.0 / 16, 0,
+                                    ls.out[i].data_ptr(), st))
+        c.trim(1)
+
+    n = len(ls.caches)
+    res = {}
+    for name, fn in (("one_launch", one), ("reference_calls", two), ("rope_update_then_attention", split)):
+        res[name] = replay_stats(torch, lambda i, f=fn: f(i, ls.stream()), n, n, reps)["median"]
+    ls.close()
+    return res
+
+
 def bench_turbo4_verify(torch, qw_amd, steps: int, warmup: int, reps: int,
                         T_prefix: int = 32768, L: int = 4):
     """A Turbo4 causal verify block (L draft rows, the reference's fused-pass
@@ -1125,6 +1180,16 @@ def main() -> int:
             "us_chunk_2048": round(rp["chunk_ms"] * 1e3, 2),
             "GB_s_chunk": round(rp["chunk_bytes"] / (rp["chunk_ms"] * 1e-3) / 1e9, 1),
             "us_rope_append_1_token": round(rp["token_ms"] * 1e3, 2)}
+        log("bench: the decode step from the projection (RoPE, append, attention)")
+        sd = {}
+        for m in ("affine4", "turbo4"):
+            r_ = bench_rope_decode(torch, qw_amd, reps, mode=None if m == "affine4" else m)
+            sd[m] = {k: round(v * 1e3, 2) for k, v in r_.items()}
+        extra["decode_step_from_projection"] = {
+            "us": sd, "rope_dims": 64, "keys": 32769,
+            "forms": "one_launch: qw_kv_rope_update_and_attention; reference_calls: "
+                     "qw_fused_rope_qk_append then qw_kv_update_and_attention; "
+                     "rope_update_then_attention: qw_kv_rope_update then qw_kv_attention"}
         log("bench: Turbo4 decode (config-2 geometry)")
         t4 = bench_turbo4_decode(torch, qw_amd, LAYERS, args.warmup, reps)
         extra["turbo4_decode"] = {

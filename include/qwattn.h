@@ -412,6 +412,23 @@ int qw_kv_rope_update(qw_kv_cache* cache, const void* qkv, int n_q_heads, int n_
                       int rope_dims, int traditional, float rope_base, float rope_scale,
                       int position0, void* q_out, void* stream);
 
+/* A decode layer's attention from the projection: what
+ * Attention::forward_fused_rope_append (crates/mlxcel-core/src/layers.rs:
+ * 2852-2905) followed by KVCache::update_and_turbo4_attention (cache.rs:3495,
+ * the served decode call, crates/runtime/src/qwen3_next.rs:297-329) computes,
+ * i.e. qw_kv_rope_update then qw_kv_attention(q_out, n_tokens, scale,
+ * causal). Arguments as qw_kv_rope_update, plus scale and causal for the
+ * attention and out [n_q_heads][n_tokens][head_dim] fp16. q_out receives the
+ * rotated q either way. Decode-route shapes (affine, Int8 and Turbo4 caches,
+ * at most 16 query rows a KV head, rope_dims a multiple of 16, a non-empty
+ * cache) run as one decode launch plus the merge: the attention workgroups
+ * rotate their q rows themselves and the launch's append unit appends the
+ * rotated k and v; other shapes run the two calls. */
+int qw_kv_rope_update_and_attention(qw_kv_cache* cache, const void* qkv, int n_q_heads,
+                                    int n_tokens, int rope_dims, int traditional, float rope_base,
+                                    float rope_scale, int position0, float scale, int causal,
+                                    void* q_out, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

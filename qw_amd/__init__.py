@@ -90,6 +90,8 @@ _SIGNATURES = {
     "qw_fused_rope_qk_append": (_i, [_p, _i, _i, _i, _i, _i, _i, _f, _f, _i, _i, _i, _p, _p, _p,
                                      _p]),
     "qw_kv_rope_update": (_i, [_p, _p, _i, _i, _i, _i, _f, _f, _i, _p, _p]),
+    "qw_kv_rope_update_and_attention": (_i, [_p, _p, _i, _i, _i, _i, _f, _f, _i, _f, _i, _p, _p,
+                                             _p]),
     "qw_dlsa_sparse_attention": (_i, [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _i, _i, _i,
                                       _i, _i, _i, _f, _p, _p]),
     "qw_dlsa_sparse_attention_with": (_i, [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _i, _i,
@@ -255,6 +257,31 @@ class KVCache:
                                        int(traditional), float(rope_base), float(rope_scale),
                                        pos, q.data_ptr(), _stream(self.device)))
         return q.unsqueeze(0)
+
+    def rope_update_and_attention(self, qkv, n_q_heads: int, rope_dims: int, rope_base: float,
+                                  scale: float, rope_scale: float = 1.0, traditional: bool = False,
+                                  position0: int | None = None, causal: bool = False):
+        """RoPE, append and attention of one projection (rope_update, then
+        attention of the rotated q over the cache; one decode launch for
+        decode-route shapes). Returns (out [1, Hq, L, D], rotated q [1, Hq,
+        L, D])."""
+        torch = _torch()
+        x = qkv[0] if qkv.dim() == 3 else qkv
+        if x.dim() != 2 or x.dtype != torch.float16 or not x.is_cuda:
+            raise QwError(1, "rope_update_and_attention: qkv must be a [1, L, W] or [L, W] fp16 "
+                             "device tensor")
+        x = x.contiguous()
+        L, W = x.shape
+        if W != (n_q_heads + 2 * self.n_kv_heads) * self.head_dim:
+            raise QwError(1, "rope_update_and_attention: qkv width does not match the head geometry")
+        pos = self.offset if position0 is None else position0
+        q = torch.empty((n_q_heads, L, self.head_dim), dtype=torch.float16, device=self.device)
+        out = torch.empty_like(q)
+        _check(lib().qw_kv_rope_update_and_attention(
+            self._h, x.data_ptr(), n_q_heads, L, rope_dims, int(traditional), float(rope_base),
+            float(rope_scale), pos, float(scale), int(causal), q.data_ptr(), out.data_ptr(),
+            _stream(self.device)))
+        return out.unsqueeze(0), q.unsqueeze(0)
 
     def dequantize(self, start: int = 0, n: int | None = None):
         torch = _torch()

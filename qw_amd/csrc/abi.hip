@@ -396,4 +396,15 @@ int qw_kv_rope_update(qw_kv_cache* cache, const void* qkv, int n_q_heads, int n_
                                        (hipStream_t)stream));
 }
 
+int qw_kv_rope_update_and_attention(qw_kv_cache* cache, const void* qkv, int n_q_heads,
+                                    int n_tokens, int rope_dims, int traditional, float rope_base,
+                                    float rope_scale, int position0, float scale, int causal,
+                                    void* q_out, void* out, void* stream) {
+    QW_HANDLE(cache);
+    QW_GUARDED(cache->impl.rope_update_and_attention(qkv, n_q_heads, n_tokens, rope_dims,
+                                                     traditional, rope_base, rope_scale, position0,
+                                                     scale, causal != 0, q_out, out,
+                                                     (hipStream_t)stream));
+}
+
 }  // extern "C"

@@ -60,7 +60,64 @@ struct DecodeArgs {
     // and writes their partial, slot ns, with the causal cut when app_causal.
     int ns, app_L, app_causal, app_int8;
     RowSrc app;
+    // ROPE launches (RoPE, append and attention in one launch): q holds the
+    // projection's unrotated rows, query row r of q head qh at
+    // q + r * q_tok_stride + qh * D, rotated with app's RoPE fields at
+    // position app.position0 + r (rope_dims a multiple of 16); the append
+    // unit writes the rotated rows to q_out [hq][Tq][D].
+    int64_t q_tok_stride;
+    f16* q_out;
 };
+
+// ROPE: the (cos, sin) table of the launch's query rows, [Tq][rope_dims / 2]
+// in LDS, as the RoPE kernels form each pair's angle (rope_cs), filled by the
+// whole workgroup; the caller's barrier follows.
+__device__ __forceinline__ void decode_rope_table(const DecodeArgs& a, float2* tab, int nthreads) {
+    const int rh = a.app.rope_dims >> 1;
+    for (int i = threadIdx.x; i < a.Tq * rh; i += nthreads) {
+        const int r = i / rh, p = i - r * rh;
+        float c, sn;
+        rope_cs(p, rh, a.app.log2_base, a.app.scale, a.app.position0 + r, c, sn);
+        tab[i] = float2{c, sn};
+    }
+}
+
+// ROPE: dims d0 .. d0 + N - 1 of query row r (x, and xp = the same dims'
+// partners for the half-split pairing), rotated as the RoPE kernels rotate
+// them (rope_rot on the pair, the result rounded to fp16). N divides 8 and
+// d0 is a multiple of N, so with rope_dims a multiple of 16 the N dims sit
+// on one side of rope_dims / 2 and of rope_dims.
+template <int N>
+__device__ __forceinline__ void decode_rope_dims(const DecodeArgs& a, const float2* tab, int r,
+                                                 int d0, const f16 (&x)[N], const f16 (&xp)[N],
+                                                 f16 (&y)[N]) {
+    const int R = a.app.rope_dims, rh = R >> 1;
+#pragma unroll
+    for (int e = 0; e < N; e++) {
+        const int d = d0 + e;
+        if (d >= R) {
+            y[e] = x[e];
+            continue;
+        }
+        bool first;
+        int pr;
+        float partner;
+        if (a.app.traditional) {
+            first = (d & 1) == 0;
+            pr = d >> 1;
+            partner = (float)x[e ^ 1];
+        } else {
+            first = d < rh;
+            pr = first ? d : d - rh;
+            partner = (float)xp[e];
+        }
+        const float2 cs = tab[r * rh + pr];
+        const float xs = (float)x[e];
+        float r1, r2;
+        rope_rot(first ? xs : partner, first ? partner : xs, cs.x, cs.y, r1, r2);
+        y[e] = (f16)(first ? r1 : r2);
+    }
+}
 
 template <int BITS, int D>
 struct DecodeShape {
@@ -151,7 +208,7 @@ __device__ __forceinline__ half8 t4_expand8(uint32_t w, float r, const float2* p
 // DPL r16 .. +DPL - 1 of keys 8g .. 8g+7 (16 lanes cover a row's D/2 bytes).
 // The centroid comes from a register table (lane i holds centroid i % 16)
 // through ds_bpermute.
-template <int BITS, int D, int NW, bool FAST, bool T4 = false, int AUX = 0>
+template <int BITS, int D, int NW, bool FAST, bool T4 = false, int AUX = 0, bool ROPE = false>
 __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)[NW], float* sm_o,
                                             half8 (*sm_q)[64], float2* sm_t4 = nullptr) {
     using S = DecodeShape<BITS, D>;
@@ -319,14 +376,23 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
         // the rotations and the table then wait for the prologue's reads only.
         constexpr int VPL = D / 64;
         static_assert(2 * NW >= 16 && 64 * NW >= 256, "two q rows a wave, a table entry a thread");
-        float yq[2][VPL];
+        f16 xq[2][VPL], xpq[2][VPL];
 #pragma unroll
         for (int k = 0; k < 2; k++) {
             const int row = wave + k * NW;
             const int rr = row < a.R ? row : 0;
-            const f16* qrow = a.q + ((int64_t)(h * a.G + rr % a.G) * a.Tq + rr / a.G) * D;
+            const f16* qrow = ROPE ? a.q + (int64_t)(rr / a.G) * a.q_tok_stride + (int64_t)(h * a.G + rr % a.G) * D
+                                   : a.q + ((int64_t)(h * a.G + rr % a.G) * a.Tq + rr / a.G) * D;
 #pragma unroll
-            for (int j = 0; j < VPL; j++) yq[k][j] = (float)qrow[lane * VPL + j];
+            for (int j = 0; j < VPL; j++) xq[k][j] = qrow[lane * VPL + j];
+            if constexpr (ROPE) {
+                // the half-split partners of the lane's dims
+                const int d0 = lane * VPL, rh = a.app.rope_dims >> 1;
+                const int pb = d0 < rh ? d0 + rh : d0 - rh;
+                const bool need = !a.app.traditional && d0 < a.app.rope_dims;
+#pragma unroll
+                for (int j = 0; j < VPL; j++) xpq[k][j] = need ? qrow[pb + j] : (f16)0.0f;
+            }
         }
         float si[VPL], so[VPL];
         t4_lane_signs<D>(a.t4_tab + T4Tab<D>::k_s1, lane, si);
@@ -336,6 +402,26 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
         const float2 pair = float2{cb[tb & 15], cb[tb >> 4]};
         load(A, s);
         if (threadIdx.x < 256) sm_t4[threadIdx.x] = pair;
+        float yq[2][VPL];
+        if constexpr (ROPE) {
+            float2* const rtab = (float2*)((char*)sm_o + 16 * D * sizeof(f16));  // behind sm_qr
+            decode_rope_table(a, rtab, 64 * NW);
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const int row = wave + k * NW;
+                const int rr = row < a.R ? row : 0;
+                f16 yk[VPL];
+                decode_rope_dims<VPL>(a, rtab, rr / a.G, lane * VPL, xq[k], xpq[k], yk);
+#pragma unroll
+                for (int j = 0; j < VPL; j++) yq[k][j] = (float)yk[j];
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 2; k++)
+#pragma unroll
+                for (int j = 0; j < VPL; j++) yq[k][j] = (float)xq[k][j];
+        }
 #pragma unroll
         for (int k = 0; k < 2; k++) {
             const int row = wave + k * NW;
@@ -353,7 +439,9 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
         // rr / G and rr % G for rr < 16 from a float reciprocal (exact here:
         // (rr + 0.5) / G is at least 0.5 / G from an integer)
         const int rq = (int)(((float)rr + 0.5f) * a.inv_g), rg_ = rr - rq * a.G;
-        const f16* qrow = T4 ? sm_qr + rr * D : a.q + ((int64_t)(h * a.G + rg_) * a.Tq + rq) * D;
+        const f16* qrow = T4     ? sm_qr + rr * D
+                          : ROPE ? a.q + (int64_t)rq * a.q_tok_stride + (int64_t)(h * a.G + rg_) * D
+                                 : a.q + ((int64_t)(h * a.G + rg_) * a.Tq + rq) * D;
         const int m = wave % NM;
         int base;
         if constexpr (T4)
@@ -365,12 +453,34 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
         else
             base = 32 * m + 8 * g;
         x = *(const half8*)(qrow + base);
+        if constexpr (ROPE && !T4) {
+            // the half-split partners of the 8 dims; rotated once the
+            // workgroup's angle table is in
+            const int rh = a.app.rope_dims >> 1;
+            const int pb = base < rh ? base + rh : base - rh;
+            const half8 xp = !a.app.traditional && base < a.app.rope_dims ? *(const half8*)(qrow + pb)
+                                                                        : half8{};
+            load(A, s);
+            float2* const rtab = (float2*)sm_o;
+            decode_rope_table(a, rtab, 64 * NW);
+            __syncthreads();
+            f16 xa[8], xpa[8], ya[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                xa[e] = x[e];
+                xpa[e] = xp[e];
+            }
+            decode_rope_dims<8>(a, rtab, rq, base, xa, xpa, ya);
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[e] = ya[e];
+        }
     }
     // The first sub-chunk's loads go out right behind Q (loads return in
     // issue order, so the Q conversion below waits for Q only: the Q barrier
     // holds every wave of the workgroup until the last one's q is in);
-    // Turbo4 issued them in its prologue above.
-    if constexpr (!T4) load(A, s);
+    // Turbo4 issued them in its prologue above (and ROPE launches after the
+    // partners of q).
+    if constexpr (!T4 && !ROPE) load(A, s);
     {
         // q' = f16(f16(scale) * q): one packed fp16 multiply rounds exactly
         // like MLX's fp16 `multiply`. Padding rows get scale 0.
@@ -705,7 +815,7 @@ static_assert(sizeof(AppendScratch<128>) >= 16 * sizeof(float), "centroid table 
 // rotation signs with the appended rows) and Turbo4 expands the new keys
 // from the quantizer's registers: each dependent memory round trip here costs
 // microseconds.
-template <int BITS, int D, bool T4>
+template <int BITS, int D, bool T4, bool ROPE = false>
 __device__ void decode_append_unit(const DecodeArgs& a, char* lds) {
     constexpr int NW = decode_waves<BITS, D>();
     constexpr int VPL = D / 64, NG = D / 64;
@@ -718,9 +828,23 @@ __device__ void decode_append_unit(const DecodeArgs& a, char* lds) {
 #pragma unroll
     for (int k = 0; k < RPW; k++) {
         const int rho = min(wave + NW * k, a.R - 1);
-        const f16* qrow = a.q + ((int64_t)(h * a.G + rho % a.G) * a.Tq + rho / a.G) * D;
+        const int qh = h * a.G + rho % a.G, r = rho / a.G;
+        if constexpr (ROPE) {
+            // the rows rotated as the RoPE kernels rotate them, and written out
+            const f16* qrow = a.q + (int64_t)r * a.q_tok_stride + (int64_t)qh * D;
+            const RowSrc& rs = a.app;
 #pragma unroll
-        for (int i = 0; i < VPL; i++) qv[k][i] = (float)qrow[lane * VPL + i];
+            for (int i = 0; i < VPL; i++) {
+                const f16 y = (f16)rope_elem(qrow, lane * VPL + i, rs.rope_dims, rs.traditional,
+                                             rs.log2_base, rs.scale, rs.position0 + r);
+                qv[k][i] = (float)y;
+                if (wave + NW * k < a.R) a.q_out[((int64_t)qh * a.Tq + r) * D + lane * VPL + i] = y;
+            }
+        } else {
+            const f16* qrow = a.q + ((int64_t)qh * a.Tq + r) * D;
+#pragma unroll
+            for (int i = 0; i < VPL; i++) qv[k][i] = (float)qrow[lane * VPL + i];
+        }
     }
     float si[VPL], so[VPL];
     if constexpr (T4) {
@@ -823,9 +947,10 @@ __device__ void decode_append_unit(const DecodeArgs& a, char* lds) {
     }
 }
 
-template <int BITS, int D, bool T4 = false, bool APP = false, bool NT = false>
+template <int BITS, int D, bool T4 = false, bool APP = false, bool NT = false, bool ROPE = false>
 __global__ __launch_bounds__((64 * decode_waves<BITS, D>()), 1) void attend_decode_kernel(
     DecodeArgs a) {
+    static_assert(!ROPE || APP, "RoPE launches append their rows");
     constexpr int NW = decode_waves<BITS, D>();
     constexpr int AUX = NT ? 2 : 0;  // the K/V loads' cache policy
     __shared__ __attribute__((aligned(16))) float2 sm_ml[16][NW];
@@ -843,18 +968,18 @@ __global__ __launch_bounds__((64 * decode_waves<BITS, D>()), 1) void attend_deco
     // Turbo4 caches have one dequant (a null flag).
     if constexpr (APP && BITS != 16) {
         if ((int)blockIdx.x == a.ns) {
-            decode_append_unit<BITS, D, T4>(a, (char*)sm_o);
+            decode_append_unit<BITS, D, T4, ROPE>(a, (char*)sm_o);
             return;
         }
     }
     if (!T4 && (BITS == 16 || a.fast_flag != nullptr)) {
-        decode_body<BITS, D, NW, true, false, AUX>(a, sm_ml, sm_o, sm_q);
+        decode_body<BITS, D, NW, true, false, AUX, ROPE>(a, sm_ml, sm_o, sm_q);
         if (BITS != 16 && *a.fast_flag == 0) {
             __syncthreads();
-            decode_body<BITS, D, NW, false, false, AUX>(a, sm_ml, sm_o, sm_q);
+            decode_body<BITS, D, NW, false, false, AUX, ROPE>(a, sm_ml, sm_o, sm_q);
         }
     } else {
-        decode_body<BITS, D, NW, false, T4, AUX>(a, sm_ml, sm_o, sm_q, sm_t4);
+        decode_body<BITS, D, NW, false, T4, AUX, ROPE>(a, sm_ml, sm_o, sm_q, sm_t4);
     }
 }
 
@@ -951,12 +1076,17 @@ __global__ __launch_bounds__(64 * kMW) void decode_merge_kernel(const float* __r
 
 // Split-K attention of the Tq rows over the first T cached keys: launches the
 // decode kernel and returns its partials (nc per KV head, 16 rows apart).
+// rope (a RoPE launch, with app_L > 0): the new rows come through *rope (K
+// rotated on load), q is the projection with token stride q_tok_stride, and
+// the rotated q rows go to q_out.
 template <int BITS, int D, bool T4 = false>
 static int launch_decode_partials(KVCache& cc, const f16* q, int G, int Tq, int T, float scale,
                                   bool causal, int* nc_out, float** po, float2** pml,
                                   hipStream_t stream, const float* t4_tab = nullptr,
                                   const f16* k_new = nullptr, const f16* v_new = nullptr,
-                                  int app_L = 0, bool app_causal = false) {
+                                  int app_L = 0, bool app_causal = false,
+                                  const RowSrc* rope = nullptr, int64_t q_tok_stride = 0,
+                                  f16* q_out = nullptr) {
     const int n_sub = (T + 31) / 32;
     // Sub-chunks a wave owns: 4-bit rows are small enough to keep 4 in flight.
     // Sub-chunks a wave keeps in flight per round, and workgroups per KV head:
@@ -1005,6 +1135,15 @@ static int launch_decode_partials(KVCache& cc, const f16* q, int G, int Tq, int 
     a.app.v = v_new;
     a.app.row_stride = D;
     a.app.head_stride = (int64_t)app_L * D;
+    a.q_tok_stride = 0;
+    a.q_out = nullptr;
+    if (rope) {
+        QW_REQUIRE(app_L > 0 && rope->rope_dims % 16 == 0 && rope->rope_dims <= D && q_out,
+                   QW_ERR_INVALID_ARGUMENT, "decode: RoPE launch outside its shapes");
+        a.app = *rope;
+        a.q_tok_stride = q_tok_stride;
+        a.q_out = q_out;
+    }
     // wave merge: accumulators NW x G4 x D float4, bias sums NW x G4 x 16
     // float4, factors 4 x NW float4
     size_t shmem = (size_t)NW * ((a.R + 3) / 4) * (D + 16) * 16 + 4 * NW * 16;
@@ -1018,7 +1157,14 @@ static int launch_decode_partials(KVCache& cc, const f16* q, int G, int Tq, int 
         hipLaunchKernelGGL(kernel, dim3(nc, cc.hkv), dim3(64 * NW), shmem, stream, a);
         return QW_OK;
     };
-    if (app) {
+    if (rope) {
+        // the angle table (behind the rotated q rows of Turbo4)
+        shmem = std::max({shmem, decode_append_lds<D>(app_L),
+                          (size_t)(T4 ? 16 * D * sizeof(f16) : 0) +
+                              (size_t)Tq * (rope->rope_dims / 2) * sizeof(float2)});
+        rc = nt ? go(attend_decode_kernel<BITS, D, T4, true, true, true>)
+                : go(attend_decode_kernel<BITS, D, T4, true, false, true>);
+    } else if (app) {
         shmem = std::max(shmem, decode_append_lds<D>(app_L));
         rc = nt ? go(attend_decode_kernel<BITS, D, T4, true, true>)
                 : go(attend_decode_kernel<BITS, D, T4, true, false>);
@@ -1192,6 +1338,25 @@ static int launch_decode_append(KVCache& cc, const f16* q, int G, int L, const f
     return launch_partial_merge(po, pml, nc, 16, 0, G * L, cc.hkv, D, G, L, out, stream);
 }
 
+// RoPE, append and attention in one decode launch (affine and Int8 caches,
+// G L <= 16): qkv is the projection [L][(G hkv + 2 hkv) D], rope carries its
+// RoPE parameters; the rotated q rows go to q_out.
+template <int BITS, int D>
+static int launch_decode_rope_append(KVCache& cc, const f16* qkv, int G, int L, const RowSrc& rope,
+                                     float scale, bool causal, f16* q_out, f16* out,
+                                     hipStream_t stream) {
+    int nc = 0;
+    float* po = nullptr;
+    float2* pml = nullptr;
+    const int64_t W = (int64_t)(G + 2) * cc.hkv * D;
+    int rc = launch_decode_partials<BITS, D>(cc, qkv, G, L, cc.offset, scale, false, &nc, &po, &pml,
+                                             stream, nullptr, rope.k, rope.v, L, causal, &rope, W,
+                                             q_out);
+    if (rc) return rc;
+    cc.offset += L;
+    return launch_partial_merge(po, pml, nc, 16, 0, G * L, cc.hkv, D, G, L, out, stream);
+}
+
 int launch_turbo4_decode_append(KVCache& cc, const f16* q, int G, int L, const f16* k_new,
                                 const f16* v_new, float scale, bool causal, const float* tab,
                                 f16* out, hipStream_t stream) {
@@ -1206,6 +1371,26 @@ int launch_turbo4_decode_append(KVCache& cc, const f16* q, int G, int L, const f
                          : launch_decode_partials<4, 128, true>(cc, q, G, L, cc.offset, scale, false,
                                                                 &nc, &po, &pml, stream, tab, k_new,
                                                                 v_new, L, causal);
+    if (rc) return rc;
+    cc.offset += L;
+    return launch_t4_merge_rotate(po, pml, nc, 16, G * L, cc.hkv, cc.D, G, L, 0, false, tab, out,
+                                  stream);
+}
+
+static int launch_turbo4_decode_rope_append(KVCache& cc, const f16* qkv, int G, int L,
+                                            const RowSrc& rope, float scale, bool causal,
+                                            const float* tab, f16* q_out, f16* out,
+                                            hipStream_t stream) {
+    int nc = 0;
+    float* po = nullptr;
+    float2* pml = nullptr;
+    const int64_t W = (int64_t)(G + 2) * cc.hkv * cc.D;
+    int rc = cc.D == 256 ? launch_decode_partials<4, 256, true>(cc, qkv, G, L, cc.offset, scale, false,
+                                                                &nc, &po, &pml, stream, tab, rope.k,
+                                                                rope.v, L, causal, &rope, W, q_out)
+                         : launch_decode_partials<4, 128, true>(cc, qkv, G, L, cc.offset, scale, false,
+                                                                &nc, &po, &pml, stream, tab, rope.k,
+                                                                rope.v, L, causal, &rope, W, q_out);
     if (rc) return rc;
     cc.offset += L;
     return launch_t4_merge_rotate(po, pml, nc, 16, G * L, cc.hkv, cc.D, G, L, 0, false, tab, out,
@@ -1640,6 +1825,61 @@ int KVCache::update_and_attention(const void* q, int n_q_heads, int n_rows, cons
     int rc = update(k_new, v_new, n_rows, stream);
     if (rc) return rc;
     return launch_attention(*this, q, n_q_heads, n_rows, scale, causal, out, stream);
+}
+
+// RoPE, append and attention of one projection: what rope_update (q rotated
+// into q_out, K rotated into the cache, V appended) followed by attention on
+// q_out computes. Decode-route shapes (affine, Int8 and Turbo4 caches, at
+// most 16 rows a KV head, rope_dims a multiple of 16) run it in one decode
+// launch plus the merge: the workgroups rotate their q rows in the prologue
+// and the append unit appends the rotated K with V and writes q_out. Other
+// shapes run the two calls.
+int KVCache::rope_update_and_attention(const void* qkv, int n_q_heads, int n_tokens, int rope_dims,
+                                       int traditional, float rope_base, float rope_scale,
+                                       int position0, float scale, bool causal, void* q_out,
+                                       void* out, hipStream_t stream) {
+    QW_REQUIRE(qkv && q_out && out, QW_ERR_INVALID_ARGUMENT, "rope_update_and_attention: null buffer");
+    QW_REQUIRE(n_q_heads > 0 && n_q_heads % hkv == 0 && n_tokens > 0, QW_ERR_INVALID_ARGUMENT,
+               "rope_update_and_attention: bad head or row geometry");
+    QW_REQUIRE(rope_dims >= 0 && rope_dims <= D && rope_dims % 2 == 0 && rope_base > 0.0f,
+               QW_ERR_INVALID_ARGUMENT, "rope_update_and_attention: bad RoPE parameters");
+    const int G = n_q_heads / hkv, T = offset + n_tokens;
+    const bool t4_decode = turbo4() && turbo4_decode_route(*this, causal, n_tokens, G);
+    const bool one_launch = QW_DECODE_APPEND && rope_dims % 16 == 0 && G * n_tokens <= 16 &&
+                            offset >= 1 && (affine() || t4_decode);
+    if (!one_launch) {
+        int rc = rope_update(qkv, n_q_heads, n_tokens, rope_dims, traditional, rope_base, rope_scale,
+                             position0, q_out, stream);
+        if (rc) return rc;
+        return launch_attention(*this, q_out, n_q_heads, n_tokens, scale, causal, out, stream);
+    }
+    DeviceGuard dg(device);
+    QW_REQUIRE(dg.ok, QW_ERR_HIP, "rope_update_and_attention: hipSetDevice failed");
+    if (T > cap) {
+        int rc = reserve(std::max(T, cap + cap / 2), stream);
+        if (rc) return rc;
+    }
+    const int64_t W = (int64_t)(n_q_heads + 2 * hkv) * D;
+    RowSrc rs;
+    rs.k = (const f16*)qkv + (int64_t)n_q_heads * D;
+    rs.v = (const f16*)qkv + (int64_t)(n_q_heads + hkv) * D;
+    rs.row_stride = W;
+    rs.head_stride = D;
+    rs.rope_dims = rope_dims;
+    rs.traditional = traditional ? 1 : 0;
+    rs.position0 = position0;
+    rs.log2_base = std::log2(rope_base);
+    rs.scale = rope_scale;
+    const f16* q = (const f16*)qkv;
+    f16 *qo = (f16*)q_out, *oo = (f16*)out;
+    if (turbo4())
+        return launch_turbo4_decode_rope_append(*this, q, G, n_tokens, rs, scale, causal, t4_tables,
+                                                qo, oo, stream);
+    if (D == 256)
+        return bits == 4 ? launch_decode_rope_append<4, 256>(*this, q, G, n_tokens, rs, scale, causal, qo, oo, stream)
+                         : launch_decode_rope_append<8, 256>(*this, q, G, n_tokens, rs, scale, causal, qo, oo, stream);
+    return bits == 4 ? launch_decode_rope_append<4, 128>(*this, q, G, n_tokens, rs, scale, causal, qo, oo, stream)
+                     : launch_decode_rope_append<8, 128>(*this, q, G, n_tokens, rs, scale, causal, qo, oo, stream);
 }
 
 }  // namespace qw

@@ -105,6 +105,13 @@ struct KVCache {
     int rope_update(const void* qkv, int n_q_heads, int n_tokens, int rope_dims, int traditional,
                     float rope_base, float rope_scale, int position0, void* q_out,
                     hipStream_t stream);
+    // fused_rope_append.cpp:80-180 then cache.rs:3495 `update_and_turbo4_attention`
+    // on its outputs: rope_update, then attention of q_out over the cache;
+    // one decode launch (plus the merge) for decode-route shapes.
+    int rope_update_and_attention(const void* qkv, int n_q_heads, int n_tokens, int rope_dims,
+                                  int traditional, float rope_base, float rope_scale, int position0,
+                                  float scale, bool causal, void* q_out, void* out,
+                                  hipStream_t stream);
     // cache.rs:2709 `update_and_fetch`
     int update_and_fetch(const void* k_new, const void* v_new, int n_tokens, void* k_out,
                          void* v_out, hipStream_t stream);
@@ -239,6 +246,9 @@ int launch_block_append_attention_t4(KVCache& c, const f16* q, int G, int n_rows
 int launch_turbo4_decode_append(KVCache& c, const f16* q, int G, int n_rows, const f16* k_new,
                                 const f16* v_new, float scale, bool causal, const float* tab,
                                 f16* out, hipStream_t stream);
+// Whether a Turbo4 update-and-attention of n_rows rows takes the decode route
+// (the append unit in the decode launch).
+bool turbo4_decode_route(const KVCache& c, bool causal, int n_rows, int G);
 // Turbo4 update-and-attention: the append in the block kernel's launch where
 // the call takes the block kernel, else turbo4_update then turbo4_attention.
 int turbo4_update_and_attention(KVCache& c, const void* q, int n_q_heads, int n_rows,

@@ -846,6 +846,11 @@ static int turbo4_block(KVCache& c, const void* q, int n_q_heads, int n_rows, fl
     return QW_OK;
 }
 
+bool turbo4_decode_route(const KVCache& c, bool causal, int n_rows, int G) {
+    return !t4_fused_route(causal, n_rows, c.offset + n_rows, G) && QW_T4_FUSED_DECODE &&
+           G * n_rows <= 16 && c.offset >= 1;
+}
+
 int turbo4_update_and_attention(KVCache& c, const void* q, int n_q_heads, int n_rows,
                                 const void* k_new, const void* v_new, float scale, bool causal,
                                 void* out, hipStream_t stream) {
@@ -855,7 +860,7 @@ int turbo4_update_and_attention(KVCache& c, const void* q, int n_q_heads, int n_
     // in the decode launch's append unit
     const bool fused = t4_fused_route(causal, n_rows, T, G);
     const bool block = QW_T4_BLOCK && block_append_fits_t4(c, G, n_rows) && (fused || G * n_rows > 16);
-    const bool decode = !fused && QW_T4_FUSED_DECODE && G * n_rows <= 16 && c.offset >= 1;
+    const bool decode = turbo4_decode_route(c, causal, n_rows, G);
     if (!(QW_T4_APPEND && (block || decode))) {
         int rc = c.update(k_new, v_new, n_rows, stream);
         if (rc) return rc;

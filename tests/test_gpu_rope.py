@@ -170,3 +170,91 @@ def test_rope_update_affine4_matches_oracle_quantize():
     k, v = map(_np, cache.dequantize())
     np.testing.assert_array_equal(k[0], rk)
     np.testing.assert_array_equal(v[0], rv)
+
+
+# qw_kv_rope_update_and_attention: the served decode step from the projection
+# (forward_fused_rope_append, then update_and_turbo4_attention) in one decode
+# launch for decode-route shapes, the two calls otherwise.
+@pytest.mark.parametrize("mode", ["affine4", "affine8", "int8", "turbo4"])
+@pytest.mark.parametrize("D,R,trad,L,T0", [
+    (256, 64, False, 1, 3000),   # the served Qwen3-Next shape: a quarter of the dims rotated
+    (256, 256, True, 2, 700),    # a 2-row causal block, every dim rotated, adjacent pairs
+    (128, 64, False, 1, 2500),
+    (128, 128, True, 2, 40),
+])
+def test_rope_update_and_attention_equals_the_two_reference_calls(mode, D, R, trad, L, T0):
+    """Bit for bit against fused_rope_qk_append followed by
+    update_and_attention on its q, k, v: the output, the rotated q, and the
+    cache's rows afterwards (the same rotation arithmetic, rope_cs / rope_rot,
+    and the same decode-launch arithmetic)."""
+    import qw_amd
+
+    hq, hkv, base = 24, 4, 1e7
+    causal = L > 1
+    print(f"mode {mode} D {D} R {R} traditional {trad} L {L} T0 {T0}", flush=True)
+    r = rng(31 + D + L)
+    k0 = _gpu(r.standard_normal((hkv, T0, D)).astype(np.float16))
+    v0 = _gpu(r.standard_normal((hkv, T0, D)).astype(np.float16))
+    a = qw_amd.KVCache(mode, hkv, D)
+    b = qw_amd.KVCache(mode, hkv, D)
+    a.update(k0, v0)
+    b.update(k0, v0)
+    for step in range(3):  # three consecutive steps: positions and appends chain
+        qkv = _gpu(r.standard_normal((1, L, (hq + 2 * hkv) * D)).astype(np.float16))
+        pos = a.offset
+        out_a, q_a = a.rope_update_and_attention(qkv, hq, R, base, 1.0 / 16, 1.0, trad, pos,
+                                                 causal)
+        q_r, k_r, v_r = qw_amd.fused_rope_qk_append(qkv, hq, hkv, D, R, base, 1.0, trad, pos, 0)
+        fn = b.update_and_causal_attention if causal else b.update_and_attention
+        out_b = fn(q_r, k_r, v_r, 1.0 / 16)
+        assert a.offset == b.offset == pos + L
+        np.testing.assert_array_equal(_np(q_a), _np(q_r), err_msg=f"q, step {step}")
+        np.testing.assert_array_equal(_np(out_a), _np(out_b), err_msg=f"out, step {step}")
+    ka, va = map(_np, a.dequantize())
+    kb, vb = map(_np, b.dequantize())
+    np.testing.assert_array_equal(ka, kb)
+    np.testing.assert_array_equal(va, vb)
+    a.close()
+    b.close()
+
+
+@pytest.mark.parametrize("mode,R,L", [
+    ("affine4", 64, 4),   # 24 rows a KV head: the block route
+    ("affine8", 24, 1),   # rope_dims not a multiple of 16
+    ("fp16", 64, 1),      # an fp16 cache
+])
+def test_rope_update_and_attention_other_shapes_are_the_two_calls(mode, R, L):
+    """Shapes outside the one-launch route run rope_update and attention."""
+    import qw_amd
+
+    hq, hkv, D, T0, base = 24, 4, 256, 1500, 1e6
+    print(f"mode {mode} R {R} L {L}", flush=True)
+    r = rng(41 + L)
+    k0 = _gpu(r.standard_normal((hkv, T0, D)).astype(np.float16))
+    v0 = _gpu(r.standard_normal((hkv, T0, D)).astype(np.float16))
+    a = qw_amd.KVCache(mode, hkv, D)
+    b = qw_amd.KVCache(mode, hkv, D)
+    a.update(k0, v0)
+    b.update(k0, v0)
+    qkv = _gpu(r.standard_normal((1, L, (hq + 2 * hkv) * D)).astype(np.float16))
+    out_a, q_a = a.rope_update_and_attention(qkv, hq, R, base, 1.0 / 16, 1.0, False, T0, True)
+    q_b = b.rope_update(qkv, hq, R, base, 1.0, False, T0)
+    out_b = b.attention(q_b, 1.0 / 16, causal=True)
+    np.testing.assert_array_equal(_np(q_a), _np(q_b))
+    np.testing.assert_array_equal(_np(out_a), _np(out_b))
+    a.close()
+    b.close()
+
+
+def test_rope_update_and_attention_contract_errors():
+    import qw_amd
+
+    c = qw_amd.KVCache("affine4", 4, 256)
+    c.update(_gpu(np.zeros((4, 10, 256), np.float16)), _gpu(np.zeros((4, 10, 256), np.float16)))
+    qkv = _gpu(np.zeros((1, 1, 32 * 256), np.float16))
+    with pytest.raises(qw_amd.QwError):
+        c.rope_update_and_attention(qkv, 24, 3, 1e6, 1.0 / 16)      # odd rope_dims
+    with pytest.raises(qw_amd.QwError):
+        c.rope_update_and_attention(qkv, 24, 64, -1.0, 1.0 / 16)    # base <= 0
+    assert c.offset == 10                                           # nothing appended
+    c.close()
