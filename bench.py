@@ -270,51 +270,53 @@ def bench_decode(torch, qw_amd, steps: int, warmup: int, reps: int, bits: int = 
 
 
 def bench_rope_decode(torch, qw_amd, reps: int, mode=None, T_prefix: int = 32768,
-                      rope_dims: int = 64):
+                      rope_dims: int = 64, L: int = 1):
     """The served decode step from the QKV projection at the config-2
-    geometry (4-bit unless `mode`): RoPE of one token (a quarter of the dims
-    rotated, Qwen3-Next's partial rotary), its append and the attention.
-    Three forms, graph-replayed over 16 caches, each call then trimmed:
-    qw_kv_rope_update_and_attention (one decode launch plus the merge); the
-    reference's two calls (qw_fused_rope_qk_append, then
-    qw_kv_update_and_attention on its q, k, v); qw_kv_rope_update then
-    qw_kv_attention."""
-    ls = LayerSet(torch, qw_amd, 7, 4, T_prefix, 1, LAYERS, causal=False, mode=mode)
+    geometry (4-bit unless `mode`): RoPE of L tokens (a quarter of the dims
+    rotated, Qwen3-Next's partial rotary), their append and the attention
+    (causal for a verify block, L > 1). Three forms, graph-replayed over 16
+    caches, each call then trimmed: qw_kv_rope_update_and_attention (one
+    attention launch plus the merge); the reference's two calls
+    (qw_fused_rope_qk_append, then qw_kv_update_and_attention on its q, k,
+    v); qw_kv_rope_update then qw_kv_attention."""
+    causal = L > 1
+    ls = LayerSet(torch, qw_amd, 7, 4, T_prefix, L, LAYERS, causal=causal, mode=mode)
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(8)
     W = (HQ + 2 * HKV) * D
-    qkv = [torch.randn((1, 1, W), device=dev, generator=g).half() for _ in ls.caches]
-    qo = [torch.empty((HQ, 1, D), dtype=torch.float16, device=dev) for _ in ls.caches]
-    kr = [torch.empty((HKV, 1, D), dtype=torch.float16, device=dev) for _ in ls.caches]
-    vr = [torch.empty((HKV, 1, D), dtype=torch.float16, device=dev) for _ in ls.caches]
-    L = ls.lib
+    qkv = [torch.randn((1, L, W), device=dev, generator=g).half() for _ in ls.caches]
+    qo = [torch.empty((HQ, L, D), dtype=torch.float16, device=dev) for _ in ls.caches]
+    kr = [torch.empty((HKV, L, D), dtype=torch.float16, device=dev) for _ in ls.caches]
+    vr = [torch.empty((HKV, L, D), dtype=torch.float16, device=dev) for _ in ls.caches]
+    cz = int(causal)
+    lib = ls.lib
     base, pos = 1e7, T_prefix
 
     def one(i, st):
         c = ls.caches[i][0]
-        ls._check(L.qw_kv_rope_update_and_attention(c._h, qkv[i].data_ptr(), HQ, 1, rope_dims, 0,
-                                                    base, 1.0, pos, 1.0 / 16, 0, qo[i].data_ptr(),
-                                                    ls.out[i].data_ptr(), st))
-        c.trim(1)
+        ls._check(lib.qw_kv_rope_update_and_attention(c._h, qkv[i].data_ptr(), HQ, L, rope_dims,
+                                                      0, base, 1.0, pos, 1.0 / 16, cz,
+                                                      qo[i].data_ptr(), ls.out[i].data_ptr(), st))
+        c.trim(L)
 
     def two(i, st):
         c = ls.caches[i][0]
-        ls._check(L.qw_fused_rope_qk_append(qkv[i].data_ptr(), 1, 1, HQ, HKV, D, rope_dims, base,
-                                            1.0, 0, pos, 0, qo[i].data_ptr(), kr[i].data_ptr(),
-                                            vr[i].data_ptr(), st))
-        ls._check(L.qw_kv_update_and_attention(c._h, qo[i].data_ptr(), HQ, 1, kr[i].data_ptr(),
-                                               vr[i].data_ptr(), 1.0 / 16, 0,
-                                               ls.out[i].data_ptr(), st))
-        c.trim(1)
+        ls._check(lib.qw_fused_rope_qk_append(qkv[i].data_ptr(), 1, L, HQ, HKV, D, rope_dims, base,
+                                              1.0, 0, pos, 0, qo[i].data_ptr(), kr[i].data_ptr(),
+                                              vr[i].data_ptr(), st))
+        ls._check(lib.qw_kv_update_and_attention(c._h, qo[i].data_ptr(), HQ, L, kr[i].data_ptr(),
+                                                 vr[i].data_ptr(), 1.0 / 16, cz,
+                                                 ls.out[i].data_ptr(), st))
+        c.trim(L)
 
     def split(i, st):
         c = ls.caches[i][0]
-        ls._check(L.qw_kv_rope_update(c._h, qkv[i].data_ptr(), HQ, 1, rope_dims, 0, base, 1.0, pos,
-                                      qo[i].data_ptr(), st))
-        ls._check(L.qw_kv_attention(c._h, qo[i].data_ptr(), HQ, 1, 1.0 / 16, 0,
-                                    ls.out[i].data_ptr(), st))
-        c.trim(1)
+        ls._check(lib.qw_kv_rope_update(c._h, qkv[i].data_ptr(), HQ, L, rope_dims, 0, base, 1.0,
+                                        pos, qo[i].data_ptr(), st))
+        ls._check(lib.qw_kv_attention(c._h, qo[i].data_ptr(), HQ, L, 1.0 / 16, cz,
+                                      ls.out[i].data_ptr(), st))
+        c.trim(L)
 
     n = len(ls.caches)
     res = {}
@@ -1183,10 +1185,11 @@ def main() -> int:
         log("bench: the decode step from the projection (RoPE, append, attention)")
         sd = {}
         for m in ("affine4", "turbo4"):
-            r_ = bench_rope_decode(torch, qw_amd, reps, mode=None if m == "affine4" else m)
-            sd[m] = {k: round(v * 1e3, 2) for k, v in r_.items()}
+            for L_ in (1, 4):
+                r_ = bench_rope_decode(torch, qw_amd, reps, mode=None if m == "affine4" else m, L=L_)
+                sd[f"{m}_{L_}row" + ("s" if L_ > 1 else "")] = {k: round(v * 1e3, 2) for k, v in r_.items()}
         extra["decode_step_from_projection"] = {
-            "us": sd, "rope_dims": 64, "keys": 32769,
+            "us": sd, "rope_dims": 64, "keys": "32768 + rows", "verify": "4 rows, causal",
             "forms": "one_launch: qw_kv_rope_update_and_attention; reference_calls: "
                      "qw_fused_rope_qk_append then qw_kv_update_and_attention; "
                      "rope_update_then_attention: qw_kv_rope_update then qw_kv_attention"}

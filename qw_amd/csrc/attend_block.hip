@@ -71,6 +71,13 @@ struct BlockArgs {
     // others are splits 0 .. n_split - 2 of the cached prefix, keys < T_pre.
     int n_app, T_pre, app_int8;
     RowSrc app;
+    // ROPE launches (RoPE, append and attention in one launch): q holds the
+    // projection's unrotated rows, query row r of q head qh at
+    // q + r * q_tok_stride + qh * D, rotated with app's RoPE fields at
+    // position app.position0 + r (rope_dims a multiple of 16); the append
+    // workgroups write the rotated rows to q_out [hq][Tq][D].
+    int64_t q_tok_stride;
+    f16* q_out;
     // Tile images (affine and Int8 prefill): img_w / img hold each key tile's
     // dequantized LDS buffer, [hkv][img_tiles][BUF bytes]; the expansion
     // launch writes them and the attention launch copies them into LDS.
@@ -216,7 +223,8 @@ __device__ __forceinline__ float wave_sum_g(float v) {
 // PM (tile images): 0 none; 1 the expansion launch (workgroup (t, h) writes
 // the image of key tile t of head h and returns); 2 attention from the images
 // (each tile's LDS buffer copied in by LDS-DMA, no dequant in the loop).
-template <int BITS, int D, int RT, bool FAST, int T4M = 0, bool APP = false, int PM = 0>
+template <int BITS, int D, int RT, bool FAST, int T4M = 0, bool APP = false, int PM = 0,
+          bool ROPE = false>
 __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     using S = BlockShape<D>;
     constexpr int KT = S::KT, NSUB = S::NSUB, NM = S::NM, NT = S::NT, NG = S::NG;
@@ -342,16 +350,46 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         float si[VPL], so[VPL];
         t4_lane_signs<D>(a.t4_tab + T4Tab<D>::k_s1, lane, si);
         t4_lane_signs<D>(a.t4_tab + T4Tab<D>::k_s2, lane, so);
+        // ROPE: the angle table in buffer 0, which the prologue leaves alone
+        float2* const rtab = (float2*)lds;
+        if constexpr (ROPE) {
+            rope_fill_table(a.app, a.Tq, rtab, 64 * NW);
+            __syncthreads();
+        }
+        const bool app_writer = ROPE && APP && key_lo > 0;  // writes q_out (one workgroup a head)
         for (int k0 = 0; k0 < (PM == 1 ? 0 : WROWS); k0 += NB) {
             if (row0 + wave + NW * k0 >= a.R) break;  // wave-uniform
             float y[NB][VPL];
 #pragma unroll
             for (int kk = 0; kk < NB; kk++) {
                 const int rho = min(row0 + wave + NW * (k0 + kk), a.R - 1);
-                const f16* qrow = a.q + ((int64_t)(h * a.G + rho % a.G) * a.Tq + rho / a.G) * D;
+                const int qh = h * a.G + rho % a.G, rq = rho / a.G;
+                const f16* qrow = ROPE ? a.q + (int64_t)rq * a.q_tok_stride + (int64_t)qh * D
+                                       : a.q + ((int64_t)qh * a.Tq + rq) * D;
                 const HV w = *(const HV*)(qrow + lane * VPL);
+                if constexpr (ROPE) {
+                    // RoPE first (as the reference's q arrives rotated), then
+                    // the K basis; the half-split partners of the lane's dims
+                    const int d0 = lane * VPL, rh = a.app.rope_dims >> 1;
+                    const bool need = !a.app.traditional && d0 < a.app.rope_dims;
+                    const HV wp = need ? *(const HV*)(qrow + (d0 < rh ? d0 + rh : d0 - rh)) : HV{};
+                    f16 xa[VPL], xpa[VPL], ya[VPL];
 #pragma unroll
-                for (int jj = 0; jj < VPL; jj++) y[kk][jj] = (float)w[jj];
+                    for (int jj = 0; jj < VPL; jj++) {
+                        xa[jj] = w[jj];
+                        xpa[jj] = wp[jj];
+                    }
+                    rope_rotate_dims<VPL>(a.app, rtab, rq, d0, xa, xpa, ya);
+                    const bool own = row0 + wave + NW * (k0 + kk) < a.R;
+#pragma unroll
+                    for (int jj = 0; jj < VPL; jj++) {
+                        y[kk][jj] = (float)ya[jj];
+                        if (app_writer && own) a.q_out[((int64_t)qh * a.Tq + rq) * D + d0 + jj] = ya[jj];
+                    }
+                } else {
+#pragma unroll
+                    for (int jj = 0; jj < VPL; jj++) y[kk][jj] = (float)w[jj];
+                }
             }
 #pragma unroll
             for (int kk = 0; kk < NB; kk++) {
@@ -369,6 +407,48 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         }
         __syncthreads();
     }
+    // ROPE (affine and Int8): the rows rotated first, as the Turbo4 staging
+    // above rotates them (angle table in buffer 0, rows staged in buffer 1,
+    // both free until the first tile's store), and written out by the head's
+    // append workgroup; the conversion below then reads them from LDS
+    f16* const sqr = (f16*)(lds + BUF);
+    if constexpr (ROPE && !T4) {
+        constexpr int VPL = D / 64, NB = 4;
+        using HV = std::conditional_t<VPL == 4, half4v, half2v>;
+        static_assert(NW * WROWS * D * sizeof(f16) <= BUF, "staged q rows exceed a tile buffer");
+        float2* const rtab = (float2*)lds;
+        rope_fill_table(a.app, a.Tq, rtab, 64 * NW);
+        __syncthreads();
+        const bool app_writer = APP && key_lo > 0;
+        for (int k0 = 0; k0 < WROWS; k0 += NB) {
+            if (row0 + wave + NW * k0 >= a.R) break;  // wave-uniform
+#pragma unroll
+            for (int kk = 0; kk < NB; kk++) {
+                const int lr = wave + NW * (k0 + kk), rho = min(row0 + lr, a.R - 1);
+                const int qh = h * a.G + rho % a.G, rq = rho / a.G;
+                const f16* qrow = a.q + (int64_t)rq * a.q_tok_stride + (int64_t)qh * D;
+                const int d0 = lane * VPL, rh = a.app.rope_dims >> 1;
+                const bool need = !a.app.traditional && d0 < a.app.rope_dims;
+                const HV w = *(const HV*)(qrow + d0);
+                const HV wp = need ? *(const HV*)(qrow + (d0 < rh ? d0 + rh : d0 - rh)) : HV{};
+                f16 xa[VPL], xpa[VPL], ya[VPL];
+#pragma unroll
+                for (int jj = 0; jj < VPL; jj++) {
+                    xa[jj] = w[jj];
+                    xpa[jj] = wp[jj];
+                }
+                rope_rotate_dims<VPL>(a.app, rtab, rq, d0, xa, xpa, ya);
+                HV y;
+#pragma unroll
+                for (int jj = 0; jj < VPL; jj++) y[jj] = ya[jj];
+                if (row0 + lr < a.R) {
+                    *(HV*)(sqr + lr * D + d0) = y;
+                    if (app_writer) *(HV*)(a.q_out + ((int64_t)qh * a.Tq + rq) * D + d0) = y;
+                }
+            }
+        }
+        __syncthreads();
+    }
 #pragma unroll
     for (int rt = 0; rt < (PM == 1 ? 0 : RT); rt++) {
         const int rho = wrow0 + 16 * rt + r16;
@@ -376,8 +456,9 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         lim[rt] = row_ok[rt] ? cut(a.causal ? a.T - a.Tq + rho / a.G : a.T - 1) : -1;
         const int rr = row_ok[rt] ? rho : 0;
         // (Turbo4 padding rows read the workgroup's first staged row; their scale is 0)
-        const f16* qrow = T4 ? sq + (row_ok[rt] ? WROWS * wave + 16 * rt + r16 : 0) * D
-                             : a.q + ((int64_t)(h * a.G + rr % a.G) * a.Tq + rr / a.G) * D;
+        const f16* qrow = T4     ? sq + (row_ok[rt] ? WROWS * wave + 16 * rt + r16 : 0) * D
+                          : ROPE ? sqr + (row_ok[rt] ? WROWS * wave + 16 * rt + r16 : 0) * D
+                                 : a.q + ((int64_t)(h * a.G + rr % a.G) * a.Tq + rr / a.G) * D;
         const f16 sc = row_ok[rt] ? (FUSED ? (f16)1.0f : (f16)a.scale_h) : (f16)0.0f;
         const half2v sc2 = {sc, sc};
 #pragma unroll
@@ -404,6 +485,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     }
 
     if constexpr (T4 && PM == 2) __syncthreads();  // staged q read before the first copy
+    if constexpr (ROPE && !T4) __syncthreads();    // the staged rows read before the first store
 
     // ---- tile loads: thread slice j (of PER) -> (key kk, 32-dim slice q32)
     // of K and (8-key block vb, 4 physical dim slots from 4 vj) of V. A
@@ -950,8 +1032,9 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     }
 }
 
-template <int BITS, int D, int RT, int T4M = 0, bool APP = false, int PM = 0>
+template <int BITS, int D, int RT, int T4M = 0, bool APP = false, int PM = 0, bool ROPE = false>
 __global__ __launch_bounds__(64 * block_waves<PM>(), 1) void attend_block_kernel(BlockArgs a) {
+    static_assert(!ROPE || (APP && PM == 0), "RoPE launches are verify blocks that append");
     // two buffers, each a K and a V tile of KT keys in fp16 (~130 KB)
     extern __shared__ __attribute__((aligned(16))) char lds_buf[];
     // The exact 2-op dequant runs without waiting for the cache's fast flag;
@@ -994,26 +1077,26 @@ __global__ __launch_bounds__(64 * block_waves<PM>(), 1) void attend_block_kernel
         // the images hold the dequantized tiles: no dequant, no fast flag
         block_body<BITS, D, RT, false, T4M, APP, 2>(a, lds_buf);
     } else if (T4M == 0 && (BITS == 16 || a.fast_flag != nullptr)) {
-        block_body<BITS, D, RT, true, 0, APP, PM>(a, lds_buf);
+        block_body<BITS, D, RT, true, 0, APP, PM, ROPE>(a, lds_buf);
         if (BITS != 16 && *a.fast_flag == 0) {
             __syncthreads();
-            block_body<BITS, D, RT, false, 0, APP, PM>(a, lds_buf);
+            block_body<BITS, D, RT, false, 0, APP, PM, ROPE>(a, lds_buf);
         }
     } else {
-        block_body<BITS, D, RT, false, T4M, APP, PM>(a, lds_buf);
+        block_body<BITS, D, RT, false, T4M, APP, PM, ROPE>(a, lds_buf);
     }
 }
 
-template <int BITS, int D, int RT, int T4M, bool APP = false, int PM = 0>
+template <int BITS, int D, int RT, int T4M, bool APP = false, int PM = 0, bool ROPE = false>
 static int launch_block_rt(KVCache& cc, BlockArgs& a, int n_qt, hipStream_t stream) {
     // two tile buffers (+ the Turbo4 centroid-pair table)
     const size_t shmem = (size_t)2 * BlockShape<D>::BUF + (T4M ? 256 * sizeof(float2) : 0);
-    int rc = ensure_dynamic_lds((const void*)attend_block_kernel<BITS, D, RT, T4M, APP, PM>, shmem);
+    int rc = ensure_dynamic_lds((const void*)attend_block_kernel<BITS, D, RT, T4M, APP, PM, ROPE>, shmem);
     if (rc) return rc;
     const dim3 grid = a.n_app > 0    ? dim3(a.n_app + cc.hkv * (a.n_split - 1))
                       : a.n_main > 0 ? dim3(a.n_main + n_qt * cc.hkv * a.n_split)
                                      : dim3(a.n_split, n_qt, cc.hkv);
-    hipLaunchKernelGGL((attend_block_kernel<BITS, D, RT, T4M, APP, PM>), grid, dim3(64 * block_waves<PM>()), shmem,
+    hipLaunchKernelGGL((attend_block_kernel<BITS, D, RT, T4M, APP, PM, ROPE>), grid, dim3(64 * block_waves<PM>()), shmem,
                        stream, a);
     QW_HIP_CHECK(hipGetLastError());
     return QW_OK;
@@ -1265,7 +1348,8 @@ int launch_block_attention_t4(KVCache& cc, const f16* q, int G, int n_rows, floa
 template <int BITS, int D, int T4M = 0>
 static int launch_block_append_bits(KVCache& cc, const f16* q, int G, int L, const f16* k_new,
                                     const f16* v_new, float scale, bool causal, f16* out,
-                                    hipStream_t stream, const float* t4_tab = nullptr) {
+                                    hipStream_t stream, const float* t4_tab = nullptr,
+                                    const RowSrc* rope = nullptr, f16* q_out = nullptr) {
     using S = BlockShape<D>;
     const int T_pre = cc.offset, T = T_pre + L, R = G * L;
     BlockArgs a;
@@ -1300,6 +1384,16 @@ static int launch_block_append_bits(KVCache& cc, const f16* q, int G, int L, con
     a.app.v = v_new;
     a.app.row_stride = D;
     a.app.head_stride = (int64_t)L * D;
+    a.q_tok_stride = 0;
+    a.q_out = nullptr;
+    if (rope) {
+        // q is the projection [L][(G hkv + 2 hkv) D]; k_new / v_new are inside it
+        QW_REQUIRE(rope->rope_dims % 16 == 0 && rope->rope_dims <= D && q_out,
+                   QW_ERR_INVALID_ARGUMENT, "block attention: RoPE launch outside its shapes");
+        a.app = *rope;
+        a.q_tok_stride = (int64_t)(G + 2) * cc.hkv * D;
+        a.q_out = q_out;
+    }
     a.img_w = nullptr;
     a.img = nullptr;
     a.img_tiles = 0;
@@ -1315,7 +1409,8 @@ static int launch_block_append_bits(KVCache& cc, const f16* q, int G, int L, con
     if (rc) return rc;
     a.part_o = (float*)cc.ws_ptr;
     a.part_ml = (float2*)((char*)cc.ws_ptr + o_bytes);
-    rc = launch_block_rt<BITS, D, 1, T4M, true>(cc, a, 1, stream);
+    rc = rope ? launch_block_rt<BITS, D, 1, T4M, true, 0, true>(cc, a, 1, stream)
+              : launch_block_rt<BITS, D, 1, T4M, true>(cc, a, 1, stream);
     if (rc) return rc;
     cc.offset = T;
     if (T4M == 2)
@@ -1339,18 +1434,18 @@ bool block_append_fits(const KVCache& cc, int G, int L) {
 
 int launch_block_append_attention(KVCache& cc, const f16* q, int G, int L, const f16* k_new,
                                   const f16* v_new, float scale, bool causal, f16* out,
-                                  hipStream_t stream) {
+                                  hipStream_t stream, const RowSrc* rope, f16* q_out) {
     QW_REQUIRE(block_append_fits(cc, G, L) && cc.offset + L <= cc.cap, QW_ERR_INVALID_ARGUMENT,
                "block attention: verify block outside the fused-append shapes");
     if (cc.D == 256)
         return cc.bits == 4 ? launch_block_append_bits<4, 256>(cc, q, G, L, k_new, v_new, scale,
-                                                               causal, out, stream)
+                                                               causal, out, stream, nullptr, rope, q_out)
                             : launch_block_append_bits<8, 256>(cc, q, G, L, k_new, v_new, scale,
-                                                               causal, out, stream);
+                                                               causal, out, stream, nullptr, rope, q_out);
     return cc.bits == 4 ? launch_block_append_bits<4, 128>(cc, q, G, L, k_new, v_new, scale, causal,
-                                                           out, stream)
+                                                           out, stream, nullptr, rope, q_out)
                         : launch_block_append_bits<8, 128>(cc, q, G, L, k_new, v_new, scale, causal,
-                                                           out, stream);
+                                                           out, stream, nullptr, rope, q_out);
 }
 
 bool block_append_fits_t4(const KVCache& cc, int G, int L) {
@@ -1359,16 +1454,19 @@ bool block_append_fits_t4(const KVCache& cc, int G, int L) {
 
 int launch_block_append_attention_t4(KVCache& cc, const f16* q, int G, int L, const f16* k_new,
                                      const f16* v_new, float scale, bool causal, bool fused,
-                                     const float* tab, f16* out, hipStream_t stream) {
+                                     const float* tab, f16* out, hipStream_t stream,
+                                     const RowSrc* rope, f16* q_out) {
     QW_REQUIRE(block_append_fits_t4(cc, G, L) && cc.offset + L <= cc.cap,
                QW_ERR_INVALID_ARGUMENT, "block attention: Turbo4 block outside the fused-append shapes");
+    QW_REQUIRE(!rope || fused, QW_ERR_INVALID_ARGUMENT,
+               "block attention: Turbo4 RoPE launches take the fused verify pass");
     if (cc.D == 256)
         return fused ? launch_block_append_bits<4, 256, 2>(cc, q, G, L, k_new, v_new, scale, causal,
-                                                           out, stream, tab)
+                                                           out, stream, tab, rope, q_out)
                      : launch_block_append_bits<4, 256, 1>(cc, q, G, L, k_new, v_new, scale, causal,
                                                            out, stream, tab);
     return fused ? launch_block_append_bits<4, 128, 2>(cc, q, G, L, k_new, v_new, scale, causal, out,
-                                                       stream, tab)
+                                                       stream, tab, rope, q_out)
                  : launch_block_append_bits<4, 128, 1>(cc, q, G, L, k_new, v_new, scale, causal, out,
                                                        stream, tab);
 }

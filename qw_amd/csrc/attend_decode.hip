@@ -69,56 +69,6 @@ struct DecodeArgs {
     f16* q_out;
 };
 
-// ROPE: the (cos, sin) table of the launch's query rows, [Tq][rope_dims / 2]
-// in LDS, as the RoPE kernels form each pair's angle (rope_cs), filled by the
-// whole workgroup; the caller's barrier follows.
-__device__ __forceinline__ void decode_rope_table(const DecodeArgs& a, float2* tab, int nthreads) {
-    const int rh = a.app.rope_dims >> 1;
-    for (int i = threadIdx.x; i < a.Tq * rh; i += nthreads) {
-        const int r = i / rh, p = i - r * rh;
-        float c, sn;
-        rope_cs(p, rh, a.app.log2_base, a.app.scale, a.app.position0 + r, c, sn);
-        tab[i] = float2{c, sn};
-    }
-}
-
-// ROPE: dims d0 .. d0 + N - 1 of query row r (x, and xp = the same dims'
-// partners for the half-split pairing), rotated as the RoPE kernels rotate
-// them (rope_rot on the pair, the result rounded to fp16). N divides 8 and
-// d0 is a multiple of N, so with rope_dims a multiple of 16 the N dims sit
-// on one side of rope_dims / 2 and of rope_dims.
-template <int N>
-__device__ __forceinline__ void decode_rope_dims(const DecodeArgs& a, const float2* tab, int r,
-                                                 int d0, const f16 (&x)[N], const f16 (&xp)[N],
-                                                 f16 (&y)[N]) {
-    const int R = a.app.rope_dims, rh = R >> 1;
-#pragma unroll
-    for (int e = 0; e < N; e++) {
-        const int d = d0 + e;
-        if (d >= R) {
-            y[e] = x[e];
-            continue;
-        }
-        bool first;
-        int pr;
-        float partner;
-        if (a.app.traditional) {
-            first = (d & 1) == 0;
-            pr = d >> 1;
-            partner = (float)x[e ^ 1];
-        } else {
-            first = d < rh;
-            pr = first ? d : d - rh;
-            partner = (float)xp[e];
-        }
-        const float2 cs = tab[r * rh + pr];
-        const float xs = (float)x[e];
-        float r1, r2;
-        rope_rot(first ? xs : partner, first ? partner : xs, cs.x, cs.y, r1, r2);
-        y[e] = (f16)(first ? r1 : r2);
-    }
-}
-
 template <int BITS, int D>
 struct DecodeShape {
     static constexpr int NM = D / 32;  // QK MFMAs per 16-key tile
@@ -405,14 +355,14 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
         float yq[2][VPL];
         if constexpr (ROPE) {
             float2* const rtab = (float2*)((char*)sm_o + 16 * D * sizeof(f16));  // behind sm_qr
-            decode_rope_table(a, rtab, 64 * NW);
+            rope_fill_table(a.app, a.Tq, rtab, 64 * NW);
             __syncthreads();
 #pragma unroll
             for (int k = 0; k < 2; k++) {
                 const int row = wave + k * NW;
                 const int rr = row < a.R ? row : 0;
                 f16 yk[VPL];
-                decode_rope_dims<VPL>(a, rtab, rr / a.G, lane * VPL, xq[k], xpq[k], yk);
+                rope_rotate_dims<VPL>(a.app, rtab, rr / a.G, lane * VPL, xq[k], xpq[k], yk);
 #pragma unroll
                 for (int j = 0; j < VPL; j++) yq[k][j] = (float)yk[j];
             }
@@ -462,7 +412,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
                                                                         : half8{};
             load(A, s);
             float2* const rtab = (float2*)sm_o;
-            decode_rope_table(a, rtab, 64 * NW);
+            rope_fill_table(a.app, a.Tq, rtab, 64 * NW);
             __syncthreads();
             f16 xa[8], xpa[8], ya[8];
 #pragma unroll
@@ -470,7 +420,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
                 xa[e] = x[e];
                 xpa[e] = xp[e];
             }
-            decode_rope_dims<8>(a, rtab, rq, base, xa, xpa, ya);
+            rope_rotate_dims<8>(a.app, rtab, rq, base, xa, xpa, ya);
 #pragma unroll
             for (int e = 0; e < 8; e++) x[e] = ya[e];
         }
@@ -1829,11 +1779,13 @@ int KVCache::update_and_attention(const void* q, int n_q_heads, int n_rows, cons
 
 // RoPE, append and attention of one projection: what rope_update (q rotated
 // into q_out, K rotated into the cache, V appended) followed by attention on
-// q_out computes. Decode-route shapes (affine, Int8 and Turbo4 caches, at
-// most 16 rows a KV head, rope_dims a multiple of 16) run it in one decode
-// launch plus the merge: the workgroups rotate their q rows in the prologue
-// and the append unit appends the rotated K with V and writes q_out. Other
-// shapes run the two calls.
+// q_out computes. With rope_dims a multiple of 16 it runs in one launch plus
+// the merge where update_and_attention would append in its attention launch:
+// decode-route shapes (affine, Int8 and Turbo4 caches, at most 16 rows a KV
+// head: the decode launch) and verify blocks (affine and Int8 blocks of 2..128
+// rows a KV head, Turbo4's fused verify pass: the block launch). Its
+// workgroups rotate their q rows in the prologue; the append workgroups append
+// the rotated K with V and write q_out. Other shapes run the two calls.
 int KVCache::rope_update_and_attention(const void* qkv, int n_q_heads, int n_tokens, int rope_dims,
                                        int traditional, float rope_base, float rope_scale,
                                        int position0, float scale, bool causal, void* q_out,
@@ -1845,9 +1797,12 @@ int KVCache::rope_update_and_attention(const void* qkv, int n_q_heads, int n_tok
                QW_ERR_INVALID_ARGUMENT, "rope_update_and_attention: bad RoPE parameters");
     const int G = n_q_heads / hkv, T = offset + n_tokens;
     const bool t4_decode = turbo4() && turbo4_decode_route(*this, causal, n_tokens, G);
-    const bool one_launch = QW_DECODE_APPEND && rope_dims % 16 == 0 && G * n_tokens <= 16 &&
-                            offset >= 1 && (affine() || t4_decode);
-    if (!one_launch) {
+    const bool decode = QW_DECODE_APPEND && rope_dims % 16 == 0 && G * n_tokens <= 16 &&
+                        offset >= 1 && (affine() || t4_decode);
+    const bool block = rope_dims % 16 == 0 && !decode &&
+                       (block_append_fits(*this, G, n_tokens) ||
+                        (turbo4() && turbo4_fused_append_route(*this, causal, n_tokens, G)));
+    if (!decode && !block) {
         int rc = rope_update(qkv, n_q_heads, n_tokens, rope_dims, traditional, rope_base, rope_scale,
                              position0, q_out, stream);
         if (rc) return rc;
@@ -1872,6 +1827,13 @@ int KVCache::rope_update_and_attention(const void* qkv, int n_q_heads, int n_tok
     rs.scale = rope_scale;
     const f16* q = (const f16*)qkv;
     f16 *qo = (f16*)q_out, *oo = (f16*)out;
+    if (block) {
+        if (turbo4())
+            return launch_block_append_attention_t4(*this, q, G, n_tokens, rs.k, rs.v, scale, causal,
+                                                    true, t4_tables, oo, stream, &rs, qo);
+        return launch_block_append_attention(*this, q, G, n_tokens, rs.k, rs.v, scale, causal, oo,
+                                             stream, &rs, qo);
+    }
     if (turbo4())
         return launch_turbo4_decode_rope_append(*this, q, G, n_tokens, rs, scale, causal, t4_tables,
                                                 qo, oo, stream);

@@ -238,7 +238,8 @@ int dlsa_sparse_attention_typed(const void* q, int q_dtype, const void* k, const
 // the rows rotated back), else its fp16 arithmetic (out: rotated-basis rows).
 int launch_block_append_attention_t4(KVCache& c, const f16* q, int G, int n_rows, const f16* k_new,
                                      const f16* v_new, float scale, bool causal, bool fused,
-                                     const float* tab, f16* out, hipStream_t stream);
+                                     const float* tab, f16* out, hipStream_t stream,
+                                     const RowSrc* rope = nullptr, f16* q_out = nullptr);
 // A Turbo4 decode-route call (G * n_rows <= 16, at least one cached row,
 // capacity reserved) that appends its n_rows rows in the decode launch (its
 // append unit) and attends them with the cached prefix; out as
@@ -249,14 +250,19 @@ int launch_turbo4_decode_append(KVCache& c, const f16* q, int G, int n_rows, con
 // Whether a Turbo4 update-and-attention of n_rows rows takes the decode route
 // (the append unit in the decode launch).
 bool turbo4_decode_route(const KVCache& c, bool causal, int n_rows, int G);
+// Whether it takes the fused verify pass with the rows appended in its launch.
+bool turbo4_fused_append_route(const KVCache& c, bool causal, int n_rows, int G);
 // Turbo4 update-and-attention: the append in the block kernel's launch where
 // the call takes the block kernel, else turbo4_update then turbo4_attention.
 int turbo4_update_and_attention(KVCache& c, const void* q, int n_q_heads, int n_rows,
                                 const void* k_new, const void* v_new, float scale, bool causal,
                                 void* out, hipStream_t stream);
+// rope (a RoPE launch): q is the projection and k_new / v_new point into it
+// through *rope; the rotated q rows go to q_out.
 int launch_block_append_attention(KVCache& c, const f16* q, int G, int n_rows, const f16* k_new,
                                   const f16* v_new, float scale, bool causal, f16* out,
-                                  hipStream_t stream);
+                                  hipStream_t stream, const RowSrc* rope = nullptr,
+                                  f16* q_out = nullptr);
 // Split-K merge: out[row0 + row] = sum_c e^(m_c - M) O_c / sum_c e^(m_c - M) l_c
 // over nc partials of [rstride][D] fp32 rows per KV head, rows 0 .. R-1.
 // slot_bits == 0: partial rows in dim order; 4/8/16: in the V plane's slot

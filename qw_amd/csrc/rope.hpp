@@ -79,4 +79,59 @@ __device__ __forceinline__ float rope_elem(const f16* __restrict__ row, int d, i
     return first ? r1 : r2;
 }
 
+
+// Launches that rotate a few query rows in their prologue (the decode and
+// block kernels' RoPE launches) share one angle table: (cos, sin) of (row r,
+// pair p) at [r * rope_dims / 2 + p], for position rs.position0 + r, formed by
+// rope_cs as every RoPE path forms it. nthreads threads of the workgroup fill
+// it; the caller's barrier follows.
+template <class Src>
+__device__ __forceinline__ void rope_fill_table(const Src& rs, int n_rows, float2* tab,
+                                                int nthreads) {
+    const int rh = rs.rope_dims >> 1;
+    for (int i = threadIdx.x; i < n_rows * rh; i += nthreads) {
+        const int r = i / rh, p = i - r * rh;
+        float c, sn;
+        rope_cs(p, rh, rs.log2_base, rs.scale, rs.position0 + r, c, sn);
+        tab[i] = float2{c, sn};
+    }
+}
+
+// Dims d0 .. d0 + N - 1 of query row r rotated as the RoPE kernels rotate
+// them (rope_rot on the pair, the result rounded to fp16): x the dims, xp
+// their half-split partners (unused for the adjacent pairing). N divides 8
+// and d0 is a multiple of N, so with rope_dims a multiple of 16 the N dims sit
+// on one side of rope_dims / 2 and of rope_dims.
+template <int N, class Src>
+__device__ __forceinline__ void rope_rotate_dims(const Src& rs, const float2* tab, int r, int d0,
+                                                 const f16 (&x)[N], const f16 (&xp)[N],
+                                                 f16 (&y)[N]) {
+    const int R = rs.rope_dims, rh = R >> 1;
+#pragma unroll
+    for (int e = 0; e < N; e++) {
+        const int d = d0 + e;
+        if (d >= R) {
+            y[e] = x[e];
+            continue;
+        }
+        bool first;
+        int pr;
+        float partner;
+        if (rs.traditional) {
+            first = (d & 1) == 0;
+            pr = d >> 1;
+            partner = (float)x[e ^ 1];
+        } else {
+            first = d < rh;
+            pr = first ? d : d - rh;
+            partner = (float)xp[e];
+        }
+        const float2 cs = tab[r * rh + pr];
+        const float xs = (float)x[e];
+        float r1, r2;
+        rope_rot(first ? xs : partner, first ? partner : xs, cs.x, cs.y, r1, r2);
+        y[e] = (f16)(first ? r1 : r2);
+    }
+}
+
 }  // namespace qw

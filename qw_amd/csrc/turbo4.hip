@@ -846,6 +846,11 @@ static int turbo4_block(KVCache& c, const void* q, int n_q_heads, int n_rows, fl
     return QW_OK;
 }
 
+bool turbo4_fused_append_route(const KVCache& c, bool causal, int n_rows, int G) {
+    return QW_T4_APPEND && QW_T4_BLOCK && t4_fused_route(causal, n_rows, c.offset + n_rows, G) &&
+           block_append_fits_t4(c, G, n_rows);
+}
+
 bool turbo4_decode_route(const KVCache& c, bool causal, int n_rows, int G) {
     return !t4_fused_route(causal, n_rows, c.offset + n_rows, G) && QW_T4_FUSED_DECODE &&
            G * n_rows <= 16 && c.offset >= 1;

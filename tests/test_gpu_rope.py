@@ -181,6 +181,8 @@ def test_rope_update_affine4_matches_oracle_quantize():
     (256, 256, True, 2, 700),    # a 2-row causal block, every dim rotated, adjacent pairs
     (128, 64, False, 1, 2500),
     (128, 128, True, 2, 40),
+    (256, 64, False, 4, 3000),   # verify blocks: the block launch (Turbo4: the fused pass)
+    (128, 128, True, 5, 2600),
 ])
 def test_rope_update_and_attention_equals_the_two_reference_calls(mode, D, R, trad, L, T0):
     """Bit for bit against fused_rope_qk_append followed by
@@ -218,16 +220,17 @@ def test_rope_update_and_attention_equals_the_two_reference_calls(mode, D, R, tr
     b.close()
 
 
-@pytest.mark.parametrize("mode,R,L", [
-    ("affine4", 64, 4),   # 24 rows a KV head: the block route
-    ("affine8", 24, 1),   # rope_dims not a multiple of 16
-    ("fp16", 64, 1),      # an fp16 cache
+@pytest.mark.parametrize("mode,R,L,T0", [
+    ("affine4", 64, 4, 100),    # a verify block over fewer than 256 cached rows
+    ("affine8", 24, 1, 1500),   # rope_dims not a multiple of 16
+    ("fp16", 64, 1, 1500),      # an fp16 cache
+    ("turbo4", 64, 4, 1500),    # a Turbo4 block under 2048 keys: no fused pass
 ])
-def test_rope_update_and_attention_other_shapes_are_the_two_calls(mode, R, L):
-    """Shapes outside the one-launch route run rope_update and attention."""
+def test_rope_update_and_attention_other_shapes_are_the_two_calls(mode, R, L, T0):
+    """Shapes outside the one-launch routes run rope_update and attention."""
     import qw_amd
 
-    hq, hkv, D, T0, base = 24, 4, 256, 1500, 1e6
+    hq, hkv, D, base = 24, 4, 256, 1e6
     print(f"mode {mode} R {R} L {L}", flush=True)
     r = rng(41 + L)
     k0 = _gpu(r.standard_normal((hkv, T0, D)).astype(np.float16))
