@@ -152,6 +152,12 @@ constexpr bool kSetprio(int pm) {
     return QW_BLOCK_SETPRIO == 2 || (QW_BLOCK_SETPRIO == 1 && pm != 2);
 }
 
+// Key-split row tiles (block_body): 1 for workgroups of 5 or 6 row tiles, 2
+// also for those of 1 or 2; 0 off.
+#ifndef QW_BLOCK_KSPLIT
+#define QW_BLOCK_KSPLIT 2
+#endif
+
 template <int D>
 struct BlockShape {
     static constexpr int KT = 16384 / D;  // keys a tile (64 at D=256, 128 at D=128)
@@ -310,6 +316,38 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
             wrow0 = min(wrow0, a.R);
         }
     }
+    // Key-split row tiles: a workgroup of 5 or 6 row tiles (one per wave
+    // leaves SIMDs 0 and 1 two tiles each, SIMDs 2 and 3 one) gives its
+    // tiles 4 and 5 to waves 4..7, each wave computing half of every key tile
+    // (tile 4: waves 4 and 6, SIMDs 0 and 2; tile 5: waves 5 and 7), so each
+    // SIMD carries 1.5 tiles; one of 1 or 2 row tiles splits them over waves
+    // 0..3, one half a SIMD. The two halves' (m, l, O) meet before the
+    // epilogue (the same combine as the split merge).
+    // (not in the affine / Int8 launches that append: measured 0.5-1 us slower
+    // there, where the attention-only launches gain 1-1.5 us and the Turbo4
+    // fused pass 7.7 us at 4 rows)
+    constexpr bool KS_OK = QW_BLOCK_KSPLIT && PM == 0 && RT == 1 && NW == 8 && NSUB % 2 == 0 &&
+                           (!APP || T4);
+    bool ks_any = false, ks_half = false;
+    int ks_ub = 0;  // the wave's first sub-block of a tile
+    if constexpr (KS_OK) {
+        const int n_rt = (row_last - row0) / 16 + 1;
+        if (n_rt == 5 || n_rt == 6) {
+            ks_any = true;
+            if (wave >= 4) {
+                ks_half = true;
+                wrow0 = row0 + 16 * (4 + (wave & 1));
+                ks_ub = ((wave >> 1) & 1) * (NSUB / 2);
+            }
+        } else if (n_rt <= 2 && QW_BLOCK_KSPLIT >= 2) {
+            ks_any = true;
+            if (wave < 4) {
+                ks_half = true;
+                wrow0 = row0 + 16 * (wave & 1);
+                ks_ub = ((wave >> 1) & 1) * (NSUB / 2);
+            }
+        }
+    }
     auto cut = [&](int lim_) { return APP ? min(lim_, key_hi - 1) : lim_; };
     const bool app_unit = APP && key_lo > 0;
     const int wg_lim = cut(a.causal ? a.T - a.Tq + row_last / a.G : a.T - 1);
@@ -456,8 +494,8 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         lim[rt] = row_ok[rt] ? cut(a.causal ? a.T - a.Tq + rho / a.G : a.T - 1) : -1;
         const int rr = row_ok[rt] ? rho : 0;
         // (Turbo4 padding rows read the workgroup's first staged row; their scale is 0)
-        const f16* qrow = T4     ? sq + (row_ok[rt] ? WROWS * wave + 16 * rt + r16 : 0) * D
-                          : ROPE ? sqr + (row_ok[rt] ? WROWS * wave + 16 * rt + r16 : 0) * D
+        const f16* qrow = T4     ? sq + (row_ok[rt] ? wrow0 - row0 + 16 * rt + r16 : 0) * D
+                          : ROPE ? sqr + (row_ok[rt] ? wrow0 - row0 + 16 * rt + r16 : 0) * D
                                  : a.q + ((int64_t)(h * a.G + rr % a.G) * a.Tq + rr / a.G) * D;
         const f16 sc = row_ok[rt] ? (FUSED ? (f16)1.0f : (f16)a.scale_h) : (f16)0.0f;
         const half2v sc2 = {sc, sc};
@@ -651,7 +689,9 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     // One tile (keys kt0 .. kt0 + KT - 1) out of buffer b: the QK MFMAs of all
     // its 32-key sub-blocks first (independent chains), one softmax step over
     // the whole tile (one max reduction, one lazy-rescale check), then P.V.
-    auto tile = [&](int b, int kt0) {
+    // (NU of the tile's NSUB sub-blocks, from sub-block ub: a key-split wave's half)
+    auto tile = [&](int b, int kt0, auto nu_c, int ub) {
+        constexpr int NU = decltype(nu_c)::value;
         const half8* sK8 = (const half8*)(lds + BUF * b);
         const half8* sV8 = (const half8*)(lds + BUF * b + KBUF);
         // S^T: A row r16 of 16-key MFMA tile (u, tt) is key 32u + 8(r16>>2) +
@@ -662,9 +702,9 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         const int b4 = (key0 >> 4) & 1;
         const half8* kbase0 = sK8 + g * KT + key0 + 4 * b4;
         const half8* kbase1 = sK8 + g * KT + key0 + 4 * (b4 ^ 1);
-        float4v acc[NSUB][2][RT];
+        float4v acc[NU][2][RT];
 #pragma unroll
-        for (int u = 0; u < NSUB; u++)
+        for (int u = 0; u < NU; u++)
 #pragma unroll
             for (int tt = 0; tt < 2; tt++)
 #pragma unroll
@@ -673,9 +713,9 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
 #pragma unroll
         for (int m = 0; m < NM; m++) {
 #pragma unroll
-            for (int u = 0; u < NSUB; u++) {
+            for (int u = 0; u < NU; u++) {
                 // chunk g + 4m of keys key0 + 32u (+4): kswz leaves bits >= 5 alone
-                const half8 ka = kbase0[4 * m * KT + 32 * u], kb2 = kbase1[4 * m * KT + 32 * u];
+                const half8 ka = kbase0[4 * m * KT + 32 * (ub + u)], kb2 = kbase1[4 * m * KT + 32 * (ub + u)];
 #pragma unroll
                 for (int rt = 0; rt < RT; rt++) {
                     acc[u][0][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[rt][m], acc[u][0][rt], 0, 0, 0);
@@ -685,7 +725,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         }
 #if QW_BLOCK_SCHED_QK
         if constexpr (RT == 1) {
-            constexpr int NQ = NM * NSUB * 2, AH = QW_BLOCK_SCHED_QK;
+            constexpr int NQ = NM * NU * 2, AH = QW_BLOCK_SCHED_QK;
             __builtin_amdgcn_sched_group_barrier(0x100, AH, 0);
 #pragma unroll
             for (int i = 0; i < NQ - AH; i++) {
@@ -696,33 +736,33 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         }
 #endif
         if constexpr (kSetprio(PM) && !FUSED) __builtin_amdgcn_s_setprio(0);
-        half8 pop[NSUB][RT];
+        half8 pop[NU][RT];
         // Scores -> fp16 rounding -> (mask) -> online softmax -> P; the mask
         // only for tiles some row of the wave cannot fully see (a scalar
         // branch around the compares: the common case carries none).
         const bool mask = kt0 + KT - 1 > wave_first_lim || (APP && kt0 < key_lo);
-        half8 popl[FUSED ? NSUB : 1][RT];  // fused pass: the remainders p - f16(p)
+        half8 popl[FUSED ? NU : 1][RT];  // fused pass: the remainders p - f16(p)
         auto softmax_fused = [&]() {
 #pragma unroll
             for (int rt = 0; rt < RT; rt++) {
                 // fp32 scores in the log2 domain (q carries scale * log2 e)
-                float sf[NSUB][8];
+                float sf[NU][8];
 #pragma unroll
-                for (int u = 0; u < NSUB; u++)
+                for (int u = 0; u < NU; u++)
 #pragma unroll
                     for (int e = 0; e < 8; e++) sf[u][e] = acc[u][e >> 2][rt][e & 3];
                 if (mask) {
 #pragma unroll
-                    for (int u = 0; u < NSUB; u++)
+                    for (int u = 0; u < NU; u++)
 #pragma unroll
                         for (int e = 0; e < 8; e++) {
-                            const int key = kt0 + 32 * u + 8 * g + (e & 3) + 4 * (e >> 2);
+                            const int key = kt0 + 32 * (ub + u) + 8 * g + (e & 3) + 4 * (e >> 2);
                             if (key > lim[rt] || (APP && key < key_lo)) sf[u][e] = -INFINITY;
                         }
                 }
                 float mx_lane = sf[0][0];
 #pragma unroll
-                for (int u = 0; u < NSUB; u++)
+                for (int u = 0; u < NU; u++)
 #pragma unroll
                     for (int e = 0; e < 8; e++) mx_lane = fmaxf(mx_lane, sf[u][e]);
                 // lazy reference in log2 units (p <= 2^5.5)
@@ -744,7 +784,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
                 }
                 const float mref = m_run[rt] == -INFINITY ? 0.0f : m_run[rt];
 #pragma unroll
-                for (int u = 0; u < NSUB; u++)
+                for (int u = 0; u < NU; u++)
 #pragma unroll
                     for (int e = 0; e < 8; e++) {
                         const float p = __builtin_amdgcn_exp2f(sf[u][e] - mref);
@@ -761,9 +801,9 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
                 // MLX rounds the score matrix to fp16 before the softmax: the
                 // scores stay packed in fp16 pairs (element e of pair j is
                 // score 2j + e: keys 32u + 8g + (idx & 3) + 4 (idx >> 2)).
-                half2v sh[NSUB][4];
+                half2v sh[NU][4];
 #pragma unroll
-                for (int u = 0; u < NSUB; u++)
+                for (int u = 0; u < NU; u++)
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
                         const float4v& av = acc[u][j >> 1][rt];
@@ -771,13 +811,13 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
                     }
                 if (mask) {
 #pragma unroll
-                    for (int u = 0; u < NSUB; u++)
+                    for (int u = 0; u < NU; u++)
 #pragma unroll
                         for (int j = 0; j < 4; j++)
 #pragma unroll
                             for (int e = 0; e < 2; e++) {
                                 const int idx = 2 * j + e;
-                                const int key = kt0 + 32 * u + 8 * g + (idx & 3) + 4 * (idx >> 2);
+                                const int key = kt0 + 32 * (ub + u) + 8 * g + (idx & 3) + 4 * (idx >> 2);
                                 if (key > lim[rt] || (APP && key < key_lo)) sh[u][j][e] = (f16)(-INFINITY);
                             }
                 }
@@ -786,7 +826,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
                 // inside fp16).
                 half2v m2 = sh[0][0];
 #pragma unroll
-                for (int u = 0; u < NSUB; u++)
+                for (int u = 0; u < NU; u++)
 #pragma unroll
                     for (int j = 0; j < 4; j++) m2 = __builtin_elementwise_max(m2, sh[u][j]);
                 // the lane's own maximum decides (m_run is the same in the
@@ -812,7 +852,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
                 }
                 const float mref2 = (m_run[rt] == -INFINITY ? 0.0f : m_run[rt]) * kLog2e;
 #pragma unroll
-                for (int u = 0; u < NSUB; u++)
+                for (int u = 0; u < NU; u++)
 #pragma unroll
                     for (int e = 0; e < 8; e++) {
                         const float x = (float)sh[u][e >> 1][e & 1];
@@ -830,8 +870,8 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         // V block 4u + g, i.e. keys 32u + 8g .. +7.
         if constexpr (kSetprio(PM) && !FUSED) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-        for (int u = 0; u < NSUB; u++) {
-            const half8* vb8 = sV8 + (4 * u + g) * VROW + r16;
+        for (int u = 0; u < NU; u++) {
+            const half8* vb8 = sV8 + (4 * (ub + u) + g) * VROW + r16;
 #pragma unroll
             for (int mm = 0; mm < NT; mm++) {
                 const half8 vv = vb8[17 * mm];  // slot 16mm + r16
@@ -847,7 +887,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         }
 #if QW_BLOCK_SCHED_PV
         if constexpr (RT == 1) {
-            constexpr int NQ = NSUB * NT, AH = QW_BLOCK_SCHED_PV;
+            constexpr int NQ = NU * NT, AH = QW_BLOCK_SCHED_PV;
             __builtin_amdgcn_sched_group_barrier(0x100, AH, 1);
 #pragma unroll
             for (int i = 0; i < NQ - AH; i++) {
@@ -859,6 +899,8 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
 #endif
         if constexpr (kSetprio(PM) && !FUSED) __builtin_amdgcn_s_setprio(0);
     };
+
+    auto run_tile = [&](int b, int kt0) { tile(b, kt0, std::integral_constant<int, NSUB>{}, 0); };
 
     if constexpr (PM == 1) {
         // the expansion: tile blockIdx.x's buffer, as the main loop stores
@@ -909,56 +951,114 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         for (int t = t0; t < t1; t++) {
             const int b = (t - t0) & 1;
             if (t + 1 < t1) dma(t + 1, b ^ 1);
-            if (wave_live && t * KT <= wave_lim) tile(b, t * KT);
+            if (wave_live && t * KT <= wave_lim) run_tile(b, t * KT);
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
         }
     } else {
-    // ---- main loop: round t dequantizes tile t+1 into LDS buffer (t+1)&1
-    // from its register stage, reuses that stage for the loads of tile
-    // t + 1 + QW_BLOCK_STAGES, and computes tile t from buffer t&1; one
-    // barrier a round. Two register stages keep two tiles of loads in flight
-    // behind the tile being computed, which the key-split verify launches
-    // (one tile of math a round) need to cover HBM latency.
+    // (one copy of the loop a tile shape, chosen outside it: a key-split
+    // wave's half tile inside the same loop body as the whole tile pushed the
+    // kernel to 256 VGPRs with spills; both copies run one barrier a round)
+    auto main_loop = [&](auto nu_c, int ub) {
+        // ---- main loop: round t dequantizes tile t+1 into LDS buffer (t+1)&1
+        // from its register stage, reuses that stage for the loads of tile
+        // t + 1 + QW_BLOCK_STAGES, and computes tile t from buffer t&1; one
+        // barrier a round. Two register stages keep two tiles of loads in flight
+        // behind the tile being computed, which the key-split verify launches
+        // (one tile of math a round) need to cover HBM latency.
 #if QW_BLOCK_STAGES == 2
-    Stage s0, s1;
-    if (t0 < t1) {
-        load(s0, t0);
-        store(s0, 0);
-        if (t0 + 1 < t1) load(s0, t0 + 1);
-        if (t0 + 2 < t1) load(s1, t0 + 2);
-    }
-    __syncthreads();
-    auto round = [&](Stage& sa, int t, int b) {
-        if (t + 1 < t1) {
-            store(sa, b ^ 1);
-            if (t + 3 < t1) load(sa, t + 3);
+        Stage s0, s1;
+        if (t0 < t1) {
+            load(s0, t0);
+            store(s0, 0);
+            if (t0 + 1 < t1) load(s0, t0 + 1);
+            if (t0 + 2 < t1) load(s1, t0 + 2);
         }
-        if (wave_live && t * KT <= wave_lim) tile(b, t * KT);
         __syncthreads();
-    };
-    for (int t = t0; t < t1; t += 2) {
-        round(s0, t, 0);
-        if (t + 1 < t1) round(s1, t + 1, 1);
-    }
+        auto round = [&](Stage& sa, int t, int b) {
+            if (t + 1 < t1) {
+                store(sa, b ^ 1);
+                if (t + 3 < t1) load(sa, t + 3);
+            }
+            if (wave_live && t * KT <= wave_lim) tile(b, t * KT, nu_c, ub);
+            __syncthreads();
+        };
+        for (int t = t0; t < t1; t += 2) {
+            round(s0, t, 0);
+            if (t + 1 < t1) round(s1, t + 1, 1);
+        }
 #else
-    Stage st;
-    if (t0 < t1) {
-        load(st, t0);
-        store(st, 0);
-        if (t0 + 1 < t1) load(st, t0 + 1);
-    }
-    __syncthreads();
-    for (int t = t0; t < t1; t++) {
-        const int b = (t - t0) & 1;
-        if (t + 1 < t1) {
-            store(st, b ^ 1);
-            if (t + 2 < t1) load(st, t + 2);
+        Stage st;
+        if (t0 < t1) {
+            load(st, t0);
+            store(st, 0);
+            if (t0 + 1 < t1) load(st, t0 + 1);
         }
-        if (wave_live && t * KT <= wave_lim) tile(b, t * KT);
         __syncthreads();
-    }
+        for (int t = t0; t < t1; t++) {
+            const int b = (t - t0) & 1;
+            if (t + 1 < t1) {
+                store(st, b ^ 1);
+                if (t + 2 < t1) load(st, t + 2);
+            }
+            if (wave_live && t * KT <= wave_lim) tile(b, t * KT, nu_c, ub);
+            __syncthreads();
+        }
 #endif
+    };
+    if constexpr (KS_OK) {
+        if (ks_half)
+            main_loop(std::integral_constant<int, NSUB / 2>{}, ks_ub);
+        else
+            main_loop(std::integral_constant<int, NSUB>{}, 0);
+    } else {
+        main_loop(std::integral_constant<int, NSUB>{}, 0);
+    }
+    }
+
+    // ---- key-split halves: the second half of each split tile (sub-blocks
+    // from NSUB/2) parks its (m, l, O) in tile buffer 0, which the loop's
+    // last barrier freed; the first half combines them into its own.
+    if constexpr (KS_OK) {
+        if (ks_any) {
+            // slot = the tile's parity: [2][64 lanes] (m, l), then [2][NT][64] O
+            float2* const kml = (float2*)lds;
+            float4v* const ko = (float4v*)(lds + 2 * 64 * sizeof(float2));
+            const int slot = ((wrow0 - row0) >> 4) & 1;
+            if (ks_half && ks_ub != 0 && wave_live) {
+                kml[slot * 64 + lane] = float2{m_run[0], l_run[0]};
+#pragma unroll
+                for (int mm = 0; mm < NT; mm++) ko[(slot * NT + mm) * 64 + lane] = acc_o[0][mm];
+            }
+            __syncthreads();
+            if (ks_half && ks_ub == 0 && wave_live) {
+                const float2 mlb = kml[slot * 64 + lane];
+                const float ma = m_run[0], mb = mlb.x, M = fmaxf(ma, mb);
+                // (the fused pass's maxima are in log2 units)
+                auto fac = [&](float mx) {
+                    return mx == -INFINITY ? 0.0f
+                                           : __builtin_amdgcn_exp2f(FUSED ? mx - M : (mx - M) * kLog2e);
+                };
+                const float fa = fac(ma), fb = fac(mb);
+                l_run[0] = l_run[0] * fa + mlb.y * fb;
+                float fai[4], fbi[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    fai[i] = __shfl(fa, 4 * g + i);
+                    fbi[i] = __shfl(fb, 4 * g + i);
+                }
+#pragma unroll
+                for (int mm = 0; mm < NT; mm++) {
+                    const float4v ob = ko[(slot * NT + mm) * 64 + lane];
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        acc_o[0][mm][i] = __builtin_fmaf(acc_o[0][mm][i], fai[i], ob[i] * fbi[i]);
+                }
+                m_run[0] = M;
+            }
+            // the second halves write nothing
+            if (ks_half && ks_ub != 0) return;
+        }
     }
 
     // ---- epilogue: per column, the row sum over the 4 lane groups.
