@@ -157,6 +157,9 @@ constexpr bool kSetprio(int pm) {
 #ifndef QW_BLOCK_KSPLIT
 #define QW_BLOCK_KSPLIT 2
 #endif
+#ifndef QW_BLOCK_KSPLIT_APP
+#define QW_BLOCK_KSPLIT_APP 0
+#endif
 
 template <int D>
 struct BlockShape {
@@ -327,7 +330,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     // there, where the attention-only launches gain 1-1.5 us and the Turbo4
     // fused pass 7.7 us at 4 rows)
     constexpr bool KS_OK = QW_BLOCK_KSPLIT && PM == 0 && RT == 1 && NW == 8 && NSUB % 2 == 0 &&
-                           (!APP || T4);
+                           (!APP || T4 || QW_BLOCK_KSPLIT_APP);
     bool ks_any = false, ks_half = false;
     int ks_ub = 0;  // the wave's first sub-block of a tile
     if constexpr (KS_OK) {
