@@ -286,6 +286,11 @@ struct SdpaOptions {
 int sdpa_general(const void* q, int n_q_heads, int n_rows, const void* k, const void* v,
                  int n_kv_heads, int n_keys, int head_dim, int64_t khs, int64_t krs, int64_t vhs,
                  int64_t vrs, float scale, const SdpaOptions& o, void* out, hipStream_t stream);
+// The first key any of n_rows causal windowed rows over T keys sees (0 without
+// a window), rounded down to a multiple of align; and the options of a call on
+// keys lo .. n_keys - 1 only (the mask's columns shifted by lo).
+int window_first_key(const SdpaOptions& o, int T, int n_rows, int align = 1);
+SdpaOptions shift_keys(const SdpaOptions& o, int lo);
 // Over a cache: without mask, softcap or window the cache's own fused
 // attention; else its rows dequantized (Turbo4: expanded in the rotated basis,
 // q rotated in and the output rotated back) and sdpa_general.

@@ -411,6 +411,21 @@ int sdpa_general(const void* q, int n_q_heads, int n_rows, const void* k, const 
     return QW_OK;
 }
 
+int window_first_key(const SdpaOptions& o, int T, int n_rows, int align) {
+    if (o.window <= 0 || !o.causal) return 0;
+    const int lo = std::max(0, T - n_rows - o.window + 1);
+    return lo / align * align;
+}
+
+SdpaOptions shift_keys(const SdpaOptions& o, int lo) {
+    SdpaOptions s = o;
+    if (s.mask && lo > 0) {
+        const int es = o.mask_dtype == QW_MASK_BOOL ? 1 : o.mask_dtype == QW_DTYPE_F32 ? 4 : 2;
+        s.mask = (const char*)o.mask + (int64_t)lo * es;  // key stride 1
+    }
+    return s;
+}
+
 int cache_attention_general(KVCache& c, const void* q, int n_q_heads, int n_rows, float scale,
                             const SdpaOptions& o, void* out, hipStream_t stream) {
     QW_REQUIRE(q && out, QW_ERR_INVALID_ARGUMENT, "attention: null q/out");
@@ -426,14 +441,20 @@ int cache_attention_general(KVCache& c, const void* q, int n_q_heads, int n_rows
     DeviceGuard dg(c.device);
     QW_REQUIRE(dg.ok, QW_ERR_HIP, "attention: hipSetDevice failed");
     const int T = c.offset, D = c.D;
-    const size_t bytes = (size_t)c.hkv * T * D * sizeof(f16);
+    // A sliding window sees no key below lo (the first row's window start):
+    // only keys lo .. T - 1 are dequantized, and the call runs on them with
+    // the positions (p - lo) and mask columns shifted alike.
+    const int lo = window_first_key(o, T, n_rows);
+    const int n = T - lo;
+    const size_t bytes = (size_t)c.hkv * n * D * sizeof(f16);
     void* ws = nullptr;
     if (int rc = gen_kv_workspace(c.device, stream, 2 * bytes, &ws)) return rc;
     char* kw = (char*)ws;
     char* vw = kw + bytes;
-    if (int rc = c.dequantize(0, T, kw, vw, stream)) return rc;  // [hkv][T][D] rows
-    return sdpa_general(q, n_q_heads, n_rows, kw, vw, c.hkv, T, D, (int64_t)T * D, D,
-                        (int64_t)T * D, D, scale, o, out, stream);
+    if (int rc = c.dequantize(lo, n, kw, vw, stream)) return rc;  // [hkv][n][D] rows
+    const SdpaOptions os = shift_keys(o, lo);
+    return sdpa_general(q, n_q_heads, n_rows, kw, vw, c.hkv, n, D, (int64_t)n * D, D,
+                        (int64_t)n * D, D, scale, os, out, stream);
 }
 
 }  // namespace qw

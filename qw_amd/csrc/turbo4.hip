@@ -167,7 +167,7 @@ template <int D, bool VROWS = false>
 __global__ __launch_bounds__(D) void turbo4_expand_kernel(
     const uint8_t* __restrict__ k_packed, const uint32_t* __restrict__ k_side,
     const uint8_t* __restrict__ v_packed, const uint32_t* __restrict__ v_side,
-    const float* __restrict__ tab, int cap, int T, int capv, f16* __restrict__ kw,
+    const float* __restrict__ tab, int cap, int T, int capv, int b0, f16* __restrict__ kw,
     f16* __restrict__ vw) {
     constexpr int CPK = D / 8;  // 8-coordinate chunks a key
     constexpr int NB = kExpandBlocks;
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(D) void turbo4_expand_kernel(
     uint32_t kb[NB], vb[NB], ks[NB], vs[NB];
 #pragma unroll
     for (int n = 0; n < NB; n++) {
-        const int t = (blockIdx.x * NB + n) * 8 + k;
+        const int t = (b0 + blockIdx.x * NB + n) * 8 + k;
         kb[n] = vb[n] = ks[n] = vs[n] = 0u;
         if (t < T) {
             const int64_t r = (int64_t)h * cap + t;
@@ -193,7 +193,7 @@ __global__ __launch_bounds__(D) void turbo4_expand_kernel(
     __syncthreads();  // s_cb
 #pragma unroll
     for (int n = 0; n < NB; n++) {
-        const int blk = blockIdx.x * NB + n;
+        const int blk = b0 + blockIdx.x * NB + n;
         const int t = blk * 8 + k;
         half8 kv8, vv8;
         if (t < T) {
@@ -966,6 +966,9 @@ static int turbo4_expansion_route(KVCache& c, const void* q, int n_q_heads, int 
     const int qrows = n_q_heads * n_rows;
     const float* tab = c.t4_tables;
     const int capv = (T + 255) / 256 * 256;
+    // with a sliding window only keys from lo (a multiple of 256) are expanded
+    // and attended; the rows keep their places in the [hkv][capv][D] planes
+    const int lo = opts ? window_first_key(*opts, T, n_rows, 256) : 0;
     const size_t kv_bytes = (size_t)c.hkv * capv * D * sizeof(f16);
     const size_t q_bytes = (size_t)n_q_heads * n_rows * D * sizeof(f16);
     const size_t need = 2 * kv_bytes + 2 * q_bytes;
@@ -978,7 +981,8 @@ static int turbo4_expansion_route(KVCache& c, const void* q, int n_q_heads, int 
     f16* o_rot = (f16*)((char*)wbuf + 2 * kv_bytes + q_bytes);
     // Every 8-key block up to capv: rows past T become zeros, as the fp16
     // cache's unused rows are, since the fp16 kernels read whole tiles.
-    dim3 eg(capv / (8 * kExpandBlocks), c.hkv);
+    dim3 eg((capv - lo) / (8 * kExpandBlocks), c.hkv);
+    const int b0 = lo / 8;  // first 8-key block expanded
     if (D == 256) {
         using TT = T4Tab<256>;
         hipLaunchKernelGGL(turbo4_rotate_kernel<256>, dim3((qrows + 3) / 4), dim3(256), 0, stream,
@@ -986,11 +990,11 @@ static int turbo4_expansion_route(KVCache& c, const void* q, int n_q_heads, int 
         if (opts)
             hipLaunchKernelGGL((turbo4_expand_kernel<256, true>), eg, dim3(256), 0, stream,
                                (const uint8_t*)c.k_data, c.k_params, (const uint8_t*)c.v_data,
-                               c.v_params, tab, c.cap, T, capv, kw, vw);
+                               c.v_params, tab, c.cap, T, capv, b0, kw, vw);
         else
             hipLaunchKernelGGL(turbo4_expand_kernel<256>, eg, dim3(256), 0, stream,
                                (const uint8_t*)c.k_data, c.k_params, (const uint8_t*)c.v_data,
-                               c.v_params, tab, c.cap, T, capv, kw, vw);
+                               c.v_params, tab, c.cap, T, capv, b0, kw, vw);
     } else {
         using TT = T4Tab<128>;
         hipLaunchKernelGGL(turbo4_rotate_kernel<128>, dim3((qrows + 3) / 4), dim3(256), 0, stream,
@@ -998,18 +1002,19 @@ static int turbo4_expansion_route(KVCache& c, const void* q, int n_q_heads, int 
         if (opts)
             hipLaunchKernelGGL((turbo4_expand_kernel<128, true>), eg, dim3(128), 0, stream,
                                (const uint8_t*)c.k_data, c.k_params, (const uint8_t*)c.v_data,
-                               c.v_params, tab, c.cap, T, capv, kw, vw);
+                               c.v_params, tab, c.cap, T, capv, b0, kw, vw);
         else
             hipLaunchKernelGGL(turbo4_expand_kernel<128>, eg, dim3(128), 0, stream,
                                (const uint8_t*)c.k_data, c.k_params, (const uint8_t*)c.v_data,
-                               c.v_params, tab, c.cap, T, capv, kw, vw);
+                               c.v_params, tab, c.cap, T, capv, b0, kw, vw);
     }
     QW_HIP_CHECK(hipGetLastError());
     int rc;
     if (opts) {
         // rotated K and V rows, [hkv][capv][D]
-        rc = sdpa_general(q_rot, n_q_heads, n_rows, kw, vw, c.hkv, T, D, (int64_t)capv * D, D,
-                          (int64_t)capv * D, D, scale, *opts, o_rot, stream);
+        rc = sdpa_general(q_rot, n_q_heads, n_rows, kw + (int64_t)lo * D, vw + (int64_t)lo * D,
+                          c.hkv, T - lo, D, (int64_t)capv * D, D, (int64_t)capv * D, D, scale,
+                          shift_keys(*opts, lo), o_rot, stream);
     } else {
         // The rotated K/V seen as an fp16 cache (not owning its planes); it
         // borrows the Turbo4 cache's split-K workspace.

@@ -170,6 +170,50 @@ def test_turbo4_masked_route():
     assert_close(out, ref, "turbo4 masked")
 
 
+@pytest.mark.parametrize("mode", ["affine4", "int8", "turbo4"])
+def test_cache_window_reads_only_the_window(mode):
+    """A sliding window over a long cache: only the keys from the first row's
+    window start are dequantized (Turbo4: expanded from the 256-key boundary
+    below it), with the positions and an additive mask's columns shifted
+    alike; the result is the windowed attention over the whole cache."""
+    import qw_amd
+
+    print(f"case window slice {mode}", flush=True)
+    r = rng(95 + len(mode))
+    hq, hkv, D, T0, L, W = 24, 4, 256, 5000, 3, 700
+    T = T0 + L
+    k = r.standard_normal((hkv, T, D)).astype(np.float16)
+    v = r.standard_normal((hkv, T, D)).astype(np.float16)
+    q = r.standard_normal((hq, L, D)).astype(np.float16)
+    cache = qw_amd.KVCache(mode, hkv, D)
+    cache.update(_gpu(k), _gpu(v))
+    # an additive mask over all T keys whose finite columns below the window
+    # would change the result if the shift were off by any amount
+    m = (r.standard_normal((L, T)) * 2).astype(np.float16)
+    m[:, T - W - L + 5::11] = -np.inf
+    for softcap, mask in ((0.0, None), (0.0, m), (15.0, m)):
+        out = _np(cache.attention_general(_gpu(q), 1 / 16, causal=True, window=W,
+                                          softcap=softcap,
+                                          mask=None if mask is None else _gpu(mask)))[0]
+        if mode == "turbo4":
+            t = cache.snapshot_tensors()
+            snap = {n: _np(x) for n, x in t.items()}
+            for n in ("k_rescale", "v_rescale"):
+                snap[n] = snap[n][..., 0]
+            tab = oracle.turbo4_tables(D)
+            q_rot = oracle.turbo4_rotate(q.astype(np.float64), tab["k_s1"],
+                                         tab["k_s2"]).astype(np.float16)
+            k_rot = oracle.turbo4_expand_rotated(snap["k_packed"], snap["k_rescale"], tab)
+            v_rot = oracle.turbo4_expand_rotated(snap["v_packed"], snap["v_rescale"], tab)
+            o_rot = oracle.sdpa_general(q_rot, k_rot, v_rot, 1 / 16, True, W, softcap, mask)
+            ref = oracle.turbo4_rotate(o_rot.astype(np.float64), tab["v_s2"],
+                                       tab["v_s1"]).astype(np.float16)
+        else:
+            kd, vd = (_np(x)[0] for x in cache.dequantize())
+            ref = oracle.sdpa_general(q, kd, vd, 1 / 16, True, W, softcap, mask)
+        assert_close(out, ref, f"{mode} window {W} softcap {softcap} mask {mask is not None}")
+
+
 def test_general_contract_errors():
     import qw_amd
 
