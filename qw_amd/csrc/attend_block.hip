@@ -90,6 +90,9 @@ struct BlockArgs {
     // so every workgroup sees about the same number of (row, key) pairs.
     int pair_h;
     const float* t4_tab;  // Turbo4 caches: the device tables (signs, centroids: T4Tab<D>)
+    // WIN launches (a causal sliding window): the row at position p sees keys
+    // p - window + 1 .. p
+    int window = 0;
     float t4_post;        // Turbo4 fused pass: scale * log2(e) in fp32
     float scale_h;      // f16(scale) as float
     uint32_t code_off2; // magic offset pair of the separately rounded dequant
@@ -233,7 +236,7 @@ __device__ __forceinline__ float wave_sum_g(float v) {
 // the image of key tile t of head h and returns); 2 attention from the images
 // (each tile's LDS buffer copied in by LDS-DMA, no dequant in the loop).
 template <int BITS, int D, int RT, bool FAST, int T4M = 0, bool APP = false, int PM = 0,
-          bool ROPE = false>
+          bool ROPE = false, bool WIN = false>
 __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     using S = BlockShape<D>;
     constexpr int KT = S::KT, NSUB = S::NSUB, NM = S::NM, NT = S::NT, NG = S::NG;
@@ -330,7 +333,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     // there, where the attention-only launches gain 1-1.5 us and the Turbo4
     // fused pass 7.7 us at 4 rows)
     constexpr bool KS_OK = QW_BLOCK_KSPLIT && PM == 0 && RT == 1 && NW == 8 && NSUB % 2 == 0 &&
-                           (!APP || T4 || QW_BLOCK_KSPLIT_APP);
+                           (!APP || T4 || QW_BLOCK_KSPLIT_APP) && !WIN;
     bool ks_any = false, ks_half = false;
     int ks_ub = 0;  // the wave's first sub-block of a tile
     if constexpr (KS_OK) {
@@ -355,7 +358,10 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     const bool app_unit = APP && key_lo > 0;
     const int wg_lim = cut(a.causal ? a.T - a.Tq + row_last / a.G : a.T - 1);
     const int n_tiles = (a.T + KT - 1) / KT;
-    const int t0 = app_unit ? key_lo / KT : sp * tiles_per_split;
+    // WIN: the splits cover the keys from the first tile any of the
+    // workgroup's rows sees (its first row's window start)
+    const int t_win = WIN ? max(0, a.T - a.Tq + row0 / a.G - a.window + 1) / KT : 0;
+    const int t0 = app_unit ? key_lo / KT : t_win + sp * tiles_per_split;
     const int t1 = app_unit ? wg_lim / KT + 1 : min(min(n_tiles, t0 + tiles_per_split), wg_lim / KT + 1);
 
     // ---- the wave's RT x 16 query rows as the B operand of S^T = K . Q'^T
@@ -367,8 +373,12 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     // the smallest key limit of the wave's live rows (padding rows see nothing
     // and are never written, so they do not count)
     const int wave_first_lim = cut(a.causal ? a.T - a.Tq + wrow0 / a.G : a.T - 1);
-    int lim[RT];
+    int lim[RT], wlo[RT];  // (WIN) the row's first visible key
     bool row_ok[RT];
+    // WIN: the window start of the wave's last row (tiles below it need the
+    // mask) and of its first row (tiles wholly below it are skipped)
+    const int wave_lo_max = WIN ? a.T - a.Tq + wave_last / a.G - a.window + 1 : 0;
+    const int wave_lo_min = WIN ? a.T - a.Tq + wrow0 / a.G - a.window + 1 : 0;
     half8 qb[RT][NM];
     // Turbo4: the workgroup's rows are rotated into the K basis (the rotation
     // kernels' arithmetic; wave w takes rows w, w + NW, ..., four at a time
@@ -495,6 +505,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         const int rho = wrow0 + 16 * rt + r16;
         row_ok[rt] = rho < a.R;
         lim[rt] = row_ok[rt] ? cut(a.causal ? a.T - a.Tq + rho / a.G : a.T - 1) : -1;
+        wlo[rt] = WIN && row_ok[rt] ? a.T - a.Tq + rho / a.G - a.window + 1 : 0;
         const int rr = row_ok[rt] ? rho : 0;
         // (Turbo4 padding rows read the workgroup's first staged row; their scale is 0)
         const f16* qrow = T4     ? sq + (row_ok[rt] ? wrow0 - row0 + 16 * rt + r16 : 0) * D
@@ -743,7 +754,8 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         // Scores -> fp16 rounding -> (mask) -> online softmax -> P; the mask
         // only for tiles some row of the wave cannot fully see (a scalar
         // branch around the compares: the common case carries none).
-        const bool mask = kt0 + KT - 1 > wave_first_lim || (APP && kt0 < key_lo);
+        const bool mask = kt0 + KT - 1 > wave_first_lim || (APP && kt0 < key_lo) ||
+                          (WIN && kt0 < wave_lo_max);
         half8 popl[FUSED ? NU : 1][RT];  // fused pass: the remainders p - f16(p)
         auto softmax_fused = [&]() {
 #pragma unroll
@@ -760,7 +772,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
 #pragma unroll
                         for (int e = 0; e < 8; e++) {
                             const int key = kt0 + 32 * (ub + u) + 8 * g + (e & 3) + 4 * (e >> 2);
-                            if (key > lim[rt] || (APP && key < key_lo)) sf[u][e] = -INFINITY;
+                            if (key > lim[rt] || (APP && key < key_lo) || (WIN && key < wlo[rt])) sf[u][e] = -INFINITY;
                         }
                 }
                 float mx_lane = sf[0][0];
@@ -821,7 +833,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
                             for (int e = 0; e < 2; e++) {
                                 const int idx = 2 * j + e;
                                 const int key = kt0 + 32 * (ub + u) + 8 * g + (idx & 3) + 4 * (idx >> 2);
-                                if (key > lim[rt] || (APP && key < key_lo)) sh[u][j][e] = (f16)(-INFINITY);
+                                if (key > lim[rt] || (APP && key < key_lo) || (WIN && key < wlo[rt])) sh[u][j][e] = (f16)(-INFINITY);
                             }
                 }
                 // Online softmax with a lazy reference: m_run moves only when a
@@ -983,7 +995,8 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
                 store(sa, b ^ 1);
                 if (t + 3 < t1) load(sa, t + 3);
             }
-            if (wave_live && t * KT <= wave_lim) tile(b, t * KT, nu_c, ub);
+            if (wave_live && t * KT <= wave_lim && (!WIN || (t + 1) * KT > wave_lo_min))
+                    tile(b, t * KT, nu_c, ub);
             __syncthreads();
         };
         for (int t = t0; t < t1; t += 2) {
@@ -1004,7 +1017,8 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
                 store(st, b ^ 1);
                 if (t + 2 < t1) load(st, t + 2);
             }
-            if (wave_live && t * KT <= wave_lim) tile(b, t * KT, nu_c, ub);
+            if (wave_live && t * KT <= wave_lim && (!WIN || (t + 1) * KT > wave_lo_min))
+                    tile(b, t * KT, nu_c, ub);
             __syncthreads();
         }
 #endif
@@ -1135,9 +1149,11 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     }
 }
 
-template <int BITS, int D, int RT, int T4M = 0, bool APP = false, int PM = 0, bool ROPE = false>
+template <int BITS, int D, int RT, int T4M = 0, bool APP = false, int PM = 0, bool ROPE = false,
+          bool WIN = false>
 __global__ __launch_bounds__(64 * block_waves<PM>(), 1) void attend_block_kernel(BlockArgs a) {
     static_assert(!ROPE || (APP && PM == 0), "RoPE launches are verify blocks that append");
+    static_assert(!WIN || (PM == 0 && !APP && T4M == 0), "window launches attend a cache as it is");
     // two buffers, each a K and a V tile of KT keys in fp16 (~130 KB)
     extern __shared__ __attribute__((aligned(16))) char lds_buf[];
     // The exact 2-op dequant runs without waiting for the cache's fast flag;
@@ -1180,26 +1196,27 @@ __global__ __launch_bounds__(64 * block_waves<PM>(), 1) void attend_block_kernel
         // the images hold the dequantized tiles: no dequant, no fast flag
         block_body<BITS, D, RT, false, T4M, APP, 2>(a, lds_buf);
     } else if (T4M == 0 && (BITS == 16 || a.fast_flag != nullptr)) {
-        block_body<BITS, D, RT, true, 0, APP, PM, ROPE>(a, lds_buf);
+        block_body<BITS, D, RT, true, 0, APP, PM, ROPE, WIN>(a, lds_buf);
         if (BITS != 16 && *a.fast_flag == 0) {
             __syncthreads();
-            block_body<BITS, D, RT, false, 0, APP, PM, ROPE>(a, lds_buf);
+            block_body<BITS, D, RT, false, 0, APP, PM, ROPE, WIN>(a, lds_buf);
         }
     } else {
-        block_body<BITS, D, RT, false, T4M, APP, PM, ROPE>(a, lds_buf);
+        block_body<BITS, D, RT, false, T4M, APP, PM, ROPE, WIN>(a, lds_buf);
     }
 }
 
-template <int BITS, int D, int RT, int T4M, bool APP = false, int PM = 0, bool ROPE = false>
+template <int BITS, int D, int RT, int T4M, bool APP = false, int PM = 0, bool ROPE = false,
+          bool WIN = false>
 static int launch_block_rt(KVCache& cc, BlockArgs& a, int n_qt, hipStream_t stream) {
     // two tile buffers (+ the Turbo4 centroid-pair table)
     const size_t shmem = (size_t)2 * BlockShape<D>::BUF + (T4M ? 256 * sizeof(float2) : 0);
-    int rc = ensure_dynamic_lds((const void*)attend_block_kernel<BITS, D, RT, T4M, APP, PM, ROPE>, shmem);
+    int rc = ensure_dynamic_lds((const void*)attend_block_kernel<BITS, D, RT, T4M, APP, PM, ROPE, WIN>, shmem);
     if (rc) return rc;
     const dim3 grid = a.n_app > 0    ? dim3(a.n_app + cc.hkv * (a.n_split - 1))
                       : a.n_main > 0 ? dim3(a.n_main + n_qt * cc.hkv * a.n_split)
                                      : dim3(a.n_split, n_qt, cc.hkv);
-    hipLaunchKernelGGL((attend_block_kernel<BITS, D, RT, T4M, APP, PM, ROPE>), grid, dim3(64 * block_waves<PM>()), shmem,
+    hipLaunchKernelGGL((attend_block_kernel<BITS, D, RT, T4M, APP, PM, ROPE, WIN>), grid, dim3(64 * block_waves<PM>()), shmem,
                        stream, a);
     QW_HIP_CHECK(hipGetLastError());
     return QW_OK;
@@ -1240,16 +1257,16 @@ static int pick_rt(int R, int hkv) {
     return best;
 }
 
-template <int BITS, int D, int T4M, int PM = 0>
+template <int BITS, int D, int T4M, int PM = 0, bool WIN = false>
 static int launch_one(KVCache& cc, BlockArgs a, int rt, int n_qt, hipStream_t stream) {
     int rc = QW_OK;
     if constexpr (QW_BLOCK_MAX_RT >= 3 || QW_BLOCK_RT == 3) {
-        if (rt == 3) rc = launch_block_rt<BITS, D, 3, T4M, false, PM>(cc, a, n_qt, stream);
+        if (rt == 3) rc = launch_block_rt<BITS, D, 3, T4M, false, PM, false, WIN>(cc, a, n_qt, stream);
     }
     if constexpr (QW_BLOCK_MAX_RT >= 2 || QW_BLOCK_RT == 2) {
-        if (rt == 2) rc = launch_block_rt<BITS, D, 2, T4M, false, PM>(cc, a, n_qt, stream);
+        if (rt == 2) rc = launch_block_rt<BITS, D, 2, T4M, false, PM, false, WIN>(cc, a, n_qt, stream);
     }
-    if (rt == 1) rc = launch_block_rt<BITS, D, 1, T4M, false, PM>(cc, a, n_qt, stream);
+    if (rt == 1) rc = launch_block_rt<BITS, D, 1, T4M, false, PM, false, WIN>(cc, a, n_qt, stream);
     return rc;
 }
 
@@ -1299,9 +1316,12 @@ static void split_keys(int n_tiles, int want, int* n_split, int* tps) {
     *n_split = (n_tiles + *tps - 1) / *tps;
 }
 
+// window > 0 (causal, T4M = 0): the WIN kernels, splits over the keys a query
+// tile's windows span
 template <int BITS, int D, int T4M = 0>
 static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float scale, bool causal,
-                             f16* out, hipStream_t stream, const float* t4_tab = nullptr) {
+                             f16* out, hipStream_t stream, const float* t4_tab = nullptr,
+                             int window = 0) {
     using S = BlockShape<D>;
     const int T = cc.offset;
     const int R = G * Tq;
@@ -1309,7 +1329,7 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     // long prefill calls dequantize (fp16: lay out) each key tile once into an
     // image of its LDS buffer and attend from the images, in query tiles of
     // 16 kImageWaves rows
-    const bool images = QW_BLOCK_IMAGES && T4M != 2 &&
+    const bool images = QW_BLOCK_IMAGES && T4M != 2 && window <= 0 &&
                         R >= (T4M ? kT4ImageMinRows : kImageMinRows) && n_tiles > 0;
     const int rt = images ? 1 : pick_rt(R, cc.hkv);
     const int wg_rows = 16 * (images ? kImageWaves : kBlockWaves) * rt;
@@ -1350,6 +1370,7 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     a.img = nullptr;
     a.img_tiles = n_tiles;
     a.pair_h = 0;
+    a.window = window > 0 ? window : 0;
     int rc;
     if constexpr (T4M != 2) {
         if (images) {
@@ -1385,6 +1406,9 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
         if constexpr (T4M != 2) {
             if (images) return launch_one<BITS, D, T4M, 2>(cc, x, rt, n_qt_, stream);
         }
+        if constexpr (T4M == 0) {
+            if (window > 0) return launch_one<BITS, D, 0, 0, true>(cc, x, rt, n_qt_, stream);
+        }
         return launch_one<BITS, D, T4M>(cc, x, rt, n_qt_, stream);
     };
     if (q_main > 0 && (q_tail == 0 || !QW_BLOCK_ONE_LAUNCH)) {
@@ -1400,7 +1424,10 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     if (q_tail == 0) return QW_OK;
     int n_split, tps;
     const int want = std::max(1, 256 / (q_tail * cc.hkv));
-    split_keys(n_tiles, T4M == 2 ? std::min(std::max(want, 2), 128) : want, &n_split, &tps);
+    // (a window: the keys from a query tile's first window start to its last row)
+    const int plan_tiles =
+        window > 0 ? std::min(n_tiles, (window + wg_rows / G + 1 + S::KT - 1) / S::KT + 1) : n_tiles;
+    split_keys(plan_tiles, T4M == 2 ? std::min(std::max(want, 2), 128) : want, &n_split, &tps);
     QW_REQUIRE(T4M != 2 || n_split > 1, QW_ERR_INVALID_ARGUMENT,
                "block attention: fused Turbo4 pass needs at least 5 key tiles");
     BlockArgs t = a;
@@ -1430,6 +1457,22 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
         return launch_partial_merge(t.part_o, t.part_ml, n_split, t.PR, t.prow0, t.PR, cc.hkv, D,
                                     G, Tq, out, stream, T4M ? 16 : BITS);
     return QW_OK;
+}
+
+int launch_block_attention_window(KVCache& cc, const f16* q, int G, int n_rows, float scale,
+                                  int window, f16* out, hipStream_t stream) {
+    QW_REQUIRE(cc.affine() || cc.bits == 16, QW_ERR_INVALID_ARGUMENT,
+               "block attention: windowed route is for affine, Int8 and fp16 caches");
+    QW_REQUIRE(window > 0 && (cc.D == 128 || cc.D == 256), QW_ERR_INVALID_ARGUMENT,
+               "block attention: window launch outside its shapes");
+    if (cc.D == 256) {
+        if (cc.bits == 4) return launch_block_bits<4, 256>(cc, q, G, n_rows, scale, true, out, stream, nullptr, window);
+        if (cc.bits == 8) return launch_block_bits<8, 256>(cc, q, G, n_rows, scale, true, out, stream, nullptr, window);
+        return launch_block_bits<16, 256>(cc, q, G, n_rows, scale, true, out, stream, nullptr, window);
+    }
+    if (cc.bits == 4) return launch_block_bits<4, 128>(cc, q, G, n_rows, scale, true, out, stream, nullptr, window);
+    if (cc.bits == 8) return launch_block_bits<8, 128>(cc, q, G, n_rows, scale, true, out, stream, nullptr, window);
+    return launch_block_bits<16, 128>(cc, q, G, n_rows, scale, true, out, stream, nullptr, window);
 }
 
 int launch_block_attention_t4(KVCache& cc, const f16* q, int G, int n_rows, float scale,

@@ -214,6 +214,45 @@ def test_cache_window_reads_only_the_window(mode):
         assert_close(out, ref, f"{mode} window {W} softcap {softcap} mask {mask is not None}")
 
 
+WIN_CASES = [
+    # mode, hq, hkv, D, T (after the rows), L, window
+    ("affine4", 24, 4, 256, 32769, 1, 4096),   # a windowed decode step at the c2 geometry
+    ("affine4", 24, 4, 256, 9000, 4, 1000),    # a verify block
+    ("affine8", 24, 4, 256, 5000, 37, 300),    # 222 rows a KV head: two query tiles
+    ("int8", 16, 2, 128, 3000, 5, 64),
+    ("fp16", 8, 8, 128, 2500, 300, 700),       # a prefill chunk whose windows slide
+    ("affine4", 6, 1, 128, 700, 3, 1),         # every row sees only its own key
+    ("affine8", 24, 4, 256, 1200, 2, 5000),    # a window wider than the cache
+]
+
+
+@pytest.mark.parametrize("mode,hq,hkv,D,T,L,W", WIN_CASES)
+def test_cache_window_fused_route(mode, hq, hkv, D, T, L, W):
+    """A causal sliding window without mask or softcap over an affine, Int8 or
+    fp16 cache runs the block kernel on the codes (a lower bound on each
+    row's keys, splits over the keys the windows span): checked against the
+    oracle on the cache's own dequantized rows."""
+    import qw_amd
+
+    print(f"case window fused {mode} hq={hq} hkv={hkv} D={D} T={T} L={L} W={W}", flush=True)
+    r = rng(700 + L + W % 97)
+    k = r.standard_normal((hkv, T, D)).astype(np.float16)
+    v = r.standard_normal((hkv, T, D)).astype(np.float16)
+    q = r.standard_normal((hq, L, D)).astype(np.float16)
+    cache = qw_amd.KVCache(mode, hkv, D)
+    cache.update(_gpu(k), _gpu(v))
+    out = _np(cache.attention_general(_gpu(q), D ** -0.5, causal=True, window=W))[0]
+    kd, vd = (_np(x)[0] for x in cache.dequantize())
+    ref = oracle.sdpa_general(q, kd, vd, D ** -0.5, True, W)
+    assert_close(out, ref, f"{mode} window {W} L {L}")
+    if W == 1:
+        # one visible key: the row is that key's V row, exactly
+        G = hq // hkv
+        for h in range(hq):
+            np.testing.assert_array_equal(out[h], vd[h // G, T - L:T])
+    cache.close()
+
+
 def test_general_contract_errors():
     import qw_amd
 
