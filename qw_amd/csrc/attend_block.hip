@@ -93,6 +93,8 @@ struct BlockArgs {
     // WIN launches (a causal sliding window): the row at position p sees keys
     // p - window + 1 .. p
     int window = 0;
+    // CAP launches (a logit softcap): s = tanh(f16(q . k) scale / softcap) softcap
+    float softcap = 0.0f, scale = 0.0f;
     float t4_post;        // Turbo4 fused pass: scale * log2(e) in fp32
     float scale_h;      // f16(scale) as float
     uint32_t code_off2; // magic offset pair of the separately rounded dequant
@@ -236,7 +238,7 @@ __device__ __forceinline__ float wave_sum_g(float v) {
 // the image of key tile t of head h and returns); 2 attention from the images
 // (each tile's LDS buffer copied in by LDS-DMA, no dequant in the loop).
 template <int BITS, int D, int RT, bool FAST, int T4M = 0, bool APP = false, int PM = 0,
-          bool ROPE = false, bool WIN = false>
+          bool ROPE = false, bool WIN = false, bool CAP = false>
 __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     using S = BlockShape<D>;
     constexpr int KT = S::KT, NSUB = S::NSUB, NM = S::NM, NT = S::NT, NG = S::NG;
@@ -511,7 +513,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         const f16* qrow = T4     ? sq + (row_ok[rt] ? wrow0 - row0 + 16 * rt + r16 : 0) * D
                           : ROPE ? sqr + (row_ok[rt] ? wrow0 - row0 + 16 * rt + r16 : 0) * D
                                  : a.q + ((int64_t)(h * a.G + rr % a.G) * a.Tq + rr / a.G) * D;
-        const f16 sc = row_ok[rt] ? (FUSED ? (f16)1.0f : (f16)a.scale_h) : (f16)0.0f;
+        const f16 sc = row_ok[rt] ? (FUSED || CAP ? (f16)1.0f : (f16)a.scale_h) : (f16)0.0f;
         const half2v sc2 = {sc, sc};
 #pragma unroll
         for (int m = 0; m < NM; m++) {
@@ -756,7 +758,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         // branch around the compares: the common case carries none).
         const bool mask = kt0 + KT - 1 > wave_first_lim || (APP && kt0 < key_lo) ||
                           (WIN && kt0 < wave_lo_max);
-        half8 popl[FUSED ? NU : 1][RT];  // fused pass: the remainders p - f16(p)
+        half8 popl[FUSED || CAP ? NU : 1][RT];  // fp32 P: the remainders p - f16(p)
         auto softmax_fused = [&]() {
 #pragma unroll
             for (int rt = 0; rt < RT; rt++) {
@@ -807,6 +809,65 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
                         const f16 ph = (f16)p;
                         pop[u][rt][e] = ph;
                         if constexpr (FUSED) popl[u][rt][e] = (f16)(p - (float)ph);
+                    }
+            }
+        };
+        // CAP: the softcap composite's arithmetic (compiled_softcap_sdpa,
+        // mlx_cxx_bridge.cpp:1573-1590): S = f16(q . k) with q unscaled, then
+        // in fp32 s = tanh(S scale / cap) cap, the softmax in fp32 and P.V
+        // with fp32 P (an fp16 high part and an fp16 remainder)
+        auto softmax_cap = [&]() {
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++) {
+                float sf[NU][8];
+#pragma unroll
+                for (int u = 0; u < NU; u++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        const float x = (float)(f16)acc[u][e >> 2][rt][e & 3];
+                        sf[u][e] = tanhf(x * a.scale / a.softcap) * a.softcap;
+                    }
+                if (mask) {
+#pragma unroll
+                    for (int u = 0; u < NU; u++)
+#pragma unroll
+                        for (int e = 0; e < 8; e++) {
+                            const int key = kt0 + 32 * (ub + u) + 8 * g + (e & 3) + 4 * (e >> 2);
+                            if (key > lim[rt] || (WIN && key < wlo[rt])) sf[u][e] = -INFINITY;
+                        }
+                }
+                float mx_lane = sf[0][0];
+#pragma unroll
+                for (int u = 0; u < NU; u++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) mx_lane = fmaxf(mx_lane, sf[u][e]);
+                if (__any(mx_lane > m_run[rt] + 5.5f)) {
+                    const float m_new = fmaxf(m_run[rt], wave_max_g(mx_lane));
+                    if (__any(m_run[rt] != -INFINITY)) {
+                        const float alpha = m_run[rt] == -INFINITY
+                                                ? 0.0f
+                                                : __builtin_amdgcn_exp2f((m_run[rt] - m_new) * kLog2e);
+                        l_run[rt] *= alpha;
+                        float f[4];
+#pragma unroll
+                        for (int i = 0; i < 4; i++) f[i] = __shfl(alpha, 4 * g + i);
+#pragma unroll
+                        for (int mm = 0; mm < NT; mm++)
+#pragma unroll
+                            for (int i = 0; i < 4; i++) acc_o[rt][mm][i] *= f[i];
+                    }
+                    m_run[rt] = m_new;
+                }
+                const float mref2 = (m_run[rt] == -INFINITY ? 0.0f : m_run[rt]) * kLog2e;
+#pragma unroll
+                for (int u = 0; u < NU; u++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sf[u][e], kLog2e, -mref2));
+                        l_run[rt] += p;
+                        const f16 ph = (f16)p;
+                        pop[u][rt][e] = ph;
+                        if constexpr (CAP) popl[u][rt][e] = (f16)(p - (float)ph);
                     }
             }
         };
@@ -879,6 +940,8 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
         };
         if constexpr (FUSED)
             softmax_fused();
+        else if constexpr (CAP)
+            softmax_cap();
         else
             softmax();
         // O += P . V: B = slot 16mm + r16 (column r16 of output tile mm) of
@@ -894,7 +957,7 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
                 for (int rt = 0; rt < RT; rt++) {
                     acc_o[rt][mm] =
                         __builtin_amdgcn_mfma_f32_16x16x32_f16(pop[u][rt], vv, acc_o[rt][mm], 0, 0, 0);
-                    if constexpr (FUSED)
+                    if constexpr (FUSED || CAP)
                         acc_o[rt][mm] =
                             __builtin_amdgcn_mfma_f32_16x16x32_f16(popl[u][rt], vv, acc_o[rt][mm], 0, 0, 0);
                 }
@@ -1150,10 +1213,11 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
 }
 
 template <int BITS, int D, int RT, int T4M = 0, bool APP = false, int PM = 0, bool ROPE = false,
-          bool WIN = false>
+          bool WIN = false, bool CAP = false>
 __global__ __launch_bounds__(64 * block_waves<PM>(), 1) void attend_block_kernel(BlockArgs a) {
     static_assert(!ROPE || (APP && PM == 0), "RoPE launches are verify blocks that append");
     static_assert(!WIN || (PM == 0 && !APP && T4M == 0), "window launches attend a cache as it is");
+    static_assert(!CAP || WIN, "softcap launches are window launches (an unbounded window)");
     // two buffers, each a K and a V tile of KT keys in fp16 (~130 KB)
     extern __shared__ __attribute__((aligned(16))) char lds_buf[];
     // The exact 2-op dequant runs without waiting for the cache's fast flag;
@@ -1196,27 +1260,27 @@ __global__ __launch_bounds__(64 * block_waves<PM>(), 1) void attend_block_kernel
         // the images hold the dequantized tiles: no dequant, no fast flag
         block_body<BITS, D, RT, false, T4M, APP, 2>(a, lds_buf);
     } else if (T4M == 0 && (BITS == 16 || a.fast_flag != nullptr)) {
-        block_body<BITS, D, RT, true, 0, APP, PM, ROPE, WIN>(a, lds_buf);
+        block_body<BITS, D, RT, true, 0, APP, PM, ROPE, WIN, CAP>(a, lds_buf);
         if (BITS != 16 && *a.fast_flag == 0) {
             __syncthreads();
-            block_body<BITS, D, RT, false, 0, APP, PM, ROPE, WIN>(a, lds_buf);
+            block_body<BITS, D, RT, false, 0, APP, PM, ROPE, WIN, CAP>(a, lds_buf);
         }
     } else {
-        block_body<BITS, D, RT, false, T4M, APP, PM, ROPE, WIN>(a, lds_buf);
+        block_body<BITS, D, RT, false, T4M, APP, PM, ROPE, WIN, CAP>(a, lds_buf);
     }
 }
 
 template <int BITS, int D, int RT, int T4M, bool APP = false, int PM = 0, bool ROPE = false,
-          bool WIN = false>
+          bool WIN = false, bool CAP = false>
 static int launch_block_rt(KVCache& cc, BlockArgs& a, int n_qt, hipStream_t stream) {
     // two tile buffers (+ the Turbo4 centroid-pair table)
     const size_t shmem = (size_t)2 * BlockShape<D>::BUF + (T4M ? 256 * sizeof(float2) : 0);
-    int rc = ensure_dynamic_lds((const void*)attend_block_kernel<BITS, D, RT, T4M, APP, PM, ROPE, WIN>, shmem);
+    int rc = ensure_dynamic_lds((const void*)attend_block_kernel<BITS, D, RT, T4M, APP, PM, ROPE, WIN, CAP>, shmem);
     if (rc) return rc;
     const dim3 grid = a.n_app > 0    ? dim3(a.n_app + cc.hkv * (a.n_split - 1))
                       : a.n_main > 0 ? dim3(a.n_main + n_qt * cc.hkv * a.n_split)
                                      : dim3(a.n_split, n_qt, cc.hkv);
-    hipLaunchKernelGGL((attend_block_kernel<BITS, D, RT, T4M, APP, PM, ROPE, WIN>), grid, dim3(64 * block_waves<PM>()), shmem,
+    hipLaunchKernelGGL((attend_block_kernel<BITS, D, RT, T4M, APP, PM, ROPE, WIN, CAP>), grid, dim3(64 * block_waves<PM>()), shmem,
                        stream, a);
     QW_HIP_CHECK(hipGetLastError());
     return QW_OK;
@@ -1257,16 +1321,16 @@ static int pick_rt(int R, int hkv) {
     return best;
 }
 
-template <int BITS, int D, int T4M, int PM = 0, bool WIN = false>
+template <int BITS, int D, int T4M, int PM = 0, bool WIN = false, bool CAP = false>
 static int launch_one(KVCache& cc, BlockArgs a, int rt, int n_qt, hipStream_t stream) {
     int rc = QW_OK;
     if constexpr (QW_BLOCK_MAX_RT >= 3 || QW_BLOCK_RT == 3) {
-        if (rt == 3) rc = launch_block_rt<BITS, D, 3, T4M, false, PM, false, WIN>(cc, a, n_qt, stream);
+        if (rt == 3) rc = launch_block_rt<BITS, D, 3, T4M, false, PM, false, WIN, CAP>(cc, a, n_qt, stream);
     }
     if constexpr (QW_BLOCK_MAX_RT >= 2 || QW_BLOCK_RT == 2) {
-        if (rt == 2) rc = launch_block_rt<BITS, D, 2, T4M, false, PM, false, WIN>(cc, a, n_qt, stream);
+        if (rt == 2) rc = launch_block_rt<BITS, D, 2, T4M, false, PM, false, WIN, CAP>(cc, a, n_qt, stream);
     }
-    if (rt == 1) rc = launch_block_rt<BITS, D, 1, T4M, false, PM, false, WIN>(cc, a, n_qt, stream);
+    if (rt == 1) rc = launch_block_rt<BITS, D, 1, T4M, false, PM, false, WIN, CAP>(cc, a, n_qt, stream);
     return rc;
 }
 
@@ -1321,7 +1385,7 @@ static void split_keys(int n_tiles, int want, int* n_split, int* tps) {
 template <int BITS, int D, int T4M = 0>
 static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float scale, bool causal,
                              f16* out, hipStream_t stream, const float* t4_tab = nullptr,
-                             int window = 0) {
+                             int window = 0, float softcap = 0.0f) {
     using S = BlockShape<D>;
     const int T = cc.offset;
     const int R = G * Tq;
@@ -1329,7 +1393,7 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     // long prefill calls dequantize (fp16: lay out) each key tile once into an
     // image of its LDS buffer and attend from the images, in query tiles of
     // 16 kImageWaves rows
-    const bool images = QW_BLOCK_IMAGES && T4M != 2 && window <= 0 &&
+    const bool images = QW_BLOCK_IMAGES && T4M != 2 && window <= 0 && softcap <= 0.0f &&
                         R >= (T4M ? kT4ImageMinRows : kImageMinRows) && n_tiles > 0;
     const int rt = images ? 1 : pick_rt(R, cc.hkv);
     const int wg_rows = 16 * (images ? kImageWaves : kBlockWaves) * rt;
@@ -1370,7 +1434,10 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     a.img = nullptr;
     a.img_tiles = n_tiles;
     a.pair_h = 0;
-    a.window = window > 0 ? window : 0;
+    // (a softcap launch without a window: one wider than any position)
+    a.window = window > 0 ? window : softcap > 0.0f ? (1 << 30) : 0;
+    a.softcap = softcap;
+    a.scale = scale;
     int rc;
     if constexpr (T4M != 2) {
         if (images) {
@@ -1407,6 +1474,7 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
             if (images) return launch_one<BITS, D, T4M, 2>(cc, x, rt, n_qt_, stream);
         }
         if constexpr (T4M == 0) {
+            if (softcap > 0.0f) return launch_one<BITS, D, 0, 0, true, true>(cc, x, rt, n_qt_, stream);
             if (window > 0) return launch_one<BITS, D, 0, 0, true>(cc, x, rt, n_qt_, stream);
         }
         return launch_one<BITS, D, T4M>(cc, x, rt, n_qt_, stream);
@@ -1459,20 +1527,23 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     return QW_OK;
 }
 
-int launch_block_attention_window(KVCache& cc, const f16* q, int G, int n_rows, float scale,
-                                  int window, f16* out, hipStream_t stream) {
+int launch_block_attention_ext(KVCache& cc, const f16* q, int G, int n_rows, float scale,
+                               bool causal, int window, float softcap, f16* out,
+                               hipStream_t stream) {
     QW_REQUIRE(cc.affine() || cc.bits == 16, QW_ERR_INVALID_ARGUMENT,
-               "block attention: windowed route is for affine, Int8 and fp16 caches");
-    QW_REQUIRE(window > 0 && (cc.D == 128 || cc.D == 256), QW_ERR_INVALID_ARGUMENT,
-               "block attention: window launch outside its shapes");
+               "block attention: window / softcap route is for affine, Int8 and fp16 caches");
+    QW_REQUIRE((window > 0 || softcap > 0.0f) && (window <= 0 || causal) &&
+                   (cc.D == 128 || cc.D == 256),
+               QW_ERR_INVALID_ARGUMENT, "block attention: window / softcap launch outside its shapes");
+    const int w = window > 0 ? window : 0;
     if (cc.D == 256) {
-        if (cc.bits == 4) return launch_block_bits<4, 256>(cc, q, G, n_rows, scale, true, out, stream, nullptr, window);
-        if (cc.bits == 8) return launch_block_bits<8, 256>(cc, q, G, n_rows, scale, true, out, stream, nullptr, window);
-        return launch_block_bits<16, 256>(cc, q, G, n_rows, scale, true, out, stream, nullptr, window);
+        if (cc.bits == 4) return launch_block_bits<4, 256>(cc, q, G, n_rows, scale, causal, out, stream, nullptr, w, softcap);
+        if (cc.bits == 8) return launch_block_bits<8, 256>(cc, q, G, n_rows, scale, causal, out, stream, nullptr, w, softcap);
+        return launch_block_bits<16, 256>(cc, q, G, n_rows, scale, causal, out, stream, nullptr, w, softcap);
     }
-    if (cc.bits == 4) return launch_block_bits<4, 128>(cc, q, G, n_rows, scale, true, out, stream, nullptr, window);
-    if (cc.bits == 8) return launch_block_bits<8, 128>(cc, q, G, n_rows, scale, true, out, stream, nullptr, window);
-    return launch_block_bits<16, 128>(cc, q, G, n_rows, scale, true, out, stream, nullptr, window);
+    if (cc.bits == 4) return launch_block_bits<4, 128>(cc, q, G, n_rows, scale, causal, out, stream, nullptr, w, softcap);
+    if (cc.bits == 8) return launch_block_bits<8, 128>(cc, q, G, n_rows, scale, causal, out, stream, nullptr, w, softcap);
+    return launch_block_bits<16, 128>(cc, q, G, n_rows, scale, causal, out, stream, nullptr, w, softcap);
 }
 
 int launch_block_attention_t4(KVCache& cc, const f16* q, int G, int n_rows, float scale,

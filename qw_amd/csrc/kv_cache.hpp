@@ -190,10 +190,12 @@ int launch_turbo4_decode(KVCache& c, const f16* q, int G, int n_rows, float scal
 // (fp16) to out; fused = true is the reference's fused verify pass (q scaled
 // by scale * log2 e, fp32 scores; every row key-split) and its merge writes
 // the rows rotated back to out. tab: the cache's device tables.
-// A causal sliding window over an affine, Int8 or fp16 cache (D 128 / 256):
-// the block kernel reading the codes, each row's keys p - window + 1 .. p.
-int launch_block_attention_window(KVCache& c, const f16* q, int G, int n_rows, float scale,
-                                  int window, f16* out, hipStream_t stream);
+// A causal sliding window (window > 0: each row's keys p - window + 1 .. p)
+// and/or a logit softcap over an affine, Int8 or fp16 cache (D 128 / 256):
+// the block kernel reading the codes.
+int launch_block_attention_ext(KVCache& c, const f16* q, int G, int n_rows, float scale,
+                               bool causal, int window, float softcap, f16* out,
+                               hipStream_t stream);
 int launch_block_attention_t4(KVCache& c, const f16* q, int G, int n_rows, float scale, bool causal,
                               bool fused, const float* tab, f16* out, hipStream_t stream);
 // Turbo4 merge of split partials ([hkv][nc][rstride][D], slot_bits as

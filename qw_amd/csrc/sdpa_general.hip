@@ -411,8 +411,9 @@ int sdpa_general(const void* q, int n_q_heads, int n_rows, const void* k, const 
     return QW_OK;
 }
 
-// 1: a causal sliding window without mask or softcap over an affine, Int8 or
-// fp16 cache runs the fused block kernel; 0: the dequantize-then-SDPA route.
+// 1: a causal sliding window and / or a softcap without a mask over an affine,
+// Int8 or fp16 cache runs the fused block kernel; 0: the dequantize-then-SDPA
+// route.
 #ifndef QW_FUSED_WINDOW
 #define QW_FUSED_WINDOW 1
 #endif
@@ -446,12 +447,13 @@ int cache_attention_general(KVCache& c, const void* q, int n_q_heads, int n_rows
     if (c.turbo4()) return turbo4_attention_general(c, q, n_q_heads, n_rows, scale, o, out, stream);
     DeviceGuard dg(c.device);
     QW_REQUIRE(dg.ok, QW_ERR_HIP, "attention: hipSetDevice failed");
-    // a causal window alone (the served arithmetic, a lower bound on each
-    // row's keys): the fused block kernel on the codes, no dequantized copy
-    if (QW_FUSED_WINDOW && !o.mask && o.softcap == 0.0f && o.window > 0 && o.causal &&
-        (c.D == 128 || c.D == 256))
-        return launch_block_attention_window(c, (const f16*)q, n_q_heads / c.hkv, n_rows, scale,
-                                             o.window, (f16*)out, stream);
+    // a causal window (the served arithmetic with a lower bound on each row's
+    // keys) and / or a softcap, without a mask: the fused block kernel on the
+    // codes, no dequantized copy
+    if (QW_FUSED_WINDOW && !o.mask && (o.softcap > 0.0f || o.window > 0) &&
+        (o.window <= 0 || o.causal) && std::isfinite(o.softcap) && (c.D == 128 || c.D == 256))
+        return launch_block_attention_ext(c, (const f16*)q, n_q_heads / c.hkv, n_rows, scale,
+                                          o.causal, o.window, o.softcap, (f16*)out, stream);
     const int T = c.offset, D = c.D;
     // A sliding window sees no key below lo (the first row's window start):
     // only keys lo .. T - 1 are dequantized, and the call runs on them with

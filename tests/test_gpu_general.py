@@ -253,6 +253,40 @@ def test_cache_window_fused_route(mode, hq, hkv, D, T, L, W):
     cache.close()
 
 
+CAP_CASES = [
+    # mode, hq, hkv, D, T (after the rows), L, window, softcap, causal
+    ("affine4", 24, 4, 256, 32769, 1, 0, 30.0, True),   # a softcapped decode step, c2 geometry
+    ("affine8", 24, 4, 256, 5000, 37, 0, 50.0, True),
+    ("int8", 16, 2, 128, 3000, 5, 0, 20.0, False),
+    ("fp16", 8, 8, 128, 2500, 300, 700, 30.0, True),   # softcap and a sliding window
+    ("affine4", 6, 1, 128, 700, 3, 0, 5.0, False),     # a cap that bends most scores
+]
+
+
+@pytest.mark.parametrize("mode,hq,hkv,D,T,L,W,cap,causal", CAP_CASES)
+def test_cache_softcap_fused_route(mode, hq, hkv, D, T, L, W, cap, causal):
+    """A logit softcap (with or without a causal window) and no mask over an
+    affine, Int8 or fp16 cache runs the block kernel on the codes with the
+    softcap composite's arithmetic (S = f16(q . k), tanh in fp32, fp32 P):
+    checked against the oracle on the cache's own dequantized rows."""
+    import qw_amd
+
+    print(f"case softcap fused {mode} D={D} T={T} L={L} W={W} cap={cap} causal={causal}",
+          flush=True)
+    r = rng(800 + L + int(cap))
+    k = (r.standard_normal((hkv, T, D)) * 2).astype(np.float16)
+    v = r.standard_normal((hkv, T, D)).astype(np.float16)
+    q = (r.standard_normal((hq, L, D)) * 2).astype(np.float16)
+    cache = qw_amd.KVCache(mode, hkv, D)
+    cache.update(_gpu(k), _gpu(v))
+    out = _np(cache.attention_general(_gpu(q), D ** -0.5, causal=causal, window=W,
+                                      softcap=cap))[0]
+    kd, vd = (_np(x)[0] for x in cache.dequantize())
+    ref = oracle.sdpa_general(q, kd, vd, D ** -0.5, causal, W, cap)
+    assert_close(out, ref, f"{mode} softcap {cap} window {W}")
+    cache.close()
+
+
 def test_general_contract_errors():
     import qw_amd
 
