@@ -287,6 +287,36 @@ def test_cache_softcap_fused_route(mode, hq, hkv, D, T, L, W, cap, causal):
     cache.close()
 
 
+@pytest.mark.parametrize("mode", ["affine4", "affine8"])
+def test_fused_options_with_extreme_scales(mode):
+    """Groups whose scales miss the 2-op dequant's exact range (|scale| < 2^-10
+    or >= 64) send the fused window and softcap launches through their second,
+    separately rounded pass, which must match the composite dequant the
+    cache's own dequantize() returns."""
+    import qw_amd
+
+    print(f"case extreme fused options {mode}", flush=True)
+    r = rng(860 + len(mode))
+    hq, hkv, D, T, L = 24, 4, 256, 3000, 4
+    k = r.standard_normal((hkv, T, D)).astype(np.float32)
+    v = r.standard_normal((hkv, T, D)).astype(np.float32)
+    k[:, 2500:2540, :64] *= 1e-3
+    k[:, 2900:2901, 64:128] *= 300.0
+    v[:, 2600:2660, 128:192] *= 1e-3
+    v[:, 2950:2960, :64] *= 100.0
+    k, v = k.astype(np.float16), v.astype(np.float16)
+    q = r.standard_normal((hq, L, D)).astype(np.float16)
+    cache = qw_amd.KVCache(mode, hkv, D)
+    cache.update(_gpu(k), _gpu(v))
+    kd, vd = (_np(x)[0] for x in cache.dequantize())
+    for W, cap in ((600, 0.0), (0, 30.0), (600, 30.0)):
+        out = _np(cache.attention_general(_gpu(q), 1 / 16, causal=True, window=W,
+                                          softcap=cap))[0]
+        ref = oracle.sdpa_general(q, kd, vd, 1 / 16, True, W, cap)
+        assert_close(out, ref, f"{mode} extreme window {W} softcap {cap}")
+    cache.close()
+
+
 def test_general_contract_errors():
     import qw_amd
 
