@@ -120,14 +120,45 @@ __device__ __forceinline__ float dpp_mov(float x) {
     return __builtin_bit_cast(
         float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
 }
+// The value lane l ^ S holds (S a power of two below 64) without an LDS
+// permute: DPP row moves for S < 16 (quad_perm for 1 and 2, a rotate by 8
+// within the 16-lane row for 8, the row shift that stays in the row for 4)
+// and the permlane swaps for 16 and 32 (after a swap of x with itself, a
+// lower-half lane holds its own value in [0] and the partner's in [1], an
+// upper-half lane the other way round). Exact copies, so any butterfly built
+// on it keeps its arithmetic bit for bit.
+template <int S>
+__device__ __forceinline__ float lane_xor(float x, int lane) {
+    const uint32_t u = __float_as_uint(x);
+    if constexpr (S == 1) {
+        return __uint_as_float(__builtin_amdgcn_update_dpp(0u, u, 0xB1, 0xF, 0xF, false));
+    } else if constexpr (S == 2) {
+        return __uint_as_float(__builtin_amdgcn_update_dpp(0u, u, 0x4E, 0xF, 0xF, false));
+    } else if constexpr (S == 4) {
+        const uint32_t up = __builtin_amdgcn_update_dpp(0u, u, 0x104, 0xF, 0xF, false);  // lane + 4
+        const uint32_t dn = __builtin_amdgcn_update_dpp(0u, u, 0x114, 0xF, 0xF, false);  // lane - 4
+        return __uint_as_float((lane & 4) ? dn : up);
+    } else if constexpr (S == 8) {
+        return __uint_as_float(__builtin_amdgcn_update_dpp(0u, u, 0x128, 0xF, 0xF, false));
+    } else if constexpr (S == 16) {
+        const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        return __uint_as_float((lane & 16) ? a[0] : a[1]);
+    } else {
+        static_assert(S == 32, "lane_xor: a power of two below 64");
+        const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        return __uint_as_float((lane & 32) ? a[0] : a[1]);
+    }
+}
+
 template <class Op>
 __device__ __forceinline__ float wave_reduce(float x, Op op) {
     x = op(x, dpp_mov<0xB1>(x));   // quad_perm [1,0,3,2]
     x = op(x, dpp_mov<0x4E>(x));   // quad_perm [2,3,0,1]
     x = op(x, dpp_mov<0x124>(x));  // row_ror 4
     x = op(x, dpp_mov<0x128>(x));  // row_ror 8
-    x = op(x, __shfl_xor(x, 16));
-    return op(x, __shfl_xor(x, 32));
+    const int lane = (int)__lane_id();
+    x = op(x, lane_xor<16>(x, lane));
+    return op(x, lane_xor<32>(x, lane));
 }
 struct OpSum {
     __device__ float operator()(float a, float b) const { return a + b; }

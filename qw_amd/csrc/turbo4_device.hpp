@@ -21,36 +21,6 @@ __host__ __device__ constexpr float wht_scale(int D) {
     return D == 256 ? 0.0625f : (D == 128 ? 0.08838834764831845f : 0.0f);
 }
 
-// The value lane l ^ S holds (S a power of two below 64) without an LDS
-// permute: DPP row moves for S < 16 (quad_perm for 1 and 2, a rotate by 8
-// within the 16-lane row for 8, the row shift that stays in the row for 4)
-// and the permlane swaps for 16 and 32 (after a swap of x with itself, a
-// lower-half lane holds its own value in [0] and the partner's in [1], an
-// upper-half lane the other way round). Exact copies, so any butterfly built
-// on it keeps its arithmetic bit for bit.
-template <int S>
-__device__ __forceinline__ float lane_xor(float x, int lane) {
-    const uint32_t u = __float_as_uint(x);
-    if constexpr (S == 1) {
-        return __uint_as_float(__builtin_amdgcn_update_dpp(0u, u, 0xB1, 0xF, 0xF, false));
-    } else if constexpr (S == 2) {
-        return __uint_as_float(__builtin_amdgcn_update_dpp(0u, u, 0x4E, 0xF, 0xF, false));
-    } else if constexpr (S == 4) {
-        const uint32_t up = __builtin_amdgcn_update_dpp(0u, u, 0x104, 0xF, 0xF, false);  // lane + 4
-        const uint32_t dn = __builtin_amdgcn_update_dpp(0u, u, 0x114, 0xF, 0xF, false);  // lane - 4
-        return __uint_as_float((lane & 4) ? dn : up);
-    } else if constexpr (S == 8) {
-        return __uint_as_float(__builtin_amdgcn_update_dpp(0u, u, 0x128, 0xF, 0xF, false));
-    } else if constexpr (S == 16) {
-        const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-        return __uint_as_float((lane & 16) ? a[0] : a[1]);
-    } else {
-        static_assert(S == 32, "lane_xor: a power of two below 64");
-        const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-        return __uint_as_float((lane & 32) ? a[0] : a[1]);
-    }
-}
-
 // Sum over the wave by an xor butterfly (offsets 32, 16, ..., 1): the order
 // every Turbo4 norm is formed in, so all kernels store the same rescales.
 __device__ __forceinline__ float t4_wave_sum(float x) {
