@@ -676,8 +676,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
         }
     }
     float lsum = l_run;
-    lsum += __shfl_xor(lsum, 16);
-    lsum += __shfl_xor(lsum, 32);
+    lsum += lane_xor<16>(lsum, lane);
+    lsum += lane_xor<32>(lsum, lane);
     // ---- merge the NW waves into the workgroup's partial. The VALU work of
     // a merge is what sits on the critical path after the last data (two
     // waves a SIMD run it at once), so each step does as little as it can:
@@ -718,8 +718,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, float2 (*sm_ml)
             sm_f[((r16 >> 2) * NW + w) * 4 + (r16 & 3)] = f;
             L = __builtin_fmaf(f, ml.y, L);
         }
-        L += __shfl_xor(L, 16);
-        L += __shfl_xor(L, 32);
+        L += lane_xor<16>(L, lane);
+        L += lane_xor<32>(L, lane);
         if (g == 0 && r16 < R) part_ml[((int64_t)h * a.nc + c) * 16 + r16] = float2{M, L};
     }
     __syncthreads();
