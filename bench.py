@@ -326,6 +326,36 @@ def bench_rope_decode(torch, qw_amd, reps: int, mode=None, T_prefix: int = 32768
     return res
 
 
+def bench_general_options(torch, qw_amd, reps: int, L: int = 1, T_prefix: int = 32768,
+                          window: int = 4096, softcap: float = 30.0):
+    """causal_attention's sliding window and softcap (lib.rs:3185) over the
+    config-2 caches as they are (4-bit, L causal rows), graph-replayed over 16
+    caches like the headline: qw_kv_attention (no option), then
+    qw_kv_attention_general with the window, and with the softcap (both run
+    the fused block kernel on the codes)."""
+    ls = LayerSet(torch, qw_amd, 11, 4, T_prefix, L, LAYERS, causal=True)
+    lib = ls.lib
+
+    def plain(i, st):
+        c = ls.caches[i][0]
+        ls._check(lib.qw_kv_attention(c._h, ls.q[i].data_ptr(), HQ, L, 1.0 / 16, 1,
+                                      ls.out[i].data_ptr(), st))
+
+    def general(i, st, w, cap):
+        c = ls.caches[i][0]
+        ls._check(lib.qw_kv_attention_general(c._h, ls.q[i].data_ptr(), HQ, L, 1.0 / 16, 1, w,
+                                              cap, None, 0, 0, 0, ls.out[i].data_ptr(), st))
+
+    n = len(ls.caches)
+    res = {}
+    for name, fn in (("attention", plain),
+                     (f"window_{window}", lambda i, st: general(i, st, window, 0.0)),
+                     (f"softcap_{int(softcap)}", lambda i, st: general(i, st, 0, softcap))):
+        res[name] = replay_stats(torch, lambda i, f=fn: f(i, ls.stream()), n, n, reps)["median"]
+    ls.close()
+    return res
+
+
 def bench_turbo4_verify(torch, qw_amd, steps: int, warmup: int, reps: int,
                         T_prefix: int = 32768, L: int = 4):
     """A Turbo4 causal verify block (L draft rows, the reference's fused-pass
@@ -1193,6 +1223,15 @@ def main() -> int:
             "forms": "one_launch: qw_kv_rope_update_and_attention; reference_calls: "
                      "qw_fused_rope_qk_append then qw_kv_update_and_attention; "
                      "rope_update_then_attention: qw_kv_rope_update then qw_kv_attention"}
+        log("bench: the general options over the config-2 caches (window, softcap)")
+        go = {}
+        for L_ in (1, 4):
+            r_ = bench_general_options(torch, qw_amd, reps, L=L_)
+            go[f"{L_}row" + ("s" if L_ > 1 else "")] = {k: round(v * 1e3, 2) for k, v in r_.items()}
+        extra["general_options"] = {
+            "us": go, "keys": 32768, "causal": True,
+            "forms": "attention: qw_kv_attention; window_4096 / softcap_30: "
+                     "qw_kv_attention_general (the fused block kernel on the codes)"}
         log("bench: Turbo4 decode (config-2 geometry)")
         t4 = bench_turbo4_decode(torch, qw_amd, LAYERS, args.warmup, reps)
         extra["turbo4_decode"] = {

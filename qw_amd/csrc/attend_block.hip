@@ -162,6 +162,9 @@ constexpr bool kSetprio(int pm) {
 #ifndef QW_BLOCK_KSPLIT
 #define QW_BLOCK_KSPLIT 2
 #endif
+#ifndef QW_WINDOW_MIN_TILES
+#define QW_WINDOW_MIN_TILES 1  // key tiles a split of a window launch takes at least
+#endif
 #ifndef QW_BLOCK_KSPLIT_APP
 #define QW_BLOCK_KSPLIT_APP 0
 #endif
@@ -1373,9 +1376,11 @@ int image_workspace(int device, hipStream_t stream, size_t need, void** out) {
 }
 }  // namespace
 
-// Splits `n_tiles` key tiles into about `want` parts of at least 4 tiles.
-static void split_keys(int n_tiles, int want, int* n_split, int* tps) {
-    int ns = std::max(1, std::min({want, (n_tiles + 3) / 4, 256}));
+// Splits `n_tiles` key tiles into about `want` parts of at least min_tiles
+// tiles (4: a workgroup's fixed costs amortized over its rounds; a window's
+// few tiles spread wider).
+static void split_keys(int n_tiles, int want, int* n_split, int* tps, int min_tiles = 4) {
+    int ns = std::max(1, std::min({want, (n_tiles + min_tiles - 1) / min_tiles, 256}));
     *tps = (n_tiles + ns - 1) / ns;
     *n_split = (n_tiles + *tps - 1) / *tps;
 }
@@ -1495,7 +1500,8 @@ static int launch_block_bits(KVCache& cc, const f16* q, int G, int Tq, float sca
     // (a window: the keys from a query tile's first window start to its last row)
     const int plan_tiles =
         window > 0 ? std::min(n_tiles, (window + wg_rows / G + 1 + S::KT - 1) / S::KT + 1) : n_tiles;
-    split_keys(plan_tiles, T4M == 2 ? std::min(std::max(want, 2), 128) : want, &n_split, &tps);
+    split_keys(plan_tiles, T4M == 2 ? std::min(std::max(want, 2), 128) : want, &n_split, &tps,
+               window > 0 ? QW_WINDOW_MIN_TILES : 4);
     QW_REQUIRE(T4M != 2 || n_split > 1, QW_ERR_INVALID_ARGUMENT,
                "block attention: fused Turbo4 pass needs at least 5 key tiles");
     BlockArgs t = a;
