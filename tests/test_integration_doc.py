@@ -1,4 +1,4 @@
-"""The Rust binding recipe in INTEGRATION.md stays in step with the build and
+"""The Rust binding recipe of the integration guide (DOC below) stays in step with the build and
 the C header: build.rs compiles exactly qw_amd/build.py's SOURCES, and the
 extern "C" block declares every entry point of include/qwattn.h with the same
 number of arguments. CPU only (text checks)."""
