@@ -257,6 +257,8 @@ def test_served_verify_blocks_vs_oracle(oracle_lib, bits, T_prefix, L, hq):
     (4, 0, 100, True, 256, 24, 4, None),        # prefill into an empty cache
     (4, 777, 5, True, 128, 32, 8, None),        # head_dim 128, G = 4
     (8, 4000, 17, True, 128, 8, 8, None),       # no GQA sharing (G = 1), 17 rows
+    (4, 3000, 24, True, 128, 32, 8, None),      # 96 rows a KV head at head_dim 128: six row tiles, key-split
+    (8, 2000, 13, True, 256, 24, 4, None),      # 78 rows a KV head: five row tiles, key-split
     # 3072+ rows a KV head: key tiles dequantized once into LDS images
     (4, 3000, 520, True, 256, 24, 4, [0, 1, 63, 64, 300, 519]),   # 3120 rows a KV head
     (4, 500, 400, False, 128, 16, 2, [0, 5, 128, 399]),           # head_dim 128, no mask
