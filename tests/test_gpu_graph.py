@@ -70,6 +70,50 @@ def test_graph_attention_replays_and_growth(mode):
     c.close()
 
 
+def test_graph_window_and_softcap_routes():
+    """The fused window and softcap launches (the block kernel's WIN / CAP
+    instances over the codes, split partials and their merge) captured in one
+    graph: replays equal the eager outputs, with eager work between them, also
+    after a larger call grows the cache's split-K workspace."""
+    r = rng(13)
+    H, G, D, T = 4, 6, 256, 9000
+    c = _cache("affine4", r, H, T, D)
+    q1 = _gpu(r.standard_normal((H * G, 1, D)).astype(np.float16))
+    q4 = _gpu(r.standard_normal((H * G, 4, D)).astype(np.float16))
+    want_w = _np(c.attention_general(q1, 1 / 16, causal=True, window=700))
+    want_c = _np(c.attention_general(q4, 1 / 16, causal=True, softcap=30.0))
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):  # size the workspace on the capture stream
+        c.attention_general(q1, 1 / 16, causal=True, window=700)
+        c.attention_general(q4, 1 / 16, causal=True, softcap=30.0)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        o_w = c.attention_general(q1, 1 / 16, causal=True, window=700)
+        o_c = c.attention_general(q4, 1 / 16, causal=True, softcap=30.0)
+    for rep in range(3):
+        o_w.zero_()
+        o_c.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(_np(o_w), want_w, err_msg=f"window replay {rep}")
+        np.testing.assert_array_equal(_np(o_c), want_c, err_msg=f"softcap replay {rep}")
+        _ = (q1.float() * 2).sum().item()  # eager work between replays
+    q2k = _gpu(r.standard_normal((H * G, 2048, D)).astype(np.float16))
+    big = _np(c.attention(q2k, 1 / 16, causal=True))
+    assert np.isfinite(big).all()
+    for rep in range(2):
+        o_w.zero_()
+        o_c.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(_np(o_w), want_w, err_msg=f"after growth, window {rep}")
+        np.testing.assert_array_equal(_np(o_c), want_c, err_msg=f"after growth, softcap {rep}")
+    del g
+    c.close()
+
+
 def test_graph_dlsa_replays_and_growth():
     """A D-LSA read captured on its own stream: replays equal the eager
     output, also after a larger call grows that stream's workspace."""
