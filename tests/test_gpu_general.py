@@ -253,6 +253,34 @@ def test_cache_window_fused_route(mode, hq, hkv, D, T, L, W):
     cache.close()
 
 
+def test_cache_window_long_prefill_rows():
+    """A windowed prefill long enough that whole rounds of query tiles run
+    unsplit and the rest split their keys (19200 rows a KV head: 128 unsplit
+    tiles, 22 split), checked row by row: row r (position p) against the
+    oracle on keys 0 .. p with the same window."""
+    import qw_amd
+
+    print("case window long prefill", flush=True)
+    r = rng(905)
+    hq, hkv, D, L, T0, W = 8, 2, 128, 4800, 1000, 700
+    T = T0 + L
+    G = hq // hkv
+    k = r.standard_normal((hkv, T, D)).astype(np.float16)
+    v = r.standard_normal((hkv, T, D)).astype(np.float16)
+    q = r.standard_normal((hq, L, D)).astype(np.float16)
+    cache = qw_amd.KVCache("affine4", hkv, D)
+    cache.update(_gpu(k), _gpu(v))
+    out = _np(cache.attention_general(_gpu(q), D ** -0.5, causal=True, window=W))[0]
+    kd, vd = (_np(x)[0] for x in cache.dequantize())
+    for row in (0, 1, 31, 32, 2000, 4095, 4096, 4500, 4799):  # rows 4096.. sit in split tiles
+        p = T0 + row
+        ref = oracle.sdpa_general(q[:, row:row + 1], kd[:, :p + 1], vd[:, :p + 1], D ** -0.5,
+                                  True, W)
+        assert_close(out[:, row:row + 1], ref, f"long window prefill row {row}")
+    assert G * L == 19200
+    cache.close()
+
+
 CAP_CASES = [
     # mode, hq, hkv, D, T (after the rows), L, window, softcap, causal
     ("affine4", 24, 4, 256, 32769, 1, 0, 30.0, True),   # a softcapped decode step, c2 geometry
