@@ -336,9 +336,11 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     // epilogue (the same combine as the split merge).
     // (not in the affine / Int8 launches that append: measured 0.5-1 us slower
     // there, where the attention-only launches gain 1-1.5 us and the Turbo4
-    // fused pass 7.7 us at 4 rows)
+    // fused pass 7.7 us at 4 rows; not in the window launches, 0.3 us slower,
+    // but in the softcap ones, whose tanh and second P.V MFMA make the tile
+    // compute-bound: 35.0 -> 24.0 us for a decode step over 32k keys)
     constexpr bool KS_OK = QW_BLOCK_KSPLIT && PM == 0 && RT == 1 && NW == 8 && NSUB % 2 == 0 &&
-                           (!APP || T4 || QW_BLOCK_KSPLIT_APP) && !WIN;
+                           (!APP || T4 || QW_BLOCK_KSPLIT_APP) && (!WIN || CAP);
     bool ks_any = false, ks_half = false;
     int ks_ub = 0;  // the wave's first sub-block of a tile
     if constexpr (KS_OK) {
