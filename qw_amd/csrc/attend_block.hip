@@ -158,7 +158,8 @@ constexpr bool kSetprio(int pm) {
 }
 
 // Key-split row tiles (block_body): 1 for workgroups of 5 or 6 row tiles, 2
-// also for those of 1 or 2; 0 off.
+// also for those of 1 or 2, 3 also for those of 3 or 4 (which the softcap
+// launches always split); 0 off.
 #ifndef QW_BLOCK_KSPLIT
 #define QW_BLOCK_KSPLIT 2
 #endif
@@ -359,6 +360,14 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
                 wrow0 = row0 + 16 * (wave & 1);
                 ks_ub = ((wave >> 1) & 1) * (NSUB / 2);
             }
+        } else if (n_rt <= 4 && (QW_BLOCK_KSPLIT >= 3 || CAP)) {
+            // 3 or 4 row tiles: tile t on waves t and t + 4 (one SIMD), a half
+            // each (softcap launches only: 37.2 -> 30.2 us at 8 rows a sequence;
+            // the affine and Turbo4 launches measured 1-3.5 us slower)
+            ks_any = true;
+            ks_half = true;
+            wrow0 = row0 + 16 * (wave & 3);
+            ks_ub = (wave >> 2) * (NSUB / 2);
         }
     }
     auto cut = [&](int lim_) { return APP ? min(lim_, key_hi - 1) : lim_; };
@@ -1106,10 +1115,12 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     // last barrier freed; the first half combines them into its own.
     if constexpr (KS_OK) {
         if (ks_any) {
-            // slot = the tile's parity: [2][64 lanes] (m, l), then [2][NT][64] O
+            // slot = the tile's place mod 4: [4][64 lanes] (m, l), then [4][NT][64] O
             float2* const kml = (float2*)lds;
-            float4v* const ko = (float4v*)(lds + 2 * 64 * sizeof(float2));
-            const int slot = ((wrow0 - row0) >> 4) & 1;
+            float4v* const ko = (float4v*)(lds + 4 * 64 * sizeof(float2));
+            static_assert(4 * 64 * sizeof(float2) + 4 * NT * 64 * sizeof(float4v) <= BUF,
+                          "the split halves' exchange fits tile buffer 0");
+            const int slot = ((wrow0 - row0) >> 4) & 3;
             if (ks_half && ks_ub != 0 && wave_live) {
                 kml[slot * 64 + lane] = float2{m_run[0], l_run[0]};
 #pragma unroll
