@@ -159,7 +159,7 @@ constexpr bool kSetprio(int pm) {
 
 // Key-split row tiles (block_body): 1 for workgroups of 5 or 6 row tiles, 2
 // also for those of 1 or 2, 3 also for those of 3 or 4 (which the softcap
-// launches always split); 0 off.
+// launches and the Turbo4 fused pass always split); 0 off.
 #ifndef QW_BLOCK_KSPLIT
 #define QW_BLOCK_KSPLIT 2
 #endif
@@ -360,10 +360,11 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
                 wrow0 = row0 + 16 * (wave & 1);
                 ks_ub = ((wave >> 1) & 1) * (NSUB / 2);
             }
-        } else if (n_rt <= 4 && (QW_BLOCK_KSPLIT >= 3 || CAP)) {
+        } else if (n_rt <= 4 && (QW_BLOCK_KSPLIT >= 3 || CAP || FUSED)) {
             // 3 or 4 row tiles: tile t on waves t and t + 4 (one SIMD), a half
-            // each (softcap launches only: 37.2 -> 30.2 us at 8 rows a sequence;
-            // the affine and Turbo4 launches measured 1-3.5 us slower)
+            // each (softcap launches: 37.2 -> 30.2 us at 8 rows a sequence; the
+            // Turbo4 fused pass at G = 8, 5 rows: 41.9 -> 37.2 us; the affine
+            // launches and the Turbo4 dequantize route measured 1-3.5 us slower)
             ks_any = true;
             ks_half = true;
             wrow0 = row0 + 16 * (wave & 3);
