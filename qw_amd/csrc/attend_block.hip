@@ -333,8 +333,10 @@ __device__ __forceinline__ void block_body(const BlockArgs& a, char* lds) {
     // tiles 4 and 5 to waves 4..7, each wave computing half of every key tile
     // (tile 4: waves 4 and 6, SIMDs 0 and 2; tile 5: waves 5 and 7), so each
     // SIMD carries 1.5 tiles; one of 1 or 2 row tiles splits them over waves
-    // 0..3, one half a SIMD. The two halves' (m, l, O) meet before the
-    // epilogue (the same combine as the split merge).
+    // 0..3, one half a SIMD; in the launches whose tile math is heaviest (the
+    // softcap's and the Turbo4 fused pass's), one of 3 or 4 row tiles puts
+    // the halves of tile t on waves t and t + 4. The two halves' (m, l, O)
+    // meet before the epilogue (the same combine as the split merge).
     // (not in the affine / Int8 launches that append: measured 0.5-1 us slower
     // there, where the attention-only launches gain 1-1.5 us and the Turbo4
     // fused pass 7.7 us at 4 rows; not in the window launches, 0.3 us slower,
