@@ -25,7 +25,7 @@ baseline is the oracle's restatement of the MLX CPU stream, timed on a
 bounded sample on this host.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--reps R] [--no-cpu] [--no-extra]
-    python bench.py --pmc-workload c2|c3|c4|c5   # short run for rocprofv3 --pmc passes
+    python bench.py --pmc-workload c1|c2|c3|c4|c5   # short run for rocprofv3 --pmc passes
     python bench.py --summarize-counters CFG DIR --out profiles/counters_<cfg>.txt
     python bench.py --summarize-trace DB --out profiles/<name>.txt
 """
@@ -75,7 +75,7 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--reps", type=int, default=50, help="timed graph replays (at least 50)")
-    ap.add_argument("--pmc-workload", choices=["c2", "c3", "c4", "c5", "gemm"],
+    ap.add_argument("--pmc-workload", choices=["c1", "c2", "c3", "c4", "c5", "gemm"],
                     help="a 256 MiB copy then the configuration's attention calls, for counter runs")
     ap.add_argument("--summarize-counters", nargs=2, metavar=("CFG", "DIR"))
     ap.add_argument("--summarize-trace", metavar="DB")
@@ -812,6 +812,7 @@ PMC_PASSES = {
 }
 PMC_CONFIGS = {
     # cfg: (what the dispatches are, algorithmic bytes a call, algorithmic flops a call)
+    "c1": "config 1: 16 qw_kv_attention calls, 8-bit, 4096 keys, 16 caches",
     "c2": "config 2: 16 qw_kv_attention calls, 4-bit, 32769 keys, 16 caches",
     "c3": "config 3: 4 qw_kv_attention calls, 2048 causal rows over 18432 keys, 8-bit, 4 caches",
     "c4": "config 4: 16 qw_kv_attention calls, 16 causal rows over 65552 keys, 4-bit, 16 caches",
@@ -823,6 +824,9 @@ GEMM_N = 8192
 
 def pmc_algorithmic(cfg: str):
     """(bytes, flops) of one call of the configuration's attention."""
+    if cfg == "c1":
+        T = 4096
+        return T * HKV * kv_bytes_per_token_head(8) + 2 * HQ * D * 2, attn_flops(1, T, False)
     if cfg == "c2":
         T = 32769
         return T * HKV * kv_bytes_per_token_head(4) + 2 * HQ * D * 2, attn_flops(1, T, False)
@@ -866,7 +870,8 @@ def pmc_workload(cfg: str) -> int:
         bench_dlsa(torch, qw_amd, 0)
         print("pmc workload c5 done", flush=True)
         return 0
-    bits, T0, L, n, causal = {"c2": (4, 32768, 1, LAYERS, False),
+    bits, T0, L, n, causal = {"c1": (8, 4095, 1, LAYERS, False),
+                              "c2": (4, 32768, 1, LAYERS, False),
                               "c3": (8, 16384, 2048, 4, True),
                               "c4": (4, 65536, 16, LAYERS, True)}[cfg]
     ls = LayerSet(torch, qw_amd, 2, bits, T0, L, n, causal=causal)
@@ -881,7 +886,7 @@ def pmc_workload(cfg: str) -> int:
     return 0
 
 
-PMC_CALLS = {"c2": LAYERS, "c3": 4, "c4": LAYERS, "c5": LAYERS, "gemm": 3}
+PMC_CALLS = {"c1": LAYERS, "c2": LAYERS, "c3": 4, "c4": LAYERS, "c5": LAYERS, "gemm": 3}
 # the kernels a call of the configuration launches (set-up appends excluded)
 PMC_KERNELS = ("attend_decode_kernel", "attend_block_kernel", "decode_merge_kernel",
                "merge_rows_", "t4_merge_rotate_kernel", "dlsa_kernel", "dlsa_merge_kernel")
